@@ -1,0 +1,181 @@
+#!/usr/bin/env python3
+"""Benchmark: causal attention fwd+bwd on one MI355X (BASELINE.json metric).
+
+Workload (one "step"): forward + backward of causal scaled-dot-product attention,
+B=8 H=12 T=1024 d=64, fp32 (configs[1] is its forward half).  Q, K, V,
+dO are synthetic N(0, 1) tensors already resident in HBM; outputs, LSE and the backward
+workspace are preallocated, so the timed region is kernels only.
+
+Prints ONE JSON line.  `value` is TFLOP/s by the FA2 convention (fwd 2*B*H*T^2*d with
+causal counted as half of T^2 -> 12.885 GFLOP; fwd+bwd 3.5x -> 45.097 GFLOP per step).
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+
+B, H, T, D = 8, 12, 1024, 64
+CAUSAL = True
+FWD_FLOP = 2.0 * B * H * T * T * D / 2.0  # causal = half of T^2
+BWD_FLOP = 2.5 * FWD_FLOP
+STEP_FLOP = FWD_FLOP + BWD_FLOP
+PEAK_F32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
+METRIC = "causal attn fwd+bwd TFLOP/s + % MFMA peak, B8 H12 T1024 d64 fp32, 1 GPU"
+HERE = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "attn_bwd_f32_c3_traffic.txt")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def read_traffic():
+    """HBM bytes per launch of the backward kernel, from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel calibration); None if absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(seconds: float):
+    """PyTorch-CPU SDPA (the reference test's comparator) on the same workload shape."""
+    sys.path.insert(0, HERE)
+    from oracle import torch_cpu
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    med, reps, threads = torch_cpu.time_fwd_bwd((B, H, T, D), CAUSAL, seconds=seconds,
+                                               threads=threads)
+    return {
+        "value": STEP_FLOP / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"torch.nn.functional.scaled_dot_product_attention fp32 causal fwd+bwd on "
+                   f"CPU tensors, full B8 H12 T1024 d64 step, median of {reps} reps "
+                   f"({med * 1e3:.1f} ms/step) over ~{seconds:.0f} s, {threads} threads"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported; this build measures one GPU "
+              f"(the attention path shards by (batch, head) with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, HERE)
+    import cudatransformer_amd as ct
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    q, k, v, do = (torch.randn((B, H, T, D), generator=g, device=dev, dtype=torch.float32)
+                   for _ in range(4))
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    ws = torch.empty(ct.bwd_workspace_bytes(torch.float32, B, H, T, D, CAUSAL), device=dev,
+                     dtype=torch.uint8)
+    stream = torch.cuda.current_stream()
+
+    def fwd():
+        ct.flash_attn_fwd(q, k, v, CAUSAL, out=o, lse=lse, stream=stream)
+
+    def bwd():
+        ct.flash_attn_bwd(q, k, v, o, do, lse, CAUSAL, dq=dq, dk=dk, dv=dv, workspace=ws,
+                          stream=stream)
+
+    def step():
+        fwd()
+        bwd()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Whole-step timing: exactly K steps between two events on the launch stream.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    log(f"step: {ms_per_step:.4f} ms")
+
+    # Per-phase timing (same stream): forward alone, backward alone.
+    def time_phase(fn, reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    fwd_ms = time_phase(fwd, args.steps)
+    bwd_ms = time_phase(bwd, args.steps)
+    log(f"fwd: {fwd_ms:.4f} ms  bwd: {bwd_ms:.4f} ms")
+
+    value = STEP_FLOP / (ms_per_step * 1e-3) / 1e12
+    achieved = BWD_FLOP / (bwd_ms * 1e-3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "pct_of_peak": round(100.0 * value / PEAK_F32_MFMA, 2),
+        "config": {
+            "workload": "causal SDPA fwd+bwd, B8 H12 T1024 d64 fp32 (BASELINE configs[2])",
+            "B": B, "H": H, "T": T, "d": D, "causal": CAUSAL,
+            "step_gflop": round(STEP_FLOP / 1e9, 3),
+            "fwd_ms": round(fwd_ms, 5),
+            "bwd_ms": round(bwd_ms, 5),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attention backward (ctattn_bwd: preprocess + main kernel)",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_F32_MFMA,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_F32_MFMA, 4),
+            "traffic": read_traffic(),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log("timing CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

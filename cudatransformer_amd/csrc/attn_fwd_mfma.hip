@@ -1,0 +1,253 @@
+// fp32 flash-attention forward on fp32 MFMA (v_mfma_f32_32x32x2f32), gfx950.
+//
+// Replaces the reference forward kernel flashAttention<float> (flash_attention.cu:57-169):
+// same result (O = softmax(Q K^T / sqrt(d)) V per (batch, head)), plus a causal mask and
+// no zero-padded keys; it saves LSE = m + ln(l) instead of (m, l).
+//
+// Work decomposition
+//   * one workgroup = 4 waves = BM = 128 query rows of one (batch, head); each wave owns
+//     32 rows and keeps them for the whole key loop.
+//   * the key loop walks BN-key blocks.  K and V blocks are staged global -> registers ->
+//     LDS; the next block's global loads are issued before the current block's MFMAs so
+//     HBM latency hides behind compute.
+//   * scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q^T held in
+//     registers for the whole kernel, pre-scaled by log2(e)/sqrt(d)).  In the resulting
+//     accumulator each lane holds ONE query row (its column) and 16 keys per 32-key tile,
+//     so the online-softmax row statistics need a single cross-lane exchange (lane ^ 32)
+//     and, after exponentiation, the accumulator registers ARE the B operand of
+//     O^T += V^T P^T without any data movement.
+//   * the running max/denominator are kept in log2 units; exp is v_exp_f32.
+//   * causal: key tiles that lie wholly above a wave's diagonal are skipped (no MFMA);
+//     workgroups are ordered longest-first so the tail of the grid is short.
+#include "attn_launch.h"
+#include "attn_mfma_common.h"
+
+#include <math.h>
+
+namespace ctattn {
+namespace {
+
+template <int D, int BN>
+struct FwdCfg {
+    static constexpr int NW = 4;               // waves per workgroup
+    static constexpr int BM = 32 * NW;         // query rows per workgroup
+    static constexpr int STRIDE = D + 4;       // LDS row stride (floats); +4 avoids b128 bank conflicts
+    static constexpr int KT = BN / 32;         // 32-key tiles per block
+    static constexpr int DT = D / 32;          // 32-wide d tiles of O^T
+    static constexpr int F4_ROW = D / 4;       // float4 per row
+    static constexpr int F4_THREAD = BN * F4_ROW / (NW * kWave);
+    static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
+    static_assert((BN * F4_ROW) % (NW * kWave) == 0, "tile load split");
+};
+
+template <int D, int BN>
+__global__ __launch_bounds__(256) void fwd_f32_mfma_kernel(const float *__restrict__ q,
+                                                          const float *__restrict__ k,
+                                                          const float *__restrict__ v,
+                                                          float *__restrict__ o,
+                                                          float *__restrict__ lse, int T,
+                                                          int BH, int causal, float qscale) {
+    using C = FwdCfg<D, BN>;
+    __shared__ __attribute__((aligned(16))) float k_lds[BN * C::STRIDE];
+    __shared__ __attribute__((aligned(16))) float v_lds[BN * C::STRIDE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    const int qb = causal ? (nqb - 1 - id / BH) : id / BH;
+    const int64_t base = int64_t(bh) * T * D;
+    const int q0 = qb * C::BM;
+    const int row = q0 + wave * 32 + col;  // query row owned by this lane
+    const int wave_last_row = q0 + wave * 32 + 31;
+
+    // Q^T as the B operand: lane (col=row, half) holds Q[row][kstep_index(s, half)].
+    float qreg[D / 2];
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) {
+        floatx4 x = {0.f, 0.f, 0.f, 0.f};
+        if (row < T) x = *reinterpret_cast<const floatx4 *>(q + base + int64_t(row) * D + 8 * m + 4 * half);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) qreg[4 * m + t] = x[t] * qscale;
+    }
+
+    floatx16 oacc[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) oacc[dt] = zero16();
+    float m_run = -INFINITY;  // running row max (log2 units), same in both halves
+    float l_run = 0.f;        // this half's share of the running denominator
+
+    const int kend = causal ? min(T, q0 + C::BM) : T;
+    const int nkb = (kend + BN - 1) / BN;
+
+    floatx4 kpre[C::F4_THREAD], vpre[C::F4_THREAD];
+    auto load_block = [&](int j0) {
+#pragma unroll
+        for (int i = 0; i < C::F4_THREAD; ++i) {
+            const int f = tid + i * C::NW * kWave;
+            const int r = f / C::F4_ROW;
+            const int c4 = f - r * C::F4_ROW;
+            const int key = j0 + r;
+            floatx4 kx = {0.f, 0.f, 0.f, 0.f}, vx = {0.f, 0.f, 0.f, 0.f};
+            if (key < T) {
+                kx = *reinterpret_cast<const floatx4 *>(k + base + int64_t(key) * D + 4 * c4);
+                vx = *reinterpret_cast<const floatx4 *>(v + base + int64_t(key) * D + 4 * c4);
+            }
+            kpre[i] = kx;
+            vpre[i] = vx;
+        }
+    };
+    auto store_block = [&]() {
+#pragma unroll
+        for (int i = 0; i < C::F4_THREAD; ++i) {
+            const int f = tid + i * C::NW * kWave;
+            const int r = f / C::F4_ROW;
+            const int c4 = f - r * C::F4_ROW;
+            *reinterpret_cast<floatx4 *>(&k_lds[r * C::STRIDE + 4 * c4]) = kpre[i];
+            *reinterpret_cast<floatx4 *>(&v_lds[r * C::STRIDE + 4 * c4]) = vpre[i];
+        }
+    };
+
+    load_block(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int j0 = kb * BN;
+        __syncthreads();  // every wave is done reading the previous block
+        store_block();
+        __syncthreads();
+        if (kb + 1 < nkb) load_block(j0 + BN);
+
+        bool active[C::KT];
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            const int t0 = j0 + kt * 32;
+            active[kt] = t0 < T && (!causal || t0 <= wave_last_row);
+        }
+
+        // S^T = K Q^T for each active 32-key tile.
+        floatx16 sacc[C::KT];
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            sacc[kt] = zero16();
+            if (!active[kt]) continue;
+            const float *krow = &k_lds[(kt * 32 + col) * C::STRIDE + 4 * half];
+#pragma unroll
+            for (int m = 0; m < D / 8; ++m) {
+                const floatx4 kv = *reinterpret_cast<const floatx4 *>(krow + 8 * m);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
+            }
+        }
+
+        // Mask, row max.
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
+            const int t0 = j0 + kt * 32;
+            const bool need_mask = (t0 + 31 >= T) || (causal && t0 + 31 > q0 + wave * 32);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float s = sacc[kt][r];
+                if (need_mask) {
+                    const int key = t0 + acc_row(r, half);
+                    if (key >= T || (causal && key > row)) s = -INFINITY;
+                }
+                sacc[kt][r] = s;
+                mloc = fmaxf(mloc, s);
+            }
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+        const float m_new = fmaxf(m_run, mloc);
+        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+        const float resc = fast_exp2(m_run - m_use);
+        float psum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = fast_exp2(sacc[kt][r] - m_use);
+                sacc[kt][r] = p;
+                psum += p;
+            }
+        }
+        l_run = l_run * resc + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) oacc[dt] *= resc;
+
+        // O^T += V^T P^T: the exponentiated S^T registers are the B operand.
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+                for (int s = 0; s < 16; ++s) {
+                    const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::STRIDE + dt * 32 + col];
+                    oacc[dt] = mfma32x32x2(a, sacc[kt][s], oacc[dt]);
+                }
+            }
+        }
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float inv_l = 1.f / l_tot;
+    if (row < T) {
+        float *orow = o + base + int64_t(row) * D;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                floatx4 x;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) x[t] = oacc[dt][4 * g + t] * inv_l;
+                *reinterpret_cast<floatx4 *>(orow + dt * 32 + 8 * g + 4 * half) = x;
+            }
+        }
+        if (lse != nullptr && half == 0) lse[int64_t(bh) * T + row] = (m_run + __log2f(l_tot)) * kLn2;
+    }
+}
+
+template <int D, int BN>
+hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, float *lse,
+                   const AttnShape &s, hipStream_t stream) {
+    using C = FwdCfg<D, BN>;
+    const int64_t nqb = (s.T + C::BM - 1) / C::BM;
+    const int64_t blocks = nqb * s.bh();
+    if (blocks > 2147483647 || s.T > 2147483647 / D)
+        return hipErrorInvalidValue;
+    const float qscale = kLog2e / sqrtf(float(D));
+    hipLaunchKernelGGL((fwd_f32_mfma_kernel<D, BN>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
+                       stream, q, k, v, o, lse, int(s.T), int(s.bh()), int(s.causal), qscale);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool mfma_fwd_supported(int dtype, int64_t d) {
+    if (dtype == 0) return d == 32 || d == 64 || d == 128;
+    return false;
+}
+
+hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
+                           float *lse, const AttnShape &s, hipStream_t stream) {
+    if (dtype != 0) return hipErrorNotSupported;
+    const float *qf = static_cast<const float *>(q);
+    const float *kf = static_cast<const float *>(k);
+    const float *vf = static_cast<const float *>(v);
+    float *of = static_cast<float *>(o);
+    switch (s.d) {
+        case 32: return fwd_f32<32, 64>(qf, kf, vf, of, lse, s, stream);
+        case 64: return fwd_f32<64, 64>(qf, kf, vf, of, lse, s, stream);
+        case 128: return fwd_f32<128, 32>(qf, kf, vf, of, lse, s, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace ctattn

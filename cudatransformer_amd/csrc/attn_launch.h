@@ -1,0 +1,43 @@
+// Internal launcher interface between the C-ABI layer (ctattn_capi.hip) and the kernel
+// translation units.  Every launcher validates nothing (the C-ABI layer already did),
+// enqueues on `stream` and returns hipGetLastError() of its launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ctattn {
+
+struct AttnShape {
+    int64_t B, H, T, d;
+    bool causal;
+    int64_t bh() const { return B * H; }
+    int64_t rows() const { return B * H * T; }
+};
+
+// ---- generic kernels: any 1 <= d <= 256, f32 (dtype 0) or bf16 (dtype 1) ----
+hipError_t launch_generic_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
+                              float *lse, const AttnShape &s, hipStream_t stream);
+hipError_t launch_generic_bwd(int dtype, const void *q, const void *k, const void *v,
+                              const void *o, const void *dout, const float *lse, void *dq,
+                              void *dk, void *dv, float *delta, const AttnShape &s,
+                              hipStream_t stream);
+
+// ---- shared backward preprocess: delta[row] = sum_c dO[row][c] * O[row][c] ----
+hipError_t launch_bwd_preprocess(int dtype, const void *o, const void *dout, float *delta,
+                                 const AttnShape &s, hipStream_t stream);
+
+// ---- MFMA kernels (fp32: d in {32, 64, 128}; bf16: d in {64, 128}) ----
+bool mfma_fwd_supported(int dtype, int64_t d);
+bool mfma_bwd_supported(int dtype, int64_t d);
+hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
+                           float *lse, const AttnShape &s, hipStream_t stream);
+int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s);
+// `delta` must already hold rowsum(dO * O) (launch_bwd_preprocess); `extra` points at
+// mfma_bwd_workspace_bytes() bytes of scratch (256-byte aligned).
+hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
+                           const void *dout, const float *lse, const float *delta, void *dq,
+                           void *dk, void *dv, void *extra, const AttnShape &s,
+                           hipStream_t stream);
+
+}  // namespace ctattn

@@ -1,0 +1,149 @@
+// C-ABI entry points of libctattn.so (declared in include/ctattn.h).
+//
+// Validates arguments on the host before any HIP call, picks the kernel family, launches
+// on the caller's stream and turns failures into (hipError_t, message) pairs.  With the
+// environment variable CTATTN_SYNC_CHECK=1 every entry point also synchronises the stream
+// and reports asynchronous kernel errors (debug mode; off by default).
+#include "attn_launch.h"
+#include "ctattn.h"
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+namespace {
+
+thread_local char g_err[512] = {0};
+std::atomic<int> g_policy{CTATTN_POLICY_AUTO};
+
+int fail(hipError_t code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return int(code);
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return 0;
+}
+
+bool sync_check_enabled() {
+    static const bool on = [] {
+        const char *e = std::getenv("CTATTN_SYNC_CHECK");
+        return e != nullptr && e[0] == '1';
+    }();
+    return on;
+}
+
+// Validates dtype and sizes; returns 0 or an error code (message set).
+int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, int64_t d) {
+    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (B < 0 || H < 0 || T < 0)
+        return fail(hipErrorInvalidValue, "%s: negative size B=%lld H=%lld T=%lld", fn,
+                    (long long)B, (long long)H, (long long)T);
+    if (d < 1 || d > 256)
+        return fail(hipErrorNotSupported, "%s: head dim d=%lld unsupported (1 <= d <= 256)", fn,
+                    (long long)d);
+    // B*H*T must fit a 1-D grid of rows, and B*H*T*d an int64 element offset.
+    const double rows = double(B) * double(H) * double(T);
+    if (rows > 2147483647.0)
+        return fail(hipErrorInvalidValue, "%s: B*H*T = %.0f exceeds 2^31-1", fn, rows);
+    return 0;
+}
+
+int finish(const char *fn, hipError_t e, hipStream_t stream) {
+    if (e != hipSuccess)
+        return fail(e, "%s: kernel launch failed: %s", fn, hipGetErrorString(e));
+    if (sync_check_enabled()) {
+        e = hipStreamSynchronize(stream);
+        if (e == hipSuccess) e = hipGetLastError();
+        if (e != hipSuccess)
+            return fail(e, "%s: kernel execution failed: %s", fn, hipGetErrorString(e));
+    }
+    return ok();
+}
+
+constexpr int64_t kAlign = 256;
+int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool use_mfma_fwd(int dtype, int64_t d) {
+    return g_policy.load() == CTATTN_POLICY_AUTO && ctattn::mfma_fwd_supported(dtype, d);
+}
+bool use_mfma_bwd(int dtype, int64_t d) {
+    return g_policy.load() == CTATTN_POLICY_AUTO && ctattn::mfma_bwd_supported(dtype, d);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, float *lse,
+               int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream) {
+    if (int rc = validate_shape("ctattn_fwd", dtype, B, H, T, d)) return rc;
+    const ctattn::AttnShape s{B, H, T, d, causal != 0};
+    if (s.rows() == 0) return ok();
+    if (!q || !k || !v || !o)
+        return fail(hipErrorInvalidValue, "ctattn_fwd: null q/k/v/o pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = use_mfma_fwd(dtype, d) ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, lse, s, st)
+                                          : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
+    return finish("ctattn_fwd", e, st);
+}
+
+int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
+                                   int causal) {
+    if (validate_shape("ctattn_bwd_workspace_bytes", dtype, B, H, T, d)) return -1;
+    const ctattn::AttnShape s{B, H, T, d, causal != 0};
+    // delta = rowsum(dO * O), fp32 [B, H, T], always first.
+    int64_t bytes = align_up(s.rows() * int64_t(sizeof(float)));
+    if (use_mfma_bwd(dtype, d)) bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s));
+    ok();
+    return bytes;
+}
+
+int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
+               const void *dout, const float *lse, void *dq, void *dk, void *dv,
+               void *workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
+               int64_t d, int causal, void *stream) {
+    if (int rc = validate_shape("ctattn_bwd", dtype, B, H, T, d)) return rc;
+    const ctattn::AttnShape s{B, H, T, d, causal != 0};
+    if (s.rows() == 0) return ok();
+    if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
+        return fail(hipErrorInvalidValue, "ctattn_bwd: null tensor pointer");
+    const int64_t need = ctattn_bwd_workspace_bytes(dtype, B, H, T, d, causal);
+    if (workspace == nullptr || workspace_bytes < need)
+        return fail(hipErrorInvalidValue,
+                    "ctattn_bwd: workspace of %lld bytes given, %lld needed "
+                    "(ctattn_bwd_workspace_bytes)",
+                    (long long)workspace_bytes, (long long)need);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    float *delta = static_cast<float *>(workspace);
+    hipError_t e;
+    if (use_mfma_bwd(dtype, d)) {
+        void *extra = static_cast<char *>(workspace) + align_up(s.rows() * int64_t(sizeof(float)));
+        e = ctattn::launch_bwd_preprocess(dtype, o, dout, delta, s, st);
+        if (e == hipSuccess)
+            e = ctattn::launch_mfma_bwd(dtype, q, k, v, dout, lse, delta, dq, dk, dv, extra, s, st);
+    } else {
+        e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, delta, s, st);
+    }
+    return finish("ctattn_bwd", e, st);
+}
+
+const char *ctattn_last_error(void) { return g_err; }
+
+int ctattn_set_policy(int policy) {
+    if (policy != CTATTN_POLICY_AUTO && policy != CTATTN_POLICY_GENERIC) return -1;
+    return g_policy.exchange(policy);
+}
+
+int ctattn_get_policy(void) { return g_policy.load(); }
+
+int ctattn_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+"""C-ABI boundary checks that need no GPU (CPU only).
+
+libctattn.so must load and export every function include/ctattn.h declares, and the
+host-side validation of every entry point must reject bad arguments before any HIP call
+(so these run in a container without a GPU).
+"""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+from cudatransformer_amd import _capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_capi.LIB_PATH):
+        subprocess.run(["make", "-s", "-j8", "-C", os.path.join(ROOT, "cudatransformer_amd", "csrc")],
+                       check=True)
+    return _capi.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = _capi.header_functions()
+    assert set(names) >= {"ctattn_fwd", "ctattn_bwd", "ctattn_bwd_workspace_bytes",
+                          "ctattn_last_error", "ctattn_set_policy", "ctattn_get_policy",
+                          "ctattn_version"}
+    raw = ctypes.CDLL(_capi.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), f"{n} declared in include/ctattn.h but not exported"
+
+
+def test_version(lib):
+    assert lib.ctattn_version() == 100
+
+
+def test_bad_dtype_rejected(lib):
+    rc = lib.ctattn_fwd(7, 1, 1, 1, 1, None, 1, 1, 8, 64, 0, None)
+    assert rc == 1  # hipErrorInvalidValue
+    assert "unknown dtype" in _capi.last_error()
+
+
+@pytest.mark.parametrize("d", [0, 257, 1024])
+def test_bad_head_dim_rejected(lib, d):
+    rc = lib.ctattn_fwd(0, 1, 1, 1, 1, None, 1, 1, 8, d, 0, None)
+    assert rc == 801  # hipErrorNotSupported
+    assert "head dim" in _capi.last_error()
+
+
+def test_negative_size_rejected(lib):
+    assert lib.ctattn_fwd(0, 1, 1, 1, 1, None, -1, 1, 8, 64, 0, None) == 1
+    assert lib.ctattn_bwd_workspace_bytes(0, 1, -3, 8, 64, 1) == -1
+
+
+def test_too_many_rows_rejected(lib):
+    assert lib.ctattn_fwd(0, 1, 1, 1, 1, None, 1 << 16, 1 << 10, 1 << 10, 64, 0, None) == 1
+    assert "2^31" in _capi.last_error()
+
+
+def test_null_pointers_rejected(lib):
+    assert lib.ctattn_fwd(0, None, 1, 1, 1, None, 1, 1, 8, 64, 0, None) == 1
+    assert "null" in _capi.last_error()
+    assert lib.ctattn_bwd(0, 1, 1, 1, 1, 1, None, 1, 1, 1, 1, 1 << 20, 1, 1, 8, 64, 0, None) == 1
+
+
+def test_empty_problem_is_a_noop(lib):
+    # No element to compute: success without touching the GPU (there is none here).
+    assert lib.ctattn_fwd(0, None, None, None, None, None, 0, 4, 16, 64, 1, None) == 0
+    assert lib.ctattn_fwd(1, None, None, None, None, None, 2, 4, 0, 64, 0, None) == 0
+    assert lib.ctattn_last_error() == b""
+
+
+def test_workspace_size_and_check(lib):
+    prev = _capi.set_policy(_capi.POLICY_GENERIC)
+    try:
+        n = lib.ctattn_bwd_workspace_bytes(0, 2, 3, 100, 48, 1)
+        assert n == ((2 * 3 * 100 * 4 + 255) // 256) * 256
+        rc = lib.ctattn_bwd(0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, n - 1, 2, 3, 100, 48, 1, None)
+        assert rc == 1 and "workspace" in _capi.last_error()
+    finally:
+        _capi.set_policy(prev)
+    n_auto = lib.ctattn_bwd_workspace_bytes(0, 8, 12, 1024, 64, 1)
+    assert n_auto >= 8 * 12 * 1024 * 4
+
+
+def test_policy_roundtrip(lib):
+    prev = _capi.set_policy(_capi.POLICY_GENERIC)
+    assert lib.ctattn_get_policy() == _capi.POLICY_GENERIC
+    _capi.set_policy(prev)
+    assert lib.ctattn_get_policy() == prev
+    with pytest.raises(ValueError):
+        _capi.set_policy(5)
+
+
+def test_no_gpu_call_raises_cleanly(lib):
+    """Without a GPU a real compute call must fail with a message, never crash."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("GPU present: covered by the GPU tests")
+    rc = lib.ctattn_fwd(0, 1, 1, 1, 1, None, 1, 1, 8, 64, 0, None)
+    assert rc != 0
+    assert _capi.last_error() != ""

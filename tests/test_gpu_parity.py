@@ -1,0 +1,186 @@
+"""GPU parity of the ctattn kernels against the fp64 oracle, through the C-ABI.
+
+Tolerances (fixed by the build's target): fp32 max|x - g| <= 1e-4 on each of O, LSE, dQ,
+dK, dV; bf16 max|x - g| / max|g| <= 2e-2 per tensor, g computed from the bf16-rounded
+inputs.  Both kernel families are exercised: POLICY_AUTO (MFMA where supported) and
+POLICY_GENERIC.
+"""
+import glob
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import cudatransformer_amd as ct
+from oracle import attention_fp64 as ora
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+F32_TOL = 1e-4
+BF16_REL_TOL = 2e-2
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(params=[ct.POLICY_AUTO, ct.POLICY_GENERIC], ids=["auto", "generic"])
+def policy(request):
+    prev = ct.set_policy(request.param)
+    yield request.param
+    ct.set_policy(prev)
+
+
+def run_gpu(q, k, v, do, causal, dtype):
+    td = torch.float32 if dtype == "f32" else torch.bfloat16
+    tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(td)
+                       for a in (q, k, v, do))
+    o, lse = ct.flash_attn_fwd(tq, tk, tv, causal)
+    dq, dk, dv = ct.flash_attn_bwd(tq, tk, tv, o, tdo, lse, causal)
+    torch.cuda.synchronize()
+    f = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
+    return {"o": f(o), "lse": f(lse), "dq": f(dq), "dk": f(dk), "dv": f(dv)}
+
+
+def assert_close(got, want, dtype, ctx):
+    for key in ("o", "lse", "dq", "dk", "dv"):
+        g, w = got[key], want[key]
+        assert g.shape == w.shape, (ctx, key)
+        assert np.all(np.isfinite(g)), f"{ctx} {key}: non-finite values"
+        err = float(np.max(np.abs(g - w))) if g.size else 0.0
+        if dtype == "f32":
+            assert err <= F32_TOL, f"{ctx} {key}: max abs err {err:.3e} > {F32_TOL}"
+        else:
+            rel = err / max(float(np.max(np.abs(w))), 1e-30)
+            assert rel <= BF16_REL_TOL, f"{ctx} {key}: rel err {rel:.3e} > {BF16_REL_TOL}"
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=os.path.basename)
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_golden_fixture(path, causal, policy):
+    z = np.load(path)
+    dtype = "bf16" if path.endswith("_bf16.npz") else "f32"
+    tag = "causal" if causal else "full"
+    say(f"golden {os.path.basename(path)} causal={causal} policy={policy}")
+    got = run_gpu(z["q"], z["k"], z["v"], z["do"], causal, dtype)
+    want = {key: z[f"{key}_{tag}"].astype(np.float64) for key in ("o", "lse", "dq", "dk", "dv")}
+    assert_close(got, want, dtype, os.path.basename(path))
+
+
+SHAPES = [
+    (2, 3, 1, 64),
+    (1, 2, 33, 32),
+    (2, 3, 257, 64),
+    (1, 2, 300, 128),
+    (1, 1, 65, 48),
+    (1, 1, 70, 256),
+    (1, 2, 129, 8),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_parity_vs_oracle(shape, causal, dtype, policy):
+    seed = 100 + SHAPES.index(shape)
+    std = 1.0 if dtype == "f32" else 0.5
+    q, k, v, do = ora.make_inputs(shape, seed, std=std, dtype=dtype)
+    say(f"parity shape={shape} causal={causal} dtype={dtype} policy={policy}")
+    got = run_gpu(q, k, v, do, causal, dtype)
+    want = ora.attention_fwd_bwd(q, k, v, do, causal)
+    assert_close(got, want, dtype, f"{shape} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_c2_c3_full_size_f32(causal):
+    """Configs 2/3: B8 H12 T1024 d64 fp32, N(0,1) seed 2 -- fwd and fwd+bwd at full size."""
+    shape = (8, 12, 1024, 64)
+    q, k, v, do = ora.make_inputs(shape, seed=2)
+    say(f"c2/c3 full size causal={causal}")
+    got = run_gpu(q, k, v, do, causal, "f32")
+    want = ora.attention_fwd_bwd(q, k, v, do, causal, chunk_heads=12)
+    assert_close(got, want, "f32", f"c3 causal={causal}")
+
+
+def test_c4_long_context_bf16():
+    """Config 4: B1 H32 T8192 d128 bf16, N(0, 0.5^2) seed 4.  Heads 0 and 31 against the
+    oracle; every head through size-independent invariants."""
+    shape = (1, 32, 8192, 128)
+    q, k, v, do = ora.make_inputs(shape, seed=4, std=0.5, dtype="bf16")
+    say("c4 full size bf16")
+    got = run_gpu(q, k, v, do, True, "bf16")
+    for h in (0, 31):
+        sl = lambda a: a[:, h:h + 1]  # noqa: E731
+        want = ora.attention_fwd_bwd(sl(q), sl(k), sl(v), sl(do), True, chunk_heads=1)
+        assert_close({kk: sl(vv) for kk, vv in got.items()}, want, "bf16", f"c4 head {h}")
+    # sum_j dK_j = 0 and sum_j dV_j = sum_i dO_i per (b, h)
+    scale_k = np.max(np.abs(got["dk"])) * 8192
+    assert np.max(np.abs(got["dk"].sum(axis=2))) <= 2e-2 * scale_k
+    dv_sum = got["dv"].sum(axis=2)
+    do_sum = do.astype(np.float64).sum(axis=2)
+    assert np.max(np.abs(dv_sum - do_sum)) <= 2e-2 * np.max(np.abs(do_sum))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_mfma_matches_generic(causal):
+    shape = (2, 4, 200, 64)
+    q, k, v, do = ora.make_inputs(shape, seed=31)
+    a = run_gpu(q, k, v, do, causal, "f32")
+    prev = ct.set_policy(ct.POLICY_GENERIC)
+    try:
+        b = run_gpu(q, k, v, do, causal, "f32")
+    finally:
+        ct.set_policy(prev)
+    for key in a:
+        assert np.max(np.abs(a[key] - b[key])) <= 5e-5, key
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_backward_is_deterministic(dtype):
+    shape = (2, 3, 300, 64)
+    q, k, v, do = ora.make_inputs(shape, seed=41, dtype=dtype)
+    r1 = run_gpu(q, k, v, do, True, dtype)
+    r2 = run_gpu(q, k, v, do, True, dtype)
+    for key in r1:
+        assert np.array_equal(r1[key], r2[key]), key
+
+
+def test_forward_without_lse():
+    lib = ct._capi.load()
+    q, k, v, _ = (torch.randn(1, 2, 96, 64, device=DEV) for _ in range(4))
+    o = torch.empty_like(q)
+    rc = lib.ctattn_fwd(0, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None,
+                        1, 2, 96, 64, 1, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, ct.last_error()
+    o_ref, _ = ct.flash_attn_fwd(q, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref)
+
+
+def test_autograd_function():
+    q, k, v = (torch.randn(2, 2, 64, 32, device=DEV, requires_grad=True) for _ in range(3))
+    o = ct.flash_attention(q, k, v, True)
+    o.sum().backward()
+    qc, kc, vc = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v))
+    oc = torch.nn.functional.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
+    oc.sum().backward()
+    assert torch.max(torch.abs(o.detach().cpu().double() - oc)) < 1e-4
+    for a, b in ((q, qc), (k, kc), (v, vc)):
+        assert torch.max(torch.abs(a.grad.cpu().double() - b.grad)) < 1e-4
+
+
+def test_invalid_inputs_raise():
+    q = torch.randn(1, 2, 16, 64, device=DEV)
+    with pytest.raises(ValueError):
+        ct.flash_attn_fwd(q, q, q.double())
+    with pytest.raises(ValueError):
+        ct.flash_attn_fwd(q.transpose(1, 2), q.transpose(1, 2), q.transpose(1, 2))
+    lib = ct._capi.load()
+    rc = lib.ctattn_fwd(0, q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(), None,
+                        1, 2, 16, 300, 0, None)
+    assert rc == 801
