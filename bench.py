@@ -6,8 +6,9 @@ B=8 H=12 T=1024 d=64, fp32 (configs[1] is its forward half)
 dO are synthetic N(0, 1) tensors already resident in HBM; outputs, LSE and the backward
 workspace are preallocated, so the timed region is kernels only.
 
-Prints ONE JSON line.  `value` is TFLOP/s by the FA2 convention (fwd 2*B*H*T^2*d with
-causal counted as half of T^2 -> 12.885 GFLOP; fwd+bwd 3.5x -> 45.097 GFLOP per step).
+Prints ONE JSON line.  `value` is TFLOP/s by the FA2 convention: the forward is two
+matmuls of 2*T^2*d flops per (b, h), causal counts half of T^2, so fwd = 2*B*H*T^2*d =
+12.885 GFLOP; the backward is 2.5x that; fwd+bwd = 3.5x -> 45.097 GFLOP per step.
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
 """
@@ -20,7 +21,7 @@ import sys
 
 B, H, T, D = 8, 12, 1024, 64
 CAUSAL = True
-FWD_FLOP = 2.0 * B * H * T * T * D / 2.0  # causal = half of T^2
+FWD_FLOP = 4.0 * B * H * T * T * D / 2.0  # QK^T + PV, 2*T^2*d each; causal = half of T^2
 BWD_FLOP = 2.5 * FWD_FLOP
 STEP_FLOP = FWD_FLOP + BWD_FLOP
 PEAK_F32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
@@ -72,6 +73,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB device copy (rocprofv3 --pmc calibration of "
+                         "FETCH_SIZE / WRITE_SIZE against a known byte count)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -86,6 +90,17 @@ def main():
     import cudatransformer_amd as ct
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 64 << 20  # 64 Mi fp32 = 256 MiB read + 256 MiB written per copy
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": True, "bytes_read_per_copy": 4 * n,
+                          "bytes_written_per_copy": 4 * n, "copies": max(args.steps, 1)}),
+              flush=True)
+        return
     g = torch.Generator(device=dev).manual_seed(2)
     q, k, v, do = (torch.randn((B, H, T, D), generator=g, device=dev, dtype=torch.float32)
                    for _ in range(4))

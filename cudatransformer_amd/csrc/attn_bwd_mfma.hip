@@ -1,17 +1,412 @@
-// fp32 / bf16 flash-attention backward on MFMA (gfx950).  Not yet enabled: the C-ABI
-// routes every backward to the generic kernels while mfma_bwd_supported() is false.
+// fp32 flash-attention backward on fp32 MFMA (gfx950).
+//
+// Replaces the reference backward kernel flashAttentionBackward<float>
+// (flash_attention.cu:226-326) with the same per-element math -- P = exp(S - LSE)
+// (:297-298), dS = P (dP - delta) (:299), dQ = dS K / sqrt(d) (:311) -- but correct dK and
+// dV (dK = dS^T Q / sqrt(d), dV = P^T dO; the reference's :312-313 sum the wrong index),
+// a causal mask, no zero-padded keys, and no atomics on dK / dV.
+//
+// Work decomposition ("key-block major")
+//   * one workgroup = 4 waves owns BN = 128 keys of one (batch, head); wave w owns keys
+//     32w .. 32w+31 and accumulates dK^T and dV^T for them in registers for the whole
+//     kernel -- dK / dV are written exactly once, no atomics.
+//   * the workgroup walks query blocks of BM = 32 rows (causal: only rows >= its first
+//     key).  Q, dO, LSE and delta of the block are staged global -> registers -> LDS; the
+//     next block's loads are issued before this block's MFMAs.
+//   * per wave and query block, with v_mfma_f32_32x32x2f32:
+//       S  = Q K^T      (A = Q from LDS, B = K^T from the LDS K block)
+//       dP = dO V^T     (A = dO from LDS, B = V^T in registers)
+//     In these accumulators each lane holds ONE key (its column) and 16 query rows, so
+//       P  = exp2(S log2(e)/sqrt(d) - LSE log2(e)),  dS = P (dP - delta)
+//     are elementwise, and P / dS are directly the B operands of
+//       dV^T += dO^T P  and  dK^T += Q^T dS     (A = dO / Q columns from LDS).
+//   * dQ needs dS with rows on lanes: each wave writes its dS tile to LDS, then every wave
+//     computes a 32 x (d/4) slice of dQ = dS K over the workgroup's 128 keys with
+//     v_mfma_f32_16x16x4f32 (A = dS rows from LDS, B = K from LDS).  The slice is either
+//     added with fp32 atomics into dq (DqMode::Atomic; dq pre-zeroed by the preprocess
+//     kernel) or stored into a per-key-block partial buffer that a second kernel sums in a
+//     fixed order (DqMode::Partial; deterministic).
 #include "attn_launch.h"
+#include "attn_mfma_common.h"
+
+#include <math.h>
 
 namespace ctattn {
+namespace {
 
-bool mfma_bwd_supported(int, int64_t) { return false; }
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-int64_t mfma_bwd_workspace_bytes(int, const AttnShape &) { return 0; }
+__device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
-hipError_t launch_mfma_bwd(int, const void *, const void *, const void *, const void *,
-                           const float *, const float *, void *, void *, void *, void *,
-                           const AttnShape &, hipStream_t) {
-    return hipErrorNotSupported;
+enum class DqMode { Atomic, Partial };
+
+template <int D>
+struct BwdCfg {
+    static constexpr int NW = 4;              // waves per workgroup
+    static constexpr int BN = 32 * NW;        // keys per workgroup
+    static constexpr int BM = 32;             // query rows per iteration
+    static constexpr int KS = D + 4;          // LDS row stride (floats) for K, Q, dO
+    static constexpr int SS = BN + 4;         // LDS row stride for dS
+    static constexpr int DT = D / 32;         // 32-wide d tiles of dK^T / dV^T
+    static constexpr int F4_ROW = D / 4;
+    static constexpr int QF4 = BM * F4_ROW / (NW * kWave);  // float4 per thread per Q block
+    static constexpr int KF4 = BN * F4_ROW / (NW * kWave);  // float4 per thread for the K block
+    static constexpr int DQ_COLS = D / NW;    // dQ columns per wave
+    static constexpr int DQ_CT = DQ_COLS / 16;  // 16-wide column tiles per wave
+    static_assert(D % 64 == 0, "MFMA backward supports d in {64, 128}");
+    static_assert(QF4 >= 1 && KF4 >= 1, "block load split");
+};
+
+template <int D, DqMode MODE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_f32_mfma_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ dout, const float *__restrict__ lse,
+    const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dq_part,
+    float *__restrict__ dk, float *__restrict__ dv, int T, int BH, int causal, float kscale,
+    float inv_sqrt_d) {
+    using C = BwdCfg<D>;
+    __shared__ __attribute__((aligned(16))) float k_lds[C::BN * C::KS];
+    __shared__ __attribute__((aligned(16))) float q_lds[C::BM * C::KS];
+    __shared__ __attribute__((aligned(16))) float do_lds[C::BM * C::KS];
+    __shared__ __attribute__((aligned(16))) float ds_lds[C::BM * C::SS];
+    __shared__ __attribute__((aligned(16))) float lse_lds[C::BM];  // log2 units
+    __shared__ __attribute__((aligned(16))) float dl_lds[C::BM];   // delta
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int c16 = lane & 15;
+    const int quad = lane >> 4;
+
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    const int kb = id / BH;  // causal: key block 0 has the most query blocks -> launched first
+    const int k0 = kb * C::BN;
+    const int64_t base = int64_t(bh) * T * D;
+    const int64_t rbase = int64_t(bh) * T;
+    const int kw0 = k0 + 32 * wave;
+    const int key = kw0 + col;  // key owned by this lane in S / dP / dK^T / dV^T
+
+    // K block -> LDS (B operand of dQ = dS K).
+#pragma unroll
+    for (int i = 0; i < C::KF4; ++i) {
+        const int f = tid + i * C::NW * kWave;
+        const int r = f / C::F4_ROW;
+        const int c4 = f - r * C::F4_ROW;
+        floatx4 x = {0.f, 0.f, 0.f, 0.f};
+        if (k0 + r < T) x = *reinterpret_cast<const floatx4 *>(k + base + int64_t(k0 + r) * D + 4 * c4);
+        *reinterpret_cast<floatx4 *>(&k_lds[r * C::KS + 4 * c4]) = x;
+    }
+    // V^T as the B operand of dP = dO V^T, held in registers for the whole kernel:
+    // lane (col = key, half) holds V[key][kstep_index(s, half)].  K^T, the B operand of
+    // S = Q K^T, is read from the K block in LDS with the same mapping.
+    float vT[D / 2];
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) {
+        floatx4 vx = {0.f, 0.f, 0.f, 0.f};
+        if (key < T) vx = *reinterpret_cast<const floatx4 *>(v + base + int64_t(key) * D + 8 * m + 4 * half);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) vT[4 * m + t] = vx[t];
+    }
+
+    floatx16 dk_acc[C::DT], dv_acc[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+        dk_acc[dt] = zero16();
+        dv_acc[dt] = zero16();
+    }
+
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int qb_begin = causal ? k0 / C::BM : 0;
+
+    floatx4 qpre[C::QF4], dopre[C::QF4];
+    float lpre = 0.f, dpre = 0.f;
+    auto load_qblock = [&](int r0) {
+#pragma unroll
+        for (int i = 0; i < C::QF4; ++i) {
+            const int f = tid + i * C::NW * kWave;
+            const int r = f / C::F4_ROW;
+            const int c4 = f - r * C::F4_ROW;
+            const int row = r0 + r;
+            floatx4 qx = {0.f, 0.f, 0.f, 0.f}, dx = {0.f, 0.f, 0.f, 0.f};
+            if (row < T) {
+                qx = *reinterpret_cast<const floatx4 *>(q + base + int64_t(row) * D + 4 * c4);
+                dx = *reinterpret_cast<const floatx4 *>(dout + base + int64_t(row) * D + 4 * c4);
+            }
+            qpre[i] = qx;
+            dopre[i] = dx;
+        }
+        if (tid < C::BM) {
+            const int row = r0 + tid;
+            lpre = row < T ? lse[rbase + row] * kLog2e : 0.f;
+            dpre = row < T ? delta[rbase + row] : 0.f;
+        }
+    };
+    auto store_qblock = [&]() {
+#pragma unroll
+        for (int i = 0; i < C::QF4; ++i) {
+            const int f = tid + i * C::NW * kWave;
+            const int r = f / C::F4_ROW;
+            const int c4 = f - r * C::F4_ROW;
+            *reinterpret_cast<floatx4 *>(&q_lds[r * C::KS + 4 * c4]) = qpre[i];
+            *reinterpret_cast<floatx4 *>(&do_lds[r * C::KS + 4 * c4]) = dopre[i];
+        }
+        if (tid < C::BM) {
+            lse_lds[tid] = lpre;
+            dl_lds[tid] = dpre;
+        }
+    };
+
+    if (qb_begin < nqb) load_qblock(qb_begin * C::BM);
+    for (int qb = qb_begin; qb < nqb; ++qb) {
+        const int r0 = qb * C::BM;
+        // All waves are past the previous iteration's dQ phase: q/do/lse/delta/dS are free.
+        __syncthreads();
+        store_qblock();
+        __syncthreads();
+        if (qb + 1 < nqb) load_qblock(r0 + C::BM);
+
+        const bool wave_active = kw0 < T && (!causal || kw0 <= r0 + C::BM - 1);
+        if (wave_active) {
+            floatx16 s = zero16(), dp = zero16();
+#pragma unroll
+            for (int m = 0; m < D / 8; ++m) {
+                const floatx4 qa = *reinterpret_cast<const floatx4 *>(&q_lds[col * C::KS + 8 * m + 4 * half]);
+                const floatx4 da = *reinterpret_cast<const floatx4 *>(&do_lds[col * C::KS + 8 * m + 4 * half]);
+                const floatx4 kb4 = *reinterpret_cast<const floatx4 *>(&k_lds[(32 * wave + col) * C::KS + 8 * m + 4 * half]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    s = mfma32x32x2(qa[t], kb4[t], s);
+                    dp = mfma32x32x2(da[t], vT[4 * m + t], dp);
+                }
+            }
+            const bool need_mask = (r0 + C::BM > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const floatx4 l4 = *reinterpret_cast<const floatx4 *>(&lse_lds[8 * g + 4 * half]);
+                const floatx4 d4 = *reinterpret_cast<const floatx4 *>(&dl_lds[8 * g + 4 * half]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int r = 4 * g + t;
+                    float p = fast_exp2(fmaf(s[r], kscale, -l4[t]));
+                    if (need_mask) {
+                        const int row = r0 + acc_row(r, half);
+                        if (row >= T || key >= T || (causal && key > row)) p = 0.f;
+                    }
+                    s[r] = p;
+                    dp[r] = p * (dp[r] - d4[t]);
+                }
+            }
+            // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over this block's 32 rows)
+#pragma unroll
+            for (int st = 0; st < 16; ++st) {
+                const int rl = kstep_index(st, half);
+#pragma unroll
+                for (int dt = 0; dt < C::DT; ++dt) {
+                    const float a_do = do_lds[rl * C::KS + dt * 32 + col];
+                    const float a_q = q_lds[rl * C::KS + dt * 32 + col];
+                    dv_acc[dt] = mfma32x32x2(a_do, s[st], dv_acc[dt]);
+                    dk_acc[dt] = mfma32x32x2(a_q, dp[st], dk_acc[dt]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
+        }
+        __syncthreads();  // dS of every wave visible
+
+        // dQ[r0 .. r0+31][wave * DQ_COLS ..] = sum over the workgroup's active keys of dS K.
+        floatx4 dq_acc[2][C::DQ_CT];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < C::DQ_CT; ++ct) dq_acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w2 = 0; w2 < C::NW; ++w2) {
+            const int kw2 = k0 + 32 * w2;
+            if (!(kw2 < T && (!causal || kw2 <= r0 + C::BM - 1))) continue;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                const int kl = 32 * w2 + 16 * sb + 4 * quad;  // local key of step t: kl + t
+                floatx4 a[2];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    a[rt] = *reinterpret_cast<const floatx4 *>(&ds_lds[(rt * 16 + c16) * C::SS + kl]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                    for (int ct = 0; ct < C::DQ_CT; ++ct) {
+                        const float b = k_lds[(kl + t) * C::KS + wave * C::DQ_COLS + ct * 16 + c16];
+#pragma unroll
+                        for (int rt = 0; rt < 2; ++rt) dq_acc[rt][ct] = mfma16x16x4(a[rt][t], b, dq_acc[rt][ct]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = r0 + rt * 16 + 4 * quad + r;
+                if (row >= T) continue;
+#pragma unroll
+                for (int ct = 0; ct < C::DQ_CT; ++ct) {
+                    const int c = wave * C::DQ_COLS + ct * 16 + c16;
+                    const float val = dq_acc[rt][ct][r] * inv_sqrt_d;
+                    if constexpr (MODE == DqMode::Atomic) {
+                        unsafeAtomicAdd(dq + base + int64_t(row) * D + c, val);
+                    } else {
+                        dq_part[(int64_t(kb) * BH * T + rbase + row) * D + c] = val;
+                    }
+                }
+            }
+        }
+    }
+
+    // dK = (Q^T dS)^T / sqrt(d), dV = (dO^T P)^T; lane (key, half) holds d = dt*32 + acc_row(r, half).
+    if (key < T) {
+        float *dkr = dk + base + int64_t(key) * D;
+        float *dvr = dv + base + int64_t(key) * D;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                floatx4 xk, xv;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    xk[t] = dk_acc[dt][4 * g + t] * inv_sqrt_d;
+                    xv[t] = dv_acc[dt][4 * g + t];
+                }
+                *reinterpret_cast<floatx4 *>(dkr + dt * 32 + 8 * g + 4 * half) = xk;
+                *reinterpret_cast<floatx4 *>(dvr + dt * 32 + 8 * g + 4 * half) = xv;
+            }
+        }
+    }
+}
+
+// delta[row] = sum_c dO[row][c] * O[row][c] (flash_attention.cu:269-273); also zeroes the
+// dq row when dQ is accumulated with atomics.  One wave per row, d <= 256.
+template <bool ZERO_DQ>
+__global__ __launch_bounds__(256) void bwd_preprocess_f32_kernel(const float *__restrict__ o,
+                                                                const float *__restrict__ dout,
+                                                                float *__restrict__ delta,
+                                                                float *__restrict__ dq,
+                                                                int64_t rows, int d) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;
+    float s = 0.f;
+    for (int c = lane; c < d; c += kWave) {
+        s += o[row * d + c] * dout[row * d + c];
+        if (ZERO_DQ) dq[row * d + c] = 0.f;
+    }
+    s = wave_sum(s);
+    if (lane == 0) delta[row] = s;
+}
+
+// dq[bh][row][:] = sum over key blocks kb <= (causal ? row / BN : nkb - 1) of dq_part[kb][bh][row][:],
+// summed in increasing kb order (deterministic).  One thread per float4.
+template <int D>
+__global__ __launch_bounds__(256) void dq_reduce_kernel(const float *__restrict__ dq_part,
+                                                       float *__restrict__ dq, int T, int BH,
+                                                       int causal, int nkb, int bn) {
+    const int64_t f = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t total = int64_t(BH) * T * (D / 4);
+    if (f >= total) return;
+    const int64_t row_g = f / (D / 4);  // bh * T + row
+    const int row = int(row_g % T);
+    const int last = causal ? row / bn : nkb - 1;
+    const int64_t plane = int64_t(BH) * T * D;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb <= last; ++kb)
+        acc += *reinterpret_cast<const floatx4 *>(dq_part + kb * plane + 4 * f);
+    *reinterpret_cast<floatx4 *>(dq + 4 * f) = acc;
+}
+
+DqMode dq_mode_for(const AttnShape &) {
+#ifdef CTATTN_DQ_PARTIAL_DEFAULT
+    return DqMode::Partial;
+#else
+    return DqMode::Atomic;
+#endif
+}
+
+template <int D>
+hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *o,
+                   const float *dout, const float *lse, float *delta, float *dq, float *dk,
+                   float *dv, float *dq_part, DqMode mode, const AttnShape &s,
+                   hipStream_t stream) {
+    using C = BwdCfg<D>;
+    const int64_t nkb = (s.T + C::BN - 1) / C::BN;
+    const int64_t blocks = nkb * s.bh();
+    if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    const int64_t rows = s.rows();
+    if (mode == DqMode::Atomic) {
+        hipLaunchKernelGGL(bwd_preprocess_f32_kernel<true>, dim3(unsigned((rows + 3) / 4)), dim3(256),
+                           0, stream, o, dout, delta, dq, rows, D);
+    } else {
+        hipLaunchKernelGGL(bwd_preprocess_f32_kernel<false>, dim3(unsigned((rows + 3) / 4)), dim3(256),
+                           0, stream, o, dout, delta, dq, rows, D);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const float kscale = kLog2e / sqrtf(float(D));
+    const float inv_sqrt_d = 1.f / sqrtf(float(D));
+    if (mode == DqMode::Atomic) {
+        hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, DqMode::Atomic>), dim3(unsigned(blocks)),
+                           dim3(C::NW * kWave), 0, stream, q, k, v, dout, lse, delta, dq, dq_part,
+                           dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale, inv_sqrt_d);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, DqMode::Partial>), dim3(unsigned(blocks)),
+                       dim3(C::NW * kWave), 0, stream, q, k, v, dout, lse, delta, dq, dq_part, dk,
+                       dv, int(s.T), int(s.bh()), int(s.causal), kscale, inv_sqrt_d);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t n4 = rows * (D / 4);
+    hipLaunchKernelGGL(dq_reduce_kernel<D>, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, stream,
+                       dq_part, dq, int(s.T), int(s.bh()), int(s.causal), int(nkb), C::BN);
+    return hipGetLastError();
+}
+
+int64_t partial_bytes(const AttnShape &s) {
+    const int64_t nkb = (s.T + 127) / 128;
+    return nkb * s.rows() * s.d * int64_t(sizeof(float));
+}
+
+}  // namespace
+
+bool mfma_bwd_supported(int dtype, int64_t d) {
+    if (dtype == 0) return d == 64 || d == 128;
+    return false;
+}
+
+int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s) {
+    if (dtype != 0) return 0;
+    return dq_mode_for(s) == DqMode::Partial ? partial_bytes(s) : 0;
+}
+
+hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
+                           const void *o, const void *dout, const float *lse, float *delta,
+                           void *dq, void *dk, void *dv, void *extra, const AttnShape &s,
+                           hipStream_t stream) {
+    if (dtype != 0) return hipErrorNotSupported;
+    const DqMode mode = dq_mode_for(s);
+    auto f = [](const void *p) { return static_cast<const float *>(p); };
+    auto g = [](void *p) { return static_cast<float *>(p); };
+    switch (s.d) {
+        case 64:
+            return bwd_f32<64>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
+                               g(extra), mode, s, stream);
+        case 128:
+            return bwd_f32<128>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
+                                g(extra), mode, s, stream);
+        default:
+            return hipErrorNotSupported;
+    }
 }
 
 }  // namespace ctattn

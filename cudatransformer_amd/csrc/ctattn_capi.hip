@@ -126,9 +126,7 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
     hipError_t e;
     if (use_mfma_bwd(dtype, d)) {
         void *extra = static_cast<char *>(workspace) + align_up(s.rows() * int64_t(sizeof(float)));
-        e = ctattn::launch_bwd_preprocess(dtype, o, dout, delta, s, st);
-        if (e == hipSuccess)
-            e = ctattn::launch_mfma_bwd(dtype, q, k, v, dout, lse, delta, dq, dk, dv, extra, s, st);
+        e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, lse, delta, dq, dk, dv, extra, s, st);
     } else {
         e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, delta, s, st);
     }
