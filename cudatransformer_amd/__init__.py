@@ -16,6 +16,7 @@ from ._capi import (  # noqa: E402
     BF16,
     F32,
     POLICY_AUTO,
+    POLICY_DETERMINISTIC,
     POLICY_GENERIC,
     FlashAttentionFunction,
     bwd_workspace_bytes,
@@ -30,6 +31,7 @@ __all__ = [
     "BF16",
     "F32",
     "POLICY_AUTO",
+    "POLICY_DETERMINISTIC",
     "POLICY_GENERIC",
     "FlashAttentionFunction",
     "bwd_workspace_bytes",

@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(_HERE, "libctattn.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "ctattn.h")
 
 F32, BF16 = 0, 1
-POLICY_AUTO, POLICY_GENERIC = 0, 1
+POLICY_AUTO, POLICY_GENERIC, POLICY_DETERMINISTIC = 0, 1, 2
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16}
 
 _lib = None

@@ -59,6 +59,61 @@ struct BwdCfg {
     static_assert(QF4 >= 1 && KF4 >= 1, "block load split");
 };
 
+// S, dP, P, dS and the dV^T / dK^T updates of one wave for one query block, then dS -> LDS.
+// MASK selects the diagonal / sequence-end variant (per-element causal and bounds checks);
+// the unmasked variant carries none.
+template <int D, bool MASK>
+__device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32],
+                                               const float (&vT)[D / 2], const float *q_lds,
+                                               const float *do_lds, const float *k_lds,
+                                               const float *lse_lds, const float *dl_lds,
+                                               float *ds_lds, int r0, int key, int T, int causal,
+                                               float kscale, int wave, int col, int half) {
+    using C = BwdCfg<D>;
+    floatx16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) {
+        const floatx4 qa = *reinterpret_cast<const floatx4 *>(&q_lds[col * C::KS + 8 * m + 4 * half]);
+        const floatx4 da = *reinterpret_cast<const floatx4 *>(&do_lds[col * C::KS + 8 * m + 4 * half]);
+        const floatx4 kb4 = *reinterpret_cast<const floatx4 *>(&k_lds[(32 * wave + col) * C::KS + 8 * m + 4 * half]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            s = mfma32x32x2(qa[t], kb4[t], s);
+            dp = mfma32x32x2(da[t], vT[4 * m + t], dp);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const floatx4 l4 = *reinterpret_cast<const floatx4 *>(&lse_lds[8 * g + 4 * half]);
+        const floatx4 d4 = *reinterpret_cast<const floatx4 *>(&dl_lds[8 * g + 4 * half]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int r = 4 * g + t;
+            float p = fast_exp2(fmaf(s[r], kscale, -l4[t]));
+            if (MASK) {
+                const int row = r0 + acc_row(r, half);
+                p = (row >= T || key >= T || (causal && key > row)) ? 0.f : p;
+            }
+            s[r] = p;
+            dp[r] = p * (dp[r] - d4[t]);
+        }
+    }
+    // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over this block's 32 rows)
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+        const int rl = kstep_index(st, half);
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+            const float a_do = do_lds[rl * C::KS + dt * 32 + col];
+            const float a_q = q_lds[rl * C::KS + dt * 32 + col];
+            dv_acc[dt] = mfma32x32x2(a_do, s[st], dv_acc[dt]);
+            dk_acc[dt] = mfma32x32x2(a_q, dp[st], dk_acc[dt]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
+}
+
 template <int D, DqMode MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_f32_mfma_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -164,57 +219,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (qb_begin < nqb) load_qblock(qb_begin * C::BM);
     for (int qb = qb_begin; qb < nqb; ++qb) {
         const int r0 = qb * C::BM;
-        // All waves are past the previous iteration's dQ phase: q/do/lse/delta/dS are free.
-        __syncthreads();
+        // q/do/lse/delta of the previous block were last read before the previous dQ-phase
+        // barrier, so they can be overwritten without another barrier; ds_lds is only
+        // rewritten after the barrier below, which every wave reaches after its dQ phase.
         store_qblock();
         __syncthreads();
         if (qb + 1 < nqb) load_qblock(r0 + C::BM);
 
         const bool wave_active = kw0 < T && (!causal || kw0 <= r0 + C::BM - 1);
         if (wave_active) {
-            floatx16 s = zero16(), dp = zero16();
-#pragma unroll
-            for (int m = 0; m < D / 8; ++m) {
-                const floatx4 qa = *reinterpret_cast<const floatx4 *>(&q_lds[col * C::KS + 8 * m + 4 * half]);
-                const floatx4 da = *reinterpret_cast<const floatx4 *>(&do_lds[col * C::KS + 8 * m + 4 * half]);
-                const floatx4 kb4 = *reinterpret_cast<const floatx4 *>(&k_lds[(32 * wave + col) * C::KS + 8 * m + 4 * half]);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    s = mfma32x32x2(qa[t], kb4[t], s);
-                    dp = mfma32x32x2(da[t], vT[4 * m + t], dp);
-                }
-            }
-            const bool need_mask = (r0 + C::BM > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0);
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const floatx4 l4 = *reinterpret_cast<const floatx4 *>(&lse_lds[8 * g + 4 * half]);
-                const floatx4 d4 = *reinterpret_cast<const floatx4 *>(&dl_lds[8 * g + 4 * half]);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int r = 4 * g + t;
-                    float p = fast_exp2(fmaf(s[r], kscale, -l4[t]));
-                    if (need_mask) {
-                        const int row = r0 + acc_row(r, half);
-                        if (row >= T || key >= T || (causal && key > row)) p = 0.f;
-                    }
-                    s[r] = p;
-                    dp[r] = p * (dp[r] - d4[t]);
-                }
-            }
-            // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over this block's 32 rows)
-#pragma unroll
-            for (int st = 0; st < 16; ++st) {
-                const int rl = kstep_index(st, half);
-#pragma unroll
-                for (int dt = 0; dt < C::DT; ++dt) {
-                    const float a_do = do_lds[rl * C::KS + dt * 32 + col];
-                    const float a_q = q_lds[rl * C::KS + dt * 32 + col];
-                    dv_acc[dt] = mfma32x32x2(a_do, s[st], dv_acc[dt]);
-                    dk_acc[dt] = mfma32x32x2(a_q, dp[st], dk_acc[dt]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
+            const bool masked = (r0 + C::BM > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0);
+            if (masked)
+                bwd_wave_block<D, true>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
+                                        ds_lds, r0, key, T, causal, kscale, wave, col, half);
+            else
+                bwd_wave_block<D, false>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
+                                         ds_lds, r0, key, T, causal, kscale, wave, col, half);
         }
         __syncthreads();  // dS of every wave visible
 
@@ -326,14 +346,6 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float *__restrict_
     *reinterpret_cast<floatx4 *>(dq + 4 * f) = acc;
 }
 
-DqMode dq_mode_for(const AttnShape &) {
-#ifdef CTATTN_DQ_PARTIAL_DEFAULT
-    return DqMode::Partial;
-#else
-    return DqMode::Atomic;
-#endif
-}
-
 template <int D>
 hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *o,
                    const float *dout, const float *lse, float *delta, float *dq, float *dk,
@@ -384,17 +396,17 @@ bool mfma_bwd_supported(int dtype, int64_t d) {
     return false;
 }
 
-int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s) {
+int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic) {
     if (dtype != 0) return 0;
-    return dq_mode_for(s) == DqMode::Partial ? partial_bytes(s) : 0;
+    return deterministic ? partial_bytes(s) : 0;
 }
 
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
                            const void *o, const void *dout, const float *lse, float *delta,
-                           void *dq, void *dk, void *dv, void *extra, const AttnShape &s,
-                           hipStream_t stream) {
+                           void *dq, void *dk, void *dv, void *extra, bool deterministic,
+                           const AttnShape &s, hipStream_t stream) {
     if (dtype != 0) return hipErrorNotSupported;
-    const DqMode mode = dq_mode_for(s);
+    const DqMode mode = deterministic ? DqMode::Partial : DqMode::Atomic;
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };
     switch (s.d) {

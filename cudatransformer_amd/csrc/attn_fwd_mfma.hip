@@ -16,9 +16,12 @@
 //     so the online-softmax row statistics need a single cross-lane exchange (lane ^ 32)
 //     and, after exponentiation, the accumulator registers ARE the B operand of
 //     O^T += V^T P^T without any data movement.
-//   * the running max/denominator are kept in log2 units; exp is v_exp_f32.
-//   * causal: key tiles that lie wholly above a wave's diagonal are skipped (no MFMA);
-//     workgroups are ordered longest-first so the tail of the grid is short.
+//   * the running max/denominator are kept in log2 units; exp is v_exp_f32.  O and l are
+//     rescaled lazily: only when the row max grows by more than 2^8.
+//   * each block runs one of two wave-uniform variants: the unmasked one (no per-element
+//     checks) for blocks wholly below the wave's diagonal and inside the sequence, the
+//     masked one otherwise.  Key tiles wholly above a wave's diagonal are skipped (no
+//     MFMA); causal workgroups are ordered longest-first so the tail of the grid is short.
 #include "attn_launch.h"
 #include "attn_mfma_common.h"
 
@@ -40,8 +43,107 @@ struct FwdCfg {
     static_assert((BN * F4_ROW) % (NW * kWave) == 0, "tile load split");
 };
 
+// Lazy online-softmax rescaling: the running row max m (log2 units) is only raised when a
+// block's max exceeds it by more than this, so most blocks skip rescaling O and l.  Scores
+// are then exponentiated against a max that may be stale by up to 2^8 -- no overflow risk in
+// fp32 -- and O / l and LSE = m + log2(l) use the same m, so the result is unchanged.
+constexpr float kRescaleThreshold = 8.0f;
+
+// Per-wave state of the forward key loop.
+template <int D>
+struct FwdState {
+    floatx16 oacc[D / 32];  // O^T accumulators: lane (col=row, half) holds d = dt*32 + acc_row(r, half)
+    float m_run;            // running row max (log2 units), identical in both halves
+    float l_run;            // this half's share of the running denominator
+};
+
+// One BN-key block for one wave.  MASK selects the diagonal / sequence-end variant: it skips
+// key tiles wholly above the wave's diagonal and masks keys > row or >= T; the unmasked
+// variant carries no per-element checks.
+template <int D, int BN, bool MASK>
+__device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D / 2],
+                                          const float *k_lds, const float *v_lds, int j0,
+                                          int row, int wave_first_row, int wave_last_row,
+                                          int T, int causal, int col, int half) {
+    using C = FwdCfg<D, BN>;
+    bool active[C::KT];
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt) {
+        const int t0 = j0 + kt * 32;
+        active[kt] = !MASK || (t0 < T && (!causal || t0 <= wave_last_row));
+    }
+
+    // S^T = K Q^T for each active 32-key tile.
+    floatx16 sacc[C::KT];
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt) {
+        sacc[kt] = zero16();
+        if (!active[kt]) continue;
+        const float *krow = &k_lds[(kt * 32 + col) * C::STRIDE + 4 * half];
+#pragma unroll
+        for (int m = 0; m < D / 8; ++m) {
+            const floatx4 kv = *reinterpret_cast<const floatx4 *>(krow + 8 * m);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
+        }
+    }
+
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt) {
+        if (!active[kt]) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float s = sacc[kt][r];
+            if (MASK) {
+                const int key = j0 + kt * 32 + acc_row(r, half);
+                s = (key >= T || (causal && key > row)) ? -INFINITY : s;
+                sacc[kt][r] = s;
+            }
+            mloc = fmaxf(mloc, s);
+        }
+    }
+    (void)wave_first_row;
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+    // Raise the running max only when it grew by more than the threshold somewhere.
+    if (__any(mloc > st.m_run + kRescaleThreshold)) {
+        const float m_new = fmaxf(st.m_run, mloc);
+        const float resc = fast_exp2(st.m_run - m_new);  // 0 on the first block (m_run = -inf)
+        st.m_run = m_new;
+        st.l_run *= resc;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) st.oacc[dt] *= resc;
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt) {
+        if (!active[kt]) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = fast_exp2(sacc[kt][r] - st.m_run);
+            sacc[kt][r] = p;
+            psum += p;
+        }
+    }
+    st.l_run += psum;
+
+    // O^T += V^T P^T: the exponentiated S^T registers are the B operand.
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt) {
+        if (!active[kt]) continue;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::STRIDE + dt * 32 + col];
+                st.oacc[dt] = mfma32x32x2(a, sacc[kt][s], st.oacc[dt]);
+            }
+        }
+    }
+}
+
 template <int D, int BN>
-__global__ __launch_bounds__(256) void fwd_f32_mfma_kernel(const float *__restrict__ q,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_f32_mfma_kernel(const float *__restrict__ q,
                                                           const float *__restrict__ k,
                                                           const float *__restrict__ v,
                                                           float *__restrict__ o,
@@ -64,7 +166,8 @@ __global__ __launch_bounds__(256) void fwd_f32_mfma_kernel(const float *__restri
     const int64_t base = int64_t(bh) * T * D;
     const int q0 = qb * C::BM;
     const int row = q0 + wave * 32 + col;  // query row owned by this lane
-    const int wave_last_row = q0 + wave * 32 + 31;
+    const int wave_first_row = q0 + wave * 32;
+    const int wave_last_row = wave_first_row + 31;
 
     // Q^T as the B operand: lane (col=row, half) holds Q[row][kstep_index(s, half)].
     float qreg[D / 2];
@@ -76,11 +179,11 @@ __global__ __launch_bounds__(256) void fwd_f32_mfma_kernel(const float *__restri
         for (int t = 0; t < 4; ++t) qreg[4 * m + t] = x[t] * qscale;
     }
 
-    floatx16 oacc[C::DT];
+    FwdState<D> st;
 #pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) oacc[dt] = zero16();
-    float m_run = -INFINITY;  // running row max (log2 units), same in both halves
-    float l_run = 0.f;        // this half's share of the running denominator
+    for (int dt = 0; dt < C::DT; ++dt) st.oacc[dt] = zero16();
+    st.m_run = -INFINITY;
+    st.l_run = 0.f;
 
     const int kend = causal ? min(T, q0 + C::BM) : T;
     const int nkb = (kend + BN - 1) / BN;
@@ -121,82 +224,19 @@ __global__ __launch_bounds__(256) void fwd_f32_mfma_kernel(const float *__restri
         __syncthreads();
         if (kb + 1 < nkb) load_block(j0 + BN);
 
-        bool active[C::KT];
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-            const int t0 = j0 + kt * 32;
-            active[kt] = t0 < T && (!causal || t0 <= wave_last_row);
-        }
-
-        // S^T = K Q^T for each active 32-key tile.
-        floatx16 sacc[C::KT];
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-            sacc[kt] = zero16();
-            if (!active[kt]) continue;
-            const float *krow = &k_lds[(kt * 32 + col) * C::STRIDE + 4 * half];
-#pragma unroll
-            for (int m = 0; m < D / 8; ++m) {
-                const floatx4 kv = *reinterpret_cast<const floatx4 *>(krow + 8 * m);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
-            }
-        }
-
-        // Mask, row max.
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-            if (!active[kt]) continue;
-            const int t0 = j0 + kt * 32;
-            const bool need_mask = (t0 + 31 >= T) || (causal && t0 + 31 > q0 + wave * 32);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float s = sacc[kt][r];
-                if (need_mask) {
-                    const int key = t0 + acc_row(r, half);
-                    if (key >= T || (causal && key > row)) s = -INFINITY;
-                }
-                sacc[kt][r] = s;
-                mloc = fmaxf(mloc, s);
-            }
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-        const float m_new = fmaxf(m_run, mloc);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float resc = fast_exp2(m_run - m_use);
-        float psum = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-            if (!active[kt]) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = fast_exp2(sacc[kt][r] - m_use);
-                sacc[kt][r] = p;
-                psum += p;
-            }
-        }
-        l_run = l_run * resc + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) oacc[dt] *= resc;
-
-        // O^T += V^T P^T: the exponentiated S^T registers are the B operand.
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-            if (!active[kt]) continue;
-#pragma unroll
-            for (int dt = 0; dt < C::DT; ++dt) {
-#pragma unroll
-                for (int s = 0; s < 16; ++s) {
-                    const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::STRIDE + dt * 32 + col];
-                    oacc[dt] = mfma32x32x2(a, sacc[kt][s], oacc[dt]);
-                }
-            }
+        // Wave-uniform: does this block touch the diagonal or the sequence end for this wave?
+        const bool masked = (j0 + BN > T) || (causal && j0 + BN - 1 > wave_first_row);
+        if (masked) {
+            if (!causal || j0 <= wave_last_row)
+                fwd_block<D, BN, true>(st, qreg, k_lds, v_lds, j0, row, wave_first_row,
+                                       wave_last_row, T, causal, col, half);
+        } else {
+            fwd_block<D, BN, false>(st, qreg, k_lds, v_lds, j0, row, wave_first_row,
+                                    wave_last_row, T, causal, col, half);
         }
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float l_tot = st.l_run + __shfl_xor(st.l_run, 32, kWave);
     const float inv_l = 1.f / l_tot;
     if (row < T) {
         float *orow = o + base + int64_t(row) * D;
@@ -206,11 +246,11 @@ __global__ __launch_bounds__(256) void fwd_f32_mfma_kernel(const float *__restri
             for (int g = 0; g < 4; ++g) {
                 floatx4 x;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) x[t] = oacc[dt][4 * g + t] * inv_l;
+                for (int t = 0; t < 4; ++t) x[t] = st.oacc[dt][4 * g + t] * inv_l;
                 *reinterpret_cast<floatx4 *>(orow + dt * 32 + 8 * g + 4 * half) = x;
             }
         }
-        if (lse != nullptr && half == 0) lse[int64_t(bh) * T + row] = (m_run + __log2f(l_tot)) * kLn2;
+        if (lse != nullptr && half == 0) lse[int64_t(bh) * T + row] = (st.m_run + __log2f(l_tot)) * kLn2;
     }
 }
 

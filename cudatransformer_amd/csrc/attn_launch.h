@@ -32,13 +32,15 @@ bool mfma_fwd_supported(int dtype, int64_t d);
 bool mfma_bwd_supported(int dtype, int64_t d);
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
                            float *lse, const AttnShape &s, hipStream_t stream);
-int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s);
+// `deterministic` selects the ordered dQ reduction (per-key-block partials in the workspace)
+// instead of fp32 atomics.
+int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic);
 // Runs the whole MFMA backward: its own preprocess (delta = rowsum(dO * O) into `delta`,
 // fp32 [B, H, T]) and the main kernel(s).  `extra` points at mfma_bwd_workspace_bytes()
 // bytes of scratch (256-byte aligned).
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
                            const void *o, const void *dout, const float *lse, float *delta,
-                           void *dq, void *dk, void *dv, void *extra, const AttnShape &s,
-                           hipStream_t stream);
+                           void *dq, void *dk, void *dv, void *extra, bool deterministic,
+                           const AttnShape &s, hipStream_t stream);
 
 }  // namespace ctattn

@@ -72,11 +72,12 @@ constexpr int64_t kAlign = 256;
 int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 bool use_mfma_fwd(int dtype, int64_t d) {
-    return g_policy.load() == CTATTN_POLICY_AUTO && ctattn::mfma_fwd_supported(dtype, d);
+    return g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::mfma_fwd_supported(dtype, d);
 }
 bool use_mfma_bwd(int dtype, int64_t d) {
-    return g_policy.load() == CTATTN_POLICY_AUTO && ctattn::mfma_bwd_supported(dtype, d);
+    return g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::mfma_bwd_supported(dtype, d);
 }
+bool deterministic_policy() { return g_policy.load() == CTATTN_POLICY_DETERMINISTIC; }
 
 }  // namespace
 
@@ -101,7 +102,8 @@ int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, i
     const ctattn::AttnShape s{B, H, T, d, causal != 0};
     // delta = rowsum(dO * O), fp32 [B, H, T], always first.
     int64_t bytes = align_up(s.rows() * int64_t(sizeof(float)));
-    if (use_mfma_bwd(dtype, d)) bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s));
+    if (use_mfma_bwd(dtype, d))
+        bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s, deterministic_policy()));
     ok();
     return bytes;
 }
@@ -126,7 +128,8 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
     hipError_t e;
     if (use_mfma_bwd(dtype, d)) {
         void *extra = static_cast<char *>(workspace) + align_up(s.rows() * int64_t(sizeof(float)));
-        e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, lse, delta, dq, dk, dv, extra, s, st);
+        e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, lse, delta, dq, dk, dv, extra,
+                                    deterministic_policy(), s, st);
     } else {
         e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, delta, s, st);
     }
@@ -136,7 +139,9 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
 const char *ctattn_last_error(void) { return g_err; }
 
 int ctattn_set_policy(int policy) {
-    if (policy != CTATTN_POLICY_AUTO && policy != CTATTN_POLICY_GENERIC) return -1;
+    if (policy != CTATTN_POLICY_AUTO && policy != CTATTN_POLICY_GENERIC &&
+        policy != CTATTN_POLICY_DETERMINISTIC)
+        return -1;
     return g_policy.exchange(policy);
 }
 

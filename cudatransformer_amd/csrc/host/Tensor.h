@@ -1,0 +1,202 @@
+// Tensor<DType>: a shape plus a shared device buffer, the allocation / transfer part of the
+// reference's Tensor (Tensor.cu:11-285, headers.cu:195-237).
+//
+// Same ownership model as the reference: copies are shallow (shared_ptr to the device
+// buffer, Tensor.cu:73-113), clone() is deep, constructors zero-fill (Tensor.cu:27-55).
+// Different mechanics: buffers come from the stream-ordered allocator (hipMallocAsync /
+// hipFreeAsync) and fills / copies are enqueued on the one runtime stream, instead of
+// cudaMalloc + fill kernel + cudaDeviceSynchronize per allocation (headers.cu:195-215).  The
+// host waits only when data comes back to the CPU (numpy(), item()) or after an upload from
+// pageable memory (fromPointer()).
+//
+// DType is float or bf16 (stored as its 16-bit pattern).  The reference's tensor algebra
+// (Tensor.cu:290-958) is not part of this path.
+#pragma once
+
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "Runtime.h"
+
+namespace ct {
+
+// bfloat16 storage type (upper half of an IEEE binary32).
+struct bf16 {
+    uint16_t bits = 0;
+    static bf16 fromFloat(float f) {
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        bf16 b;
+        if ((u & 0x7fffffffu) > 0x7f800000u) {
+            b.bits = uint16_t((u >> 16) | 0x40);  // quiet NaN
+        } else {
+            u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
+            b.bits = uint16_t(u >> 16);
+        }
+        return b;
+    }
+    float toFloat() const {
+        uint32_t u = uint32_t(bits) << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        return f;
+    }
+};
+
+template <typename DType> struct DTypeCode;
+template <> struct DTypeCode<float> { static constexpr int value = CTATTN_F32; };
+template <> struct DTypeCode<bf16> { static constexpr int value = CTATTN_BF16; };
+
+template <typename DType> inline DType fromFloat(float x);
+template <> inline float fromFloat<float>(float x) { return x; }
+template <> inline bf16 fromFloat<bf16>(float x) { return bf16::fromFloat(x); }
+inline float toFloat(float x) { return x; }
+inline float toFloat(bf16 x) { return x.toFloat(); }
+
+// Stream-ordered device allocation with a stream-ordered free as deleter.
+template <typename T>
+std::shared_ptr<T[]> deviceAlloc(size_t count) {
+    if (count == 0) return nullptr;
+    void *p = nullptr;
+    hipCheck(hipMallocAsync(&p, count * sizeof(T), Runtime::stream()), "hipMallocAsync");
+    return std::shared_ptr<T[]>(static_cast<T *>(p), [](T *q) { (void)hipFreeAsync(q, Runtime::stream()); });
+}
+
+template <typename DType = float>
+class Tensor {
+public:
+    Tensor() = default;
+
+    // Zero-initialised tensor of the given shape (Tensor.cu:36-43).
+    explicit Tensor(const std::vector<size_t> &shape, float value = 0.f) : shape_(shape) {
+        if (shape_.size() > 8) throw std::invalid_argument("Tensor does not support more than 8 dimensions");
+        size_ = std::accumulate(shape_.begin(), shape_.end(), size_t(1), std::multiplies<size_t>());
+        data_ = deviceAlloc<DType>(size_);
+        fill(value);
+    }
+
+    // Uninitialised tensor, for outputs a kernel overwrites completely.
+    static Tensor empty(const std::vector<size_t> &shape) {
+        Tensor t;
+        if (shape.size() > 8) throw std::invalid_argument("Tensor does not support more than 8 dimensions");
+        t.shape_ = shape;
+        t.size_ = std::accumulate(shape.begin(), shape.end(), size_t(1), std::multiplies<size_t>());
+        t.data_ = deviceAlloc<DType>(t.size_);
+        return t;
+    }
+
+    // Shallow wrap of an existing buffer (Tensor.cu:62-66).
+    Tensor(std::shared_ptr<DType[]> data, const std::vector<size_t> &shape) : shape_(shape) {
+        size_ = std::accumulate(shape_.begin(), shape_.end(), size_t(1), std::multiplies<size_t>());
+        data_ = std::move(data);
+    }
+
+    // Copies host values (in this DType's layout) into a new device tensor.
+    static Tensor fromPointer(const std::vector<size_t> &shape, const DType *host) {
+        Tensor t = empty(shape);
+        if (t.size_ > 0) {
+            hipCheck(hipMemcpyAsync(t.data_.get(), host, t.size_ * sizeof(DType), hipMemcpyHostToDevice,
+                                    Runtime::stream()),
+                     "hipMemcpyAsync H2D");
+            Runtime::synchronize();  // `host` may be released as soon as we return
+        }
+        return t;
+    }
+
+    // Converts float host values to DType (round to nearest even for bf16) and uploads.
+    static Tensor fromFloats(const std::vector<size_t> &shape, const float *host) {
+        const size_t n = std::accumulate(shape.begin(), shape.end(), size_t(1), std::multiplies<size_t>());
+        if constexpr (std::is_same_v<DType, float>) {
+            return fromPointer(shape, host);
+        } else {
+            std::vector<DType> tmp(n);
+            for (size_t i = 0; i < n; ++i) tmp[i] = fromFloat<DType>(host[i]);
+            return fromPointer(shape, tmp.data());
+        }
+    }
+
+    // Device values as floats on the host (waits for the stream).
+    std::vector<float> toFloats() const {
+        std::vector<DType> raw(size_);
+        if (size_ > 0) {
+            hipCheck(hipMemcpyAsync(raw.data(), data_.get(), size_ * sizeof(DType), hipMemcpyDeviceToHost,
+                                    Runtime::stream()),
+                     "hipMemcpyAsync D2H");
+            Runtime::synchronize();
+        }
+        std::vector<float> out(size_);
+        for (size_t i = 0; i < size_; ++i) out[i] = toFloat(raw[i]);
+        return out;
+    }
+
+    // Deep copy (Tensor.cu:119-123, headers.cu:224-237), stream-ordered D2D.
+    Tensor clone() const {
+        Tensor t;
+        t.shape_ = shape_;
+        t.size_ = size_;
+        t.data_ = deviceAlloc<DType>(size_);
+        if (size_ > 0)
+            hipCheck(hipMemcpyAsync(t.data_.get(), data_.get(), size_ * sizeof(DType), hipMemcpyDeviceToDevice,
+                                    Runtime::stream()),
+                     "hipMemcpyAsync D2D");
+        return t;
+    }
+
+    // Fills every element with `value` (Tensor.cu:360).  Zero is a stream-ordered memset;
+    // other values are staged on the host.
+    void fill(float value) {
+        if (size_ == 0) return;
+        const DType v = fromFloat<DType>(value);
+        uint8_t first;
+        std::memcpy(&first, &v, 1);
+        bool bytewise = true;
+        for (size_t b = 0; b < sizeof(DType); ++b)
+            bytewise = bytewise && reinterpret_cast<const uint8_t *>(&v)[b] == first;
+        if (bytewise) {
+            hipCheck(hipMemsetAsync(data_.get(), first, size_ * sizeof(DType), Runtime::stream()), "hipMemsetAsync");
+        } else {
+            std::vector<DType> tmp(size_, v);
+            hipCheck(hipMemcpyAsync(data_.get(), tmp.data(), size_ * sizeof(DType), hipMemcpyHostToDevice,
+                                    Runtime::stream()),
+                     "hipMemcpyAsync fill");
+            Runtime::synchronize();
+        }
+    }
+
+    // Shallow reshape (Tensor.cu:547-570).
+    Tensor reshape(const std::vector<size_t> &shape) const {
+        const size_t n = std::accumulate(shape.begin(), shape.end(), size_t(1), std::multiplies<size_t>());
+        if (n != size_) throw std::invalid_argument("reshape: element count changes");
+        return Tensor(data_, shape);
+    }
+
+    float item() const {
+        if (size_ != 1) throw std::runtime_error("Tensor is not a scalar");
+        return toFloats()[0];
+    }
+
+    const std::vector<size_t> &shape() const { return shape_; }
+    size_t shape(size_t dim) const {
+        if (dim >= shape_.size()) throw std::invalid_argument("Invalid dimension");
+        return shape_[dim];
+    }
+    size_t size() const { return size_; }
+    size_t nDim() const { return shape_.size(); }
+    DType *get() const { return data_.get(); }
+    DType *data() { return data_.get(); }
+    const DType *data() const { return data_.get(); }
+    std::shared_ptr<DType[]> dataPtr() const { return data_; }
+    bool empty() const { return data_ == nullptr; }
+
+private:
+    std::vector<size_t> shape_;
+    size_t size_ = 0;
+    std::shared_ptr<DType[]> data_;
+};
+
+}  // namespace ct

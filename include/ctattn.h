@@ -34,9 +34,18 @@ extern "C" {
 
 enum ctattn_dtype { CTATTN_F32 = 0, CTATTN_BF16 = 1 };
 
-/* Kernel selection policy (process-wide).  AUTO picks the MFMA kernels where they apply;
- * GENERIC forces the generic kernels (used to cross-check the two paths). */
-enum ctattn_policy { CTATTN_POLICY_AUTO = 0, CTATTN_POLICY_GENERIC = 1 };
+/* Kernel selection policy (process-wide).
+ *   AUTO           MFMA kernels where they apply (fastest).  The MFMA backward adds dQ
+ *                  contributions of different key blocks with fp32 atomics, so dQ may
+ *                  differ between runs in the last bits; dK, dV, O and LSE do not.
+ *   GENERIC        the generic kernels only (used to cross-check the two paths).
+ *   DETERMINISTIC  MFMA kernels, with dQ summed over key blocks in a fixed order through a
+ *                  workspace buffer: bitwise-reproducible gradients, larger workspace. */
+enum ctattn_policy {
+    CTATTN_POLICY_AUTO = 0,
+    CTATTN_POLICY_GENERIC = 1,
+    CTATTN_POLICY_DETERMINISTIC = 2
+};
 
 /*
  * Forward: O = softmax(Q K^T / sqrt(d)) V and LSE.
@@ -62,8 +71,8 @@ int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, i
  * Replaces the flashAttentionBackward<DType> launch of FlashAttentionLayer::computeBackward
  * (reference FlashAttentionLayer.cu:129-140; kernel flash_attention.cu:226-326).
  * dq, dk, dv are fully overwritten (no pre-zeroing needed).  workspace must hold at least
- * ctattn_bwd_workspace_bytes(...) bytes (it may be NULL when that is 0).  Deterministic:
- * the same inputs give bitwise-identical gradients.
+ * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy.  Reproducibility
+ * depends on the policy (see enum ctattn_policy).
  */
 int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
                const void *dout, const float *lse, void *dq, void *dk, void *dv,
@@ -73,8 +82,9 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
 /* Message describing the last failure of a ctattn_* call on this thread ("" if none). */
 const char *ctattn_last_error(void);
 
-/* Set / get the process-wide kernel selection policy (enum ctattn_policy). Returns the
- * previous policy, or -1 for an unknown value. */
+/* Set / get the process-wide kernel selection policy (enum ctattn_policy).  Returns the
+ * previous policy, or -1 for an unknown value.  Not synchronised with calls in flight on
+ * other threads: set it before issuing work. */
 int ctattn_set_policy(int policy);
 int ctattn_get_policy(void);
 

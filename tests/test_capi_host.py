@@ -91,8 +91,22 @@ def test_policy_roundtrip(lib):
     assert lib.ctattn_get_policy() == _capi.POLICY_GENERIC
     _capi.set_policy(prev)
     assert lib.ctattn_get_policy() == prev
+    prev = _capi.set_policy(_capi.POLICY_DETERMINISTIC)
+    assert lib.ctattn_get_policy() == _capi.POLICY_DETERMINISTIC
+    _capi.set_policy(prev)
     with pytest.raises(ValueError):
         _capi.set_policy(5)
+
+
+def test_deterministic_policy_needs_more_workspace(lib):
+    prev = _capi.set_policy(_capi.POLICY_DETERMINISTIC)
+    try:
+        n_det = lib.ctattn_bwd_workspace_bytes(0, 8, 12, 1024, 64, 1)
+    finally:
+        _capi.set_policy(prev)
+    n_auto = lib.ctattn_bwd_workspace_bytes(0, 8, 12, 1024, 64, 1)
+    # per-128-key-block dQ partials: 8 blocks x [B, H, T, d] fp32
+    assert n_det == n_auto + 8 * 8 * 12 * 1024 * 64 * 4
 
 
 def test_no_gpu_call_raises_cleanly(lib):

@@ -2,8 +2,8 @@
 
 Tolerances (fixed by the build's target): fp32 max|x - g| <= 1e-4 on each of O, LSE, dQ,
 dK, dV; bf16 max|x - g| / max|g| <= 2e-2 per tensor, g computed from the bf16-rounded
-inputs.  Both kernel families are exercised: POLICY_AUTO (MFMA where supported) and
-POLICY_GENERIC.
+inputs.  Every kernel policy is exercised: POLICY_AUTO (MFMA where supported, dQ by fp32
+atomics), POLICY_DETERMINISTIC (MFMA, ordered dQ reduction) and POLICY_GENERIC.
 """
 import glob
 import os
@@ -29,7 +29,8 @@ def say(msg):
     sys.stdout.flush()
 
 
-@pytest.fixture(params=[ct.POLICY_AUTO, ct.POLICY_GENERIC], ids=["auto", "generic"])
+@pytest.fixture(params=[ct.POLICY_AUTO, ct.POLICY_GENERIC, ct.POLICY_DETERMINISTIC],
+                ids=["auto", "generic", "deterministic"])
 def policy(request):
     prev = ct.set_policy(request.param)
     yield request.param
@@ -141,13 +142,31 @@ def test_mfma_matches_generic(causal):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_backward_is_deterministic(dtype):
-    shape = (2, 3, 300, 64)
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_deterministic_policy_is_bitwise_reproducible(dtype, causal):
+    shape = (2, 3, 1000, 64)
     q, k, v, do = ora.make_inputs(shape, seed=41, dtype=dtype)
-    r1 = run_gpu(q, k, v, do, True, dtype)
-    r2 = run_gpu(q, k, v, do, True, dtype)
+    prev = ct.set_policy(ct.POLICY_DETERMINISTIC)
+    try:
+        r1 = run_gpu(q, k, v, do, causal, dtype)
+        r2 = run_gpu(q, k, v, do, causal, dtype)
+    finally:
+        ct.set_policy(prev)
     for key in r1:
         assert np.array_equal(r1[key], r2[key]), key
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_auto_policy_reproducibility(causal):
+    """AUTO: O, LSE, dK, dV bitwise reproducible; dQ (fp32 atomics across key blocks)
+    reproducible up to the order of fp32 additions."""
+    shape = (2, 3, 1000, 64)
+    q, k, v, do = ora.make_inputs(shape, seed=42)
+    r1 = run_gpu(q, k, v, do, causal, "f32")
+    r2 = run_gpu(q, k, v, do, causal, "f32")
+    for key in ("o", "lse", "dk", "dv"):
+        assert np.array_equal(r1[key], r2[key]), key
+    assert np.max(np.abs(r1["dq"] - r2["dq"])) <= 1e-5 * max(1.0, np.max(np.abs(r1["dq"])))
 
 
 def test_forward_without_lse():
