@@ -19,13 +19,23 @@ import json
 import os
 import sys
 
+# Workloads.  The default, c3, is the headline metric; c4 is the
+# bf16 long-context config, reported separately (python bench.py --workload c4).
+WORKLOADS = {
+    "c3": dict(B=8, H=12, T=1024, D=64, dtype="f32", std=1.0, peak=157.3,
+               metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B8 H12 T1024 d64 fp32, 1 GPU",
+               label="causal SDPA fwd+bwd, B8 H12 T1024 d64 fp32 (BASELINE configs[2])"),
+    "c4": dict(B=1, H=32, T=8192, D=128, dtype="bf16", std=0.5, peak=2516.6,
+               metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 bf16, 1 GPU",
+               label="causal SDPA fwd+bwd, B1 H32 T8192 d128 bf16 in / fp32 accumulate (BASELINE configs[3])"),
+}
 B, H, T, D = 8, 12, 1024, 64
 CAUSAL = True
 FWD_FLOP = 4.0 * B * H * T * T * D / 2.0  # QK^T + PV, 2*T^2*d each; causal = half of T^2
 BWD_FLOP = 2.5 * FWD_FLOP
 STEP_FLOP = FWD_FLOP + BWD_FLOP
 PEAK_F32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
-METRIC = "causal attn fwd+bwd TFLOP/s + % MFMA peak, B8 H12 T1024 d64 fp32, 1 GPU"
+METRIC = WORKLOADS["c3"]["metric"]
 HERE = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "attn_bwd_f32_c3_traffic.txt")
 
@@ -73,10 +83,22 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (rocprofv3 --pmc calibration of "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count)")
     args = ap.parse_args()
+
+    global B, H, T, D, FWD_FLOP, BWD_FLOP, STEP_FLOP, PEAK_F32_MFMA, METRIC
+    wl = WORKLOADS[args.workload]
+    B, H, T, D = wl["B"], wl["H"], wl["T"], wl["D"]
+    FWD_FLOP = 4.0 * B * H * T * T * D / 2.0
+    BWD_FLOP = 2.5 * FWD_FLOP
+    STEP_FLOP = FWD_FLOP + BWD_FLOP
+    PEAK_F32_MFMA = wl["peak"]
+    METRIC = wl["metric"]
+    if args.workload != "c3":
+        args.no_cpu_baseline = True  # the CPU baseline is quoted for the headline config
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this build measures one GPU "
@@ -102,12 +124,13 @@ def main():
               flush=True)
         return
     g = torch.Generator(device=dev).manual_seed(2)
-    q, k, v, do = (torch.randn((B, H, T, D), generator=g, device=dev, dtype=torch.float32)
-                   for _ in range(4))
+    tdt = torch.float32 if wl["dtype"] == "f32" else torch.bfloat16
+    q, k, v, do = ((wl["std"] * torch.randn((B, H, T, D), generator=g, device=dev,
+                                            dtype=torch.float32)).to(tdt) for _ in range(4))
     o = torch.empty_like(q)
     lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-    ws = torch.empty(ct.bwd_workspace_bytes(torch.float32, B, H, T, D, CAUSAL), device=dev,
+    ws = torch.empty(ct.bwd_workspace_bytes(tdt, B, H, T, D, CAUSAL), device=dev,
                      dtype=torch.uint8)
     stream = torch.cuda.current_stream()
 
@@ -165,11 +188,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": wl["dtype"],
         "data": "synthetic",
         "pct_of_peak": round(100.0 * value / PEAK_F32_MFMA, 2),
         "config": {
-            "workload": "causal SDPA fwd+bwd, B8 H12 T1024 d64 fp32 (BASELINE configs[2])",
+            "workload": wl["label"],
             "B": B, "H": H, "T": T, "d": D, "causal": CAUSAL,
             "step_gflop": round(STEP_FLOP / 1e9, 3),
             "fwd_ms": round(fwd_ms, 5),
@@ -182,7 +205,7 @@ def main():
             "peak": PEAK_F32_MFMA,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_F32_MFMA, 4),
-            "traffic": read_traffic(),
+            "traffic": read_traffic() if args.workload == "c3" else None,
         },
         "cpu_baseline": None,
     }

@@ -392,12 +392,12 @@ int64_t partial_bytes(const AttnShape &s) {
 }  // namespace
 
 bool mfma_bwd_supported(int dtype, int64_t d) {
-    if (dtype == 0) return d == 64 || d == 128;
-    return false;
+    (void)dtype;
+    return d == 64 || d == 128;
 }
 
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic) {
-    if (dtype != 0) return 0;
+    if (dtype == 1) return bf16_bwd_workspace_bytes(s, deterministic);
     return deterministic ? partial_bytes(s) : 0;
 }
 
@@ -405,7 +405,8 @@ hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *
                            const void *o, const void *dout, const float *lse, float *delta,
                            void *dq, void *dk, void *dv, void *extra, bool deterministic,
                            const AttnShape &s, hipStream_t stream) {
-    if (dtype != 0) return hipErrorNotSupported;
+    if (dtype == 1)
+        return launch_bf16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, deterministic, s, stream);
     const DqMode mode = deterministic ? DqMode::Partial : DqMode::Atomic;
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };

@@ -272,12 +272,12 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
 
 bool mfma_fwd_supported(int dtype, int64_t d) {
     if (dtype == 0) return d == 32 || d == 64 || d == 128;
-    return false;
+    return d == 64 || d == 128;
 }
 
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
                            float *lse, const AttnShape &s, hipStream_t stream) {
-    if (dtype != 0) return hipErrorNotSupported;
+    if (dtype == 1) return launch_bf16_fwd(q, k, v, o, lse, s, stream);
     const float *qf = static_cast<const float *>(q);
     const float *kf = static_cast<const float *>(k);
     const float *vf = static_cast<const float *>(v);

@@ -34,6 +34,16 @@ hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *
                            float *lse, const AttnShape &s, hipStream_t stream);
 // `deterministic` selects the ordered dQ reduction (per-key-block partials in the workspace)
 // instead of fp32 atomics.
+// bf16 forward on bf16 MFMA (d in {64, 128}); called by launch_mfma_fwd for dtype 1.
+hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                           const AttnShape &s, hipStream_t stream);
+// bf16 backward on bf16 MFMA (d in {64, 128}); called by launch_mfma_bwd for dtype 1.
+// Scratch: an fp32 dQ accumulator [B, H, T, d], or per-128-key-block partials when
+// deterministic.
+int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic);
+hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
+                           const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
+                           bool deterministic, const AttnShape &s, hipStream_t stream);
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic);
 // Runs the whole MFMA backward: its own preprocess (delta = rowsum(dO * O) into `delta`,
 // fp32 [B, H, T]) and the main kernel(s).  `extra` points at mfma_bwd_workspace_bytes()
