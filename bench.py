@@ -25,6 +25,9 @@ WORKLOADS = {
     "c3": dict(B=8, H=12, T=1024, D=64, dtype="f32", std=1.0, peak=157.3,
                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B8 H12 T1024 d64 fp32, 1 GPU",
                label="causal SDPA fwd+bwd, B8 H12 T1024 d64 fp32 (BASELINE configs[2])"),
+    "c5": dict(B=16, H=6, T=256, D=64, dtype="f32", std=1.0, peak=157.3,
+               metric="NanoGPT config-5 training step tokens/s (attention on ctattn), fp32, 1 GPU",
+               label="NanoGPT 6L d384 6H T256 B16 vocab65 GELU, Adam lr 3e-4, fp32 (BASELINE configs[4])"),
     "c4": dict(B=1, H=32, T=8192, D=128, dtype="bf16", std=0.5, peak=2516.6,
                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 bf16, 1 GPU",
                label="causal SDPA fwd+bwd, B1 H32 T8192 d128 bf16 in / fp32 accumulate (BASELINE configs[3])"),
@@ -112,6 +115,8 @@ def main():
     import cudatransformer_amd as ct
 
     dev = torch.device("cuda:0")
+    if args.workload == "c5":
+        return bench_nanogpt(args, wl, dev)
     if args.copy_calibration:
         n = 64 << 20  # 64 Mi fp32 = 256 MiB read + 256 MiB written per copy
         src = torch.ones(n, device=dev, dtype=torch.float32)
@@ -212,6 +217,42 @@ def main():
     if not args.no_cpu_baseline:
         log("timing CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def bench_nanogpt(args, wl, dev):
+    """Config 5: full training steps (forward, backward, Adam) of the NanoGPT host with its
+    attention on the ctattn kernels; tokens/s and the losses of the timed steps."""
+    import torch
+
+    from cudatransformer_amd.nanogpt import (CONFIG5, NanoGPT, attention_flops_per_step, make_batch,
+                                             model_flops_per_step, train_step)
+
+    cfg = CONFIG5
+    model = NanoGPT(**cfg, attention="ctattn").init_weights(5).to(dev)
+    opt = torch.optim.Adam(model.parameters(), lr=cfg["lr"], betas=(0.9, 0.999), eps=1e-8)
+    ids, tgt = make_batch(cfg["batch"], cfg["seq_len"], cfg["vocab"], seed=5)
+    ids, tgt = ids.to(dev), tgt.to(dev)
+    for _ in range(args.warmup):
+        train_step(model, opt, ids, tgt)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    losses = [train_step(model, opt, ids, tgt) for _ in range(args.steps)]
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    tokens = cfg["batch"] * cfg["seq_len"]
+    out = {
+        "metric": wl["metric"], "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": wl["label"], "model_tflops": round(model_flops_per_step() / (ms * 1e-3) / 1e12, 2),
+                   "attention_gflop_per_step": round(attention_flops_per_step() / 1e9, 3),
+                   "loss_first": round(float(losses[0]), 4), "loss_last": round(float(losses[-1]), 4)},
+        "roofline": None, "cpu_baseline": None,
+    }
     print(json.dumps(out), flush=True)
 
 
