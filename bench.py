@@ -10,7 +10,7 @@ Prints ONE JSON line.  `value` is TFLOP/s by the FA2 convention: the forward is 
 matmuls of 2*T^2*d flops per (b, h), causal counts half of T^2, so fwd = 2*B*H*T^2*d =
 12.885 GFLOP; the backward is 2.5x that; fwd+bwd = 3.5x -> 45.097 GFLOP per step.
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+  python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--no-cpu-baseline]
 """
 from __future__ import annotations
 
@@ -82,8 +82,10 @@ def cpu_baseline(seconds: float):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 50 warmup steps (~25 ms of kernels) let the GPU clocks ramp before timing; with only a
+    # handful the first timed steps still run at idle clocks (about 7% slower for c3).
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3")

@@ -7,9 +7,12 @@
 // Work decomposition
 //   * one workgroup = 4 waves = BM = 128 query rows of one (batch, head); each wave owns
 //     32 rows and keeps them for the whole key loop.
-//   * the key loop walks BN-key blocks.  K and V blocks are staged global -> registers ->
-//     LDS; the next block's global loads are issued before the current block's MFMAs so
-//     HBM latency hides behind compute.
+//   * the key loop walks BN-key blocks.  K and V blocks go straight from global memory to
+//     LDS (global_load_lds_dwordx4, no staging registers), double-buffered: the next
+//     block's loads are in flight during the current block's MFMAs, one barrier per block.
+//     Rows are stored unpadded with 16-byte chunks XOR-swizzled by (row & 7), which keeps
+//     the K (ds_read_b128, one key row per lane) and V (ds_read_b32, one d column per
+//     lane) operand reads free of bank conflicts.
 //   * scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q^T held in
 //     registers for the whole kernel, pre-scaled by log2(e)/sqrt(d)).  In the resulting
 //     accumulator each lane holds ONE query row (its column) and 16 keys per 32-key tile,
@@ -34,14 +37,20 @@ template <int D, int BN>
 struct FwdCfg {
     static constexpr int NW = 4;               // waves per workgroup
     static constexpr int BM = 32 * NW;         // query rows per workgroup
-    static constexpr int STRIDE = D + 4;       // LDS row stride (floats); +4 avoids b128 bank conflicts
     static constexpr int KT = BN / 32;         // 32-key tiles per block
     static constexpr int DT = D / 32;          // 32-wide d tiles of O^T
-    static constexpr int F4_ROW = D / 4;       // float4 per row
-    static constexpr int F4_THREAD = BN * F4_ROW / (NW * kWave);
+    static constexpr int C4 = D / 4;           // 16-byte chunks per row
+    static constexpr int TILE = BN * D;        // floats per K (or V) tile
+    static constexpr int INSTR = TILE / 4 / (NW * kWave);  // 16-byte loads per lane per tile
     static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
-    static_assert((BN * F4_ROW) % (NW * kWave) == 0, "tile load split");
+    static_assert(INSTR * 4 * NW * kWave == TILE, "tile load split");
 };
+
+// Float offset of 16-byte chunk c4 of row `row` in an unpadded, XOR-swizzled tile.
+template <int D>
+__device__ __forceinline__ int swz(int row, int c4) { return row * D + ((c4 ^ (row & 7)) << 2); }
+
+#define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
 // Lazy online-softmax rescaling: the running row max m (log2 units) is only raised when a
 // block's max exceeds it by more than this, so most blocks skip rescaling O and l.  Scores
@@ -79,10 +88,10 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
     for (int kt = 0; kt < C::KT; ++kt) {
         sacc[kt] = zero16();
         if (!active[kt]) continue;
-        const float *krow = &k_lds[(kt * 32 + col) * C::STRIDE + 4 * half];
+        const int key = kt * 32 + col;
 #pragma unroll
         for (int m = 0; m < D / 8; ++m) {
-            const floatx4 kv = *reinterpret_cast<const floatx4 *>(krow + 8 * m);
+            const floatx4 kv = *reinterpret_cast<const floatx4 *>(k_lds + swz<D>(key, 2 * m + half));
 #pragma unroll
             for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
         }
@@ -135,7 +144,8 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
         for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
-                const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::STRIDE + dt * 32 + col];
+                const int d = dt * 32 + col;
+                const float a = v_lds[swz<D>(kt * 32 + kstep_index(s, half), d >> 2) + (d & 3)];
                 st.oacc[dt] = mfma32x32x2(a, sacc[kt][s], st.oacc[dt]);
             }
         }
@@ -150,8 +160,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                           float *__restrict__ lse, int T,
                                                           int BH, int causal, float qscale) {
     using C = FwdCfg<D, BN>;
-    __shared__ __attribute__((aligned(16))) float k_lds[BN * C::STRIDE];
-    __shared__ __attribute__((aligned(16))) float v_lds[BN * C::STRIDE];
+    __shared__ __attribute__((aligned(16))) float k_lds[2][C::TILE];
+    __shared__ __attribute__((aligned(16))) float v_lds[2][C::TILE];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -188,50 +198,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int kend = causal ? min(T, q0 + C::BM) : T;
     const int nkb = (kend + BN - 1) / BN;
 
-    floatx4 kpre[C::F4_THREAD], vpre[C::F4_THREAD];
-    auto load_block = [&](int j0) {
+    // Global -> LDS for one block: lane writes LDS chunk P (tile position, in 16-byte units)
+    // = (wave * INSTR + i) * 64 + lane, i.e. row P / C4, swizzled chunk P % C4, so it loads
+    // chunk (P % C4) ^ (row & 7) of that key row.  Rows past T re-read row T - 1 (masked).
+    auto issue = [&](int j0, int buf) {
 #pragma unroll
-        for (int i = 0; i < C::F4_THREAD; ++i) {
-            const int f = tid + i * C::NW * kWave;
-            const int r = f / C::F4_ROW;
-            const int c4 = f - r * C::F4_ROW;
-            const int key = j0 + r;
-            floatx4 kx = {0.f, 0.f, 0.f, 0.f}, vx = {0.f, 0.f, 0.f, 0.f};
-            if (key < T) {
-                kx = *reinterpret_cast<const floatx4 *>(k + base + int64_t(key) * D + 4 * c4);
-                vx = *reinterpret_cast<const floatx4 *>(v + base + int64_t(key) * D + 4 * c4);
-            }
-            kpre[i] = kx;
-            vpre[i] = vx;
-        }
-    };
-    auto store_block = [&]() {
-#pragma unroll
-        for (int i = 0; i < C::F4_THREAD; ++i) {
-            const int f = tid + i * C::NW * kWave;
-            const int r = f / C::F4_ROW;
-            const int c4 = f - r * C::F4_ROW;
-            *reinterpret_cast<floatx4 *>(&k_lds[r * C::STRIDE + 4 * c4]) = kpre[i];
-            *reinterpret_cast<floatx4 *>(&v_lds[r * C::STRIDE + 4 * c4]) = vpre[i];
+        for (int i = 0; i < C::INSTR; ++i) {
+            const int P = (wave * C::INSTR + i) * kWave + lane;
+            const int r = P / C::C4;
+            const int c4 = (P % C::C4) ^ (r & 7);
+            const int64_t goff = base + int64_t(min(j0 + r, T - 1)) * D + 4 * c4;
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(k + goff),
+                                             CTATTN_LDS(&k_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(v + goff),
+                                             CTATTN_LDS(&v_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
         }
     };
 
-    load_block(0);
+    issue(0, 0);
     for (int kb = 0; kb < nkb; ++kb) {
         const int j0 = kb * BN;
-        __syncthreads();  // every wave is done reading the previous block
-        store_block();
+        const int buf = kb & 1;
+        // This lane's loads into `buf` have landed (vmcnt = 0); the barrier then makes every
+        // lane's loads visible and guarantees every wave is done reading buf ^ 1.
+        __builtin_amdgcn_s_waitcnt(0xF70);
         __syncthreads();
-        if (kb + 1 < nkb) load_block(j0 + BN);
+        if (kb + 1 < nkb) issue(j0 + BN, buf ^ 1);
 
         // Wave-uniform: does this block touch the diagonal or the sequence end for this wave?
         const bool masked = (j0 + BN > T) || (causal && j0 + BN - 1 > wave_first_row);
         if (masked) {
             if (!causal || j0 <= wave_last_row)
-                fwd_block<D, BN, true>(st, qreg, k_lds, v_lds, j0, row, wave_first_row,
+                fwd_block<D, BN, true>(st, qreg, k_lds[buf], v_lds[buf], j0, row, wave_first_row,
                                        wave_last_row, T, causal, col, half);
         } else {
-            fwd_block<D, BN, false>(st, qreg, k_lds, v_lds, j0, row, wave_first_row,
+            fwd_block<D, BN, false>(st, qreg, k_lds[buf], v_lds[buf], j0, row, wave_first_row,
                                     wave_last_row, T, causal, col, half);
         }
     }
