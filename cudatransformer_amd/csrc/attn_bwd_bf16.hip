@@ -237,7 +237,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdBf16Occu
         __syncthreads();  // dS of every wave visible
 
         // dQ[r0..r0+31][32*wave .. 32*wave+31] over the workgroup's active keys; waves past
-        // d / 32 have no columns (d = 64: waves 2, 3 skip this phase).
+        // d / 32 have no columns (d = 64: waves 2, 3 skip this phase; d = 32: waves 1-3).
         if (wave >= C::DT) continue;
         floatx16 dq = zero16();
 #pragma unroll
@@ -394,6 +394,7 @@ hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const vo
                            bool deterministic, const AttnShape &s, hipStream_t stream) {
     float *acc = static_cast<float *>(extra);
     switch (s.d) {
+        case 32: return bwd_bf16<32>(q, k, v, o, dout, lse, delta, dq, dk, dv, acc, deterministic, s, stream);
         case 64: return bwd_bf16<64>(q, k, v, o, dout, lse, delta, dq, dk, dv, acc, deterministic, s, stream);
         case 128: return bwd_bf16<128>(q, k, v, o, dout, lse, delta, dq, dk, dv, acc, deterministic, s, stream);
         default: return hipErrorNotSupported;

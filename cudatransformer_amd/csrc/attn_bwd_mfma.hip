@@ -21,7 +21,7 @@
 //     are elementwise, and P / dS are directly the B operands of
 //       dV^T += dO^T P  and  dK^T += Q^T dS     (A = dO / Q columns from LDS).
 //   * dQ needs dS with rows on lanes: each wave writes its dS tile to LDS, then every wave
-//     computes a 32 x (d/4) slice of dQ = dS K over the workgroup's 128 keys with
+//     computes a quarter of the 32 x d block of dQ = dS K over the workgroup's 128 keys with
 //     v_mfma_f32_16x16x4f32 (A = dS rows from LDS, B = K from LDS).  The slice is either
 //     added with fp32 atomics into dq (DqMode::Atomic; dq pre-zeroed by the preprocess
 //     kernel) or stored into a per-key-block partial buffer that a second kernel sums in a
@@ -53,9 +53,14 @@ struct BwdCfg {
     static constexpr int F4_ROW = D / 4;
     static constexpr int QF4 = BM * F4_ROW / (NW * kWave);  // float4 per thread per Q block
     static constexpr int KF4 = BN * F4_ROW / (NW * kWave);  // float4 per thread for the K block
-    static constexpr int DQ_COLS = D / NW;    // dQ columns per wave
-    static constexpr int DQ_CT = DQ_COLS / 16;  // 16-wide column tiles per wave
-    static_assert(D % 64 == 0, "MFMA backward supports d in {64, 128}");
+    // dQ of one 32-row block is (2 x D/16) 16x16 tiles; each wave takes a quarter: for
+    // d >= 64 both row tiles of a D/4-column slice, for d = 32 one tile
+    // (row tile wave >> 1, column tile wave & 1).
+    static constexpr int DQ_RT = D >= 64 ? 2 : 1;   // 16-row tiles per wave
+    static constexpr int DQ_COLS = D >= 64 ? D / NW : 16;  // dQ columns per wave
+    static constexpr int DQ_CT = DQ_COLS / 16;      // 16-wide column tiles per wave
+    static_assert(D == 32 || D == 64 || D == 128, "MFMA backward supports d in {32, 64, 128}");
+    static_assert(DQ_RT * DQ_CT * NW == 2 * (D / 16), "dQ tiles split over the waves");
     static_assert(QF4 >= 1 && KF4 >= 1, "block load split");
 };
 
@@ -114,8 +119,13 @@ __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], float
     for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
 }
 
+// Waves per SIMD the kernel is compiled for: two for d <= 64 (<= 256 VGPRs); d = 128 needs
+// more registers than that and runs one wave per SIMD.
+template <int D> struct BwdF32Occupancy { static constexpr int waves = D <= 64 ? 2 : 1; };
+
 template <int D, DqMode MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_f32_mfma_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occupancy<D>::waves,
+                                                                     BwdF32Occupancy<D>::waves))) void bwd_f32_mfma_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dq_part,
@@ -239,9 +249,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         __syncthreads();  // dS of every wave visible
 
         // dQ[r0 .. r0+31][wave * DQ_COLS ..] = sum over the workgroup's active keys of dS K.
-        floatx4 dq_acc[2][C::DQ_CT];
+        const int rt0 = D >= 64 ? 0 : (wave >> 1);                 // first 16-row tile
+        const int dq_col0 = D >= 64 ? wave * C::DQ_COLS : (wave & 1) * 16;  // first column
+        floatx4 dq_acc[C::DQ_RT][C::DQ_CT];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < C::DQ_RT; ++rt)
 #pragma unroll
             for (int ct = 0; ct < C::DQ_CT; ++ct) dq_acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -251,30 +263,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
                 const int kl = 32 * w2 + 16 * sb + 4 * quad;  // local key of step t: kl + t
-                floatx4 a[2];
+                floatx4 a[C::DQ_RT];
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
-                    a[rt] = *reinterpret_cast<const floatx4 *>(&ds_lds[(rt * 16 + c16) * C::SS + kl]);
+                for (int rt = 0; rt < C::DQ_RT; ++rt)
+                    a[rt] = *reinterpret_cast<const floatx4 *>(&ds_lds[((rt0 + rt) * 16 + c16) * C::SS + kl]);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
 #pragma unroll
                     for (int ct = 0; ct < C::DQ_CT; ++ct) {
-                        const float b = k_lds[(kl + t) * C::KS + wave * C::DQ_COLS + ct * 16 + c16];
+                        const float b = k_lds[(kl + t) * C::KS + dq_col0 + ct * 16 + c16];
 #pragma unroll
-                        for (int rt = 0; rt < 2; ++rt) dq_acc[rt][ct] = mfma16x16x4(a[rt][t], b, dq_acc[rt][ct]);
+                        for (int rt = 0; rt < C::DQ_RT; ++rt) dq_acc[rt][ct] = mfma16x16x4(a[rt][t], b, dq_acc[rt][ct]);
                     }
                 }
             }
         }
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
+        for (int rt = 0; rt < C::DQ_RT; ++rt) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = r0 + rt * 16 + 4 * quad + r;
+                const int row = r0 + (rt0 + rt) * 16 + 4 * quad + r;
                 if (row >= T) continue;
 #pragma unroll
                 for (int ct = 0; ct < C::DQ_CT; ++ct) {
-                    const int c = wave * C::DQ_COLS + ct * 16 + c16;
+                    const int c = dq_col0 + ct * 16 + c16;
                     const float val = dq_acc[rt][ct][r] * inv_sqrt_d;
                     if constexpr (MODE == DqMode::Atomic) {
                         unsafeAtomicAdd(dq + base + int64_t(row) * D + c, val);
@@ -392,8 +404,8 @@ int64_t partial_bytes(const AttnShape &s) {
 }  // namespace
 
 bool mfma_bwd_supported(int dtype, int64_t d) {
-    (void)dtype;
-    return d == 64 || d == 128;
+    (void)dtype;  // fp32 and bf16 kernels both cover d in {32, 64, 128}
+    return d == 32 || d == 64 || d == 128;
 }
 
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic) {
@@ -411,6 +423,9 @@ hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };
     switch (s.d) {
+        case 32:
+            return bwd_f32<32>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
+                               g(extra), mode, s, stream);
         case 64:
             return bwd_f32<64>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
                                g(extra), mode, s, stream);

@@ -287,6 +287,7 @@ hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float 
 hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
                            const AttnShape &s, hipStream_t stream) {
     switch (s.d) {
+        case 32: return fwd_bf16<32>(q, k, v, o, lse, s, stream);
         case 64: return fwd_bf16<64>(q, k, v, o, lse, s, stream);
         case 128: return fwd_bf16<128>(q, k, v, o, lse, s, stream);
         default: return hipErrorNotSupported;

@@ -272,8 +272,8 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
 }  // namespace
 
 bool mfma_fwd_supported(int dtype, int64_t d) {
-    if (dtype == 0) return d == 32 || d == 64 || d == 128;
-    return d == 64 || d == 128;
+    (void)dtype;  // fp32 and bf16 kernels both cover d in {32, 64, 128}
+    return d == 32 || d == 64 || d == 128;
 }
 
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,

@@ -27,17 +27,17 @@ hipError_t launch_generic_bwd(int dtype, const void *q, const void *k, const voi
 hipError_t launch_bwd_preprocess(int dtype, const void *o, const void *dout, float *delta,
                                  const AttnShape &s, hipStream_t stream);
 
-// ---- MFMA kernels (fp32: d in {32, 64, 128}; bf16: d in {64, 128}) ----
+// ---- MFMA kernels (fp32 and bf16: d in {32, 64, 128}) ----
 bool mfma_fwd_supported(int dtype, int64_t d);
 bool mfma_bwd_supported(int dtype, int64_t d);
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
                            float *lse, const AttnShape &s, hipStream_t stream);
 // `deterministic` selects the ordered dQ reduction (per-key-block partials in the workspace)
 // instead of fp32 atomics.
-// bf16 forward on bf16 MFMA (d in {64, 128}); called by launch_mfma_fwd for dtype 1.
+// bf16 forward on bf16 MFMA (d in {32, 64, 128}); called by launch_mfma_fwd for dtype 1.
 hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
                            const AttnShape &s, hipStream_t stream);
-// bf16 backward on bf16 MFMA (d in {64, 128}); called by launch_mfma_bwd for dtype 1.
+// bf16 backward on bf16 MFMA (d in {32, 64, 128}); called by launch_mfma_bwd for dtype 1.
 // Scratch: an fp32 dQ accumulator [B, H, T, d], or per-128-key-block partials when
 // deterministic.
 int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic);

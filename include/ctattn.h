@@ -20,13 +20,17 @@
  *     return hipErrorInvalidValue (1); unsupported head dims return
  *     hipErrorNotSupported (801).
  *   - supported: dtype f32 or bf16 (storage; all arithmetic accumulates in fp32),
- *     1 <= d <= 256, T >= 0, B, H >= 0.  d in {64, 128} (and 32 for f32) run on the MFMA
+ *     1 <= d <= 256, T >= 0, B, H >= 0.  d in {32, 64, 128} run on the MFMA
  *     kernels; other d on a generic kernel.
  */
 #ifndef CTATTN_H
 #define CTATTN_H
 
 #include <stdint.h>
+
+/* Only the functions below are exported from libctattn.so (it is built with hidden
+ * visibility), so two builds of the library can share a process without interposing. */
+#define CTATTN_API __attribute__((visibility("default")))
 
 #ifdef __cplusplus
 extern "C" {
@@ -55,7 +59,7 @@ enum ctattn_policy {
  * (flash_attention.cu:164-167); this boundary writes the single fp32 LSE instead.
  * lse may be NULL when the caller does not keep state for a backward.
  */
-int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, float *lse,
+CTATTN_API int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, float *lse,
                int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream);
 
 /*
@@ -63,7 +67,7 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
  * arguments.  Replaces nothing in the reference: its backward zero-fills and atomically
  * accumulates straight into dq/dk/dv (FlashAttentionLayer.cu:103-106, flash_attention.cu:317-321).
  */
-int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
+CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal);
 
 /*
@@ -74,22 +78,22 @@ int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, i
  * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy.  Reproducibility
  * depends on the policy (see enum ctattn_policy).
  */
-int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
+CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
                const void *dout, const float *lse, void *dq, void *dk, void *dv,
                void *workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
                int64_t d, int causal, void *stream);
 
 /* Message describing the last failure of a ctattn_* call on this thread ("" if none). */
-const char *ctattn_last_error(void);
+CTATTN_API const char *ctattn_last_error(void);
 
 /* Set / get the process-wide kernel selection policy (enum ctattn_policy).  Returns the
  * previous policy, or -1 for an unknown value.  Not synchronised with calls in flight on
  * other threads: set it before issuing work. */
-int ctattn_set_policy(int policy);
-int ctattn_get_policy(void);
+CTATTN_API int ctattn_set_policy(int policy);
+CTATTN_API int ctattn_get_policy(void);
 
 /* Library version, major * 10000 + minor * 100 + patch. */
-int ctattn_version(void);
+CTATTN_API int ctattn_version(void);
 
 #ifdef __cplusplus
 }

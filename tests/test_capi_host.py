@@ -33,6 +33,19 @@ def test_exports_every_declared_symbol(lib):
         assert hasattr(raw, n), f"{n} declared in include/ctattn.h but not exported"
 
 
+def test_exports_nothing_else(lib):
+    """The library is built with hidden visibility: its dynamic symbol table defines exactly
+    the functions the header declares (internal C++ symbols stay private, so two builds
+    loaded in one process cannot interpose on each other)."""
+    nm = subprocess.run(["nm", "-D", "--defined-only", _capi.LIB_PATH], capture_output=True,
+                        text=True)
+    if nm.returncode != 0:
+        pytest.skip("nm unavailable")
+    funcs = {line.split()[-1] for line in nm.stdout.splitlines()
+             if len(line.split()) == 3 and line.split()[1] == "T"}
+    assert funcs == set(_capi.header_functions())
+
+
 def test_version(lib):
     assert lib.ctattn_version() == 100
 

@@ -81,6 +81,7 @@ SHAPES = [
     (1, 1, 65, 48),
     (1, 1, 70, 256),
     (1, 2, 129, 8),
+    (2, 2, 300, 32),
 ]
 
 
@@ -127,9 +128,10 @@ def test_c4_long_context_bf16():
     assert np.max(np.abs(dv_sum - do_sum)) <= 2e-2 * np.max(np.abs(do_sum))
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_mfma_matches_generic(causal):
-    shape = (2, 4, 200, 64)
+def test_mfma_matches_generic(causal, d):
+    shape = (2, 4, 200, d)
     q, k, v, do = ora.make_inputs(shape, seed=31)
     a = run_gpu(q, k, v, do, causal, "f32")
     prev = ct.set_policy(ct.POLICY_GENERIC)
