@@ -24,7 +24,12 @@ from ._capi import (  # noqa: E402
     flash_attn_bwd,
     flash_attn_fwd,
     last_error,
+    out_proj_bwd,
+    out_proj_fwd,
+    qkv_proj_bwd,
+    qkv_proj_fwd,
     set_policy,
+    sgd_update,
 )
 
 __all__ = [
@@ -38,6 +43,11 @@ __all__ = [
     "flash_attention",
     "flash_attn_bwd",
     "flash_attn_fwd",
+    "out_proj_bwd",
+    "out_proj_fwd",
+    "qkv_proj_bwd",
+    "qkv_proj_fwd",
+    "sgd_update",
     "last_error",
     "set_policy",
 ]

@@ -60,6 +60,21 @@ def load() -> ctypes.CDLL:
     lib.ctattn_get_policy.restype = c_int
     lib.ctattn_version.argtypes = []
     lib.ctattn_version.restype = c_int
+    shape5 = [i64] * 5  # B, T, E, H, d
+    lib.ctattn_qkv_proj_fwd.argtypes = [c_int] + [vp] * 10 + shape5 + [vp]
+    lib.ctattn_qkv_proj_fwd.restype = c_int
+    lib.ctattn_qkv_proj_bwd_workspace_bytes.argtypes = [c_int] + shape5
+    lib.ctattn_qkv_proj_bwd_workspace_bytes.restype = i64
+    lib.ctattn_qkv_proj_bwd.argtypes = [c_int] + [vp] * 15 + [i64] + shape5 + [vp]
+    lib.ctattn_qkv_proj_bwd.restype = c_int
+    lib.ctattn_out_proj_fwd.argtypes = [c_int] + [vp] * 4 + shape5 + [vp]
+    lib.ctattn_out_proj_fwd.restype = c_int
+    lib.ctattn_out_proj_bwd_workspace_bytes.argtypes = [c_int] + shape5
+    lib.ctattn_out_proj_bwd_workspace_bytes.restype = i64
+    lib.ctattn_out_proj_bwd.argtypes = [c_int] + [vp] * 7 + [i64] + shape5 + [vp]
+    lib.ctattn_out_proj_bwd.restype = c_int
+    lib.ctattn_sgd_update.argtypes = [c_int, vp, vp, ctypes.c_float, i64, vp]
+    lib.ctattn_sgd_update.restype = c_int
     _lib = lib
     return lib
 
@@ -173,3 +188,100 @@ class FlashAttentionFunction(torch.autograd.Function):
 def flash_attention(q, k, v, causal: bool = False):
     """Differentiable attention on the ctattn kernels."""
     return FlashAttentionFunction.apply(q, k, v, causal)
+
+
+# ---- attention-layer projections -------------------------------------------------------
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check_dev(name, dtype, *ts):
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda or not t.is_contiguous() or t.dtype != dtype:
+            raise ValueError(f"{name}: tensors must be contiguous {dtype} on the GPU")
+
+
+def qkv_proj_fwd(x, wq, wk, wv, bq, bk, bv, num_heads: int, head_dim: int, stream=None):
+    """Q, K, V [B, H, T, d] = x [B, T, E] W^T + b (W: [H*d, E]; biases may be None)."""
+    if x.dim() != 3:
+        raise ValueError("qkv_proj_fwd: x must be [B, T, E]")
+    b, t, e = x.shape
+    hd = num_heads * head_dim
+    _check_dev("qkv_proj_fwd", x.dtype, x, wq, wk, wv, bq, bk, bv)
+    for w in (wq, wk, wv):
+        if tuple(w.shape) != (hd, e):
+            raise ValueError(f"qkv_proj_fwd: weights must be [{hd}, {e}], got {tuple(w.shape)}")
+    q, k, v = (torch.empty((b, num_heads, t, head_dim), dtype=x.dtype, device=x.device) for _ in range(3))
+    rc = load().ctattn_qkv_proj_fwd(_DTYPE_CODE[x.dtype], _ptr(x), _ptr(wq), _ptr(wk), _ptr(wv), _ptr(bq),
+                                    _ptr(bk), _ptr(bv), _ptr(q), _ptr(k), _ptr(v), b, t, e, num_heads,
+                                    head_dim, _stream_handle(stream))
+    _check(rc, "ctattn_qkv_proj_fwd")
+    return q, k, v
+
+
+def qkv_proj_bwd(x, dq, dk, dv, wq, wk, wv, dw=None, db=None, want_dx=True, stream=None):
+    """Backward of qkv_proj_fwd.  dw / db: tuples of three tensors accumulated in place
+    (or None to skip).  Returns dx [B, T, E] (or None)."""
+    b, t, e = x.shape
+    _, h, _, d = dq.shape
+    _check_dev("qkv_proj_bwd", x.dtype, x, dq, dk, dv, wq, wk, wv, *(dw or ()), *(db or ()))
+    code = _DTYPE_CODE[x.dtype]
+    lib = load()
+    need = lib.ctattn_qkv_proj_bwd_workspace_bytes(code, b, t, e, h, d)
+    if need < 0:
+        raise RuntimeError(f"ctattn_qkv_proj_bwd_workspace_bytes failed: {last_error()}")
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    dx = torch.empty_like(x) if want_dx else None
+    dw = dw or (None, None, None)
+    db = db or (None, None, None)
+    rc = lib.ctattn_qkv_proj_bwd(code, _ptr(x), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(wq), _ptr(wk), _ptr(wv),
+                                 *map(_ptr, dw), *map(_ptr, db), _ptr(dx), _ptr(ws), ws.numel(), b, t, e, h,
+                                 d, _stream_handle(stream))
+    _check(rc, "ctattn_qkv_proj_bwd")
+    return dx
+
+
+def out_proj_fwd(c, wo, bo, stream=None):
+    """y [B, T, E] = c W_o^T + b_o, c: attention output [B, H, T, d], W_o: [E, H*d]."""
+    b, h, t, d = c.shape
+    e = wo.shape[0]
+    _check_dev("out_proj_fwd", c.dtype, c, wo, bo)
+    if tuple(wo.shape) != (e, h * d):
+        raise ValueError(f"out_proj_fwd: wo must be [E, {h * d}]")
+    y = torch.empty((b, t, e), dtype=c.dtype, device=c.device)
+    rc = load().ctattn_out_proj_fwd(_DTYPE_CODE[c.dtype], _ptr(c), _ptr(wo), _ptr(bo), _ptr(y), b, t, e, h, d,
+                                    _stream_handle(stream))
+    _check(rc, "ctattn_out_proj_fwd")
+    return y
+
+
+def out_proj_bwd(c, dy, wo, dwo=None, dbo=None, want_dc=True, stream=None):
+    """Backward of out_proj_fwd: dwo / dbo accumulated in place (None to skip); returns dc."""
+    b, h, t, d = c.shape
+    e = wo.shape[0]
+    _check_dev("out_proj_bwd", c.dtype, c, dy, wo, dwo, dbo)
+    code = _DTYPE_CODE[c.dtype]
+    lib = load()
+    need = lib.ctattn_out_proj_bwd_workspace_bytes(code, b, t, e, h, d)
+    if need < 0:
+        raise RuntimeError(f"ctattn_out_proj_bwd_workspace_bytes failed: {last_error()}")
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=c.device)
+    dc = torch.empty_like(c) if want_dc else None
+    rc = lib.ctattn_out_proj_bwd(code, _ptr(c), _ptr(dy), _ptr(wo), _ptr(dwo), _ptr(dbo), _ptr(dc), _ptr(ws),
+                                 ws.numel(), b, t, e, h, d, _stream_handle(stream))
+    _check(rc, "ctattn_out_proj_bwd")
+    return dc
+
+
+def sgd_update(params, grads, lr: float, stream=None):
+    """params -= lr * grads, in place, on the GPU."""
+    _check_dev("sgd_update", params.dtype, params, grads)
+    if params.numel() != grads.numel():
+        raise ValueError("sgd_update: size mismatch")
+    rc = load().ctattn_sgd_update(_DTYPE_CODE[params.dtype], _ptr(params), _ptr(grads), float(lr),
+                                  params.numel(), _stream_handle(stream))
+    _check(rc, "ctattn_sgd_update")

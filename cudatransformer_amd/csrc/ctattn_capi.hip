@@ -5,6 +5,7 @@
 // environment variable CTATTN_SYNC_CHECK=1 every entry point also synchronises the stream
 // and reports asynchronous kernel errors (debug mode; off by default).
 #include "attn_launch.h"
+#include "capi_util.h"
 #include "ctattn.h"
 
 #include <atomic>
@@ -13,10 +14,10 @@
 #include <cstdlib>
 #include <cstring>
 
-namespace {
+namespace ctattn {
+namespace capi {
 
 thread_local char g_err[512] = {0};
-std::atomic<int> g_policy{CTATTN_POLICY_AUTO};
 
 int fail(hipError_t code, const char *fmt, ...) {
     va_list ap;
@@ -39,6 +40,32 @@ bool sync_check_enabled() {
     return on;
 }
 
+int finish(const char *fn, hipError_t e, hipStream_t stream) {
+    if (e != hipSuccess)
+        return fail(e, "%s: kernel launch failed: %s", fn, hipGetErrorString(e));
+    if (sync_check_enabled()) {
+        e = hipStreamSynchronize(stream);
+        if (e == hipSuccess) e = hipGetLastError();
+        if (e != hipSuccess)
+            return fail(e, "%s: kernel execution failed: %s", fn, hipGetErrorString(e));
+    }
+    return ok();
+}
+
+int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+}  // namespace capi
+}  // namespace ctattn
+
+namespace {
+
+using ctattn::capi::align_up;
+using ctattn::capi::fail;
+using ctattn::capi::finish;
+using ctattn::capi::ok;
+
+std::atomic<int> g_policy{CTATTN_POLICY_AUTO};
+
 // Validates dtype and sizes; returns 0 or an error code (message set).
 int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, int64_t d) {
     if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
@@ -55,21 +82,6 @@ int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, i
         return fail(hipErrorInvalidValue, "%s: B*H*T = %.0f exceeds 2^31-1", fn, rows);
     return 0;
 }
-
-int finish(const char *fn, hipError_t e, hipStream_t stream) {
-    if (e != hipSuccess)
-        return fail(e, "%s: kernel launch failed: %s", fn, hipGetErrorString(e));
-    if (sync_check_enabled()) {
-        e = hipStreamSynchronize(stream);
-        if (e == hipSuccess) e = hipGetLastError();
-        if (e != hipSuccess)
-            return fail(e, "%s: kernel execution failed: %s", fn, hipGetErrorString(e));
-    }
-    return ok();
-}
-
-constexpr int64_t kAlign = 256;
-int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 bool use_mfma_fwd(int dtype, int64_t d) {
     return g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::mfma_fwd_supported(dtype, d);
@@ -136,7 +148,7 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
     return finish("ctattn_bwd", e, st);
 }
 
-const char *ctattn_last_error(void) { return g_err; }
+const char *ctattn_last_error(void) { return ctattn::capi::g_err; }
 
 int ctattn_set_policy(int policy) {
     if (policy != CTATTN_POLICY_AUTO && policy != CTATTN_POLICY_GENERIC &&
@@ -147,6 +159,6 @@ int ctattn_set_policy(int policy) {
 
 int ctattn_get_policy(void) { return g_policy.load(); }
 
-int ctattn_version(void) { return 100; }
+int ctattn_version(void) { return 200; }
 
 }  // extern "C"

@@ -1,18 +1,26 @@
 // pybind11 module `cuda_transformer`: the attention-path part of the reference's Python API
-// (cuda_transformer.cu:22-119 declare_tensor, :257-324 the attention bindings), on the
-// MI355X kernels behind include/ctattn.h.
+// (cuda_transformer.cu:22-119 declare_tensor, :147-157 the Module base, :257-324 the
+// attention layer bindings, :437 and :825 the Attention factories), on the MI355X kernels
+// behind include/ctattn.h.
 //
 // Names follow the reference: FloatTensor / BFloatTensor with fromNumpy, numpy, shape,
-// clone, item, fill, reshape.  The reference does not bind FlashAttentionLayer itself (it is
-// reached only through AttentionLayer); here it is bound as FloatFlashAttentionLayer /
-// BFloatFlashAttentionLayer with the C++ method names (computeAttention, computeBackward,
-// clearCache, clone), plus the factories FlashAttention / FlashAttentionFloat /
-// FlashAttentionBFloat.  bf16 tensors take and return float32 numpy arrays (numpy has no
-// bfloat16; values are rounded to nearest even on upload).
+// clone, item, fill, reshape; FloatModule / BFloatModule (the Layer base: forward, backward,
+// getParameters, setParameters, getGradients, zeroGrad, sgdUpdate, __call__);
+// FloatAttentionLayer / BFloatAttentionLayer (forward, forward_caching, backward,
+// backward_caching, sgdUpdate, the get/set{Query,Key,Value,Output}{Weights,Biases} pairs,
+// __call__) and the factories AttentionFloat / AttentionBFloat / Attention(input_dim,
+// num_heads, head_dim).  The reference does not bind FlashAttentionLayer itself (it is
+// reached only through AttentionLayer); here it is bound as well, as
+// FloatFlashAttentionLayer / BFloatFlashAttentionLayer with the C++ method names
+// (computeAttention, computeBackward, clearCache, clone) and the factories FlashAttention /
+// FlashAttentionFloat / FlashAttentionBFloat.  Attention factories take an extra
+// causal=False.  bf16 tensors take and return float32 numpy arrays (numpy has no bfloat16;
+// values are rounded to nearest even on upload).
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include "AttentionLayer.h"
 #include "FlashAttentionLayer.h"
 #include "ModuleLayer.h"
 #include "Tensor.h"
@@ -89,18 +97,113 @@ void declareFlashAttention(py::module_ &m, const std::string &suffix) {
         .def("clone", &FA::clone, "A new layer with the same configuration and no cache.");
 }
 
+// The Layer base class (ModuleLayer.cu:15-91), bound as <suffix>Module.
+template <typename DType>
+void declareModule(py::module_ &m, const std::string &suffix) {
+    using L = Layer<DType>;
+    py::class_<L, std::shared_ptr<L>>(m, (suffix + "Module").c_str(),
+                                      "Abstract layer: forward, backward, parameters, gradients, SGD.")
+        .def("forward", &L::forward, py::arg("input"), "Runs the layer on `input`.")
+        .def("backward", &L::backward, py::arg("input"), py::arg("grad_output"),
+             "Backpropagates `grad_output`, accumulating parameter gradients; returns the input gradient.")
+        .def("getParameters", &L::getParameters, "Parameter tensors by name (shared buffers).")
+        .def("setParameters", &L::setParameters, py::arg("params"), "Adopts the given parameter tensors.")
+        .def("getGradients", &L::getGradients, "Gradient tensors by name (shared buffers).")
+        .def("zeroGrad", &L::zeroGrad, "Zeroes the accumulated gradients.")
+        .def("sgdUpdate", &L::sgdUpdate, py::arg("lr"), "param -= lr * grad for every parameter.")
+        .def("clone", &L::clone, "Deep copy of the layer's parameters.")
+        .def("__call__", &L::operator(), py::arg("input"), "Shorthand for forward(input).");
+}
+
+// AttentionLayer (cuda_transformer.cu:257-324).
+template <typename DType>
+void declareAttention(py::module_ &m, const std::string &suffix) {
+    using A = AttentionLayer<DType>;
+    using T = Tensor<DType>;
+    py::class_<A, Layer<DType>, std::shared_ptr<A>>(
+        m, (suffix + "AttentionLayer").c_str(),
+        "Multi-head attention: QKV projection -> flash attention -> output projection.\n"
+        "All get/set methods are shallow (shared GPU buffer).  Q/K/V weight shape [headDim*numHeads, inputDim]\n"
+        "(row j = output feature j); output weight shape [inputDim, headDim*numHeads].")
+        .def(py::init<int, int, int, bool>(), py::arg("input_dim"), py::arg("num_heads"), py::arg("head_dim"),
+             py::arg("causal") = false)
+        .def_readonly("inputDim", &A::inputDim)
+        .def_readonly("numHeads", &A::numHeads)
+        .def_readonly("headDim", &A::headDim)
+        .def_property_readonly("causal", &A::causal)
+        .def("forward", static_cast<T (A::*)(T)>(&A::forward), py::arg("input"),
+             "QKV projection -> attention -> output projection; returns [batch, seq, inputDim].")
+        .def("forward_caching",
+             [](A &layer, T input) {
+                 std::array<T, 4> states;
+                 T out = layer.forward(input, states.data());
+                 py::list py_states;
+                 for (auto &st : states) py_states.append(st);
+                 return py::make_tuple(out, py_states);
+             },
+             py::arg("input"), "Returns (output, [Q, K, V, attention output]).")
+        .def("backward", static_cast<T (A::*)(T, T)>(&A::backward), py::arg("input"), py::arg("grad_output"),
+             "Recomputes the forward, backpropagates, accumulates every parameter gradient; returns dInput.")
+        .def("backward_caching",
+             [](A &layer, T input, T gradOutput, py::list py_states) {
+                 if (py_states.size() != 4) throw std::runtime_error("States list must have exactly 4 Tensors");
+                 std::array<T, 4> states;
+                 for (size_t i = 0; i < 4; ++i) states[i] = py_states[i].cast<T>();
+                 return layer.backward(input, gradOutput, states.data());
+             },
+             py::arg("input"), py::arg("grad_output"), py::arg("states"),
+             "Backpropagates using the states [Q, K, V, attention output] from forward_caching.")
+        .def("sgdUpdate", &A::sgdUpdate, py::arg("lr"), "SGD on all eight parameter buffers.")
+        .def("zeroGrad", &A::zeroGrad, "Zeroes the accumulated gradients.")
+        .def("getQueryWeights", &A::getQueryWeights)
+        .def("setQueryWeights", &A::setQueryWeights, py::arg("tensor"))
+        .def("getQueryBiases", &A::getQueryBiases)
+        .def("setQueryBiases", &A::setQueryBiases, py::arg("tensor"))
+        .def("getKeyWeights", &A::getKeyWeights)
+        .def("setKeyWeights", &A::setKeyWeights, py::arg("tensor"))
+        .def("getKeyBiases", &A::getKeyBiases)
+        .def("setKeyBiases", &A::setKeyBiases, py::arg("tensor"))
+        .def("getValueWeights", &A::getValueWeights)
+        .def("setValueWeights", &A::setValueWeights, py::arg("tensor"))
+        .def("getValueBiases", &A::getValueBiases)
+        .def("setValueBiases", &A::setValueBiases, py::arg("tensor"))
+        .def("getOutputWeights", &A::getOutputWeights)
+        .def("setOutputWeights", &A::setOutputWeights, py::arg("tensor"))
+        .def("getOutputBiases", &A::getOutputBiases)
+        .def("setOutputBiases", &A::setOutputBiases, py::arg("tensor"))
+        .def("__call__", &A::operator(), py::arg("input"), "Shorthand for forward(input).");
+    m.def(("Attention" + suffix).c_str(),
+          [](int inputDim, int numHeads, int headDim, bool causal) {
+              return std::make_shared<A>(inputDim, numHeads, headDim, causal);
+          },
+          py::arg("input_dim"), py::arg("num_heads"), py::arg("head_dim"), py::arg("causal") = false,
+          "Creates a multi-head AttentionLayer (QKV projection + flash attention + output projection).");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(cuda_transformer, m) {
     m.doc() =
         "cuda_transformer (MI355X): the flash-attention path of CudaTransformer on gfx950 HIP kernels.\n"
-        "Tensors: FloatTensor, BFloatTensor.  Attention core: FloatFlashAttentionLayer,\n"
-        "BFloatFlashAttentionLayer, FlashAttention(head_dim, num_heads, causal=False).";
+        "Tensors: FloatTensor, BFloatTensor.  Layers: FloatModule / BFloatModule (base),\n"
+        "FloatAttentionLayer / BFloatAttentionLayer (AttentionFloat, AttentionBFloat, Attention),\n"
+        "FloatFlashAttentionLayer / BFloatFlashAttentionLayer (FlashAttention(head_dim, num_heads,\n"
+        "causal=False)).";
 
     declareTensor<float>(m, "Float");
     declareTensor<bf16>(m, "BFloat");
     declareFlashAttention<float>(m, "Float");
     declareFlashAttention<bf16>(m, "BFloat");
+    declareModule<float>(m, "Float");
+    declareModule<bf16>(m, "BFloat");
+    declareAttention<float>(m, "Float");
+    declareAttention<bf16>(m, "BFloat");
+    m.def("Attention",
+          [](int inputDim, int numHeads, int headDim, bool causal) {
+              return std::make_shared<AttentionLayer<float>>(inputDim, numHeads, headDim, causal);
+          },
+          py::arg("input_dim"), py::arg("num_heads"), py::arg("head_dim"), py::arg("causal") = false,
+          "Creates a float multi-head AttentionLayer.");
 
     auto makeFloat = [](int headDim, int numHeads, bool causal) {
         return std::make_shared<FlashAttentionLayer<float>>(headDim, numHeads, causal);

@@ -1,0 +1,275 @@
+// C-ABI entry points of the attention layer's projections (declared in include/ctattn.h).
+//
+// Each entry point validates its arguments on the host, describes its products as
+// separable views (row-major [B*T, E] activations, [B, H, T, d] attention tensors, [out][in]
+// weights) and launches the MFMA GEMM family of proj_gemm.hip on the caller's stream.
+#include "capi_util.h"
+#include "ctattn.h"
+#include "proj_launch.h"
+
+#include <algorithm>
+#include <cstdint>
+
+namespace {
+
+using ctattn::GemmParams;
+using ctattn::head_view;
+using ctattn::linear_view;
+using ctattn::MatView;
+using ctattn::capi::align_up;
+using ctattn::capi::fail;
+using ctattn::capi::finish;
+using ctattn::capi::ok;
+
+struct ProjShape {
+    int64_t B, T, E, H, d;
+    int64_t rows() const { return B * T; }
+    int64_t hd() const { return H * d; }
+};
+
+int validate_proj(const char *fn, int dtype, const ProjShape &s) {
+    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (s.B < 0 || s.T < 0)
+        return fail(hipErrorInvalidValue, "%s: negative size B=%lld T=%lld", fn, (long long)s.B,
+                    (long long)s.T);
+    if (s.E < 1 || s.H < 1 || s.d < 1)
+        return fail(hipErrorInvalidValue, "%s: E=%lld H=%lld d=%lld must be >= 1", fn, (long long)s.E,
+                    (long long)s.H, (long long)s.d);
+    // GEMM indices (rows B*T, columns E and H*d) are 32-bit in the kernels.
+    const double lim = 2147483647.0;
+    if (double(s.B) * double(s.T) > lim || double(s.E) > lim || double(s.H) * double(s.d) > lim)
+        return fail(hipErrorInvalidValue, "%s: B*T, E and H*d must each be below 2^31", fn);
+    return 0;
+}
+
+int elem_bytes(int dtype) { return dtype == CTATTN_F32 ? 4 : 2; }
+
+// 4-element vector loads need every pitch / head dim to be a multiple of 4 and every base
+// pointer 4-element aligned.
+bool vec4_ok(int dtype, const ProjShape &s, std::initializer_list<const void *> ptrs) {
+    if (s.E % 4 != 0 || s.d % 4 != 0) return false;
+    const uintptr_t a = uintptr_t(4 * elem_bytes(dtype));
+    for (const void *p : ptrs)
+        if (p != nullptr && uintptr_t(p) % a != 0) return false;
+    return true;
+}
+
+// K splits for a small-output, long-K product (weight gradients): enough workgroups to cover
+// the GPU several times, at least 16 K steps (256 k) per split.
+int choose_splits(int64_t M, int64_t N, int64_t K, int nbatch) {
+    const int64_t tiles = int64_t(ctattn::gemm_tile_count(M, N)) * nbatch;
+    int64_t s = (1024 + tiles - 1) / tiles;
+    s = std::min<int64_t>(s, std::max<int64_t>(1, ctattn::gemm_k_steps(K) / 16));
+    return int(std::max<int64_t>(1, std::min<int64_t>(s, 16)));
+}
+
+int64_t splitk_bytes(int64_t M, int64_t N, int64_t K, int nbatch) {
+    const int s = choose_splits(M, N, K, nbatch);
+    return s > 1 ? align_up(int64_t(s) * nbatch * M * N * int64_t(sizeof(float))) : 0;
+}
+
+GemmParams make_params(int64_t M, int64_t N, int64_t K, int beta, int splits, MatView outv, float *ws) {
+    GemmParams p{};
+    p.M = int32_t(M);
+    p.N = int32_t(N);
+    p.K = int32_t(K);
+    p.beta = beta;
+    p.splits = splits;
+    p.outv = outv;
+    p.ws = ws;
+    return p;
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+int ctattn_qkv_proj_fwd(int dtype, const void *x, const void *wq, const void *wk, const void *wv,
+                        const void *bq, const void *bk, const void *bv, void *q, void *k, void *v,
+                        int64_t B, int64_t T, int64_t E, int64_t H, int64_t d, void *stream) {
+    const char *fn = "ctattn_qkv_proj_fwd";
+    const ProjShape s{B, T, E, H, d};
+    if (int rc = validate_proj(fn, dtype, s)) return rc;
+    if (s.rows() == 0) return ok();
+    if (!x || !wq || !wk || !wv || !q || !k || !v) return fail(hipErrorInvalidValue, "%s: null tensor pointer", fn);
+    // q/k/v(r, j) = sum_i x[r][i] w[j][i] + b[j]: A = x [rows][E] (K-contiguous), B = w [HD][E]
+    // (K-contiguous), out in [B, H, T, d].
+    GemmParams p = make_params(s.rows(), s.hd(), E, 0, 1, head_view(nullptr, T, H, d), nullptr);
+    const void *w[3] = {wq, wk, wv}, *b[3] = {bq, bk, bv};
+    void *o[3] = {q, k, v};
+    for (int z = 0; z < 3; ++z) {
+        p.batch[z].nseg = 1;
+        p.batch[z].a[0] = linear_view(x, E);
+        p.batch[z].b[0] = linear_view(w[z], E);
+        p.batch[z].out = o[z];
+        p.batch[z].bias = b[z];
+    }
+    const bool v4 = vec4_ok(dtype, s, {x, wq, wk, wv, q, k, v});
+    return finish(fn, ctattn::launch_proj_gemm(dtype, p, 3, true, true, v4, as_stream(stream)), as_stream(stream));
+}
+
+int64_t ctattn_qkv_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t E, int64_t H, int64_t d) {
+    const ProjShape s{B, T, E, H, d};
+    if (validate_proj("ctattn_qkv_proj_bwd_workspace_bytes", dtype, s)) return -1;
+    ok();
+    return splitk_bytes(s.hd(), E, s.rows(), 3) +
+           align_up(ctattn::colsum_workspace_floats(s.rows(), s.hd()) * int64_t(sizeof(float)));
+}
+
+int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk, const void *dv,
+                        const void *wq, const void *wk, const void *wv, void *dwq, void *dwk, void *dwv,
+                        void *dbq, void *dbk, void *dbv, void *dx, void *workspace, int64_t workspace_bytes,
+                        int64_t B, int64_t T, int64_t E, int64_t H, int64_t d, void *stream) {
+    const char *fn = "ctattn_qkv_proj_bwd";
+    const ProjShape s{B, T, E, H, d};
+    if (int rc = validate_proj(fn, dtype, s)) return rc;
+    if (s.rows() == 0) return ok();
+    if (!x || !dq || !dk || !dv) return fail(hipErrorInvalidValue, "%s: null x/dq/dk/dv pointer", fn);
+    const bool want_dw = dwq || dwk || dwv, want_db = dbq || dbk || dbv;
+    if (want_dw && !(dwq && dwk && dwv)) return fail(hipErrorInvalidValue, "%s: give all of dwq/dwk/dwv or none", fn);
+    if (want_db && !(dbq && dbk && dbv)) return fail(hipErrorInvalidValue, "%s: give all of dbq/dbk/dbv or none", fn);
+    if (dx && !(wq && wk && wv)) return fail(hipErrorInvalidValue, "%s: dx needs wq/wk/wv", fn);
+    const int64_t need = ctattn_qkv_proj_bwd_workspace_bytes(dtype, B, T, E, H, d);
+    if ((want_dw || want_db) && (workspace == nullptr || workspace_bytes < need))
+        return fail(hipErrorInvalidValue,
+                    "%s: workspace of %lld bytes given, %lld needed (ctattn_qkv_proj_bwd_workspace_bytes)", fn,
+                    (long long)workspace_bytes, (long long)need);
+    hipStream_t st = as_stream(stream);
+    const bool v4 = vec4_ok(dtype, s, {x, dq, dk, dv, wq, wk, wv, dwq, dwk, dwv, dx});
+    const void *g[3] = {dq, dk, dv};
+    hipError_t e = hipSuccess;
+    float *ws = static_cast<float *>(workspace);
+    if (want_dw) {
+        // dw[j][i] += sum_r g(r, j) x[r][i]: M = HD, N = E, K = rows.  A(m=j, k=r) = g stored
+        // [k][m] (head-split), B(k=r, n=i) = x stored [k][n].
+        const int splits = choose_splits(s.hd(), E, s.rows(), 3);
+        GemmParams p = make_params(s.hd(), E, s.rows(), 1, splits, linear_view(nullptr, E), ws);
+        void *o[3] = {dwq, dwk, dwv};
+        for (int z = 0; z < 3; ++z) {
+            p.batch[z].nseg = 1;
+            p.batch[z].a[0] = head_view(g[z], T, H, d);
+            p.batch[z].b[0] = linear_view(x, E);
+            p.batch[z].out = o[z];
+            p.batch[z].bias = nullptr;
+        }
+        e = ctattn::launch_proj_gemm(dtype, p, 3, false, false, v4, st);
+        if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (want_db) {
+        float *cws = reinterpret_cast<float *>(static_cast<char *>(workspace) + splitk_bytes(s.hd(), E, s.rows(), 3));
+        void *o[3] = {dbq, dbk, dbv};
+        for (int z = 0; z < 3 && e == hipSuccess; ++z)
+            e = ctattn::launch_colsum_add(dtype, head_view(g[z], T, H, d), int(s.rows()), int(s.hd()), o[z], cws, st);
+        if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (dx) {
+        // dx[r][i] = sum_z sum_j g_z(r, j) w_z[j][i]: A = g (head-split, K-contiguous), B = w
+        // stored [k][n]; three K segments into one output.
+        GemmParams p = make_params(s.rows(), E, s.hd(), 0, 1, linear_view(nullptr, E), nullptr);
+        const void *w[3] = {wq, wk, wv};
+        p.batch[0].nseg = 3;
+        for (int z = 0; z < 3; ++z) {
+            p.batch[0].a[z] = head_view(g[z], T, H, d);
+            p.batch[0].b[z] = linear_view(w[z], E);
+        }
+        p.batch[0].out = dx;
+        p.batch[0].bias = nullptr;
+        e = ctattn::launch_proj_gemm(dtype, p, 1, true, false, v4, st);
+    }
+    return finish(fn, e, st);
+}
+
+int ctattn_out_proj_fwd(int dtype, const void *c, const void *wo, const void *bo, void *y, int64_t B,
+                        int64_t T, int64_t E, int64_t H, int64_t d, void *stream) {
+    const char *fn = "ctattn_out_proj_fwd";
+    const ProjShape s{B, T, E, H, d};
+    if (int rc = validate_proj(fn, dtype, s)) return rc;
+    if (s.rows() == 0) return ok();
+    if (!c || !wo || !y) return fail(hipErrorInvalidValue, "%s: null tensor pointer", fn);
+    // y[r][e] = sum_c attn(r, c) wo[e][c] + bo[e]: A = attention output (head-split,
+    // K-contiguous), B = wo [E][HD] (K-contiguous).
+    GemmParams p = make_params(s.rows(), E, s.hd(), 0, 1, linear_view(nullptr, E), nullptr);
+    p.batch[0].nseg = 1;
+    p.batch[0].a[0] = head_view(c, T, H, d);
+    p.batch[0].b[0] = linear_view(wo, s.hd());
+    p.batch[0].out = y;
+    p.batch[0].bias = bo;
+    const bool v4 = vec4_ok(dtype, s, {c, wo, y});
+    return finish(fn, ctattn::launch_proj_gemm(dtype, p, 1, true, true, v4, as_stream(stream)), as_stream(stream));
+}
+
+int64_t ctattn_out_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t E, int64_t H, int64_t d) {
+    const ProjShape s{B, T, E, H, d};
+    if (validate_proj("ctattn_out_proj_bwd_workspace_bytes", dtype, s)) return -1;
+    ok();
+    return splitk_bytes(E, s.hd(), s.rows(), 1) +
+           align_up(ctattn::colsum_workspace_floats(s.rows(), E) * int64_t(sizeof(float)));
+}
+
+int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo, void *dwo, void *dbo,
+                        void *dc, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t E,
+                        int64_t H, int64_t d, void *stream) {
+    const char *fn = "ctattn_out_proj_bwd";
+    const ProjShape s{B, T, E, H, d};
+    if (int rc = validate_proj(fn, dtype, s)) return rc;
+    if (s.rows() == 0) return ok();
+    if (!dy) return fail(hipErrorInvalidValue, "%s: null dy pointer", fn);
+    if (dwo && !c) return fail(hipErrorInvalidValue, "%s: dwo needs the attention output c", fn);
+    if (dc && !wo) return fail(hipErrorInvalidValue, "%s: dc needs wo", fn);
+    const int64_t need = ctattn_out_proj_bwd_workspace_bytes(dtype, B, T, E, H, d);
+    if ((dwo || dbo) && (workspace == nullptr || workspace_bytes < need))
+        return fail(hipErrorInvalidValue,
+                    "%s: workspace of %lld bytes given, %lld needed (ctattn_out_proj_bwd_workspace_bytes)", fn,
+                    (long long)workspace_bytes, (long long)need);
+    hipStream_t st = as_stream(stream);
+    const bool v4 = vec4_ok(dtype, s, {c, dy, wo, dwo, dc});
+    float *ws = static_cast<float *>(workspace);
+    hipError_t e = hipSuccess;
+    if (dwo) {
+        // dwo[e][c] += sum_r dy[r][e] attn(r, c): M = E, N = HD, K = rows.  A(m=e, k=r) = dy
+        // stored [k][m]; B(k=r, n=c) = attention output stored [k][n] (head-split).
+        const int splits = choose_splits(E, s.hd(), s.rows(), 1);
+        GemmParams p = make_params(E, s.hd(), s.rows(), 1, splits, linear_view(nullptr, s.hd()), ws);
+        p.batch[0].nseg = 1;
+        p.batch[0].a[0] = linear_view(dy, E);
+        p.batch[0].b[0] = head_view(c, T, H, d);
+        p.batch[0].out = dwo;
+        p.batch[0].bias = nullptr;
+        e = ctattn::launch_proj_gemm(dtype, p, 1, false, false, v4, st);
+        if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (dbo) {
+        float *cws = reinterpret_cast<float *>(static_cast<char *>(workspace) + splitk_bytes(E, s.hd(), s.rows(), 1));
+        e = ctattn::launch_colsum_add(dtype, linear_view(dy, E), int(s.rows()), int(E), dbo, cws, st);
+        if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (dc) {
+        // dc(r, c) = sum_e dy[r][e] wo[e][c]: A = dy (K-contiguous), B = wo stored [k][n]; out
+        // in [B, H, T, d].
+        GemmParams p = make_params(s.rows(), s.hd(), E, 0, 1, head_view(nullptr, T, H, d), nullptr);
+        p.batch[0].nseg = 1;
+        p.batch[0].a[0] = linear_view(dy, E);
+        p.batch[0].b[0] = linear_view(wo, s.hd());
+        p.batch[0].out = dc;
+        p.batch[0].bias = nullptr;
+        e = ctattn::launch_proj_gemm(dtype, p, 1, true, false, v4, st);
+    }
+    return finish(fn, e, st);
+}
+
+int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n, void *stream) {
+    const char *fn = "ctattn_sgd_update";
+    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (n < 0) return fail(hipErrorInvalidValue, "%s: negative size %lld", fn, (long long)n);
+    if (n == 0) return ok();
+    if (!params || !grads) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    if (double(n) > 2147483647.0 * 256.0) return fail(hipErrorInvalidValue, "%s: n too large", fn);
+    hipStream_t st = as_stream(stream);
+    return finish(fn, ctattn::launch_sgd(dtype, params, grads, lr, n, st), st);
+}
+
+}  // extern "C"

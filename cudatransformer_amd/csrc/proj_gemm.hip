@@ -1,0 +1,391 @@
+// MFMA GEMMs of the attention layer's projections (fp32 MFMA v_mfma_f32_32x32x2f32, gfx950).
+//
+// Replaces the reference's shared-memory-tiled scalar projection kernels
+// (attention_qkv_kernels.cu:51-364: getQKVmatrices, qkvBackwardWB, qkvBackward;
+// attention_proj_kernels.cu:48-290: attentionProj, projBackwardWB, projBackward).  All six
+// products are one kernel family:
+//
+//     out(m, n) [+]= sum_k A(m, k) B(k, n)   (+ bias(n))
+//
+// where every operand is a separable 2-D view of memory, element (i, j) at
+// base + row_off(i) + col_off(j), with either plain row-major offsets (i * ld, j) or the
+// head-split offsets of a [B, H, T, d] tensor seen as a [B*T, H*d] matrix:
+//     row_off(r) = ((r / T) * H * T + r % T) * d,   col_off(c) = (c / d) * T * d + c % d.
+// So the QKV projection writes Q/K/V in attention layout and the output projection reads the
+// attention output in place: no transpose kernels, no extra HBM passes.
+//
+// Tiling: a workgroup (4 waves) computes a 128 x 128 tile of out, each wave a 64 x 64 block
+// as 2 x 2 32x32 MFMA tiles, over K in steps of 16.  Operand tiles are staged global ->
+// registers -> LDS (double-buffered, one barrier per step; the next step's global loads are
+// in flight during this step's MFMAs).  A K-contiguous operand is stored [row][k] in LDS
+// and read as float4 along k; an M/N-contiguous one is stored [k][row] and read per element
+// -- each lane (i, h) feeds MFMA (s, t) with k = 8s + 4h + t for both operands, which is a
+// valid pairing of the 32x32x2 instruction's two k slots.  Storage may be fp32 or bf16; bf16
+// is widened to fp32 on its way into LDS, arithmetic is fp32 throughout.
+//
+// Weight gradients (K = B*T, small M x N) split K over several workgroups; the partial
+// tiles go to a workspace and a second kernel adds them in a fixed order (deterministic,
+// no atomics).  Bias gradients are column sums, also two-stage and deterministic.
+#include "proj_launch.h"
+
+#include "attn_common.h"
+#include "attn_mfma_common.h"
+
+namespace ctattn {
+namespace {
+
+constexpr int kBM = 128, kBN = 128, kBK = 16;
+constexpr int kThreads = 256;
+
+template <typename T> __device__ __forceinline__ float load_f(const T *p);
+template <> __device__ __forceinline__ float load_f<float>(const float *p) { return *p; }
+template <> __device__ __forceinline__ float load_f<uint16_t>(const uint16_t *p) {
+    return __uint_as_float(uint32_t(*p) << 16);
+}
+template <typename T> __device__ __forceinline__ floatx4 load4_f(const T *p);
+template <> __device__ __forceinline__ floatx4 load4_f<float>(const float *p) {
+    return *reinterpret_cast<const floatx4 *>(p);
+}
+template <> __device__ __forceinline__ floatx4 load4_f<uint16_t>(const uint16_t *p) {
+    typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+    const u16x4 u = *reinterpret_cast<const u16x4 *>(p);
+    return floatx4{__uint_as_float(uint32_t(u[0]) << 16), __uint_as_float(uint32_t(u[1]) << 16),
+                   __uint_as_float(uint32_t(u[2]) << 16), __uint_as_float(uint32_t(u[3]) << 16)};
+}
+template <typename T> __device__ __forceinline__ void store_f(T *p, float x);
+template <> __device__ __forceinline__ void store_f<float>(float *p, float x) { *p = x; }
+template <> __device__ __forceinline__ void store_f<uint16_t>(uint16_t *p, float x) { *p = f32_to_bf16(x).bits; }
+
+// Indices are < 2^31 (checked on the host), so the divisions are 32-bit.
+__device__ __forceinline__ int64_t view_row_off(const MatView &v, int i) {
+    if (v.kind == kViewLinear) return int64_t(i) * v.ld;
+    return (int64_t(i / v.T) * v.H * v.T + i % v.T) * v.d;
+}
+__device__ __forceinline__ int64_t view_col_off(const MatView &v, int j) {
+    if (v.kind == kViewLinear) return j;
+    return int64_t(j / v.d) * v.T * v.d + j % v.d;
+}
+
+// Loads one operand tile (rows = the operand's M or N index, k = its K index) into registers.
+// KC: the operand is K-contiguous in memory (storage rows = tile rows, storage cols = k);
+// otherwise storage rows = k and storage cols = tile rows.  VEC elements per load.  The
+// tile-row part of each address (with its integer divisions for head-split views) is fixed
+// for the whole K loop and computed once in init().
+template <typename T, bool KC, int VEC>
+struct TileLoader {
+    static constexpr int LOADS = kBM * kBK / VEC / kThreads;  // per thread
+    floatx4 reg[LOADS];
+    int64_t rpart[LOADS];  // offset of this load's tile row; -1 when the row is out of range
+
+    __device__ __forceinline__ static void coords(int tid, int i, int &r, int &kk) {
+        const int e = (tid + i * kThreads) * VEC;  // element index in the tile, storage-row-major
+        if (KC) {  // storage [row][k]: 16 k per row
+            r = e / kBK;
+            kk = e % kBK;
+        } else {  // storage [k][row]: 128 rows per k
+            kk = e / kBM;
+            r = e % kBM;
+        }
+    }
+
+    __device__ __forceinline__ void init(const MatView &v, int row0, int nrows, int tid) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            int r, kk;
+            coords(tid, i, r, kk);
+            rpart[i] = row0 + r < nrows ? (KC ? view_row_off(v, row0 + r) : view_col_off(v, row0 + r)) : -1;
+        }
+    }
+
+    // VEC = 4: KC -> 4 consecutive k of one row; !KC -> 4 consecutive rows of one k.  Callers
+    // guarantee every extent is a multiple of 4, so a vector is wholly in or out of range.
+    __device__ __forceinline__ void load(const MatView &v, int k0, int kend, int tid) {
+        const T *base = static_cast<const T *>(v.p);
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            int r, kk;
+            coords(tid, i, r, kk);
+            floatx4 x = {0.f, 0.f, 0.f, 0.f};
+            if (rpart[i] >= 0 && k0 + kk < kend) {
+                const int64_t off = rpart[i] + (KC ? view_col_off(v, k0 + kk) : view_row_off(v, k0 + kk));
+                if (VEC == 4) x = load4_f<T>(base + off);
+                else x[0] = load_f<T>(base + off);
+            }
+            reg[i] = x;
+        }
+    }
+
+    // LDS layouts: KC -> [row][KS] with KS = 20 (float4-aligned, conflict-light float4 reads);
+    // !KC -> [k][MS] with MS = 132.
+    static constexpr int KS = kBK + 4;
+    static constexpr int MS = kBM + 4;
+    static constexpr int LDS_FLOATS = KC ? kBM * KS : kBK * MS;
+
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int e = (tid + i * kThreads) * VEC;
+            if (KC) {
+                const int r = e / kBK, kk = e % kBK;
+                if (VEC == 4) *reinterpret_cast<floatx4 *>(lds + r * KS + kk) = reg[i];
+                else lds[r * KS + kk] = reg[i][0];
+            } else {
+                const int kk = e / kBM, r = e % kBM;
+                if (VEC == 4) *reinterpret_cast<floatx4 *>(lds + kk * MS + r) = reg[i];
+                else lds[kk * MS + r] = reg[i][0];
+            }
+        }
+    }
+
+    // Operand values of lane (row rl, half h) for the four MFMAs of k-group s: k = 8s + 4h + t.
+    __device__ __forceinline__ static floatx4 fetch(const float *lds, int rl, int s, int h) {
+        if (KC) return *reinterpret_cast<const floatx4 *>(lds + rl * KS + 8 * s + 4 * h);
+        floatx4 x;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[t] = lds[(8 * s + 4 * h + t) * MS + rl];
+        return x;
+    }
+};
+
+template <typename T, bool A_KC, bool B_KC, int VEC>
+__global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
+    using LA = TileLoader<T, A_KC, VEC>;
+    using LB = TileLoader<T, B_KC, VEC>;
+    __shared__ __attribute__((aligned(16))) float a_lds[2][LA::LDS_FLOATS];
+    __shared__ __attribute__((aligned(16))) float b_lds[2][LB::LDS_FLOATS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    const int m0 = blockIdx.x * kBM;
+    const int n0 = blockIdx.y * kBN;
+    const int batch = blockIdx.z / prm.splits;
+    const int split = blockIdx.z % prm.splits;
+    const GemmBatch &bt = prm.batch[batch];
+
+    // Flat list of K steps over the segments: step st -> segment st / nks, k0 = (st % nks) * BK.
+    const int nks = (prm.K + kBK - 1) / kBK;
+    const int total = bt.nseg * nks;
+    const int per = (total + prm.splits - 1) / prm.splits;
+    const int st_begin = split * per;
+    const int st_end = min(total, st_begin + per);
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+
+    // Every segment's views share their kind and shape (only the base pointer differs), so
+    // the row parts computed from segment 0 hold for all of them.
+    LA la;
+    LB lb;
+    la.init(bt.a[0], m0, prm.M, tid);
+    lb.init(bt.b[0], n0, prm.N, tid);
+    auto load_step = [&](int st) {
+        const int seg = st / nks;
+        const int k0 = (st % nks) * kBK;
+        la.load(bt.a[seg], k0, prm.K, tid);
+        lb.load(bt.b[seg], k0, prm.K, tid);
+    };
+
+    if (st_begin < st_end) load_step(st_begin);
+    for (int st = st_begin; st < st_end; ++st) {
+        const int buf = (st - st_begin) & 1;
+        la.store(a_lds[buf], tid);
+        lb.store(b_lds[buf], tid);
+        // One barrier per step: buffer `buf` was last read two steps ago, before the previous
+        // step's barrier, so the stores above cannot race with readers.
+        __syncthreads();
+        if (st + 1 < st_end) load_step(st + 1);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            floatx4 a4[2], b4[2];
+#pragma unroll
+            for (int tm = 0; tm < 2; ++tm) a4[tm] = LA::fetch(a_lds[buf], wm * 64 + tm * 32 + col, s, half);
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) b4[tn] = LB::fetch(b_lds[buf], wn * 64 + tn * 32 + col, s, half);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+                    for (int tn = 0; tn < 2; ++tn)
+                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[tm][t], b4[tn][t], acc[tm][tn], 0, 0, 0);
+        }
+    }
+
+    // Epilogue.  acc[tm][tn]: lane (col, half), register r holds out row acc_row(r, half),
+    // column col of the 32x32 tile.  The MFMA's A operand is the row index here (A = rows of
+    // out), B the column: D[i][j] = sum_k A[i][k] B[k][j].
+    if (prm.splits > 1) {
+        float *ws = prm.ws + int64_t(blockIdx.z) * prm.M * prm.N;
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                const int n = n0 + wn * 64 + tn * 32 + col;
+                if (n >= prm.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + tm * 32 + acc_row(r, half);
+                    if (m < prm.M) ws[int64_t(m) * prm.N + n] = acc[tm][tn][r];
+                }
+            }
+        return;
+    }
+    T *out = static_cast<T *>(bt.out);
+    const T *bias = static_cast<const T *>(bt.bias);
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+        const int n = n0 + wn * 64 + tn * 32 + col;
+        if (n >= prm.N) continue;
+        const float bn = bias != nullptr ? load_f<T>(bias + n) : 0.f;
+        const int64_t coff = view_col_off(prm.outv, n);
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + tm * 32 + acc_row(r, half);
+                if (m >= prm.M) continue;
+                T *p = out + view_row_off(prm.outv, m) + coff;
+                float x = acc[tm][tn][r] + bn;
+                if (prm.beta) x += load_f<T>(p);
+                store_f<T>(p, x);
+            }
+        }
+    }
+}
+
+// out(m, n) [+]= sum_s ws[batch][s][m][n], s in increasing order.
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams prm) {
+    const int64_t mn = int64_t(prm.M) * prm.N;
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int batch = blockIdx.y;
+    if (idx >= mn) return;
+    const int m = int(idx / prm.N), n = int(idx % prm.N);
+    const float *ws = prm.ws + int64_t(batch) * prm.splits * mn + idx;
+    float x = 0.f;
+    for (int s = 0; s < prm.splits; ++s) x += ws[int64_t(s) * mn];
+    const GemmBatch &bt = prm.batch[batch];
+    T *p = static_cast<T *>(bt.out) + view_row_off(prm.outv, m) + view_col_off(prm.outv, n);
+    if (bt.bias != nullptr) x += load_f<T>(static_cast<const T *>(bt.bias) + n);
+    if (prm.beta) x += load_f<T>(p);
+    store_f<T>(p, x);
+}
+
+// Column sums, stage 1: part[rb][c] = sum of rows rb*kColRows .. +kColRows-1 of column c.
+// 256 threads = 64 columns x 4 row lanes; rows are summed in a fixed order.
+constexpr int kColRows = 256;
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, int C, float *part) {
+    __shared__ float red[4][64];
+    const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
+    const int r0 = blockIdx.y * kColRows;
+    const T *base = static_cast<const T *>(g.p);
+    float s = 0.f;
+    if (c < C) {
+        const int64_t coff = view_col_off(g, c);
+        for (int r = r0 + rl; r < min(R, r0 + kColRows); r += 4) s += load_f<T>(base + view_row_off(g, r) + coff);
+    }
+    red[rl][cl] = s;
+    __syncthreads();
+    if (rl == 0 && c < C) part[int64_t(blockIdx.y) * C + c] = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
+}
+
+// Stage 2: out[c] += sum over row blocks of part[rb][c], in increasing rb.
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_final_kernel(const float *part, int nrb, int C, T *out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    float s = 0.f;
+    for (int rb = 0; rb < nrb; ++rb) s += part[int64_t(rb) * C + c];
+    store_f<T>(out + c, load_f<T>(out + c) + s);
+}
+
+// params[i] -= lr * grads[i]  (headers.cu:249-275: sgdUpdateKernel / runSgdUpdate).
+template <typename T>
+__global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, float lr, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    store_f<T>(params + i, load_f<T>(params + i) - lr * load_f<T>(grads + i));
+}
+
+template <typename T, bool A_KC, bool B_KC>
+hipError_t launch_gemm_t(const GemmParams &prm, int nbatch, bool vec4, hipStream_t stream) {
+    const dim3 grid(unsigned((prm.M + kBM - 1) / kBM), unsigned((prm.N + kBN - 1) / kBN),
+                    unsigned(nbatch * prm.splits));
+    if (vec4)
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4>), grid, dim3(kThreads), 0, stream, prm);
+    else
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 1>), grid, dim3(kThreads), 0, stream, prm);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || prm.splits == 1) return e;
+    const int64_t mn = int64_t(prm.M) * prm.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel<T>, dim3(unsigned((mn + 255) / 256), unsigned(nbatch)), dim3(256), 0,
+                       stream, prm);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_gemm_dt(const GemmParams &prm, int nbatch, bool a_kc, bool b_kc, bool vec4,
+                          hipStream_t stream) {
+    if (a_kc && b_kc) return launch_gemm_t<T, true, true>(prm, nbatch, vec4, stream);
+    if (a_kc && !b_kc) return launch_gemm_t<T, true, false>(prm, nbatch, vec4, stream);
+    if (!a_kc && !b_kc) return launch_gemm_t<T, false, false>(prm, nbatch, vec4, stream);
+    return launch_gemm_t<T, false, true>(prm, nbatch, vec4, stream);
+}
+
+}  // namespace
+
+int gemm_tile_count(int64_t M, int64_t N) { return int(((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN)); }
+int gemm_k_steps(int64_t K) { return int((K + kBK - 1) / kBK); }
+
+hipError_t launch_proj_gemm(int dtype, const GemmParams &prm, int nbatch, bool a_kc, bool b_kc,
+                            bool vec4, hipStream_t stream) {
+    if (prm.M <= 0 || prm.N <= 0 || nbatch <= 0) return hipSuccess;
+    if (dtype == 0) return launch_gemm_dt<float>(prm, nbatch, a_kc, b_kc, vec4, stream);
+    return launch_gemm_dt<uint16_t>(prm, nbatch, a_kc, b_kc, vec4, stream);
+}
+
+int64_t colsum_workspace_floats(int64_t R, int64_t C) { return ((R + kColRows - 1) / kColRows) * C; }
+
+hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *out, float *ws,
+                             hipStream_t stream) {
+    if (R <= 0 || C <= 0) return hipSuccess;
+    const int nrb = (R + kColRows - 1) / kColRows;
+    const dim3 grid1(unsigned((C + 63) / 64), unsigned(nrb));
+    if (dtype == 0)
+        hipLaunchKernelGGL(colsum_partial_kernel<float>, grid1, dim3(256), 0, stream, g, R, C, ws);
+    else
+        hipLaunchKernelGGL(colsum_partial_kernel<uint16_t>, grid1, dim3(256), 0, stream, g, R, C, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid2(unsigned((C + 255) / 256));
+    if (dtype == 0)
+        hipLaunchKernelGGL(colsum_final_kernel<float>, grid2, dim3(256), 0, stream, ws, nrb, C, static_cast<float *>(out));
+    else
+        hipLaunchKernelGGL(colsum_final_kernel<uint16_t>, grid2, dim3(256), 0, stream, ws, nrb, C,
+                           static_cast<uint16_t *>(out));
+    return hipGetLastError();
+}
+
+hipError_t launch_sgd(int dtype, void *params, const void *grads, float lr, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid(unsigned((n + 255) / 256));
+    if (dtype == 0)
+        hipLaunchKernelGGL(sgd_kernel<float>, grid, dim3(256), 0, stream, static_cast<float *>(params),
+                           static_cast<const float *>(grads), lr, n);
+    else
+        hipLaunchKernelGGL(sgd_kernel<uint16_t>, grid, dim3(256), 0, stream, static_cast<uint16_t *>(params),
+                           static_cast<const uint16_t *>(grads), lr, n);
+    return hipGetLastError();
+}
+
+}  // namespace ctattn

@@ -95,6 +95,83 @@ CTATTN_API int ctattn_get_policy(void);
 /* Library version, major * 10000 + minor * 100 + patch. */
 CTATTN_API int ctattn_version(void);
 
+/* ---- Attention-layer projections (the producer and consumer of the [B, H, T, d] layout) ----
+ *
+ * x, dx, y, dy: [B, T, E] row-major.  q, k, v, dq, dk, dv, c (the attention output), dc:
+ * [B, H, T, d].  wq, wk, wv: [H*d][E] (row j holds the weights of output feature j, as the
+ * reference's kernels index them, attention_qkv_kernels.cu:92; its getter's [E, H*d] shape
+ * is only a label).  wo: [E][H*d].  bq, bk, bv: [H*d]; bo: [E].  Same dtype codes as above;
+ * all arithmetic accumulates in fp32.  E >= 1, H >= 1, d >= 1 (any values; multiples of 4
+ * take the vectorised loads), B*T, E and H*d below 2^31.  Asynchronous on `stream`.
+ */
+
+/*
+ * q/k/v = x W^T + b, written straight into [B, H, T, d].  Bias pointers may be NULL (no bias).
+ * Replaces the getQKVmatrices launch of QKVProjectionLayer::computeQKV
+ * (QKVProjectionLayer.cu:82-87; kernel attention_qkv_kernels.cu:51-122).
+ */
+CTATTN_API int ctattn_qkv_proj_fwd(int dtype, const void *x, const void *wq, const void *wk,
+                                   const void *wv, const void *bq, const void *bk, const void *bv,
+                                   void *q, void *k, void *v, int64_t B, int64_t T, int64_t E,
+                                   int64_t H, int64_t d, void *stream);
+
+/* Workspace bytes ctattn_qkv_proj_bwd needs (>= 0), or -1 on invalid arguments. */
+CTATTN_API int64_t ctattn_qkv_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t E,
+                                                       int64_t H, int64_t d);
+
+/*
+ * Backward of the QKV projection:
+ *   dwq/dwk/dwv += dq/dk/dv^T x   (accumulated into the existing gradient, like the
+ *                                  reference's atomicAdd into weightsQueryGrad etc.)
+ *   dbq/dbk/dbv += column sums of dq/dk/dv over all B*T rows
+ *   dx = dq wq + dk wk + dv wv     (overwritten)
+ * Pass NULL for all three dw (or all three db, or dx) to skip that part; the workspace is
+ * only needed for dw / db.  Replaces the qkvBackwardWB and qkvBackward launches of
+ * QKVProjectionLayer::computeBackward (QKVProjectionLayer.cu:124-137; kernels
+ * attention_qkv_kernels.cu:171-364).  Unlike the reference's bias gradient, which sums only
+ * the first row of each 32-row tile (attention_qkv_kernels.cu:233-237), every row counts.
+ * Deterministic: no atomics.
+ */
+CTATTN_API int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk,
+                                   const void *dv, const void *wq, const void *wk, const void *wv,
+                                   void *dwq, void *dwk, void *dwv, void *dbq, void *dbk, void *dbv,
+                                   void *dx, void *workspace, int64_t workspace_bytes, int64_t B,
+                                   int64_t T, int64_t E, int64_t H, int64_t d, void *stream);
+
+/*
+ * y = c wo^T + bo, reading the attention output c in [B, H, T, d]; bo may be NULL.
+ * Replaces the attentionProj launch of OutputProjectionLayer::forward
+ * (OutputProjectionLayer.cu:60-63; kernel attention_proj_kernels.cu:48-98).
+ */
+CTATTN_API int ctattn_out_proj_fwd(int dtype, const void *c, const void *wo, const void *bo, void *y,
+                                   int64_t B, int64_t T, int64_t E, int64_t H, int64_t d,
+                                   void *stream);
+
+/* Workspace bytes ctattn_out_proj_bwd needs (>= 0), or -1 on invalid arguments. */
+CTATTN_API int64_t ctattn_out_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int64_t E,
+                                                       int64_t H, int64_t d);
+
+/*
+ * Backward of the output projection:
+ *   dwo += dy^T c,  dbo += column sums of dy,  dc = dy wo  (dc in [B, H, T, d], overwritten).
+ * dwo, dbo or dc may be NULL to skip; the workspace is only needed for dwo / dbo.  Replaces
+ * the projBackwardWB and projBackward launches of OutputProjectionLayer::backward
+ * (OutputProjectionLayer.cu:83-94; kernels attention_proj_kernels.cu:142-288), with every
+ * row in the bias gradient (the reference's sums one row per 32-row tile,
+ * attention_proj_kernels.cu:188,194-196).  Deterministic.
+ */
+CTATTN_API int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo,
+                                   void *dwo, void *dbo, void *dc, void *workspace,
+                                   int64_t workspace_bytes, int64_t B, int64_t T, int64_t E,
+                                   int64_t H, int64_t d, void *stream);
+
+/*
+ * params[i] -= lr * grads[i] for i < n.  Replaces runSgdUpdate / sgdUpdateKernel
+ * (headers.cu:249-275), which every layer's sgdUpdate calls (AttentionLayer.cu:326-333).
+ */
+CTATTN_API int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n,
+                                 void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,7 +47,7 @@ def test_exports_nothing_else(lib):
 
 
 def test_version(lib):
-    assert lib.ctattn_version() == 100
+    assert lib.ctattn_version() == 200
 
 
 def test_bad_dtype_rejected(lib):

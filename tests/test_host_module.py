@@ -19,7 +19,7 @@ def test_api_surface():
                  "FlashAttention", "FlashAttentionFloat", "FlashAttentionBFloat", "synchronize",
                  "set_policy", "version"):
         assert hasattr(ctm, name), name
-    assert ctm.version() == 100
+    assert ctm.version() == 200
     layer = ctm.FloatFlashAttentionLayer(64, 12)
     assert (layer.headDim, layer.numHeads, layer.causal) == (64, 12, False)
     layer.causal = True
