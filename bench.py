@@ -20,7 +20,8 @@ import os
 import sys
 
 # Workloads.  The default, c3, is the headline metric; c4 is the
-# bf16 long-context config, reported separately (python bench.py --workload c4).
+# bf16 long-context config, c5 the NanoGPT training step, and "layer" the reference test's
+# whole attention layer, each reported separately (python bench.py --workload c4).
 WORKLOADS = {
     "c3": dict(B=8, H=12, T=1024, D=64, dtype="f32", std=1.0, peak=157.3,
                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B8 H12 T1024 d64 fp32, 1 GPU",
@@ -28,6 +29,11 @@ WORKLOADS = {
     "c5": dict(B=16, H=6, T=256, D=64, dtype="f32", std=1.0, peak=157.3,
                metric="NanoGPT config-5 training step tokens/s (attention on ctattn), fp32, 1 GPU",
                label="NanoGPT 6L d384 6H T256 B16 vocab65 GELU, Adam lr 3e-4, fp32 (BASELINE configs[4])"),
+    "layer": dict(B=8, H=16, T=1024, D=64, E=1024, dtype="f32", std=1.0, peak=157.3,
+                  metric="attention layer (QKV proj + attention + out proj) fwd+bwd TFLOP/s, "
+                         "B8 N1024 E1024 H16 D64 fp32, 1 GPU",
+                  label="AttentionFloat(input_dim=1024, num_heads=16, head_dim=64) on X[8, 1024, 1024], "
+                        "non-causal, the reference test's configuration (test_flash_attention.py:9-12) at N=1024"),
     "c4": dict(B=1, H=32, T=8192, D=128, dtype="bf16", std=0.5, peak=2516.6,
                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 bf16, 1 GPU",
                label="causal SDPA fwd+bwd, B1 H32 T8192 d128 bf16 in / fp32 accumulate (BASELINE configs[3])"),
@@ -119,6 +125,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "c5":
         return bench_nanogpt(args, wl, dev)
+    if args.workload == "layer":
+        return bench_layer(args, wl)
     if args.copy_calibration:
         n = 64 << 20  # 64 Mi fp32 = 256 MiB read + 256 MiB written per copy
         src = torch.ones(n, device=dev, dtype=torch.float32)
@@ -181,6 +189,7 @@ def main():
     fwd_ms = time_phase(fwd, args.steps)
     bwd_ms = time_phase(bwd, args.steps)
     log(f"fwd: {fwd_ms:.4f} ms  bwd: {bwd_ms:.4f} ms")
+    layer_ms = time_layer_path(q, do, args) if wl["dtype"] == "f32" else None
 
     value = STEP_FLOP / (ms_per_step * 1e-3) / 1e12
     achieved = BWD_FLOP / (bwd_ms * 1e-3) / 1e12
@@ -204,6 +213,10 @@ def main():
             "step_gflop": round(STEP_FLOP / 1e9, 3),
             "fwd_ms": round(fwd_ms, 5),
             "bwd_ms": round(bwd_ms, 5),
+            # The C++ FlashAttentionLayer path (pybind): computeAttention(save_states=True) +
+            # computeBackward per step, output / gradient / workspace allocation included,
+            # host wall clock around synchronised steps.
+            "layer_path_ms": None if layer_ms is None else round(layer_ms, 5),
         },
         "roofline": {
             "bound": "mfma",
@@ -219,6 +232,93 @@ def main():
     if not args.no_cpu_baseline:
         log("timing CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def time_layer_path(q, do, args):
+    """ms per fwd+bwd step of the C++ FlashAttentionLayer through pybind, allocations included."""
+    import time
+
+    import torch
+    from cudatransformer_amd import cuda_transformer as ctm
+
+    g = torch.Generator(device=q.device).manual_seed(3)
+    arrs = [torch.randn(q.shape, generator=g, device=q.device).cpu().numpy() for _ in range(3)]
+    tq, tk, tv = (ctm.FloatTensor.fromNumpy(a) for a in arrs)
+    tdo = ctm.FloatTensor.fromNumpy(do.float().cpu().numpy())
+    layer = ctm.FlashAttention(D, H, CAUSAL)
+
+    def step():
+        layer.computeAttention(tq, tk, tv, True)
+        layer.computeBackward(tq, tk, tv, tdo)
+
+    for _ in range(args.warmup):
+        step()
+    ctm.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctm.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / args.steps
+
+
+def bench_layer(args, wl):
+    """The reference test's AttentionLayer (QKV projection -> attention -> output projection)
+    through the C++ AttentionFloat layer (pybind): forward_caching + backward_caching per
+    step, every output, gradient and workspace allocated by the layer as in real use; host
+    wall clock around synchronised steps."""
+    import time
+
+    import numpy as np
+    import torch
+    from cudatransformer_amd import cuda_transformer as ctm
+
+    b, h, n, d, e = wl["B"], wl["H"], wl["T"], wl["D"], wl["E"]
+    hd = h * d
+    rng = np.random.default_rng(12)
+    layer = ctm.AttentionFloat(input_dim=e, num_heads=h, head_dim=d)
+    for part, shape, scale in (("Query", (hd, e), e), ("Key", (hd, e), e), ("Value", (hd, e), e),
+                               ("Output", (e, hd), hd)):
+        getattr(layer, f"set{part}Weights")(ctm.FloatTensor.fromNumpy(
+            (rng.standard_normal(shape) / np.sqrt(scale)).astype(np.float32)))
+    x = ctm.FloatTensor.fromNumpy(rng.standard_normal((b, n, e)).astype(np.float32))
+    dy = ctm.FloatTensor.fromNumpy(rng.standard_normal((b, n, e)).astype(np.float32))
+
+    def fwd():
+        return layer(x)
+
+    def step():
+        _, states = layer.forward_caching(x)
+        layer.backward_caching(x, dy, states)
+
+    def timed(fn, k):
+        for _ in range(args.warmup):
+            fn()
+        ctm.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(k):
+            fn()
+        ctm.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / k
+
+    fwd_ms = timed(fwd, args.steps)
+    ms = timed(step, args.steps)
+    rows = b * n
+    gemm = 2.0 * rows * hd * e
+    attn_fwd = 4.0 * b * h * n * n * d
+    fwd_flop = 4 * gemm + attn_fwd               # Q, K, V, output projections + attention
+    step_flop = fwd_flop + 8 * gemm + 2.5 * attn_fwd  # + dW and dX of all four, attention bwd
+    value = step_flop / (ms * 1e-3) / 1e12
+    out = {
+        "metric": wl["metric"], "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "pct_of_peak": round(100.0 * value / wl["peak"], 2),
+        "config": {"workload": wl["label"], "B": b, "N": n, "E": e, "H": h, "d": d, "causal": False,
+                   "step_gflop": round(step_flop / 1e9, 3), "fwd_ms": round(fwd_ms, 5),
+                   "fwd_tflops": round(fwd_flop / (fwd_ms * 1e-3) / 1e12, 3)},
+        "roofline": None, "cpu_baseline": None,
+    }
     print(json.dumps(out), flush=True)
 
 
