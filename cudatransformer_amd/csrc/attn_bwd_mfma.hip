@@ -7,25 +7,34 @@
 // a causal mask, no zero-padded keys, and no atomics on dK / dV.
 //
 // Work decomposition ("key-block major")
-//   * one workgroup = 4 waves owns BN = 128 keys of one (batch, head); wave w owns keys
-//     32w .. 32w+31 and accumulates dK^T and dV^T for them in registers for the whole
-//     kernel -- dK / dV are written exactly once, no atomics.
-//   * the workgroup walks query blocks of BM = 32 rows (causal: only rows >= its first
-//     key).  Q, dO, LSE and delta of the block are staged global -> registers -> LDS; the
-//     next block's loads are issued before this block's MFMAs.
+//   * one workgroup = 4 waves owns BN = 64 keys of one (batch, head) and walks query blocks
+//     of BM = 64 rows (causal: only rows >= its first key).  The waves form 2 key slices x
+//     2 row slices: wave (ks, rs) handles keys 32ks..32ks+31 against rows 32rs..32rs+31 of
+//     each query block and accumulates dK^T and dV^T of its keys in registers; the two row
+//     slices' partial sums are added through LDS once at the end, so dK / dV are written
+//     exactly once, without atomics.  With 64-key blocks the causal diagonal leaves one
+//     wave in four idle for one block per workgroup, and there are twice as many, half as
+//     long workgroups as with 128-key blocks, which balances the causal grid.
+//   * Q, dO, LSE and delta of a query block go straight from global memory to LDS
+//     (global_load_lds into rows padded by one 16-byte chunk, no staging registers); the
+//     next block's loads are issued once every wave is past the block's S/dP/dV/dK phase
+//     and land during the dQ phase.
 //   * per wave and query block, with v_mfma_f32_32x32x2f32:
-//       S  = Q K^T      (A = Q from LDS, B = K^T from the LDS K block)
-//       dP = dO V^T     (A = dO from LDS, B = V^T in registers)
+//       S  = Q K^T      (A = Q rows from LDS, B = K^T from the LDS K block)
+//       dP = dO V^T     (A = dO rows from LDS, B = V^T held in registers)
 //     In these accumulators each lane holds ONE key (its column) and 16 query rows, so
 //       P  = exp2(S log2(e)/sqrt(d) - LSE log2(e)),  dS = P (dP - delta)
 //     are elementwise, and P / dS are directly the B operands of
 //       dV^T += dO^T P  and  dK^T += Q^T dS     (A = dO / Q columns from LDS).
 //   * dQ needs dS with rows on lanes: each wave writes its dS tile to LDS, then every wave
-//     computes a quarter of the 32 x d block of dQ = dS K over the workgroup's 128 keys with
-//     v_mfma_f32_16x16x4f32 (A = dS rows from LDS, B = K from LDS).  The slice is either
-//     added with fp32 atomics into dq (DqMode::Atomic; dq pre-zeroed by the preprocess
-//     kernel) or stored into a per-key-block partial buffer that a second kernel sums in a
-//     fixed order (DqMode::Partial; deterministic).
+//     computes a 32-row x (d/2)-column tile of dQ = dS K over the block's 64 keys (d = 32:
+//     two waves, 32 x 32 each) and adds it with fp32 atomics into dq (pre-zeroed by the
+//     preprocess kernel), one iteration later (see flush_dq).
+//
+// Which main kernel runs: this 64-key kernel for causal masks with atomic dQ and d >= 64
+// (where its balance and smaller diagonal win); the 128-key kernel of attn_bwd_k128.hip,
+// with half the dQ atomics, without a mask, at d = 32, and for the deterministic
+// per-key-block dQ partials, which the ordered reduction kernel here then sums.
 #include "attn_launch.h"
 #include "attn_mfma_common.h"
 
@@ -34,53 +43,55 @@
 namespace ctattn {
 namespace {
 
-typedef float floatx4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
 enum class DqMode { Atomic, Partial };
 
 template <int D>
 struct BwdCfg {
     static constexpr int NW = 4;              // waves per workgroup
-    static constexpr int BN = 32 * NW;        // keys per workgroup
-    static constexpr int BM = 32;             // query rows per iteration
-    static constexpr int KS = D + 4;          // LDS row stride (floats) for K, Q, dO
-    static constexpr int SS = BN + 4;         // LDS row stride for dS
+    static constexpr int BN = 64;             // keys per workgroup
+    static constexpr int BM = 64;             // query rows per iteration
+    static constexpr int KS = D + 4;          // LDS row stride (floats) of K, Q and dO
+    static constexpr int SS = BN + 4;         // LDS row stride of dS
     static constexpr int DT = D / 32;         // 32-wide d tiles of dK^T / dV^T
-    static constexpr int F4_ROW = D / 4;
-    static constexpr int QF4 = BM * F4_ROW / (NW * kWave);  // float4 per thread per Q block
-    static constexpr int KF4 = BN * F4_ROW / (NW * kWave);  // float4 per thread for the K block
-    // dQ of one 32-row block is (2 x D/16) 16x16 tiles; each wave takes a quarter: for
-    // d >= 64 both row tiles of a D/4-column slice, for d = 32 one tile
-    // (row tile wave >> 1, column tile wave & 1).
-    static constexpr int DQ_RT = D >= 64 ? 2 : 1;   // 16-row tiles per wave
-    static constexpr int DQ_COLS = D >= 64 ? D / NW : 16;  // dQ columns per wave
-    static constexpr int DQ_CT = DQ_COLS / 16;      // 16-wide column tiles per wave
+    static constexpr int C4 = D / 4;          // 16-byte chunks per row of data
+    static constexpr int C4P = C4 + 1;        // ... per LDS row, including the pad chunk
+    static constexpr int TILE = BM * KS;      // floats per padded Q (or dO) block
+    static constexpr int CHUNKS = BM * C4P;   // 16-byte chunks per padded block
+    static constexpr int INSTR = (CHUNKS + NW * kWave - 1) / (NW * kWave);  // direct loads per lane per tensor
+    static constexpr int KF4 = BN * C4 / (NW * kWave);    // float4 per thread for the K block
+    // dQ of a 64 x D block: d >= 64 -> every wave a 32 x D/2 tile (row slice wave >> 1,
+    // column half wave & 1); d = 32 -> waves 0, 1 a 32 x 32 tile each.
+    static constexpr int DQ_WAVES = D >= 64 ? 4 : 2;
+    static constexpr int DQ_COLS = D >= 64 ? D / 2 : 32;
+    static constexpr int DQ_T = DQ_COLS / 32;  // 32x32 dQ tiles per wave
     static_assert(D == 32 || D == 64 || D == 128, "MFMA backward supports d in {32, 64, 128}");
-    static_assert(DQ_RT * DQ_CT * NW == 2 * (D / 16), "dQ tiles split over the waves");
-    static_assert(QF4 >= 1 && KF4 >= 1, "block load split");
+    static_assert(KF4 * NW * kWave == BN * C4, "block load split");
 };
 
-// S, dP, P, dS and the dV^T / dK^T updates of one wave for one query block, then dS -> LDS.
-// MASK selects the diagonal / sequence-end variant (per-element causal and bounds checks);
-// the unmasked variant carries none.
+#define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Waves per SIMD the kernel is compiled for: two for d <= 64 (<= 256 VGPRs); d = 128 needs
+// more registers than that and runs one wave per SIMD.
+template <int D> struct BwdF32Occupancy { static constexpr int waves = D <= 64 ? 2 : 1; };
+
+// S, dP, P, dS and the dV^T / dK^T updates of wave (ks, rs) for one query block, then its
+// dS tile -> LDS.  rb = 32 rs is the wave's first row in the block, r0w its global index.
+// MASK selects the diagonal / sequence-end variant (per-element causal and bounds checks).
 template <int D, bool MASK>
 __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32],
                                                const float (&vT)[D / 2], const float *q_lds,
                                                const float *do_lds, const float *k_lds,
                                                const float *lse_lds, const float *dl_lds,
-                                               float *ds_lds, int r0, int key, int T, int causal,
-                                               float kscale, int wave, int col, int half) {
+                                               float *ds_lds, int rb, int r0w, int kb_local, int key,
+                                               int T, int causal, float kscale, int col, int half) {
     using C = BwdCfg<D>;
     floatx16 s = zero16(), dp = zero16();
+    const int qrow = rb + col;  // A-operand row of this lane
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
-        const floatx4 qa = *reinterpret_cast<const floatx4 *>(&q_lds[col * C::KS + 8 * m + 4 * half]);
-        const floatx4 da = *reinterpret_cast<const floatx4 *>(&do_lds[col * C::KS + 8 * m + 4 * half]);
-        const floatx4 kb4 = *reinterpret_cast<const floatx4 *>(&k_lds[(32 * wave + col) * C::KS + 8 * m + 4 * half]);
+        const floatx4 qa = *reinterpret_cast<const floatx4 *>(&q_lds[qrow * C::KS + 8 * m + 4 * half]);
+        const floatx4 da = *reinterpret_cast<const floatx4 *>(&do_lds[qrow * C::KS + 8 * m + 4 * half]);
+        const floatx4 kb4 = *reinterpret_cast<const floatx4 *>(&k_lds[(kb_local + col) * C::KS + 8 * m + 4 * half]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             s = mfma32x32x2(qa[t], kb4[t], s);
@@ -89,54 +100,49 @@ __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], float
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const floatx4 l4 = *reinterpret_cast<const floatx4 *>(&lse_lds[8 * g + 4 * half]);
-        const floatx4 d4 = *reinterpret_cast<const floatx4 *>(&dl_lds[8 * g + 4 * half]);
+        const floatx4 l4 = *reinterpret_cast<const floatx4 *>(&lse_lds[rb + 8 * g + 4 * half]);
+        const floatx4 d4 = *reinterpret_cast<const floatx4 *>(&dl_lds[rb + 8 * g + 4 * half]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int r = 4 * g + t;
-            float p = fast_exp2(fmaf(s[r], kscale, -l4[t]));
+            float p = fast_exp2(fmaf(s[r], kscale, l4[t] * -kLog2e));
             if (MASK) {
-                const int row = r0 + acc_row(r, half);
+                const int row = r0w + acc_row(r, half);
                 p = (row >= T || key >= T || (causal && key > row)) ? 0.f : p;
             }
             s[r] = p;
             dp[r] = p * (dp[r] - d4[t]);
         }
     }
-    // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over this block's 32 rows)
+    // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over the wave's 32 rows)
 #pragma unroll
     for (int st = 0; st < 16; ++st) {
-        const int rl = kstep_index(st, half);
+        const int rl = rb + kstep_index(st, half);
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt) {
-            const float a_do = do_lds[rl * C::KS + dt * 32 + col];
-            const float a_q = q_lds[rl * C::KS + dt * 32 + col];
-            dv_acc[dt] = mfma32x32x2(a_do, s[st], dv_acc[dt]);
-            dk_acc[dt] = mfma32x32x2(a_q, dp[st], dk_acc[dt]);
+            const int off = rl * C::KS + dt * 32 + col;
+            dv_acc[dt] = mfma32x32x2(do_lds[off], s[st], dv_acc[dt]);
+            dk_acc[dt] = mfma32x32x2(q_lds[off], dp[st], dk_acc[dt]);
         }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
+    for (int r = 0; r < 16; ++r) ds_lds[(rb + acc_row(r, half)) * C::SS + kb_local + col] = dp[r];
 }
 
-// Waves per SIMD the kernel is compiled for: two for d <= 64 (<= 256 VGPRs); d = 128 needs
-// more registers than that and runs one wave per SIMD.
-template <int D> struct BwdF32Occupancy { static constexpr int waves = D <= 64 ? 2 : 1; };
-
-template <int D, DqMode MODE>
+template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occupancy<D>::waves,
                                                                      BwdF32Occupancy<D>::waves))) void bwd_f32_mfma_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
-    const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dq_part,
-    float *__restrict__ dk, float *__restrict__ dv, int T, int BH, int causal, float kscale,
-    float inv_sqrt_d) {
+    const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dk,
+    float *__restrict__ dv, int T, int BH, int causal, float kscale, float inv_sqrt_d) {
     using C = BwdCfg<D>;
+    __shared__ __attribute__((aligned(16))) float qdo_lds[2 * C::TILE];  // Q then dO, [BM][KS] each
+    float *q_lds = qdo_lds;
+    float *do_lds = qdo_lds + C::TILE;
     __shared__ __attribute__((aligned(16))) float k_lds[C::BN * C::KS];
-    __shared__ __attribute__((aligned(16))) float q_lds[C::BM * C::KS];
-    __shared__ __attribute__((aligned(16))) float do_lds[C::BM * C::KS];
     __shared__ __attribute__((aligned(16))) float ds_lds[C::BM * C::SS];
-    __shared__ __attribute__((aligned(16))) float lse_lds[C::BM];  // log2 units
+    __shared__ __attribute__((aligned(16))) float lse_lds[C::BM];  // natural-log LSE
     __shared__ __attribute__((aligned(16))) float dl_lds[C::BM];   // delta
 
     const int tid = threadIdx.x;
@@ -144,8 +150,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
     const int wave = tid / kWave;
     const int col = lane & 31;
     const int half = lane >> 5;
-    const int c16 = lane & 15;
-    const int quad = lane >> 4;
+    const int ks = wave & 1, rs = wave >> 1;
 
     const int id = blockIdx.x;
     const int bh = id % BH;
@@ -153,22 +158,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
     const int k0 = kb * C::BN;
     const int64_t base = int64_t(bh) * T * D;
     const int64_t rbase = int64_t(bh) * T;
-    const int kw0 = k0 + 32 * wave;
+    const int kw0 = k0 + 32 * ks;
     const int key = kw0 + col;  // key owned by this lane in S / dP / dK^T / dV^T
 
-    // K block -> LDS (B operand of dQ = dS K).
+    // K block -> LDS (B operand of S = Q K^T and of dQ = dS K), rows past T zero.
 #pragma unroll
     for (int i = 0; i < C::KF4; ++i) {
         const int f = tid + i * C::NW * kWave;
-        const int r = f / C::F4_ROW;
-        const int c4 = f - r * C::F4_ROW;
+        const int r = f / C::C4;
+        const int c4 = f - r * C::C4;
         floatx4 x = {0.f, 0.f, 0.f, 0.f};
         if (k0 + r < T) x = *reinterpret_cast<const floatx4 *>(k + base + int64_t(k0 + r) * D + 4 * c4);
         *reinterpret_cast<floatx4 *>(&k_lds[r * C::KS + 4 * c4]) = x;
     }
     // V^T as the B operand of dP = dO V^T, held in registers for the whole kernel:
-    // lane (col = key, half) holds V[key][kstep_index(s, half)].  K^T, the B operand of
-    // S = Q K^T, is read from the K block in LDS with the same mapping.
+    // lane (col = key, half) holds V[key][kstep_index(s, half)].
     float vT[D / 2];
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
@@ -188,118 +192,121 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
     const int nqb = (T + C::BM - 1) / C::BM;
     const int qb_begin = causal ? k0 / C::BM : 0;
 
-    floatx4 qpre[C::QF4], dopre[C::QF4];
-    float lpre = 0.f, dpre = 0.f;
-    auto load_qblock = [&](int r0) {
+    // Global -> LDS for one query block: lane writes LDS chunk P = (wave * INSTR + i) * 64 +
+    // lane of the padded block, i.e. row P / C4P, chunk P % C4P; the pad chunk (C4) re-reads
+    // chunk 0 of the row and is never used.  Rows past T re-read row T - 1 (their P is
+    // masked to 0).  Waves 0 / 1 also fetch the block's LSE / delta (one dword per lane).
+    auto issue = [&](int r0) {
 #pragma unroll
-        for (int i = 0; i < C::QF4; ++i) {
-            const int f = tid + i * C::NW * kWave;
-            const int r = f / C::F4_ROW;
-            const int c4 = f - r * C::F4_ROW;
-            const int row = r0 + r;
-            floatx4 qx = {0.f, 0.f, 0.f, 0.f}, dx = {0.f, 0.f, 0.f, 0.f};
-            if (row < T) {
-                qx = *reinterpret_cast<const floatx4 *>(q + base + int64_t(row) * D + 4 * c4);
-                dx = *reinterpret_cast<const floatx4 *>(dout + base + int64_t(row) * D + 4 * c4);
+        for (int i = 0; i < C::INSTR; ++i) {
+            const int P = (wave * C::INSTR + i) * kWave + lane;
+            if (C::CHUNKS % (C::NW * kWave) == 0 || P < C::CHUNKS) {
+                const int r = P / C::C4P;
+                const int c = P - r * C::C4P;
+                const int64_t goff = base + int64_t(min(r0 + r, T - 1)) * D + 4 * (c < C::C4 ? c : 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(q + goff),
+                                                 CTATTN_LDS(&q_lds[(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(dout + goff),
+                                                 CTATTN_LDS(&do_lds[(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
             }
-            qpre[i] = qx;
-            dopre[i] = dx;
         }
-        if (tid < C::BM) {
-            const int row = r0 + tid;
-            lpre = row < T ? lse[rbase + row] * kLog2e : 0.f;
-            dpre = row < T ? delta[rbase + row] : 0.f;
-        }
-    };
-    auto store_qblock = [&]() {
-#pragma unroll
-        for (int i = 0; i < C::QF4; ++i) {
-            const int f = tid + i * C::NW * kWave;
-            const int r = f / C::F4_ROW;
-            const int c4 = f - r * C::F4_ROW;
-            *reinterpret_cast<floatx4 *>(&q_lds[r * C::KS + 4 * c4]) = qpre[i];
-            *reinterpret_cast<floatx4 *>(&do_lds[r * C::KS + 4 * c4]) = dopre[i];
-        }
-        if (tid < C::BM) {
-            lse_lds[tid] = lpre;
-            dl_lds[tid] = dpre;
+        if (wave < 2) {
+            const float *src = wave == 0 ? lse : delta;
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(src + rbase + min(r0 + lane, T - 1)),
+                                             CTATTN_LDS(wave == 0 ? lse_lds : dl_lds), 4, 0, 0);
         }
     };
 
-    if (qb_begin < nqb) load_qblock(qb_begin * C::BM);
+    // dQ tile of this wave: rows 32 * qrs .. of the block, columns dq_col0 ..
+    const bool dq_wave = wave < C::DQ_WAVES;
+    const int qrs = D >= 64 ? (wave >> 1) : wave;
+    const int dq_col0 = D >= 64 ? (wave & 1) * C::DQ_COLS : 0;
+
+    // A block's dQ tile is added to global memory one iteration late, right after the next
+    // block's first barrier: the wait for the next block's loads at the top of each
+    // iteration (vmcnt counts both) then finds those atomics long completed instead of
+    // stalling on atomics issued just before it.
+    floatx16 dq_pend[C::DQ_T];
+    int pend_rq0 = -1;  // first row of the pending tile, -1 if none
+    auto flush_dq = [&]() {
+        // Lane (col, half), register r: row pend_rq0 + acc_row(r, half), column dq_col0 + 32 j + col.
+        const int row0 = pend_rq0 + 4 * half;
+        float *p0 = dq + base + int64_t(row0) * D + dq_col0 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int dr = acc_row(r, 0);  // row offset from row0, a compile-time constant
+            if (row0 + dr >= T) continue;
+#pragma unroll
+            for (int j = 0; j < C::DQ_T; ++j) unsafeAtomicAdd(p0 + dr * D + 32 * j, dq_pend[j][r] * inv_sqrt_d);
+        }
+    };
+
+    issue(qb_begin * C::BM);
     for (int qb = qb_begin; qb < nqb; ++qb) {
         const int r0 = qb * C::BM;
-        // q/do/lse/delta of the previous block were last read before the previous dQ-phase
-        // barrier, so they can be overwritten without another barrier; ds_lds is only
-        // rewritten after the barrier below, which every wave reaches after its dQ phase.
-        store_qblock();
+        // The block's loads have landed (vmcnt = 0) and, after the barrier, every wave's are
+        // visible; every wave is also done reading the previous block's dS.
+        __builtin_amdgcn_s_waitcnt(0xF70);
         __syncthreads();
-        if (qb + 1 < nqb) load_qblock(r0 + C::BM);
+        if (pend_rq0 >= 0) flush_dq();
 
-        const bool wave_active = kw0 < T && (!causal || kw0 <= r0 + C::BM - 1);
+        const int r0w = r0 + 32 * rs;
+        const bool wave_active = kw0 < T && r0w < T && (!causal || kw0 <= r0w + 31);
         if (wave_active) {
-            const bool masked = (r0 + C::BM > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0);
+            const bool masked = (r0w + 32 > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0w);
             if (masked)
-                bwd_wave_block<D, true>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
-                                        ds_lds, r0, key, T, causal, kscale, wave, col, half);
+                bwd_wave_block<D, true>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds, ds_lds,
+                                        32 * rs, r0w, 32 * ks, key, T, causal, kscale, col, half);
             else
-                bwd_wave_block<D, false>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
-                                         ds_lds, r0, key, T, causal, kscale, wave, col, half);
+                bwd_wave_block<D, false>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds, ds_lds,
+                                         32 * rs, r0w, 32 * ks, key, T, causal, kscale, col, half);
         }
-        __syncthreads();  // dS of every wave visible
+        __syncthreads();  // dS of every wave visible; Q / dO / LSE / delta no longer read
+        if (qb + 1 < nqb) issue(r0 + C::BM);
 
-        // dQ[r0 .. r0+31][wave * DQ_COLS ..] = sum over the workgroup's active keys of dS K.
-        const int rt0 = D >= 64 ? 0 : (wave >> 1);                 // first 16-row tile
-        const int dq_col0 = D >= 64 ? wave * C::DQ_COLS : (wave & 1) * 16;  // first column
-        floatx4 dq_acc[C::DQ_RT][C::DQ_CT];
+        // dQ[r0 + 32 qrs .. +31][dq_col0 ..] = sum over the block's active keys of dS K.
+        if (dq_wave) {
 #pragma unroll
-        for (int rt = 0; rt < C::DQ_RT; ++rt)
+            for (int j = 0; j < C::DQ_T; ++j) dq_pend[j] = zero16();
+            const int rq0 = r0 + 32 * qrs;
 #pragma unroll
-            for (int ct = 0; ct < C::DQ_CT; ++ct) dq_acc[rt][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int ks2 = 0; ks2 < 2; ++ks2) {
+                const int kw2 = k0 + 32 * ks2;
+                if (!(kw2 < T && rq0 < T && (!causal || kw2 <= rq0 + 31))) continue;
 #pragma unroll
-        for (int w2 = 0; w2 < C::NW; ++w2) {
-            const int kw2 = k0 + 32 * w2;
-            if (!(kw2 < T && (!causal || kw2 <= r0 + C::BM - 1))) continue;
+                for (int m = 0; m < 4; ++m) {
+                    const int kl = 32 * ks2 + 8 * m + 4 * half;  // local key of step t: kl + t
+                    const floatx4 a = *reinterpret_cast<const floatx4 *>(&ds_lds[(32 * qrs + col) * C::SS + kl]);
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
-                const int kl = 32 * w2 + 16 * sb + 4 * quad;  // local key of step t: kl + t
-                floatx4 a[C::DQ_RT];
+                    for (int t = 0; t < 4; ++t) {
 #pragma unroll
-                for (int rt = 0; rt < C::DQ_RT; ++rt)
-                    a[rt] = *reinterpret_cast<const floatx4 *>(&ds_lds[((rt0 + rt) * 16 + c16) * C::SS + kl]);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                    for (int ct = 0; ct < C::DQ_CT; ++ct) {
-                        const float b = k_lds[(kl + t) * C::KS + dq_col0 + ct * 16 + c16];
-#pragma unroll
-                        for (int rt = 0; rt < C::DQ_RT; ++rt) dq_acc[rt][ct] = mfma16x16x4(a[rt][t], b, dq_acc[rt][ct]);
+                        for (int j = 0; j < C::DQ_T; ++j)
+                            dq_pend[j] = mfma32x32x2(a[t], k_lds[(kl + t) * C::KS + dq_col0 + 32 * j + col], dq_pend[j]);
                     }
                 }
             }
-        }
-#pragma unroll
-        for (int rt = 0; rt < C::DQ_RT; ++rt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = r0 + (rt0 + rt) * 16 + 4 * quad + r;
-                if (row >= T) continue;
-#pragma unroll
-                for (int ct = 0; ct < C::DQ_CT; ++ct) {
-                    const int c = dq_col0 + ct * 16 + c16;
-                    const float val = dq_acc[rt][ct][r] * inv_sqrt_d;
-                    if constexpr (MODE == DqMode::Atomic) {
-                        unsafeAtomicAdd(dq + base + int64_t(row) * D + c, val);
-                    } else {
-                        dq_part[(int64_t(kb) * BH * T + rbase + row) * D + c] = val;
-                    }
-                }
-            }
+            pend_rq0 = rq0;
         }
     }
+    if (pend_rq0 >= 0) flush_dq();
 
-    // dK = (Q^T dS)^T / sqrt(d), dV = (dO^T P)^T; lane (key, half) holds d = dt*32 + acc_row(r, half).
-    if (key < T) {
+    // dK^T / dV^T of the two row slices: rs = 1 hands its sums to rs = 0 through LDS (the Q /
+    // dO blocks are free: no load is in flight after the last block, and every wave has
+    // passed the last block's second barrier).  Lane (key, half) holds d = dt*32 + acc_row(r, half).
+    float *red = qdo_lds;  // 2 (ks) x DT x 2 (dk, dv) x 16 x 64 floats
+    static_assert(2 * C::DT * 2 * 16 * kWave <= 2 * C::TILE, "reduction buffer");
+    __syncthreads();
+    if (rs == 1) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                red[(((ks * C::DT + dt) * 2 + 0) * 16 + r) * kWave + lane] = dk_acc[dt][r];
+                red[(((ks * C::DT + dt) * 2 + 1) * 16 + r) * kWave + lane] = dv_acc[dt][r];
+            }
+    }
+    __syncthreads();
+    if (rs == 0 && key < T) {
         float *dkr = dk + base + int64_t(key) * D;
         float *dvr = dv + base + int64_t(key) * D;
 #pragma unroll
@@ -309,8 +316,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
                 floatx4 xk, xv;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    xk[t] = dk_acc[dt][4 * g + t] * inv_sqrt_d;
-                    xv[t] = dv_acc[dt][4 * g + t];
+                    const int r = 4 * g + t;
+                    xk[t] = (dk_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 0) * 16 + r) * kWave + lane]) * inv_sqrt_d;
+                    xv[t] = dv_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 1) * 16 + r) * kWave + lane];
                 }
                 *reinterpret_cast<floatx4 *>(dkr + dt * 32 + 8 * g + 4 * half) = xk;
                 *reinterpret_cast<floatx4 *>(dvr + dt * 32 + 8 * g + 4 * half) = xv;
@@ -358,16 +366,20 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float *__restrict_
     *reinterpret_cast<floatx4 *>(dq + 4 * f) = acc;
 }
 
+// Key-block size of the deterministic dQ partials: they come from the 128-key kernel.
+constexpr int kPartialBN = 128;
+
+bool use_k64_kernel(const AttnShape &s, DqMode mode) {
+    return s.causal && s.d >= 64 && mode == DqMode::Atomic;
+}
+
 template <int D>
 hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *o,
                    const float *dout, const float *lse, float *delta, float *dq, float *dk,
                    float *dv, float *dq_part, DqMode mode, const AttnShape &s,
                    hipStream_t stream) {
-    using C = BwdCfg<D>;
-    const int64_t nkb = (s.T + C::BN - 1) / C::BN;
-    const int64_t blocks = nkb * s.bh();
-    if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const int64_t rows = s.rows();
+    if (s.T > 2147483647 / D) return hipErrorInvalidValue;
     if (mode == DqMode::Atomic) {
         hipLaunchKernelGGL(bwd_preprocess_f32_kernel<true>, dim3(unsigned((rows + 3) / 4)), dim3(256),
                            0, stream, o, dout, delta, dq, rows, D);
@@ -377,27 +389,30 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const float kscale = kLog2e / sqrtf(float(D));
-    const float inv_sqrt_d = 1.f / sqrtf(float(D));
-    if (mode == DqMode::Atomic) {
-        hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, DqMode::Atomic>), dim3(unsigned(blocks)),
-                           dim3(C::NW * kWave), 0, stream, q, k, v, dout, lse, delta, dq, dq_part,
-                           dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale, inv_sqrt_d);
+    if constexpr (D >= 64) {
+      if (use_k64_kernel(s, mode)) {
+        using C = BwdCfg<D>;
+        const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh();
+        if (blocks > 2147483647) return hipErrorInvalidValue;
+        const float kscale = kLog2e / sqrtf(float(D));
+        const float inv_sqrt_d = 1.f / sqrtf(float(D));
+        hipLaunchKernelGGL((bwd_f32_mfma_kernel<D>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream, q, k,
+                           v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
+                           inv_sqrt_d);
         return hipGetLastError();
+      }
     }
-    hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, DqMode::Partial>), dim3(unsigned(blocks)),
-                       dim3(C::NW * kWave), 0, stream, q, k, v, dout, lse, delta, dq, dq_part, dk,
-                       dv, int(s.T), int(s.bh()), int(s.causal), kscale, inv_sqrt_d);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    e = launch_bwd_f32_k128(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode == DqMode::Partial, s, stream);
+    if (e != hipSuccess || mode == DqMode::Atomic) return e;
+    const int64_t nkb = (s.T + kPartialBN - 1) / kPartialBN;
     const int64_t n4 = rows * (D / 4);
     hipLaunchKernelGGL(dq_reduce_kernel<D>, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, stream,
-                       dq_part, dq, int(s.T), int(s.bh()), int(s.causal), int(nkb), C::BN);
+                       dq_part, dq, int(s.T), int(s.bh()), int(s.causal), int(nkb), kPartialBN);
     return hipGetLastError();
 }
 
 int64_t partial_bytes(const AttnShape &s) {
-    const int64_t nkb = (s.T + 127) / 128;
+    const int64_t nkb = (s.T + kPartialBN - 1) / kPartialBN;
     return nkb * s.rows() * s.d * int64_t(sizeof(float));
 }
 

@@ -45,6 +45,12 @@ hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const vo
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
                            bool deterministic, const AttnShape &s, hipStream_t stream);
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic);
+// fp32 backward main kernel with 128-key workgroups (attn_bwd_k128.hip), d in {32, 64, 128}:
+// dq is accumulated with atomics (pre-zeroed), or, with `partial`, per-128-key-block
+// partials go to dq_part.  delta must already hold rowsum(dO * O).
+hipError_t launch_bwd_f32_k128(const float *q, const float *k, const float *v, const float *dout,
+                               const float *lse, const float *delta, float *dq, float *dq_part, float *dk,
+                               float *dv, bool partial, const AttnShape &s, hipStream_t stream);
 // Runs the whole MFMA backward: its own preprocess (delta = rowsum(dO * O) into `delta`,
 // fp32 [B, H, T]) and the main kernel(s).  `extra` points at mfma_bwd_workspace_bytes()
 // bytes of scratch (256-byte aligned).
