@@ -10,9 +10,9 @@
 //   * the key loop walks BN-key blocks.  K and V blocks go straight from global memory to
 //     LDS (global_load_lds_dwordx4, no staging registers), double-buffered: the next
 //     block's loads are in flight during the current block's MFMAs, one barrier per block.
-//     Rows are stored unpadded with 16-byte chunks XOR-swizzled by (row & 7), which keeps
-//     the K (ds_read_b128, one key row per lane) and V (ds_read_b32, one d column per
-//     lane) operand reads free of bank conflicts.
+//     Rows are padded by one 16-byte chunk (stride d + 4 floats), which keeps the K
+//     (ds_read_b128, one key row per lane) and V (ds_read_b32, one d column per lane)
+//     operand reads free of bank conflicts and their addresses affine.
 //   * scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q^T held in
 //     registers for the whole kernel, pre-scaled by log2(e)/sqrt(d)).  In the resulting
 //     accumulator each lane holds ONE query row (its column) and 16 keys per 32-key tile,
@@ -39,16 +39,14 @@ struct FwdCfg {
     static constexpr int BM = 32 * NW;         // query rows per workgroup
     static constexpr int KT = BN / 32;         // 32-key tiles per block
     static constexpr int DT = D / 32;          // 32-wide d tiles of O^T
-    static constexpr int C4 = D / 4;           // 16-byte chunks per row
-    static constexpr int TILE = BN * D;        // floats per K (or V) tile
-    static constexpr int INSTR = TILE / 4 / (NW * kWave);  // 16-byte loads per lane per tile
+    static constexpr int KS = D + 4;           // LDS row stride (floats): one pad chunk
+    static constexpr int C4 = D / 4;           // 16-byte chunks of data per row
+    static constexpr int C4P = C4 + 1;         // ... per LDS row
+    static constexpr int TILE = BN * KS;       // floats per padded K (or V) tile
+    static constexpr int CHUNKS = BN * C4P;    // 16-byte chunks per padded tile
+    static constexpr int INSTR = (CHUNKS + NW * kWave - 1) / (NW * kWave);  // loads per lane per tile
     static_assert(D % 32 == 0 && BN % 32 == 0, "tile shape");
-    static_assert(INSTR * 4 * NW * kWave == TILE, "tile load split");
 };
-
-// Float offset of 16-byte chunk c4 of row `row` in an unpadded, XOR-swizzled tile.
-template <int D>
-__device__ __forceinline__ int swz(int row, int c4) { return row * D + ((c4 ^ (row & 7)) << 2); }
 
 #define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
@@ -91,7 +89,7 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
         const int key = kt * 32 + col;
 #pragma unroll
         for (int m = 0; m < D / 8; ++m) {
-            const floatx4 kv = *reinterpret_cast<const floatx4 *>(k_lds + swz<D>(key, 2 * m + half));
+            const floatx4 kv = *reinterpret_cast<const floatx4 *>(k_lds + key * C::KS + 8 * m + 4 * half);
 #pragma unroll
             for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
         }
@@ -144,8 +142,7 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
         for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
-                const int d = dt * 32 + col;
-                const float a = v_lds[swz<D>(kt * 32 + kstep_index(s, half), d >> 2) + (d & 3)];
+                const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::KS + dt * 32 + col];
                 st.oacc[dt] = mfma32x32x2(a, sacc[kt][s], st.oacc[dt]);
             }
         }
@@ -198,20 +195,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int kend = causal ? min(T, q0 + C::BM) : T;
     const int nkb = (kend + BN - 1) / BN;
 
-    // Global -> LDS for one block: lane writes LDS chunk P (tile position, in 16-byte units)
-    // = (wave * INSTR + i) * 64 + lane, i.e. row P / C4, swizzled chunk P % C4, so it loads
-    // chunk (P % C4) ^ (row & 7) of that key row.  Rows past T re-read row T - 1 (masked).
+    // Global -> LDS for one block: lane writes LDS chunk P = (wave * INSTR + i) * 64 + lane of
+    // the padded tile, i.e. row P / C4P, chunk P % C4P; the pad chunk (C4) re-reads chunk 0
+    // of the row and is never used.  Rows past T re-read row T - 1 (masked).
     auto issue = [&](int j0, int buf) {
 #pragma unroll
         for (int i = 0; i < C::INSTR; ++i) {
             const int P = (wave * C::INSTR + i) * kWave + lane;
-            const int r = P / C::C4;
-            const int c4 = (P % C::C4) ^ (r & 7);
-            const int64_t goff = base + int64_t(min(j0 + r, T - 1)) * D + 4 * c4;
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(k + goff),
-                                             CTATTN_LDS(&k_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(v + goff),
-                                             CTATTN_LDS(&v_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+            if (C::CHUNKS % (C::NW * kWave) == 0 || P < C::CHUNKS) {
+                const int r = P / C::C4P;
+                const int c = P - r * C::C4P;
+                const int64_t goff = base + int64_t(min(j0 + r, T - 1)) * D + 4 * (c < C::C4 ? c : 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(k + goff),
+                                                 CTATTN_LDS(&k_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(v + goff),
+                                                 CTATTN_LDS(&v_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+            }
         }
     };
 
