@@ -252,17 +252,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdBf16Occu
                 dq = mfma_bf16(a, b, dq);
             }
         }
-        // dq tile: lane (col = d - 32*wave, half), register r -> row acc_row(r, half).
+        // dq tile: lane (col = d - 32*wave, half), register r -> row acc_row(r, half) =
+        // row0 + acc_row(r, 0), with the offset acc_row(r, 0) * D a compile-time constant.
+        const int row0 = r0 + 4 * half;
+        float *p0 = dq_acc + (PARTIAL ? int64_t(kb) * BH * T * D : 0) + (rbase + row0) * D + 32 * wave + col;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int row = r0 + acc_row(r, half);
-            if (row >= T) continue;
-            const int64_t off = (rbase + row) * D + 32 * wave + col;
+            const int dr = acc_row(r, 0);
+            if (row0 + dr >= T) continue;
             const float val = dq[r] * inv_sqrt_d;
             if constexpr (PARTIAL) {
-                dq_acc[int64_t(kb) * BH * T * D + off] = val;
+                p0[dr * D] = val;
             } else {
-                unsafeAtomicAdd(dq_acc + off, val);
+                unsafeAtomicAdd(p0 + dr * D, val);
             }
         }
     }
