@@ -5,161 +5,267 @@
 // computed in fp32 and rounded to bf16 only as MFMA operands; dK, dV, dQ accumulate in fp32
 // and are rounded to bf16 once.
 //
-// Decomposition: a workgroup of 4 waves owns 128 keys (wave w: 32 keys) and keeps dK^T,
-// dV^T in registers; it walks 32-row query blocks from the LAST block down to its diagonal,
-// so the key-block workgroups of one (batch, head) add into the same dQ rows at the same
-// time (those lines stay in L2).  Per wave and query block (lane l: col = l & 31, half =
-// l >> 5; 32x32x16 bf16 operands take 8 consecutive k from lane (i, k/8)):
-//   S = Q K^T, dP = dO V^T   A = Q / dO rows from LDS, B = K / V rows in registers
-//   P = exp2(S c - LSE log2 e), dS = P (dP - delta)        (lane = one key, 16 rows)
-//   dV^T += dO^T P, dK^T += Q^T dS   B = P / dS straight from the accumulator (registers
-//                                    8s..8s+7 = rows 16s + 8(e/4) + 4 half + e%4), A = dO^T /
-//                                    Q^T rows, staged TRANSPOSED in LDS next to Q / dO
-//   dQ = dS K                        dS -> LDS ([row][key]); A = dS rows, B = K^T rows
-//                                    (staged once); fp32 atomics into the dq accumulator or a
-//                                    per-key-block partial buffer (deterministic policy).
+// Two kernels, no atomics.  fp32 global atomics run at ~1.35 TB/s on MI355X, and the fused
+// key-major design's dQ atomics (T^2/2 * d / 128 per head, 4.3 GB at B1 H32 T8192 d128)
+// bound it at ~3 ms; recomputing S and dP in a second, query-major kernel costs 2 of the
+// backward's 5 matmuls again but runs at MFMA speed and is deterministic by construction.
+//   * bwd_bf16_dkdv_kernel (key-major): a workgroup of 4 waves owns 128 keys (wave w: 32),
+//     keeps dK^T and dV^T in registers and walks 32-row query blocks (causal: from its
+//     diagonal on).  S = Q K^T, dP = dO V^T (lane = one key, registers = rows), then
+//     P = exp2(S c + nl2), dS = P (dP - delta) elementwise, and dV^T += dO^T P,
+//     dK^T += Q^T dS with P / dS straight from the accumulator as B operands.
+//   * bwd_bf16_dq_kernel (query-major): a workgroup of 4 waves owns 128 query rows (wave w:
+//     32), keeps dQ in registers and walks 32-key blocks (causal: up to its diagonal).
+//     S^T = K Q^T, dP^T = V dO^T (lane = one row), P^T, dS^T elementwise, and
+//     dQ += dS K with dS straight from the accumulator as the A operand.
+// A 32x32x16 operand takes 8 consecutive contraction indices from lane (i, k / 8); an S /
+// dP accumulator holds rows 16 s + 8 (e / 4) + 4 half + e % 4 in registers 8 s + e, so the
+// contractions over rows (dV, dK) and keys (dQ) run in that permuted order, and their other
+// operand (dO^T, Q^T, K^T) is read column-wise from the same row-major LDS tile with
+// ds_read_b64_tr_b16 (two reads of 4 rows each).
+//
+// LDS tiles are row-major, D bf16 per row, loaded global -> LDS directly
+// (global_load_lds_dwordx4), with the 16-byte chunk index XOR-swizzled by the row
+// (Tile<D>::swz) so that both the row reads (16 lanes, 16 rows, one chunk) and the
+// transposed reads (32 lanes, 4 rows x 4 chunks) hit 64 distinct banks.
 #include "attn_launch.h"
 #include "attn_mfma_common.h"
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace ctattn {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+#define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
 
 __device__ __forceinline__ floatx16 mfma_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Row-major bf16 tile with D elements (D / 8 16-byte chunks) per row.  Logical chunk c of
+// row r sits at physical chunk c ^ swz(r).  The LDS has 64 four-byte banks (256 bytes per
+// bank row); swz makes
+//   * a row read (lanes 0-15: rows r0..r0+15, one chunk) and
+//   * a transposed read (lanes 0-31: rows R..R+3, R % 4 == 0, chunks C..C+3, C % 4 == 0)
+// touch each bank once.
 template <int D>
-struct BwdBf16Cfg {
-    static constexpr int NW = 4;
-    static constexpr int BN = 32 * NW;  // keys per workgroup
-    static constexpr int BM = 32;       // query rows per iteration
-    static constexpr int QS = D + 8;    // row stride (bf16) of Q / dO in LDS
-    static constexpr int TS = BM + 4;   // row stride of Q^T / dO^T (conflict-free 8-byte reads)
-    static constexpr int KS = BN + 8;   // row stride of K^T and of dS
-    static constexpr int DT = D / 32;
-    static constexpr int PATCHES = (BM / 4) * (D / 8);  // 4-row x 8-d patches per block (per tensor)
-    static_assert(D % 32 == 0 && 2 * PATCHES <= NW * kWave, "tile shape");
+struct Tile {
+    static_assert(D == 32 || D == 64 || D == 128, "bf16 MFMA backward supports d in {32, 64, 128}");
+    static constexpr int CH = D / 8;         // 16-byte chunks per row
+    static constexpr int ROW_BYTES = 2 * D;  // bytes per row
+    __device__ static constexpr int swz(int r) {
+        return D == 128 ? 4 * (r & 3) + ((r >> 2) & 3)
+             : D == 64  ? 4 * ((r >> 1) & 1) + ((r >> 2) & 3)
+                        : (r >> 2) & 3;
+    }
+    __device__ static int off(int r, int chunk) { return r * ROW_BYTES + ((chunk ^ swz(r)) << 4); }
 };
 
-// Gathers A-operand element e of a transposed row: rows r0..r0+3 and r0+8..r0+11.
-__device__ __forceinline__ bf16x8 load_split8(const __bf16 *p) {
-    const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(p);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(p + 8);
-    bf16x8 a;
+// Loads rows r0 .. r0 + ROWS - 1 of one (batch, head)'s [T][D] tensor into a swizzled tile:
+// lane writes the 16-byte LDS chunk P = (wave * NL + i) * 64 + lane, i.e. row P / CH,
+// physical chunk P % CH, which holds logical chunk (P % CH) ^ swz(row).  Rows past T re-read
+// row T - 1 (their results are masked).  Every wave calls this; waves past the tile skip.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void load_tile(char *tile, const uint16_t *src, int r0, int T, int wave, int lane) {
+    using L = Tile<D>;
+    constexpr int TOTAL = ROWS * L::CH;
+    constexpr int NL = (TOTAL + NW * kWave - 1) / (NW * kWave);
+    static_assert(TOTAL % kWave == 0, "tile size");
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        a[e] = lo[e];
-        a[4 + e] = hi[e];
+    for (int i = 0; i < NL; ++i) {
+        const int P = (wave * NL + i) * kWave + lane;
+        if (TOTAL % (NW * kWave) == 0 || (wave * NL + i) * kWave < TOTAL) {
+            const int r = P / L::CH;
+            const int lc = (P % L::CH) ^ L::swz(r);
+            const uint16_t *g = src + int64_t(min(r0 + r, T - 1)) * D + 8 * lc;
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(g),
+                                             CTATTN_LDS(tile + (wave * NL + i) * kWave * 16), 16, 0, 0);
+        }
     }
-    return a;
 }
 
+// LDS reads by byte address (LDS addresses are 32-bit).
+typedef __attribute__((address_space(3))) const bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) const floatx4 lds_floatx4;
+
+__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) { return *(lds_bf16x8 *)(uintptr_t)(addr); }
+__device__ __forceinline__ floatx4 lds_f4(uint32_t addr) { return *(lds_floatx4 *)(uintptr_t)(addr); }
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return uint32_t(uintptr_t((__attribute__((address_space(3))) const char *)p));
+}
+
+// Operand reads.  Tiles start on 1 KiB boundaries and a row's chunk field occupies address
+// bits 4 .. 4 + log2(D / 8) - 1, so with row_base(r) = tile + Tile::off(r, half):
+//   * row read, step st (elements 16 st + 8 half .. + 7 of row r):  row_base ^ (st << 5),
+//     because (2 st + half) ^ swz = (2 st) ^ (half ^ swz);
+//   * column read, d-tile dt (column 32 dt + col), k-step kk: rows 16 kk + 4 half + e and
+//     16 kk + 8 + 4 half + (e - 4) -- the row order of accumulator registers 8 kk .. 8 kk + 7
+//     -- from two ds_read_b64_tr_b16 at (col_base[hi] ^ (dt << 6)) + 16 kk * ROW, hi = 0, 1.
+//     In each 16-lane group, lane s addresses 4 elements of row R + s / 4 at column
+//     cb + 4 (s % 4) and lane l receives column cb + l of rows R .. R + 3; the swizzle of those
+//     rows does not depend on kk and flips only the chunk bits that dt sets (bits 6, 7).
+template <int D>
+__device__ __forceinline__ uint32_t row_base(uint32_t tile, int r, int half) {
+    return tile + uint32_t(Tile<D>::off(r, half));
+}
+template <int D>
+__device__ __forceinline__ uint32_t col_base(uint32_t tile, int r0, int hi, int lane) {
+    const int s = lane & 15;
+    const int half = lane >> 5;
+    const int chunk = 2 * ((lane >> 4) & 1) + ((s & 3) >> 1);
+    return tile + uint32_t(Tile<D>::off(r0 + 4 * half + (s >> 2) + 8 * hi, chunk) + 8 * (s & 1));
+}
+template <int D>
+__device__ __forceinline__ bf16x8 read_col(uint32_t cb0, uint32_t cb1, int kk, int dt) {
+    const uint32_t off = uint32_t(16 * kk * 2 * D);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb0 ^ uint32_t(dt << 6)) + off));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb1 ^ uint32_t(dt << 6)) + off));
+    const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, x);
+}
+
+// Scheduling fence between a step's operand reads and the previous step's MFMAs: nothing
+// crosses it, so step st + 1's reads are issued before step st's MFMAs and about two steps'
+// operands are live at once (the MFMAs of step st wait only for step st's reads).
+__device__ __forceinline__ void read_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// ---------------------------------------------------------------------------------------
+// dK / dV (key-major)
+// ---------------------------------------------------------------------------------------
+template <int D>
+struct KvCfg {
+    static constexpr int NW = 8;       // waves: 4 key slices (ks = wave & 3) x 2 row slices (rs = wave >> 2)
+    static constexpr int BN = 128;     // keys per workgroup; key slice ks: 32 ks .. 32 ks + 31
+    static constexpr int BM = 64;      // query rows per iteration; row slice rs: 32 rs .. 32 rs + 31
+    static constexpr int DT = D / 32;
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int ROW = 2 * D;            // bytes per tile row
+    static constexpr int KV_BYTES = BN * ROW;    // K (or V) tile
+    static constexpr int Q_BYTES = BM * ROW;     // Q (or dO) tile
+    // LDS map: per buffer b, Q and dO at Q_OFF + b * 2 * Q_BYTES (+ Q_BYTES); then K, V; then
+    // per buffer b, nl2 and delta (BM floats each) at S_OFF + b * 2 * BM * 4.  Every offset
+    // added to a per-lane address is an immediate (< 64 KiB).
+    static constexpr int Q_OFF = 0;
+    static constexpr int K_OFF = 4 * Q_BYTES;
+    static constexpr int V_OFF = K_OFF + KV_BYTES;
+    static constexpr int S_OFF = V_OFF + KV_BYTES;
+    static constexpr int LDS_BYTES = S_OFF + 4 * BM * 4;
+    static_assert(Q_BYTES + 16 * ROW < 65536 && KV_BYTES < 65536, "immediate offsets");
+    // The row slices' dK^T / dV^T partial sums meet in LDS at the end.
+    static_assert(4 * DT * 2 * 16 * kWave * 4 <= LDS_BYTES, "reduction buffer");
+};
+
+// One 32-row x 32-key wave tile: S, dP, P, dS and the dV^T / dK^T updates.
+//   aq   : row_base of this wave's first Q row in the block's Q tile (dO at + Q_BYTES)
+//   ak   : row_base of this wave's first key in the K tile (V at + KV_BYTES)
+//   ac0/1: col_base of the wave's Q rows (dO at + Q_BYTES)
+//   anl  : address of nl2[32 rs + 4 half] of the block (delta at + BM * 4)
 template <int D, bool MASK>
-__device__ __forceinline__ void bwd_bf16_wave_block(
-    floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32], const bf16x8 (&kB)[D / 16],
-    const bf16x8 (&vB)[D / 16], const __bf16 *q_lds, const __bf16 *do_lds, const __bf16 *qt_lds,
-    const __bf16 *dot_lds, const float *lse_lds, const float *dl_lds, __bf16 *ds_lds, int r0, int key,
-    int T, int causal, float c, int wave, int col, int half) {
-    using C = BwdBf16Cfg<D>;
+__device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32], uint32_t aq,
+                                         uint32_t ak, uint32_t ac0, uint32_t ac1, uint32_t anl, int r0w,
+                                         int key, int T, int causal, float c, int half) {
+    using C = KvCfg<D>;
     floatx16 s = zero16(), dp = zero16();
+    {
+        bf16x8 qa[2], ka[2], da[2], va[2];
+        qa[0] = lds_b128(aq);
+        ka[0] = lds_b128(ak);
+        da[0] = lds_b128(aq + C::Q_BYTES);
+        va[0] = lds_b128(ak + C::KV_BYTES);
 #pragma unroll
-    for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 qa = *reinterpret_cast<const bf16x8 *>(q_lds + col * C::QS + 16 * st + 8 * half);
-        const bf16x8 da = *reinterpret_cast<const bf16x8 *>(do_lds + col * C::QS + 16 * st + 8 * half);
-        s = mfma_bf16(qa, kB[st], s);
-        dp = mfma_bf16(da, vB[st], dp);
+        for (int st = 0; st < C::KSTEPS; ++st) {
+            const int cur = st & 1, nxt = cur ^ 1;
+            if (st + 1 < C::KSTEPS) {
+                const uint32_t xq = aq ^ uint32_t((st + 1) << 5), xk = ak ^ uint32_t((st + 1) << 5);
+                qa[nxt] = lds_b128(xq);
+                ka[nxt] = lds_b128(xk);
+                da[nxt] = lds_b128(xq + C::Q_BYTES);
+                va[nxt] = lds_b128(xk + C::KV_BYTES);
+            }
+            read_fence();
+            s = mfma_bf16(qa[cur], ka[cur], s);
+            dp = mfma_bf16(da[cur], va[cur], dp);
+        }
     }
+    // lane = key; register r = row r0w + acc_row(r, half)
     bf16x8 pb[2], dsb[2];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const floatx4 l4 = *reinterpret_cast<const floatx4 *>(&lse_lds[8 * g + 4 * half]);
-        const floatx4 d4 = *reinterpret_cast<const floatx4 *>(&dl_lds[8 * g + 4 * half]);
+        const floatx4 n4 = lds_f4(anl + 32 * g);
+        const floatx4 d4 = lds_f4(anl + C::BM * 4 + 32 * g);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int r = 4 * g + t;
-            float p = fast_exp2(fmaf(s[r], c, -l4[t]));
+            float p = fast_exp2(fmaf(s[r], c, n4[t]));
             if (MASK) {
-                const int row = r0 + acc_row(r, half);
+                const int row = r0w + acc_row(r, half);
                 p = (row >= T || key >= T || (causal && key > row)) ? 0.f : p;
             }
-            const float ds = p * (dp[r] - d4[t]);
             pb[r / 8][r % 8] = (__bf16)p;
-            dsb[r / 8][r % 8] = (__bf16)ds;
-            ds_lds[acc_row(r, half) * C::KS + 32 * wave + col] = (__bf16)ds;
+            dsb[r / 8][r % 8] = (__bf16)(p * (dp[r] - d4[t]));
         }
     }
-    // dV^T += dO^T P, dK^T += Q^T dS over this block's 32 rows (2 k-steps of 16 rows).
+    // dV^T += dO^T P, dK^T += Q^T dS over the tile's 32 rows (two k-steps of 16).
+    {
+        constexpr int NS = 2 * C::DT;
+        bf16x8 ao[2], aqT[2];
+        ao[0] = read_col<D>(ac0 + C::Q_BYTES, ac1 + C::Q_BYTES, 0, 0);
+        aqT[0] = read_col<D>(ac0, ac1, 0, 0);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int rr = 16 * ks + 4 * half;  // rows rr..rr+3 and rr+8..rr+11
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
-            const bf16x8 a_do = load_split8(dot_lds + (dt * 32 + col) * C::TS + rr);
-            const bf16x8 a_q = load_split8(qt_lds + (dt * 32 + col) * C::TS + rr);
-            dv_acc[dt] = mfma_bf16(a_do, pb[ks], dv_acc[dt]);
-            dk_acc[dt] = mfma_bf16(a_q, dsb[ks], dk_acc[dt]);
+        for (int i = 0; i < NS; ++i) {
+            const int cur = i & 1, nxt = cur ^ 1;
+            if (i + 1 < NS) {
+                const int kk = (i + 1) / C::DT, dt = (i + 1) % C::DT;
+                ao[nxt] = read_col<D>(ac0 + C::Q_BYTES, ac1 + C::Q_BYTES, kk, dt);
+                aqT[nxt] = read_col<D>(ac0, ac1, kk, dt);
+            }
+            read_fence();
+            const int kk = i / C::DT, dt = i % C::DT;
+            dv_acc[dt] = mfma_bf16(ao[cur], pb[kk], dv_acc[dt]);
+            dk_acc[dt] = mfma_bf16(aqT[cur], dsb[kk], dk_acc[dt]);
         }
     }
 }
 
-// d = 64 fits 256 registers (2 waves per SIMD); d = 128 needs more than 256 and runs one
-// wave per SIMD with up to 512.
-template <int D> struct BwdBf16Occupancy { static constexpr int waves = D <= 64 ? 2 : 1; };
-
-template <int D, bool PARTIAL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdBf16Occupancy<D>::waves,
-                                                                      BwdBf16Occupancy<D>::waves))) void bwd_bf16_mfma_kernel(
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_bf16_dkdv_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
-    const uint16_t *__restrict__ dout, const float *__restrict__ lse, const float *__restrict__ delta,
-    float *__restrict__ dq_acc, uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, int T, int BH,
-    int causal, float c, float inv_sqrt_d) {
-    using C = BwdBf16Cfg<D>;
-    __shared__ __attribute__((aligned(16))) __bf16 q_lds[C::BM * C::QS];
-    __shared__ __attribute__((aligned(16))) __bf16 do_lds[C::BM * C::QS];
-    __shared__ __attribute__((aligned(16))) __bf16 qt_lds[D * C::TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dot_lds[D * C::TS];
-    __shared__ __attribute__((aligned(16))) __bf16 kt_lds[D * C::KS];
-    __shared__ __attribute__((aligned(16))) __bf16 ds_lds[C::BM * C::KS];
-    __shared__ __attribute__((aligned(16))) float lse_lds[C::BM];
-    __shared__ __attribute__((aligned(16))) float dl_lds[C::BM];
+    const uint16_t *__restrict__ dout, const float *__restrict__ nl2, const float *__restrict__ delta,
+    uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, int T, int BH, int causal, float c,
+    float inv_sqrt_d) {
+    using C = KvCfg<D>;
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+    const uint32_t L = lds_addr(smem);
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
     const int col = lane & 31;
     const int half = lane >> 5;
+    const int ks = wave & 3, rs = wave >> 2;
 
     const int id = blockIdx.x;
     const int bh = id % BH;
-    const int kb = id / BH;
+    const int kb = id / BH;  // causal: key block 0 has the most query blocks -> launched first
     const int k0 = kb * C::BN;
     const int64_t base = int64_t(bh) * T * D;
     const int64_t rbase = int64_t(bh) * T;
-    const int kw0 = k0 + 32 * wave;
+    const int kw0 = k0 + 32 * ks;
     const int key = kw0 + col;
 
-    // K / V rows of this lane's key as B operands (8 consecutive d per step); K^T -> LDS.
-    bf16x8 kB[D / 16], vB[D / 16];
-#pragma unroll
-    for (int st = 0; st < D / 16; ++st) {
-        u16x8 kx = {0, 0, 0, 0, 0, 0, 0, 0}, vx = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (key < T) {
-            kx = *reinterpret_cast<const u16x8 *>(k + base + int64_t(key) * D + 16 * st + 8 * half);
-            vx = *reinterpret_cast<const u16x8 *>(v + base + int64_t(key) * D + 16 * st + 8 * half);
-        }
-        kB[st] = __builtin_bit_cast(bf16x8, kx);
-        vB[st] = __builtin_bit_cast(bf16x8, vx);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kt_lds[(16 * st + 8 * half + e) * C::KS + 32 * wave + col] = kB[st][e];
-    }
-
+    load_tile<D, C::BN, C::NW>(smem + C::K_OFF, k + base, k0, T, wave, lane);
+    load_tile<D, C::BN, C::NW>(smem + C::V_OFF, v + base, k0, T, wave, lane);
     floatx16 dk_acc[C::DT], dv_acc[C::DT];
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
@@ -167,109 +273,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdBf16Occu
         dv_acc[dt] = zero16();
     }
 
+    // Per-lane parts of the operand addresses (the swizzle depends on the row mod 16 only, so
+    // the slice offsets 32 rs / 32 ks rows keep the pattern).
+    const uint32_t rq = uint32_t(Tile<D>::off(32 * rs + col, half));
+    const uint32_t ak = row_base<D>(L + C::K_OFF, 32 * ks + col, half);
+    const uint32_t cq0 = col_base<D>(0, 32 * rs, 0, lane), cq1 = col_base<D>(0, 32 * rs, 1, lane);
+    const uint32_t rnl = uint32_t(4 * (32 * rs + 4 * half));
+
     const int nqb = (T + C::BM - 1) / C::BM;
     const int qb_first = causal ? k0 / C::BM : 0;
-
-    // Staging: threads [0, PATCHES) take Q, [PATCHES, 2*PATCHES) take dO; each holds a
-    // 4-row x 8-d patch and writes it row-major (4 x 16 B) and transposed (8 x 8 B).
-    const bool stager = tid < 2 * C::PATCHES;
-    const bool is_do = tid >= C::PATCHES;
-    const int pt = is_do ? tid - C::PATCHES : tid;
-    const int prg = pt % (C::BM / 4);  // rows 4*prg .. 4*prg+3
-    const int pdg = pt / (C::BM / 4);  // d 8*pdg .. 8*pdg+7
-    const uint16_t *src = is_do ? dout : q;
-    __bf16 *dst = is_do ? do_lds : q_lds;
-    __bf16 *dstT = is_do ? dot_lds : qt_lds;
-    u16x8 pre[4];
-    float lpre = 0.f, dpre = 0.f;
-    auto load_qblock = [&](int r0) {
-        if (stager) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = r0 + 4 * prg + i;
-                u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
-                if (row < T) x = *reinterpret_cast<const u16x8 *>(src + base + int64_t(row) * D + 8 * pdg);
-                pre[i] = x;
-            }
-        }
-        if (tid < C::BM) {
-            const int row = r0 + tid;
-            lpre = row < T ? lse[rbase + row] * kLog2e : 0.f;
-            dpre = row < T ? delta[rbase + row] : 0.f;
-        }
-    };
-    auto store_qblock = [&]() {
-        if (stager) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u16x8 *>(dst + (4 * prg + i) * C::QS + 8 * pdg) = pre[i];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const u16x4 t = {pre[0][e], pre[1][e], pre[2][e], pre[3][e]};
-                *reinterpret_cast<u16x4 *>(dstT + (8 * pdg + e) * C::TS + 4 * prg) = t;
-            }
-        }
-        if (tid < C::BM) {
-            lse_lds[tid] = lpre;
-            dl_lds[tid] = dpre;
+    auto issue = [&](int r0, int buf) {
+        char *qt = smem + C::Q_OFF + buf * 2 * C::Q_BYTES;
+        load_tile<D, C::BM, C::NW>(qt, q + base, r0, T, wave, lane);
+        load_tile<D, C::BM, C::NW>(qt + C::Q_BYTES, dout + base, r0, T, wave, lane);
+        if (wave >= C::NW - 2) {  // nl2 / delta of the block's rows, one dword per lane
+            const bool is_nl = wave == C::NW - 2;
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void *>((is_nl ? nl2 : delta) + rbase + min(r0 + lane, T - 1)),
+                CTATTN_LDS(smem + C::S_OFF + buf * 2 * C::BM * 4 + (is_nl ? 0 : C::BM * 4)), 4, 0, 0);
         }
     };
 
-    if (qb_first < nqb) load_qblock((nqb - 1) * C::BM);
-    for (int qb = nqb - 1; qb >= qb_first; --qb) {
-        const int r0 = qb * C::BM;
-        // Q / dO / LSE / delta of the previous block were last read before the previous
-        // dQ-phase barrier; ds_lds is rewritten only after the barrier below.
-        store_qblock();
+    if (qb_first < nqb) issue(qb_first * C::BM, 0);
+    for (int qb = qb_first; qb < nqb; ++qb) {
+        const int buf = (qb - qb_first) & 1;
+        // This wave's loads of `buf` have landed (vmcnt = 0); after the barrier every wave's
+        // have, and every wave is done reading buf ^ 1.
+        __builtin_amdgcn_s_waitcnt(0xF70);
         __syncthreads();
-        if (qb - 1 >= qb_first) load_qblock(r0 - C::BM);
-
-        const bool wave_active = kw0 < T && (!causal || kw0 <= r0 + C::BM - 1);
-        if (wave_active) {
-            const bool masked = (r0 + C::BM > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0);
-            if (masked)
-                bwd_bf16_wave_block<D, true>(dk_acc, dv_acc, kB, vB, q_lds, do_lds, qt_lds, dot_lds, lse_lds,
-                                             dl_lds, ds_lds, r0, key, T, causal, c, wave, col, half);
-            else
-                bwd_bf16_wave_block<D, false>(dk_acc, dv_acc, kB, vB, q_lds, do_lds, qt_lds, dot_lds, lse_lds,
-                                              dl_lds, ds_lds, r0, key, T, causal, c, wave, col, half);
-        }
-        __syncthreads();  // dS of every wave visible
-
-        // dQ[r0..r0+31][32*wave .. 32*wave+31] over the workgroup's active keys; waves past
-        // d / 32 have no columns (d = 64: waves 2, 3 skip this phase; d = 32: waves 1-3).
-        if (wave >= C::DT) continue;
-        floatx16 dq = zero16();
-#pragma unroll
-        for (int w2 = 0; w2 < C::NW; ++w2) {
-            const int kw2 = k0 + 32 * w2;
-            if (!(kw2 < T && (!causal || kw2 <= r0 + C::BM - 1))) continue;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int kl = 32 * w2 + 16 * ks + 8 * half;
-                const bf16x8 a = *reinterpret_cast<const bf16x8 *>(ds_lds + col * C::KS + kl);
-                const bf16x8 b = *reinterpret_cast<const bf16x8 *>(kt_lds + (32 * wave + col) * C::KS + kl);
-                dq = mfma_bf16(a, b, dq);
-            }
-        }
-        // dq tile: lane (col = d - 32*wave, half), register r -> row acc_row(r, half) =
-        // row0 + acc_row(r, 0), with the offset acc_row(r, 0) * D a compile-time constant.
-        const int row0 = r0 + 4 * half;
-        float *p0 = dq_acc + (PARTIAL ? int64_t(kb) * BH * T * D : 0) + (rbase + row0) * D + 32 * wave + col;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int dr = acc_row(r, 0);
-            if (row0 + dr >= T) continue;
-            const float val = dq[r] * inv_sqrt_d;
-            if constexpr (PARTIAL) {
-                p0[dr * D] = val;
-            } else {
-                unsafeAtomicAdd(p0 + dr * D, val);
-            }
-        }
+        if (qb + 1 < nqb) issue((qb + 1) * C::BM, buf ^ 1);
+        const int r0w = qb * C::BM + 32 * rs;
+        const bool active = kw0 < T && r0w < T && (!causal || kw0 <= r0w + 31);
+        if (!active) continue;
+        const uint32_t qt = L + C::Q_OFF + uint32_t(buf * 2 * C::Q_BYTES);
+        const uint32_t anl = L + C::S_OFF + uint32_t(buf * 2 * C::BM * 4) + rnl;
+        const bool masked = (r0w + 32 > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0w);
+        if (masked)
+            kv_block<D, true>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
+        else
+            kv_block<D, false>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
     }
 
-    if (key < T) {
+    // Row slice 1 hands its dK^T / dV^T sums to row slice 0 through LDS (no load is in flight
+    // and, after the barrier, no wave reads a tile any more).  Lane (key, half), register r
+    // of tile dt holds d = 32 dt + acc_row(r, half).
+    float *red = reinterpret_cast<float *>(smem);
+    __syncthreads();
+    if (rs == 1) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                red[(((ks * C::DT + dt) * 2 + 0) * 16 + r) * kWave + lane] = dk_acc[dt][r];
+                red[(((ks * C::DT + dt) * 2 + 1) * 16 + r) * kWave + lane] = dv_acc[dt][r];
+            }
+    }
+    __syncthreads();
+    if (rs == 0 && key < T) {
         uint16_t *dkr = dk + base + int64_t(key) * D;
         uint16_t *dvr = dv + base + int64_t(key) * D;
 #pragma unroll
@@ -279,8 +339,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdBf16Occu
                 u16x4 xk, xv;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    xk[t] = f32_to_bf16(dk_acc[dt][4 * g + t] * inv_sqrt_d).bits;
-                    xv[t] = f32_to_bf16(dv_acc[dt][4 * g + t]).bits;
+                    const int r = 4 * g + t;
+                    const float sk = dk_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 0) * 16 + r) * kWave + lane];
+                    const float sv = dv_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 1) * 16 + r) * kWave + lane];
+                    xk[t] = f32_to_bf16(sk * inv_sqrt_d).bits;
+                    xv[t] = f32_to_bf16(sv).bits;
                 }
                 *reinterpret_cast<u16x4 *>(dkr + dt * 32 + 8 * g + 4 * half) = xk;
                 *reinterpret_cast<u16x4 *>(dvr + dt * 32 + 8 * g + 4 * half) = xv;
@@ -289,116 +352,223 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdBf16Occu
     }
 }
 
-// delta[row] = sum_c dO[row][c] O[row][c] from bf16 (flash_attention.cu:269-273); zeroes the
-// fp32 dq accumulator row when ZERO.  One wave per row.
-template <bool ZERO>
+// ---------------------------------------------------------------------------------------
+// dQ (query-major)
+// ---------------------------------------------------------------------------------------
+template <int D>
+struct QCfg {
+    static constexpr int NW = 4;
+    static constexpr int BM = 32 * NW;  // query rows per workgroup
+    static constexpr int BN = 32;       // keys per iteration
+    static constexpr int DT = D / 32;
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int KB = BN * 2 * D;       // bytes of a K (or V) tile
+    static constexpr int LDS_BYTES = 4 * KB;    // buffer b: K at 2 b KB, V at 2 b KB + KB
+};
+
+// One 32-key block for one wave (32 rows): S^T, dP^T, P^T, dS^T and the dQ update.
+//   ak   : row_base of the block's K tile for key `col` (V at + KB)
+//   ac0/1: col_base of the K tile
+template <int D, bool MASK>
+__device__ __forceinline__ void dq_block(floatx16 (&dq_acc)[D / 32], const bf16x8 (&qB)[D / 16],
+                                         const bf16x8 (&doB)[D / 16], uint32_t ak, uint32_t ac0, uint32_t ac1,
+                                         float nlr, float dlr, int j0, int row, int T, int causal, float c,
+                                         int half) {
+    using C = QCfg<D>;
+    floatx16 s = zero16(), dp = zero16();
+    {
+        bf16x8 ka[2], va[2];
+        ka[0] = lds_b128(ak);
+        va[0] = lds_b128(ak + C::KB);
+#pragma unroll
+        for (int st = 0; st < C::KSTEPS; ++st) {
+            const int cur = st & 1, nxt = cur ^ 1;
+            if (st + 1 < C::KSTEPS) {
+                const uint32_t x = ak ^ uint32_t((st + 1) << 5);
+                ka[nxt] = lds_b128(x);
+                va[nxt] = lds_b128(x + C::KB);
+            }
+            read_fence();
+            s = mfma_bf16(ka[cur], qB[st], s);
+            dp = mfma_bf16(va[cur], doB[st], dp);
+        }
+    }
+    // lane = query row; register r = key j0 + acc_row(r, half)
+    bf16x8 dsb[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(s[r], c, nlr));
+        if (MASK) {
+            const int key = j0 + acc_row(r, half);
+            p = (key >= T || row >= T || (causal && key > row)) ? 0.f : p;
+        }
+        dsb[r / 8][r % 8] = (__bf16)(p * (dp[r] - dlr));
+    }
+    // dQ += dS K over the block's 32 keys (two k-steps of 16).
+    {
+        constexpr int NS = 2 * C::DT;
+        bf16x8 kt[2];
+        kt[0] = read_col<D>(ac0, ac1, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const int cur = i & 1, nxt = cur ^ 1;
+            if (i + 1 < NS) kt[nxt] = read_col<D>(ac0, ac1, (i + 1) / C::DT, (i + 1) % C::DT);
+            read_fence();
+            dq_acc[i % C::DT] = mfma_bf16(dsb[i / C::DT], kt[cur], dq_acc[i % C::DT]);
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_bf16_dq_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    const uint16_t *__restrict__ dout, const float *__restrict__ nl2, const float *__restrict__ delta,
+    uint16_t *__restrict__ dq, int T, int BH, int causal, float c, float inv_sqrt_d) {
+    using C = QCfg<D>;
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+    const uint32_t L = lds_addr(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    const int qb = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
+    const int64_t base = int64_t(bh) * T * D;
+    const int64_t rbase = int64_t(bh) * T;
+    const int r0 = qb * C::BM;
+    const int wave_first_row = r0 + 32 * wave;
+    const int wave_last_row = wave_first_row + 31;
+    const int row = wave_first_row + col;
+
+    // Q^T and dO^T as B operands: lane (row, half) holds Q[row][16 st + 8 half ..].
+    bf16x8 qB[C::KSTEPS], doB[C::KSTEPS];
+#pragma unroll
+    for (int st = 0; st < C::KSTEPS; ++st) {
+        u16x8 xq = {0, 0, 0, 0, 0, 0, 0, 0}, xd = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (row < T) {
+            xq = *reinterpret_cast<const u16x8 *>(q + base + int64_t(row) * D + 16 * st + 8 * half);
+            xd = *reinterpret_cast<const u16x8 *>(dout + base + int64_t(row) * D + 16 * st + 8 * half);
+        }
+        qB[st] = __builtin_bit_cast(bf16x8, xq);
+        doB[st] = __builtin_bit_cast(bf16x8, xd);
+    }
+    const float nlr = row < T ? nl2[rbase + row] : 0.f;
+    const float dlr = row < T ? delta[rbase + row] : 0.f;
+    floatx16 dq_acc[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) dq_acc[dt] = zero16();
+
+    const uint32_t rk = uint32_t(Tile<D>::off(col, half));
+    const uint32_t ck0 = col_base<D>(0, 0, 0, lane), ck1 = col_base<D>(0, 0, 1, lane);
+
+    const int kend = causal ? min(T, r0 + C::BM) : T;
+    const int nkb = (kend + C::BN - 1) / C::BN;
+    auto issue = [&](int j0, int buf) {
+        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB, k + base, j0, T, wave, lane);
+        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB + C::KB, v + base, j0, T, wave, lane);
+    };
+
+    issue(0, 0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        __builtin_amdgcn_s_waitcnt(0xF70);
+        __syncthreads();
+        if (kb + 1 < nkb) issue((kb + 1) * C::BN, buf ^ 1);
+        const int j0 = kb * C::BN;
+        const uint32_t kt = L + uint32_t(2 * buf * C::KB);
+        const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
+        if (masked) {
+            if (!causal || j0 <= wave_last_row)
+                dq_block<D, true>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
+                                  half);
+        } else {
+            dq_block<D, false>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
+                               half);
+        }
+    }
+
+    // dq_acc[dt]: lane (col, half), register r -> row wave_first_row + acc_row(r, half),
+    // column 32 dt + col.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int rr = wave_first_row + acc_row(r, half);
+        if (rr >= T) continue;
+        uint16_t *p = dq + base + int64_t(rr) * D + col;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) p[32 * dt] = f32_to_bf16(dq_acc[dt][r] * inv_sqrt_d).bits;
+    }
+}
+
+// delta[row] = sum_c dO[row][c] O[row][c] from bf16 (flash_attention.cu:269-273) and
+// nl2[row] = -LSE[row] * log2(e), the per-row term of P = exp2(S log2(e)/sqrt(d) + nl2).
+// One wave per row.
 __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t *__restrict__ o,
                                                                  const uint16_t *__restrict__ dout,
+                                                                 const float *__restrict__ lse,
                                                                  float *__restrict__ delta,
-                                                                 float *__restrict__ dq_acc, int64_t rows,
-                                                                 int d) {
+                                                                 float *__restrict__ nl2, int64_t rows, int d) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (row >= rows) return;
     float s = 0.f;
-    for (int cc = lane; cc < d; cc += kWave) {
+    for (int cc = lane; cc < d; cc += kWave)
         s += to_f32(bf16_t{o[row * d + cc]}) * to_f32(bf16_t{dout[row * d + cc]});
-        if (ZERO) dq_acc[row * d + cc] = 0.f;
-    }
     s = wave_sum(s);
-    if (lane == 0) delta[row] = s;
-}
-
-// dq (bf16) = fp32 accumulator, rounded to nearest even.  4 elements per thread.
-__global__ __launch_bounds__(256) void dq_to_bf16_kernel(const float *__restrict__ acc,
-                                                        uint16_t *__restrict__ dq, int64_t n4) {
-    const int64_t f = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (f >= n4) return;
-    const floatx4 x = *reinterpret_cast<const floatx4 *>(acc + 4 * f);
-    u16x4 y;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) y[t] = f32_to_bf16(x[t]).bits;
-    *reinterpret_cast<u16x4 *>(dq + 4 * f) = y;
-}
-
-// dq (bf16) = sum over key blocks kb <= last(row) of the partials, in increasing kb order.
-template <int D>
-__global__ __launch_bounds__(256) void dq_reduce_bf16_kernel(const float *__restrict__ part,
-                                                            uint16_t *__restrict__ dq, int T, int BH,
-                                                            int causal, int nkb, int bn) {
-    const int64_t f = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t total = int64_t(BH) * T * (D / 4);
-    if (f >= total) return;
-    const int64_t row_g = f / (D / 4);
-    const int row = int(row_g % T);
-    const int last = causal ? row / bn : nkb - 1;
-    const int64_t plane = int64_t(BH) * T * D;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb <= last; ++kb) acc += *reinterpret_cast<const floatx4 *>(part + kb * plane + 4 * f);
-    u16x4 y;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) y[t] = f32_to_bf16(acc[t]).bits;
-    *reinterpret_cast<u16x4 *>(dq + 4 * f) = y;
+    if (lane == 0) {
+        delta[row] = s;
+        nl2[row] = -lse[row] * kLog2e;
+    }
 }
 
 template <int D>
 hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, const void *dout,
-                    const float *lse, float *delta, void *dq, void *dk, void *dv, float *acc,
-                    bool deterministic, const AttnShape &s, hipStream_t stream) {
-    using C = BwdBf16Cfg<D>;
-    const int64_t nkb = (s.T + C::BN - 1) / C::BN;
-    const int64_t blocks = nkb * s.bh();
-    if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+                    const float *lse, float *delta, void *dq, void *dk, void *dv, float *nl2,
+                    const AttnShape &s, hipStream_t stream) {
+    using KC = KvCfg<D>;
+    using QC = QCfg<D>;
+    const int64_t kv_blocks = ((s.T + KC::BN - 1) / KC::BN) * s.bh();
+    const int64_t q_blocks = ((s.T + QC::BM - 1) / QC::BM) * s.bh();
+    if (kv_blocks > 2147483647 || q_blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const int64_t rows = s.rows();
     auto u16 = [](const void *p) { return static_cast<const uint16_t *>(p); };
-    if (deterministic)
-        hipLaunchKernelGGL(bwd_preprocess_bf16_kernel<false>, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,
-                           stream, u16(o), u16(dout), delta, acc, rows, D);
-    else
-        hipLaunchKernelGGL(bwd_preprocess_bf16_kernel<true>, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,
-                           stream, u16(o), u16(dout), delta, acc, rows, D);
+    hipLaunchKernelGGL(bwd_preprocess_bf16_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream, u16(o),
+                       u16(dout), lse, delta, nl2, rows, D);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const float c = kLog2e / sqrtf(float(D));
     const float inv_sqrt_d = 1.f / sqrtf(float(D));
-    if (deterministic)
-        hipLaunchKernelGGL((bwd_bf16_mfma_kernel<D, true>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
-                           stream, u16(q), u16(k), u16(v), u16(dout), lse, delta, acc,
-                           static_cast<uint16_t *>(dk), static_cast<uint16_t *>(dv), int(s.T), int(s.bh()),
-                           int(s.causal), c, inv_sqrt_d);
-    else
-        hipLaunchKernelGGL((bwd_bf16_mfma_kernel<D, false>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
-                           stream, u16(q), u16(k), u16(v), u16(dout), lse, delta, acc,
-                           static_cast<uint16_t *>(dk), static_cast<uint16_t *>(dv), int(s.T), int(s.bh()),
-                           int(s.causal), c, inv_sqrt_d);
+    hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0, stream,
+                       u16(q), u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dk),
+                       static_cast<uint16_t *>(dv), int(s.T), int(s.bh()), int(s.causal), c, inv_sqrt_d);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t n4 = rows * (D / 4);
-    if (deterministic)
-        hipLaunchKernelGGL(dq_reduce_bf16_kernel<D>, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, stream, acc,
-                           static_cast<uint16_t *>(dq), int(s.T), int(s.bh()), int(s.causal), int(nkb), C::BN);
-    else
-        hipLaunchKernelGGL(dq_to_bf16_kernel, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, stream, acc,
-                           static_cast<uint16_t *>(dq), n4);
+    hipLaunchKernelGGL((bwd_bf16_dq_kernel<D>), dim3(unsigned(q_blocks)), dim3(QC::NW * kWave), 0, stream, u16(q),
+                       u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dq), int(s.T), int(s.bh()),
+                       int(s.causal), c, inv_sqrt_d);
     return hipGetLastError();
 }
 
 }  // namespace
 
 int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic) {
-    const int64_t plane = s.rows() * s.d * int64_t(sizeof(float));
-    const int64_t nkb = (s.T + 127) / 128;
-    return deterministic ? nkb * plane : plane;
+    (void)deterministic;  // both kernels are deterministic: no atomics, fixed summation order
+    return s.rows() * int64_t(sizeof(float));  // nl2
 }
 
 hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
                            bool deterministic, const AttnShape &s, hipStream_t stream) {
-    float *acc = static_cast<float *>(extra);
+    (void)deterministic;
+    float *nl2 = static_cast<float *>(extra);
     switch (s.d) {
-        case 32: return bwd_bf16<32>(q, k, v, o, dout, lse, delta, dq, dk, dv, acc, deterministic, s, stream);
-        case 64: return bwd_bf16<64>(q, k, v, o, dout, lse, delta, dq, dk, dv, acc, deterministic, s, stream);
-        case 128: return bwd_bf16<128>(q, k, v, o, dout, lse, delta, dq, dk, dv, acc, deterministic, s, stream);
+        case 32: return bwd_bf16<32>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 64: return bwd_bf16<64>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 128: return bwd_bf16<128>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
         default: return hipErrorNotSupported;
     }
 }
