@@ -1,0 +1,120 @@
+// bf16 LDS tile machinery shared by the bf16 attention kernels (gfx950): swizzled row-major
+// tiles loaded global -> LDS directly, row and transposed (ds_read_b64_tr_b16) MFMA operand
+// reads by explicit LDS byte address, and the v_mfma_f32_32x32x16_bf16 wrapper.
+//
+// 32x32x16 operand layout (lane l, col = l & 31, half = l >> 5): A[i][k] comes from lane
+// (i, k / 8) element k % 8, B[k][j] from lane (j, k / 8) element k % 8; accumulator register r
+// of lane (j, half) holds row acc_row(r, half) of column j.
+#pragma once
+
+#include "attn_mfma_common.h"
+
+#include <stdint.h>
+
+namespace ctattn {
+namespace bf16tile {
+
+#define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ floatx16 mfma_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row-major bf16 tile with D elements (D / 8 16-byte chunks) per row.  Logical chunk c of
+// row r sits at physical chunk c ^ swz(r).  The LDS has 64 four-byte banks (256 bytes per
+// bank row); swz makes
+//   * a row read (lanes 0-15: rows r0..r0+15, one chunk) and
+//   * a transposed read (lanes 0-31: rows R..R+3, R % 4 == 0, chunks C..C+3, C % 4 == 0)
+// touch each bank once.
+template <int D>
+struct Tile {
+    static_assert(D == 32 || D == 64 || D == 128, "bf16 MFMA kernels support d in {32, 64, 128}");
+    static constexpr int CH = D / 8;         // 16-byte chunks per row
+    static constexpr int ROW_BYTES = 2 * D;  // bytes per row
+    __device__ static constexpr int swz(int r) {
+        return D == 128 ? 4 * (r & 3) + ((r >> 2) & 3)
+             : D == 64  ? 4 * ((r >> 1) & 1) + ((r >> 2) & 3)
+                        : (r >> 2) & 3;
+    }
+    __device__ static int off(int r, int chunk) { return r * ROW_BYTES + ((chunk ^ swz(r)) << 4); }
+};
+
+// Loads rows r0 .. r0 + ROWS - 1 of one (batch, head)'s [T][D] tensor into a swizzled tile:
+// lane writes the 16-byte LDS chunk P = (wave * NL + i) * 64 + lane, i.e. row P / CH,
+// physical chunk P % CH, which holds logical chunk (P % CH) ^ swz(row).  Rows past T re-read
+// row T - 1 (their results are masked).  Every wave calls this; waves past the tile skip.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void load_tile(char *tile, const uint16_t *src, int r0, int T, int wave, int lane) {
+    using L = Tile<D>;
+    constexpr int TOTAL = ROWS * L::CH;
+    constexpr int NL = (TOTAL + NW * kWave - 1) / (NW * kWave);
+    static_assert(TOTAL % kWave == 0, "tile size");
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int P = (wave * NL + i) * kWave + lane;
+        if (TOTAL % (NW * kWave) == 0 || (wave * NL + i) * kWave < TOTAL) {
+            const int r = P / L::CH;
+            const int lc = (P % L::CH) ^ L::swz(r);
+            const uint16_t *g = src + int64_t(min(r0 + r, T - 1)) * D + 8 * lc;
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(g),
+                                             CTATTN_LDS(tile + (wave * NL + i) * kWave * 16), 16, 0, 0);
+        }
+    }
+}
+
+// LDS reads by byte address (LDS addresses are 32-bit).
+typedef __attribute__((address_space(3))) const bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) const floatx4 lds_floatx4;
+
+__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) { return *(lds_bf16x8 *)(uintptr_t)(addr); }
+__device__ __forceinline__ floatx4 lds_f4(uint32_t addr) { return *(lds_floatx4 *)(uintptr_t)(addr); }
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return uint32_t(uintptr_t((__attribute__((address_space(3))) const char *)p));
+}
+
+// Operand reads.  Tiles start on 1 KiB boundaries and a row's chunk field occupies address
+// bits 4 .. 4 + log2(D / 8) - 1, so with row_base(r) = tile + Tile::off(r, half):
+//   * row read, step st (elements 16 st + 8 half .. + 7 of row r):  row_base ^ (st << 5),
+//     because (2 st + half) ^ swz = (2 st) ^ (half ^ swz);
+//   * column read, d-tile dt (column 32 dt + col), k-step kk: rows 16 kk + 4 half + e and
+//     16 kk + 8 + 4 half + (e - 4) -- the row order of accumulator registers 8 kk .. 8 kk + 7
+//     -- from two ds_read_b64_tr_b16 at (col_base[hi] ^ (dt << 6)) + 16 kk * ROW, hi = 0, 1.
+//     In each 16-lane group, lane s addresses 4 elements of row R + s / 4 at column
+//     cb + 4 (s % 4) and lane l receives column cb + l of rows R .. R + 3; the swizzle of those
+//     rows does not depend on kk and flips only the chunk bits that dt sets (bits 6, 7).
+template <int D>
+__device__ __forceinline__ uint32_t row_base(uint32_t tile, int r, int half) {
+    return tile + uint32_t(Tile<D>::off(r, half));
+}
+template <int D>
+__device__ __forceinline__ uint32_t col_base(uint32_t tile, int r0, int hi, int lane) {
+    const int s = lane & 15;
+    const int half = lane >> 5;
+    const int chunk = 2 * ((lane >> 4) & 1) + ((s & 3) >> 1);
+    return tile + uint32_t(Tile<D>::off(r0 + 4 * half + (s >> 2) + 8 * hi, chunk) + 8 * (s & 1));
+}
+template <int D>
+__device__ __forceinline__ bf16x8 read_col(uint32_t cb0, uint32_t cb1, int kk, int dt) {
+    const uint32_t off = uint32_t(16 * kk * 2 * D);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb0 ^ uint32_t(dt << 6)) + off));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb1 ^ uint32_t(dt << 6)) + off));
+    const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, x);
+}
+
+// Scheduling fence between a step's operand reads and the previous step's MFMAs: nothing
+// crosses it, so step st + 1's reads are issued before step st's MFMAs and about two steps'
+// operands are live at once (the MFMAs of step st wait only for step st's reads).
+__device__ __forceinline__ void read_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+}  // namespace bf16tile
+}  // namespace ctattn

@@ -28,8 +28,8 @@
 // (global_load_lds_dwordx4), with the 16-byte chunk index XOR-swizzled by the row
 // (Tile<D>::swz) so that both the row reads (16 lanes, 16 rows, one chunk) and the
 // transposed reads (32 lanes, 4 rows x 4 chunks) hit 64 distinct banks.
+#include "attn_bf16_tiles.h"
 #include "attn_launch.h"
-#include "attn_mfma_common.h"
 
 #include <math.h>
 
@@ -38,107 +38,7 @@
 namespace ctattn {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-#define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
-
-__device__ __forceinline__ floatx16 mfma_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// Row-major bf16 tile with D elements (D / 8 16-byte chunks) per row.  Logical chunk c of
-// row r sits at physical chunk c ^ swz(r).  The LDS has 64 four-byte banks (256 bytes per
-// bank row); swz makes
-//   * a row read (lanes 0-15: rows r0..r0+15, one chunk) and
-//   * a transposed read (lanes 0-31: rows R..R+3, R % 4 == 0, chunks C..C+3, C % 4 == 0)
-// touch each bank once.
-template <int D>
-struct Tile {
-    static_assert(D == 32 || D == 64 || D == 128, "bf16 MFMA backward supports d in {32, 64, 128}");
-    static constexpr int CH = D / 8;         // 16-byte chunks per row
-    static constexpr int ROW_BYTES = 2 * D;  // bytes per row
-    __device__ static constexpr int swz(int r) {
-        return D == 128 ? 4 * (r & 3) + ((r >> 2) & 3)
-             : D == 64  ? 4 * ((r >> 1) & 1) + ((r >> 2) & 3)
-                        : (r >> 2) & 3;
-    }
-    __device__ static int off(int r, int chunk) { return r * ROW_BYTES + ((chunk ^ swz(r)) << 4); }
-};
-
-// Loads rows r0 .. r0 + ROWS - 1 of one (batch, head)'s [T][D] tensor into a swizzled tile:
-// lane writes the 16-byte LDS chunk P = (wave * NL + i) * 64 + lane, i.e. row P / CH,
-// physical chunk P % CH, which holds logical chunk (P % CH) ^ swz(row).  Rows past T re-read
-// row T - 1 (their results are masked).  Every wave calls this; waves past the tile skip.
-template <int D, int ROWS, int NW>
-__device__ __forceinline__ void load_tile(char *tile, const uint16_t *src, int r0, int T, int wave, int lane) {
-    using L = Tile<D>;
-    constexpr int TOTAL = ROWS * L::CH;
-    constexpr int NL = (TOTAL + NW * kWave - 1) / (NW * kWave);
-    static_assert(TOTAL % kWave == 0, "tile size");
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-        const int P = (wave * NL + i) * kWave + lane;
-        if (TOTAL % (NW * kWave) == 0 || (wave * NL + i) * kWave < TOTAL) {
-            const int r = P / L::CH;
-            const int lc = (P % L::CH) ^ L::swz(r);
-            const uint16_t *g = src + int64_t(min(r0 + r, T - 1)) * D + 8 * lc;
-            __builtin_amdgcn_global_load_lds(static_cast<const void *>(g),
-                                             CTATTN_LDS(tile + (wave * NL + i) * kWave * 16), 16, 0, 0);
-        }
-    }
-}
-
-// LDS reads by byte address (LDS addresses are 32-bit).
-typedef __attribute__((address_space(3))) const bf16x8 lds_bf16x8;
-typedef __attribute__((address_space(3))) const floatx4 lds_floatx4;
-
-__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) { return *(lds_bf16x8 *)(uintptr_t)(addr); }
-__device__ __forceinline__ floatx4 lds_f4(uint32_t addr) { return *(lds_floatx4 *)(uintptr_t)(addr); }
-
-// LDS byte address of a __shared__ object.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return uint32_t(uintptr_t((__attribute__((address_space(3))) const char *)p));
-}
-
-// Operand reads.  Tiles start on 1 KiB boundaries and a row's chunk field occupies address
-// bits 4 .. 4 + log2(D / 8) - 1, so with row_base(r) = tile + Tile::off(r, half):
-//   * row read, step st (elements 16 st + 8 half .. + 7 of row r):  row_base ^ (st << 5),
-//     because (2 st + half) ^ swz = (2 st) ^ (half ^ swz);
-//   * column read, d-tile dt (column 32 dt + col), k-step kk: rows 16 kk + 4 half + e and
-//     16 kk + 8 + 4 half + (e - 4) -- the row order of accumulator registers 8 kk .. 8 kk + 7
-//     -- from two ds_read_b64_tr_b16 at (col_base[hi] ^ (dt << 6)) + 16 kk * ROW, hi = 0, 1.
-//     In each 16-lane group, lane s addresses 4 elements of row R + s / 4 at column
-//     cb + 4 (s % 4) and lane l receives column cb + l of rows R .. R + 3; the swizzle of those
-//     rows does not depend on kk and flips only the chunk bits that dt sets (bits 6, 7).
-template <int D>
-__device__ __forceinline__ uint32_t row_base(uint32_t tile, int r, int half) {
-    return tile + uint32_t(Tile<D>::off(r, half));
-}
-template <int D>
-__device__ __forceinline__ uint32_t col_base(uint32_t tile, int r0, int hi, int lane) {
-    const int s = lane & 15;
-    const int half = lane >> 5;
-    const int chunk = 2 * ((lane >> 4) & 1) + ((s & 3) >> 1);
-    return tile + uint32_t(Tile<D>::off(r0 + 4 * half + (s >> 2) + 8 * hi, chunk) + 8 * (s & 1));
-}
-template <int D>
-__device__ __forceinline__ bf16x8 read_col(uint32_t cb0, uint32_t cb1, int kk, int dt) {
-    const uint32_t off = uint32_t(16 * kk * 2 * D);
-    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb0 ^ uint32_t(dt << 6)) + off));
-    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb1 ^ uint32_t(dt << 6)) + off));
-    const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8, x);
-}
-
-// Scheduling fence between a step's operand reads and the previous step's MFMAs: nothing
-// crosses it, so step st + 1's reads are issued before step st's MFMAs and about two steps'
-// operands are live at once (the MFMAs of step st wait only for step st's reads).
-__device__ __forceinline__ void read_fence() { __builtin_amdgcn_sched_barrier(0); }
+using namespace bf16tile;
 
 // ---------------------------------------------------------------------------------------
 // dK / dV (key-major)
@@ -506,20 +406,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 // delta[row] = sum_c dO[row][c] O[row][c] from bf16 (flash_attention.cu:269-273) and
 // nl2[row] = -LSE[row] * log2(e), the per-row term of P = exp2(S log2(e)/sqrt(d) + nl2).
-// One wave per row.
+// D / 8 lanes per row, one 16-byte load of O and of dO each.
+template <int D>
 __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t *__restrict__ o,
                                                                  const uint16_t *__restrict__ dout,
                                                                  const float *__restrict__ lse,
                                                                  float *__restrict__ delta,
-                                                                 float *__restrict__ nl2, int64_t rows, int d) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
-    if (row >= rows) return;
+                                                                 float *__restrict__ nl2, int64_t rows) {
+    constexpr int LPR = D / 8;  // lanes per row
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t row = t / LPR;
+    const int c8 = int(t % LPR);
     float s = 0.f;
-    for (int cc = lane; cc < d; cc += kWave)
-        s += to_f32(bf16_t{o[row * d + cc]}) * to_f32(bf16_t{dout[row * d + cc]});
-    s = wave_sum(s);
-    if (lane == 0) {
+    if (row < rows) {
+        const u16x8 a = *reinterpret_cast<const u16x8 *>(o + row * D + 8 * c8);
+        const u16x8 b = *reinterpret_cast<const u16x8 *>(dout + row * D + 8 * c8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += to_f32(bf16_t{a[e]}) * to_f32(bf16_t{b[e]});
+    }
+    s = group_sum<LPR>(s);
+    if (row < rows && c8 == 0) {
         delta[row] = s;
         nl2[row] = -lse[row] * kLog2e;
     }
@@ -533,11 +439,14 @@ hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, 
     using QC = QCfg<D>;
     const int64_t kv_blocks = ((s.T + KC::BN - 1) / KC::BN) * s.bh();
     const int64_t q_blocks = ((s.T + QC::BM - 1) / QC::BM) * s.bh();
-    if (kv_blocks > 2147483647 || q_blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    if (kv_blocks > 2147483647 || q_blocks > 2147483647 || s.T > 2147483647 / D ||
+        s.rows() * (D / 8) / 256 >= 2147483647)
+        return hipErrorInvalidValue;
     const int64_t rows = s.rows();
     auto u16 = [](const void *p) { return static_cast<const uint16_t *>(p); };
-    hipLaunchKernelGGL(bwd_preprocess_bf16_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream, u16(o),
-                       u16(dout), lse, delta, nl2, rows, D);
+    const int64_t pre_threads = rows * (D / 8);
+    hipLaunchKernelGGL(bwd_preprocess_bf16_kernel<D>, dim3(unsigned((pre_threads + 255) / 256)), dim3(256), 0, stream,
+                       u16(o), u16(dout), lse, delta, nl2, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const float c = kLog2e / sqrtf(float(D));

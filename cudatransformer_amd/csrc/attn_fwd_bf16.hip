@@ -5,35 +5,26 @@
 // accumulates the dot products in bf16, flash_attention.cu:112-116).  O is rounded to bf16
 // (nearest even) once at the end; LSE is fp32.
 //
-// Decomposition as in the fp32 kernel (attn_fwd_mfma.hip): a workgroup of 4 waves owns 128
-// query rows, a wave 32 rows; keys stream through LDS in 64-key blocks; scores are computed
-// transposed, S^T = K Q^T, so each lane holds one query row.  MFMA operand layout of
-// 32x32x16 bf16 (lane l, col = l & 31, half = l >> 5): A[i][k] comes from lane
-// (i, k / 8) element k % 8, B[k][j] from lane (j, k / 8) element k % 8, D as for 32x32x2.
-//   * S^T: A = 8 consecutive d of one key row (one ds_read_b128), B = 8 consecutive d of
-//     this lane's query row, in registers for the whole kernel.
-//   * O^T += V^T P^T: B = P^T straight from the S^T accumulator -- step s of a 32-key tile
-//     takes accumulator registers 8s..8s+7 converted to bf16, i.e. keys
-//     16s + 8*(e/4) + 4*half + e%4 -- and A = V^T rows for those keys.  V is therefore
-//     staged TRANSPOSED in LDS ([d][key]), so one operand is two 8-byte LDS reads.
-//   * the score scale log2(e)/sqrt(d) is applied in fp32 inside exp2's argument (an fma),
-//     not folded into bf16 Q.
+// Decomposition: a workgroup of 4 waves owns 128 query rows (wave w: 32 rows for the whole
+// key loop); K and V stream through LDS in 64-key blocks, loaded global -> LDS directly into
+// swizzled row-major tiles (attn_bf16_tiles.h), double-buffered with one barrier per block.
+// Scores are computed transposed, S^T = K Q^T (A = K rows from LDS, B = this lane's Q row in
+// registers for the whole kernel), so each lane holds one query row and the online-softmax
+// statistics need one lane ^ 32 exchange.  After exponentiation the accumulator registers
+// 8 s .. 8 s + 7 are the B operand of O^T += V^T P^T for keys 16 s + 8 (e / 4) + 4 half +
+// e % 4, and A = V^T comes from the row-major V tile through ds_read_b64_tr_b16 in that key
+// order.  The score scale log2(e)/sqrt(d) is applied in fp32 inside exp2's argument (an fma),
+// not folded into bf16 Q; O and l are rescaled lazily, only when the row max grows by more
+// than 2^8.
+#include "attn_bf16_tiles.h"
 #include "attn_launch.h"
-#include "attn_mfma_common.h"
 
 #include <math.h>
 
 namespace ctattn {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
-typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ floatx16 mfma_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
+using namespace bf16tile;
 
 template <int D>
 struct FwdBf16Cfg {
@@ -42,27 +33,28 @@ struct FwdBf16Cfg {
     static constexpr int BN = 64;        // keys per block
     static constexpr int KT = BN / 32;   // 32-key tiles per block
     static constexpr int DT = D / 32;    // 32-wide d tiles of O^T
-    static constexpr int KS = D + 8;     // K row stride (bf16): 16-byte pad, conflict-free b128 reads
-    static constexpr int VS = BN + 4;    // V^T row stride (bf16): 8-byte pad, conflict-free b64 reads
-    static constexpr int K_CHUNKS = BN * D / 8 / (NW * kWave);  // 16-byte K chunks per thread
-    static constexpr int V_PATCHES = (BN / 4) * (D / 8);        // 4-key x 8-d patches per block
-    static_assert(D % 32 == 0 && K_CHUNKS >= 1 && V_PATCHES <= NW * kWave, "tile shape");
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int ROW = 2 * D;             // bytes per tile row
+    static constexpr int KB = BN * ROW;           // bytes of a K (or V) block tile
+    static constexpr int LDS_BYTES = 4 * KB;      // buffer b: K at 2 b KB, V at 2 b KB + KB
+    static_assert(KB + BN * ROW <= 65536, "immediate offsets");
 };
 
 constexpr float kRescaleThresholdBf16 = 8.0f;
 
 template <int D>
 struct FwdBf16State {
-    floatx16 oacc[D / 32];
-    float m_run;  // running max of S * log2(e)/sqrt(d), identical in both halves
-    float l_run;
+    floatx16 oacc[D / 32];  // O^T: lane (row, half), register r of tile dt -> d = 32 dt + acc_row(r, half)
+    float m_run;            // running max of S * log2(e)/sqrt(d), identical in both halves
+    float l_run;            // this half's share of the running denominator
 };
 
+// One 64-key block for one wave.  ak: row_base of the block's K tile for key `col` (V at
+// + KB); vc0 / vc1: col_base of the V tile.  MASK selects the diagonal / sequence-end variant.
 template <int D, bool MASK>
-__device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8 (&qb)[D / 16],
-                                               const __bf16 *k_lds, const __bf16 *vt_lds, int j0,
-                                               int row, int wave_last_row, int T, int causal,
-                                               float c, int col, int half) {
+__device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8 (&qb)[D / 16], uint32_t ak,
+                                               uint32_t vc0, uint32_t vc1, int j0, int row, int wave_last_row,
+                                               int T, int causal, float c, int half) {
     using C = FwdBf16Cfg<D>;
     bool active[C::KT];
 #pragma unroll
@@ -75,11 +67,14 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8
     for (int kt = 0; kt < C::KT; ++kt) {
         sacc[kt] = zero16();
         if (!active[kt]) continue;
-        const __bf16 *krow = k_lds + (kt * 32 + col) * C::KS + 8 * half;
+        const uint32_t a = ak + uint32_t(32 * kt * C::ROW);
+        bf16x8 ka[2];
+        ka[0] = lds_b128(a);
 #pragma unroll
-        for (int s = 0; s < D / 16; ++s) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(krow + 16 * s);
-            sacc[kt] = mfma_bf16(a, qb[s], sacc[kt]);
+        for (int s = 0; s < C::KSTEPS; ++s) {
+            if (s + 1 < C::KSTEPS) ka[(s + 1) & 1] = lds_b128(a ^ uint32_t((s + 1) << 5));
+            read_fence();
+            sacc[kt] = mfma_bf16(ka[s & 1], qb[s], sacc[kt]);
         }
     }
     float mloc = -INFINITY;
@@ -124,25 +119,18 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8
         }
     }
     st.l_run += psum;
+    // O^T += V^T P^T: k-step kk of key tile kt covers tile rows 16 (2 kt + kk) + ...
 #pragma unroll
     for (int kt = 0; kt < C::KT; ++kt) {
         if (!active[kt]) continue;
+        constexpr int NS = 2 * C::DT;
+        bf16x8 va[2];
+        va[0] = read_col<D>(vc0, vc1, 2 * kt, 0);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int k0 = kt * 32 + 16 * s + 4 * half;  // keys k0..k0+3 and k0+8..k0+11
-#pragma unroll
-            for (int dt = 0; dt < C::DT; ++dt) {
-                const __bf16 *vrow = vt_lds + (dt * 32 + col) * C::VS;
-                const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(vrow + k0);
-                const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(vrow + k0 + 8);
-                bf16x8 a;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    a[e] = lo[e];
-                    a[4 + e] = hi[e];
-                }
-                st.oacc[dt] = mfma_bf16(a, pb[kt][s], st.oacc[dt]);
-            }
+        for (int i = 0; i < NS; ++i) {
+            if (i + 1 < NS) va[(i + 1) & 1] = read_col<D>(vc0, vc1, 2 * kt + (i + 1) / C::DT, (i + 1) % C::DT);
+            read_fence();
+            st.oacc[i % C::DT] = mfma_bf16(va[i & 1], pb[kt][i / C::DT], st.oacc[i % C::DT]);
         }
     }
 }
@@ -152,8 +140,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     uint16_t *__restrict__ o, float *__restrict__ lse, int T, int BH, int causal, float c) {
     using C = FwdBf16Cfg<D>;
-    __shared__ __attribute__((aligned(16))) __bf16 k_lds[C::BN * C::KS];
-    __shared__ __attribute__((aligned(16))) __bf16 vt_lds[D * C::VS];
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+    const uint32_t L = lds_addr(smem);
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -164,7 +152,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int nqb = (T + C::BM - 1) / C::BM;
     const int id = blockIdx.x;
     const int bh = id % BH;
-    const int qblk = causal ? (nqb - 1 - id / BH) : id / BH;
+    const int qblk = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
     const int64_t base = int64_t(bh) * T * D;
     const int q0 = qblk * C::BM;
     const int row = q0 + wave * 32 + col;
@@ -172,9 +160,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int wave_last_row = wave_first_row + 31;
 
     // Q^T as the B operand: lane (row, half) holds Q[row][16s + 8*half .. +7].
-    bf16x8 qb[D / 16];
+    bf16x8 qb[C::KSTEPS];
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
+    for (int s = 0; s < C::KSTEPS; ++s) {
         u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
         if (row < T) x = *reinterpret_cast<const u16x8 *>(q + base + int64_t(row) * D + 16 * s + 8 * half);
         qb[s] = __builtin_bit_cast(bf16x8, x);
@@ -186,66 +174,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     st.m_run = -INFINITY;
     st.l_run = 0.f;
 
+    const uint32_t rk = uint32_t(Tile<D>::off(col, half));
+    const uint32_t cv0 = col_base<D>(0, 0, 0, lane), cv1 = col_base<D>(0, 0, 1, lane);
+
     const int kend = causal ? min(T, q0 + C::BM) : T;
     const int nkb = (kend + C::BN - 1) / C::BN;
-
-    // Staging registers: K as 16-byte row chunks; V as a 4-key x 8-d patch per thread.
-    u16x8 kpre[C::K_CHUNKS];
-    u16x8 vpre[4];
-    const bool v_owner = tid < C::V_PATCHES;
-    const int vkg = tid % (C::BN / 4);  // keys 4*vkg .. 4*vkg+3
-    const int vdg = tid / (C::BN / 4);  // d 8*vdg .. 8*vdg+7
-    auto load_block = [&](int j0) {
-#pragma unroll
-        for (int i = 0; i < C::K_CHUNKS; ++i) {
-            const int f = tid + i * C::NW * kWave;
-            const int r = f / (D / 8);
-            const int c8 = f - r * (D / 8);
-            u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (j0 + r < T) x = *reinterpret_cast<const u16x8 *>(k + base + int64_t(j0 + r) * D + 8 * c8);
-            kpre[i] = x;
-        }
-        if (v_owner) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = j0 + 4 * vkg + i;
-                u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
-                if (key < T) x = *reinterpret_cast<const u16x8 *>(v + base + int64_t(key) * D + 8 * vdg);
-                vpre[i] = x;
-            }
-        }
-    };
-    auto store_block = [&]() {
-#pragma unroll
-        for (int i = 0; i < C::K_CHUNKS; ++i) {
-            const int f = tid + i * C::NW * kWave;
-            const int r = f / (D / 8);
-            const int c8 = f - r * (D / 8);
-            *reinterpret_cast<u16x8 *>(k_lds + r * C::KS + 8 * c8) = kpre[i];
-        }
-        if (v_owner) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const u16x4 t = {vpre[0][e], vpre[1][e], vpre[2][e], vpre[3][e]};
-                *reinterpret_cast<u16x4 *>(vt_lds + (8 * vdg + e) * C::VS + 4 * vkg) = t;
-            }
-        }
+    auto issue = [&](int j0, int buf) {
+        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB, k + base, j0, T, wave, lane);
+        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB + C::KB, v + base, j0, T, wave, lane);
     };
 
-    load_block(0);
+    issue(0, 0);
     for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        // This wave's loads of `buf` have landed (vmcnt = 0); after the barrier every wave's
+        // have, and every wave is done reading buf ^ 1.
+        __builtin_amdgcn_s_waitcnt(0xF70);
+        __syncthreads();
+        if (kb + 1 < nkb) issue((kb + 1) * C::BN, buf ^ 1);
         const int j0 = kb * C::BN;
-        __syncthreads();
-        store_block();
-        __syncthreads();
-        if (kb + 1 < nkb) load_block(j0 + C::BN);
+        const uint32_t kt = L + uint32_t(2 * buf * C::KB);
         const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
         if (masked) {
             if (!causal || j0 <= wave_last_row)
-                fwd_bf16_block<D, true>(st, qb, k_lds, vt_lds, j0, row, wave_last_row, T, causal, c, col,
-                                        half);
+                fwd_bf16_block<D, true>(st, qb, kt + rk, kt + C::KB + cv0, kt + C::KB + cv1, j0, row,
+                                        wave_last_row, T, causal, c, half);
         } else {
-            fwd_bf16_block<D, false>(st, qb, k_lds, vt_lds, j0, row, wave_last_row, T, causal, c, col, half);
+            fwd_bf16_block<D, false>(st, qb, kt + rk, kt + C::KB + cv0, kt + C::KB + cv1, j0, row, wave_last_row,
+                                     T, causal, c, half);
         }
     }
 
