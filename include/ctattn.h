@@ -39,12 +39,14 @@ extern "C" {
 enum ctattn_dtype { CTATTN_F32 = 0, CTATTN_BF16 = 1 };
 
 /* Kernel selection policy (process-wide).
- *   AUTO           MFMA kernels where they apply (fastest).  The MFMA backward adds dQ
- *                  contributions of different key blocks with fp32 atomics, so dQ may
- *                  differ between runs in the last bits; dK, dV, O and LSE do not.
+ *   AUTO           MFMA kernels where they apply (fastest).  The fp32 MFMA backward adds
+ *                  dQ contributions of different key blocks with fp32 atomics, so an fp32
+ *                  dQ may differ between runs in the last bits; dK, dV, O and LSE do not,
+ *                  and the bf16 MFMA backward uses no atomics (bitwise reproducible).
  *   GENERIC        the generic kernels only (used to cross-check the two paths).
- *   DETERMINISTIC  MFMA kernels, with dQ summed over key blocks in a fixed order through a
- *                  workspace buffer: bitwise-reproducible gradients, larger workspace. */
+ *   DETERMINISTIC  MFMA kernels, with the fp32 dQ summed over key blocks in a fixed order
+ *                  through a workspace buffer: bitwise-reproducible gradients, larger
+ *                  workspace (bf16: the same kernels as AUTO). */
 enum ctattn_policy {
     CTATTN_POLICY_AUTO = 0,
     CTATTN_POLICY_GENERIC = 1,
