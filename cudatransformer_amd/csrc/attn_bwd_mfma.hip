@@ -328,23 +328,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
 }
 
 // delta[row] = sum_c dO[row][c] * O[row][c] (flash_attention.cu:269-273); also zeroes the
-// dq row when dQ is accumulated with atomics.  One wave per row, d <= 256.
-template <bool ZERO_DQ>
+// dq row when dQ is accumulated with atomics.  D / 4 lanes per row, one 16-byte load of O and
+// of dO (and one 16-byte store of zeros) each.
+template <int D, bool ZERO_DQ>
 __global__ __launch_bounds__(256) void bwd_preprocess_f32_kernel(const float *__restrict__ o,
                                                                 const float *__restrict__ dout,
                                                                 float *__restrict__ delta,
                                                                 float *__restrict__ dq,
-                                                                int64_t rows, int d) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
-    if (row >= rows) return;
+                                                                int64_t rows) {
+    constexpr int LPR = D / 4;  // lanes per row
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t row = t / LPR;
+    const int c4 = int(t % LPR);
     float s = 0.f;
-    for (int c = lane; c < d; c += kWave) {
-        s += o[row * d + c] * dout[row * d + c];
-        if (ZERO_DQ) dq[row * d + c] = 0.f;
+    if (row < rows) {
+        const floatx4 a = *reinterpret_cast<const floatx4 *>(o + row * D + 4 * c4);
+        const floatx4 b = *reinterpret_cast<const floatx4 *>(dout + row * D + 4 * c4);
+        s = (a[0] * b[0] + a[1] * b[1]) + (a[2] * b[2] + a[3] * b[3]);
+        if (ZERO_DQ) *reinterpret_cast<floatx4 *>(dq + row * D + 4 * c4) = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    s = wave_sum(s);
-    if (lane == 0) delta[row] = s;
+    s = group_sum<LPR>(s);
+    if (row < rows && c4 == 0) delta[row] = s;
 }
 
 // dq[bh][row][:] = sum over key blocks kb <= (causal ? row / BN : nkb - 1) of dq_part[kb][bh][row][:],
@@ -380,12 +384,14 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
                    hipStream_t stream) {
     const int64_t rows = s.rows();
     if (s.T > 2147483647 / D) return hipErrorInvalidValue;
+    const int64_t pre_blocks = (rows * (D / 4) + 255) / 256;
+    if (pre_blocks > 2147483647) return hipErrorInvalidValue;
     if (mode == DqMode::Atomic) {
-        hipLaunchKernelGGL(bwd_preprocess_f32_kernel<true>, dim3(unsigned((rows + 3) / 4)), dim3(256),
-                           0, stream, o, dout, delta, dq, rows, D);
+        hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, true>), dim3(unsigned(pre_blocks)), dim3(256), 0, stream,
+                           o, dout, delta, dq, rows);
     } else {
-        hipLaunchKernelGGL(bwd_preprocess_f32_kernel<false>, dim3(unsigned((rows + 3) / 4)), dim3(256),
-                           0, stream, o, dout, delta, dq, rows, D);
+        hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, false>), dim3(unsigned(pre_blocks)), dim3(256), 0, stream,
+                           o, dout, delta, dq, rows);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
