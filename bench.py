@@ -113,7 +113,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this build measures one GPU "
-              f"(the attention path shards by (batch, head) with no exchange; see DESIGN.md)",
+              f"(the attention path shards by (batch, head) with no exchange between GPUs)",
               file=sys.stderr)
         sys.exit(2)
 

@@ -75,6 +75,28 @@ def load() -> ctypes.CDLL:
     lib.ctattn_out_proj_bwd.restype = c_int
     lib.ctattn_sgd_update.argtypes = [c_int, vp, vp, ctypes.c_float, i64, vp]
     lib.ctattn_sgd_update.restype = c_int
+    f32 = ctypes.c_float
+    sigs = {
+        "ctattn_linear_fwd": ([c_int] + [vp] * 4 + [i64] * 3 + [vp], c_int),
+        "ctattn_linear_bwd_workspace_bytes": ([c_int] + [i64] * 3, i64),
+        "ctattn_linear_bwd": ([c_int] + [vp] * 7 + [i64] * 4 + [vp], c_int),
+        "ctattn_layernorm_fwd": ([c_int] + [vp] * 6 + [i64, i64, f32, vp], c_int),
+        "ctattn_layernorm_bwd_workspace_bytes": ([c_int, i64, i64], i64),
+        "ctattn_layernorm_bwd": ([c_int] + [vp] * 9 + [i64] * 3 + [vp], c_int),
+        "ctattn_activation_fwd": ([c_int, c_int, vp, vp, i64, vp], c_int),
+        "ctattn_activation_bwd": ([c_int, c_int, vp, vp, vp, i64, vp], c_int),
+        "ctattn_embedding_fwd": ([c_int] + [vp] * 4 + [i64] * 5 + [vp], c_int),
+        "ctattn_embedding_bwd": ([c_int] + [vp] * 4 + [i64] * 4 + [vp], c_int),
+        "ctattn_softmax_fwd": ([c_int, vp, vp, i64, i64, f32, vp], c_int),
+        "ctattn_softmax_bwd": ([c_int, vp, vp, vp, i64, i64, f32, vp], c_int),
+        "ctattn_cross_entropy_fwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
+        "ctattn_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
+        "ctattn_softmax_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, f32, vp], c_int),
+        "ctattn_adam_update": ([c_int, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, i64, c_int, vp], c_int),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(lib, name)
+        fn.argtypes, fn.restype = args, res
     _lib = lib
     return lib
 
@@ -285,3 +307,205 @@ def sgd_update(params, grads, lr: float, stream=None):
     rc = load().ctattn_sgd_update(_DTYPE_CODE[params.dtype], _ptr(params), _ptr(grads), float(lr),
                                   params.numel(), _stream_handle(stream))
     _check(rc, "ctattn_sgd_update")
+
+
+# ---- layers around attention (NanoGPT training step) -----------------------------------
+
+ACT_RELU, ACT_GELU, ACT_SIGMOID, ACT_TANH = 0, 1, 2, 3
+
+
+def _rows(x, last: int, name: str) -> int:
+    if x.dim() < 1 or x.shape[-1] != last:
+        raise ValueError(f"{name}: last dimension must be {last}, got {tuple(x.shape)}")
+    return x.numel() // last if last else 0
+
+
+def _workspace(need: int, fn: str, device):
+    if need < 0:
+        raise RuntimeError(f"{fn} failed: {last_error()}")
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+
+
+def _check_ids(name, *ts):
+    for t in ts:
+        if not t.is_cuda or not t.is_contiguous() or t.dtype != torch.int32:
+            raise ValueError(f"{name}: ids / targets must be contiguous int32 on the GPU")
+
+
+def linear_fwd(x, w, b=None, stream=None):
+    """y [..., N] = x [..., K] w^T + b (w: [N, K], b: [N] or None)."""
+    n, k = w.shape
+    m = _rows(x, k, "linear_fwd")
+    _check_dev("linear_fwd", x.dtype, x, w, b)
+    y = torch.empty((*x.shape[:-1], n), dtype=x.dtype, device=x.device)
+    rc = load().ctattn_linear_fwd(_DTYPE_CODE[x.dtype], _ptr(x), _ptr(w), _ptr(b), _ptr(y), m, n, k,
+                                  _stream_handle(stream))
+    _check(rc, "ctattn_linear_fwd")
+    return y
+
+
+def linear_bwd(x, w, dy, dw=None, db=None, want_dx=True, stream=None):
+    """dw += dy^T x, db += colsum(dy) in place (None to skip); returns dx = dy w (or None)."""
+    n, k = w.shape
+    m = _rows(x, k, "linear_bwd")
+    if _rows(dy, n, "linear_bwd") != m:
+        raise ValueError("linear_bwd: dy rows do not match x")
+    _check_dev("linear_bwd", x.dtype, x, w, dy, dw, db)
+    code = _DTYPE_CODE[x.dtype]
+    lib = load()
+    ws = _workspace(lib.ctattn_linear_bwd_workspace_bytes(code, m, n, k), "ctattn_linear_bwd_workspace_bytes",
+                    x.device)
+    dx = torch.empty_like(x) if want_dx else None
+    rc = lib.ctattn_linear_bwd(code, _ptr(x), _ptr(w), _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), _ptr(ws),
+                               ws.numel(), m, n, k, _stream_handle(stream))
+    _check(rc, "ctattn_linear_bwd")
+    return dx
+
+
+def layernorm_fwd(x, gamma, beta, eps: float = 1e-5, stream=None):
+    """Returns (y, mean, rstd): LayerNorm over the last dimension, fp32 row statistics."""
+    d = gamma.numel()
+    n = _rows(x, d, "layernorm_fwd")
+    _check_dev("layernorm_fwd", x.dtype, x, gamma, beta)
+    y = torch.empty_like(x)
+    mean = torch.empty(n, dtype=torch.float32, device=x.device)
+    rstd = torch.empty(n, dtype=torch.float32, device=x.device)
+    rc = load().ctattn_layernorm_fwd(_DTYPE_CODE[x.dtype], _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), _ptr(mean),
+                                     _ptr(rstd), n, d, float(eps), _stream_handle(stream))
+    _check(rc, "ctattn_layernorm_fwd")
+    return y, mean, rstd
+
+
+def layernorm_bwd(x, gamma, dy, mean, rstd, dgamma=None, dbeta=None, stream=None):
+    """Returns dx; dgamma / dbeta accumulated in place (None to skip)."""
+    d = gamma.numel()
+    n = _rows(x, d, "layernorm_bwd")
+    _check_dev("layernorm_bwd", x.dtype, x, gamma, dy, dgamma, dbeta)
+    _check_dev("layernorm_bwd", torch.float32, mean, rstd)
+    code = _DTYPE_CODE[x.dtype]
+    lib = load()
+    ws = _workspace(lib.ctattn_layernorm_bwd_workspace_bytes(code, n, d), "ctattn_layernorm_bwd_workspace_bytes",
+                    x.device)
+    dx = torch.empty_like(x)
+    rc = lib.ctattn_layernorm_bwd(code, _ptr(x), _ptr(gamma), _ptr(dy), _ptr(mean), _ptr(rstd), _ptr(dx),
+                                  _ptr(dgamma), _ptr(dbeta), _ptr(ws), ws.numel(), n, d, _stream_handle(stream))
+    _check(rc, "ctattn_layernorm_bwd")
+    return dx
+
+
+def activation_fwd(x, kind: int, stream=None):
+    _check_dev("activation_fwd", x.dtype, x)
+    y = torch.empty_like(x)
+    rc = load().ctattn_activation_fwd(_DTYPE_CODE[x.dtype], int(kind), _ptr(x), _ptr(y), x.numel(),
+                                      _stream_handle(stream))
+    _check(rc, "ctattn_activation_fwd")
+    return y
+
+
+def activation_bwd(x, dy, kind: int, stream=None):
+    _check_dev("activation_bwd", x.dtype, x, dy)
+    dx = torch.empty_like(x)
+    rc = load().ctattn_activation_bwd(_DTYPE_CODE[x.dtype], int(kind), _ptr(x), _ptr(dy), _ptr(dx), x.numel(),
+                                      _stream_handle(stream))
+    _check(rc, "ctattn_activation_bwd")
+    return dx
+
+
+def embedding_fwd(ids, tok=None, pos=None, stream=None):
+    """out [B, T, E] = tok[ids] + pos[t] (either table may be None); ids int32 [B, T]."""
+    table = tok if tok is not None else pos
+    b, t = ids.shape
+    e = table.shape[1]
+    _check_ids("embedding_fwd", ids)
+    _check_dev("embedding_fwd", table.dtype, tok, pos)
+    vocab = tok.shape[0] if tok is not None else 1
+    max_len = pos.shape[0] if pos is not None else max(t, 1)
+    out = torch.empty((b, t, e), dtype=table.dtype, device=ids.device)
+    rc = load().ctattn_embedding_fwd(_DTYPE_CODE[table.dtype], _ptr(ids), _ptr(tok), _ptr(pos), _ptr(out), b, t, e,
+                                     vocab, max_len, _stream_handle(stream))
+    _check(rc, "ctattn_embedding_fwd")
+    return out
+
+
+def embedding_bwd(ids, dout, dtok=None, dpos=None, vocab: int | None = None, stream=None):
+    """dtok[ids] += dout, dpos[t] += sum_b dout (fp32, in place; either may be None)."""
+    b, t = ids.shape
+    e = dout.shape[-1]
+    _check_ids("embedding_bwd", ids)
+    _check_dev("embedding_bwd", torch.float32, dout, dtok, dpos)
+    vocab = vocab if vocab is not None else (dtok.shape[0] if dtok is not None else 1)
+    rc = load().ctattn_embedding_bwd(F32, _ptr(ids), _ptr(dout), _ptr(dtok), _ptr(dpos), b, t, e, vocab,
+                                     _stream_handle(stream))
+    _check(rc, "ctattn_embedding_bwd")
+
+
+def softmax_fwd(z, temperature: float = 1.0, stream=None):
+    v = z.shape[-1]
+    _check_dev("softmax_fwd", z.dtype, z)
+    p = torch.empty_like(z)
+    rc = load().ctattn_softmax_fwd(_DTYPE_CODE[z.dtype], _ptr(z), _ptr(p), _rows(z, v, "softmax_fwd"), v,
+                                   float(temperature), _stream_handle(stream))
+    _check(rc, "ctattn_softmax_fwd")
+    return p
+
+
+def softmax_bwd(p, dp, temperature: float = 1.0, stream=None):
+    v = p.shape[-1]
+    _check_dev("softmax_bwd", p.dtype, p, dp)
+    dz = torch.empty_like(p)
+    rc = load().ctattn_softmax_bwd(_DTYPE_CODE[p.dtype], _ptr(p), _ptr(dp), _ptr(dz), _rows(p, v, "softmax_bwd"), v,
+                                   float(temperature), _stream_handle(stream))
+    _check(rc, "ctattn_softmax_bwd")
+    return dz
+
+
+def cross_entropy_fwd(p, target, stream=None):
+    """Per-row -log p[target] / N (fp32, the shape of target)."""
+    v = p.shape[-1]
+    n = _rows(p, v, "cross_entropy_fwd")
+    _check_dev("cross_entropy_fwd", p.dtype, p)
+    _check_ids("cross_entropy_fwd", target)
+    if target.numel() != n:
+        raise ValueError("cross_entropy_fwd: one target per row")
+    loss = torch.empty(target.shape, dtype=torch.float32, device=p.device)
+    rc = load().ctattn_cross_entropy_fwd(_DTYPE_CODE[p.dtype], _ptr(p), _ptr(target), _ptr(loss), n, v,
+                                         _stream_handle(stream))
+    _check(rc, "ctattn_cross_entropy_fwd")
+    return loss
+
+
+def cross_entropy_bwd(p, target, stream=None):
+    v = p.shape[-1]
+    n = _rows(p, v, "cross_entropy_bwd")
+    _check_dev("cross_entropy_bwd", p.dtype, p)
+    _check_ids("cross_entropy_bwd", target)
+    dp = torch.empty_like(p)
+    rc = load().ctattn_cross_entropy_bwd(_DTYPE_CODE[p.dtype], _ptr(p), _ptr(target), _ptr(dp), n, v,
+                                         _stream_handle(stream))
+    _check(rc, "ctattn_cross_entropy_bwd")
+    return dp
+
+
+def softmax_cross_entropy_bwd(p, target, temperature: float = 1.0, stream=None):
+    v = p.shape[-1]
+    n = _rows(p, v, "softmax_cross_entropy_bwd")
+    _check_dev("softmax_cross_entropy_bwd", p.dtype, p)
+    _check_ids("softmax_cross_entropy_bwd", target)
+    dz = torch.empty_like(p)
+    rc = load().ctattn_softmax_cross_entropy_bwd(_DTYPE_CODE[p.dtype], _ptr(p), _ptr(target), _ptr(dz), n, v,
+                                                 float(temperature), _stream_handle(stream))
+    _check(rc, "ctattn_softmax_cross_entropy_bwd")
+    return dz
+
+
+def adam_update(param, grad, m, v, step: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0,
+                decoupled: bool = False, stream=None):
+    """One Adam (decoupled=False) or AdamW step, in place on fp32 param / m / v."""
+    _check_dev("adam_update", torch.float32, param, grad, m, v)
+    n = param.numel()
+    if not (grad.numel() == m.numel() == v.numel() == n):
+        raise ValueError("adam_update: size mismatch")
+    rc = load().ctattn_adam_update(F32, _ptr(param), _ptr(grad), _ptr(m), _ptr(v), n, float(lr), float(beta1),
+                                   float(beta2), float(eps), float(weight_decay), int(step), int(bool(decoupled)),
+                                   _stream_handle(stream))
+    _check(rc, "ctattn_adam_update")

@@ -1,0 +1,610 @@
+// Kernels and C-ABI entry points of the layers around the attention path that a NanoGPT
+// training step needs (declared in include/ctattn.h): LayerNorm, the elementwise
+// activations, token + position embeddings, softmax with temperature, cross-entropy on
+// probabilities, and the Adam update.  The linear layers run on the MFMA GEMM family
+// (proj_capi.hip).
+//
+// These replace the reference's per-layer kernels (layer_norm_kernels.cu, relu_/gelu_/
+// sigmoid_/tanh_kernels.cu, embedding_kernels.cu, loss_kernels.cu, adam_kernels.cu) with
+// the same math, with these deliberate differences:
+//   * LayerNorm keeps its row statistics in fp32 buffers the caller owns and sums the gamma /
+//     beta gradients deterministically (two-stage column sums, no atomics; the reference
+//     atomically adds every row, layer_norm_kernels.cu backward);
+//   * one wave per row (64 lanes) for the row-wise kernels instead of one thread per row
+//     (loss_kernels.cu: softmaxKernel walks a whole row in one thread);
+//   * ids / targets outside [0, vocab) read nothing: an embedding row of zeros and a zero
+//     loss (the reference checks targets, loss_kernels.cu, but not embedding ids);
+//   * the position embedding is indexed by the position t of each row, not by the flattened
+//     b * T + t (out of bounds for B > 1 in embedding_kernels.cu);
+//   * Adam / AdamW are the textbook updates, the step counter advanced once per step by the
+//     caller (the reference increments it twice per step, AdamOptimizer.cu:75,95, and stores
+//     the bias-corrected moments back, adam_kernels.cu adamUpdateKernel).
+// Storage is fp32 or bf16 (bf16 widened to fp32 for arithmetic); the embedding backward and
+// Adam, which accumulate into fp32 state, take fp32 storage only.
+#include "attn_common.h"
+#include "capi_util.h"
+#include "ctattn.h"
+
+#include <math.h>
+
+#include <type_traits>
+
+namespace ctattn {
+namespace {
+
+template <typename T> __device__ __forceinline__ float ld(const T *p, int64_t i);
+template <> __device__ __forceinline__ float ld<float>(const float *p, int64_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ld<bf16_t>(const bf16_t *p, int64_t i) { return to_f32(p[i]); }
+template <typename T> __device__ __forceinline__ void st(T *p, int64_t i, float x) { p[i] = from_f32<T>(x); }
+
+// ---------------------------------------------------------------------------------------
+// LayerNorm over the last dimension (layer_norm_kernels.cu): y = (x - mean) rstd g + b.
+// One wave per row.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_fwd_kernel(const T *__restrict__ x, const T *__restrict__ g,
+                                                           const T *__restrict__ b, T *__restrict__ y,
+                                                           float *__restrict__ mean_out, float *__restrict__ rstd_out,
+                                                           int64_t N, int D, float eps) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= N) return;
+    const T *xr = x + row * D;
+    float s = 0.f;
+    for (int c = lane; c < D; c += kWave) s += ld(xr, c);
+    const float mean = wave_sum(s) / float(D);
+    float v = 0.f;
+    for (int c = lane; c < D; c += kWave) {
+        const float dx = ld(xr, c) - mean;
+        v += dx * dx;
+    }
+    const float rstd = 1.f / sqrtf(wave_sum(v) / float(D) + eps);
+    T *yr = y + row * D;
+    for (int c = lane; c < D; c += kWave) st(yr, c, (ld(xr, c) - mean) * rstd * ld(g, c) + ld(b, c));
+    if (lane == 0) {
+        mean_out[row] = mean;
+        rstd_out[row] = rstd;
+    }
+}
+
+// dx = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)), dxhat = dy g.  One wave per row.
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_bwd_dx_kernel(const T *__restrict__ x, const T *__restrict__ g,
+                                                              const T *__restrict__ dy, const float *__restrict__ mean,
+                                                              const float *__restrict__ rstd, T *__restrict__ dx,
+                                                              int64_t N, int D) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= N) return;
+    const T *xr = x + row * D;
+    const T *dyr = dy + row * D;
+    const float mu = mean[row], rs = rstd[row];
+    float s1 = 0.f, s2 = 0.f;
+    for (int c = lane; c < D; c += kWave) {
+        const float xh = (ld(xr, c) - mu) * rs;
+        const float dxh = ld(dyr, c) * ld(g, c);
+        s1 += dxh;
+        s2 += dxh * xh;
+    }
+    const float m1 = wave_sum(s1) / float(D), m2 = wave_sum(s2) / float(D);
+    T *dxr = dx + row * D;
+    for (int c = lane; c < D; c += kWave) {
+        const float xh = (ld(xr, c) - mu) * rs;
+        st(dxr, c, rs * (ld(dyr, c) * ld(g, c) - m1 - xh * m2));
+    }
+}
+
+constexpr int kLnRowsPerChunk = 64;
+
+// Stage 1 of the gamma / beta gradients: part[chunk][c] = sum over the chunk's rows of
+// dy * xhat (first D floats) and dy (next D floats).  One thread per column.
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_bwd_part_kernel(const T *__restrict__ x, const T *__restrict__ dy,
+                                                                const float *__restrict__ mean,
+                                                                const float *__restrict__ rstd,
+                                                                float *__restrict__ part, int64_t N, int D) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t chunk = blockIdx.y;
+    if (c >= D) return;
+    const int64_t r0 = chunk * kLnRowsPerChunk;
+    const int64_t r1 = r0 + kLnRowsPerChunk < N ? r0 + kLnRowsPerChunk : N;
+    float sg = 0.f, sb = 0.f;
+    for (int64_t r = r0; r < r1; ++r) {
+        const float d = ld(dy, r * D + c);
+        sg += d * (ld(x, r * D + c) - mean[r]) * rstd[r];
+        sb += d;
+    }
+    part[chunk * 2 * D + c] = sg;
+    part[chunk * 2 * D + D + c] = sb;
+}
+
+// Stage 2: dgamma[c] += sum_chunk part[chunk][c], dbeta likewise, in chunk order.
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *__restrict__ part, T *__restrict__ dg,
+                                                                  T *__restrict__ db, int64_t chunks, int D) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= D) return;
+    float sg = 0.f, sb = 0.f;
+    for (int64_t k = 0; k < chunks; ++k) {
+        sg += part[k * 2 * D + c];
+        sb += part[k * 2 * D + D + c];
+    }
+    if (dg != nullptr) st(dg, c, ld(dg, c) + sg);
+    if (db != nullptr) st(db, c, ld(db, c) + sb);
+}
+
+// ---------------------------------------------------------------------------------------
+// Activations (relu_/gelu_/sigmoid_/tanh_kernels.cu), elementwise.
+// ---------------------------------------------------------------------------------------
+constexpr float kGeluC = 0.7978845608028654f;  // sqrt(2 / pi)
+constexpr float kGeluA = 0.044715f;
+
+__device__ __forceinline__ float act_fwd(int kind, float x) {
+    switch (kind) {
+        case CTATTN_ACT_RELU: return x > 0.f ? x : 0.f;
+        case CTATTN_ACT_GELU: return 0.5f * x * (1.f + tanhf(kGeluC * (x + kGeluA * x * x * x)));
+        case CTATTN_ACT_SIGMOID: return 1.f / (1.f + expf(-x));
+        default: return tanhf(x);
+    }
+}
+
+__device__ __forceinline__ float act_grad(int kind, float x) {
+    switch (kind) {
+        case CTATTN_ACT_RELU: return x > 0.f ? 1.f : 0.f;
+        case CTATTN_ACT_GELU: {
+            const float t = tanhf(kGeluC * (x + kGeluA * x * x * x));
+            return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * kGeluC * (1.f + 3.f * kGeluA * x * x);
+        }
+        case CTATTN_ACT_SIGMOID: {
+            const float s = 1.f / (1.f + expf(-x));
+            return s * (1.f - s);
+        }
+        default: {
+            const float t = tanhf(x);
+            return 1.f - t * t;
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void act_fwd_kernel(int kind, const T *__restrict__ x, T *__restrict__ y, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+        st(y, i, act_fwd(kind, ld(x, i)));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void act_bwd_kernel(int kind, const T *__restrict__ x, const T *__restrict__ dy,
+                                                     T *__restrict__ dx, int64_t n) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+        st(dx, i, act_grad(kind, ld(x, i)) * ld(dy, i));
+}
+
+// ---------------------------------------------------------------------------------------
+// Token + position embedding (embedding_kernels.cu).
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void embedding_fwd_kernel(const int32_t *__restrict__ ids, const T *__restrict__ tok,
+                                                           const T *__restrict__ pos, T *__restrict__ out, int64_t rows,
+                                                           int T_, int E, int64_t vocab) {
+    const int64_t n = rows * E;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t r = i / E;
+        const int e = int(i - r * E);
+        const int t = int(r % T_);
+        float v = pos != nullptr ? ld(pos, int64_t(t) * E + e) : 0.f;
+        if (tok != nullptr) {
+            const int64_t id = ids[r];
+            if (id >= 0 && id < vocab) v += ld(tok, id * E + e);
+        }
+        st(out, i, v);
+    }
+}
+
+// dtok[ids[r]][e] += dout[r][e] (fp32 atomics); dpos[t][e] += sum_b dout[b][t][e] (one thread
+// per (t, e), fixed order over b).
+__global__ __launch_bounds__(256) void embedding_bwd_tok_kernel(const int32_t *__restrict__ ids,
+                                                               const float *__restrict__ dout, float *__restrict__ dtok,
+                                                               int64_t rows, int E, int64_t vocab) {
+    const int64_t n = rows * E;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t r = i / E;
+        const int64_t id = ids[r];
+        if (id >= 0 && id < vocab) unsafeAtomicAdd(dtok + id * E + (i - r * E), dout[i]);
+    }
+}
+
+__global__ __launch_bounds__(256) void embedding_bwd_pos_kernel(const float *__restrict__ dout, float *__restrict__ dpos,
+                                                               int64_t B, int T_, int E) {
+    const int64_t n = int64_t(T_) * E;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        float s = 0.f;
+        for (int64_t b = 0; b < B; ++b) s += dout[b * n + i];
+        dpos[i] += s;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Softmax with temperature, cross-entropy (loss_kernels.cu).  One wave per row.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_fwd_kernel(const T *__restrict__ z, T *__restrict__ p, int64_t N, int V,
+                                                         float inv_temp) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= N) return;
+    const T *zr = z + row * V;
+    float m = -INFINITY;
+    for (int c = lane; c < V; c += kWave) m = fmaxf(m, ld(zr, c));
+    m = wave_max(m);
+    float s = 0.f;
+    for (int c = lane; c < V; c += kWave) s += expf((ld(zr, c) - m) * inv_temp);
+    const float inv_s = 1.f / wave_sum(s);
+    T *pr = p + row * V;
+    for (int c = lane; c < V; c += kWave) st(pr, c, expf((ld(zr, c) - m) * inv_temp) * inv_s);
+}
+
+// dz = p (dp - sum_c p dp) / temperature (softmaxBackwardKernel's formula, from p).
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(const T *__restrict__ p, const T *__restrict__ dp,
+                                                         T *__restrict__ dz, int64_t N, int V, float inv_temp) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= N) return;
+    const T *pr = p + row * V;
+    const T *dpr = dp + row * V;
+    float s = 0.f;
+    for (int c = lane; c < V; c += kWave) s += ld(pr, c) * ld(dpr, c);
+    s = wave_sum(s);
+    T *dzr = dz + row * V;
+    for (int c = lane; c < V; c += kWave) st(dzr, c, ld(pr, c) * (ld(dpr, c) - s) * inv_temp);
+}
+
+// loss[r] = -log(p[r][target[r]]) / N (0 for a target outside [0, V)).  One thread per row.
+template <typename T>
+__global__ __launch_bounds__(256) void xent_fwd_kernel(const T *__restrict__ p, const int32_t *__restrict__ tgt,
+                                                      float *__restrict__ loss, int64_t N, int V) {
+    const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= N) return;
+    const int t = tgt[r];
+    loss[r] = (t >= 0 && t < V) ? -logf(ld(p, r * V + t)) / float(N) : 0.f;
+}
+
+// dp[r][c] = -1 / (p N) at the target, 0 elsewhere (crossEntropyLossBackwardKernel).
+template <typename T>
+__global__ __launch_bounds__(256) void xent_bwd_kernel(const T *__restrict__ p, const int32_t *__restrict__ tgt,
+                                                      T *__restrict__ dp, int64_t N, int V) {
+    const int64_t n = N * V;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t r = i / V;
+        const int c = int(i - r * V);
+        st(dp, i, c == tgt[r] ? -1.f / (ld(p, i) * float(N)) : 0.f);
+    }
+}
+
+// The two above composed with the softmax backward: dz = (p - onehot(target)) / (N T), the
+// same gradient without dividing by p.
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_xent_bwd_kernel(const T *__restrict__ p, const int32_t *__restrict__ tgt,
+                                                              T *__restrict__ dz, int64_t N, int V, float scale) {
+    const int64_t n = N * V;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t r = i / V;
+        const int c = int(i - r * V);
+        const int t = tgt[r];
+        const float onehot = c == t ? 1.f : 0.f;
+        st(dz, i, (t >= 0 && t < V) ? (ld(p, i) - onehot) * scale : 0.f);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Adam / AdamW (adam_kernels.cu:25 adamUpdateKernel, adamWUpdateKernel), textbook
+// bias-corrected form.  Adam folds the weight decay into the gradient (g + decay p, as
+// adamUpdateKernel does); AdamW decays the parameter itself, p (1 - lr decay) - lr update
+// (adamWUpdateKernel).  m and v keep the uncorrected moments (the reference stores the
+// bias-corrected ones back, so its correction compounds from step to step).
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void adam_kernel(float *__restrict__ param, const float *__restrict__ grad,
+                                                  float *__restrict__ m, float *__restrict__ v, int64_t n, float lr,
+                                                  float b1, float b2, float eps, float decay, int decoupled, float c1,
+                                                  float c2) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const float p = param[i];
+        const float g = decoupled ? grad[i] : grad[i] + decay * p;
+        const float mi = b1 * m[i] + (1.f - b1) * g;
+        const float vi = b2 * v[i] + (1.f - b2) * g * g;
+        m[i] = mi;
+        v[i] = vi;
+        const float upd = lr * (mi * c1) / (sqrtf(vi * c2) + eps);
+        param[i] = decoupled ? p * (1.f - lr * decay) - upd : p - upd;
+    }
+}
+
+unsigned grid_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return unsigned(b < 65536 ? (b > 0 ? b : 1) : 65536);
+}
+
+unsigned rows_grid(int64_t rows) { return unsigned((rows + 3) / 4); }  // 4 waves (rows) per block
+
+}  // namespace
+}  // namespace ctattn
+
+namespace {
+
+using ctattn::bf16_t;
+using ctattn::capi::align_up;
+using ctattn::capi::fail;
+using ctattn::capi::finish;
+using ctattn::capi::ok;
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+int check_dtype(const char *fn, int dtype, bool f32_only = false) {
+    if (dtype == CTATTN_F32 || (!f32_only && dtype == CTATTN_BF16)) return 0;
+    if (dtype == CTATTN_BF16) return fail(hipErrorNotSupported, "%s: bf16 storage is not supported (fp32 only)", fn);
+    return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+}
+
+int check_rows(const char *fn, int64_t N, int64_t D, const char *dname) {
+    if (N < 0 || D < 1)
+        return fail(hipErrorInvalidValue, "%s: need rows >= 0 and %s >= 1 (got %lld, %lld)", fn, dname, (long long)N,
+                    (long long)D);
+    if (D > 2147483647 || N > 2147483647) return fail(hipErrorInvalidValue, "%s: sizes too large", fn);
+    return 0;
+}
+
+template <typename F>
+hipError_t by_dtype(int dtype, F f) {
+    if (dtype == CTATTN_F32) return f(static_cast<float *>(nullptr));
+    return f(static_cast<bf16_t *>(nullptr));
+}
+
+}  // namespace
+
+extern "C" {
+
+int ctattn_layernorm_fwd(int dtype, const void *x, const void *gamma, const void *beta, void *y, float *mean,
+                         float *rstd, int64_t N, int64_t D, float eps, void *stream) {
+    const char *fn = "ctattn_layernorm_fwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, D, "D")) return rc;
+    if (N == 0) return ok();
+    if (!x || !gamma || !beta || !y || !mean || !rstd) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    if (!(eps >= 0.f)) return fail(hipErrorInvalidValue, "%s: eps must be >= 0", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::layernorm_fwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
+                           static_cast<const T *>(x), static_cast<const T *>(gamma), static_cast<const T *>(beta),
+                           static_cast<T *>(y), mean, rstd, N, int(D), eps);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int64_t ctattn_layernorm_bwd_workspace_bytes(int dtype, int64_t N, int64_t D) {
+    if (check_dtype("ctattn_layernorm_bwd_workspace_bytes", dtype) ||
+        check_rows("ctattn_layernorm_bwd_workspace_bytes", N, D, "D"))
+        return -1;
+    ok();
+    const int64_t chunks = (N + ctattn::kLnRowsPerChunk - 1) / ctattn::kLnRowsPerChunk;
+    return align_up(chunks * 2 * D * int64_t(sizeof(float)));
+}
+
+int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void *dy, const float *mean,
+                         const float *rstd, void *dx, void *dgamma, void *dbeta, void *workspace,
+                         int64_t workspace_bytes, int64_t N, int64_t D, void *stream) {
+    const char *fn = "ctattn_layernorm_bwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, D, "D")) return rc;
+    if (N == 0) return ok();
+    if (!x || !dy || !mean || !rstd) return fail(hipErrorInvalidValue, "%s: null x/dy/mean/rstd pointer", fn);
+    if (dx && !gamma) return fail(hipErrorInvalidValue, "%s: dx needs gamma", fn);
+    const int64_t chunks = (N + ctattn::kLnRowsPerChunk - 1) / ctattn::kLnRowsPerChunk;
+    if (chunks > 65535) return fail(hipErrorInvalidValue, "%s: N = %lld rows exceed the gradient reduction's limit", fn, (long long)N);
+    const int64_t need = ctattn_layernorm_bwd_workspace_bytes(dtype, N, D);
+    if ((dgamma || dbeta) && (workspace == nullptr || workspace_bytes < need))
+        return fail(hipErrorInvalidValue, "%s: workspace of %lld bytes given, %lld needed", fn,
+                    (long long)workspace_bytes, (long long)need);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        const T *xt = static_cast<const T *>(x);
+        const T *dyt = static_cast<const T *>(dy);
+        if (dx)
+            hipLaunchKernelGGL(ctattn::layernorm_bwd_dx_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st, xt,
+                               static_cast<const T *>(gamma), dyt, mean, rstd, static_cast<T *>(dx), N, int(D));
+        if (dgamma || dbeta) {
+            float *part = static_cast<float *>(workspace);
+            hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 255) / 256), unsigned(chunks)),
+                               dim3(256), 0, st, xt, dyt, mean, rstd, part, N, int(D));
+            hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 255) / 256)), dim3(256), 0,
+                               st, part, static_cast<T *>(dgamma), static_cast<T *>(dbeta), chunks, int(D));
+        }
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_activation_fwd(int dtype, int kind, const void *x, void *y, int64_t n, void *stream) {
+    const char *fn = "ctattn_activation_fwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (kind < CTATTN_ACT_RELU || kind > CTATTN_ACT_TANH)
+        return fail(hipErrorInvalidValue, "%s: unknown activation %d", fn, kind);
+    if (n < 0) return fail(hipErrorInvalidValue, "%s: negative size", fn);
+    if (n == 0) return ok();
+    if (!x || !y) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::act_fwd_kernel<T>, dim3(ctattn::grid_for(n)), dim3(256), 0, st, kind,
+                           static_cast<const T *>(x), static_cast<T *>(y), n);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_activation_bwd(int dtype, int kind, const void *x, const void *dy, void *dx, int64_t n, void *stream) {
+    const char *fn = "ctattn_activation_bwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (kind < CTATTN_ACT_RELU || kind > CTATTN_ACT_TANH)
+        return fail(hipErrorInvalidValue, "%s: unknown activation %d", fn, kind);
+    if (n < 0) return fail(hipErrorInvalidValue, "%s: negative size", fn);
+    if (n == 0) return ok();
+    if (!x || !dy || !dx) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::act_bwd_kernel<T>, dim3(ctattn::grid_for(n)), dim3(256), 0, st, kind,
+                           static_cast<const T *>(x), static_cast<const T *>(dy), static_cast<T *>(dx), n);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_embedding_fwd(int dtype, const int32_t *ids, const void *tok, const void *pos, void *out, int64_t B,
+                         int64_t T, int64_t E, int64_t vocab, int64_t max_len, void *stream) {
+    const char *fn = "ctattn_embedding_fwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (B < 0 || T < 0 || E < 1 || vocab < 1 || max_len < 1 || T > max_len || E > 2147483647 || T > 2147483647)
+        return fail(hipErrorInvalidValue, "%s: invalid sizes B=%lld T=%lld E=%lld vocab=%lld max_len=%lld", fn,
+                    (long long)B, (long long)T, (long long)E, (long long)vocab, (long long)max_len);
+    if (B * T == 0) return ok();
+    if (!ids || !out || (!tok && !pos)) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T_ = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::embedding_fwd_kernel<T_>, dim3(ctattn::grid_for(B * T * E)), dim3(256), 0, st, ids,
+                           static_cast<const T_ *>(tok), static_cast<const T_ *>(pos), static_cast<T_ *>(out), B * T,
+                           int(T), int(E), vocab);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_embedding_bwd(int dtype, const int32_t *ids, const void *dout, void *dtok, void *dpos, int64_t B,
+                         int64_t T, int64_t E, int64_t vocab, void *stream) {
+    const char *fn = "ctattn_embedding_bwd";
+    if (int rc = check_dtype(fn, dtype, true)) return rc;
+    if (B < 0 || T < 0 || E < 1 || vocab < 1 || E > 2147483647 || T > 2147483647)
+        return fail(hipErrorInvalidValue, "%s: invalid sizes", fn);
+    if (B * T == 0) return ok();
+    if (!ids || !dout) return fail(hipErrorInvalidValue, "%s: null ids/dout pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const float *g = static_cast<const float *>(dout);
+    if (dtok)
+        hipLaunchKernelGGL(ctattn::embedding_bwd_tok_kernel, dim3(ctattn::grid_for(B * T * E)), dim3(256), 0, st, ids, g,
+                           static_cast<float *>(dtok), B * T, int(E), vocab);
+    if (dpos)
+        hipLaunchKernelGGL(ctattn::embedding_bwd_pos_kernel, dim3(ctattn::grid_for(T * E)), dim3(256), 0, st, g,
+                           static_cast<float *>(dpos), B, int(T), int(E));
+    return finish(fn, hipGetLastError(), st);
+}
+
+int ctattn_softmax_fwd(int dtype, const void *z, void *p, int64_t N, int64_t V, float temperature, void *stream) {
+    const char *fn = "ctattn_softmax_fwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, V, "V")) return rc;
+    if (!(temperature > 0.f)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
+    if (N == 0) return ok();
+    if (!z || !p) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::softmax_fwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
+                           static_cast<const T *>(z), static_cast<T *>(p), N, int(V), 1.f / temperature);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_softmax_bwd(int dtype, const void *p, const void *dp, void *dz, int64_t N, int64_t V, float temperature,
+                       void *stream) {
+    const char *fn = "ctattn_softmax_bwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, V, "V")) return rc;
+    if (!(temperature > 0.f)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
+    if (N == 0) return ok();
+    if (!p || !dp || !dz) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::softmax_bwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
+                           static_cast<const T *>(p), static_cast<const T *>(dp), static_cast<T *>(dz), N, int(V),
+                           1.f / temperature);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, float *loss, int64_t N, int64_t V,
+                             void *stream) {
+    const char *fn = "ctattn_cross_entropy_fwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, V, "V")) return rc;
+    if (N == 0) return ok();
+    if (!p || !target || !loss) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::xent_fwd_kernel<T>, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st,
+                           static_cast<const T *>(p), target, loss, N, int(V));
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_cross_entropy_bwd(int dtype, const void *p, const int32_t *target, void *dp, int64_t N, int64_t V,
+                             void *stream) {
+    const char *fn = "ctattn_cross_entropy_bwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, V, "V")) return rc;
+    if (N == 0) return ok();
+    if (!p || !target || !dp) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::xent_bwd_kernel<T>, dim3(ctattn::grid_for(N * V)), dim3(256), 0, st,
+                           static_cast<const T *>(p), target, static_cast<T *>(dp), N, int(V));
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_softmax_cross_entropy_bwd(int dtype, const void *p, const int32_t *target, void *dz, int64_t N, int64_t V,
+                                     float temperature, void *stream) {
+    const char *fn = "ctattn_softmax_cross_entropy_bwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, V, "V")) return rc;
+    if (!(temperature > 0.f)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
+    if (N == 0) return ok();
+    if (!p || !target || !dz) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const float scale = 1.f / (float(N) * temperature);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::softmax_xent_bwd_kernel<T>, dim3(ctattn::grid_for(N * V)), dim3(256), 0, st,
+                           static_cast<const T *>(p), target, static_cast<T *>(dz), N, int(V), scale);
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_adam_update(int dtype, void *param, const void *grad, float *m, float *v, int64_t n, float lr, float beta1,
+                       float beta2, float eps, float weight_decay, int64_t step, int decoupled, void *stream) {
+    const char *fn = "ctattn_adam_update";
+    if (int rc = check_dtype(fn, dtype, true)) return rc;
+    if (n < 0 || step < 1 || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps > 0.f))
+        return fail(hipErrorInvalidValue, "%s: need n >= 0, step >= 1, 0 <= beta < 1, eps > 0", fn);
+    if (n == 0) return ok();
+    if (!param || !grad || !m || !v) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    const float c1 = float(1.0 / (1.0 - pow(double(beta1), double(step))));
+    const float c2 = float(1.0 / (1.0 - pow(double(beta2), double(step))));
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(ctattn::adam_kernel, dim3(ctattn::grid_for(n)), dim3(256), 0, st, static_cast<float *>(param),
+                       static_cast<const float *>(grad), m, v, n, lr, beta1, beta2, eps, weight_decay, decoupled ? 1 : 0,
+                       c1, c2);
+    return finish(fn, hipGetLastError(), st);
+}
+
+}  // extern "C"

@@ -260,6 +260,102 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
     return finish(fn, e, st);
 }
 
+// ---- plain linear layers (LinearLayer.cu / linear_kernels.cu; also the un-embedding) ----
+
+namespace {
+
+int validate_linear(const char *fn, int dtype, int64_t M, int64_t N, int64_t K) {
+    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (M < 0 || N < 1 || K < 1)
+        return fail(hipErrorInvalidValue, "%s: need M >= 0, N >= 1, K >= 1 (got %lld, %lld, %lld)", fn, (long long)M,
+                    (long long)N, (long long)K);
+    if (M > 2147483647 || N > 2147483647 || K > 2147483647)
+        return fail(hipErrorInvalidValue, "%s: M, N and K must each be below 2^31", fn);
+    return 0;
+}
+
+bool linear_vec4(int dtype, int64_t M, int64_t N, int64_t K, std::initializer_list<const void *> ptrs) {
+    if (M % 4 != 0 || N % 4 != 0 || K % 4 != 0) return false;
+    const uintptr_t a = uintptr_t(4 * elem_bytes(dtype));
+    for (const void *p : ptrs)
+        if (p != nullptr && uintptr_t(p) % a != 0) return false;
+    return true;
+}
+
+}  // namespace
+
+int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, void *y, int64_t M, int64_t N,
+                      int64_t K, void *stream) {
+    const char *fn = "ctattn_linear_fwd";
+    if (int rc = validate_linear(fn, dtype, M, N, K)) return rc;
+    if (M == 0) return ok();
+    if (!x || !w || !y) return fail(hipErrorInvalidValue, "%s: null x/w/y pointer", fn);
+    // y[m][n] = sum_k x[m][k] w[n][k] + b[n]: A = x [M][K], B = w [N][K], both K-contiguous.
+    GemmParams p = make_params(M, N, K, 0, 1, linear_view(nullptr, N), nullptr);
+    p.batch[0].nseg = 1;
+    p.batch[0].a[0] = linear_view(x, K);
+    p.batch[0].b[0] = linear_view(w, K);
+    p.batch[0].out = y;
+    p.batch[0].bias = b;
+    const bool v4 = linear_vec4(dtype, M, N, K, {x, w, y});
+    return finish(fn, ctattn::launch_proj_gemm(dtype, p, 1, true, true, v4, as_stream(stream)), as_stream(stream));
+}
+
+int64_t ctattn_linear_bwd_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K) {
+    if (validate_linear("ctattn_linear_bwd_workspace_bytes", dtype, M, N, K)) return -1;
+    ok();
+    return splitk_bytes(N, K, M, 1) + align_up(ctattn::colsum_workspace_floats(M, N) * int64_t(sizeof(float)));
+}
+
+int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, void *dx, void *dw, void *db,
+                      void *workspace, int64_t workspace_bytes, int64_t M, int64_t N, int64_t K, void *stream) {
+    const char *fn = "ctattn_linear_bwd";
+    if (int rc = validate_linear(fn, dtype, M, N, K)) return rc;
+    if (M == 0) return ok();
+    if (!dy) return fail(hipErrorInvalidValue, "%s: null dy pointer", fn);
+    if (dw && !x) return fail(hipErrorInvalidValue, "%s: dw needs x", fn);
+    if (dx && !w) return fail(hipErrorInvalidValue, "%s: dx needs w", fn);
+    const int64_t need = ctattn_linear_bwd_workspace_bytes(dtype, M, N, K);
+    if ((dw || db) && (workspace == nullptr || workspace_bytes < need))
+        return fail(hipErrorInvalidValue,
+                    "%s: workspace of %lld bytes given, %lld needed (ctattn_linear_bwd_workspace_bytes)", fn,
+                    (long long)workspace_bytes, (long long)need);
+    hipStream_t st = as_stream(stream);
+    const bool v4 = linear_vec4(dtype, M, N, K, {x, w, dy, dx, dw});
+    float *ws = static_cast<float *>(workspace);
+    hipError_t e = hipSuccess;
+    if (dw) {
+        // dw[n][k] += sum_m dy[m][n] x[m][k]: M' = N, N' = K, K' = M.  A(m'=n, k'=m) = dy stored
+        // [k'][m']; B(k'=m, n'=k) = x stored [k'][n'].
+        const int splits = choose_splits(N, K, M, 1);
+        GemmParams p = make_params(N, K, M, 1, splits, linear_view(nullptr, K), ws);
+        p.batch[0].nseg = 1;
+        p.batch[0].a[0] = linear_view(dy, N);
+        p.batch[0].b[0] = linear_view(x, K);
+        p.batch[0].out = dw;
+        p.batch[0].bias = nullptr;
+        e = ctattn::launch_proj_gemm(dtype, p, 1, false, false, v4, st);
+        if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (db) {
+        float *cws = reinterpret_cast<float *>(static_cast<char *>(workspace) + splitk_bytes(N, K, M, 1));
+        e = ctattn::launch_colsum_add(dtype, linear_view(dy, N), int(M), int(N), db, cws, st);
+        if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (dx) {
+        // dx[m][k] = sum_n dy[m][n] w[n][k]: A = dy [M][N] (K-contiguous), B = w stored [k'][n'].
+        GemmParams p = make_params(M, K, N, 0, 1, linear_view(nullptr, K), nullptr);
+        p.batch[0].nseg = 1;
+        p.batch[0].a[0] = linear_view(dy, N);
+        p.batch[0].b[0] = linear_view(w, K);
+        p.batch[0].out = dx;
+        p.batch[0].bias = nullptr;
+        e = ctattn::launch_proj_gemm(dtype, p, 1, true, false, v4, st);
+    }
+    return finish(fn, e, st);
+}
+
 int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n, void *stream) {
     const char *fn = "ctattn_sgd_update";
     if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)

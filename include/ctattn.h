@@ -174,6 +174,158 @@ CTATTN_API int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, con
 CTATTN_API int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n,
                                  void *stream);
 
+/* ---- Layers around the attention path that a NanoGPT training step needs ----
+ *
+ * Activations are row-major [rows, features]; ids / targets are int32 device arrays.  Same
+ * dtype codes as above (fp32 or bf16 storage, fp32 arithmetic) unless noted; the embedding
+ * backward and Adam take fp32 only.  Asynchronous on `stream`, 0 or a hipError_t value.
+ */
+
+/*
+ * Linear layer: y[m][n] = sum_k x[m][k] w[n][k] + b[n] (w is [N][K], b [N] or NULL), on the
+ * MFMA GEMMs.  Replaces the linearForward launch of LinearLayer::forward (LinearLayer.cu:55;
+ * kernel linear_kernels.cu:36) and of UnEmbedding::forward (Embedding.cu:346).
+ */
+CTATTN_API int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, void *y,
+                                 int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Workspace bytes ctattn_linear_bwd needs (>= 0), or -1 on invalid arguments. */
+CTATTN_API int64_t ctattn_linear_bwd_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K);
+
+/*
+ * Backward of the linear layer: dw += dy^T x, db += column sums of dy, dx = dy w
+ * (overwritten).  dw, db or dx may be NULL to skip; the workspace is only needed for dw / db.
+ * Replaces the linearBackwardWB and linearBackward launches of LinearLayer::backward
+ * (LinearLayer.cu:83,95; kernels linear_kernels.cu:115,199) and UnEmbedding::backward
+ * (Embedding.cu:378,390).  Deterministic.
+ */
+CTATTN_API int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, void *dx,
+                                 void *dw, void *db, void *workspace, int64_t workspace_bytes,
+                                 int64_t M, int64_t N, int64_t K, void *stream);
+
+/*
+ * LayerNorm over the last dimension of x [N][D]: y = (x - mean) * rstd * gamma + beta, with
+ * the row statistics written to mean / rstd (fp32 [N]).  Replaces the layerNormForwardKernel
+ * launch of LayerNormLayer::forward (LayerNorm.cu:119; kernel layer_norm_kernels.cu).
+ */
+CTATTN_API int ctattn_layernorm_fwd(int dtype, const void *x, const void *gamma, const void *beta,
+                                    void *y, float *mean, float *rstd, int64_t N, int64_t D,
+                                    float eps, void *stream);
+
+/* Workspace bytes ctattn_layernorm_bwd needs for the gamma / beta gradients. */
+CTATTN_API int64_t ctattn_layernorm_bwd_workspace_bytes(int dtype, int64_t N, int64_t D);
+
+/*
+ * Backward of LayerNorm from the forward's mean / rstd: dx (overwritten), dgamma +=
+ * sum_rows dy * xhat, dbeta += sum_rows dy (either may be NULL; deterministic, no atomics).
+ * Replaces the layerNormBackwardKernel launch of LayerNormLayer::backward (LayerNorm.cu:143).
+ */
+CTATTN_API int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void *dy,
+                                    const float *mean, const float *rstd, void *dx, void *dgamma,
+                                    void *dbeta, void *workspace, int64_t workspace_bytes,
+                                    int64_t N, int64_t D, void *stream);
+
+/* Activation kinds (the reference's ActivationType: ReLU, GELU (tanh form), Sigmoid, Tanh). */
+enum ctattn_activation { CTATTN_ACT_RELU = 0, CTATTN_ACT_GELU = 1, CTATTN_ACT_SIGMOID = 2, CTATTN_ACT_TANH = 3 };
+
+/*
+ * y = act(x), elementwise over n values.  Replaces the four forward launches of
+ * ActivationLayer::forward (ActivationLayer.cu:55-64; kernels relu_kernels.cu:26,
+ * gelu_kernels.cu:31, sigmoid_kernels.cu:26, tanh_kernels.cu:27).
+ */
+CTATTN_API int ctattn_activation_fwd(int dtype, int kind, const void *x, void *y, int64_t n,
+                                     void *stream);
+
+/*
+ * dx = act'(x) * dy, elementwise (dx overwritten).  Replaces the backward launches of
+ * ActivationLayer::backward (ActivationLayer.cu:83-92; kernels relu_kernels.cu:62,
+ * gelu_kernels.cu:79, sigmoid_kernels.cu:63, tanh_kernels.cu:62).
+ */
+CTATTN_API int ctattn_activation_bwd(int dtype, int kind, const void *x, const void *dy, void *dx,
+                                     int64_t n, void *stream);
+
+/*
+ * out[b][t][:] = tok[ids[b][t]][:] + pos[t][:] for ids [B][T] (int32), tok [vocab][E],
+ * pos [max_len][E], T <= max_len; an id outside [0, vocab) contributes a zero row.  Either
+ * table may be NULL (not both) to look up only the other.
+ * Replaces the tokenEmbeddingForwardKernel and positionEmbeddingForwardKernel launches
+ * (Embedding.cu:49,200; kernels embedding_kernels.cu:26,64), indexing positions by t (the
+ * reference's position kernel uses the flattened row b * T + t).
+ */
+CTATTN_API int ctattn_embedding_fwd(int dtype, const int32_t *ids, const void *tok, const void *pos,
+                                    void *out, int64_t B, int64_t T, int64_t E, int64_t vocab,
+                                    int64_t max_len, void *stream);
+
+/*
+ * dtok[ids[b][t]][:] += dout[b][t][:] (fp32 atomics), dpos[t][:] += sum_b dout[b][t][:]
+ * (deterministic); dtok or dpos may be NULL.  fp32 only.  Replaces the
+ * tokenEmbeddingBackwardKernel and positionEmbeddingBackwardKernel launches
+ * (Embedding.cu:82,234; kernels embedding_kernels.cu:98,135).
+ */
+CTATTN_API int ctattn_embedding_bwd(int dtype, const int32_t *ids, const void *dout, void *dtok,
+                                    void *dpos, int64_t B, int64_t T, int64_t E, int64_t vocab,
+                                    void *stream);
+
+/*
+ * p = softmax(z / temperature) over the last dimension of z [N][V].  Replaces the
+ * softmaxKernel launch of Softmax::forward (SoftmaxLoss.cu:42; kernel loss_kernels.cu:29).
+ */
+CTATTN_API int ctattn_softmax_fwd(int dtype, const void *z, void *p, int64_t N, int64_t V,
+                                  float temperature, void *stream);
+
+/*
+ * dz = p * (dp - sum_c p dp) / temperature from the forward's output p.  Replaces the
+ * softmaxBackwardKernel launch of Softmax::backward (SoftmaxLoss.cu:69; kernel
+ * loss_kernels.cu:87), which recomputes p from z.
+ */
+CTATTN_API int ctattn_softmax_bwd(int dtype, const void *p, const void *dp, void *dz, int64_t N,
+                                  int64_t V, float temperature, void *stream);
+
+/*
+ * Cross-entropy on probabilities: loss[r] = -log(p[r][target[r]]) / N (fp32 [N]; 0 for a
+ * target outside [0, V)), so sum(loss) is the mean loss.  Replaces the
+ * crossEntropyLossKernel launch of CrossEntropyLoss::forward (SoftmaxLoss.cu:177; kernel
+ * loss_kernels.cu:150), with an output of N rows (the reference allocates shape[0]).
+ */
+CTATTN_API int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, float *loss,
+                                        int64_t N, int64_t V, void *stream);
+
+/*
+ * dp[r][c] = -1 / (p[r][c] N) at c == target[r], 0 elsewhere.  Replaces the
+ * crossEntropyLossBackwardKernel launch of CrossEntropyLoss::backward (SoftmaxLoss.cu:205;
+ * kernel loss_kernels.cu:191).
+ */
+CTATTN_API int ctattn_cross_entropy_bwd(int dtype, const void *p, const int32_t *target, void *dp,
+                                        int64_t N, int64_t V, void *stream);
+
+/*
+ * The two backward passes above composed: dz = (p - onehot(target)) / (N * temperature), the
+ * gradient of the mean cross-entropy of softmax(z / temperature) without the division by p.
+ * No counterpart in the reference, which chains CrossEntropyLoss::backward and
+ * Softmax::backward (NanoGPT.cu backward); used by NanoGPT training steps.
+ */
+CTATTN_API int ctattn_softmax_cross_entropy_bwd(int dtype, const void *p, const int32_t *target,
+                                                void *dz, int64_t N, int64_t V, float temperature,
+                                                void *stream);
+
+/*
+ * One Adam or AdamW step on n fp32 parameters with fp32 moments m, v (step >= 1, the 1-based
+ * count of this update), c1 = 1 / (1 - b1^step), c2 = 1 / (1 - b2^step):
+ *   decoupled = 0 (Adam):  g = grad + weight_decay * param,
+ *                          param -= lr * c1 m / (sqrt(c2 v) + eps);
+ *   decoupled = 1 (AdamW): g = grad,
+ *                          param = param (1 - lr weight_decay) - lr * c1 m / (sqrt(c2 v) + eps);
+ * after m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g^2 (m, v keep the uncorrected moments).
+ * Replaces the adamUpdateKernel launch of AdamOptimizer::step (AdamOptimizer.cu:90; kernel
+ * adam_kernels.cu:25) and the adamWUpdateKernel launch of AdamWOptimizer::step
+ * (AdamOptimizer.cu:195).  The reference advances its step counter twice per update and
+ * stores the bias-corrected moments back; here the caller passes the step and the moments
+ * stay uncorrected.
+ */
+CTATTN_API int ctattn_adam_update(int dtype, void *param, const void *grad, float *m, float *v,
+                                  int64_t n, float lr, float beta1, float beta2, float eps,
+                                  float weight_decay, int64_t step, int decoupled, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,27 @@ def test_exports_every_declared_symbol(lib):
         assert hasattr(raw, n), f"{n} declared in include/ctattn.h but not exported"
 
 
+def _header_arity() -> dict:
+    """Parameter count of every function include/ctattn.h declares."""
+    import re
+    text = re.sub(r"/\*.*?\*/", "", open(_capi.HEADER_PATH).read(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(ctattn_\w+)\s*\(([^)]*)\)", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_header(lib):
+    """Every ctypes signature the Python binding declares has the header's parameter count."""
+    arity = _header_arity()
+    assert set(arity) == set(_capi.header_functions())
+    for name, n in arity.items():
+        argtypes = getattr(lib, name).argtypes
+        assert argtypes is not None, f"{name}: no ctypes signature"
+        assert len(argtypes) == n, f"{name}: ctypes declares {len(argtypes)} parameters, header {n}"
+
+
 def test_exports_nothing_else(lib):
     """The library is built with hidden visibility: its dynamic symbol table defines exactly
     the functions the header declares (internal C++ symbols stay private, so two builds

@@ -1,0 +1,301 @@
+"""The layers around attention in libctattn.so, op by op through the C-ABI (ctypes), against
+float64 references computed by torch on the CPU.
+
+Each op follows a reference kernel (linear_kernels.cu, layer_norm_kernels.cu, relu / gelu /
+sigmoid / tanh_kernels.cu, embedding_kernels.cu, loss_kernels.cu, adam_kernels.cu); the
+float64 formulas here are the textbook definitions those kernels implement (GELU in its tanh
+form, LayerNorm with the biased variance and eps inside the square root, softmax with a
+temperature, cross-entropy -log p[target] / N).  Tolerances are stated per test: fp32
+storage is held to a few fp32 ulps of the result's scale, bf16 storage to bf16 rounding of
+the inputs and output.  Integer work (embedding lookup) is bit-exact.
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from cudatransformer_amd import _capi
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+F64 = torch.float64
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _randn(shape, seed, scale=1.0):
+    return torch.randn(shape, generator=_gen(seed), dtype=F64) * scale
+
+
+def _dev(t, dtype):
+    return t.to(dtype).contiguous().to(DEV)
+
+
+def _as64(t_dev_or_cpu, dtype):
+    """The values the GPU actually received (rounded to the storage dtype), as float64."""
+    return t_dev_or_cpu.to(dtype).to(F64).cpu()
+
+
+def _close(got, ref, rel, what, abs_floor=0.0):
+    got = got.detach().to(F64).cpu()
+    scale = float(ref.abs().max()) if ref.numel() else 0.0
+    err = float((got - ref).abs().max()) if ref.numel() else 0.0
+    assert err <= rel * scale + abs_floor, f"{what}: max err {err:.3e} vs scale {scale:.3e} (rel {rel})"
+
+
+TOL = {torch.float32: 2e-5, torch.bfloat16: 1.6e-2}
+
+
+# ---- linear --------------------------------------------------------------------------------
+
+LINEAR_SHAPES = [(1, 1, 1), (37, 130, 65), (256, 384, 384), (300, 65, 1536), (64, 4, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mnk", LINEAR_SHAPES)
+@pytest.mark.parametrize("bias", [True, False])
+def test_linear_fwd_bwd(dtype, mnk, bias):
+    m, n, k = mnk
+    print(f"linear {dtype} M={m} N={n} K={k} bias={bias}", flush=True)
+    x = _dev(_randn((m, k), 1), dtype)
+    w = _dev(_randn((n, k), 2, 1 / math.sqrt(k)), dtype)
+    b = _dev(_randn((n,), 3), dtype) if bias else None
+    dy = _dev(_randn((m, n), 4), dtype)
+    dw0 = _randn((n, k), 5)
+    db0 = _randn((n,), 6)
+    dw = _dev(dw0, dtype)
+    db = _dev(db0, dtype) if bias else None
+
+    y = _capi.linear_fwd(x, w, b)
+    dx = _capi.linear_bwd(x, w, dy, dw, db)
+    torch.cuda.synchronize()
+
+    x64, w64, dy64 = _as64(x, dtype), _as64(w, dtype), _as64(dy, dtype)
+    ref_y = x64 @ w64.T + (_as64(b, dtype) if bias else 0.0)
+    _close(y, ref_y, TOL[dtype], "y")
+    _close(dx, dy64 @ w64, TOL[dtype], "dx")
+    # dw / db accumulate into what the buffers held.
+    _close(dw, _as64(dw0, dtype) + dy64.T @ x64, TOL[dtype], "dw")
+    if bias:
+        _close(db, _as64(db0, dtype) + dy64.sum(0), TOL[dtype], "db")
+
+
+def test_linear_bwd_skips_and_empty():
+    x = _dev(_randn((16, 8), 7), torch.float32)
+    w = _dev(_randn((12, 8), 8), torch.float32)
+    dy = _dev(_randn((16, 12), 9), torch.float32)
+    assert _capi.linear_bwd(x, w, dy, None, None, want_dx=False) is None
+    dx = _capi.linear_bwd(x, w, dy)
+    torch.cuda.synchronize()
+    _close(dx, _as64(dy, torch.float32) @ _as64(w, torch.float32), TOL[torch.float32], "dx only")
+    y = _capi.linear_fwd(x[:0], w)
+    assert y.shape == (0, 12)
+
+
+# ---- layernorm -----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nd", [(1, 32), (7, 65), (300, 384), (33, 1536)])
+def test_layernorm_fwd_bwd(dtype, nd):
+    n, d = nd
+    print(f"layernorm {dtype} N={n} D={d}", flush=True)
+    x = _dev(_randn((n, d), 10, 3.0) + 1.5, dtype)
+    g = _dev(1.0 + 0.1 * _randn((d,), 11), dtype)
+    b = _dev(0.1 * _randn((d,), 12), dtype)
+    dy = _dev(_randn((n, d), 13), dtype)
+    dg0, db0 = _randn((d,), 14), _randn((d,), 15)
+    dg, db = _dev(dg0, dtype), _dev(db0, dtype)
+
+    y, mean, rstd = _capi.layernorm_fwd(x, g, b, 1e-5)
+    dx = _capi.layernorm_bwd(x, g, dy, mean, rstd, dg, db)
+    torch.cuda.synchronize()
+
+    x64 = _as64(x, dtype).requires_grad_(True)
+    g64 = _as64(g, dtype).requires_grad_(True)
+    b64 = _as64(b, dtype).requires_grad_(True)
+    ref = F.layer_norm(x64, (d,), g64, b64, 1e-5)
+    ref.backward(_as64(dy, dtype))
+    _close(y, ref.detach(), TOL[dtype], "y")
+    _close(mean, x64.detach().mean(-1), TOL[torch.float32], "mean")
+    _close(rstd, 1 / torch.sqrt(x64.detach().var(-1, unbiased=False) + 1e-5), TOL[torch.float32], "rstd")
+    _close(dx, x64.grad, TOL[dtype] * 2, "dx")
+    _close(dg, _as64(dg0, dtype) + g64.grad, TOL[dtype] * 2, "dgamma")
+    _close(db, _as64(db0, dtype) + b64.grad, TOL[dtype] * 2, "dbeta")
+
+
+def test_layernorm_bwd_is_deterministic():
+    x = _dev(_randn((4099, 384), 16), torch.float32)
+    g = _dev(_randn((384,), 17), torch.float32)
+    dy = _dev(_randn((4099, 384), 18), torch.float32)
+    _, mean, rstd = _capi.layernorm_fwd(x, g, torch.zeros_like(g))
+    outs = []
+    for _ in range(2):
+        dg, db = torch.zeros_like(g), torch.zeros_like(g)
+        _capi.layernorm_bwd(x, g, dy, mean, rstd, dg, db)
+        outs.append((dg.cpu(), db.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+# ---- activations ---------------------------------------------------------------------------
+
+ACTS = {
+    _capi.ACT_RELU: torch.relu,
+    _capi.ACT_GELU: lambda x: F.gelu(x, approximate="tanh"),
+    _capi.ACT_SIGMOID: torch.sigmoid,
+    _capi.ACT_TANH: torch.tanh,
+}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", sorted(ACTS))
+def test_activation_fwd_bwd(dtype, kind):
+    n = 10007
+    x = _dev(_randn((n,), 20 + kind, 3.0), dtype)
+    dy = _dev(_randn((n,), 30 + kind), dtype)
+    y = _capi.activation_fwd(x, kind)
+    dx = _capi.activation_bwd(x, dy, kind)
+    torch.cuda.synchronize()
+    x64 = _as64(x, dtype).requires_grad_(True)
+    ref = ACTS[kind](x64)
+    ref.backward(_as64(dy, dtype))
+    tol = 4e-6 if dtype == torch.float32 else TOL[dtype]
+    _close(y, ref.detach(), tol, "y")
+    _close(dx, x64.grad, tol, "dx")
+
+
+def test_activation_rejects_unknown_kind():
+    x = torch.zeros(8, device=DEV)
+    with pytest.raises(RuntimeError, match="unknown activation"):
+        _capi.activation_fwd(x, 7)
+
+
+# ---- embeddings ----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_embedding_fwd_is_exact(dtype):
+    b, t, e, vocab, max_len = 3, 50, 96, 65, 64
+    ids = torch.randint(0, vocab, (b, t), generator=_gen(40), dtype=torch.int32)
+    ids[0, 0], ids[1, 5], ids[2, 7] = -1, vocab, 1 << 30  # out-of-range ids read a zero row
+    tok = _randn((vocab, e), 41).to(dtype)
+    pos = _randn((max_len, e), 42).to(dtype)
+    got = _capi.embedding_fwd(ids.to(DEV), tok.to(DEV), pos.to(DEV))
+    only_tok = _capi.embedding_fwd(ids.to(DEV), tok.to(DEV), None)
+    only_pos = _capi.embedding_fwd(ids.to(DEV), None, pos.to(DEV))
+    torch.cuda.synchronize()
+    valid = (ids >= 0) & (ids < vocab)
+    rows = torch.where(valid[..., None], tok.float()[ids.clamp(0, vocab - 1).long()], torch.zeros(()))
+    ref_tok = rows
+    ref_pos = pos.float()[:t].expand(b, t, e)
+    assert torch.equal(only_tok.float().cpu(), ref_tok.to(dtype).float())
+    assert torch.equal(only_pos.float().cpu(), ref_pos)
+    assert torch.equal(got.float().cpu(), (ref_tok + ref_pos).to(dtype).float())
+
+
+def test_embedding_bwd():
+    b, t, e, vocab, max_len = 4, 33, 40, 17, 40
+    ids = torch.randint(0, vocab, (b, t), generator=_gen(43), dtype=torch.int32)
+    ids[3, 3] = -2
+    dout = _randn((b, t, e), 44)
+    dtok0, dpos0 = _randn((vocab, e), 45), _randn((max_len, e), 46)
+    dtok, dpos = _dev(dtok0, torch.float32), _dev(dpos0, torch.float32)
+    _capi.embedding_bwd(ids.to(DEV), _dev(dout, torch.float32), dtok, dpos, vocab=vocab)
+    torch.cuda.synchronize()
+    d32 = dout.float().double()
+    ref_tok = dtok0.float().double().clone()
+    valid = ids.flatten() >= 0
+    ref_tok.index_add_(0, ids.flatten()[valid].long(), d32.reshape(-1, e)[valid])
+    ref_pos = dpos0.float().double().clone()
+    ref_pos[:t] += d32.sum(0)
+    _close(dtok, ref_tok, 1e-6, "dtok")
+    _close(dpos, ref_pos, 1e-6, "dpos")
+
+
+def test_embedding_rejects_long_sequence():
+    ids = torch.zeros((1, 9), dtype=torch.int32, device=DEV)
+    tab = torch.zeros((8, 4), device=DEV)
+    with pytest.raises(RuntimeError, match="invalid sizes"):
+        _capi.embedding_fwd(ids, tab, tab)
+
+
+# ---- softmax / cross-entropy ---------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nv", [(1, 1), (37, 65), (4, 50257)])
+@pytest.mark.parametrize("temp", [1.0, 0.7])
+def test_softmax_fwd_bwd(dtype, nv, temp):
+    n, v = nv
+    z = _dev(_randn((n, v), 50, 4.0), dtype)
+    dp = _dev(_randn((n, v), 51), dtype)
+    p = _capi.softmax_fwd(z, temp)
+    dz = _capi.softmax_bwd(p, dp, temp)
+    torch.cuda.synchronize()
+    z64 = _as64(z, dtype).requires_grad_(True)
+    ref = torch.softmax(z64 / temp, -1)
+    ref.backward(_as64(dp, dtype))
+    tol = 1e-5 if dtype == torch.float32 else TOL[dtype]
+    _close(p, ref.detach(), tol, "p")
+    assert torch.allclose(p.double().sum(-1).cpu(), torch.ones(n, dtype=F64), atol=1e-5 if dtype == torch.float32 else 2e-2)
+    # The backward works from the forward's p; compare with the autograd gradient at z.
+    _close(dz, z64.grad, tol * 4, "dz")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cross_entropy_and_fused_backward(dtype):
+    n, v, temp = 300, 65, 0.8
+    z = _randn((n, v), 60, 2.0)
+    tgt = torch.randint(0, v, (n,), generator=_gen(61), dtype=torch.int32)
+    tgt[5], tgt[77] = -1, v  # outside [0, V): zero loss, zero gradient
+    p = _dev(torch.softmax(z / temp, -1), dtype)
+    loss = _capi.cross_entropy_fwd(p, tgt.to(DEV))
+    dp = _capi.cross_entropy_bwd(p, tgt.to(DEV))
+    dz = _capi.softmax_cross_entropy_bwd(p, tgt.to(DEV), temp)
+    torch.cuda.synchronize()
+    p64 = _as64(p, dtype)
+    valid = (tgt >= 0) & (tgt < v)
+    safe = tgt.clamp(0, v - 1).long()
+    ref_loss = torch.where(valid, -torch.log(p64.gather(1, safe[:, None])[:, 0]) / n, torch.zeros((), dtype=F64))
+    _close(loss, ref_loss, 1e-6, "loss")
+    onehot = F.one_hot(safe, v).to(F64) * valid[:, None]
+    ref_dp = torch.where(onehot > 0, -1.0 / (p64 * n), torch.zeros((), dtype=F64))
+    _close(dp, ref_dp, TOL[dtype], "dp")
+    # dz is the gradient of the mean cross-entropy of softmax(l / T) with respect to logits l
+    # whose softmax is the p the kernel saw: l = T log p (invalid rows contribute nothing).
+    logits = (temp * torch.log(p64)).requires_grad_(True)
+    lp = torch.log_softmax(logits / temp, -1)
+    (-(lp.gather(1, safe[:, None])[:, 0] * valid).sum() / n).backward()
+    _close(dz, logits.grad, TOL[dtype] * 2, "dz")
+    assert float(dz[5].abs().max()) == 0.0 and float(dz[77].abs().max()) == 0.0
+
+
+# ---- Adam / AdamW --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("decoupled", [False, True])
+def test_adam_matches_torch(decoupled):
+    n, lr, wd = 5000, 1e-2, 0.05
+    p0 = _randn((n,), 70)
+    grads = [_randn((n,), 71 + s) for s in range(4)]
+    p = _dev(p0, torch.float32)
+    m = torch.zeros(n, device=DEV)
+    v = torch.zeros(n, device=DEV)
+    ref = p0.float().double().clone().requires_grad_(True)
+    opt_cls = torch.optim.AdamW if decoupled else torch.optim.Adam
+    opt = opt_cls([ref], lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
+    for step, g in enumerate(grads, start=1):
+        _capi.adam_update(p, _dev(g, torch.float32), m, v, step, lr=lr, weight_decay=wd, decoupled=decoupled)
+        ref.grad = g.float().double()
+        opt.step()
+    torch.cuda.synchronize()
+    assert float((p.double().cpu() - ref.detach()).abs().max()) <= 2e-6
+
+
+def test_adam_rejects_step_zero():
+    t = torch.zeros(4, device=DEV)
+    with pytest.raises(RuntimeError, match="step >= 1"):
+        _capi.adam_update(t, t, t.clone(), t.clone(), 0)
