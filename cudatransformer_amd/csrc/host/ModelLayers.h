@@ -1,0 +1,569 @@
+// The layers a NanoGPT training step stacks around AttentionLayer, with the reference's
+// Layer<DType> interface and semantics, computing in libctattn.so:
+//   LinearLayer            LinearLayer.cu:13-223 (y = x W^T + b, W [out][in])
+//   LayerNormLayer         LayerNorm.cu:13-165 (gamma = 1, beta = 0, eps 1e-5)
+//   ActivationLayer        ActivationLayer.cu:13-151 (ReLU, GELU tanh form, Sigmoid, Tanh)
+//   MLPLayer               MLPLayer.cu:13-172 (a sequence of layers)
+//   TransformerBlockLayer  TransformerBlockLayer.cu:13-220 (LayerNorm -> Attention ->
+//                          LayerNorm -> MLP, no residual connections, as the reference has it)
+//   TransformerLayer       TransformerLayer.cu:13-249 (a stack of blocks)
+//   AdamOptimizer          AdamOptimizer.cu:21-140 (over parameter / gradient maps)
+//   AdamWOptimizer         AdamOptimizer.cu:142-233
+// Same conventions as the reference: weights start at zero (cudaMakeShared zero-fills,
+// LinearLayer.cu:28), LayerNorm at (1, 0); gradients accumulate across backward calls until
+// zeroGrad; backward(input, gradOutput) recomputes the forward activations it needs from
+// `input` (TransformerBlockLayer.cu backward).  Differences: gradient buffers are allocated on
+// the first backward; setParameters copies into the layer's buffers (the attention layer's
+// setters adopt the buffer, as the reference's do); Adam advances its step once per step
+// (the reference advances it twice, AdamOptimizer.cu:75,95).
+#pragma once
+
+#include <cmath>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "AttentionLayer.h"
+#include "ModuleLayer.h"
+#include "ProjectionLayers.h"
+#include "Tensor.h"
+
+namespace ct {
+
+// The reference's ActivationType (ActivationLayer.cu).
+enum class ActivationType { ReLU = CTATTN_ACT_RELU, GELU = CTATTN_ACT_GELU, Sigmoid = CTATTN_ACT_SIGMOID, Tanh = CTATTN_ACT_TANH };
+
+namespace detail {
+
+template <typename DType>
+inline std::shared_ptr<DType[]> filled(size_t n, float value) {
+    return Tensor<DType>(std::vector<size_t>{n}, value).dataPtr();
+}
+
+template <typename DType>
+inline void copyInto(const std::shared_ptr<DType[]> &dst, const Tensor<DType> &src, size_t n, const std::string &what) {
+    if (src.size() != n)
+        throw std::invalid_argument(what + ": expected " + std::to_string(n) + " elements, got " +
+                                    std::to_string(src.size()));
+    if (n > 0)
+        hipCheck(hipMemcpyAsync(dst.get(), src.get(), n * sizeof(DType), hipMemcpyDeviceToDevice, Runtime::stream()),
+                 "hipMemcpyAsync D2D");
+}
+
+template <typename DType>
+inline std::shared_ptr<DType[]> cloneBuffer(const std::shared_ptr<DType[]> &src, size_t n) {
+    auto dst = deviceAlloc<DType>(n);
+    if (n > 0)
+        hipCheck(hipMemcpyAsync(dst.get(), src.get(), n * sizeof(DType), hipMemcpyDeviceToDevice, Runtime::stream()),
+                 "hipMemcpyAsync D2D");
+    return dst;
+}
+
+template <typename DType>
+inline void zeroBuffer(const std::shared_ptr<DType[]> &g, size_t n) {
+    if (g != nullptr && n > 0)
+        hipCheck(hipMemsetAsync(g.get(), 0, n * sizeof(DType), Runtime::stream()), "hipMemsetAsync");
+}
+
+template <typename DType>
+inline void sgdStep(const std::shared_ptr<DType[]> &p, const std::shared_ptr<DType[]> &g, float lr, size_t n) {
+    if (g == nullptr) return;
+    ctattnCheck(ctattn_sgd_update(DTypeCode<DType>::value, p.get(), g.get(), lr, int64_t(n), Runtime::stream()),
+                "ctattn_sgd_update");
+}
+
+// Rows of an activation [..., dim] (its element count over the last dimension).
+template <typename DType>
+inline size_t rowsOf(const Tensor<DType> &t, size_t dim, const char *what) {
+    if (t.nDim() < 1 || t.shape(t.nDim() - 1) != dim)
+        throw std::invalid_argument(std::string(what) + ": last dimension must be " + std::to_string(dim));
+    return t.size() / dim;
+}
+
+inline std::string prefixed(const std::string &prefix, const std::string &name) { return prefix + "." + name; }
+
+// Splits a prefixed map: entries "prefix.rest" -> "rest".
+template <typename DType>
+inline std::map<std::string, Tensor<DType>> sub(const std::map<std::string, Tensor<DType>> &m, const std::string &prefix) {
+    std::map<std::string, Tensor<DType>> out;
+    const std::string p = prefix + ".";
+    for (const auto &[k, v] : m)
+        if (k.compare(0, p.size(), p) == 0) out[k.substr(p.size())] = v;
+    return out;
+}
+
+template <typename DType>
+inline void merge(std::map<std::string, Tensor<DType>> &into, const std::string &prefix,
+                  const std::map<std::string, Tensor<DType>> &from) {
+    for (const auto &[k, v] : from) into[prefixed(prefix, k)] = v;
+}
+
+}  // namespace detail
+
+template <typename DType = float>
+struct LinearLayer : public Layer<DType> {
+    int inputDim = 1;
+    int outputDim = 1;
+    bool useBias = true;
+    std::shared_ptr<DType[]> weights, biases, weightsGrad, biasesGrad;
+
+    LinearLayer(int inputDim, int outputDim, bool useBias = true)
+        : inputDim(inputDim), outputDim(outputDim), useBias(useBias) {
+        if (inputDim < 1 || outputDim < 1) throw std::invalid_argument("LinearLayer: dimensions must be >= 1");
+        weights = detail::zeros<DType>(weightSize());
+        if (useBias) biases = detail::zeros<DType>(size_t(outputDim));
+    }
+
+    size_t weightSize() const { return size_t(inputDim) * outputDim; }
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        auto c = std::make_shared<LinearLayer<DType>>(inputDim, outputDim, useBias);
+        c->weights = detail::cloneBuffer(weights, weightSize());
+        if (useBias) c->biases = detail::cloneBuffer(biases, size_t(outputDim));
+        return c;
+    }
+
+    // [..., inputDim] -> [..., outputDim] (LinearLayer.cu forward).
+    Tensor<DType> forward(Tensor<DType> input) override {
+        const size_t rows = detail::rowsOf(input, size_t(inputDim), "LinearLayer input");
+        std::vector<size_t> shape = input.shape();
+        shape.back() = size_t(outputDim);
+        Tensor<DType> out = Tensor<DType>::empty(shape);
+        ctattnCheck(ctattn_linear_fwd(DTypeCode<DType>::value, input.get(), weights.get(),
+                                      useBias ? biases.get() : nullptr, out.get(), int64_t(rows), outputDim, inputDim,
+                                      Runtime::stream()),
+                    "ctattn_linear_fwd");
+        return out;
+    }
+
+    // Accumulates dW (and dB), returns dInput (LinearLayer.cu backward).
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
+        const size_t rows = detail::rowsOf(input, size_t(inputDim), "LinearLayer input");
+        if (detail::rowsOf(gradOutput, size_t(outputDim), "LinearLayer grad_output") != rows)
+            throw std::invalid_argument("LinearLayer: grad_output rows do not match the input");
+        ensureGrads();
+        Tensor<DType> inputGrad = Tensor<DType>::empty(input.shape());
+        const int dt = DTypeCode<DType>::value;
+        const int64_t wsBytes = ctattn_linear_bwd_workspace_bytes(dt, int64_t(rows), outputDim, inputDim);
+        auto ws = detail::workspace(wsBytes, "ctattn_linear_bwd_workspace_bytes");
+        ctattnCheck(ctattn_linear_bwd(dt, input.get(), weights.get(), gradOutput.get(), inputGrad.get(),
+                                      weightsGrad.get(), useBias ? biasesGrad.get() : nullptr, ws.get(), wsBytes,
+                                      int64_t(rows), outputDim, inputDim, Runtime::stream()),
+                    "ctattn_linear_bwd");
+        return inputGrad;
+    }
+
+    std::map<std::string, Tensor<DType>> getParameters() override {
+        std::map<std::string, Tensor<DType>> m{{"weights", Tensor<DType>(weights, weightShape())}};
+        if (useBias) m["biases"] = Tensor<DType>(biases, {size_t(outputDim)});
+        return m;
+    }
+    void setParameters(const std::map<std::string, Tensor<DType>> &p) override {
+        if (p.count("weights")) detail::copyInto(weights, p.at("weights"), weightSize(), "LinearLayer weights");
+        if (useBias && p.count("biases")) detail::copyInto(biases, p.at("biases"), size_t(outputDim), "LinearLayer biases");
+    }
+    std::map<std::string, Tensor<DType>> getGradients() override {
+        ensureGrads();
+        std::map<std::string, Tensor<DType>> m{{"weights", Tensor<DType>(weightsGrad, weightShape())}};
+        if (useBias) m["biases"] = Tensor<DType>(biasesGrad, {size_t(outputDim)});
+        return m;
+    }
+    void zeroGrad() override {
+        detail::zeroBuffer(weightsGrad, weightSize());
+        detail::zeroBuffer(biasesGrad, size_t(outputDim));
+    }
+    void sgdUpdate(float lr) override {
+        detail::sgdStep(weights, weightsGrad, lr, weightSize());
+        if (useBias) detail::sgdStep(biases, biasesGrad, lr, size_t(outputDim));
+    }
+
+    // Shallow accessors (LinearLayer.cu:140-223): getters share the buffer, setters adopt it.
+    Tensor<DType> getWeights() { return Tensor<DType>(weights, weightShape()); }
+    void setWeights(const Tensor<DType> &t) { weights = adopt(t, weightSize(), "weights"); }
+    Tensor<DType> getBiases() { return useBias ? Tensor<DType>(biases, {size_t(outputDim)}) : Tensor<DType>(); }
+    void setBiases(const Tensor<DType> &t) { biases = adopt(t, useBias ? size_t(outputDim) : 0, "biases"); }
+    Tensor<DType> getWeightGrad() {
+        ensureGrads();
+        return Tensor<DType>(weightsGrad, weightShape());
+    }
+    void setWeightGrad(const Tensor<DType> &t) { weightsGrad = adopt(t, weightSize(), "weight gradient"); }
+    Tensor<DType> getBiasGrad() {
+        ensureGrads();
+        return useBias ? Tensor<DType>(biasesGrad, {size_t(outputDim)}) : Tensor<DType>();
+    }
+    void setBiasGrad(const Tensor<DType> &t) { biasesGrad = adopt(t, useBias ? size_t(outputDim) : 0, "bias gradient"); }
+
+private:
+    static std::shared_ptr<DType[]> adopt(const Tensor<DType> &t, size_t n, const char *what) {
+        if (n == 0) throw std::invalid_argument(std::string("LinearLayer has no ") + what);
+        if (t.size() != n)
+            throw std::invalid_argument(std::string("LinearLayer ") + what + ": expected " + std::to_string(n) +
+                                        " elements, got " + std::to_string(t.size()));
+        return t.dataPtr();
+    }
+    std::vector<size_t> weightShape() const { return {size_t(outputDim), size_t(inputDim)}; }
+    void ensureGrads() {
+        if (weightsGrad == nullptr) weightsGrad = detail::zeros<DType>(weightSize());
+        if (useBias && biasesGrad == nullptr) biasesGrad = detail::zeros<DType>(size_t(outputDim));
+    }
+};
+
+template <typename DType = float>
+struct LayerNormLayer : public Layer<DType> {
+    int inputDim = 1;
+    float epsilon = 1e-5f;
+    std::shared_ptr<DType[]> weights, biases, weightsGrad, biasesGrad;
+
+    LayerNormLayer(int inputDim, float epsilon = 1e-5f) : inputDim(inputDim), epsilon(epsilon) {
+        if (inputDim < 1) throw std::invalid_argument("LayerNormLayer: inputDim must be >= 1");
+        weights = detail::filled<DType>(size_t(inputDim), 1.f);
+        biases = detail::zeros<DType>(size_t(inputDim));
+    }
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        auto c = std::make_shared<LayerNormLayer<DType>>(inputDim, epsilon);
+        c->weights = detail::cloneBuffer(weights, size_t(inputDim));
+        c->biases = detail::cloneBuffer(biases, size_t(inputDim));
+        return c;
+    }
+
+    Tensor<DType> forward(Tensor<DType> input) override { return run(input).first; }
+
+    // Recomputes the row statistics of `input` (the reference reuses the last forward's,
+    // LayerNorm.cu:143), then dX and the accumulated dGamma / dBeta.
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
+        const size_t rows = detail::rowsOf(input, size_t(inputDim), "LayerNormLayer input");
+        if (gradOutput.size() != input.size()) throw std::invalid_argument("LayerNormLayer: grad_output shape");
+        auto stats = run(input).second;
+        ensureGrads();
+        Tensor<DType> inputGrad = Tensor<DType>::empty(input.shape());
+        const int dt = DTypeCode<DType>::value;
+        const int64_t wsBytes = ctattn_layernorm_bwd_workspace_bytes(dt, int64_t(rows), inputDim);
+        auto ws = detail::workspace(wsBytes, "ctattn_layernorm_bwd_workspace_bytes");
+        ctattnCheck(ctattn_layernorm_bwd(dt, input.get(), weights.get(), gradOutput.get(), stats.get(),
+                                         stats.get() + rows, inputGrad.get(), weightsGrad.get(), biasesGrad.get(),
+                                         ws.get(), wsBytes, int64_t(rows), inputDim, Runtime::stream()),
+                    "ctattn_layernorm_bwd");
+        return inputGrad;
+    }
+
+    std::map<std::string, Tensor<DType>> getParameters() override {
+        return {{"weights", Tensor<DType>(weights, {size_t(inputDim)})}, {"biases", Tensor<DType>(biases, {size_t(inputDim)})}};
+    }
+    void setParameters(const std::map<std::string, Tensor<DType>> &p) override {
+        if (p.count("weights")) detail::copyInto(weights, p.at("weights"), size_t(inputDim), "LayerNorm weights");
+        if (p.count("biases")) detail::copyInto(biases, p.at("biases"), size_t(inputDim), "LayerNorm biases");
+    }
+    std::map<std::string, Tensor<DType>> getGradients() override {
+        ensureGrads();
+        return {{"weights", Tensor<DType>(weightsGrad, {size_t(inputDim)})},
+                {"biases", Tensor<DType>(biasesGrad, {size_t(inputDim)})}};
+    }
+    void zeroGrad() override {
+        detail::zeroBuffer(weightsGrad, size_t(inputDim));
+        detail::zeroBuffer(biasesGrad, size_t(inputDim));
+    }
+    void sgdUpdate(float lr) override {
+        detail::sgdStep(weights, weightsGrad, lr, size_t(inputDim));
+        detail::sgdStep(biases, biasesGrad, lr, size_t(inputDim));
+    }
+
+private:
+    // Output and the fp32 row statistics [mean (rows) | rstd (rows)].
+    std::pair<Tensor<DType>, std::shared_ptr<float[]>> run(const Tensor<DType> &input) {
+        const size_t rows = detail::rowsOf(input, size_t(inputDim), "LayerNormLayer input");
+        Tensor<DType> out = Tensor<DType>::empty(input.shape());
+        auto stats = deviceAlloc<float>(2 * rows);
+        ctattnCheck(ctattn_layernorm_fwd(DTypeCode<DType>::value, input.get(), weights.get(), biases.get(), out.get(),
+                                         stats.get(), stats.get() + rows, int64_t(rows), inputDim, epsilon,
+                                         Runtime::stream()),
+                    "ctattn_layernorm_fwd");
+        return {out, stats};
+    }
+    void ensureGrads() {
+        if (weightsGrad == nullptr) weightsGrad = detail::zeros<DType>(size_t(inputDim));
+        if (biasesGrad == nullptr) biasesGrad = detail::zeros<DType>(size_t(inputDim));
+    }
+};
+
+template <typename DType = float>
+struct ActivationLayer : public Layer<DType> {
+    int inputDim = 1;
+    ActivationType activationType = ActivationType::ReLU;
+
+    ActivationLayer(int inputDim, ActivationType type) : inputDim(inputDim), activationType(type) {}
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        return std::make_shared<ActivationLayer<DType>>(inputDim, activationType);
+    }
+    Tensor<DType> forward(Tensor<DType> input) override {
+        Tensor<DType> out = Tensor<DType>::empty(input.shape());
+        ctattnCheck(ctattn_activation_fwd(DTypeCode<DType>::value, int(activationType), input.get(), out.get(),
+                                          int64_t(input.size()), Runtime::stream()),
+                    "ctattn_activation_fwd");
+        return out;
+    }
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
+        if (gradOutput.size() != input.size()) throw std::invalid_argument("ActivationLayer: grad_output shape");
+        Tensor<DType> inputGrad = Tensor<DType>::empty(input.shape());
+        ctattnCheck(ctattn_activation_bwd(DTypeCode<DType>::value, int(activationType), input.get(), gradOutput.get(),
+                                          inputGrad.get(), int64_t(input.size()), Runtime::stream()),
+                    "ctattn_activation_bwd");
+        return inputGrad;
+    }
+};
+
+// A sequence of layers; parameters are keyed "layer_<index>.<name>" (MLPLayer.cu:105-146).
+template <typename DType = float>
+struct MLPLayer : public Layer<DType> {
+    std::vector<Module<DType>> layers;
+
+    explicit MLPLayer(std::vector<Module<DType>> layers) : layers(std::move(layers)) {}
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        std::vector<Module<DType>> c;
+        for (auto &l : layers) c.push_back(l->clone());
+        return std::make_shared<MLPLayer<DType>>(c);
+    }
+    Tensor<DType> forward(Tensor<DType> input) override {
+        for (auto &l : layers) input = l->forward(input);
+        return input;
+    }
+    // Recomputes every layer's input, then backpropagates through them in reverse.
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
+        std::vector<Tensor<DType>> inputs{input};
+        for (size_t i = 0; i + 1 < layers.size(); ++i) inputs.push_back(layers[i]->forward(inputs.back()));
+        for (size_t i = layers.size(); i-- > 0;) gradOutput = layers[i]->backward(inputs[i], gradOutput);
+        return gradOutput;
+    }
+    std::map<std::string, Tensor<DType>> getParameters() override {
+        std::map<std::string, Tensor<DType>> m;
+        for (size_t i = 0; i < layers.size(); ++i) detail::merge(m, key(i), layers[i]->getParameters());
+        return m;
+    }
+    void setParameters(const std::map<std::string, Tensor<DType>> &p) override {
+        for (size_t i = 0; i < layers.size(); ++i) layers[i]->setParameters(detail::sub(p, key(i)));
+    }
+    std::map<std::string, Tensor<DType>> getGradients() override {
+        std::map<std::string, Tensor<DType>> m;
+        for (size_t i = 0; i < layers.size(); ++i) detail::merge(m, key(i), layers[i]->getGradients());
+        return m;
+    }
+    void zeroGrad() override {
+        for (auto &l : layers) l->zeroGrad();
+    }
+    void sgdUpdate(float lr) override {
+        for (auto &l : layers) l->sgdUpdate(lr);
+    }
+
+private:
+    static std::string key(size_t i) { return "layer_" + std::to_string(i); }
+};
+
+template <typename DType = float>
+struct TransformerBlockLayer : public Layer<DType> {
+    std::shared_ptr<LayerNormLayer<DType>> firstNorm;
+    std::shared_ptr<AttentionLayer<DType>> attention;
+    std::shared_ptr<LayerNormLayer<DType>> secondNorm;
+    std::shared_ptr<MLPLayer<DType>> mlp;
+    int inputDim = 1, numHeads = 1, headDim = 1, mlpDim = 1;
+    ActivationType activationType = ActivationType::ReLU;
+
+    TransformerBlockLayer(int inputDim, int numHeads, int headDim, int mlpDim,
+                          ActivationType activationType = ActivationType::ReLU, bool causal = false)
+        : inputDim(inputDim), numHeads(numHeads), headDim(headDim), mlpDim(mlpDim), activationType(activationType) {
+        firstNorm = std::make_shared<LayerNormLayer<DType>>(inputDim);
+        attention = std::make_shared<AttentionLayer<DType>>(inputDim, numHeads, headDim, causal);
+        secondNorm = std::make_shared<LayerNormLayer<DType>>(inputDim);
+        mlp = std::make_shared<MLPLayer<DType>>(std::vector<Module<DType>>{
+            std::make_shared<LinearLayer<DType>>(inputDim, mlpDim),
+            std::make_shared<ActivationLayer<DType>>(mlpDim, activationType),
+            std::make_shared<LinearLayer<DType>>(mlpDim, inputDim)});
+    }
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        auto c = std::make_shared<TransformerBlockLayer<DType>>(inputDim, numHeads, headDim, mlpDim, activationType,
+                                                                attention->causal());
+        c->firstNorm = std::static_pointer_cast<LayerNormLayer<DType>>(firstNorm->clone());
+        c->attention = std::static_pointer_cast<AttentionLayer<DType>>(attention->clone());
+        c->secondNorm = std::static_pointer_cast<LayerNormLayer<DType>>(secondNorm->clone());
+        c->mlp = std::static_pointer_cast<MLPLayer<DType>>(mlp->clone());
+        return c;
+    }
+
+    // LayerNorm -> Attention -> LayerNorm -> MLP (TransformerBlockLayer.cu:60-66).
+    Tensor<DType> forward(Tensor<DType> input) override {
+        return mlp->forward(secondNorm->forward(attention->forward(firstNorm->forward(input))));
+    }
+
+    // Recomputes the block's activations (attention with its cached states), then
+    // backpropagates (TransformerBlockLayer.cu:74-87).
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
+        Tensor<DType> normed = firstNorm->forward(input);
+        std::array<Tensor<DType>, 4> states;
+        Tensor<DType> attn = attention->forward(normed, states.data());
+        Tensor<DType> normed2 = secondNorm->forward(attn);
+        Tensor<DType> g = mlp->backward(normed2, gradOutput);
+        g = secondNorm->backward(attn, g);
+        g = attention->backward(normed, g, states.data());
+        return firstNorm->backward(input, g);
+    }
+
+    std::map<std::string, Tensor<DType>> getParameters() override { return collect(false); }
+    std::map<std::string, Tensor<DType>> getGradients() override { return collect(true); }
+    void setParameters(const std::map<std::string, Tensor<DType>> &p) override {
+        firstNorm->setParameters(detail::sub(p, "firstNorm"));
+        attention->setParameters(detail::sub(p, "attention"));
+        secondNorm->setParameters(detail::sub(p, "secondNorm"));
+        mlp->setParameters(detail::sub(p, "mlp"));
+    }
+    void zeroGrad() override {
+        firstNorm->zeroGrad();
+        attention->zeroGrad();
+        secondNorm->zeroGrad();
+        mlp->zeroGrad();
+    }
+    void sgdUpdate(float lr) override {
+        firstNorm->sgdUpdate(lr);
+        attention->sgdUpdate(lr);
+        secondNorm->sgdUpdate(lr);
+        mlp->sgdUpdate(lr);
+    }
+
+private:
+    std::map<std::string, Tensor<DType>> collect(bool grads) {
+        std::map<std::string, Tensor<DType>> m;
+        auto get = [grads](Layer<DType> &l) { return grads ? l.getGradients() : l.getParameters(); };
+        detail::merge(m, "firstNorm", get(*firstNorm));
+        detail::merge(m, "attention", get(*attention));
+        detail::merge(m, "secondNorm", get(*secondNorm));
+        detail::merge(m, "mlp", get(*mlp));
+        return m;
+    }
+};
+
+// A stack of numLayers blocks (TransformerLayer.cu:29-41).  Parameters are keyed
+// "layer_<slot>.<name>" where slot is the block's position in the reference's layer list,
+// which holds a CheckpointLayer before every checkpointGap-th block (checkpointGap > 0), so
+// the keys match the reference's for every checkpointGap.  backward recomputes each block's
+// input from `input` and backpropagates block by block; the gradients equal the reference's
+// for any checkpointGap (its checkpoints only change what it keeps in memory).
+template <typename DType = float>
+struct TransformerLayer : public Layer<DType> {
+    std::vector<std::shared_ptr<TransformerBlockLayer<DType>>> blocks;
+    int inputDim = 1, numHeads = 1, headDim = 1, mlpDim = 1, numLayers = 1, checkpointGap = 0;
+    ActivationType activationType = ActivationType::ReLU;
+
+    TransformerLayer(int inputDim, int numHeads, int headDim, int mlpDim, int numLayers, int checkpointGap = 0,
+                     ActivationType activationType = ActivationType::ReLU, bool causal = false)
+        : inputDim(inputDim), numHeads(numHeads), headDim(headDim), mlpDim(mlpDim), numLayers(numLayers),
+          checkpointGap(checkpointGap), activationType(activationType) {
+        if (numLayers < 1) throw std::invalid_argument("TransformerLayer: numLayers must be >= 1");
+        if (checkpointGap < 0) throw std::invalid_argument("TransformerLayer: checkpointGap must be >= 0");
+        for (int i = 0; i < numLayers; ++i)
+            blocks.push_back(std::make_shared<TransformerBlockLayer<DType>>(inputDim, numHeads, headDim, mlpDim,
+                                                                           activationType, causal));
+    }
+
+    bool causal() const { return blocks.front()->attention->causal(); }
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        auto c = std::make_shared<TransformerLayer<DType>>(*this);
+        for (auto &b : c->blocks) b = std::static_pointer_cast<TransformerBlockLayer<DType>>(b->clone());
+        return c;
+    }
+    Tensor<DType> forward(Tensor<DType> input) override {
+        for (auto &b : blocks) input = b->forward(input);
+        return input;
+    }
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
+        std::vector<Tensor<DType>> inputs{input};
+        for (size_t i = 0; i + 1 < blocks.size(); ++i) inputs.push_back(blocks[i]->forward(inputs.back()));
+        for (size_t i = blocks.size(); i-- > 0;) {
+            gradOutput = blocks[i]->backward(inputs[i], gradOutput);
+            inputs[i] = Tensor<DType>();
+        }
+        return gradOutput;
+    }
+    std::map<std::string, Tensor<DType>> getParameters() override {
+        std::map<std::string, Tensor<DType>> m;
+        for (size_t i = 0; i < blocks.size(); ++i) detail::merge(m, key(i), blocks[i]->getParameters());
+        return m;
+    }
+    void setParameters(const std::map<std::string, Tensor<DType>> &p) override {
+        for (size_t i = 0; i < blocks.size(); ++i) blocks[i]->setParameters(detail::sub(p, key(i)));
+    }
+    std::map<std::string, Tensor<DType>> getGradients() override {
+        std::map<std::string, Tensor<DType>> m;
+        for (size_t i = 0; i < blocks.size(); ++i) detail::merge(m, key(i), blocks[i]->getGradients());
+        return m;
+    }
+    void zeroGrad() override {
+        for (auto &b : blocks) b->zeroGrad();
+    }
+    void sgdUpdate(float lr) override {
+        for (auto &b : blocks) b->sgdUpdate(lr);
+    }
+
+private:
+    std::string key(size_t i) const {
+        const size_t slot = i + (checkpointGap > 0 ? i / size_t(checkpointGap) : 0);
+        return "layer_" + std::to_string(slot);
+    }
+};
+
+// Adam / AdamW over a parameter map (AdamOptimizer.cu:21-140 AdamOptimizer, :142-233
+// AdamWOptimizer): step(grads) updates every parameter, and throws if `grads` lacks one or
+// a size differs, as the reference does.  fp32 moments are zero at construction; the step
+// counter advances once per step (the reference advances it twice).  decoupled = false is
+// the reference's AdamOptimizer (decay folded into the gradient), true its AdamWOptimizer.
+struct AdamOptimizer {
+    std::map<std::string, Tensor<float>> parameters;
+    double learningRate, beta1, beta2, epsilon, decay;
+    bool decoupled = false;
+    int timeStep = 0;
+    std::map<std::string, std::pair<std::shared_ptr<float[]>, std::shared_ptr<float[]>>> moments;
+
+    explicit AdamOptimizer(std::map<std::string, Tensor<float>> params, double lr = 1e-3, double b1 = 0.9,
+                           double b2 = 0.999, double eps = 1e-8, double decay = 0.0, bool decoupled = false)
+        : parameters(std::move(params)), learningRate(lr), beta1(b1), beta2(b2), epsilon(eps), decay(decay),
+          decoupled(decoupled) {
+        for (const auto &[name, p] : parameters)
+            moments[name] = {detail::zeros<float>(p.size()), detail::zeros<float>(p.size())};
+    }
+
+    void step(const std::map<std::string, Tensor<float>> &grads) {
+        for (const auto &[name, p] : parameters) {
+            auto g = grads.find(name);
+            if (g == grads.end())
+                throw std::invalid_argument("Gradient for parameter '" + name + "' not found in gradients map.");
+            if (g->second.size() != p.size())
+                throw std::invalid_argument("Size mismatch between parameter '" + name + "' and its gradient.");
+        }
+        ++timeStep;
+        for (const auto &[name, p] : parameters) {
+            auto &mv = moments[name];
+            ctattnCheck(ctattn_adam_update(CTATTN_F32, p.get(), grads.at(name).get(), mv.first.get(), mv.second.get(),
+                                           int64_t(p.size()), float(learningRate), float(beta1), float(beta2),
+                                           float(epsilon), float(decay), timeStep, decoupled ? 1 : 0,
+                                           Runtime::stream()),
+                        "ctattn_adam_update");
+        }
+    }
+
+    double getLearningRate() const { return learningRate; }
+    void setLearningRate(double lr) { learningRate = lr; }
+    int getTimeStep() const { return timeStep; }
+    void setTimeStep(int t) { timeStep = t; }
+};
+
+// AdamW: the decoupled-decay variant (AdamOptimizer.cu:142-233).
+struct AdamWOptimizer : public AdamOptimizer {
+    explicit AdamWOptimizer(std::map<std::string, Tensor<float>> params, double lr = 1e-3, double b1 = 0.9,
+                            double b2 = 0.999, double eps = 1e-8, double decay = 0.0)
+        : AdamOptimizer(std::move(params), lr, b1, b2, eps, decay, true) {}
+};
+
+}  // namespace ct

@@ -9,8 +9,8 @@
 // host waits only when data comes back to the CPU (numpy(), item()) or after an upload from
 // pageable memory (fromPointer()).
 //
-// DType is float or bf16 (stored as its 16-bit pattern).  The reference's tensor algebra
-// (Tensor.cu:290-958) is not part of this path.
+// DType is float or bf16 (stored as its 16-bit pattern), or int32_t for token ids.  The
+// reference's tensor algebra (Tensor.cu:290-958) is not part of this path.
 #pragma once
 
 #include <cstdint>
@@ -55,8 +55,10 @@ template <> struct DTypeCode<bf16> { static constexpr int value = CTATTN_BF16; }
 template <typename DType> inline DType fromFloat(float x);
 template <> inline float fromFloat<float>(float x) { return x; }
 template <> inline bf16 fromFloat<bf16>(float x) { return bf16::fromFloat(x); }
+template <> inline int32_t fromFloat<int32_t>(float x) { return int32_t(x); }
 inline float toFloat(float x) { return x; }
 inline float toFloat(bf16 x) { return x.toFloat(); }
+inline float toFloat(int32_t x) { return float(x); }
 
 // Stream-ordered device allocation with a stream-ordered free as deleter.
 template <typename T>

@@ -16,13 +16,26 @@
 // FlashAttentionFloat / FlashAttentionBFloat.  Attention factories take an extra
 // causal=False.  bf16 tensors take and return float32 numpy arrays (numpy has no bfloat16;
 // values are rounded to nearest even on upload).
+//
+// Around attention, with the reference's names (cuda_transformer.cu:178-370, 384-410,
+// 495-787): <T>LayerNormLayer, <T>LinearLayer, <T>ActivationLayer, <T>MLPLayer,
+// <T>TransformerBlockLayer, <T>TransformerLayer and their factories (LayerNorm, Linear,
+// Activation, ReLU, GELU, Sigmoid, Tanh, MLP, TransformerBlock, Transformer; Float / BFloat
+// suffixes, float without one), <T>Softmax, <T>CrossEntropyLoss, IntTensor for ids, and in
+// fp32 FloatTokenEmbedding, FloatPositionEmbedding, FloatUnEmbedding, FloatNanoGPT,
+// FloatAdamOptimizer, FloatAdamWOptimizer; enums ActivationType and SamplingMode.  Id
+// arguments accept an IntTensor, a NumPy array or a list.
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <type_traits>
+
 #include "AttentionLayer.h"
 #include "FlashAttentionLayer.h"
+#include "ModelLayers.h"
 #include "ModuleLayer.h"
+#include "NanoGPT.h"
 #include "Tensor.h"
 
 namespace py = pybind11;
@@ -30,20 +43,53 @@ using namespace ct;
 
 namespace {
 
+// NumPy element type of a tensor: int32 for ids, float32 for the float and bf16 tensors.
 template <typename DType>
-Tensor<DType> tensorFromNumpy(const py::array_t<float, py::array::c_style | py::array::forcecast> &arr) {
+using NpType = std::conditional_t<std::is_same_v<DType, int32_t>, int32_t, float>;
+using IdArray = py::array_t<int32_t, py::array::c_style | py::array::forcecast>;
+
+template <typename DType>
+Tensor<DType> tensorFromNumpy(const py::array_t<NpType<DType>, py::array::c_style | py::array::forcecast> &arr) {
     std::vector<size_t> shape(arr.shape(), arr.shape() + arr.ndim());
     if (shape.size() > 8) throw std::invalid_argument("Tensor dimension exceeds 8");
-    return Tensor<DType>::fromFloats(shape, arr.data());
+    if constexpr (std::is_same_v<DType, int32_t>)
+        return Tensor<int32_t>::fromPointer(shape, arr.data());
+    else
+        return Tensor<DType>::fromFloats(shape, arr.data());
 }
 
 template <typename DType>
-py::array_t<float> tensorToNumpy(const Tensor<DType> &t) {
-    std::vector<float> host = t.toFloats();
+py::array_t<NpType<DType>> tensorToNumpy(const Tensor<DType> &t) {
     std::vector<py::ssize_t> shape(t.shape().begin(), t.shape().end());
-    py::array_t<float> out(shape);
-    if (!host.empty()) std::memcpy(out.mutable_data(), host.data(), host.size() * sizeof(float));
+    py::array_t<NpType<DType>> out(shape);
+    if constexpr (std::is_same_v<DType, int32_t>) {
+        if (t.size() > 0) {
+            hipCheck(hipMemcpyAsync(out.mutable_data(), t.get(), t.size() * sizeof(int32_t), hipMemcpyDeviceToHost,
+                                    Runtime::stream()),
+                     "hipMemcpyAsync D2H");
+            Runtime::synchronize();
+        }
+    } else {
+        std::vector<float> host = t.toFloats();
+        if (!host.empty()) std::memcpy(out.mutable_data(), host.data(), host.size() * sizeof(float));
+    }
     return out;
+}
+
+// An id argument given as an IntTensor, a NumPy array or a list.
+Tensor<int32_t> idsFrom(const py::object &o) {
+    if (py::isinstance<Tensor<int32_t>>(o)) return o.cast<Tensor<int32_t>>();
+    return tensorFromNumpy<int32_t>(o.cast<IdArray>());
+}
+
+std::vector<int32_t> idVector(const py::object &o) {
+    if (py::isinstance<Tensor<int32_t>>(o)) {
+        const Tensor<int32_t> t = o.cast<Tensor<int32_t>>();
+        std::vector<float> f = t.toFloats();
+        return std::vector<int32_t>(f.begin(), f.end());
+    }
+    IdArray a = o.cast<IdArray>();
+    return std::vector<int32_t>(a.data(), a.data() + a.size());
 }
 
 template <typename DType>
@@ -55,8 +101,9 @@ void declareTensor(py::module_ &m, const std::string &suffix) {
         .def(py::init([](const std::vector<size_t> &shape) { return Tensor<DType>(shape); }), py::arg("shape"),
              "Constructs a zero-initialised tensor with the given shape on the GPU.")
         .def_static("fromNumpy", &tensorFromNumpy<DType>, py::arg("array"),
-                    "Copies a NumPy array (cast to float32, C order) to a new GPU tensor.")
-        .def("numpy", &tensorToNumpy<DType>, "Copies the tensor to the CPU and returns it as a float32 NumPy array.")
+                    "Copies a NumPy array (cast to the tensor's NumPy type, C order) to a new GPU tensor.")
+        .def("numpy", &tensorToNumpy<DType>,
+             "Copies the tensor to the CPU and returns it as a NumPy array (float32; int32 for IntTensor).")
         .def("shape", [](const Tensor<DType> &t) { return t.shape(); }, "Returns the tensor shape as a list of ints.")
         .def("size", &Tensor<DType>::size, "Number of elements.")
         .def("clone", &Tensor<DType>::clone, "Returns a deep copy with its own GPU buffer.")
@@ -180,6 +227,240 @@ void declareAttention(py::module_ &m, const std::string &suffix) {
           "Creates a multi-head AttentionLayer (QKV projection + flash attention + output projection).");
 }
 
+// The layers around attention (cuda_transformer.cu:178-370 and the factories :411-444).
+template <typename DType>
+void declareLayers(py::module_ &m, const std::string &suffix) {
+    using L = Layer<DType>;
+    using LN = LayerNormLayer<DType>;
+    using LIN = LinearLayer<DType>;
+    using ACT = ActivationLayer<DType>;
+    using MLP = MLPLayer<DType>;
+    using TB = TransformerBlockLayer<DType>;
+    using TR = TransformerLayer<DType>;
+
+    py::class_<LN, L, std::shared_ptr<LN>>(m, (suffix + "LayerNormLayer").c_str(),
+                                           "Layer normalisation over the last dimension with learnable scale "
+                                           "(weights, initially 1) and shift (biases, initially 0).")
+        .def(py::init<int, float>(), py::arg("input_dim"), py::arg("epsilon") = 1e-5f)
+        .def_readonly("inputDim", &LN::inputDim)
+        .def_readonly("epsilon", &LN::epsilon);
+    py::class_<ACT, L, std::shared_ptr<ACT>>(m, (suffix + "ActivationLayer").c_str(),
+                                             "Elementwise ReLU / GELU (tanh form) / Sigmoid / Tanh.")
+        .def(py::init<int, ActivationType>(), py::arg("input_dim"), py::arg("activation_type"))
+        .def_readonly("activationType", &ACT::activationType);
+    py::class_<LIN, L, std::shared_ptr<LIN>>(m, (suffix + "LinearLayer").c_str(),
+                                             "Fully connected layer y = x W^T + b, W [output_dim, input_dim]; "
+                                             "get/set methods are shallow (shared GPU buffer).")
+        .def(py::init<int, int, bool>(), py::arg("input_dim"), py::arg("output_dim"), py::arg("use_bias") = true)
+        .def_readonly("inputDim", &LIN::inputDim)
+        .def_readonly("outputDim", &LIN::outputDim)
+        .def("getWeights", &LIN::getWeights)
+        .def("setWeights", &LIN::setWeights, py::arg("tensor"))
+        .def("getBiases", &LIN::getBiases)
+        .def("setBiases", &LIN::setBiases, py::arg("tensor"))
+        .def("getWeightGrad", &LIN::getWeightGrad)
+        .def("setWeightGrad", &LIN::setWeightGrad, py::arg("tensor"))
+        .def("getBiasGrad", &LIN::getBiasGrad)
+        .def("setBiasGrad", &LIN::setBiasGrad, py::arg("tensor"));
+    py::class_<MLP, L, std::shared_ptr<MLP>>(m, (suffix + "MLPLayer").c_str(),
+                                             "Sequential container; parameters keyed 'layer_<i>.<name>'.")
+        .def(py::init<std::vector<Module<DType>>>(), py::arg("layers"))
+        .def_readonly("layers", &MLP::layers);
+    py::class_<TB, L, std::shared_ptr<TB>>(m, (suffix + "TransformerBlockLayer").c_str(),
+                                           "LayerNorm -> Attention -> LayerNorm -> MLP (Linear, Activation, "
+                                           "Linear), without residual connections.")
+        .def(py::init<int, int, int, int, ActivationType, bool>(), py::arg("input_dim"), py::arg("num_heads"),
+             py::arg("head_dim"), py::arg("mlp_dim"), py::arg("activation_type") = ActivationType::ReLU,
+             py::arg("causal") = false)
+        .def_readonly("firstNorm", &TB::firstNorm)
+        .def_readonly("attention", &TB::attention)
+        .def_readonly("secondNorm", &TB::secondNorm)
+        .def_readonly("mlp", &TB::mlp);
+    py::class_<TR, L, std::shared_ptr<TR>>(m, (suffix + "TransformerLayer").c_str(),
+                                           "A stack of transformer blocks; parameters keyed 'layer_<i>.<name>'.")
+        .def(py::init<int, int, int, int, int, int, ActivationType, bool>(), py::arg("input_dim"),
+             py::arg("num_heads"), py::arg("head_dim"), py::arg("mlp_dim"), py::arg("num_layers"),
+             py::arg("checkpoint_gap") = 0, py::arg("activation_type") = ActivationType::ReLU,
+             py::arg("causal") = false)
+        .def_readonly("blocks", &TR::blocks)
+        .def_readonly("numLayers", &TR::numLayers)
+        .def_readonly("checkpointGap", &TR::checkpointGap);
+
+}
+
+// Factories LayerNorm<suffix>, Linear<suffix>, … (cuda_transformer.cu:411-444; the
+// un-suffixed float names, :811-836, come from suffix "").
+template <typename DType>
+void declareFactories(py::module_ &m, const std::string &suffix) {
+    using LN = LayerNormLayer<DType>;
+    using LIN = LinearLayer<DType>;
+    using ACT = ActivationLayer<DType>;
+    using MLP = MLPLayer<DType>;
+    using TB = TransformerBlockLayer<DType>;
+    using TR = TransformerLayer<DType>;
+    auto def = [&](const std::string &name, auto fn, auto... args) { m.def((name + suffix).c_str(), fn, args...); };
+    def("LayerNorm", [](int d, float eps) { return std::make_shared<LN>(d, eps); }, py::arg("input_dim"),
+        py::arg("epsilon") = 1e-5f);
+    def("Linear", [](int i, int o, bool b) { return std::make_shared<LIN>(i, o, b); }, py::arg("input_dim"),
+        py::arg("output_dim"), py::arg("use_bias") = true);
+    def("Activation", [](int d, ActivationType t) { return std::make_shared<ACT>(d, t); }, py::arg("input_dim"),
+        py::arg("activation_type"));
+    def("ReLU", [](int d) { return std::make_shared<ACT>(d, ActivationType::ReLU); }, py::arg("input_dim"));
+    def("GELU", [](int d) { return std::make_shared<ACT>(d, ActivationType::GELU); }, py::arg("input_dim"));
+    def("Sigmoid", [](int d) { return std::make_shared<ACT>(d, ActivationType::Sigmoid); }, py::arg("input_dim"));
+    def("Tanh", [](int d) { return std::make_shared<ACT>(d, ActivationType::Tanh); }, py::arg("input_dim"));
+    def("MLP", [](std::vector<Module<DType>> layers) { return std::make_shared<MLP>(layers); }, py::arg("layers"));
+    def("TransformerBlock",
+        [](int e, int h, int d, int mlp, ActivationType a, bool c) { return std::make_shared<TB>(e, h, d, mlp, a, c); },
+        py::arg("input_dim"), py::arg("num_heads"), py::arg("head_dim"), py::arg("mlp_dim"),
+        py::arg("activation_type") = ActivationType::ReLU, py::arg("causal") = false);
+    def("Transformer",
+        [](int e, int h, int d, int mlp, int n, int gap, ActivationType a, bool c) {
+            return std::make_shared<TR>(e, h, d, mlp, n, gap, a, c);
+        },
+        py::arg("input_dim"), py::arg("num_heads"), py::arg("head_dim"), py::arg("mlp_dim"), py::arg("num_layers"),
+        py::arg("checkpoint_gap") = 0, py::arg("activation_type") = ActivationType::ReLU, py::arg("causal") = false);
+}
+
+// Softmax and cross-entropy (cuda_transformer.cu:579-633).
+template <typename DType>
+void declareLosses(py::module_ &m, const std::string &suffix) {
+    using T = Tensor<DType>;
+    py::class_<Softmax<DType>>(m, (suffix + "Softmax").c_str(), "Softmax over the last dimension with temperature.")
+        .def(py::init<double>(), py::arg("temperature") = 1.0)
+        .def_readwrite("temperature", &Softmax<DType>::temperature)
+        .def("forward", &Softmax<DType>::forward, py::arg("input"))
+        .def("__call__", &Softmax<DType>::forward, py::arg("input"))
+        .def("backward", &Softmax<DType>::backward, py::arg("input"), py::arg("grad_output"),
+             "Gradient with respect to the softmax input, given that input.");
+    py::class_<CrossEntropyLoss<DType>>(m, (suffix + "CrossEntropyLoss").c_str(),
+                                        "-log p[target] / N per row, on probabilities (fp32 loss tensor).")
+        .def(py::init<>())
+        .def("forward", [](const CrossEntropyLoss<DType> &l, const T &p, py::object t) { return l.forward(p, idsFrom(t)); },
+             py::arg("input"), py::arg("target"))
+        .def("__call__", [](const CrossEntropyLoss<DType> &l, const T &p, py::object t) { return l.forward(p, idsFrom(t)); },
+             py::arg("input"), py::arg("target"))
+        .def("backward", [](const CrossEntropyLoss<DType> &l, const T &p, py::object t) { return l.backward(p, idsFrom(t)); },
+             py::arg("input"), py::arg("target"));
+}
+
+// Embeddings, NanoGPT and the Adam optimizers (cuda_transformer.cu:384-410, 495-578, 634-787),
+// fp32 (their gradients accumulate in fp32).
+void declareNanoGPT(py::module_ &m) {
+    using T = Tensor<float>;
+    using G = NanoGPT<float>;
+    py::class_<TokenEmbedding<float>>(m, "FloatTokenEmbedding", "Token id -> embedding row lookup.")
+        .def(py::init<int, int>(), py::arg("vocab_size"), py::arg("embedding_dim"))
+        .def("forward", [](const TokenEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+             py::arg("input"))
+        .def("__call__", [](const TokenEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+             py::arg("input"))
+        .def("backward", [](TokenEmbedding<float> &e, py::object ids, const T &g) { e.backward(idsFrom(ids), g); },
+             py::arg("input"), py::arg("grad_output"))
+        .def("getParameters", &TokenEmbedding<float>::getParameters)
+        .def("setParameters", &TokenEmbedding<float>::setParameters, py::arg("tensor"))
+        .def("getGradients", &TokenEmbedding<float>::getGradients)
+        .def("zeroGrad", &TokenEmbedding<float>::zeroGrad)
+        .def("sgdUpdate", &TokenEmbedding<float>::sgdUpdate, py::arg("lr"))
+        .def("clone", &TokenEmbedding<float>::clone);
+    py::class_<PositionEmbedding<float>>(m, "FloatPositionEmbedding", "Learned position embedding [max_seq_len, E].")
+        .def(py::init<int, int>(), py::arg("max_seq_len"), py::arg("embedding_dim"))
+        .def("forward", [](const PositionEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+             py::arg("input"))
+        .def("__call__", [](const PositionEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+             py::arg("input"))
+        .def("backward", [](PositionEmbedding<float> &e, py::object ids, const T &g) { e.backward(idsFrom(ids), g); },
+             py::arg("input"), py::arg("grad_output"))
+        .def("getParameters", &PositionEmbedding<float>::getParameters)
+        .def("setParameters", &PositionEmbedding<float>::setParameters, py::arg("tensor"))
+        .def("getGradients", &PositionEmbedding<float>::getGradients)
+        .def("zeroGrad", &PositionEmbedding<float>::zeroGrad)
+        .def("sgdUpdate", &PositionEmbedding<float>::sgdUpdate, py::arg("lr"))
+        .def("clone", &PositionEmbedding<float>::clone);
+    py::class_<UnEmbedding<float>>(m, "FloatUnEmbedding", "Bias-free projection [..., E] -> [..., vocab].")
+        .def(py::init<int, int>(), py::arg("vocab_size"), py::arg("embedding_dim"))
+        .def("forward", &UnEmbedding<float>::forward, py::arg("input"))
+        .def("__call__", &UnEmbedding<float>::forward, py::arg("input"))
+        .def("backward", &UnEmbedding<float>::backward, py::arg("input"), py::arg("grad_output"))
+        .def("getParameters", &UnEmbedding<float>::getParameters)
+        .def("setParameters", &UnEmbedding<float>::setParameters, py::arg("tensor"))
+        .def("getGradients", &UnEmbedding<float>::getGradients)
+        .def("zeroGrad", &UnEmbedding<float>::zeroGrad)
+        .def("sgdUpdate", &UnEmbedding<float>::sgdUpdate, py::arg("lr"))
+        .def("clone", &UnEmbedding<float>::clone);
+
+    auto generate = [](G &g, py::object input, int n, SamplingMode mode, int K, double P) -> py::object {
+        std::vector<int32_t> out = g.generate(idVector(input), n, mode, K, P);
+        if (py::isinstance<Tensor<int32_t>>(input)) return py::cast(Tensor<int32_t>::fromPointer({out.size()}, out.data()));
+        if (py::isinstance<py::list>(input)) return py::cast(out);
+        IdArray a(py::ssize_t(out.size()));
+        std::copy(out.begin(), out.end(), a.mutable_data());
+        return std::move(a);
+    };
+    py::class_<G>(m, "FloatNanoGPT",
+                  "GPT language model: token + position embedding -> Transformer -> un-embedding -> softmax.\n"
+                  "forward returns probabilities [..., T, vocab]; backward(input, probs, target) accumulates the\n"
+                  "gradients of the mean cross-entropy.  Weights start at zero (set them with setParameters).")
+        .def(py::init<int, int, int, int, int, int, int, int, double, ActivationType, bool>(), py::arg("vocab_size"),
+             py::arg("max_seq_len"), py::arg("embedding_dim"), py::arg("num_heads"), py::arg("head_dim"),
+             py::arg("mlp_dim"), py::arg("num_layers"), py::arg("checkpoint_gap") = 0, py::arg("temperature") = 1.0,
+             py::arg("activation_type") = ActivationType::ReLU, py::arg("causal") = false)
+        .def("vocabSize", &G::vocabSize)
+        .def("maxSeqLen", &G::maxSeqLen)
+        .def("embeddingDim", &G::embeddingDim)
+        .def("numHeads", &G::numHeads)
+        .def("headDim", &G::headDim)
+        .def("mlpDim", &G::mlpDim)
+        .def("numLayers", &G::numLayers)
+        .def("checkpointGap", &G::checkpointGap)
+        .def("activationType", &G::activationType)
+        .def("causal", &G::causal)
+        .def("getTemperature", &G::getTemperature)
+        .def("setTemperature", &G::setTemperature, py::arg("temperature"))
+        .def("forward", [](G &g, py::object ids) { return g.forward(idsFrom(ids)); }, py::arg("input"),
+             "Token ids [..., T] (IntTensor, NumPy array or list) -> probabilities [..., T, vocab].")
+        .def("__call__", [](G &g, py::object ids) { return g.forward(idsFrom(ids)); }, py::arg("input"))
+        .def("loss", [](const G &g, const T &probs, py::object target) { return g.loss(probs, idsFrom(target)); },
+             py::arg("logits"), py::arg("target"), "Per-position cross-entropy -log p[target] / N (sums to the mean).")
+        .def("backward",
+             [](G &g, py::object input, const T &probs, py::object target) {
+                 g.backward(idsFrom(input), probs, idsFrom(target));
+             },
+             py::arg("input"), py::arg("logits"), py::arg("target"),
+             "Accumulates all parameter gradients; call with forward's input and output.")
+        .def("predict", &G::predict, py::arg("logits"), py::arg("mode"), py::arg("K") = 10, py::arg("P") = 0.1,
+             "Next token from probabilities [seqLen, vocab] (last row).")
+        .def("sample",
+             [](G &g, py::object input, SamplingMode mode, int K, double P) {
+                 return g.sample(idVector(input), mode, K, P);
+             },
+             py::arg("input"), py::arg("mode"), py::arg("K") = 10, py::arg("P") = 0.1)
+        .def("generate", generate, py::arg("input"), py::arg("num_tokens"), py::arg("mode"), py::arg("K") = 10,
+             py::arg("P") = 0.1, "Appends num_tokens sampled tokens; returns the input's type.")
+        .def("zeroGrad", &G::zeroGrad)
+        .def("sgdUpdate", &G::sgdUpdate, py::arg("lr"))
+        .def("clone", &G::clone)
+        .def("clear", &G::clear, "Drops the checkpointed activation.")
+        .def("getParameters", &G::getParameters)
+        .def("setParameters", &G::setParameters, py::arg("params"))
+        .def("getGradients", &G::getGradients)
+        .def_readonly("transformerLayer", &G::transformerLayer);
+
+    py::class_<AdamOptimizer>(m, "FloatAdamOptimizer", "Adam over a parameter map (decay folded into the gradient).")
+        .def(py::init<std::map<std::string, T>, double, double, double, double, double, bool>(), py::arg("params"),
+             py::arg("lr") = 0.001, py::arg("b1") = 0.9, py::arg("b2") = 0.999, py::arg("eps") = 1e-8,
+             py::arg("decay") = 0.0, py::arg("decoupled") = false)
+        .def("step", &AdamOptimizer::step, py::arg("grads"), "One update of every parameter from `grads`.")
+        .def("getLearningRate", &AdamOptimizer::getLearningRate)
+        .def("setLearningRate", &AdamOptimizer::setLearningRate, py::arg("lr"))
+        .def("getTimeStep", &AdamOptimizer::getTimeStep)
+        .def("setTimeStep", &AdamOptimizer::setTimeStep, py::arg("t"));
+    py::class_<AdamWOptimizer, AdamOptimizer>(m, "FloatAdamWOptimizer", "AdamW over a parameter map (decoupled decay).")
+        .def(py::init<std::map<std::string, T>, double, double, double, double, double>(), py::arg("params"),
+             py::arg("lr") = 0.001, py::arg("b1") = 0.9, py::arg("b2") = 0.999, py::arg("eps") = 1e-8,
+             py::arg("decay") = 0.0);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(cuda_transformer, m) {
@@ -188,16 +469,42 @@ PYBIND11_MODULE(cuda_transformer, m) {
         "Tensors: FloatTensor, BFloatTensor.  Layers: FloatModule / BFloatModule (base),\n"
         "FloatAttentionLayer / BFloatAttentionLayer (AttentionFloat, AttentionBFloat, Attention),\n"
         "FloatFlashAttentionLayer / BFloatFlashAttentionLayer (FlashAttention(head_dim, num_heads,\n"
-        "causal=False)).";
+        "causal=False)).\n"
+        "Around attention: <T>LayerNormLayer, <T>LinearLayer, <T>ActivationLayer, <T>MLPLayer,\n"
+        "<T>TransformerBlockLayer, <T>TransformerLayer (factories LayerNorm, Linear, Activation, ReLU,\n"
+        "GELU, Sigmoid, Tanh, MLP, TransformerBlock, Transformer, with Float / BFloat suffixes),\n"
+        "<T>Softmax, <T>CrossEntropyLoss; IntTensor for token ids; FloatTokenEmbedding,\n"
+        "FloatPositionEmbedding, FloatUnEmbedding, FloatNanoGPT, FloatAdamOptimizer,\n"
+        "FloatAdamWOptimizer; enums ActivationType, SamplingMode.";
+
+    py::enum_<ActivationType>(m, "ActivationType", "Activation of the MLP sub-layers.")
+        .value("ReLU", ActivationType::ReLU)
+        .value("GELU", ActivationType::GELU, "tanh approximation")
+        .value("Sigmoid", ActivationType::Sigmoid)
+        .value("Tanh", ActivationType::Tanh);
+    py::enum_<SamplingMode>(m, "SamplingMode", "Next-token choice of NanoGPT.predict / sample / generate.")
+        .value("Greedy", SamplingMode::Greedy)
+        .value("Random", SamplingMode::Random)
+        .value("Nucleus", SamplingMode::Nucleus)
+        .value("TopK", SamplingMode::TopK);
 
     declareTensor<float>(m, "Float");
     declareTensor<bf16>(m, "BFloat");
+    declareTensor<int32_t>(m, "Int");
     declareFlashAttention<float>(m, "Float");
     declareFlashAttention<bf16>(m, "BFloat");
     declareModule<float>(m, "Float");
     declareModule<bf16>(m, "BFloat");
     declareAttention<float>(m, "Float");
     declareAttention<bf16>(m, "BFloat");
+    declareLayers<float>(m, "Float");
+    declareLayers<bf16>(m, "BFloat");
+    declareFactories<float>(m, "Float");
+    declareFactories<bf16>(m, "BFloat");
+    declareFactories<float>(m, "");
+    declareLosses<float>(m, "Float");
+    declareLosses<bf16>(m, "BFloat");
+    declareNanoGPT(m);
     m.def("Attention",
           [](int inputDim, int numHeads, int headDim, bool causal) {
               return std::make_shared<AttentionLayer<float>>(inputDim, numHeads, headDim, causal);

@@ -1,19 +1,22 @@
-"""NanoGPT training step with its attention on the MI355X kernels.
+"""NanoGPT in torch with its attention on the MI355X kernels.
 
-This is the drop-in host for the attention path, not a re-implementation of the reference's
-other layers: the architecture follows the reference's NanoGPT
+Two roles: the torch-hosted training step (torch supplies the layers around attention), and,
+with ``attention="sdpa"`` in float64 on the CPU, the reference that the fully native model
+``cuda_transformer.FloatNanoGPT`` (every layer in libctattn.so) is checked against.  The
+architecture follows the reference's NanoGPT
 (``NanoGPT.cu:83-94``: token + position embedding -> Transformer -> un-embedding ->
 softmax; ``TransformerBlockLayer.cu:60-66``: LayerNorm -> Attention -> LayerNorm -> MLP
 with **no residual connections**; ``AttentionLayer.cu:75-102``: QKV projection with bias ->
-flash attention -> output projection with bias; ``MLPLayer`` Linear -> GELU (tanh
-approximation, ``gelu_kernels.cu:31-50``) -> Linear; ``Embedding.cu:314-360``:
+flash attention -> output projection with bias; ``MLPLayer`` Linear -> activation (GELU in
+its tanh approximation by default, ``gelu_kernels.cu:31-50``; ReLU / Sigmoid / Tanh) ->
+Linear; ``Embedding.cu:314-360``:
 un-embedding without bias; LayerNorm epsilon 1e-5, ``LayerNorm.cu:31``), while torch
 supplies the surrounding layers and Adam.  Attention itself (forward and backward) runs in
 libctattn.so through ``cudatransformer_amd.flash_attention``; with ``attention="sdpa"`` the
 same module uses torch's SDPA instead, which is how the fp64 CPU reference of a training
 step is built in the tests.
 
-Deliberate departures: causal attention (config 5), textbook Adam
+Deliberate departures from the reference: causal attention (config 5), textbook Adam
 (the reference increments its step twice, ``AdamOptimizer.cu:75,95``), mean cross-entropy
 over all tokens on logits (mathematically -log softmax), weights initialised N(0, 0.02^2)
 (the reference initialises every weight to zero, ``LinearLayer.cu:28``).
@@ -28,6 +31,15 @@ from ._capi import flash_attention
 
 CONFIG5 = dict(vocab=65, max_seq_len=256, d_model=384, n_heads=6, head_dim=64, mlp_dim=1536,
                n_layers=6, batch=16, seq_len=256, lr=3e-4)
+
+
+# MLP activations of the reference's ActivationType (gelu: tanh approximation).
+_ACTIVATIONS = {
+    "relu": F.relu,
+    "gelu": lambda x: F.gelu(x, approximate="tanh"),
+    "sigmoid": torch.sigmoid,
+    "tanh": torch.tanh,
+}
 
 
 class Attention(nn.Module):
@@ -57,8 +69,11 @@ class Attention(nn.Module):
 class Block(nn.Module):
     """LayerNorm -> Attention -> LayerNorm -> MLP, no residuals (TransformerBlockLayer.cu:60-66)."""
 
-    def __init__(self, d_model, n_heads, head_dim, mlp_dim, causal, attention):
+    def __init__(self, d_model, n_heads, head_dim, mlp_dim, causal, attention, activation="gelu"):
         super().__init__()
+        if activation not in _ACTIVATIONS:
+            raise ValueError(f"activation must be one of {sorted(_ACTIVATIONS)}")
+        self.act = _ACTIVATIONS[activation]
         self.ln1 = nn.LayerNorm(d_model, eps=1e-5)
         self.attn = Attention(d_model, n_heads, head_dim, causal, attention)
         self.ln2 = nn.LayerNorm(d_model, eps=1e-5)
@@ -67,19 +82,19 @@ class Block(nn.Module):
 
     def forward(self, x):
         x = self.attn(self.ln1(x))
-        return self.fc2(F.gelu(self.fc1(self.ln2(x)), approximate="tanh"))
+        return self.fc2(self.act(self.fc1(self.ln2(x))))
 
 
 class NanoGPT(nn.Module):
     def __init__(self, vocab, max_seq_len, d_model, n_heads, head_dim, mlp_dim, n_layers,
-                 causal=True, attention="ctattn", **_):
+                 causal=True, attention="ctattn", activation="gelu", **_):
         super().__init__()
         if attention not in ("ctattn", "sdpa"):
             raise ValueError("attention must be 'ctattn' or 'sdpa'")
         self.tok = nn.Embedding(vocab, d_model)
         self.pos = nn.Embedding(max_seq_len, d_model)
         self.blocks = nn.ModuleList(
-            Block(d_model, n_heads, head_dim, mlp_dim, causal, attention) for _ in range(n_layers))
+            Block(d_model, n_heads, head_dim, mlp_dim, causal, attention, activation) for _ in range(n_layers))
         self.unembed = nn.Linear(d_model, vocab, bias=False)
 
     def init_weights(self, seed: int):
