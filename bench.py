@@ -29,6 +29,11 @@ WORKLOADS = {
     "c5": dict(B=16, H=6, T=256, D=64, dtype="f32", std=1.0, peak=157.3,
                metric="NanoGPT config-5 training step tokens/s (attention on ctattn), fp32, 1 GPU",
                label="NanoGPT 6L d384 6H T256 B16 vocab65 GELU, Adam lr 3e-4, fp32 (BASELINE configs[4])"),
+    "c5n": dict(B=16, H=6, T=256, D=64, dtype="f32", std=1.0, peak=157.3,
+                metric="NanoGPT config-5 training step tokens/s (native host, every layer on libctattn), "
+                       "fp32, 1 GPU",
+                label="NanoGPT 6L d384 6H T256 B16 vocab65 GELU causal, Adam lr 3e-4, fp32 (BASELINE "
+                      "configs[4]) on the native C++ host: forward, loss, backward, Adam"),
     "layer": dict(B=8, H=16, T=1024, D=64, E=1024, dtype="f32", std=1.0, peak=157.3,
                   metric="attention layer (QKV proj + attention + out proj) fwd+bwd TFLOP/s, "
                          "B8 N1024 E1024 H16 D64 fp32, 1 GPU",
@@ -125,6 +130,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "c5":
         return bench_nanogpt(args, wl, dev)
+    if args.workload == "c5n":
+        return bench_native_nanogpt(args, wl)
     if args.workload == "layer":
         return bench_layer(args, wl)
     if args.copy_calibration:
@@ -353,6 +360,56 @@ def bench_nanogpt(args, wl, dev):
         "config": {"workload": wl["label"], "model_tflops": round(model_flops_per_step() / (ms * 1e-3) / 1e12, 2),
                    "attention_gflop_per_step": round(attention_flops_per_step() / 1e9, 3),
                    "loss_first": round(float(losses[0]), 4), "loss_last": round(float(losses[-1]), 4)},
+        "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_native_nanogpt(args, wl):
+    """Config 5 on the native host (cuda_transformer.FloatNanoGPT, every layer in
+    libctattn.so): forward (probabilities), loss, zeroGrad, backward, Adam step.  The host
+    orders all work on its own stream, so the timed region is bracketed by host clocks
+    around that stream's synchronisation."""
+    import time
+
+    import numpy as np
+
+    from cudatransformer_amd import cuda_transformer as ctm
+    from cudatransformer_amd.nanogpt import (CONFIG5, NanoGPT, attention_flops_per_step, make_batch,
+                                             model_flops_per_step, to_native)
+
+    cfg = CONFIG5
+    model = to_native(NanoGPT(**cfg, attention="sdpa").init_weights(5))
+    opt = ctm.FloatAdamOptimizer(model.getParameters(), lr=cfg["lr"], b1=0.9, b2=0.999, eps=1e-8)
+    ids, tgt = make_batch(cfg["batch"], cfg["seq_len"], cfg["vocab"], seed=5)
+    ids = ctm.IntTensor.fromNumpy(ids.numpy().astype(np.int32))
+    tgt = ctm.IntTensor.fromNumpy(tgt.numpy().astype(np.int32))
+
+    def step():
+        probs = model.forward(ids)
+        loss = model.loss(probs, tgt)
+        model.zeroGrad()
+        model.backward(ids, probs, tgt)
+        opt.step(model.getGradients())
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    ctm.synchronize()
+    t0 = time.perf_counter()
+    losses = [step() for _ in range(args.steps)]
+    ctm.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    first, last = float(losses[0].numpy().sum()), float(losses[-1].numpy().sum())
+    tokens = cfg["batch"] * cfg["seq_len"]
+    out = {
+        "metric": wl["metric"], "value": round(tokens / (ms * 1e-3), 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": wl["label"], "model_tflops": round(model_flops_per_step() / (ms * 1e-3) / 1e12, 2),
+                   "attention_gflop_per_step": round(attention_flops_per_step() / 1e9, 3),
+                   "loss_first": round(first, 4), "loss_last": round(last, 4)},
         "roofline": None, "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)

@@ -11,11 +11,18 @@
 //   AdamWOptimizer         AdamOptimizer.cu:142-233
 // Same conventions as the reference: weights start at zero (cudaMakeShared zero-fills,
 // LinearLayer.cu:28), LayerNorm at (1, 0); gradients accumulate across backward calls until
-// zeroGrad; backward(input, gradOutput) recomputes the forward activations it needs from
-// `input` (TransformerBlockLayer.cu backward).  Differences: gradient buffers are allocated on
-// the first backward; setParameters copies into the layer's buffers (the attention layer's
-// setters adopt the buffer, as the reference's do); Adam advances its step once per step
-// (the reference advances it twice, AdamOptimizer.cu:75,95).
+// zeroGrad; backward(input, gradOutput) works for any `input`.  Differences: the reference
+// recomputes every activation in backward (TransformerBlockLayer.cu backward,
+// TransformerLayer.cu:78-140).  Here LayerNorm, MLP, block and transformer layers keep the
+// activations of their last forward and their backward reuses them when it is given that
+// forward's input tensor (the same device buffer and shape); any other input is recomputed
+// as the reference does.  The kept activations are released by the backward that consumes
+// them, by the next forward, or by clear().  The results are the same either way; the kept
+// activations cost HBM (about 0.6 GB for the 6-layer d384 B16 T256 model) and save the
+// recomputation.  Also: gradient buffers are allocated on the first backward; setParameters
+// copies into the layer's buffers (the attention layer's setters adopt the buffer, as the
+// reference's do); Adam advances its step once per step (the reference advances it twice,
+// AdamOptimizer.cu:75,95).
 #pragma once
 
 #include <cmath>
@@ -83,6 +90,13 @@ inline size_t rowsOf(const Tensor<DType> &t, size_t dim, const char *what) {
 }
 
 inline std::string prefixed(const std::string &prefix, const std::string &name) { return prefix + "." + name; }
+
+// Whether `a` is the tensor `b` (same device buffer and shape): the test for reusing the
+// activations a forward on `b` kept.
+template <typename DType>
+inline bool sameTensor(const Tensor<DType> &a, const Tensor<DType> &b) {
+    return !a.empty() && a.get() == b.get() && a.shape() == b.shape();
+}
 
 // Splits a prefixed map: entries "prefix.rest" -> "rest".
 template <typename DType>
@@ -229,14 +243,20 @@ struct LayerNormLayer : public Layer<DType> {
         return c;
     }
 
-    Tensor<DType> forward(Tensor<DType> input) override { return run(input).first; }
+    Tensor<DType> forward(Tensor<DType> input) override {
+        auto [out, stats] = run(input);
+        cachedInput = input;
+        cachedStats = stats;
+        return out;
+    }
 
-    // Recomputes the row statistics of `input` (the reference reuses the last forward's,
-    // LayerNorm.cu:143), then dX and the accumulated dGamma / dBeta.
+    // dX and the accumulated dGamma / dBeta (LayerNorm.cu:143), from the row statistics the
+    // last forward kept when `input` is its input, else recomputed from `input`.
     Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
         const size_t rows = detail::rowsOf(input, size_t(inputDim), "LayerNormLayer input");
         if (gradOutput.size() != input.size()) throw std::invalid_argument("LayerNormLayer: grad_output shape");
-        auto stats = run(input).second;
+        auto stats = detail::sameTensor(cachedInput, input) ? cachedStats : run(input).second;
+        clear();
         ensureGrads();
         Tensor<DType> inputGrad = Tensor<DType>::empty(input.shape());
         const int dt = DTypeCode<DType>::value;
@@ -269,8 +289,15 @@ struct LayerNormLayer : public Layer<DType> {
         detail::sgdStep(weights, weightsGrad, lr, size_t(inputDim));
         detail::sgdStep(biases, biasesGrad, lr, size_t(inputDim));
     }
+    void clear() override {
+        cachedInput = Tensor<DType>();
+        cachedStats = nullptr;
+    }
 
 private:
+    Tensor<DType> cachedInput;
+    std::shared_ptr<float[]> cachedStats;
+
     // Output and the fp32 row statistics [mean (rows) | rstd (rows)].
     std::pair<Tensor<DType>, std::shared_ptr<float[]>> run(const Tensor<DType> &input) {
         const size_t rows = detail::rowsOf(input, size_t(inputDim), "LayerNormLayer input");
@@ -328,15 +355,33 @@ struct MLPLayer : public Layer<DType> {
         return std::make_shared<MLPLayer<DType>>(c);
     }
     Tensor<DType> forward(Tensor<DType> input) override {
-        for (auto &l : layers) input = l->forward(input);
+        cachedInputs.clear();
+        for (auto &l : layers) {
+            cachedInputs.push_back(input);
+            input = l->forward(input);
+        }
         return input;
     }
-    // Recomputes every layer's input, then backpropagates through them in reverse.
+    // Backpropagates through the layers in reverse, from the layer inputs the last forward
+    // kept when `input` is its input, else from inputs recomputed from `input`.
     Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
-        std::vector<Tensor<DType>> inputs{input};
-        for (size_t i = 0; i + 1 < layers.size(); ++i) inputs.push_back(layers[i]->forward(inputs.back()));
-        for (size_t i = layers.size(); i-- > 0;) gradOutput = layers[i]->backward(inputs[i], gradOutput);
+        std::vector<Tensor<DType>> inputs;
+        if (!cachedInputs.empty() && detail::sameTensor(cachedInputs.front(), input)) {
+            inputs.swap(cachedInputs);
+        } else {
+            clear();
+            inputs.push_back(input);
+            for (size_t i = 0; i + 1 < layers.size(); ++i) inputs.push_back(layers[i]->forward(inputs.back()));
+        }
+        for (size_t i = layers.size(); i-- > 0;) {
+            gradOutput = layers[i]->backward(inputs[i], gradOutput);
+            inputs[i] = Tensor<DType>();
+        }
         return gradOutput;
+    }
+    void clear() override {
+        cachedInputs.clear();
+        for (auto &l : layers) l->clear();
     }
     std::map<std::string, Tensor<DType>> getParameters() override {
         std::map<std::string, Tensor<DType>> m;
@@ -359,6 +404,7 @@ struct MLPLayer : public Layer<DType> {
     }
 
 private:
+    std::vector<Tensor<DType>> cachedInputs;  // each layer's input in the last forward
     static std::string key(size_t i) { return "layer_" + std::to_string(i); }
 };
 
@@ -393,22 +439,39 @@ struct TransformerBlockLayer : public Layer<DType> {
         return c;
     }
 
-    // LayerNorm -> Attention -> LayerNorm -> MLP (TransformerBlockLayer.cu:60-66).
+    // LayerNorm -> Attention -> LayerNorm -> MLP (TransformerBlockLayer.cu:60-66), keeping
+    // the activations and attention states for backward.
     Tensor<DType> forward(Tensor<DType> input) override {
-        return mlp->forward(secondNorm->forward(attention->forward(firstNorm->forward(input))));
+        Kept k = run(input);
+        Tensor<DType> out = mlp->forward(k.normed2);
+        kept = std::move(k);
+        return out;
     }
 
-    // Recomputes the block's activations (attention with its cached states), then
-    // backpropagates (TransformerBlockLayer.cu:74-87).
+    // Backpropagates through MLP, LayerNorm, attention and LayerNorm
+    // (TransformerBlockLayer.cu:74-87), from the last forward's activations when `input` is
+    // its input, else from activations recomputed from `input`.
     Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
-        Tensor<DType> normed = firstNorm->forward(input);
-        std::array<Tensor<DType>, 4> states;
-        Tensor<DType> attn = attention->forward(normed, states.data());
-        Tensor<DType> normed2 = secondNorm->forward(attn);
-        Tensor<DType> g = mlp->backward(normed2, gradOutput);
-        g = secondNorm->backward(attn, g);
-        g = attention->backward(normed, g, states.data());
+        Kept k;
+        if (detail::sameTensor(kept.input, input)) {
+            std::swap(k, kept);
+        } else {
+            clear();
+            k = run(input);
+        }
+        Tensor<DType> g = mlp->backward(k.normed2, gradOutput);
+        k.normed2 = Tensor<DType>();
+        g = secondNorm->backward(k.attn, g);
+        k.attn = Tensor<DType>();
+        g = attention->backward(k.normed, g, k.states.data());
         return firstNorm->backward(input, g);
+    }
+    void clear() override {
+        kept = Kept();
+        firstNorm->clear();
+        secondNorm->clear();
+        mlp->clear();
+        attention->flashAttn.clearCache();
     }
 
     std::map<std::string, Tensor<DType>> getParameters() override { return collect(false); }
@@ -433,6 +496,22 @@ struct TransformerBlockLayer : public Layer<DType> {
     }
 
 private:
+    struct Kept {
+        Tensor<DType> input, normed, attn, normed2;
+        std::array<Tensor<DType>, 4> states;  // attention's [Q, K, V, attention output]
+    };
+    Kept kept;
+
+    // The activations up to the MLP's input.
+    Kept run(const Tensor<DType> &input) {
+        Kept k;
+        k.input = input;
+        k.normed = firstNorm->forward(input);
+        k.attn = attention->forward(k.normed, k.states.data());
+        k.normed2 = secondNorm->forward(k.attn);
+        return k;
+    }
+
     std::map<std::string, Tensor<DType>> collect(bool grads) {
         std::map<std::string, Tensor<DType>> m;
         auto get = [grads](Layer<DType> &l) { return grads ? l.getGradients() : l.getParameters(); };
@@ -447,9 +526,9 @@ private:
 // A stack of numLayers blocks (TransformerLayer.cu:29-41).  Parameters are keyed
 // "layer_<slot>.<name>" where slot is the block's position in the reference's layer list,
 // which holds a CheckpointLayer before every checkpointGap-th block (checkpointGap > 0), so
-// the keys match the reference's for every checkpointGap.  backward recomputes each block's
-// input from `input` and backpropagates block by block; the gradients equal the reference's
-// for any checkpointGap (its checkpoints only change what it keeps in memory).
+// the keys match the reference's for every checkpointGap.  backward backpropagates block by
+// block; the gradients equal the reference's for any checkpointGap (its checkpoints only
+// change what it keeps in memory).
 template <typename DType = float>
 struct TransformerLayer : public Layer<DType> {
     std::vector<std::shared_ptr<TransformerBlockLayer<DType>>> blocks;
@@ -471,21 +550,36 @@ struct TransformerLayer : public Layer<DType> {
 
     std::shared_ptr<Layer<DType>> clone() override {
         auto c = std::make_shared<TransformerLayer<DType>>(*this);
+        c->blockInputs.clear();
         for (auto &b : c->blocks) b = std::static_pointer_cast<TransformerBlockLayer<DType>>(b->clone());
         return c;
     }
     Tensor<DType> forward(Tensor<DType> input) override {
-        for (auto &b : blocks) input = b->forward(input);
+        blockInputs.clear();
+        for (auto &b : blocks) {
+            blockInputs.push_back(input);
+            input = b->forward(input);
+        }
         return input;
     }
     Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
-        std::vector<Tensor<DType>> inputs{input};
-        for (size_t i = 0; i + 1 < blocks.size(); ++i) inputs.push_back(blocks[i]->forward(inputs.back()));
+        std::vector<Tensor<DType>> inputs;
+        if (!blockInputs.empty() && detail::sameTensor(blockInputs.front(), input)) {
+            inputs.swap(blockInputs);
+        } else {
+            clear();
+            inputs.push_back(input);
+            for (size_t i = 0; i + 1 < blocks.size(); ++i) inputs.push_back(blocks[i]->forward(inputs.back()));
+        }
         for (size_t i = blocks.size(); i-- > 0;) {
             gradOutput = blocks[i]->backward(inputs[i], gradOutput);
             inputs[i] = Tensor<DType>();
         }
         return gradOutput;
+    }
+    void clear() override {
+        blockInputs.clear();
+        for (auto &b : blocks) b->clear();
     }
     std::map<std::string, Tensor<DType>> getParameters() override {
         std::map<std::string, Tensor<DType>> m;
@@ -508,6 +602,8 @@ struct TransformerLayer : public Layer<DType> {
     }
 
 private:
+    std::vector<Tensor<DType>> blockInputs;  // each block's input in the last forward
+
     std::string key(size_t i) const {
         const size_t slot = i + (checkpointGap > 0 ? i / size_t(checkpointGap) : 0);
         return "layer_" + std::to_string(slot);

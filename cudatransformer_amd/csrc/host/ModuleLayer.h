@@ -1,6 +1,6 @@
 // Layer<DType>: the reference's layer interface (ModuleLayer.cu:15-91), unchanged in shape:
 // virtual clone / forward / backward, operator(), parameter and gradient maps, zeroGrad,
-// sgdUpdate, and Module<DType> = shared_ptr<Layer<DType>>.
+// sgdUpdate, and Module<DType> = shared_ptr<Layer<DType>>; plus clear().
 #pragma once
 
 #include <map>
@@ -27,6 +27,9 @@ struct Layer {
     virtual std::map<std::string, Tensor<DType>> getGradients() { return {}; }
     virtual void zeroGrad() {}
     virtual void sgdUpdate(float) {}
+    // Drops the activations a layer keeps from its last forward for its backward (the
+    // reference's TransformerLayer / MLPLayer::clear free their checkpoints).
+    virtual void clear() {}
 };
 
 template <typename DType = float>

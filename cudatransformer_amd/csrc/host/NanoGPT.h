@@ -10,6 +10,9 @@
 // un-embedding; parameter keys "tokenEmbedding", "positionEmbedding", "unEmbedding" and the
 // transformer's "layer_<i>.…"; weights start at zero; greedy / random / nucleus / top-k
 // sampling on the host.  Differences, all deliberate:
+//   * forward keeps its embedding and every layer's activations; a backward given that
+//     forward's ids tensor reuses them instead of recomputing (same result, see
+//     ModelLayers.h), any other ids are recomputed as the reference does;
 //   * the softmax and cross-entropy backward are one kernel, dz = (p - onehot) / (N temp),
 //     from the probabilities passed to backward (the reference chains the two backward passes
 //     and re-derives p from a recomputed un-embedding, NanoGPT.cu:365-368; same result);
@@ -292,7 +295,9 @@ struct NanoGPT {
 
     // ids [..., T] (T <= maxSeqLen) -> probabilities [..., T, vocab] (NanoGPT.cu:83-94).
     Tensor<DType> forward(const Tensor<int32_t> &ids) {
-        Tensor<DType> x = transformerLayer.forward(embed(ids));
+        keptIds = ids;
+        keptEmbedding = embed(ids);
+        Tensor<DType> x = transformerLayer.forward(keptEmbedding);
         preUnembeddingCheckpoint = x;
         return softmax.forward(unEmbedding.forward(x)).reshape(detail::withLast(ids.shape(), size_t(vocabSize())));
     }
@@ -308,13 +313,17 @@ struct NanoGPT {
 
     // Accumulates every parameter gradient of the mean cross-entropy (NanoGPT.cu:357-377).
     // `probs` are forward(input)'s output; the transformer output comes from the checkpoint
-    // that forward left, or is recomputed when it does not match `input`.
+    // that forward left, or is recomputed when it does not match `input`.  When `input` is
+    // the ids tensor of the last forward, the embedding and the transformer's activations
+    // that forward kept are reused instead of recomputed.
     void backward(const Tensor<int32_t> &input, const Tensor<DType> &probs, const Tensor<int32_t> &target) {
         auto [B, T] = detail::idRows(input, "NanoGPT.backward");
         const size_t rows = B * T, V = size_t(vocabSize()), E = size_t(embeddingDim());
         if (probs.size() != rows * V) throw std::invalid_argument("NanoGPT.backward: probs must be [..., T, vocab]");
         if (target.size() != rows) throw std::invalid_argument("NanoGPT.backward: target must match the input");
-        Tensor<DType> embedded = embed(input);
+        Tensor<DType> embedded = detail::sameTensor(keptIds, input) ? keptEmbedding : embed(input);
+        keptIds = Tensor<int32_t>();
+        keptEmbedding = Tensor<DType>();
         Tensor<DType> x = preUnembeddingCheckpoint;
         if (x.empty() || x.size() != rows * E) x = transformerLayer.forward(embedded);
         x = x.reshape({B, T, E});
@@ -334,8 +343,13 @@ struct NanoGPT {
                     "ctattn_embedding_bwd");
     }
 
-    // Drops the checkpointed activation (NanoGPT.cu:466).
-    void clear() { preUnembeddingCheckpoint = Tensor<DType>(); }
+    // Drops the checkpointed and kept activations (NanoGPT.cu:466).
+    void clear() {
+        preUnembeddingCheckpoint = Tensor<DType>();
+        keptIds = Tensor<int32_t>();
+        keptEmbedding = Tensor<DType>();
+        transformerLayer.clear();
+    }
 
     void zeroGrad() {
         tokenEmbedding.zeroGrad();
@@ -357,6 +371,8 @@ struct NanoGPT {
         c.transformerLayer = *std::static_pointer_cast<TransformerLayer<DType>>(transformerLayer.clone());
         c.unEmbedding = unEmbedding.clone();
         c.preUnembeddingCheckpoint = Tensor<DType>();
+        c.keptIds = Tensor<int32_t>();
+        c.keptEmbedding = Tensor<DType>();
         return c;
     }
 
@@ -428,6 +444,9 @@ struct NanoGPT {
     }
 
 private:
+    Tensor<int32_t> keptIds;      // the ids of the last forward
+    Tensor<DType> keptEmbedding;  // and their embedding
+
     Tensor<DType> embed(const Tensor<int32_t> &ids) {
         auto [B, T] = detail::idRows(ids, "NanoGPT");
         if (T > size_t(maxSeqLen()))

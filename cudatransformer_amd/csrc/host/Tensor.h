@@ -3,9 +3,9 @@
 //
 // Same ownership model as the reference: copies are shallow (shared_ptr to the device
 // buffer, Tensor.cu:73-113), clone() is deep, constructors zero-fill (Tensor.cu:27-55).
-// Different mechanics: buffers come from the stream-ordered allocator (hipMallocAsync /
-// hipFreeAsync) and fills / copies are enqueued on the one runtime stream, instead of
-// cudaMalloc + fill kernel + cudaDeviceSynchronize per allocation (headers.cu:195-215).  The
+// Different mechanics: buffers come from a caching allocator (BlockCache) and fills /
+// copies are enqueued on the one runtime stream, instead of cudaMalloc + fill kernel +
+// cudaDeviceSynchronize per allocation (headers.cu:195-215).  The
 // host waits only when data comes back to the CPU (numpy(), item()) or after an upload from
 // pageable memory (fromPointer()).
 //
@@ -15,7 +15,9 @@
 
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <numeric>
 #include <stdexcept>
 #include <string>
@@ -60,13 +62,93 @@ inline float toFloat(float x) { return x; }
 inline float toFloat(bf16 x) { return x.toFloat(); }
 inline float toFloat(int32_t x) { return float(x); }
 
-// Stream-ordered device allocation with a stream-ordered free as deleter.
+// Caching device allocator for the host layer's buffers.  A freed block goes to a free list
+// keyed by its rounded size and is handed out again to the next request of that size, with
+// no HIP call.  Reuse is safe without events because every kernel and copy of the host layer
+// is ordered on the one Runtime stream: work on a block's next owner is enqueued after all
+// work on its previous owner.  hipMalloc runs only when no cached block fits (the first
+// steps of a training loop); on hipErrorOutOfMemory the cache is returned to the driver and
+// the allocation retried.  (hipFreeAsync on the default pool stalled the host for up to
+// 10 ms per call in a training step.)
+class BlockCache {
+public:
+    static BlockCache &instance() {
+        static BlockCache *cache = new BlockCache();  // never destroyed: outlives static tensors
+        return *cache;
+    }
+
+    void *allocate(size_t bytes) {
+        const size_t size = rounded(bytes);
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            auto it = free_.find(size);
+            if (it != free_.end() && !it->second.empty()) {
+                void *p = it->second.back();
+                it->second.pop_back();
+                cachedBytes_ -= size;
+                return p;
+            }
+        }
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, size);
+        if (e == hipErrorOutOfMemory) {
+            (void)hipGetLastError();
+            emptyCache();
+            e = hipMalloc(&p, size);
+        }
+        hipCheck(e, "hipMalloc");
+        std::lock_guard<std::mutex> lock(mutex_);
+        reservedBytes_ += size;
+        return p;
+    }
+
+    void release(void *p, size_t bytes) {
+        std::lock_guard<std::mutex> lock(mutex_);
+        free_[rounded(bytes)].push_back(p);
+        cachedBytes_ += rounded(bytes);
+    }
+
+    // Returns every cached block to the driver (after the stream has drained).
+    void emptyCache() {
+        Runtime::synchronize();
+        std::lock_guard<std::mutex> lock(mutex_);
+        for (auto &[size, blocks] : free_) {
+            for (void *p : blocks) (void)hipFree(p);
+            reservedBytes_ -= size * blocks.size();
+        }
+        free_.clear();
+        cachedBytes_ = 0;
+    }
+
+    size_t cachedBytes() {
+        std::lock_guard<std::mutex> lock(mutex_);
+        return cachedBytes_;
+    }
+    size_t reservedBytes() {
+        std::lock_guard<std::mutex> lock(mutex_);
+        return reservedBytes_;
+    }
+
+private:
+    // 512-byte granules below 1 MiB, 64 KiB granules above.
+    static size_t rounded(size_t bytes) {
+        const size_t g = bytes < (size_t(1) << 20) ? 512 : (size_t(64) << 10);
+        return (bytes + g - 1) / g * g;
+    }
+
+    std::mutex mutex_;
+    std::map<size_t, std::vector<void *>> free_;
+    size_t cachedBytes_ = 0, reservedBytes_ = 0;
+};
+
+// Device allocation from the block cache; the deleter hands the block back.
 template <typename T>
 std::shared_ptr<T[]> deviceAlloc(size_t count) {
     if (count == 0) return nullptr;
-    void *p = nullptr;
-    hipCheck(hipMallocAsync(&p, count * sizeof(T), Runtime::stream()), "hipMallocAsync");
-    return std::shared_ptr<T[]>(static_cast<T *>(p), [](T *q) { (void)hipFreeAsync(q, Runtime::stream()); });
+    const size_t bytes = count * sizeof(T);
+    Runtime::stream();  // the stream (and device) exist before the first block
+    void *p = BlockCache::instance().allocate(bytes);
+    return std::shared_ptr<T[]>(static_cast<T *>(p), [bytes](T *q) { BlockCache::instance().release(q, bytes); });
 }
 
 template <typename DType = float>

@@ -159,6 +159,7 @@ void declareModule(py::module_ &m, const std::string &suffix) {
         .def("zeroGrad", &L::zeroGrad, "Zeroes the accumulated gradients.")
         .def("sgdUpdate", &L::sgdUpdate, py::arg("lr"), "param -= lr * grad for every parameter.")
         .def("clone", &L::clone, "Deep copy of the layer's parameters.")
+        .def("clear", &L::clear, "Drops the activations kept from the last forward for backward.")
         .def("__call__", &L::operator(), py::arg("input"), "Shorthand for forward(input).");
 }
 
@@ -440,7 +441,7 @@ void declareNanoGPT(py::module_ &m) {
         .def("zeroGrad", &G::zeroGrad)
         .def("sgdUpdate", &G::sgdUpdate, py::arg("lr"))
         .def("clone", &G::clone)
-        .def("clear", &G::clear, "Drops the checkpointed activation.")
+        .def("clear", &G::clear, "Drops the checkpointed activation and the activations kept for backward.")
         .def("getParameters", &G::getParameters)
         .def("setParameters", &G::setParameters, py::arg("params"))
         .def("getGradients", &G::getGradients)
@@ -526,6 +527,12 @@ PYBIND11_MODULE(cuda_transformer, m) {
           py::arg("head_dim"), py::arg("num_heads"), py::arg("causal") = false,
           "Creates a bfloat16 FlashAttentionLayer (fp32 accumulation).");
     m.def("synchronize", &Runtime::synchronize, "Waits for all work queued by this module.");
+    m.def("empty_cache", [] { BlockCache::instance().emptyCache(); },
+          "Returns the device memory cached for reuse by this module's tensors to the driver.");
+    m.def("memory_cached", [] { return BlockCache::instance().cachedBytes(); },
+          "Bytes of freed tensor memory held for reuse.");
+    m.def("memory_reserved", [] { return BlockCache::instance().reservedBytes(); },
+          "Bytes of device memory this module's allocator holds (in use or cached).");
     m.def("set_policy", &ctattn_set_policy, py::arg("policy"),
           "Kernel selection policy: 0 = MFMA (fastest), 1 = generic kernels, 2 = MFMA with a "
           "deterministic dQ reduction.  Returns the previous policy.");

@@ -94,41 +94,64 @@ __global__ __launch_bounds__(256) void layernorm_bwd_dx_kernel(const T *__restri
     }
 }
 
-constexpr int kLnRowsPerChunk = 64;
+constexpr int kLnRowsPerChunk = 32;
 
 // Stage 1 of the gamma / beta gradients: part[chunk][c] = sum over the chunk's rows of
-// dy * xhat (first D floats) and dy (next D floats).  One thread per column.
+// dy * xhat (first D floats) and dy (next D floats).  256 threads = 64 columns x 4 row lanes
+// (8 rows each), combined in LDS in a fixed order.
 template <typename T>
 __global__ __launch_bounds__(256) void layernorm_bwd_part_kernel(const T *__restrict__ x, const T *__restrict__ dy,
                                                                 const float *__restrict__ mean,
                                                                 const float *__restrict__ rstd,
                                                                 float *__restrict__ part, int64_t N, int D) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    __shared__ float red[2][4][64];
+    const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
     const int64_t chunk = blockIdx.y;
-    if (c >= D) return;
     const int64_t r0 = chunk * kLnRowsPerChunk;
-    const int64_t r1 = r0 + kLnRowsPerChunk < N ? r0 + kLnRowsPerChunk : N;
     float sg = 0.f, sb = 0.f;
-    for (int64_t r = r0; r < r1; ++r) {
-        const float d = ld(dy, r * D + c);
-        sg += d * (ld(x, r * D + c) - mean[r]) * rstd[r];
-        sb += d;
+    if (c < D) {
+#pragma unroll
+        for (int i = 0; i < kLnRowsPerChunk / 4; ++i) {
+            const int64_t r = r0 + rl + 4 * i;
+            if (r < N) {
+                const float d = ld(dy, r * D + c);
+                sg += d * (ld(x, r * D + c) - mean[r]) * rstd[r];
+                sb += d;
+            }
+        }
     }
-    part[chunk * 2 * D + c] = sg;
-    part[chunk * 2 * D + D + c] = sb;
+    red[0][rl][cl] = sg;
+    red[1][rl][cl] = sb;
+    __syncthreads();
+    if (rl == 0 && c < D) {
+        part[chunk * 2 * D + c] = ((red[0][0][cl] + red[0][1][cl]) + red[0][2][cl]) + red[0][3][cl];
+        part[chunk * 2 * D + D + c] = ((red[1][0][cl] + red[1][1][cl]) + red[1][2][cl]) + red[1][3][cl];
+    }
 }
 
-// Stage 2: dgamma[c] += sum_chunk part[chunk][c], dbeta likewise, in chunk order.
+// Stage 2: dgamma[c] += sum_chunk part[chunk][c], dbeta likewise.  64 columns x 4 lanes per
+// block; lane l takes chunks l, l+4, ... in increasing order, then the lanes add in a fixed
+// order.
 template <typename T>
 __global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *__restrict__ part, T *__restrict__ dg,
                                                                   T *__restrict__ db, int64_t chunks, int D) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= D) return;
+    __shared__ float red[2][4][64];
+    const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
     float sg = 0.f, sb = 0.f;
-    for (int64_t k = 0; k < chunks; ++k) {
-        sg += part[k * 2 * D + c];
-        sb += part[k * 2 * D + D + c];
+    if (c < D) {
+        for (int64_t k = rl; k < chunks; k += 4) {
+            sg += part[k * 2 * D + c];
+            sb += part[k * 2 * D + D + c];
+        }
     }
+    red[0][rl][cl] = sg;
+    red[1][rl][cl] = sb;
+    __syncthreads();
+    if (rl != 0 || c >= D) return;
+    sg = ((red[0][0][cl] + red[0][1][cl]) + red[0][2][cl]) + red[0][3][cl];
+    sb = ((red[1][0][cl] + red[1][1][cl]) + red[1][2][cl]) + red[1][3][cl];
     if (dg != nullptr) st(dg, c, ld(dg, c) + sg);
     if (db != nullptr) st(db, c, ld(db, c) + sb);
 }
@@ -416,9 +439,9 @@ int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void
                                static_cast<const T *>(gamma), dyt, mean, rstd, static_cast<T *>(dx), N, int(D));
         if (dgamma || dbeta) {
             float *part = static_cast<float *>(workspace);
-            hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 255) / 256), unsigned(chunks)),
+            hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 63) / 64), unsigned(chunks)),
                                dim3(256), 0, st, xt, dyt, mean, rstd, part, N, int(D));
-            hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 255) / 256)), dim3(256), 0,
+            hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 63) / 64)), dim3(256), 0,
                                st, part, static_cast<T *>(dgamma), static_cast<T *>(dbeta), chunks, int(D));
         }
         return hipGetLastError();

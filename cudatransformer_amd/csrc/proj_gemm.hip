@@ -14,8 +14,13 @@
 // So the QKV projection writes Q/K/V in attention layout and the output projection reads the
 // attention output in place: no transpose kernels, no extra HBM passes.
 //
-// Tiling: a workgroup (4 waves) computes a 128 x 128 tile of out, each wave a 64 x 64 block
-// as 2 x 2 32x32 MFMA tiles, over K in steps of 16.  Operand tiles are staged global ->
+// Tiling: a workgroup (4 waves, 2 x 2) computes a BM x BN tile of out, BM, BN in {64, 128},
+// each wave a (BM/2) x (BN/2) block of 32x32 MFMA tiles, over K in steps of BK.  The tile
+// configurations are 128 x 128 x 16, 128 x 64 x 32, 64 x 128 x 32 and 64 x 64 x 64: each
+// gives a wave 32 MFMAs (2048 cycles) per K step, so smaller tiles wait on their global
+// loads as rarely as the large one.  The launch takes the largest tile that still gives at
+// least one workgroup per CU (256): the 4096 x 384 products of a d384 model run 64 x 64,
+// the large ones 128 x 128.  Operand tiles are staged global ->
 // registers -> LDS (double-buffered, one barrier per step; the next step's global loads are
 // in flight during this step's MFMAs).  A K-contiguous operand is stored [row][k] in LDS
 // and read as float4 along k; an M/N-contiguous one is stored [k][row] and read per element
@@ -34,8 +39,8 @@
 namespace ctattn {
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 16;
 constexpr int kThreads = 256;
+constexpr int kFillWorkgroups = 256;  // one per CU
 
 template <typename T> __device__ __forceinline__ float load_f(const T *p);
 template <> __device__ __forceinline__ float load_f<float>(const float *p) { return *p; }
@@ -71,20 +76,21 @@ __device__ __forceinline__ int64_t view_col_off(const MatView &v, int j) {
 // otherwise storage rows = k and storage cols = tile rows.  VEC elements per load.  The
 // tile-row part of each address (with its integer divisions for head-split views) is fixed
 // for the whole K loop and computed once in init().
-template <typename T, bool KC, int VEC>
+template <typename T, bool KC, int VEC, int ROWS, int BK>
 struct TileLoader {
-    static constexpr int LOADS = kBM * kBK / VEC / kThreads;  // per thread
+    static constexpr int LOADS = ROWS * BK / VEC / kThreads;  // per thread
+    static_assert(LOADS >= 1 && LOADS * VEC * kThreads == ROWS * BK, "tile does not split over the workgroup");
     floatx4 reg[LOADS];
     int64_t rpart[LOADS];  // offset of this load's tile row; -1 when the row is out of range
 
     __device__ __forceinline__ static void coords(int tid, int i, int &r, int &kk) {
         const int e = (tid + i * kThreads) * VEC;  // element index in the tile, storage-row-major
-        if (KC) {  // storage [row][k]: 16 k per row
-            r = e / kBK;
-            kk = e % kBK;
-        } else {  // storage [k][row]: 128 rows per k
-            kk = e / kBM;
-            r = e % kBM;
+        if (KC) {  // storage [row][k]: BK k per row
+            r = e / BK;
+            kk = e % BK;
+        } else {  // storage [k][row]: ROWS rows per k
+            kk = e / ROWS;
+            r = e % ROWS;
         }
     }
 
@@ -115,22 +121,23 @@ struct TileLoader {
         }
     }
 
-    // LDS layouts: KC -> [row][KS] with KS = 20 (float4-aligned, conflict-light float4 reads);
-    // !KC -> [k][MS] with MS = 132.
-    static constexpr int KS = kBK + 4;
-    static constexpr int MS = kBM + 4;
-    static constexpr int LDS_FLOATS = KC ? kBM * KS : kBK * MS;
+    // LDS layouts: KC -> [row][KS] with KS = BK + 4 (float4-aligned; the 16 lanes of a
+    // float4 read hit 16 distinct 4-bank groups for BK = 16, 32, 64); !KC -> [k][MS] with
+    // MS = ROWS + 4.
+    static constexpr int KS = BK + 4;
+    static constexpr int MS = ROWS + 4;
+    static constexpr int LDS_FLOATS = KC ? ROWS * KS : BK * MS;
 
     __device__ __forceinline__ void store(float *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const int e = (tid + i * kThreads) * VEC;
             if (KC) {
-                const int r = e / kBK, kk = e % kBK;
+                const int r = e / BK, kk = e % BK;
                 if (VEC == 4) *reinterpret_cast<floatx4 *>(lds + r * KS + kk) = reg[i];
                 else lds[r * KS + kk] = reg[i][0];
             } else {
-                const int kk = e / kBM, r = e % kBM;
+                const int kk = e / ROWS, r = e % ROWS;
                 if (VEC == 4) *reinterpret_cast<floatx4 *>(lds + kk * MS + r) = reg[i];
                 else lds[kk * MS + r] = reg[i][0];
             }
@@ -147,10 +154,12 @@ struct TileLoader {
     }
 };
 
-template <typename T, bool A_KC, bool B_KC, int VEC>
+template <typename T, bool A_KC, bool B_KC, int VEC, int BM, int BN, int BK>
 __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
-    using LA = TileLoader<T, A_KC, VEC>;
-    using LB = TileLoader<T, B_KC, VEC>;
+    using LA = TileLoader<T, A_KC, VEC, BM, BK>;
+    using LB = TileLoader<T, B_KC, VEC, BN, BK>;
+    constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 MFMA tiles per wave along M and N
+    constexpr int WM = BM / 2, WN = BN / 2;    // the wave's block of out
     __shared__ __attribute__((aligned(16))) float a_lds[2][LA::LDS_FLOATS];
     __shared__ __attribute__((aligned(16))) float b_lds[2][LB::LDS_FLOATS];
 
@@ -161,24 +170,24 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
     const int half = lane >> 5;
     const int wm = wave & 1, wn = wave >> 1;
 
-    const int m0 = blockIdx.x * kBM;
-    const int n0 = blockIdx.y * kBN;
+    const int m0 = blockIdx.x * BM;
+    const int n0 = blockIdx.y * BN;
     const int batch = blockIdx.z / prm.splits;
     const int split = blockIdx.z % prm.splits;
     const GemmBatch &bt = prm.batch[batch];
 
     // Flat list of K steps over the segments: step st -> segment st / nks, k0 = (st % nks) * BK.
-    const int nks = (prm.K + kBK - 1) / kBK;
+    const int nks = (prm.K + BK - 1) / BK;
     const int total = bt.nseg * nks;
     const int per = (total + prm.splits - 1) / prm.splits;
     const int st_begin = split * per;
     const int st_end = min(total, st_begin + per);
 
-    floatx16 acc[2][2];
+    floatx16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = zero16();
+        for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
 
     // Every segment's views share their kind and shape (only the base pointer differs), so
     // the row parts computed from segment 0 hold for all of them.
@@ -188,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
     lb.init(bt.b[0], n0, prm.N, tid);
     auto load_step = [&](int st) {
         const int seg = st / nks;
-        const int k0 = (st % nks) * kBK;
+        const int k0 = (st % nks) * BK;
         la.load(bt.a[seg], k0, prm.K, tid);
         lb.load(bt.b[seg], k0, prm.K, tid);
     };
@@ -203,18 +212,18 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
         __syncthreads();
         if (st + 1 < st_end) load_step(st + 1);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            floatx4 a4[2], b4[2];
+        for (int s = 0; s < BK / 8; ++s) {
+            floatx4 a4[TM], b4[TN];
 #pragma unroll
-            for (int tm = 0; tm < 2; ++tm) a4[tm] = LA::fetch(a_lds[buf], wm * 64 + tm * 32 + col, s, half);
+            for (int tm = 0; tm < TM; ++tm) a4[tm] = LA::fetch(a_lds[buf], wm * WM + tm * 32 + col, s, half);
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn) b4[tn] = LB::fetch(b_lds[buf], wn * 64 + tn * 32 + col, s, half);
+            for (int tn = 0; tn < TN; ++tn) b4[tn] = LB::fetch(b_lds[buf], wn * WN + tn * 32 + col, s, half);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int tm = 0; tm < 2; ++tm)
+                for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-                    for (int tn = 0; tn < 2; ++tn)
+                    for (int tn = 0; tn < TN; ++tn)
                         acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[tm][t], b4[tn][t], acc[tm][tn], 0, 0, 0);
         }
     }
@@ -225,14 +234,14 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
     if (prm.splits > 1) {
         float *ws = prm.ws + int64_t(blockIdx.z) * prm.M * prm.N;
 #pragma unroll
-        for (int tm = 0; tm < 2; ++tm)
+        for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int tn = 0; tn < 2; ++tn) {
-                const int n = n0 + wn * 64 + tn * 32 + col;
+            for (int tn = 0; tn < TN; ++tn) {
+                const int n = n0 + wn * WN + tn * 32 + col;
                 if (n >= prm.N) continue;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int m = m0 + wm * 64 + tm * 32 + acc_row(r, half);
+                    const int m = m0 + wm * WM + tm * 32 + acc_row(r, half);
                     if (m < prm.M) ws[int64_t(m) * prm.N + n] = acc[tm][tn][r];
                 }
             }
@@ -241,16 +250,16 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
     T *out = static_cast<T *>(bt.out);
     const T *bias = static_cast<const T *>(bt.bias);
 #pragma unroll
-    for (int tn = 0; tn < 2; ++tn) {
-        const int n = n0 + wn * 64 + tn * 32 + col;
+    for (int tn = 0; tn < TN; ++tn) {
+        const int n = n0 + wn * WN + tn * 32 + col;
         if (n >= prm.N) continue;
         const float bn = bias != nullptr ? load_f<T>(bias + n) : 0.f;
         const int64_t coff = view_col_off(prm.outv, n);
 #pragma unroll
-        for (int tm = 0; tm < 2; ++tm) {
+        for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + tm * 32 + acc_row(r, half);
+                const int m = m0 + wm * WM + tm * 32 + acc_row(r, half);
                 if (m >= prm.M) continue;
                 T *p = out + view_row_off(prm.outv, m) + coff;
                 float x = acc[tm][tn][r] + bn;
@@ -280,8 +289,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams prm) {
 }
 
 // Column sums, stage 1: part[rb][c] = sum of rows rb*kColRows .. +kColRows-1 of column c.
-// 256 threads = 64 columns x 4 row lanes; rows are summed in a fixed order.
-constexpr int kColRows = 256;
+// 256 threads = 64 columns x 4 row lanes, each lane 8 rows; the lanes combine in LDS in a
+// fixed order.  32-row blocks give 768 workgroups for a 4096 x 384 gradient.
+constexpr int kColRows = 32;
 template <typename T>
 __global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, int C, float *part) {
     __shared__ float red[4][64];
@@ -292,21 +302,32 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, i
     float s = 0.f;
     if (c < C) {
         const int64_t coff = view_col_off(g, c);
-        for (int r = r0 + rl; r < min(R, r0 + kColRows); r += 4) s += load_f<T>(base + view_row_off(g, r) + coff);
+        const int r1 = min(R, r0 + kColRows);
+#pragma unroll
+        for (int i = 0; i < kColRows / 4; ++i) {
+            const int r = r0 + rl + 4 * i;
+            if (r < r1) s += load_f<T>(base + view_row_off(g, r) + coff);
+        }
     }
     red[rl][cl] = s;
     __syncthreads();
     if (rl == 0 && c < C) part[int64_t(blockIdx.y) * C + c] = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
 }
 
-// Stage 2: out[c] += sum over row blocks of part[rb][c], in increasing rb.
+// Stage 2: out[c] += sum over row blocks of part[rb][c].  64 columns x 4 lanes per block;
+// lane l sums row blocks l, l+4, ... in increasing order, then the lanes add in a fixed order.
 template <typename T>
 __global__ __launch_bounds__(256) void colsum_final_kernel(const float *part, int nrb, int C, T *out) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C) return;
+    __shared__ float red[4][64];
+    const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
     float s = 0.f;
-    for (int rb = 0; rb < nrb; ++rb) s += part[int64_t(rb) * C + c];
-    store_f<T>(out + c, load_f<T>(out + c) + s);
+    if (c < C)
+        for (int rb = rl; rb < nrb; rb += 4) s += part[int64_t(rb) * C + c];
+    red[rl][cl] = s;
+    __syncthreads();
+    if (rl == 0 && c < C)
+        store_f<T>(out + c, load_f<T>(out + c) + (((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl]));
 }
 
 // params[i] -= lr * grads[i]  (headers.cu:249-275: sgdUpdateKernel / runSgdUpdate).
@@ -317,14 +338,32 @@ __global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, flo
     store_f<T>(params + i, load_f<T>(params + i) - lr * load_f<T>(grads + i));
 }
 
+template <typename T, bool A_KC, bool B_KC, int BM, int BN>
+void launch_tile(const GemmParams &prm, int nbatch, bool vec4, hipStream_t stream) {
+    constexpr int BK = 16 * (128 / BM) * (128 / BN);  // 32 MFMAs per wave per K step
+    const dim3 grid(unsigned((prm.M + BM - 1) / BM), unsigned((prm.N + BN - 1) / BN), unsigned(nbatch * prm.splits));
+    if (vec4)
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK>), grid, dim3(kThreads), 0, stream, prm);
+    else
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 1, BM, BN, BK>), grid, dim3(kThreads), 0, stream, prm);
+}
+
+// Workgroups of a BM x BN tiling of the launch.
+int64_t tile_workgroups(const GemmParams &prm, int nbatch, int bm, int bn) {
+    return int64_t((prm.M + bm - 1) / bm) * ((prm.N + bn - 1) / bn) * nbatch * prm.splits;
+}
+
 template <typename T, bool A_KC, bool B_KC>
 hipError_t launch_gemm_t(const GemmParams &prm, int nbatch, bool vec4, hipStream_t stream) {
-    const dim3 grid(unsigned((prm.M + kBM - 1) / kBM), unsigned((prm.N + kBN - 1) / kBN),
-                    unsigned(nbatch * prm.splits));
-    if (vec4)
-        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4>), grid, dim3(kThreads), 0, stream, prm);
+    // The largest tile that fills the CUs; 64 x 64 when none does.
+    if (tile_workgroups(prm, nbatch, 128, 128) >= kFillWorkgroups)
+        launch_tile<T, A_KC, B_KC, 128, 128>(prm, nbatch, vec4, stream);
+    else if (prm.M >= prm.N && tile_workgroups(prm, nbatch, 128, 64) >= kFillWorkgroups)
+        launch_tile<T, A_KC, B_KC, 128, 64>(prm, nbatch, vec4, stream);
+    else if (prm.M < prm.N && tile_workgroups(prm, nbatch, 64, 128) >= kFillWorkgroups)
+        launch_tile<T, A_KC, B_KC, 64, 128>(prm, nbatch, vec4, stream);
     else
-        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 1>), grid, dim3(kThreads), 0, stream, prm);
+        launch_tile<T, A_KC, B_KC, 64, 64>(prm, nbatch, vec4, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || prm.splits == 1) return e;
     const int64_t mn = int64_t(prm.M) * prm.N;
@@ -344,8 +383,8 @@ hipError_t launch_gemm_dt(const GemmParams &prm, int nbatch, bool a_kc, bool b_k
 
 }  // namespace
 
-int gemm_tile_count(int64_t M, int64_t N) { return int(((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN)); }
-int gemm_k_steps(int64_t K) { return int((K + kBK - 1) / kBK); }
+int gemm_tile_count(int64_t M, int64_t N) { return int(((M + 127) / 128) * ((N + 127) / 128)); }
+int gemm_k_steps(int64_t K) { return int((K + 15) / 16); }
 
 hipError_t launch_proj_gemm(int dtype, const GemmParams &prm, int nbatch, bool a_kc, bool b_kc,
                             bool vec4, hipStream_t stream) {
@@ -360,6 +399,7 @@ hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *ou
                              hipStream_t stream) {
     if (R <= 0 || C <= 0) return hipSuccess;
     const int nrb = (R + kColRows - 1) / kColRows;
+    if (nrb > 65535) return hipErrorInvalidValue;  // grid.y limit: at most 2^21 - 32 rows
     const dim3 grid1(unsigned((C + 63) / 64), unsigned(nrb));
     if (dtype == 0)
         hipLaunchKernelGGL(colsum_partial_kernel<float>, grid1, dim3(256), 0, stream, g, R, C, ws);
@@ -367,7 +407,7 @@ hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *ou
         hipLaunchKernelGGL(colsum_partial_kernel<uint16_t>, grid1, dim3(256), 0, stream, g, R, C, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid2(unsigned((C + 255) / 256));
+    const dim3 grid2(unsigned((C + 63) / 64));
     if (dtype == 0)
         hipLaunchKernelGGL(colsum_final_kernel<float>, grid2, dim3(256), 0, stream, ws, nrb, C, static_cast<float *>(out));
     else

@@ -91,6 +91,9 @@ class NanoGPT(nn.Module):
         super().__init__()
         if attention not in ("ctattn", "sdpa"):
             raise ValueError("attention must be 'ctattn' or 'sdpa'")
+        self.config = dict(vocab=vocab, max_seq_len=max_seq_len, d_model=d_model, n_heads=n_heads,
+                           head_dim=head_dim, mlp_dim=mlp_dim, n_layers=n_layers, causal=causal,
+                           activation=activation)
         self.tok = nn.Embedding(vocab, d_model)
         self.pos = nn.Embedding(max_seq_len, d_model)
         self.blocks = nn.ModuleList(
@@ -121,6 +124,48 @@ class NanoGPT(nn.Module):
     def loss(self, ids, targets):
         logits = self.forward(ids)
         return F.cross_entropy(logits.reshape(-1, logits.shape[-1]), targets.reshape(-1))
+
+
+_NATIVE_PARTS = {
+    ("ln1",): "firstNorm", ("ln2",): "secondNorm",
+    ("attn", "q"): "attention.query", ("attn", "k"): "attention.key",
+    ("attn", "v"): "attention.value", ("attn", "o"): "attention.output",
+    ("fc1",): "mlp.layer_0", ("fc2",): "mlp.layer_2",
+}
+_NATIVE_FIXED = {"tok.weight": "tokenEmbedding", "pos.weight": "positionEmbedding", "unembed.weight": "unEmbedding"}
+
+
+def native_parameter_name(name: str, checkpoint_gap: int = 0) -> str:
+    """Name of a parameter of this module in the native model's (and the reference's)
+    parameter map: "tokenEmbedding", "positionEmbedding", "unEmbedding" and
+    "layer_<slot>.<sub-layer>.<weights|biases>" (TransformerLayer.cu:167-215,
+    TransformerBlockLayer.cu:119-145, MLPLayer.cu:105-118), where slot counts the
+    CheckpointLayer the reference inserts before every checkpoint_gap-th block."""
+    if name in _NATIVE_FIXED:
+        return _NATIVE_FIXED[name]
+    _, i, *rest = name.split(".")
+    i = int(i)
+    slot = i + (i // checkpoint_gap if checkpoint_gap else 0)
+    leaf = {"weight": "weights", "bias": "biases"}[rest[-1]]
+    return f"layer_{slot}.{_NATIVE_PARTS[tuple(rest[:-1])]}.{leaf}"
+
+
+_NATIVE_ACT = {"relu": "ReLU", "gelu": "GELU", "sigmoid": "Sigmoid", "tanh": "Tanh"}
+
+
+def to_native(model: "NanoGPT", checkpoint_gap: int = 0, temperature: float = 1.0):
+    """A cuda_transformer.FloatNanoGPT with this module's configuration and weights."""
+    from . import cuda_transformer as ctm
+
+    c = model.config
+    nat = ctm.FloatNanoGPT(c["vocab"], c["max_seq_len"], c["d_model"], c["n_heads"], c["head_dim"], c["mlp_dim"],
+                           c["n_layers"], checkpoint_gap=checkpoint_gap, temperature=temperature,
+                           activation_type=getattr(ctm.ActivationType, _NATIVE_ACT[c["activation"]]),
+                           causal=c["causal"])
+    nat.setParameters({native_parameter_name(n, checkpoint_gap):
+                       ctm.FloatTensor.fromNumpy(p.detach().double().cpu().numpy())
+                       for n, p in model.named_parameters()})
+    return nat
 
 
 def make_batch(batch, seq_len, vocab, seed: int):

@@ -15,29 +15,14 @@ import torch
 
 import cudatransformer_amd  # noqa: F401  (torch first, then the native libraries)
 from cudatransformer_amd import cuda_transformer as ctm
-from cudatransformer_amd.nanogpt import NanoGPT, make_batch
+from cudatransformer_amd.nanogpt import NanoGPT, make_batch, native_parameter_name, to_native
 
 TINY = dict(vocab=17, max_seq_len=32, d_model=32, n_heads=2, head_dim=16, mlp_dim=64, n_layers=2)
 ACT = {"relu": "ReLU", "gelu": "GELU", "sigmoid": "Sigmoid", "tanh": "Tanh"}
 
 
 def native_key(name: str, gap: int = 0) -> str:
-    """torch parameter name -> native (reference) parameter key."""
-    fixed = {"tok.weight": "tokenEmbedding", "pos.weight": "positionEmbedding", "unembed.weight": "unEmbedding"}
-    if name in fixed:
-        return fixed[name]
-    _, i, *rest = name.split(".")
-    i = int(i)
-    slot = i + (i // gap if gap else 0)
-    leaf = {"weight": "weights", "bias": "biases"}[rest[-1]]
-    sub = rest[:-1]
-    part = {
-        ("ln1",): "firstNorm", ("ln2",): "secondNorm",
-        ("attn", "q"): "attention.query", ("attn", "k"): "attention.key",
-        ("attn", "v"): "attention.value", ("attn", "o"): "attention.output",
-        ("fc1",): "mlp.layer_0", ("fc2",): "mlp.layer_2",
-    }[tuple(sub)]
-    return f"layer_{slot}.{part}.{leaf}"
+    return native_parameter_name(name, gap)
 
 
 def test_api_surface():
@@ -74,11 +59,8 @@ def test_no_gpu_raises_runtime_error():
 
 def build_pair(seed=7, causal=True, activation="gelu", gap=0):
     ref = NanoGPT(**TINY, causal=causal, activation=activation, attention="sdpa").init_weights(seed).double()
-    nat = ctm.FloatNanoGPT(TINY["vocab"], TINY["max_seq_len"], TINY["d_model"], TINY["n_heads"], TINY["head_dim"],
-                           TINY["mlp_dim"], TINY["n_layers"], checkpoint_gap=gap,
-                           activation_type=getattr(ctm.ActivationType, ACT[activation]), causal=causal)
-    nat.setParameters({native_key(n, gap): ctm.FloatTensor.fromNumpy(p.detach().numpy())
-                       for n, p in ref.named_parameters()})
+    nat = to_native(ref, checkpoint_gap=gap)
+    assert nat.activationType() == getattr(ctm.ActivationType, ACT[activation]) and nat.causal() == causal
     return ref, nat
 
 
@@ -90,12 +72,17 @@ def ref_step(ref, ids, tgt):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("causal,activation,gap", [(True, "gelu", 0), (False, "relu", 0), (True, "tanh", 1)])
-def test_step_matches_fp64_reference(causal, activation, gap):
-    print(f"native nanogpt causal={causal} act={activation} gap={gap}", flush=True)
+@pytest.mark.parametrize("causal,activation,gap,id_tensor", [(True, "gelu", 0, True), (True, "gelu", 0, False),
+                                                            (False, "relu", 0, True), (True, "tanh", 1, False)])
+def test_step_matches_fp64_reference(causal, activation, gap, id_tensor):
+    """id_tensor: the ids go in as one IntTensor, so backward reuses the activations forward
+    kept; otherwise as NumPy arrays (a new device tensor per call), so backward recomputes."""
+    print(f"native nanogpt causal={causal} act={activation} gap={gap} id_tensor={id_tensor}", flush=True)
     ref, nat = build_pair(causal=causal, activation=activation, gap=gap)
     ids, tgt = make_batch(4, 32, TINY["vocab"], seed=5)
     ids_np, tgt_np = ids.numpy().astype(np.int32), tgt.numpy().astype(np.int32)
+    if id_tensor:
+        ids_np, tgt_np = ctm.IntTensor.fromNumpy(ids_np), ctm.IntTensor.fromNumpy(tgt_np)
 
     params = nat.getParameters()
     assert set(params) == {native_key(n, gap) for n, _ in ref.named_parameters()}
@@ -151,6 +138,26 @@ def test_backward_without_checkpoint_recomputes():
     nat.backward(ids_np, probs, tgt_np)
     for k, v in nat.getGradients().items():
         np.testing.assert_allclose(v.numpy(), with_ckpt[k], rtol=1e-5, atol=1e-8)
+
+
+@pytest.mark.gpu
+def test_kept_activations_match_recompute():
+    """backward on the forward's own ids tensor (kept activations) and after clear()
+    (everything recomputed from the ids) give the same gradients."""
+    _, nat = build_pair(seed=8)
+    ids, tgt = make_batch(4, 32, TINY["vocab"], seed=10)
+    ids = ctm.IntTensor.fromNumpy(ids.numpy().astype(np.int32))
+    tgt = ctm.IntTensor.fromNumpy(tgt.numpy().astype(np.int32))
+    grads = []
+    for drop in (False, True):
+        probs = nat.forward(ids)
+        if drop:
+            nat.clear()
+        nat.zeroGrad()
+        nat.backward(ids, probs, tgt)
+        grads.append({k: v.numpy().copy() for k, v in nat.getGradients().items()})
+    for k, v in grads[0].items():
+        np.testing.assert_allclose(grads[1][k], v, rtol=1e-5, atol=1e-6 * max(np.abs(v).max(), 1e-30), err_msg=k)
 
 
 @pytest.mark.gpu
