@@ -18,9 +18,9 @@
 // each wave a (BM/2) x (BN/2) block of 32x32 MFMA tiles, over K in steps of BK.  The tile
 // configurations are 128 x 128 x 16, 128 x 64 x 32, 64 x 128 x 32 and 64 x 64 x 64: each
 // gives a wave 32 MFMAs (2048 cycles) per K step, so smaller tiles wait on their global
-// loads as rarely as the large one.  The launch takes the largest tile that still gives at
-// least one workgroup per CU (256): the 4096 x 384 products of a d384 model run 64 x 64,
-// the large ones 128 x 128.  Operand tiles are staged global ->
+// loads as rarely as the large one.  choose_tile() picks one by a makespan model (rounds of
+// 256 workgroups x tile area / measured tile efficiency): the 4096 x 384 products of a d384
+// model run 64 x 64, 4096 x 1536 runs 64 x 128, the E = 1024 layer 128 x 128.  Operand tiles are staged global ->
 // registers -> LDS (double-buffered, one barrier per step; the next step's global loads are
 // in flight during this step's MFMAs).  A K-contiguous operand is stored [row][k] in LDS
 // and read as float4 along k; an M/N-contiguous one is stored [k][row] and read per element
@@ -32,6 +32,8 @@
 // tiles go to a workspace and a second kernel adds them in a fixed order (deterministic,
 // no atomics).  Bias gradients are column sums, also two-stage and deterministic.
 #include "proj_launch.h"
+
+#include <type_traits>
 
 #include "attn_common.h"
 #include "attn_mfma_common.h"
@@ -103,6 +105,30 @@ struct TileLoader {
         }
     }
 
+    // Fast path (row-major views, fp32, VEC = 4, K a multiple of BK): each lane's vector sits
+    // at a fixed byte offset from the workgroup's tile origin, which moves by a uniform
+    // amount per K step, so a load needs no address arithmetic, bounds test or zero fill.
+    // Rows past the matrix are clamped to its last row (vector); their results are never
+    // stored.  Offsets are 32-bit: the host requires ld < 2^21 elements.
+    uint32_t loff[LOADS];
+
+    __device__ __forceinline__ void init_fast(int64_t ld, int row0, int nrows, int tid) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            int r, kk;
+            coords(tid, i, r, kk);
+            const int rc = min(row0 + r, nrows - (KC ? 1 : VEC)) - row0;
+            loff[i] = uint32_t((KC ? int64_t(rc) * ld + kk : int64_t(kk) * ld + rc) * int64_t(sizeof(T)));
+        }
+    }
+
+    // `origin`: element (row0, k0) of the operand.
+    __device__ __forceinline__ void load_fast(const T *origin) {
+        const char *o = reinterpret_cast<const char *>(origin);
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) reg[i] = *reinterpret_cast<const floatx4 *>(o + loff[i]);
+    }
+
     // VEC = 4: KC -> 4 consecutive k of one row; !KC -> 4 consecutive rows of one k.  Callers
     // guarantee every extent is a multiple of 4, so a vector is wholly in or out of range.
     __device__ __forceinline__ void load(const MatView &v, int k0, int kend, int tid) {
@@ -154,8 +180,9 @@ struct TileLoader {
     }
 };
 
-template <typename T, bool A_KC, bool B_KC, int VEC, int BM, int BN, int BK>
+template <typename T, bool A_KC, bool B_KC, int VEC, int BM, int BN, int BK, bool FAST>
 __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
+    static_assert(!FAST || (VEC == 4 && std::is_same_v<T, float>), "the fast path is fp32 with vector loads");
     using LA = TileLoader<T, A_KC, VEC, BM, BK>;
     using LB = TileLoader<T, B_KC, VEC, BN, BK>;
     constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 MFMA tiles per wave along M and N
@@ -193,13 +220,27 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
     // the row parts computed from segment 0 hold for all of them.
     LA la;
     LB lb;
-    la.init(bt.a[0], m0, prm.M, tid);
-    lb.init(bt.b[0], n0, prm.N, tid);
+    if constexpr (FAST) {
+        la.init_fast(bt.a[0].ld, m0, prm.M, tid);
+        lb.init_fast(bt.b[0].ld, n0, prm.N, tid);
+    } else {
+        la.init(bt.a[0], m0, prm.M, tid);
+        lb.init(bt.b[0], n0, prm.N, tid);
+    }
     auto load_step = [&](int st) {
         const int seg = st / nks;
         const int k0 = (st % nks) * BK;
-        la.load(bt.a[seg], k0, prm.K, tid);
-        lb.load(bt.b[seg], k0, prm.K, tid);
+        if constexpr (FAST) {
+            // Tile origins: A(m0, k0), B(k0, n0) in their storage layouts.
+            const MatView &va = bt.a[seg], &vb = bt.b[seg];
+            const T *pa = static_cast<const T *>(va.p) + (A_KC ? int64_t(m0) * va.ld + k0 : int64_t(k0) * va.ld + m0);
+            const T *pb = static_cast<const T *>(vb.p) + (B_KC ? int64_t(n0) * vb.ld + k0 : int64_t(k0) * vb.ld + n0);
+            la.load_fast(pa);
+            lb.load_fast(pb);
+        } else {
+            la.load(bt.a[seg], k0, prm.K, tid);
+            lb.load(bt.b[seg], k0, prm.K, tid);
+        }
     };
 
     if (st_begin < st_end) load_step(st_begin);
@@ -338,14 +379,33 @@ __global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, flo
     store_f<T>(params + i, load_f<T>(params + i) - lr * load_f<T>(grads + i));
 }
 
+// The fast load path applies when every operand view is row-major with a pitch below 2^21
+// elements (32-bit lane offsets), loads are vectors, storage is fp32 and K is a multiple of
+// the K step (no K tail).
+bool fast_path_ok(const GemmParams &prm, int nbatch, bool vec4, int bk, bool fp32) {
+    if (!fp32 || !vec4 || prm.K % bk != 0) return false;
+    for (int z = 0; z < nbatch; ++z)
+        for (int sg = 0; sg < prm.batch[z].nseg; ++sg)
+            for (const MatView *v : {&prm.batch[z].a[sg], &prm.batch[z].b[sg]})
+                if (v->kind != kViewLinear || v->ld >= (int64_t(1) << 21)) return false;
+    return true;
+}
+
 template <typename T, bool A_KC, bool B_KC, int BM, int BN>
 void launch_tile(const GemmParams &prm, int nbatch, bool vec4, hipStream_t stream) {
     constexpr int BK = 16 * (128 / BM) * (128 / BN);  // 32 MFMAs per wave per K step
     const dim3 grid(unsigned((prm.M + BM - 1) / BM), unsigned((prm.N + BN - 1) / BN), unsigned(nbatch * prm.splits));
+    if constexpr (std::is_same_v<T, float>) {
+        if (fast_path_ok(prm, nbatch, vec4, BK, true)) {
+            hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK, true>), grid, dim3(kThreads), 0, stream,
+                               prm);
+            return;
+        }
+    }
     if (vec4)
-        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK>), grid, dim3(kThreads), 0, stream, prm);
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK, false>), grid, dim3(kThreads), 0, stream, prm);
     else
-        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 1, BM, BN, BK>), grid, dim3(kThreads), 0, stream, prm);
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 1, BM, BN, BK, false>), grid, dim3(kThreads), 0, stream, prm);
 }
 
 // Workgroups of a BM x BN tiling of the launch.
@@ -353,17 +413,40 @@ int64_t tile_workgroups(const GemmParams &prm, int nbatch, int bm, int bn) {
     return int64_t((prm.M + bm - 1) / bm) * ((prm.N + bn - 1) / bn) * nbatch * prm.splits;
 }
 
+// Tile choice by a makespan model: the CUs take workgroups in rounds of kFillWorkgroups, a
+// round costs the tile's area over its relative MFMA efficiency (measured on MI355X at
+// 8192 x 1024 x 1024: 64 x 128 and 128 x 64 tiles run at 0.963 and 0.955 of 128 x 128, 64 x 64
+// at 0.915).  Ties keep the larger tile.  Returns 0: 128 x 128, 1: 64 x 128, 2: 128 x 64,
+// 3: 64 x 64.  At the 4096 x {384, 1152, 1536} products this picks within 8% of the fastest
+// tile measured, where "largest tile that fills the CUs" lost up to 27%.
+int choose_tile(const GemmParams &prm, int nbatch) {
+    struct Cand {
+        int bm, bn;
+        double eff;
+    };
+    static constexpr Cand cands[4] = {{128, 128, 1.0}, {64, 128, 0.963}, {128, 64, 0.955}, {64, 64, 0.915}};
+    int best = 0;
+    double best_cost = 0.0;
+    for (int c = 0; c < 4; ++c) {
+        const int64_t rounds = (tile_workgroups(prm, nbatch, cands[c].bm, cands[c].bn) + kFillWorkgroups - 1) /
+                               kFillWorkgroups;
+        const double cost = double(rounds) * cands[c].bm * cands[c].bn / cands[c].eff;
+        if (c == 0 || cost < best_cost * 0.999) {
+            best = c;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
 template <typename T, bool A_KC, bool B_KC>
 hipError_t launch_gemm_t(const GemmParams &prm, int nbatch, bool vec4, hipStream_t stream) {
-    // The largest tile that fills the CUs; 64 x 64 when none does.
-    if (tile_workgroups(prm, nbatch, 128, 128) >= kFillWorkgroups)
-        launch_tile<T, A_KC, B_KC, 128, 128>(prm, nbatch, vec4, stream);
-    else if (prm.M >= prm.N && tile_workgroups(prm, nbatch, 128, 64) >= kFillWorkgroups)
-        launch_tile<T, A_KC, B_KC, 128, 64>(prm, nbatch, vec4, stream);
-    else if (prm.M < prm.N && tile_workgroups(prm, nbatch, 64, 128) >= kFillWorkgroups)
-        launch_tile<T, A_KC, B_KC, 64, 128>(prm, nbatch, vec4, stream);
-    else
-        launch_tile<T, A_KC, B_KC, 64, 64>(prm, nbatch, vec4, stream);
+    switch (choose_tile(prm, nbatch)) {
+        case 0: launch_tile<T, A_KC, B_KC, 128, 128>(prm, nbatch, vec4, stream); break;
+        case 1: launch_tile<T, A_KC, B_KC, 64, 128>(prm, nbatch, vec4, stream); break;
+        case 2: launch_tile<T, A_KC, B_KC, 128, 64>(prm, nbatch, vec4, stream); break;
+        default: launch_tile<T, A_KC, B_KC, 64, 64>(prm, nbatch, vec4, stream); break;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || prm.splits == 1) return e;
     const int64_t mn = int64_t(prm.M) * prm.N;
