@@ -93,6 +93,8 @@ def load() -> ctypes.CDLL:
         "ctattn_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
         "ctattn_softmax_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, f32, vp], c_int),
         "ctattn_adam_update": ([c_int, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, i64, c_int, vp], c_int),
+        "ctattn_adam_update_multi": ([c_int, vp, vp, vp, vp, vp, f32, f32, f32, f32, f32, i64, c_int, vp], c_int),
+        "ctattn_zero_multi": ([c_int, vp, vp, vp], c_int),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -509,3 +511,36 @@ def adam_update(param, grad, m, v, step: int, lr=1e-3, beta1=0.9, beta2=0.999, e
                                    float(beta2), float(eps), float(weight_decay), int(step), int(bool(decoupled)),
                                    _stream_handle(stream))
     _check(rc, "ctattn_adam_update")
+
+
+def _ptr_table(ts):
+    arr = (ctypes.c_void_p * max(len(ts), 1))()
+    for i, t in enumerate(ts):
+        arr[i] = None if t is None else t.data_ptr()
+    return arr
+
+
+def adam_update_multi(params, grads, ms, vs, step: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
+                      weight_decay=0.0, decoupled: bool = False, stream=None):
+    """ctattn_adam_update over lists of fp32 tensors, one launch per 32 tensors."""
+    if not (len(params) == len(grads) == len(ms) == len(vs)):
+        raise ValueError("adam_update_multi: list lengths differ")
+    for group in zip(params, grads, ms, vs):
+        _check_dev("adam_update_multi", torch.float32, *group)
+        if len({t.numel() for t in group}) != 1:
+            raise ValueError("adam_update_multi: size mismatch")
+    n = (ctypes.c_int64 * max(len(params), 1))(*[p.numel() for p in params])
+    rc = load().ctattn_adam_update_multi(len(params), _ptr_table(params), _ptr_table(grads), _ptr_table(ms),
+                                         _ptr_table(vs), n, float(lr), float(beta1), float(beta2), float(eps),
+                                         float(weight_decay), int(step), int(bool(decoupled)), _stream_handle(stream))
+    _check(rc, "ctattn_adam_update_multi")
+
+
+def zero_multi(tensors, stream=None):
+    """Zeroes a list of device tensors in one launch per 32 tensors."""
+    for t in tensors:
+        if not t.is_cuda or not t.is_contiguous():
+            raise ValueError("zero_multi: tensors must be contiguous on the GPU")
+    nb = (ctypes.c_int64 * max(len(tensors), 1))(*[t.numel() * t.element_size() for t in tensors])
+    rc = load().ctattn_zero_multi(len(tensors), _ptr_table(tensors), nb, _stream_handle(stream))
+    _check(rc, "ctattn_zero_multi")

@@ -611,8 +611,8 @@ private:
 };
 
 // Adam / AdamW over a parameter map (AdamOptimizer.cu:21-140 AdamOptimizer, :142-233
-// AdamWOptimizer): step(grads) updates every parameter, and throws if `grads` lacks one or
-// a size differs, as the reference does.  fp32 moments are zero at construction; the step
+// AdamWOptimizer): step(grads) updates every parameter (one launch per 32 tensors), and
+// throws if `grads` lacks one or a size differs, as the reference does.  fp32 moments are zero at construction; the step
 // counter advances once per step (the reference advances it twice).  decoupled = false is
 // the reference's AdamOptimizer (decay folded into the gradient), true its AdamWOptimizer.
 struct AdamOptimizer {
@@ -639,14 +639,22 @@ struct AdamOptimizer {
                 throw std::invalid_argument("Size mismatch between parameter '" + name + "' and its gradient.");
         }
         ++timeStep;
+        std::vector<void *> ps;
+        std::vector<const void *> gs;
+        std::vector<float *> ms, vs;
+        std::vector<int64_t> ns;
         for (const auto &[name, p] : parameters) {
             auto &mv = moments[name];
-            ctattnCheck(ctattn_adam_update(CTATTN_F32, p.get(), grads.at(name).get(), mv.first.get(), mv.second.get(),
-                                           int64_t(p.size()), float(learningRate), float(beta1), float(beta2),
-                                           float(epsilon), float(decay), timeStep, decoupled ? 1 : 0,
-                                           Runtime::stream()),
-                        "ctattn_adam_update");
+            ps.push_back(p.get());
+            gs.push_back(grads.at(name).get());
+            ms.push_back(mv.first.get());
+            vs.push_back(mv.second.get());
+            ns.push_back(int64_t(p.size()));
         }
+        ctattnCheck(ctattn_adam_update_multi(int(ps.size()), ps.data(), gs.data(), ms.data(), vs.data(), ns.data(),
+                                             float(learningRate), float(beta1), float(beta2), float(epsilon),
+                                             float(decay), timeStep, decoupled ? 1 : 0, Runtime::stream()),
+                    "ctattn_adam_update_multi");
     }
 
     double getLearningRate() const { return learningRate; }

@@ -351,11 +351,17 @@ struct NanoGPT {
         transformerLayer.clear();
     }
 
+    // Zeroes every gradient buffer in one launch per 32 buffers (allocating those that do not
+    // exist yet), instead of one fill per buffer.
     void zeroGrad() {
-        tokenEmbedding.zeroGrad();
-        positionEmbedding.zeroGrad();
-        transformerLayer.zeroGrad();
-        unEmbedding.zeroGrad();
+        std::vector<void *> ptrs;
+        std::vector<int64_t> bytes;
+        for (auto &[name, g] : getGradients()) {
+            ptrs.push_back(g.get());
+            bytes.push_back(int64_t(g.size() * sizeof(DType)));
+        }
+        ctattnCheck(ctattn_zero_multi(int(ptrs.size()), ptrs.data(), bytes.data(), Runtime::stream()),
+                    "ctattn_zero_multi");
     }
     void sgdUpdate(float lr) {
         tokenEmbedding.sgdUpdate(lr);

@@ -27,6 +27,7 @@
 
 #include <math.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace ctattn {
@@ -130,18 +131,18 @@ __global__ __launch_bounds__(256) void layernorm_bwd_part_kernel(const T *__rest
     }
 }
 
-// Stage 2: dgamma[c] += sum_chunk part[chunk][c], dbeta likewise.  64 columns x 4 lanes per
-// block; lane l takes chunks l, l+4, ... in increasing order, then the lanes add in a fixed
-// order.
+// Stage 2: dgamma[c] += sum_chunk part[chunk][c], dbeta likewise.  16 columns x 16 lanes per
+// block; lane l takes chunks l, l+16, ... in increasing order, then lane 0 adds the 16 lane
+// sums in order.
 template <typename T>
 __global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *__restrict__ part, T *__restrict__ dg,
                                                                   T *__restrict__ db, int64_t chunks, int D) {
-    __shared__ float red[2][4][64];
-    const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + cl;
+    __shared__ float red[2][16][17];
+    const int cl = threadIdx.x & 15, rl = threadIdx.x >> 4;
+    const int c = blockIdx.x * 16 + cl;
     float sg = 0.f, sb = 0.f;
     if (c < D) {
-        for (int64_t k = rl; k < chunks; k += 4) {
+        for (int64_t k = rl; k < chunks; k += 16) {
             sg += part[k * 2 * D + c];
             sb += part[k * 2 * D + D + c];
         }
@@ -150,8 +151,13 @@ __global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *
     red[1][rl][cl] = sb;
     __syncthreads();
     if (rl != 0 || c >= D) return;
-    sg = ((red[0][0][cl] + red[0][1][cl]) + red[0][2][cl]) + red[0][3][cl];
-    sb = ((red[1][0][cl] + red[1][1][cl]) + red[1][2][cl]) + red[1][3][cl];
+    sg = 0.f;
+    sb = 0.f;
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+        sg += red[0][l][cl];
+        sb += red[1][l][cl];
+    }
     if (dg != nullptr) st(dg, c, ld(dg, c) + sg);
     if (db != nullptr) st(db, c, ld(db, c) + sb);
 }
@@ -342,6 +348,69 @@ __global__ __launch_bounds__(256) void adam_kernel(float *__restrict__ param, co
     }
 }
 
+// Multi-tensor launches: up to kMultiMax tensors per launch, described in the kernel
+// arguments (no device-side table).  Each workgroup takes one kMultiChunk-element chunk of one
+// tensor; chunk_begin[i] is the first chunk of tensor i (chunk_begin[count] = total).
+constexpr int kMultiMax = 32;
+constexpr int kMultiChunk = 4096;  // elements per workgroup: 256 threads x 16
+
+struct AdamMulti {
+    float *param[kMultiMax];
+    const float *grad[kMultiMax];
+    float *m[kMultiMax];
+    float *v[kMultiMax];
+    int64_t n[kMultiMax];
+    int32_t chunk_begin[kMultiMax + 1];
+    int32_t count;
+};
+
+struct ZeroMulti {
+    void *p[kMultiMax];
+    int64_t bytes[kMultiMax];
+    int32_t chunk_begin[kMultiMax + 1];  // chunks of kMultiChunk * 4 bytes
+    int32_t count;
+};
+
+// Tensor owning chunk `b` (a uniform linear scan over at most kMultiMax entries).
+__device__ __forceinline__ int multi_owner(const int32_t *chunk_begin, int count, int b) {
+    int t = 0;
+    while (t + 1 < count && chunk_begin[t + 1] <= b) ++t;
+    return t;
+}
+
+__global__ __launch_bounds__(256) void adam_multi_kernel(AdamMulti a, float lr, float b1, float b2, float eps,
+                                                        float decay, int decoupled, float c1, float c2) {
+    const int t = multi_owner(a.chunk_begin, a.count, int(blockIdx.x));
+    const int64_t base = int64_t(blockIdx.x - a.chunk_begin[t]) * kMultiChunk;
+    const int64_t end = min(a.n[t], base + kMultiChunk);
+    float *__restrict__ param = a.param[t];
+    const float *__restrict__ grad = a.grad[t];
+    float *__restrict__ m = a.m[t];
+    float *__restrict__ v = a.v[t];
+    for (int64_t i = base + threadIdx.x; i < end; i += blockDim.x) {
+        const float p = param[i];
+        const float g = decoupled ? grad[i] : grad[i] + decay * p;
+        const float mi = b1 * m[i] + (1.f - b1) * g;
+        const float vi = b2 * v[i] + (1.f - b2) * g * g;
+        m[i] = mi;
+        v[i] = vi;
+        const float upd = lr * (mi * c1) / (sqrtf(vi * c2) + eps);
+        param[i] = decoupled ? p * (1.f - lr * decay) - upd : p - upd;
+    }
+}
+
+// Zeroes whole 4-byte words; a byte tail (sizes not a multiple of 4) is cleared bytewise.
+__global__ __launch_bounds__(256) void zero_multi_kernel(ZeroMulti z) {
+    const int t = multi_owner(z.chunk_begin, z.count, int(blockIdx.x));
+    const int64_t words = z.bytes[t] / 4;
+    const int64_t base = int64_t(blockIdx.x - z.chunk_begin[t]) * kMultiChunk;
+    const int64_t end = min(words, base + kMultiChunk);
+    uint32_t *w = static_cast<uint32_t *>(z.p[t]);
+    for (int64_t i = base + threadIdx.x; i < end; i += blockDim.x) w[i] = 0u;
+    if (blockIdx.x == z.chunk_begin[t] && threadIdx.x < (z.bytes[t] & 3))
+        static_cast<unsigned char *>(z.p[t])[words * 4 + threadIdx.x] = 0;
+}
+
 unsigned grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return unsigned(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -441,7 +510,7 @@ int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void
             float *part = static_cast<float *>(workspace);
             hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 63) / 64), unsigned(chunks)),
                                dim3(256), 0, st, xt, dyt, mean, rstd, part, N, int(D));
-            hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 63) / 64)), dim3(256), 0,
+            hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 15) / 16)), dim3(256), 0,
                                st, part, static_cast<T *>(dgamma), static_cast<T *>(dbeta), chunks, int(D));
         }
         return hipGetLastError();
@@ -628,6 +697,80 @@ int ctattn_adam_update(int dtype, void *param, const void *grad, float *m, float
                        static_cast<const float *>(grad), m, v, n, lr, beta1, beta2, eps, weight_decay, decoupled ? 1 : 0,
                        c1, c2);
     return finish(fn, hipGetLastError(), st);
+}
+
+int ctattn_adam_update_multi(int count, void *const *param, const void *const *grad, float *const *m, float *const *v,
+                             const int64_t *n, float lr, float beta1, float beta2, float eps, float weight_decay,
+                             int64_t step, int decoupled, void *stream) {
+    const char *fn = "ctattn_adam_update_multi";
+    if (count < 0 || step < 1 || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps > 0.f))
+        return fail(hipErrorInvalidValue, "%s: need count >= 0, step >= 1, 0 <= beta < 1, eps > 0", fn);
+    if (count == 0) return ok();
+    if (!param || !grad || !m || !v || !n) return fail(hipErrorInvalidValue, "%s: null table", fn);
+    for (int i = 0; i < count; ++i) {
+        if (n[i] < 0) return fail(hipErrorInvalidValue, "%s: tensor %d has a negative size", fn, i);
+        if (n[i] > 0 && (!param[i] || !grad[i] || !m[i] || !v[i]))
+            return fail(hipErrorInvalidValue, "%s: null pointer for tensor %d", fn, i);
+        if ((n[i] + ctattn::kMultiChunk - 1) / ctattn::kMultiChunk > (int64_t(1) << 30))
+            return fail(hipErrorInvalidValue, "%s: tensor %d too large", fn, i);
+    }
+    const float c1 = float(1.0 / (1.0 - pow(double(beta1), double(step))));
+    const float c2 = float(1.0 / (1.0 - pow(double(beta2), double(step))));
+    hipStream_t st = as_stream(stream);
+    for (int first = 0; first < count; first += ctattn::kMultiMax) {
+        ctattn::AdamMulti a{};
+        int64_t chunks = 0;
+        for (int i = first; i < count && a.count < ctattn::kMultiMax; ++i) {
+            if (n[i] == 0) continue;
+            const int k = a.count++;
+            a.param[k] = static_cast<float *>(param[i]);
+            a.grad[k] = static_cast<const float *>(grad[i]);
+            a.m[k] = m[i];
+            a.v[k] = v[i];
+            a.n[k] = n[i];
+            a.chunk_begin[k] = int32_t(chunks);
+            chunks += (n[i] + ctattn::kMultiChunk - 1) / ctattn::kMultiChunk;
+            if (chunks > (int64_t(1) << 30)) return fail(hipErrorInvalidValue, "%s: too many elements per launch", fn);
+        }
+        if (a.count == 0) continue;
+        a.chunk_begin[a.count] = int32_t(chunks);
+        hipLaunchKernelGGL(ctattn::adam_multi_kernel, dim3(unsigned(chunks)), dim3(256), 0, st, a, lr, beta1, beta2,
+                           eps, weight_decay, decoupled ? 1 : 0, c1, c2);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return finish(fn, e, st);
+    }
+    return finish(fn, hipSuccess, st);
+}
+
+int ctattn_zero_multi(int count, void *const *ptr, const int64_t *bytes, void *stream) {
+    const char *fn = "ctattn_zero_multi";
+    if (count < 0) return fail(hipErrorInvalidValue, "%s: negative count", fn);
+    if (count == 0) return ok();
+    if (!ptr || !bytes) return fail(hipErrorInvalidValue, "%s: null table", fn);
+    for (int i = 0; i < count; ++i) {
+        if (bytes[i] < 0) return fail(hipErrorInvalidValue, "%s: buffer %d has a negative size", fn, i);
+        if (bytes[i] > 0 && !ptr[i]) return fail(hipErrorInvalidValue, "%s: null pointer for buffer %d", fn, i);
+        if (bytes[i] > 0 && (uintptr_t(ptr[i]) & 3) != 0)
+            return fail(hipErrorInvalidValue, "%s: buffer %d is not 4-byte aligned", fn, i);
+    }
+    hipStream_t st = as_stream(stream);
+    for (int first = 0; first < count; first += ctattn::kMultiMax) {
+        ctattn::ZeroMulti z{};
+        int64_t chunks = 0;
+        for (int i = first; i < count && z.count < ctattn::kMultiMax; ++i) {
+            if (bytes[i] == 0) continue;
+            const int k = z.count++;
+            z.p[k] = ptr[i];
+            z.bytes[k] = bytes[i];
+            z.chunk_begin[k] = int32_t(chunks);
+            chunks += std::max<int64_t>(1, (bytes[i] / 4 + ctattn::kMultiChunk - 1) / ctattn::kMultiChunk);
+            if (chunks > (int64_t(1) << 30)) return fail(hipErrorInvalidValue, "%s: too many bytes per launch", fn);
+        }
+        if (z.count == 0) continue;
+        z.chunk_begin[z.count] = int32_t(chunks);
+        hipLaunchKernelGGL(ctattn::zero_multi_kernel, dim3(unsigned(chunks)), dim3(256), 0, st, z);
+        if (hipError_t e = hipGetLastError(); e != hipSuccess) return finish(fn, e, st);
+    }
+    return finish(fn, hipSuccess, st);
 }
 
 }  // extern "C"

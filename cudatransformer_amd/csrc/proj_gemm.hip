@@ -105,28 +105,77 @@ struct TileLoader {
         }
     }
 
-    // Fast path (row-major views, fp32, VEC = 4, K a multiple of BK): each lane's vector sits
-    // at a fixed byte offset from the workgroup's tile origin, which moves by a uniform
-    // amount per K step, so a load needs no address arithmetic, bounds test or zero fill.
-    // Rows past the matrix are clamped to its last row (vector); their results are never
-    // stored.  Offsets are 32-bit: the host requires ld < 2^21 elements.
+    // Fast path (VEC = 4, K a multiple of BK, every K step inside one head of a head-split
+    // K-contiguous view and inside one sequence of a head-split M/N-contiguous one): each
+    // lane's vector sits at a fixed byte offset from the tile origin, which moves by a
+    // uniform amount per K step, so a load needs no address arithmetic, bounds test or zero
+    // fill.  Rows past the matrix are clamped to its last row (vector); their results are
+    // never stored.  Offsets are 32-bit; the host checks that they fit.
     uint32_t loff[LOADS];
 
-    __device__ __forceinline__ void init_fast(int64_t ld, int row0, int nrows, int tid) {
+    __device__ __forceinline__ void init_fast(const MatView &v, int row0, int nrows, int tid) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             int r, kk;
             coords(tid, i, r, kk);
-            const int rc = min(row0 + r, nrows - (KC ? 1 : VEC)) - row0;
-            loff[i] = uint32_t((KC ? int64_t(rc) * ld + kk : int64_t(kk) * ld + rc) * int64_t(sizeof(T)));
+            const int rc = min(row0 + r, nrows - (KC ? 1 : VEC));
+            // KC: storage row = tile row, column = k; else storage row = k, column = tile row.
+            const int64_t e = KC ? view_row_off(v, rc) - view_row_off(v, row0) + kk
+                                 : view_col_off(v, rc) - view_col_off(v, row0) +
+                                       int64_t(kk) * (v.kind == kViewLinear ? v.ld : int64_t(v.d));
+            loff[i] = uint32_t(e * int64_t(sizeof(T)));
         }
     }
 
-    // `origin`: element (row0, k0) of the operand.
-    __device__ __forceinline__ void load_fast(const T *origin) {
-        const char *o = reinterpret_cast<const char *>(origin);
+    // The tile origin, element (row0, k0), of the operand in the fast path, kept as a cursor
+    // that advances one K step at a time with uniform adds instead of recomputing the view's
+    // divisions: within a period (one head of a K-contiguous head-split view, one sequence
+    // of an M/N-contiguous one) the k part grows by BK * unit, crossing a period boundary
+    // adds `jump` once, and a new K segment restarts at k = 0.
+    struct Cursor {
+        int64_t row_part;  // elements: the (row0) part of the origin
+        int64_t k_part;    // elements: the (k0) part
+        int64_t unit, jump;
+        int kin, period;   // k0 within the current period; period 0 = none (row-major view)
+
+        __device__ __forceinline__ void init(const MatView &v, int row0, int k0) {
+            row_part = KC ? view_row_off(v, row0) : view_col_off(v, row0);
+            k_part = KC ? view_col_off(v, k0) : view_row_off(v, k0);
+            if (v.kind == kViewLinear) {
+                unit = KC ? 1 : v.ld;
+                jump = 0;
+                period = 0;
+                kin = 0;
+            } else {
+                unit = KC ? 1 : v.d;
+                period = KC ? v.d : v.T;
+                jump = KC ? int64_t(v.T) * v.d - v.d : (int64_t(v.H) - 1) * v.T * v.d;
+                kin = k0 % period;
+            }
+        }
+        __device__ __forceinline__ void step() {
+            k_part += BK * unit;
+            if (period != 0) {
+                kin += BK;
+                if (kin == period) {
+                    kin = 0;
+                    k_part += jump;
+                }
+            }
+        }
+        __device__ __forceinline__ void restart() {
+            k_part = 0;
+            kin = 0;
+        }
+        __device__ __forceinline__ const T *origin(const void *base) const {
+            return static_cast<const T *>(base) + row_part + k_part;
+        }
+    };
+
+    __device__ __forceinline__ void load_fast(const T *org) {
+        const char *o = reinterpret_cast<const char *>(org);
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) reg[i] = *reinterpret_cast<const floatx4 *>(o + loff[i]);
+        for (int i = 0; i < LOADS; ++i) reg[i] = load4_f<T>(reinterpret_cast<const T *>(o + loff[i]));
     }
 
     // VEC = 4: KC -> 4 consecutive k of one row; !KC -> 4 consecutive rows of one k.  Callers
@@ -182,7 +231,7 @@ struct TileLoader {
 
 template <typename T, bool A_KC, bool B_KC, int VEC, int BM, int BN, int BK, bool FAST>
 __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
-    static_assert(!FAST || (VEC == 4 && std::is_same_v<T, float>), "the fast path is fp32 with vector loads");
+    static_assert(!FAST || VEC == 4, "the fast path uses vector loads");
     using LA = TileLoader<T, A_KC, VEC, BM, BK>;
     using LB = TileLoader<T, B_KC, VEC, BN, BK>;
     constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 MFMA tiles per wave along M and N
@@ -221,23 +270,40 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmParams prm) {
     LA la;
     LB lb;
     if constexpr (FAST) {
-        la.init_fast(bt.a[0].ld, m0, prm.M, tid);
-        lb.init_fast(bt.b[0].ld, n0, prm.N, tid);
+        la.init_fast(bt.a[0], m0, prm.M, tid);
+        lb.init_fast(bt.b[0], n0, prm.N, tid);
     } else {
         la.init(bt.a[0], m0, prm.M, tid);
         lb.init(bt.b[0], n0, prm.N, tid);
     }
+    // Fast path: cursors at step st_begin; load_step is called for st_begin, st_begin + 1, ...
+    // in order and advances them.
+    typename LA::Cursor ca{};
+    typename LB::Cursor cb{};
+    int cur_seg = 0, cur_k0 = 0;
+    if constexpr (FAST) {
+        cur_seg = st_begin / nks;
+        cur_k0 = (st_begin % nks) * BK;
+        ca.init(bt.a[0], m0, cur_k0);
+        cb.init(bt.b[0], n0, cur_k0);
+    }
     auto load_step = [&](int st) {
-        const int seg = st / nks;
-        const int k0 = (st % nks) * BK;
         if constexpr (FAST) {
-            // Tile origins: A(m0, k0), B(k0, n0) in their storage layouts.
-            const MatView &va = bt.a[seg], &vb = bt.b[seg];
-            const T *pa = static_cast<const T *>(va.p) + (A_KC ? int64_t(m0) * va.ld + k0 : int64_t(k0) * va.ld + m0);
-            const T *pb = static_cast<const T *>(vb.p) + (B_KC ? int64_t(n0) * vb.ld + k0 : int64_t(k0) * vb.ld + n0);
-            la.load_fast(pa);
-            lb.load_fast(pb);
+            la.load_fast(ca.origin(bt.a[cur_seg].p));
+            lb.load_fast(cb.origin(bt.b[cur_seg].p));
+            cur_k0 += BK;
+            if (cur_k0 == prm.K) {
+                cur_k0 = 0;
+                ++cur_seg;
+                ca.restart();
+                cb.restart();
+            } else {
+                ca.step();
+                cb.step();
+            }
         } else {
+            const int seg = st / nks;
+            const int k0 = (st % nks) * BK;
             la.load(bt.a[seg], k0, prm.K, tid);
             lb.load(bt.b[seg], k0, prm.K, tid);
         }
@@ -355,20 +421,25 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, i
     if (rl == 0 && c < C) part[int64_t(blockIdx.y) * C + c] = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
 }
 
-// Stage 2: out[c] += sum over row blocks of part[rb][c].  64 columns x 4 lanes per block;
-// lane l sums row blocks l, l+4, ... in increasing order, then the lanes add in a fixed order.
+// Stage 2: out[c] += sum over row blocks of part[rb][c].  16 columns x 16 lanes per block;
+// lane l sums row blocks l, l+16, ... in increasing order, then lane 0 adds the 16 lane sums
+// in order (fixed order: deterministic).
 template <typename T>
 __global__ __launch_bounds__(256) void colsum_final_kernel(const float *part, int nrb, int C, T *out) {
-    __shared__ float red[4][64];
-    const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + cl;
+    __shared__ float red[16][17];
+    const int cl = threadIdx.x & 15, rl = threadIdx.x >> 4;
+    const int c = blockIdx.x * 16 + cl;
     float s = 0.f;
     if (c < C)
-        for (int rb = rl; rb < nrb; rb += 4) s += part[int64_t(rb) * C + c];
+        for (int rb = rl; rb < nrb; rb += 16) s += part[int64_t(rb) * C + c];
     red[rl][cl] = s;
     __syncthreads();
-    if (rl == 0 && c < C)
-        store_f<T>(out + c, load_f<T>(out + c) + (((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl]));
+    if (rl == 0 && c < C) {
+        float t = 0.f;
+#pragma unroll
+        for (int l = 0; l < 16; ++l) t += red[l][cl];
+        store_f<T>(out + c, load_f<T>(out + c) + t);
+    }
 }
 
 // params[i] -= lr * grads[i]  (headers.cu:249-275: sgdUpdateKernel / runSgdUpdate).
@@ -379,15 +450,33 @@ __global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, flo
     store_f<T>(params + i, load_f<T>(params + i) - lr * load_f<T>(grads + i));
 }
 
-// The fast load path applies when every operand view is row-major with a pitch below 2^21
-// elements (32-bit lane offsets), loads are vectors, storage is fp32 and K is a multiple of
-// the K step (no K tail).
-bool fast_path_ok(const GemmParams &prm, int nbatch, bool vec4, int bk, bool fp32) {
-    if (!fp32 || !vec4 || prm.K % bk != 0) return false;
+// Whether a view can take the fast load path as a K-contiguous (kc) or M/N-contiguous
+// operand of a tile with at most 128 rows: the lane offsets must be affine in the K step
+// (a head-split view needs every K step inside one head, kc: d % BK == 0, or inside one
+// sequence, T % BK == 0) and the largest one must fit 31 bits.
+bool fast_view_ok(const MatView &v, bool kc, int bk, int elem_bytes) {
+    int64_t max_elems;
+    if (v.kind == kViewLinear) {
+        max_elems = kc ? 127 * v.ld + bk : int64_t(bk) * v.ld + 128;
+    } else {
+        if (kc ? v.d % bk != 0 : v.T % bk != 0) return false;
+        const int64_t htd = int64_t(v.H) * v.T * v.d;
+        // 128 consecutive rows (b, t) span at most 127 / T + 2 batch slices; 128 columns
+        // (h, dd) at most 127 / d + 2 heads.
+        max_elems = kc ? (127 / v.T + 2) * htd + bk : (127 / v.d + 2) * int64_t(v.T) * v.d + int64_t(bk) * v.d;
+    }
+    return max_elems * elem_bytes < (int64_t(1) << 31);
+}
+
+// The fast load path applies when loads are vectors, K is a multiple of the K step (no K
+// tail) and every operand view qualifies.
+bool fast_path_ok(const GemmParams &prm, int nbatch, bool vec4, int bk, bool a_kc, bool b_kc, int elem_bytes) {
+    if (!vec4 || prm.K % bk != 0) return false;
     for (int z = 0; z < nbatch; ++z)
         for (int sg = 0; sg < prm.batch[z].nseg; ++sg)
-            for (const MatView *v : {&prm.batch[z].a[sg], &prm.batch[z].b[sg]})
-                if (v->kind != kViewLinear || v->ld >= (int64_t(1) << 21)) return false;
+            if (!fast_view_ok(prm.batch[z].a[sg], a_kc, bk, elem_bytes) ||
+                !fast_view_ok(prm.batch[z].b[sg], b_kc, bk, elem_bytes))
+                return false;
     return true;
 }
 
@@ -395,12 +484,9 @@ template <typename T, bool A_KC, bool B_KC, int BM, int BN>
 void launch_tile(const GemmParams &prm, int nbatch, bool vec4, hipStream_t stream) {
     constexpr int BK = 16 * (128 / BM) * (128 / BN);  // 32 MFMAs per wave per K step
     const dim3 grid(unsigned((prm.M + BM - 1) / BM), unsigned((prm.N + BN - 1) / BN), unsigned(nbatch * prm.splits));
-    if constexpr (std::is_same_v<T, float>) {
-        if (fast_path_ok(prm, nbatch, vec4, BK, true)) {
-            hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK, true>), grid, dim3(kThreads), 0, stream,
-                               prm);
-            return;
-        }
+    if (fast_path_ok(prm, nbatch, vec4, BK, A_KC, B_KC, int(sizeof(T)))) {
+        hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK, true>), grid, dim3(kThreads), 0, stream, prm);
+        return;
     }
     if (vec4)
         hipLaunchKernelGGL((proj_gemm_kernel<T, A_KC, B_KC, 4, BM, BN, BK, false>), grid, dim3(kThreads), 0, stream, prm);
@@ -490,7 +576,7 @@ hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *ou
         hipLaunchKernelGGL(colsum_partial_kernel<uint16_t>, grid1, dim3(256), 0, stream, g, R, C, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid2(unsigned((C + 63) / 64));
+    const dim3 grid2(unsigned((C + 15) / 16));
     if (dtype == 0)
         hipLaunchKernelGGL(colsum_final_kernel<float>, grid2, dim3(256), 0, stream, ws, nrb, C, static_cast<float *>(out));
     else

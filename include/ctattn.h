@@ -326,6 +326,26 @@ CTATTN_API int ctattn_adam_update(int dtype, void *param, const void *grad, floa
                                   int64_t n, float lr, float beta1, float beta2, float eps,
                                   float weight_decay, int64_t step, int decoupled, void *stream);
 
+/*
+ * ctattn_adam_update over `count` fp32 tensors in one launch per 32 tensors: tensor i has n[i]
+ * elements at param[i], grad[i], m[i], v[i] (host arrays of device pointers; the tables are
+ * copied into the launch, so they may be freed on return).  Same arithmetic as
+ * ctattn_adam_update.  No counterpart in the reference, whose AdamOptimizer::step launches one
+ * adamUpdateKernel per tensor (AdamOptimizer.cu:90); used by the optimizer classes here.
+ */
+CTATTN_API int ctattn_adam_update_multi(int count, void *const *param, const void *const *grad,
+                                        float *const *m, float *const *v, const int64_t *n,
+                                        float lr, float beta1, float beta2, float eps,
+                                        float weight_decay, int64_t step, int decoupled,
+                                        void *stream);
+
+/*
+ * Zeroes `count` device buffers (bytes[i] bytes at ptr[i], 4-byte aligned; host tables) in one
+ * launch per 32 buffers.  No counterpart in the reference (each layer's zeroGrad issues its
+ * own cudaMemset, e.g. LinearLayer.cu zeroGrad); used by NanoGPT::zeroGrad here.
+ */
+CTATTN_API int ctattn_zero_multi(int count, void *const *ptr, const int64_t *bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -299,3 +299,33 @@ def test_adam_rejects_step_zero():
     t = torch.zeros(4, device=DEV)
     with pytest.raises(RuntimeError, match="step >= 1"):
         _capi.adam_update(t, t, t.clone(), t.clone(), 0)
+
+
+def test_adam_multi_matches_single_bitwise():
+    """One launch per 32 tensors gives exactly the per-tensor update (same arithmetic)."""
+    sizes = [1, 3, 4096, 4097, 70000] + [5 + 13 * i for i in range(35)]  # 40 tensors: two launches
+    ps = [_dev(_randn((n,), 80 + i), torch.float32) for i, n in enumerate(sizes)]
+    gs = [_dev(_randn((n,), 180 + i), torch.float32) for i, n in enumerate(sizes)]
+    ms = [torch.zeros(n, device=DEV) for n in sizes]
+    vs = [torch.zeros(n, device=DEV) for n in sizes]
+    ref = [(p.clone(), m.clone(), v.clone()) for p, m, v in zip(ps, ms, vs)]
+    for decoupled in (False, True):
+        for step in (1, 2):
+            _capi.adam_update_multi(ps, gs, ms, vs, step, lr=3e-3, weight_decay=0.01, decoupled=decoupled)
+            for (p, m, v), g in zip(ref, gs):
+                _capi.adam_update(p, g, m, v, step, lr=3e-3, weight_decay=0.01, decoupled=decoupled)
+    torch.cuda.synchronize()
+    for (p, m, v), p2, m2, v2 in zip(ref, ps, ms, vs):
+        assert torch.equal(p, p2) and torch.equal(m, m2) and torch.equal(v, v2)
+
+
+def test_zero_multi_clears_exactly_the_given_bytes():
+    arena = torch.full((1 << 16,), 0xAB, dtype=torch.uint8, device=DEV)
+    spans = [(0, 4), (16, 7), (64, 4096 * 4 + 3), (40000, 1)] + [(50000 + 64 * i, 12) for i in range(34)]
+    views = [arena[o:o + n] for o, n in spans]
+    _capi.zero_multi(views)
+    torch.cuda.synchronize()
+    expect = torch.full_like(arena, 0xAB).cpu()
+    for o, n in spans:
+        expect[o:o + n] = 0
+    assert torch.equal(arena.cpu(), expect)
