@@ -20,9 +20,14 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libctattn.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "ctattn.h")
 
-F32, BF16 = 0, 1
+F32, BF16, F16, F64 = 0, 1, 2, 3
 POLICY_AUTO, POLICY_GENERIC, POLICY_DETERMINISTIC = 0, 1, 2
-_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16}
+_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.float64: F64}
+
+
+def _stat_dtype(dtype):
+    """Element type of LSE / delta for a storage dtype: float64 for float64, else float32."""
+    return torch.float64 if dtype == torch.float64 else torch.float32
 
 _lib = None
 
@@ -129,7 +134,7 @@ def _check_qkv(name, *ts):
     if ref.dim() != 4:
         raise ValueError(f"{name}: tensors must be [B, H, T, d], got {tuple(ref.shape)}")
     if ref.dtype not in _DTYPE_CODE:
-        raise ValueError(f"{name}: dtype {ref.dtype} unsupported (float32 or bfloat16)")
+        raise ValueError(f"{name}: dtype {ref.dtype} unsupported (float32, bfloat16, float16, float64)")
     for t in ts:
         if not t.is_cuda:
             raise ValueError(f"{name}: tensors must live on the GPU")
@@ -146,11 +151,12 @@ def flash_attn_fwd(q, k, v, causal: bool = False, out=None, lse=None, stream=Non
     b, h, t, d = q.shape
     if out is None:
         out = torch.empty_like(q)
+    stat = _stat_dtype(q.dtype)
     if lse is None:
-        lse = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+        lse = torch.empty((b, h, t), dtype=stat, device=q.device)
     _check_qkv("flash_attn_fwd", q, out)
-    if lse.dtype != torch.float32 or tuple(lse.shape) != (b, h, t) or not lse.is_contiguous():
-        raise ValueError("flash_attn_fwd: lse must be contiguous float32 [B, H, T]")
+    if lse.dtype != stat or tuple(lse.shape) != (b, h, t) or not lse.is_contiguous():
+        raise ValueError(f"flash_attn_fwd: lse must be contiguous {stat} [B, H, T]")
     rc = load().ctattn_fwd(_DTYPE_CODE[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
                            out.data_ptr(), lse.data_ptr(), b, h, t, d, int(bool(causal)),
                            _stream_handle(stream))
@@ -175,8 +181,9 @@ def flash_attn_bwd(q, k, v, o, do, lse, causal: bool = False, dq=None, dk=None, 
     dk = torch.empty_like(q) if dk is None else dk
     dv = torch.empty_like(q) if dv is None else dv
     _check_qkv("flash_attn_bwd", q, dq, dk, dv)
-    if lse.dtype != torch.float32 or tuple(lse.shape) != (b, h, t) or not lse.is_contiguous():
-        raise ValueError("flash_attn_bwd: lse must be contiguous float32 [B, H, T]")
+    stat = _stat_dtype(q.dtype)
+    if lse.dtype != stat or tuple(lse.shape) != (b, h, t) or not lse.is_contiguous():
+        raise ValueError(f"flash_attn_bwd: lse must be contiguous {stat} [B, H, T]")
     need = bwd_workspace_bytes(q.dtype, b, h, t, d, causal)
     if workspace is None:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)

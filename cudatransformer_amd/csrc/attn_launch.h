@@ -15,16 +15,17 @@ struct AttnShape {
     int64_t rows() const { return B * H * T; }
 };
 
-// ---- generic kernels: any 1 <= d <= 256, f32 (dtype 0) or bf16 (dtype 1) ----
+// ---- generic kernels: any 1 <= d <= 256; dtype 0 fp32, 1 bf16, 2 fp16, 3 fp64.  lse and
+// delta are fp64 for dtype 3 and fp32 otherwise. ----
 hipError_t launch_generic_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
-                              float *lse, const AttnShape &s, hipStream_t stream);
+                              void *lse, const AttnShape &s, hipStream_t stream);
 hipError_t launch_generic_bwd(int dtype, const void *q, const void *k, const void *v,
-                              const void *o, const void *dout, const float *lse, void *dq,
-                              void *dk, void *dv, float *delta, const AttnShape &s,
+                              const void *o, const void *dout, const void *lse, void *dq,
+                              void *dk, void *dv, void *delta, const AttnShape &s,
                               hipStream_t stream);
 
 // ---- shared backward preprocess: delta[row] = sum_c dO[row][c] * O[row][c] ----
-hipError_t launch_bwd_preprocess(int dtype, const void *o, const void *dout, float *delta,
+hipError_t launch_bwd_preprocess(int dtype, const void *o, const void *dout, void *delta,
                                  const AttnShape &s, hipStream_t stream);
 
 // ---- MFMA kernels (fp32 and bf16: d in {32, 64, 128}) ----

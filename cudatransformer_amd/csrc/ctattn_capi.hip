@@ -68,8 +68,9 @@ std::atomic<int> g_policy{CTATTN_POLICY_AUTO};
 
 // Validates dtype and sizes; returns 0 or an error code (message set).
 int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, int64_t d) {
-    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
-        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16 && dtype != CTATTN_F16 && dtype != CTATTN_F64)
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16, 2 = f16, 3 = f64)", fn,
+                    dtype);
     if (B < 0 || H < 0 || T < 0)
         return fail(hipErrorInvalidValue, "%s: negative size B=%lld H=%lld T=%lld", fn,
                     (long long)B, (long long)H, (long long)T);
@@ -83,19 +84,24 @@ int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, i
     return 0;
 }
 
+// fp16 and fp64 storage always run the generic kernels.
 bool use_mfma_fwd(int dtype, int64_t d) {
-    return g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::mfma_fwd_supported(dtype, d);
+    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
+           ctattn::mfma_fwd_supported(dtype, d);
 }
 bool use_mfma_bwd(int dtype, int64_t d) {
-    return g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::mfma_bwd_supported(dtype, d);
+    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
+           ctattn::mfma_bwd_supported(dtype, d);
 }
+// Bytes of one LSE / delta element: fp64 for fp64 storage, fp32 otherwise.
+int64_t stat_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : 4; }
 bool deterministic_policy() { return g_policy.load() == CTATTN_POLICY_DETERMINISTIC; }
 
 }  // namespace
 
 extern "C" {
 
-int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, float *lse,
+int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, void *lse,
                int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream) {
     if (int rc = validate_shape("ctattn_fwd", dtype, B, H, T, d)) return rc;
     const ctattn::AttnShape s{B, H, T, d, causal != 0};
@@ -103,8 +109,9 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
     if (!q || !k || !v || !o)
         return fail(hipErrorInvalidValue, "ctattn_fwd: null q/k/v/o pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = use_mfma_fwd(dtype, d) ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, lse, s, st)
-                                          : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
+    hipError_t e = use_mfma_fwd(dtype, d)
+                       ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
+                       : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
     return finish("ctattn_fwd", e, st);
 }
 
@@ -112,8 +119,8 @@ int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, i
                                    int causal) {
     if (validate_shape("ctattn_bwd_workspace_bytes", dtype, B, H, T, d)) return -1;
     const ctattn::AttnShape s{B, H, T, d, causal != 0};
-    // delta = rowsum(dO * O), fp32 [B, H, T], always first.
-    int64_t bytes = align_up(s.rows() * int64_t(sizeof(float)));
+    // delta = rowsum(dO * O), [B, H, T] (fp64 for fp64 storage, else fp32), always first.
+    int64_t bytes = align_up(s.rows() * stat_bytes(dtype));
     if (use_mfma_bwd(dtype, d))
         bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s, deterministic_policy()));
     ok();
@@ -121,7 +128,7 @@ int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, i
 }
 
 int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
-               const void *dout, const float *lse, void *dq, void *dk, void *dv,
+               const void *dout, const void *lse, void *dq, void *dk, void *dv,
                void *workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
                int64_t d, int causal, void *stream) {
     if (int rc = validate_shape("ctattn_bwd", dtype, B, H, T, d)) return rc;
@@ -136,14 +143,14 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
                     "(ctattn_bwd_workspace_bytes)",
                     (long long)workspace_bytes, (long long)need);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    float *delta = static_cast<float *>(workspace);
     hipError_t e;
     if (use_mfma_bwd(dtype, d)) {
-        void *extra = static_cast<char *>(workspace) + align_up(s.rows() * int64_t(sizeof(float)));
-        e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, lse, delta, dq, dk, dv, extra,
-                                    deterministic_policy(), s, st);
+        void *extra = static_cast<char *>(workspace) + align_up(s.rows() * stat_bytes(dtype));
+        e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, static_cast<const float *>(lse),
+                                    static_cast<float *>(workspace), dq, dk, dv, extra, deterministic_policy(), s,
+                                    st);
     } else {
-        e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, delta, s, st);
+        e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, workspace, s, st);
     }
     return finish("ctattn_bwd", e, st);
 }

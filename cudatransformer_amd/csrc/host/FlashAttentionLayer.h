@@ -15,6 +15,7 @@
 #pragma once
 
 #include <array>
+#include <type_traits>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -26,12 +27,13 @@ namespace ct {
 
 template <typename DType = float>
 struct FlashAttentionLayer {
+    using Stat = std::conditional_t<std::is_same_v<DType, double>, double, float>;  // LSE element type
     int headDim = 1;
     int numHeads = 1;
     bool causal = false;
 
     // Cached forward state (FlashAttentionLayer.cu:18-22).
-    Tensor<float> cachedLse;
+    Tensor<Stat> cachedLse;  // LSE [B, H, T]: fp64 for double, fp32 otherwise
     Tensor<DType> cachedOutput;
     int cachedBatchSize = 0;
     int cachedSequenceLength = 0;
@@ -57,7 +59,7 @@ struct FlashAttentionLayer {
         sameShape(queries, values, "values");
         const size_t B = queries.shape(0), T = queries.shape(2);
         Tensor<DType> output = Tensor<DType>::empty(queries.shape());  // fully written by the kernel
-        Tensor<float> lse = Tensor<float>::empty({B, size_t(numHeads), T});
+        Tensor<Stat> lse = Tensor<Stat>::empty({B, size_t(numHeads), T});
         ctattnCheck(ctattn_fwd(DTypeCode<DType>::value, queries.get(), keys.get(), values.get(), output.get(),
                                lse.get(), int64_t(B), numHeads, int64_t(T), headDim, causal ? 1 : 0,
                                Runtime::stream()),
@@ -80,11 +82,11 @@ struct FlashAttentionLayer {
         sameShape(queries, values, "values");
         sameShape(queries, outputGrad, "outputGrad");
         const size_t B = queries.shape(0), T = queries.shape(2);
-        Tensor<float> lse = cachedLse;
+        Tensor<Stat> lse = cachedLse;
         Tensor<DType> output = cachedOutput;
         if (lse.empty() || output.empty() || cachedBatchSize != int(B) || cachedSequenceLength != int(T)) {
             // No usable cached forward: recompute it (FlashAttentionLayer.cu:114-127).
-            lse = Tensor<float>::empty({B, size_t(numHeads), T});
+            lse = Tensor<Stat>::empty({B, size_t(numHeads), T});
             output = Tensor<DType>::empty(queries.shape());
             ctattnCheck(ctattn_fwd(DTypeCode<DType>::value, queries.get(), keys.get(), values.get(), output.get(),
                                    lse.get(), int64_t(B), numHeads, int64_t(T), headDim, causal ? 1 : 0,
@@ -109,7 +111,7 @@ struct FlashAttentionLayer {
 
     // Drops the cached forward state (FlashAttentionLayer.cu:145-149).
     void clearCache() {
-        cachedLse = Tensor<float>();
+        cachedLse = Tensor<Stat>();
         cachedOutput = Tensor<DType>();
         cachedBatchSize = 0;
         cachedSequenceLength = 0;

@@ -9,8 +9,8 @@
 // host waits only when data comes back to the CPU (numpy(), item()) or after an upload from
 // pageable memory (fromPointer()).
 //
-// DType is float or bf16 (stored as its 16-bit pattern), or int32_t for token ids.  The
-// reference's tensor algebra (Tensor.cu:290-958) is not part of this path.
+// DType is float, double, bf16 or f16 (both stored as their 16-bit patterns), or int32_t for
+// token ids.  The reference's tensor algebra (Tensor.cu:290-958) is not part of this path.
 #pragma once
 
 #include <cstdint>
@@ -21,6 +21,7 @@
 #include <numeric>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "Runtime.h"
@@ -50,17 +51,95 @@ struct bf16 {
     }
 };
 
+// IEEE binary16 storage type, converted on the host with round to nearest even (subnormals,
+// infinities and NaN included).
+struct f16 {
+    uint16_t bits = 0;
+    static f16 fromFloat(float f) {
+        uint32_t x;
+        std::memcpy(&x, &f, 4);
+        const uint32_t sign = (x >> 16) & 0x8000u;
+        uint32_t mant = x & 0x7fffffu;
+        const int exp = int((x >> 23) & 0xffu);
+        f16 h;
+        if (exp == 255) {  // inf / NaN (NaN stays quiet)
+            h.bits = uint16_t(sign | 0x7c00u | (mant ? 0x200u | (mant >> 13) : 0u));
+            return h;
+        }
+        const int e = exp - 127 + 15;
+        if (e >= 31) {
+            h.bits = uint16_t(sign | 0x7c00u);
+        } else if (e <= 0) {  // subnormal half, or zero
+            if (e < -10) {
+                h.bits = uint16_t(sign);
+            } else {
+                mant |= 0x800000u;
+                const int shift = 14 - e;
+                uint32_t v = mant >> shift;
+                const uint32_t rem = mant & ((1u << shift) - 1u), halfway = 1u << (shift - 1);
+                if (rem > halfway || (rem == halfway && (v & 1u))) ++v;
+                h.bits = uint16_t(sign | v);
+            }
+        } else {
+            uint32_t v = (uint32_t(e) << 10) | (mant >> 13);
+            const uint32_t rem = mant & 0x1fffu;
+            if (rem > 0x1000u || (rem == 0x1000u && (v & 1u))) ++v;  // a carry may reach inf: correct
+            h.bits = uint16_t(sign | v);
+        }
+        return h;
+    }
+    float toFloat() const {
+        const uint32_t sign = uint32_t(bits & 0x8000u) << 16;
+        uint32_t exp = (bits >> 10) & 0x1fu, mant = bits & 0x3ffu, u;
+        if (exp == 0) {
+            if (mant == 0) {
+                u = sign;
+            } else {  // subnormal: normalise
+                exp = 127 - 15 + 1;
+                while (!(mant & 0x400u)) {
+                    mant <<= 1;
+                    --exp;
+                }
+                u = sign | (exp << 23) | ((mant & 0x3ffu) << 13);
+            }
+        } else if (exp == 31) {
+            u = sign | 0x7f800000u | (mant << 13);
+        } else {
+            u = sign | ((exp - 15 + 127) << 23) | (mant << 13);
+        }
+        float f;
+        std::memcpy(&f, &u, 4);
+        return f;
+    }
+};
+
 template <typename DType> struct DTypeCode;
 template <> struct DTypeCode<float> { static constexpr int value = CTATTN_F32; };
 template <> struct DTypeCode<bf16> { static constexpr int value = CTATTN_BF16; };
+template <> struct DTypeCode<f16> { static constexpr int value = CTATTN_F16; };
+template <> struct DTypeCode<double> { static constexpr int value = CTATTN_F64; };
 
 template <typename DType> inline DType fromFloat(float x);
 template <> inline float fromFloat<float>(float x) { return x; }
 template <> inline bf16 fromFloat<bf16>(float x) { return bf16::fromFloat(x); }
+template <> inline f16 fromFloat<f16>(float x) { return f16::fromFloat(x); }
+template <> inline double fromFloat<double>(float x) { return double(x); }
 template <> inline int32_t fromFloat<int32_t>(float x) { return int32_t(x); }
 inline float toFloat(float x) { return x; }
 inline float toFloat(bf16 x) { return x.toFloat(); }
+inline float toFloat(f16 x) { return x.toFloat(); }
+inline float toFloat(double x) { return float(x); }
 inline float toFloat(int32_t x) { return float(x); }
+// Scalars given or returned at full precision: exact for double tensors, rounded once to the
+// storage type otherwise.
+template <typename DType> inline DType fromDouble(double x) {
+    if constexpr (std::is_same_v<DType, double>) return x;
+    else if constexpr (std::is_same_v<DType, int32_t>) return int32_t(x);
+    else return fromFloat<DType>(float(x));
+}
+inline double toDouble(double x) { return x; }
+inline double toDouble(int32_t x) { return x; }
+template <typename DType> inline double toDouble(DType x) { return double(toFloat(x)); }
 
 // Caching device allocator for the host layer's buffers.  A freed block goes to a free list
 // keyed by its rounded size and is handed out again to the next request of that size, with
@@ -204,6 +283,18 @@ public:
         }
     }
 
+    // Device values on the host in their own type (waits for the stream).
+    std::vector<DType> toHost() const {
+        std::vector<DType> raw(size_);
+        if (size_ > 0) {
+            hipCheck(hipMemcpyAsync(raw.data(), data_.get(), size_ * sizeof(DType), hipMemcpyDeviceToHost,
+                                    Runtime::stream()),
+                     "hipMemcpyAsync D2H");
+            Runtime::synchronize();
+        }
+        return raw;
+    }
+
     // Device values as floats on the host (waits for the stream).
     std::vector<float> toFloats() const {
         std::vector<DType> raw(size_);
@@ -233,9 +324,9 @@ public:
 
     // Fills every element with `value` (Tensor.cu:360).  Zero is a stream-ordered memset;
     // other values are staged on the host.
-    void fill(float value) {
+    void fill(double value) {
         if (size_ == 0) return;
-        const DType v = fromFloat<DType>(value);
+        const DType v = fromDouble<DType>(value);
         uint8_t first;
         std::memcpy(&first, &v, 1);
         bool bytewise = true;
@@ -259,9 +350,9 @@ public:
         return Tensor(data_, shape);
     }
 
-    float item() const {
+    double item() const {
         if (size_ != 1) throw std::runtime_error("Tensor is not a scalar");
-        return toFloats()[0];
+        return toDouble(toHost()[0]);
     }
 
     const std::vector<size_t> &shape() const { return shape_; }

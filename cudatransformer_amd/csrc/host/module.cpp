@@ -43,17 +43,21 @@ using namespace ct;
 
 namespace {
 
-// NumPy element type of a tensor: int32 for ids, float32 for the float and bf16 tensors.
+// NumPy element type of a tensor: int32 for ids, float64 for double, float32 for the float,
+// bf16 and f16 tensors (numpy has no bfloat16; f16 values are rounded to nearest even).
 template <typename DType>
-using NpType = std::conditional_t<std::is_same_v<DType, int32_t>, int32_t, float>;
+using NpType = std::conditional_t<std::is_same_v<DType, int32_t>, int32_t,
+                                  std::conditional_t<std::is_same_v<DType, double>, double, float>>;
+template <typename DType>
+constexpr bool kRawNumpy = std::is_same_v<DType, int32_t> || std::is_same_v<DType, double>;
 using IdArray = py::array_t<int32_t, py::array::c_style | py::array::forcecast>;
 
 template <typename DType>
 Tensor<DType> tensorFromNumpy(const py::array_t<NpType<DType>, py::array::c_style | py::array::forcecast> &arr) {
     std::vector<size_t> shape(arr.shape(), arr.shape() + arr.ndim());
     if (shape.size() > 8) throw std::invalid_argument("Tensor dimension exceeds 8");
-    if constexpr (std::is_same_v<DType, int32_t>)
-        return Tensor<int32_t>::fromPointer(shape, arr.data());
+    if constexpr (kRawNumpy<DType>)
+        return Tensor<DType>::fromPointer(shape, arr.data());
     else
         return Tensor<DType>::fromFloats(shape, arr.data());
 }
@@ -62,13 +66,9 @@ template <typename DType>
 py::array_t<NpType<DType>> tensorToNumpy(const Tensor<DType> &t) {
     std::vector<py::ssize_t> shape(t.shape().begin(), t.shape().end());
     py::array_t<NpType<DType>> out(shape);
-    if constexpr (std::is_same_v<DType, int32_t>) {
-        if (t.size() > 0) {
-            hipCheck(hipMemcpyAsync(out.mutable_data(), t.get(), t.size() * sizeof(int32_t), hipMemcpyDeviceToHost,
-                                    Runtime::stream()),
-                     "hipMemcpyAsync D2H");
-            Runtime::synchronize();
-        }
+    if constexpr (kRawNumpy<DType>) {
+        std::vector<DType> host = t.toHost();
+        if (!host.empty()) std::memcpy(out.mutable_data(), host.data(), host.size() * sizeof(DType));
     } else {
         std::vector<float> host = t.toFloats();
         if (!host.empty()) std::memcpy(out.mutable_data(), host.data(), host.size() * sizeof(float));
@@ -83,11 +83,7 @@ Tensor<int32_t> idsFrom(const py::object &o) {
 }
 
 std::vector<int32_t> idVector(const py::object &o) {
-    if (py::isinstance<Tensor<int32_t>>(o)) {
-        const Tensor<int32_t> t = o.cast<Tensor<int32_t>>();
-        std::vector<float> f = t.toFloats();
-        return std::vector<int32_t>(f.begin(), f.end());
-    }
+    if (py::isinstance<Tensor<int32_t>>(o)) return o.cast<Tensor<int32_t>>().toHost();
     IdArray a = o.cast<IdArray>();
     return std::vector<int32_t>(a.data(), a.data() + a.size());
 }
@@ -491,13 +487,21 @@ PYBIND11_MODULE(cuda_transformer, m) {
 
     declareTensor<float>(m, "Float");
     declareTensor<bf16>(m, "BFloat");
+    declareTensor<f16>(m, "Half");
+    declareTensor<double>(m, "Double");
     declareTensor<int32_t>(m, "Int");
     declareFlashAttention<float>(m, "Float");
     declareFlashAttention<bf16>(m, "BFloat");
+    declareFlashAttention<f16>(m, "Half");
+    declareFlashAttention<double>(m, "Double");
     declareModule<float>(m, "Float");
     declareModule<bf16>(m, "BFloat");
+    declareModule<f16>(m, "Half");
+    declareModule<double>(m, "Double");
     declareAttention<float>(m, "Float");
     declareAttention<bf16>(m, "BFloat");
+    declareAttention<f16>(m, "Half");
+    declareAttention<double>(m, "Double");
     declareLayers<float>(m, "Float");
     declareLayers<bf16>(m, "BFloat");
     declareFactories<float>(m, "Float");
@@ -526,6 +530,18 @@ PYBIND11_MODULE(cuda_transformer, m) {
           },
           py::arg("head_dim"), py::arg("num_heads"), py::arg("causal") = false,
           "Creates a bfloat16 FlashAttentionLayer (fp32 accumulation).");
+    m.def("FlashAttentionHalf",
+          [](int headDim, int numHeads, bool causal) {
+              return std::make_shared<FlashAttentionLayer<f16>>(headDim, numHeads, causal);
+          },
+          py::arg("head_dim"), py::arg("num_heads"), py::arg("causal") = false,
+          "Creates a float16 FlashAttentionLayer (generic kernels, fp32 accumulation).");
+    m.def("FlashAttentionDouble",
+          [](int headDim, int numHeads, bool causal) {
+              return std::make_shared<FlashAttentionLayer<double>>(headDim, numHeads, causal);
+          },
+          py::arg("head_dim"), py::arg("num_heads"), py::arg("causal") = false,
+          "Creates a float64 FlashAttentionLayer (generic kernels, fp64 arithmetic and LSE).");
     m.def("synchronize", &Runtime::synchronize, "Waits for all work queued by this module.");
     m.def("empty_cache", [] { BlockCache::instance().emptyCache(); },
           "Returns the device memory cached for reuse by this module's tensors to the driver.");

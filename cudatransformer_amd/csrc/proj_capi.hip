@@ -27,9 +27,13 @@ struct ProjShape {
     int64_t hd() const { return H * d; }
 };
 
+bool known_dtype(int dtype) {
+    return dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16 || dtype == CTATTN_F64;
+}
+
 int validate_proj(const char *fn, int dtype, const ProjShape &s) {
-    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
-        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (!known_dtype(dtype))
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16, 2 = f16, 3 = f64)", fn, dtype);
     if (s.B < 0 || s.T < 0)
         return fail(hipErrorInvalidValue, "%s: negative size B=%lld T=%lld", fn, (long long)s.B,
                     (long long)s.T);
@@ -43,7 +47,7 @@ int validate_proj(const char *fn, int dtype, const ProjShape &s) {
     return 0;
 }
 
-int elem_bytes(int dtype) { return dtype == CTATTN_F32 ? 4 : 2; }
+int elem_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : dtype == CTATTN_F32 ? 4 : 2; }
 
 // 4-element vector loads need every pitch / head dim to be a multiple of 4 and every base
 // pointer 4-element aligned.
@@ -56,16 +60,17 @@ bool vec4_ok(int dtype, const ProjShape &s, std::initializer_list<const void *> 
 }
 
 // K splits for a small-output, long-K product (weight gradients): enough workgroups to cover
-// the GPU several times, at least 16 K steps (256 k) per split.
-int choose_splits(int64_t M, int64_t N, int64_t K, int nbatch) {
+// the GPU several times, at least 16 K steps (256 k) per split.  The fp64 GEMM does not split.
+int choose_splits(int dtype, int64_t M, int64_t N, int64_t K, int nbatch) {
+    if (dtype == CTATTN_F64) return 1;
     const int64_t tiles = int64_t(ctattn::gemm_tile_count(M, N)) * nbatch;
     int64_t s = (1024 + tiles - 1) / tiles;
     s = std::min<int64_t>(s, std::max<int64_t>(1, ctattn::gemm_k_steps(K) / 16));
     return int(std::max<int64_t>(1, std::min<int64_t>(s, 16)));
 }
 
-int64_t splitk_bytes(int64_t M, int64_t N, int64_t K, int nbatch) {
-    const int s = choose_splits(M, N, K, nbatch);
+int64_t splitk_bytes(int dtype, int64_t M, int64_t N, int64_t K, int nbatch) {
+    const int s = choose_splits(dtype, M, N, K, nbatch);
     return s > 1 ? align_up(int64_t(s) * nbatch * M * N * int64_t(sizeof(float))) : 0;
 }
 
@@ -115,8 +120,8 @@ int64_t ctattn_qkv_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int
     const ProjShape s{B, T, E, H, d};
     if (validate_proj("ctattn_qkv_proj_bwd_workspace_bytes", dtype, s)) return -1;
     ok();
-    return splitk_bytes(s.hd(), E, s.rows(), 3) +
-           align_up(ctattn::colsum_workspace_floats(s.rows(), s.hd()) * int64_t(sizeof(float)));
+    return splitk_bytes(dtype, s.hd(), E, s.rows(), 3) +
+           align_up(ctattn::colsum_workspace_bytes(dtype, s.rows(), s.hd()));
 }
 
 int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk, const void *dv,
@@ -145,7 +150,7 @@ int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk
     if (want_dw) {
         // dw[j][i] += sum_r g(r, j) x[r][i]: M = HD, N = E, K = rows.  A(m=j, k=r) = g stored
         // [k][m] (head-split), B(k=r, n=i) = x stored [k][n].
-        const int splits = choose_splits(s.hd(), E, s.rows(), 3);
+        const int splits = choose_splits(dtype, s.hd(), E, s.rows(), 3);
         GemmParams p = make_params(s.hd(), E, s.rows(), 1, splits, linear_view(nullptr, E), ws);
         void *o[3] = {dwq, dwk, dwv};
         for (int z = 0; z < 3; ++z) {
@@ -159,7 +164,7 @@ int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (want_db) {
-        float *cws = reinterpret_cast<float *>(static_cast<char *>(workspace) + splitk_bytes(s.hd(), E, s.rows(), 3));
+        void *cws = static_cast<char *>(workspace) + splitk_bytes(dtype, s.hd(), E, s.rows(), 3);
         void *o[3] = {dbq, dbk, dbv};
         for (int z = 0; z < 3 && e == hipSuccess; ++z)
             e = ctattn::launch_colsum_add(dtype, head_view(g[z], T, H, d), int(s.rows()), int(s.hd()), o[z], cws, st);
@@ -205,8 +210,8 @@ int64_t ctattn_out_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int
     const ProjShape s{B, T, E, H, d};
     if (validate_proj("ctattn_out_proj_bwd_workspace_bytes", dtype, s)) return -1;
     ok();
-    return splitk_bytes(E, s.hd(), s.rows(), 1) +
-           align_up(ctattn::colsum_workspace_floats(s.rows(), E) * int64_t(sizeof(float)));
+    return splitk_bytes(dtype, E, s.hd(), s.rows(), 1) +
+           align_up(ctattn::colsum_workspace_bytes(dtype, s.rows(), E));
 }
 
 int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo, void *dwo, void *dbo,
@@ -231,7 +236,7 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
     if (dwo) {
         // dwo[e][c] += sum_r dy[r][e] attn(r, c): M = E, N = HD, K = rows.  A(m=e, k=r) = dy
         // stored [k][m]; B(k=r, n=c) = attention output stored [k][n] (head-split).
-        const int splits = choose_splits(E, s.hd(), s.rows(), 1);
+        const int splits = choose_splits(dtype, E, s.hd(), s.rows(), 1);
         GemmParams p = make_params(E, s.hd(), s.rows(), 1, splits, linear_view(nullptr, s.hd()), ws);
         p.batch[0].nseg = 1;
         p.batch[0].a[0] = linear_view(dy, E);
@@ -242,7 +247,7 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (dbo) {
-        float *cws = reinterpret_cast<float *>(static_cast<char *>(workspace) + splitk_bytes(E, s.hd(), s.rows(), 1));
+        void *cws = static_cast<char *>(workspace) + splitk_bytes(dtype, E, s.hd(), s.rows(), 1);
         e = ctattn::launch_colsum_add(dtype, linear_view(dy, E), int(s.rows()), int(E), dbo, cws, st);
         if (e != hipSuccess) return finish(fn, e, st);
     }
@@ -265,8 +270,8 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
 namespace {
 
 int validate_linear(const char *fn, int dtype, int64_t M, int64_t N, int64_t K) {
-    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
-        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (!known_dtype(dtype))
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16, 2 = f16, 3 = f64)", fn, dtype);
     if (M < 0 || N < 1 || K < 1)
         return fail(hipErrorInvalidValue, "%s: need M >= 0, N >= 1, K >= 1 (got %lld, %lld, %lld)", fn, (long long)M,
                     (long long)N, (long long)K);
@@ -305,7 +310,7 @@ int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, vo
 int64_t ctattn_linear_bwd_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K) {
     if (validate_linear("ctattn_linear_bwd_workspace_bytes", dtype, M, N, K)) return -1;
     ok();
-    return splitk_bytes(N, K, M, 1) + align_up(ctattn::colsum_workspace_floats(M, N) * int64_t(sizeof(float)));
+    return splitk_bytes(dtype, N, K, M, 1) + align_up(ctattn::colsum_workspace_bytes(dtype, M, N));
 }
 
 int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, void *dx, void *dw, void *db,
@@ -328,7 +333,7 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     if (dw) {
         // dw[n][k] += sum_m dy[m][n] x[m][k]: M' = N, N' = K, K' = M.  A(m'=n, k'=m) = dy stored
         // [k'][m']; B(k'=m, n'=k) = x stored [k'][n'].
-        const int splits = choose_splits(N, K, M, 1);
+        const int splits = choose_splits(dtype, N, K, M, 1);
         GemmParams p = make_params(N, K, M, 1, splits, linear_view(nullptr, K), ws);
         p.batch[0].nseg = 1;
         p.batch[0].a[0] = linear_view(dy, N);
@@ -339,7 +344,7 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (db) {
-        float *cws = reinterpret_cast<float *>(static_cast<char *>(workspace) + splitk_bytes(N, K, M, 1));
+        void *cws = static_cast<char *>(workspace) + splitk_bytes(dtype, N, K, M, 1);
         e = ctattn::launch_colsum_add(dtype, linear_view(dy, N), int(M), int(N), db, cws, st);
         if (e != hipSuccess) return finish(fn, e, st);
     }
@@ -358,8 +363,8 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
 
 int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n, void *stream) {
     const char *fn = "ctattn_sgd_update";
-    if (dtype != CTATTN_F32 && dtype != CTATTN_BF16)
-        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+    if (!known_dtype(dtype))
+        return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16, 2 = f16, 3 = f64)", fn, dtype);
     if (n < 0) return fail(hipErrorInvalidValue, "%s: negative size %lld", fn, (long long)n);
     if (n == 0) return ok();
     if (!params || !grads) return fail(hipErrorInvalidValue, "%s: null pointer", fn);

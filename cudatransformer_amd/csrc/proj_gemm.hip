@@ -59,9 +59,22 @@ template <> __device__ __forceinline__ floatx4 load4_f<uint16_t>(const uint16_t 
     return floatx4{__uint_as_float(uint32_t(u[0]) << 16), __uint_as_float(uint32_t(u[1]) << 16),
                    __uint_as_float(uint32_t(u[2]) << 16), __uint_as_float(uint32_t(u[3]) << 16)};
 }
+template <> __device__ __forceinline__ float load_f<f16_t>(const f16_t *p) { return to_f32(*p); }
+template <> __device__ __forceinline__ floatx4 load4_f<f16_t>(const f16_t *p) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 u = *reinterpret_cast<const h4 *>(p);
+    return floatx4{float(u[0]), float(u[1]), float(u[2]), float(u[3])};
+}
 template <typename T> __device__ __forceinline__ void store_f(T *p, float x);
 template <> __device__ __forceinline__ void store_f<float>(float *p, float x) { *p = x; }
 template <> __device__ __forceinline__ void store_f<uint16_t>(uint16_t *p, float x) { *p = f32_to_bf16(x).bits; }
+template <> __device__ __forceinline__ void store_f<f16_t>(f16_t *p, float x) { *p = from_f32<f16_t>(x); }
+
+// Loads / stores in the accumulation type: fp64 for fp64 storage, fp32 otherwise.
+template <typename T> __device__ __forceinline__ acc_t<T> load_a(const T *p) { return load_f<T>(p); }
+template <> __device__ __forceinline__ double load_a<double>(const double *p) { return *p; }
+template <typename T> __device__ __forceinline__ void store_a(T *p, acc_t<T> x) { store_f<T>(p, x); }
+template <> __device__ __forceinline__ void store_a<double>(double *p, double x) { *p = x; }
 
 // Indices are < 2^31 (checked on the host), so the divisions are 32-bit.
 __device__ __forceinline__ int64_t view_row_off(const MatView &v, int i) {
@@ -397,23 +410,24 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams prm) {
 
 // Column sums, stage 1: part[rb][c] = sum of rows rb*kColRows .. +kColRows-1 of column c.
 // 256 threads = 64 columns x 4 row lanes, each lane 8 rows; the lanes combine in LDS in a
-// fixed order.  32-row blocks give 768 workgroups for a 4096 x 384 gradient.
+// fixed order.  32-row blocks give 768 workgroups for a 4096 x 384 gradient.  Partial sums
+// are in the accumulation type (fp64 for fp64 storage).
 constexpr int kColRows = 32;
-template <typename T>
-__global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, int C, float *part) {
-    __shared__ float red[4][64];
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, int C, A *part) {
+    __shared__ A red[4][64];
     const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + cl;
     const int r0 = blockIdx.y * kColRows;
     const T *base = static_cast<const T *>(g.p);
-    float s = 0.f;
+    A s = 0;
     if (c < C) {
         const int64_t coff = view_col_off(g, c);
         const int r1 = min(R, r0 + kColRows);
 #pragma unroll
         for (int i = 0; i < kColRows / 4; ++i) {
             const int r = r0 + rl + 4 * i;
-            if (r < r1) s += load_f<T>(base + view_row_off(g, r) + coff);
+            if (r < r1) s += load_a<T>(base + view_row_off(g, r) + coff);
         }
     }
     red[rl][cl] = s;
@@ -424,21 +438,21 @@ __global__ __launch_bounds__(256) void colsum_partial_kernel(MatView g, int R, i
 // Stage 2: out[c] += sum over row blocks of part[rb][c].  16 columns x 16 lanes per block;
 // lane l sums row blocks l, l+16, ... in increasing order, then lane 0 adds the 16 lane sums
 // in order (fixed order: deterministic).
-template <typename T>
-__global__ __launch_bounds__(256) void colsum_final_kernel(const float *part, int nrb, int C, T *out) {
-    __shared__ float red[16][17];
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void colsum_final_kernel(const A *part, int nrb, int C, T *out) {
+    __shared__ A red[16][17];
     const int cl = threadIdx.x & 15, rl = threadIdx.x >> 4;
     const int c = blockIdx.x * 16 + cl;
-    float s = 0.f;
+    A s = 0;
     if (c < C)
         for (int rb = rl; rb < nrb; rb += 16) s += part[int64_t(rb) * C + c];
     red[rl][cl] = s;
     __syncthreads();
     if (rl == 0 && c < C) {
-        float t = 0.f;
+        A t = 0;
 #pragma unroll
         for (int l = 0; l < 16; ++l) t += red[l][cl];
-        store_f<T>(out + c, load_f<T>(out + c) + t);
+        store_a<T>(out + c, load_a<T>(out + c) + t);
     }
 }
 
@@ -447,7 +461,70 @@ template <typename T>
 __global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, float lr, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    store_f<T>(params + i, load_f<T>(params + i) - lr * load_f<T>(grads + i));
+    store_a<T>(params + i, load_a<T>(params + i) - acc_t<T>(lr) * load_a<T>(grads + i));
+}
+
+// fp64 GEMM for fp64 storage (the reference's Double classes): the same products and views as
+// proj_gemm_kernel, on fp64 FMAs (no K split).  64 x 64 output tile per 256-thread workgroup,
+// 4 x 4 outputs per thread, K steps of 16 staged in LDS.
+constexpr int kF64Tile = 64, kF64K = 16;
+__global__ __launch_bounds__(256) void gemm_f64_kernel(GemmParams prm, int a_kc, int b_kc) {
+    __shared__ double as[kF64K][kF64Tile + 1];
+    __shared__ double bs[kF64K][kF64Tile + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int m0 = blockIdx.x * kF64Tile, n0 = blockIdx.y * kF64Tile;
+    const GemmBatch &bt = prm.batch[blockIdx.z];
+    double acc[4][4] = {};
+    for (int seg = 0; seg < bt.nseg; ++seg) {
+        const MatView &va = bt.a[seg], &vb = bt.b[seg];
+        const double *pa = static_cast<const double *>(va.p), *pb = static_cast<const double *>(vb.p);
+        for (int k0 = 0; k0 < prm.K; k0 += kF64K) {
+            // Element e of the 64 x 16 tile: row e % 64, k e / 64.
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int e = threadIdx.x + 256 * l;
+                const int r = e % kF64Tile, kk = e / kF64Tile;
+                const int m = m0 + r, n = n0 + r, k = k0 + kk;
+                double a = 0.0, b = 0.0;
+                if (m < prm.M && k < prm.K)
+                    a = pa[a_kc ? view_row_off(va, m) + view_col_off(va, k) : view_row_off(va, k) + view_col_off(va, m)];
+                if (n < prm.N && k < prm.K)
+                    b = pb[b_kc ? view_row_off(vb, n) + view_col_off(vb, k) : view_row_off(vb, k) + view_col_off(vb, n)];
+                as[kk][r] = a;
+                bs[kk][r] = b;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < kF64K; ++kk) {
+                double a[4], b[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = as[kk][ty * 4 + i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[j] = bs[kk][tx * 4 + j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = fma(a[i], b[j], acc[i][j]);
+            }
+            __syncthreads();
+        }
+    }
+    double *out = static_cast<double *>(bt.out);
+    const double *bias = static_cast<const double *>(bt.bias);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + ty * 4 + i;
+        if (m >= prm.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + tx * 4 + j;
+            if (n >= prm.N) continue;
+            double *p = out + view_row_off(prm.outv, m) + view_col_off(prm.outv, n);
+            double x = acc[i][j] + (bias != nullptr ? bias[n] : 0.0);
+            if (prm.beta) x += *p;
+            *p = x;
+        }
+    }
 }
 
 // Whether a view can take the fast load path as a K-contiguous (kc) or M/N-contiguous
@@ -555,46 +632,67 @@ hipError_t launch_gemm_dt(const GemmParams &prm, int nbatch, bool a_kc, bool b_k
 int gemm_tile_count(int64_t M, int64_t N) { return int(((M + 127) / 128) * ((N + 127) / 128)); }
 int gemm_k_steps(int64_t K) { return int((K + 15) / 16); }
 
+// Storage type of a dtype code: 0 fp32, 1 bf16 (raw 16-bit), 2 fp16, 3 fp64.
+template <typename F>
+hipError_t by_storage(int dtype, F &&f) {
+    switch (dtype) {
+        case 0: return f(static_cast<float *>(nullptr));
+        case 1: return f(static_cast<uint16_t *>(nullptr));
+        case 2: return f(static_cast<f16_t *>(nullptr));
+        default: return f(static_cast<double *>(nullptr));
+    }
+}
+
 hipError_t launch_proj_gemm(int dtype, const GemmParams &prm, int nbatch, bool a_kc, bool b_kc,
                             bool vec4, hipStream_t stream) {
     if (prm.M <= 0 || prm.N <= 0 || nbatch <= 0) return hipSuccess;
-    if (dtype == 0) return launch_gemm_dt<float>(prm, nbatch, a_kc, b_kc, vec4, stream);
-    return launch_gemm_dt<uint16_t>(prm, nbatch, a_kc, b_kc, vec4, stream);
+    if (dtype == 3) {
+        if (prm.splits != 1) return hipErrorInvalidValue;  // the fp64 GEMM does not split K
+        if ((prm.N + kF64Tile - 1) / kF64Tile > 65535) return hipErrorInvalidValue;  // grid.y limit
+        const dim3 grid(unsigned((prm.M + kF64Tile - 1) / kF64Tile), unsigned((prm.N + kF64Tile - 1) / kF64Tile),
+                        unsigned(nbatch));
+        hipLaunchKernelGGL(gemm_f64_kernel, grid, dim3(256), 0, stream, prm, int(a_kc), int(b_kc));
+        return hipGetLastError();
+    }
+    return by_storage(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        if constexpr (std::is_same_v<T, double>) return hipErrorInvalidValue;
+        else return launch_gemm_dt<T>(prm, nbatch, a_kc, b_kc, vec4, stream);
+    });
 }
 
-int64_t colsum_workspace_floats(int64_t R, int64_t C) { return ((R + kColRows - 1) / kColRows) * C; }
+int64_t colsum_workspace_bytes(int dtype, int64_t R, int64_t C) {
+    return ((R + kColRows - 1) / kColRows) * C * (dtype == 3 ? 8 : 4);
+}
 
-hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *out, float *ws,
+hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *out, void *ws,
                              hipStream_t stream) {
     if (R <= 0 || C <= 0) return hipSuccess;
     const int nrb = (R + kColRows - 1) / kColRows;
     if (nrb > 65535) return hipErrorInvalidValue;  // grid.y limit: at most 2^21 - 32 rows
     const dim3 grid1(unsigned((C + 63) / 64), unsigned(nrb));
-    if (dtype == 0)
-        hipLaunchKernelGGL(colsum_partial_kernel<float>, grid1, dim3(256), 0, stream, g, R, C, ws);
-    else
-        hipLaunchKernelGGL(colsum_partial_kernel<uint16_t>, grid1, dim3(256), 0, stream, g, R, C, ws);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     const dim3 grid2(unsigned((C + 15) / 16));
-    if (dtype == 0)
-        hipLaunchKernelGGL(colsum_final_kernel<float>, grid2, dim3(256), 0, stream, ws, nrb, C, static_cast<float *>(out));
-    else
-        hipLaunchKernelGGL(colsum_final_kernel<uint16_t>, grid2, dim3(256), 0, stream, ws, nrb, C,
-                           static_cast<uint16_t *>(out));
-    return hipGetLastError();
+    return by_storage(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
+        hipLaunchKernelGGL(colsum_partial_kernel<T>, grid1, dim3(256), 0, stream, g, R, C, static_cast<A *>(ws));
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(colsum_final_kernel<T>, grid2, dim3(256), 0, stream, static_cast<const A *>(ws), nrb, C,
+                           static_cast<T *>(out));
+        return hipGetLastError();
+    });
 }
 
 hipError_t launch_sgd(int dtype, void *params, const void *grads, float lr, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const dim3 grid(unsigned((n + 255) / 256));
-    if (dtype == 0)
-        hipLaunchKernelGGL(sgd_kernel<float>, grid, dim3(256), 0, stream, static_cast<float *>(params),
-                           static_cast<const float *>(grads), lr, n);
-    else
-        hipLaunchKernelGGL(sgd_kernel<uint16_t>, grid, dim3(256), 0, stream, static_cast<uint16_t *>(params),
-                           static_cast<const uint16_t *>(grads), lr, n);
-    return hipGetLastError();
+    return by_storage(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(sgd_kernel<T>, grid, dim3(256), 0, stream, static_cast<T *>(params),
+                           static_cast<const T *>(grads), lr, n);
+        return hipGetLastError();
+    });
 }
 
 }  // namespace ctattn

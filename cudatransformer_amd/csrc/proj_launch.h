@@ -45,15 +45,16 @@ struct GemmParams {
 int gemm_tile_count(int64_t M, int64_t N);
 int gemm_k_steps(int64_t K);
 
-// a_kc / b_kc: operand is K-contiguous in memory (A stored [m][k], B stored [n][k]); else
+// dtype: 0 fp32, 1 bf16, 2 fp16 (MFMA GEMM, fp32 arithmetic), 3 fp64 (fp64 GEMM; splits must
+// be 1).  a_kc / b_kc: operand is K-contiguous in memory (A stored [m][k], B stored [n][k]); else
 // A is stored [k][m], B [k][n].  vec4: every extent, pitch and head dim is a multiple of 4
 // and every base pointer is 4-element aligned.
 hipError_t launch_proj_gemm(int dtype, const GemmParams &prm, int nbatch, bool a_kc, bool b_kc,
                             bool vec4, hipStream_t stream);
 
-// out[c] += sum_r g(r, c), deterministic; ws holds colsum_workspace_floats(R, C) floats.
-int64_t colsum_workspace_floats(int64_t R, int64_t C);
-hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *out, float *ws,
+// out[c] += sum_r g(r, c), deterministic; ws holds colsum_workspace_bytes(dtype, R, C) bytes.
+int64_t colsum_workspace_bytes(int dtype, int64_t R, int64_t C);
+hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *out, void *ws,
                              hipStream_t stream);
 
 // params -= lr * grads, elementwise.

@@ -9,7 +9,8 @@
  * Conventions shared by every entry point
  *   - q, k, v, o, dout, dq, dk, dv are DEVICE pointers to contiguous row-major
  *     [B, H, T, d] tensors of the element type `dtype`; lse is a DEVICE pointer to a
- *     contiguous fp32 [B, H, T] tensor holding LSE_i = m_i + ln(l_i) (natural log).
+ *     contiguous [B, H, T] tensor holding LSE_i = m_i + ln(l_i) (natural log), fp64 for
+ *     dtype CTATTN_F64 and fp32 for every other dtype.
  *   - the score scale is 1/sqrt(d); causal != 0 masks key j > query i.  causal == 0 is
  *     the reference's behaviour (it has no mask).
  *   - keys past T do not take part in the softmax (no zero padding).
@@ -19,9 +20,10 @@
  *     message (per calling thread).  Argument errors are detected before any launch and
  *     return hipErrorInvalidValue (1); unsupported head dims return
  *     hipErrorNotSupported (801).
- *   - supported: dtype f32 or bf16 (storage; all arithmetic accumulates in fp32),
- *     1 <= d <= 256, T >= 0, B, H >= 0.  d in {32, 64, 128} run on the MFMA
- *     kernels; other d on a generic kernel.
+ *   - supported: dtype f32, bf16 or f16 (storage; arithmetic accumulates in fp32) or f64
+ *     (arithmetic in fp64, the reference's ComputeType<double>), 1 <= d <= 256, T >= 0,
+ *     B, H >= 0.  f32 and bf16 with d in {32, 64, 128} run on the MFMA kernels; every
+ *     other case on the generic kernels.
  */
 #ifndef CTATTN_H
 #define CTATTN_H
@@ -36,7 +38,7 @@
 extern "C" {
 #endif
 
-enum ctattn_dtype { CTATTN_F32 = 0, CTATTN_BF16 = 1 };
+enum ctattn_dtype { CTATTN_F32 = 0, CTATTN_BF16 = 1, CTATTN_F16 = 2, CTATTN_F64 = 3 };
 
 /* Kernel selection policy (process-wide).
  *   AUTO           MFMA kernels where they apply (fastest).  The fp32 MFMA backward adds
@@ -58,10 +60,10 @@ enum ctattn_policy {
  * Replaces the flashAttention<DType> launch of FlashAttentionLayer::computeAttention
  * (reference FlashAttentionLayer.cu:73-79; kernel flash_attention.cu:57-169).  The
  * reference writes (maxScores, denominators) as two [B,H,T] DType buffers
- * (flash_attention.cu:164-167); this boundary writes the single fp32 LSE instead.
- * lse may be NULL when the caller does not keep state for a backward.
+ * (flash_attention.cu:164-167); this boundary writes the single LSE instead (fp32, or fp64
+ * for f64).  lse may be NULL when the caller does not keep state for a backward.
  */
-CTATTN_API int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, float *lse,
+CTATTN_API int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, void *lse,
                int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream);
 
 /*
@@ -81,7 +83,7 @@ CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, i
  * depends on the policy (see enum ctattn_policy).
  */
 CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
-               const void *dout, const float *lse, void *dq, void *dk, void *dv,
+               const void *dout, const void *lse, void *dq, void *dk, void *dv,
                void *workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
                int64_t d, int causal, void *stream);
 

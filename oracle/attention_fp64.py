@@ -35,6 +35,7 @@ import numpy as np
 
 __all__ = [
     "round_to_bf16",
+    "round_to_f16",
     "cast_inputs",
     "scores",
     "attention_fwd",
@@ -58,14 +59,23 @@ def round_to_bf16(x: np.ndarray) -> np.ndarray:
     return u.astype(np.uint32).view(np.float32)
 
 
+def round_to_f16(x: np.ndarray) -> np.ndarray:
+    """Round to the nearest IEEE binary16 (numpy's float16 cast, ties to even); returns
+    float32."""
+    return np.asarray(x, dtype=np.float64).astype(np.float16).astype(np.float32)
+
+
 def cast_inputs(arrays, dtype: str):
-    """Round each array to the storage dtype ("f32" or "bf16") and promote to fp64."""
+    """Round each array to the storage dtype ("f32", "bf16", "f16" or "f64") and promote to
+    fp64."""
     out = []
     for a in arrays:
         if dtype == "f32":
             out.append(np.asarray(a, dtype=np.float32).astype(np.float64))
         elif dtype == "bf16":
             out.append(round_to_bf16(a).astype(np.float64))
+        elif dtype == "f16":
+            out.append(round_to_f16(a).astype(np.float64))
         elif dtype == "f64":
             out.append(np.asarray(a, dtype=np.float64))
         else:
@@ -168,14 +178,19 @@ def attention_fwd_bwd(q, k, v, do, causal: bool = False, chunk_heads: int = 8):
 
 def make_inputs(shape, seed: int, std: float = 1.0, dtype: str = "f32"):
     """Synthetic inputs: draw Q, K, V, dO in that order from ``default_rng(seed)`` in fp64,
-    scale by ``std`` and round to the storage dtype.  Returns float32 arrays (bf16 values
-    are returned as float32 holding exactly-representable bf16 numbers)."""
+    scale by ``std`` and round to the storage dtype.  Returns float32 arrays (bf16 and f16
+    values are returned as float32 holding exactly-representable numbers), or float64 arrays
+    for dtype "f64"."""
     rng = np.random.default_rng(seed)
     out = []
     for _ in range(4):
         a = rng.standard_normal(size=shape) * std
         if dtype == "bf16":
             out.append(round_to_bf16(a))
+        elif dtype == "f16":
+            out.append(round_to_f16(a))
+        elif dtype == "f64":
+            out.append(a)
         else:
             out.append(a.astype(np.float32))
     return out

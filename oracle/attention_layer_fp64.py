@@ -95,7 +95,7 @@ def make_layer_inputs(b, t, e, h, d, seed, dtype="f32", weight_scale=None, bias_
     """Seeded x [B, T, E] ~ N(0, 1), weights ~ N(0, 1/E) (Wq/Wk/Wv [H*d, E]) and
     N(0, 1/(H*d)) (Wo [E, H*d]) -- the scaling the reference's test uses
     (``test_flash_attention.py:20-23``) -- biases ~ N(0, bias_std^2), dY ~ N(0, 1); all
-    cast to the run's dtype and returned as float32 arrays."""
+    cast to the run's dtype and returned as float32 arrays (float64 for dtype "f64")."""
     rng = np.random.default_rng(seed)
     hd = h * d
     ws_in = weight_scale if weight_scale is not None else 1.0 / np.sqrt(e)
@@ -112,5 +112,6 @@ def make_layer_inputs(b, t, e, h, d, seed, dtype="f32", weight_scale=None, bias_
         bo=rng.standard_normal(e) * bias_std,
         dy=rng.standard_normal((b, t, e)),
     )
-    cast = (lambda a: attn.round_to_bf16(a)) if dtype == "bf16" else (lambda a: a.astype(np.float32))
+    cast = {"bf16": attn.round_to_bf16, "f16": attn.round_to_f16, "f64": lambda a: a,
+            "f32": lambda a: a.astype(np.float32)}[dtype]
     return {k: cast(v) for k, v in arrs.items()}

@@ -1,0 +1,250 @@
+"""fp16 and fp64 storage: the generic attention kernels, the fp16 / fp64 projection GEMMs and
+the Half / Double classes of the host module.
+
+fp64 runs accumulate in fp64 (LSE and delta are fp64 too), so they match the fp64 oracle to
+rounding: tolerance 1e-10 relative to the largest value.  fp16 stores IEEE binary16 and
+accumulates in fp32; it is compared with the oracle on the same fp16-rounded inputs at 4e-3
+relative to the largest value (binary16's unit roundoff is 2^-11 = 4.9e-4, and outputs pass
+through one or two fp16-rounded intermediates).
+"""
+import numpy as np
+import pytest
+import torch
+
+from cudatransformer_amd import _capi as ct
+from cudatransformer_amd import cuda_transformer as ctm
+from oracle import attention_fp64 as ora
+from oracle import attention_layer_fp64 as lay
+
+F64_REL = 1e-10
+F16_REL = 4e-3
+NAME = {torch.float64: "f64", torch.float16: "f16"}
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def rel_check(got, want, rel, what, floor=1e-30):
+    """max |got - want| <= rel * max(max |want|, floor); `floor` bounds the scale of
+    quantities that are zero in exact arithmetic (the key bias gradient)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    if not want.size:
+        return
+    err = float(np.max(np.abs(got - want)))
+    scale = max(float(np.max(np.abs(want))), floor)
+    assert err <= rel * scale, f"{what}: max abs err {err:.3e} vs scale {scale:.3e}"
+
+
+def dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float64)).to("cuda", dtype)
+
+
+def host(t):
+    return t.double().cpu().numpy()
+
+
+def test_half_double_api_surface():
+    for name in ("HalfTensor", "DoubleTensor", "HalfModule", "DoubleModule", "HalfFlashAttentionLayer",
+                 "DoubleFlashAttentionLayer", "FlashAttentionHalf", "FlashAttentionDouble",
+                 "HalfAttentionLayer", "DoubleAttentionLayer", "AttentionHalf", "AttentionDouble"):
+        assert hasattr(ctm, name), name
+    assert issubclass(ctm.DoubleAttentionLayer, ctm.DoubleModule)
+    assert issubclass(ctm.HalfAttentionLayer, ctm.HalfModule)
+    layer = ctm.FlashAttentionDouble(head_dim=40, num_heads=3, causal=True)
+    assert (layer.headDim, layer.numHeads, layer.causal) == (40, 3, True)
+
+
+def test_lse_dtype_follows_storage():
+    assert ct._stat_dtype(torch.float64) == torch.float64
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        assert ct._stat_dtype(dt) == torch.float32
+
+
+ATTN_SHAPES = [
+    (2, 3, 77, 64),   # ragged T, MFMA-sized head dim (fp16 / fp64 always take the generic kernels)
+    (1, 2, 130, 40),  # head dim off the MFMA set
+    (1, 1, 1, 8),     # a single row
+    (1, 2, 64, 128),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ATTN_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float16], ids=["f64", "f16"])
+def test_flash_attn_capi_matches_oracle(shape, causal, dtype):
+    say(f"flash_attn capi shape={shape} causal={causal} dtype={dtype}")
+    name = NAME[dtype]
+    q, k, v, do = ora.make_inputs(shape, seed=300 + ATTN_SHAPES.index(shape), dtype=name)
+    want = ora.attention_fwd_bwd(*ora.cast_inputs((q, k, v, do), name), causal)
+    tq, tk, tv, tdo = (dev(a, dtype) for a in (q, k, v, do))
+    o, lse = ct.flash_attn_fwd(tq, tk, tv, causal)
+    assert lse.dtype == ct._stat_dtype(dtype)
+    dq, dk, dv = ct.flash_attn_bwd(tq, tk, tv, o, tdo, lse, causal)
+    torch.cuda.synchronize()
+    rel = F64_REL if dtype == torch.float64 else F16_REL
+    for key, t in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert t.dtype == (lse.dtype if key == "lse" else dtype)
+        rel_check(host(t), want[key], rel, f"{name} {key}")
+
+
+@pytest.mark.gpu
+def test_f16_output_is_rounded_to_nearest():
+    """fp16 O equals the fp64 oracle's O rounded to binary16 except where the fp32
+    accumulation lands within a few fp32 ulps of a rounding tie (at most one binary16 ulp
+    away)."""
+    shape = (1, 2, 96, 64)
+    q, k, v, do = ora.make_inputs(shape, seed=310, dtype="f16")
+    want = ora.attention_fwd(*ora.cast_inputs((q, k, v), "f16"), True)[0]
+    o, _ = ct.flash_attn_fwd(*(dev(a, torch.float16) for a in (q, k, v)), True)
+    got = host(o)
+    exact = ora.round_to_f16(want).astype(np.float64)
+    ulp = np.abs(exact) * 2.0 ** -10 + 2.0 ** -24
+    assert np.all(np.abs(got - exact) <= ulp * 1.0001)
+    assert np.mean(got == exact) > 0.99
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float16], ids=["f64", "f16"])
+def test_flash_layer_pybind(dtype):
+    name = NAME[dtype]
+    say(f"flash layer pybind dtype={dtype}")
+    tensor_cls = ctm.DoubleTensor if dtype == torch.float64 else ctm.HalfTensor
+    factory = ctm.FlashAttentionDouble if dtype == torch.float64 else ctm.FlashAttentionHalf
+    shape = (2, 3, 100, 32)
+    q, k, v, do = ora.make_inputs(shape, seed=320, std=0.7, dtype=name)
+    want = ora.attention_fwd_bwd(*ora.cast_inputs((q, k, v, do), name), True)
+    rel = F64_REL if dtype == torch.float64 else F16_REL
+    layer = factory(32, 3, True)
+    tq, tk, tv, tdo = (tensor_cls.fromNumpy(a) for a in (q, k, v, do))
+    for save in (True, False):
+        o = layer.computeAttention(tq, tk, tv, save)
+        assert layer.hasCache() == save
+        dq, dk, dv = layer.computeBackward(tq, tk, tv, tdo)
+        for key, t in (("o", o), ("dq", dq), ("dk", dk), ("dv", dv)):
+            val = t.numpy()
+            assert val.dtype == (np.float64 if dtype == torch.float64 else np.float32)
+            rel_check(val, want[key], rel, f"{name} save={save} {key}")
+        layer.clearCache()
+        assert not layer.hasCache()
+
+
+@pytest.mark.gpu
+def test_tensor_roundtrip_half_double():
+    x = np.concatenate([np.random.default_rng(1).standard_normal(1000) * 100,
+                        1.0 + (np.arange(50) * 2 + 1) * 2.0 ** -11,  # binary16 ties
+                        [65504.0, 6.0e-8, 1e-5, -0.0]])
+    h = ctm.HalfTensor.fromNumpy(x.astype(np.float32))
+    assert np.array_equal(h.numpy(), ora.round_to_f16(x.astype(np.float32)))
+    d = ctm.DoubleTensor.fromNumpy(x + 1e-12)  # values fp32 cannot hold
+    back = d.numpy()
+    assert back.dtype == np.float64 and np.array_equal(back, x + 1e-12)
+    c = d.clone()
+    d.fill(0.1)
+    assert np.all(d.numpy() == 0.1) and np.array_equal(c.numpy(), x + 1e-12)
+
+
+# ---- projections and the whole attention layer -------------------------------------------
+
+LAYER_SHAPES = [
+    (2, 40, 12, 2, 4),      # E != H*d
+    (1, 65, 10, 3, 6),      # E, d not multiples of 4
+    (2, 130, 64, 4, 16),    # several GEMM tiles
+    (1, 256, 256, 4, 64),   # large K: fp16 weight gradients take the split-K path
+]
+
+
+def oracle_layer(inp, h, d, causal):
+    f = lay.layer_fwd(inp["x"], inp["wq"], inp["wk"], inp["wv"], inp["bq"], inp["bk"], inp["bv"], inp["wo"],
+                      inp["bo"], h, d, causal)
+    g = lay.layer_bwd(inp["x"], inp["wq"], inp["wk"], inp["wv"], inp["wo"], f, inp["dy"], causal)
+    return {**f, **g}
+
+
+def run_ctypes_layer(inp, h, d, causal, dtype):
+    t = {k: dev(v, dtype) for k, v in inp.items()}
+    q, k, v = ct.qkv_proj_fwd(t["x"], t["wq"], t["wk"], t["wv"], t["bq"], t["bk"], t["bv"], h, d)
+    c, lse = ct.flash_attn_fwd(q, k, v, causal)
+    y = ct.out_proj_fwd(c, t["wo"], t["bo"])
+    g = {n: torch.zeros_like(t[n]) for n in ("wq", "wk", "wv", "bq", "bk", "bv", "wo", "bo")}
+    dc = ct.out_proj_bwd(c, t["dy"], t["wo"], dwo=g["wo"], dbo=g["bo"])
+    dq, dk, dv = ct.flash_attn_bwd(q, k, v, c, dc, lse, causal)
+    dx = ct.qkv_proj_bwd(t["x"], dq, dk, dv, t["wq"], t["wk"], t["wv"], dw=(g["wq"], g["wk"], g["wv"]),
+                         db=(g["bq"], g["bk"], g["bv"]))
+    torch.cuda.synchronize()
+    out = dict(q=q, k=k, v=v, c=c, y=y, dc=dc, dq=dq, dk=dk, dv=dv, dx=dx)
+    out.update({"d" + n: gg for n, gg in g.items()})
+    return {n: host(val) for n, val in out.items()}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dims", LAYER_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float16], ids=["f64", "f16"])
+def test_projection_layer_capi(dims, causal, dtype):
+    b, t, e, h, d = dims
+    name = NAME[dtype]
+    say(f"layer capi dims={dims} causal={causal} dtype={dtype}")
+    inp = lay.make_layer_inputs(b, t, e, h, d, seed=330 + LAYER_SHAPES.index(dims), dtype=name)
+    got = run_ctypes_layer(inp, h, d, causal, dtype)
+    want = oracle_layer(inp, h, d, causal)
+    if dtype == torch.float64:
+        for key in ("q", "k", "v", "y", "dc", "dx", "dwq", "dwk", "dwv", "dbq", "dbk", "dbv", "dwo", "dbo"):
+            rel_check(got[key], want[key], F64_REL, f"f64 {dims} {key}", floor=1.0)
+        return
+    for key in ("q", "k", "v", "y"):
+        rel_check(got[key], want[key], F16_REL, f"f16 {dims} {key}")
+    # fp16 gradients go through fp16-rounded intermediates (c, dc, dq, ...): check each product
+    # against the oracle applied to the GPU's own fp16 operands.
+    xr = inp["x"].astype(np.float64).reshape(b * t, e)
+    dyr = inp["dy"].astype(np.float64).reshape(b * t, e)
+    rel_check(got["dwo"], dyr.T @ lay.to_rows(got["c"]), F16_REL, "dwo")
+    rel_check(got["dbo"], dyr.sum(0), F16_REL, "dbo")
+    rel_check(got["dc"], lay.from_rows(dyr @ inp["wo"].astype(np.float64), b, h, t, d), F16_REL, "dc")
+    for n in ("q", "k", "v"):
+        gr = lay.to_rows(got["d" + n])
+        rel_check(got["dw" + n], gr.T @ xr, F16_REL, "dw" + n)
+        rel_check(got["db" + n], gr.sum(0), F16_REL, "db" + n)
+    dx = sum(lay.to_rows(got["d" + n]) @ inp["w" + n].astype(np.float64) for n in ("q", "k", "v"))
+    rel_check(got["dx"], dx.reshape(b, t, e), F16_REL, "dx")
+
+
+def make_pybind_layer(factory, tensor_cls, inp, h, d, causal):
+    layer = factory(inp["x"].shape[2], h, d, causal)
+    for part, w, bname in (("Query", "wq", "bq"), ("Key", "wk", "bk"), ("Value", "wv", "bv"), ("Output", "wo", "bo")):
+        getattr(layer, f"set{part}Weights")(tensor_cls.fromNumpy(inp[w]))
+        getattr(layer, f"set{part}Biases")(tensor_cls.fromNumpy(inp[bname]))
+    return layer
+
+
+@pytest.mark.gpu
+def test_attention_layer_double():
+    b, t, e, h, d = 2, 90, 48, 3, 16
+    say("attention layer pybind f64")
+    inp = lay.make_layer_inputs(b, t, e, h, d, seed=340, dtype="f64")
+    want = oracle_layer(inp, h, d, True)
+    layer = make_pybind_layer(ctm.AttentionDouble, ctm.DoubleTensor, inp, h, d, True)
+    x = ctm.DoubleTensor.fromNumpy(inp["x"])
+    y = layer(x)
+    dx = layer.backward(x, ctm.DoubleTensor.fromNumpy(inp["dy"]))
+    rel_check(y.numpy(), want["y"], F64_REL, "y")
+    rel_check(dx.numpy(), want["dx"], F64_REL, "dx")
+    grads = layer.getGradients()
+    for key, name in (("query.weights", "dwq"), ("key.weights", "dwk"), ("value.weights", "dwv"),
+                      ("output.weights", "dwo"), ("query.biases", "dbq"), ("value.biases", "dbv"),
+                      ("output.biases", "dbo")):
+        rel_check(grads[key].numpy(), want[name], F64_REL, key)
+
+
+@pytest.mark.gpu
+def test_attention_layer_half():
+    b, t, e, h, d = 2, 96, 64, 2, 32
+    say("attention layer pybind f16")
+    inp = lay.make_layer_inputs(b, t, e, h, d, seed=341, dtype="f16")
+    want = oracle_layer(inp, h, d, True)
+    layer = make_pybind_layer(ctm.AttentionHalf, ctm.HalfTensor, inp, h, d, True)
+    y = layer(ctm.HalfTensor.fromNumpy(inp["x"]))
+    rel_check(y.numpy(), want["y"], F16_REL, "f16 y")

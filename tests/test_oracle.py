@@ -174,6 +174,17 @@ def test_round_to_bf16_matches_torch():
     assert np.array_equal(ora.round_to_bf16(x), ref)
 
 
+def test_round_to_f16_matches_torch():
+    rng = np.random.default_rng(12)
+    x = np.concatenate([rng.standard_normal(4096).astype(np.float32) * 8,
+                        np.array([1.0, 1.00048828125, 65504.0, 6.0e-8, -0.0, 1e-3], np.float32)])
+    # values exactly halfway between two binary16 numbers in [1, 2) (ties to even)
+    ties = (np.float32(1.0) + (np.arange(0, 200, dtype=np.float32) * 2 + 1) * np.float32(2.0 ** -11))
+    x = np.concatenate([x, ties, -ties])
+    ref = torch.tensor(x).to(torch.float16).to(torch.float32).numpy()
+    assert np.array_equal(ora.round_to_f16(x), ref)
+
+
 # ----------------------------------------------------------------------------------
 # planted mistakes: each plausible bug must trip a check above
 # ----------------------------------------------------------------------------------
