@@ -78,27 +78,29 @@ def load() -> ctypes.CDLL:
     lib.ctattn_out_proj_bwd_workspace_bytes.restype = i64
     lib.ctattn_out_proj_bwd.argtypes = [c_int] + [vp] * 7 + [i64] + shape5 + [vp]
     lib.ctattn_out_proj_bwd.restype = c_int
-    lib.ctattn_sgd_update.argtypes = [c_int, vp, vp, ctypes.c_float, i64, vp]
+    lib.ctattn_sgd_update.argtypes = [c_int, vp, vp, ctypes.c_double, i64, vp]
     lib.ctattn_sgd_update.restype = c_int
-    f32 = ctypes.c_float
+    f64 = ctypes.c_double
     sigs = {
         "ctattn_linear_fwd": ([c_int] + [vp] * 4 + [i64] * 3 + [vp], c_int),
         "ctattn_linear_bwd_workspace_bytes": ([c_int] + [i64] * 3, i64),
         "ctattn_linear_bwd": ([c_int] + [vp] * 7 + [i64] * 4 + [vp], c_int),
-        "ctattn_layernorm_fwd": ([c_int] + [vp] * 6 + [i64, i64, f32, vp], c_int),
+        "ctattn_layernorm_fwd": ([c_int] + [vp] * 6 + [i64, i64, f64, vp], c_int),
         "ctattn_layernorm_bwd_workspace_bytes": ([c_int, i64, i64], i64),
         "ctattn_layernorm_bwd": ([c_int] + [vp] * 9 + [i64] * 3 + [vp], c_int),
         "ctattn_activation_fwd": ([c_int, c_int, vp, vp, i64, vp], c_int),
         "ctattn_activation_bwd": ([c_int, c_int, vp, vp, vp, i64, vp], c_int),
         "ctattn_embedding_fwd": ([c_int] + [vp] * 4 + [i64] * 5 + [vp], c_int),
         "ctattn_embedding_bwd": ([c_int] + [vp] * 4 + [i64] * 4 + [vp], c_int),
-        "ctattn_softmax_fwd": ([c_int, vp, vp, i64, i64, f32, vp], c_int),
-        "ctattn_softmax_bwd": ([c_int, vp, vp, vp, i64, i64, f32, vp], c_int),
+        "ctattn_softmax_fwd": ([c_int, vp, vp, i64, i64, f64, vp], c_int),
+        "ctattn_softmax_bwd": ([c_int, vp, vp, vp, i64, i64, f64, vp], c_int),
         "ctattn_cross_entropy_fwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
         "ctattn_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
-        "ctattn_softmax_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, f32, vp], c_int),
-        "ctattn_adam_update": ([c_int, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, i64, c_int, vp], c_int),
-        "ctattn_adam_update_multi": ([c_int, vp, vp, vp, vp, vp, f32, f32, f32, f32, f32, i64, c_int, vp], c_int),
+        "ctattn_softmax_cross_entropy_bwd": ([c_int, vp, vp, vp, i64, i64, f64, vp], c_int),
+        "ctattn_mse_loss_fwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
+        "ctattn_mse_loss_bwd": ([c_int, vp, vp, vp, i64, i64, vp], c_int),
+        "ctattn_adam_update": ([c_int, vp, vp, vp, vp, i64] + [f64] * 5 + [i64, c_int, vp], c_int),
+        "ctattn_adam_update_multi": ([c_int, c_int] + [vp] * 5 + [f64] * 5 + [i64, c_int, vp], c_int),
         "ctattn_zero_multi": ([c_int, vp, vp, vp], c_int),
     }
     for name, (args, res) in sigs.items():
@@ -372,13 +374,14 @@ def linear_bwd(x, w, dy, dw=None, db=None, want_dx=True, stream=None):
 
 
 def layernorm_fwd(x, gamma, beta, eps: float = 1e-5, stream=None):
-    """Returns (y, mean, rstd): LayerNorm over the last dimension, fp32 row statistics."""
+    """Returns (y, mean, rstd): LayerNorm over the last dimension; the row statistics are
+    float64 for float64 input, float32 otherwise."""
     d = gamma.numel()
     n = _rows(x, d, "layernorm_fwd")
     _check_dev("layernorm_fwd", x.dtype, x, gamma, beta)
     y = torch.empty_like(x)
-    mean = torch.empty(n, dtype=torch.float32, device=x.device)
-    rstd = torch.empty(n, dtype=torch.float32, device=x.device)
+    mean = torch.empty(n, dtype=_stat_dtype(x.dtype), device=x.device)
+    rstd = torch.empty(n, dtype=_stat_dtype(x.dtype), device=x.device)
     rc = load().ctattn_layernorm_fwd(_DTYPE_CODE[x.dtype], _ptr(x), _ptr(gamma), _ptr(beta), _ptr(y), _ptr(mean),
                                      _ptr(rstd), n, d, float(eps), _stream_handle(stream))
     _check(rc, "ctattn_layernorm_fwd")
@@ -390,7 +393,7 @@ def layernorm_bwd(x, gamma, dy, mean, rstd, dgamma=None, dbeta=None, stream=None
     d = gamma.numel()
     n = _rows(x, d, "layernorm_bwd")
     _check_dev("layernorm_bwd", x.dtype, x, gamma, dy, dgamma, dbeta)
-    _check_dev("layernorm_bwd", torch.float32, mean, rstd)
+    _check_dev("layernorm_bwd", _stat_dtype(x.dtype), mean, rstd)
     code = _DTYPE_CODE[x.dtype]
     lib = load()
     ws = _workspace(lib.ctattn_layernorm_bwd_workspace_bytes(code, n, d), "ctattn_layernorm_bwd_workspace_bytes",
@@ -437,13 +440,13 @@ def embedding_fwd(ids, tok=None, pos=None, stream=None):
 
 
 def embedding_bwd(ids, dout, dtok=None, dpos=None, vocab: int | None = None, stream=None):
-    """dtok[ids] += dout, dpos[t] += sum_b dout (fp32, in place; either may be None)."""
+    """dtok[ids] += dout, dpos[t] += sum_b dout (in place, dout's dtype; either may be None)."""
     b, t = ids.shape
     e = dout.shape[-1]
     _check_ids("embedding_bwd", ids)
-    _check_dev("embedding_bwd", torch.float32, dout, dtok, dpos)
+    _check_dev("embedding_bwd", dout.dtype, dout, dtok, dpos)
     vocab = vocab if vocab is not None else (dtok.shape[0] if dtok is not None else 1)
-    rc = load().ctattn_embedding_bwd(F32, _ptr(ids), _ptr(dout), _ptr(dtok), _ptr(dpos), b, t, e, vocab,
+    rc = load().ctattn_embedding_bwd(_DTYPE_CODE[dout.dtype], _ptr(ids), _ptr(dout), _ptr(dtok), _ptr(dpos), b, t, e, vocab,
                                      _stream_handle(stream))
     _check(rc, "ctattn_embedding_bwd")
 
@@ -469,14 +472,14 @@ def softmax_bwd(p, dp, temperature: float = 1.0, stream=None):
 
 
 def cross_entropy_fwd(p, target, stream=None):
-    """Per-row -log p[target] / N (fp32, the shape of target)."""
+    """Per-row -log p[target] / N (the shape of target; float64 for float64 p, else float32)."""
     v = p.shape[-1]
     n = _rows(p, v, "cross_entropy_fwd")
     _check_dev("cross_entropy_fwd", p.dtype, p)
     _check_ids("cross_entropy_fwd", target)
     if target.numel() != n:
         raise ValueError("cross_entropy_fwd: one target per row")
-    loss = torch.empty(target.shape, dtype=torch.float32, device=p.device)
+    loss = torch.empty(target.shape, dtype=_stat_dtype(p.dtype), device=p.device)
     rc = load().ctattn_cross_entropy_fwd(_DTYPE_CODE[p.dtype], _ptr(p), _ptr(target), _ptr(loss), n, v,
                                          _stream_handle(stream))
     _check(rc, "ctattn_cross_entropy_fwd")
@@ -507,14 +510,44 @@ def softmax_cross_entropy_bwd(p, target, temperature: float = 1.0, stream=None):
     return dz
 
 
+def mse_loss_fwd(x, target, stream=None):
+    """Per-row mean of (x - target)^2 over the last dimension (float64 for float64 x, else
+    float32; the shape of x without its last dimension)."""
+    d = x.shape[-1]
+    n = _rows(x, d, "mse_loss_fwd")
+    _check_dev("mse_loss_fwd", x.dtype, x, target)
+    if target.shape != x.shape:
+        raise ValueError("mse_loss_fwd: x and target shapes differ")
+    loss = torch.empty(x.shape[:-1], dtype=_stat_dtype(x.dtype), device=x.device)
+    rc = load().ctattn_mse_loss_fwd(_DTYPE_CODE[x.dtype], _ptr(x), _ptr(target), _ptr(loss), n, d,
+                                    _stream_handle(stream))
+    _check(rc, "ctattn_mse_loss_fwd")
+    return loss
+
+
+def mse_loss_bwd(x, target, stream=None):
+    d = x.shape[-1]
+    n = _rows(x, d, "mse_loss_bwd")
+    _check_dev("mse_loss_bwd", x.dtype, x, target)
+    if target.shape != x.shape:
+        raise ValueError("mse_loss_bwd: x and target shapes differ")
+    dx = torch.empty_like(x)
+    rc = load().ctattn_mse_loss_bwd(_DTYPE_CODE[x.dtype], _ptr(x), _ptr(target), _ptr(dx), n, d,
+                                    _stream_handle(stream))
+    _check(rc, "ctattn_mse_loss_bwd")
+    return dx
+
+
 def adam_update(param, grad, m, v, step: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0,
                 decoupled: bool = False, stream=None):
-    """One Adam (decoupled=False) or AdamW step, in place on fp32 param / m / v."""
-    _check_dev("adam_update", torch.float32, param, grad, m, v)
+    """One Adam (decoupled=False) or AdamW step, in place on param / m / v (moments float64 for
+    float64 parameters, float32 otherwise)."""
+    _check_dev("adam_update", param.dtype, param, grad)
+    _check_dev("adam_update", _stat_dtype(param.dtype), m, v)
     n = param.numel()
     if not (grad.numel() == m.numel() == v.numel() == n):
         raise ValueError("adam_update: size mismatch")
-    rc = load().ctattn_adam_update(F32, _ptr(param), _ptr(grad), _ptr(m), _ptr(v), n, float(lr), float(beta1),
+    rc = load().ctattn_adam_update(_DTYPE_CODE[param.dtype], _ptr(param), _ptr(grad), _ptr(m), _ptr(v), n, float(lr), float(beta1),
                                    float(beta2), float(eps), float(weight_decay), int(step), int(bool(decoupled)),
                                    _stream_handle(stream))
     _check(rc, "ctattn_adam_update")
@@ -529,15 +562,17 @@ def _ptr_table(ts):
 
 def adam_update_multi(params, grads, ms, vs, step: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
                       weight_decay=0.0, decoupled: bool = False, stream=None):
-    """ctattn_adam_update over lists of fp32 tensors, one launch per 32 tensors."""
+    """ctattn_adam_update over lists of tensors of one dtype, one launch per 32 tensors."""
     if not (len(params) == len(grads) == len(ms) == len(vs)):
         raise ValueError("adam_update_multi: list lengths differ")
-    for group in zip(params, grads, ms, vs):
-        _check_dev("adam_update_multi", torch.float32, *group)
-        if len({t.numel() for t in group}) != 1:
+    dtype = params[0].dtype if params else torch.float32
+    for p, g, m, v in zip(params, grads, ms, vs):
+        _check_dev("adam_update_multi", dtype, p, g)
+        _check_dev("adam_update_multi", _stat_dtype(dtype), m, v)
+        if len({t.numel() for t in (p, g, m, v)}) != 1:
             raise ValueError("adam_update_multi: size mismatch")
     n = (ctypes.c_int64 * max(len(params), 1))(*[p.numel() for p in params])
-    rc = load().ctattn_adam_update_multi(len(params), _ptr_table(params), _ptr_table(grads), _ptr_table(ms),
+    rc = load().ctattn_adam_update_multi(_DTYPE_CODE[dtype], len(params), _ptr_table(params), _ptr_table(grads), _ptr_table(ms),
                                          _ptr_table(vs), n, float(lr), float(beta1), float(beta2), float(eps),
                                          float(weight_decay), int(step), int(bool(decoupled)), _stream_handle(stream))
     _check(rc, "ctattn_adam_update_multi")

@@ -133,7 +133,7 @@ struct AttentionLayer : public Layer<DType> {
 
     // p -= lr * grad on all eight buffers; gradient buffers are allocated (zero) if backward
     // never ran (AttentionLayer.cu:302-334).
-    void sgdUpdate(float lr) override {
+    void sgdUpdate(double lr) override {
         ensureGrads();
         sgd(qkvProj.weightsQuery, qkvProj.weightsQueryGrad, lr, qkvProj.projSize());
         sgd(qkvProj.biasesQuery, qkvProj.biasesQueryGrad, lr, qkvProj.biasSize());
@@ -200,7 +200,7 @@ private:
             hipCheck(hipMemsetAsync(g.get(), 0, n * sizeof(DType), Runtime::stream()), "hipMemsetAsync");
     }
 
-    static void sgd(const std::shared_ptr<DType[]> &p, const std::shared_ptr<DType[]> &g, float lr, size_t n) {
+    static void sgd(const std::shared_ptr<DType[]> &p, const std::shared_ptr<DType[]> &g, double lr, size_t n) {
         ctattnCheck(ctattn_sgd_update(DTypeCode<DType>::value, p.get(), g.get(), lr, int64_t(n), Runtime::stream()),
                     "ctattn_sgd_update");
     }

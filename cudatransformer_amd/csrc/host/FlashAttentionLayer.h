@@ -27,7 +27,7 @@ namespace ct {
 
 template <typename DType = float>
 struct FlashAttentionLayer {
-    using Stat = std::conditional_t<std::is_same_v<DType, double>, double, float>;  // LSE element type
+    using Stat = StatOf<DType>;  // LSE element type
     int headDim = 1;
     int numHeads = 1;
     bool causal = false;

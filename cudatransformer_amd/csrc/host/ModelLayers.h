@@ -7,6 +7,8 @@
 //   TransformerBlockLayer  TransformerBlockLayer.cu:13-220 (LayerNorm -> Attention ->
 //                          LayerNorm -> MLP, no residual connections, as the reference has it)
 //   TransformerLayer       TransformerLayer.cu:13-249 (a stack of blocks)
+//   CheckpointLayer        CheckpointLayer.cu:10-58 (keeps its input, identity)
+//   SGDOptimizer           SGDOptimizer.cu (over parameter / gradient maps)
 //   AdamOptimizer          AdamOptimizer.cu:21-140 (over parameter / gradient maps)
 //   AdamWOptimizer         AdamOptimizer.cu:142-233
 // Same conventions as the reference: weights start at zero (cudaMakeShared zero-fills,
@@ -75,7 +77,7 @@ inline void zeroBuffer(const std::shared_ptr<DType[]> &g, size_t n) {
 }
 
 template <typename DType>
-inline void sgdStep(const std::shared_ptr<DType[]> &p, const std::shared_ptr<DType[]> &g, float lr, size_t n) {
+inline void sgdStep(const std::shared_ptr<DType[]> &p, const std::shared_ptr<DType[]> &g, double lr, size_t n) {
     if (g == nullptr) return;
     ctattnCheck(ctattn_sgd_update(DTypeCode<DType>::value, p.get(), g.get(), lr, int64_t(n), Runtime::stream()),
                 "ctattn_sgd_update");
@@ -188,7 +190,7 @@ struct LinearLayer : public Layer<DType> {
         detail::zeroBuffer(weightsGrad, weightSize());
         detail::zeroBuffer(biasesGrad, size_t(outputDim));
     }
-    void sgdUpdate(float lr) override {
+    void sgdUpdate(double lr) override {
         detail::sgdStep(weights, weightsGrad, lr, weightSize());
         if (useBias) detail::sgdStep(biases, biasesGrad, lr, size_t(outputDim));
     }
@@ -227,10 +229,10 @@ private:
 template <typename DType = float>
 struct LayerNormLayer : public Layer<DType> {
     int inputDim = 1;
-    float epsilon = 1e-5f;
+    double epsilon = 1e-5;
     std::shared_ptr<DType[]> weights, biases, weightsGrad, biasesGrad;
 
-    LayerNormLayer(int inputDim, float epsilon = 1e-5f) : inputDim(inputDim), epsilon(epsilon) {
+    LayerNormLayer(int inputDim, double epsilon = 1e-5) : inputDim(inputDim), epsilon(epsilon) {
         if (inputDim < 1) throw std::invalid_argument("LayerNormLayer: inputDim must be >= 1");
         weights = detail::filled<DType>(size_t(inputDim), 1.f);
         biases = detail::zeros<DType>(size_t(inputDim));
@@ -285,7 +287,7 @@ struct LayerNormLayer : public Layer<DType> {
         detail::zeroBuffer(weightsGrad, size_t(inputDim));
         detail::zeroBuffer(biasesGrad, size_t(inputDim));
     }
-    void sgdUpdate(float lr) override {
+    void sgdUpdate(double lr) override {
         detail::sgdStep(weights, weightsGrad, lr, size_t(inputDim));
         detail::sgdStep(biases, biasesGrad, lr, size_t(inputDim));
     }
@@ -296,13 +298,13 @@ struct LayerNormLayer : public Layer<DType> {
 
 private:
     Tensor<DType> cachedInput;
-    std::shared_ptr<float[]> cachedStats;
+    std::shared_ptr<StatOf<DType>[]> cachedStats;
 
-    // Output and the fp32 row statistics [mean (rows) | rstd (rows)].
-    std::pair<Tensor<DType>, std::shared_ptr<float[]>> run(const Tensor<DType> &input) {
+    // Output and the row statistics [mean (rows) | rstd (rows)] (fp64 for double, else fp32).
+    std::pair<Tensor<DType>, std::shared_ptr<StatOf<DType>[]>> run(const Tensor<DType> &input) {
         const size_t rows = detail::rowsOf(input, size_t(inputDim), "LayerNormLayer input");
         Tensor<DType> out = Tensor<DType>::empty(input.shape());
-        auto stats = deviceAlloc<float>(2 * rows);
+        auto stats = deviceAlloc<StatOf<DType>>(2 * rows);
         ctattnCheck(ctattn_layernorm_fwd(DTypeCode<DType>::value, input.get(), weights.get(), biases.get(), out.get(),
                                          stats.get(), stats.get() + rows, int64_t(rows), inputDim, epsilon,
                                          Runtime::stream()),
@@ -399,7 +401,7 @@ struct MLPLayer : public Layer<DType> {
     void zeroGrad() override {
         for (auto &l : layers) l->zeroGrad();
     }
-    void sgdUpdate(float lr) override {
+    void sgdUpdate(double lr) override {
         for (auto &l : layers) l->sgdUpdate(lr);
     }
 
@@ -488,7 +490,7 @@ struct TransformerBlockLayer : public Layer<DType> {
         secondNorm->zeroGrad();
         mlp->zeroGrad();
     }
-    void sgdUpdate(float lr) override {
+    void sgdUpdate(double lr) override {
         firstNorm->sgdUpdate(lr);
         attention->sgdUpdate(lr);
         secondNorm->sgdUpdate(lr);
@@ -597,7 +599,7 @@ struct TransformerLayer : public Layer<DType> {
     void zeroGrad() override {
         for (auto &b : blocks) b->zeroGrad();
     }
-    void sgdUpdate(float lr) override {
+    void sgdUpdate(double lr) override {
         for (auto &b : blocks) b->sgdUpdate(lr);
     }
 
@@ -610,38 +612,89 @@ private:
     }
 };
 
+// Gradient-checkpoint marker (CheckpointLayer.cu:10-58): forward keeps its input and
+// returns it, backward passes the gradient through, clear() drops the kept input.
+template <typename DType = float>
+struct CheckpointLayer : public Layer<DType> {
+    Tensor<DType> activationStorage;
+
+    std::shared_ptr<Layer<DType>> clone() override {
+        auto c = std::make_shared<CheckpointLayer<DType>>();
+        if (activationStorage.size() > 0) c->activationStorage = activationStorage.clone();
+        return c;
+    }
+    Tensor<DType> forward(Tensor<DType> input) override {
+        activationStorage = input;
+        return input;
+    }
+    Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override { return gradOutput; }
+    void clear() override { activationStorage = Tensor<DType>(); }
+};
+
+namespace detail {
+// The checks every optimizer's step makes before updating anything (AdamOptimizer.cu step,
+// SGDOptimizer.cu step): each parameter has a gradient of its size.
+template <typename DType>
+inline void checkGrads(const std::map<std::string, Tensor<DType>> &params,
+                       const std::map<std::string, Tensor<DType>> &grads) {
+    for (const auto &[name, p] : params) {
+        auto g = grads.find(name);
+        if (g == grads.end())
+            throw std::invalid_argument("Gradient for parameter '" + name + "' not found in gradients map.");
+        if (g->second.size() != p.size())
+            throw std::invalid_argument("Size mismatch between parameter '" + name + "' and its gradient.");
+    }
+}
+}  // namespace detail
+
+// SGD over a parameter map (SGDOptimizer.cu): step(grads) does params[k] -= lr * grads[k] for
+// every parameter, after checking that each has a gradient of its size.
+template <typename DType = float>
+struct SGDOptimizer {
+    std::map<std::string, Tensor<DType>> parameters;
+    double learningRate;
+
+    SGDOptimizer(std::map<std::string, Tensor<DType>> params, double lr)
+        : parameters(std::move(params)), learningRate(lr) {}
+
+    void step(const std::map<std::string, Tensor<DType>> &grads) {
+        detail::checkGrads(parameters, grads);
+        for (const auto &[name, p] : parameters)
+            detail::sgdStep(p.dataPtr(), grads.at(name).dataPtr(), learningRate, p.size());
+    }
+    double getLearningRate() const { return learningRate; }
+    void setLearningRate(double lr) { learningRate = lr; }
+};
+
 // Adam / AdamW over a parameter map (AdamOptimizer.cu:21-140 AdamOptimizer, :142-233
 // AdamWOptimizer): step(grads) updates every parameter (one launch per 32 tensors), and
-// throws if `grads` lacks one or a size differs, as the reference does.  fp32 moments are zero at construction; the step
-// counter advances once per step (the reference advances it twice).  decoupled = false is
-// the reference's AdamOptimizer (decay folded into the gradient), true its AdamWOptimizer.
+// throws if `grads` lacks one or a size differs, as the reference does.  The moments (fp64
+// for double parameters, fp32 otherwise) are zero at construction; the step counter advances
+// once per step (the reference advances it twice).  decoupled = false is the reference's
+// AdamOptimizer (decay folded into the gradient), true its AdamWOptimizer.
+template <typename DType = float>
 struct AdamOptimizer {
-    std::map<std::string, Tensor<float>> parameters;
+    using Stat = StatOf<DType>;
+    std::map<std::string, Tensor<DType>> parameters;
     double learningRate, beta1, beta2, epsilon, decay;
     bool decoupled = false;
     int timeStep = 0;
-    std::map<std::string, std::pair<std::shared_ptr<float[]>, std::shared_ptr<float[]>>> moments;
+    std::map<std::string, std::pair<std::shared_ptr<Stat[]>, std::shared_ptr<Stat[]>>> moments;
 
-    explicit AdamOptimizer(std::map<std::string, Tensor<float>> params, double lr = 1e-3, double b1 = 0.9,
+    explicit AdamOptimizer(std::map<std::string, Tensor<DType>> params, double lr = 1e-3, double b1 = 0.9,
                            double b2 = 0.999, double eps = 1e-8, double decay = 0.0, bool decoupled = false)
         : parameters(std::move(params)), learningRate(lr), beta1(b1), beta2(b2), epsilon(eps), decay(decay),
           decoupled(decoupled) {
         for (const auto &[name, p] : parameters)
-            moments[name] = {detail::zeros<float>(p.size()), detail::zeros<float>(p.size())};
+            moments[name] = {detail::zeros<Stat>(p.size()), detail::zeros<Stat>(p.size())};
     }
 
-    void step(const std::map<std::string, Tensor<float>> &grads) {
-        for (const auto &[name, p] : parameters) {
-            auto g = grads.find(name);
-            if (g == grads.end())
-                throw std::invalid_argument("Gradient for parameter '" + name + "' not found in gradients map.");
-            if (g->second.size() != p.size())
-                throw std::invalid_argument("Size mismatch between parameter '" + name + "' and its gradient.");
-        }
+    void step(const std::map<std::string, Tensor<DType>> &grads) {
+        detail::checkGrads(parameters, grads);
         ++timeStep;
         std::vector<void *> ps;
         std::vector<const void *> gs;
-        std::vector<float *> ms, vs;
+        std::vector<void *> ms, vs;
         std::vector<int64_t> ns;
         for (const auto &[name, p] : parameters) {
             auto &mv = moments[name];
@@ -651,9 +704,9 @@ struct AdamOptimizer {
             vs.push_back(mv.second.get());
             ns.push_back(int64_t(p.size()));
         }
-        ctattnCheck(ctattn_adam_update_multi(int(ps.size()), ps.data(), gs.data(), ms.data(), vs.data(), ns.data(),
-                                             float(learningRate), float(beta1), float(beta2), float(epsilon),
-                                             float(decay), timeStep, decoupled ? 1 : 0, Runtime::stream()),
+        ctattnCheck(ctattn_adam_update_multi(DTypeCode<DType>::value, int(ps.size()), ps.data(), gs.data(), ms.data(),
+                                             vs.data(), ns.data(), learningRate, beta1, beta2, epsilon, decay,
+                                             timeStep, decoupled ? 1 : 0, Runtime::stream()),
                     "ctattn_adam_update_multi");
     }
 
@@ -664,10 +717,11 @@ struct AdamOptimizer {
 };
 
 // AdamW: the decoupled-decay variant (AdamOptimizer.cu:142-233).
-struct AdamWOptimizer : public AdamOptimizer {
-    explicit AdamWOptimizer(std::map<std::string, Tensor<float>> params, double lr = 1e-3, double b1 = 0.9,
+template <typename DType = float>
+struct AdamWOptimizer : public AdamOptimizer<DType> {
+    explicit AdamWOptimizer(std::map<std::string, Tensor<DType>> params, double lr = 1e-3, double b1 = 0.9,
                             double b2 = 0.999, double eps = 1e-8, double decay = 0.0)
-        : AdamOptimizer(std::move(params), lr, b1, b2, eps, decay, true) {}
+        : AdamOptimizer<DType>(std::move(params), lr, b1, b2, eps, decay, true) {}
 };
 
 }  // namespace ct

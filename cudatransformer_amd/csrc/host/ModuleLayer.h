@@ -26,7 +26,7 @@ struct Layer {
     virtual void setParameters(const std::map<std::string, Tensor<DType>> &) {}
     virtual std::map<std::string, Tensor<DType>> getGradients() { return {}; }
     virtual void zeroGrad() {}
-    virtual void sgdUpdate(float) {}
+    virtual void sgdUpdate(double) {}
     // Drops the activations a layer keeps from its last forward for its backward (the
     // reference's TransformerLayer / MLPLayer::clear free their checkpoints).
     virtual void clear() {}

@@ -20,8 +20,8 @@
 //   * an optional causal mask on every attention layer (default off, as in the reference);
 //   * generate() feeds at most the last maxSeqLen tokens back (the reference overruns its
 //     position table past maxSeqLen); top-k clamps K to the vocabulary.
-// The embedding backward accumulates in fp32, so NanoGPT, TokenEmbedding and
-// PositionEmbedding are instantiated for float.
+// Every class is instantiated for float, bfloat16, half and double storage; losses are fp64
+// for double and fp32 otherwise.
 #pragma once
 
 #include <algorithm>
@@ -77,7 +77,7 @@ struct EmbeddingTable {
     void setParameters(const Tensor<DType> &t) { detail::copyInto(embeddingMatrix, t, elements(), "embedding table"); }
     Tensor<DType> getGradients() { return Tensor<DType>(gradEmbeddingMatrix, tableShape()); }
     void zeroGrad() { detail::zeroBuffer(gradEmbeddingMatrix, elements()); }
-    void sgdUpdate(float lr) { detail::sgdStep(embeddingMatrix, gradEmbeddingMatrix, lr, elements()); }
+    void sgdUpdate(double lr) { detail::sgdStep(embeddingMatrix, gradEmbeddingMatrix, lr, elements()); }
 
 protected:
     void copyFrom(const EmbeddingTable &o) {
@@ -180,7 +180,7 @@ struct UnEmbedding {
     void setParameters(const Tensor<DType> &t) { proj->setParameters({{"weights", t}}); }
     Tensor<DType> getGradients() { return proj->getGradients().at("weights"); }
     void zeroGrad() { proj->zeroGrad(); }
-    void sgdUpdate(float lr) { proj->sgdUpdate(lr); }
+    void sgdUpdate(double lr) { proj->sgdUpdate(lr); }
     UnEmbedding clone() const {
         UnEmbedding c(vocabSize, embeddingDim);
         c.proj = std::static_pointer_cast<LinearLayer<DType>>(proj->clone());
@@ -199,7 +199,7 @@ struct Softmax {
         const size_t V = lastDim(input);
         Tensor<DType> out = Tensor<DType>::empty(input.shape());
         ctattnCheck(ctattn_softmax_fwd(DTypeCode<DType>::value, input.get(), out.get(), int64_t(input.size() / V),
-                                       int64_t(V), float(temperature), Runtime::stream()),
+                                       int64_t(V), temperature, Runtime::stream()),
                     "ctattn_softmax_fwd");
         return out;
     }
@@ -212,7 +212,7 @@ struct Softmax {
         Tensor<DType> p = forward(input);
         Tensor<DType> dz = Tensor<DType>::empty(input.shape());
         ctattnCheck(ctattn_softmax_bwd(DTypeCode<DType>::value, p.get(), gradOutput.get(), dz.get(),
-                                       int64_t(input.size() / V), int64_t(V), float(temperature), Runtime::stream()),
+                                       int64_t(input.size() / V), int64_t(V), temperature, Runtime::stream()),
                     "ctattn_softmax_bwd");
         return dz;
     }
@@ -228,15 +228,15 @@ private:
 // (the positions), loss[r] = -log p[r][target[r]] / N.
 template <typename DType = float>
 struct CrossEntropyLoss {
-    Tensor<float> forward(const Tensor<DType> &input, const Tensor<int32_t> &target) const {
+    Tensor<StatOf<DType>> forward(const Tensor<DType> &input, const Tensor<int32_t> &target) const {
         const size_t V = checkShapes(input, target);
-        Tensor<float> loss = Tensor<float>::empty(target.shape());
+        auto loss = Tensor<StatOf<DType>>::empty(target.shape());
         ctattnCheck(ctattn_cross_entropy_fwd(DTypeCode<DType>::value, input.get(), target.get(), loss.get(),
                                              int64_t(target.size()), int64_t(V), Runtime::stream()),
                     "ctattn_cross_entropy_fwd");
         return loss;
     }
-    Tensor<float> operator()(const Tensor<DType> &input, const Tensor<int32_t> &target) const {
+    Tensor<StatOf<DType>> operator()(const Tensor<DType> &input, const Tensor<int32_t> &target) const {
         return forward(input, target);
     }
     Tensor<DType> backward(const Tensor<DType> &input, const Tensor<int32_t> &target) const {
@@ -255,6 +255,41 @@ struct CrossEntropyLoss {
         if (target.size() * V != input.size())
             throw std::invalid_argument("CrossEntropyLoss: target must hold one class id per row of the input");
         return V;
+    }
+};
+
+// Mean squared error per row (SoftmaxLoss.cu:214-272): loss[..] = sum_j (x - y)^2 / D over
+// the last dimension, shaped like the input without it (the reference allocates only
+// shape[0] entries, SoftmaxLoss.cu:234, and writes every row); backward = 2 (x - y) / D.
+template <typename DType = float>
+struct MSELoss {
+    Tensor<StatOf<DType>> forward(const Tensor<DType> &input, const Tensor<DType> &target) const {
+        const size_t D = checkShapes(input, target);
+        std::vector<size_t> shape(input.shape().begin(), input.shape().end() - 1);
+        if (shape.empty()) shape.push_back(1);
+        auto loss = Tensor<StatOf<DType>>::empty(shape);
+        ctattnCheck(ctattn_mse_loss_fwd(DTypeCode<DType>::value, input.get(), target.get(), loss.get(),
+                                        int64_t(input.size() / D), int64_t(D), Runtime::stream()),
+                    "ctattn_mse_loss_fwd");
+        return loss;
+    }
+    Tensor<StatOf<DType>> operator()(const Tensor<DType> &input, const Tensor<DType> &target) const {
+        return forward(input, target);
+    }
+    Tensor<DType> backward(const Tensor<DType> &input, const Tensor<DType> &target) const {
+        const size_t D = checkShapes(input, target);
+        Tensor<DType> grad = Tensor<DType>::empty(input.shape());
+        ctattnCheck(ctattn_mse_loss_bwd(DTypeCode<DType>::value, input.get(), target.get(), grad.get(),
+                                        int64_t(input.size() / D), int64_t(D), Runtime::stream()),
+                    "ctattn_mse_loss_bwd");
+        return grad;
+    }
+
+    static size_t checkShapes(const Tensor<DType> &input, const Tensor<DType> &target) {
+        if (input.nDim() < 1 || input.shape(input.nDim() - 1) == 0)
+            throw std::invalid_argument("MSELoss: empty last dimension");
+        if (input.shape() != target.shape()) throw std::invalid_argument("MSELoss: input and target shapes differ");
+        return input.shape(input.nDim() - 1);
     }
 };
 
@@ -307,7 +342,7 @@ struct NanoGPT {
     }
 
     // Per-position cross-entropy [..., T] (NanoGPT.cu:345-347).
-    Tensor<float> loss(const Tensor<DType> &probs, const Tensor<int32_t> &target) const {
+    Tensor<StatOf<DType>> loss(const Tensor<DType> &probs, const Tensor<int32_t> &target) const {
         return crossEntropyLoss.forward(probs, target);
     }
 
@@ -329,7 +364,7 @@ struct NanoGPT {
         x = x.reshape({B, T, E});
         Tensor<DType> dz = Tensor<DType>::empty({B, T, V});
         ctattnCheck(ctattn_softmax_cross_entropy_bwd(DTypeCode<DType>::value, probs.get(), target.get(), dz.get(),
-                                                     int64_t(rows), int64_t(V), float(softmax.temperature),
+                                                     int64_t(rows), int64_t(V), softmax.temperature,
                                                      Runtime::stream()),
                     "ctattn_softmax_cross_entropy_bwd");
         Tensor<DType> g = unEmbedding.backward(x, dz);
@@ -363,7 +398,7 @@ struct NanoGPT {
         ctattnCheck(ctattn_zero_multi(int(ptrs.size()), ptrs.data(), bytes.data(), Runtime::stream()),
                     "ctattn_zero_multi");
     }
-    void sgdUpdate(float lr) {
+    void sgdUpdate(double lr) {
         tokenEmbedding.sgdUpdate(lr);
         positionEmbedding.sgdUpdate(lr);
         transformerLayer.sgdUpdate(lr);

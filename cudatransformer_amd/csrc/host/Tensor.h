@@ -119,6 +119,10 @@ template <> struct DTypeCode<bf16> { static constexpr int value = CTATTN_BF16; }
 template <> struct DTypeCode<f16> { static constexpr int value = CTATTN_F16; };
 template <> struct DTypeCode<double> { static constexpr int value = CTATTN_F64; };
 
+// Type of the statistics the kernels keep beside a tensor of DType (row statistics, LSE,
+// losses, optimizer moments): double for double, float for every narrower type.
+template <typename DType> using StatOf = std::conditional_t<std::is_same_v<DType, double>, double, float>;
+
 template <typename DType> inline DType fromFloat(float x);
 template <> inline float fromFloat<float>(float x) { return x; }
 template <> inline bf16 fromFloat<bf16>(float x) { return bf16::fromFloat(x); }

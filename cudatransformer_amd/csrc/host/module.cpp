@@ -17,14 +17,16 @@
 // causal=False.  bf16 tensors take and return float32 numpy arrays (numpy has no bfloat16;
 // values are rounded to nearest even on upload).
 //
-// Around attention, with the reference's names (cuda_transformer.cu:178-370, 384-410,
-// 495-787): <T>LayerNormLayer, <T>LinearLayer, <T>ActivationLayer, <T>MLPLayer,
-// <T>TransformerBlockLayer, <T>TransformerLayer and their factories (LayerNorm, Linear,
-// Activation, ReLU, GELU, Sigmoid, Tanh, MLP, TransformerBlock, Transformer; Float / BFloat
-// suffixes, float without one), <T>Softmax, <T>CrossEntropyLoss, IntTensor for ids, and in
-// fp32 FloatTokenEmbedding, FloatPositionEmbedding, FloatUnEmbedding, FloatNanoGPT,
-// FloatAdamOptimizer, FloatAdamWOptimizer; enums ActivationType and SamplingMode.  Id
-// arguments accept an IntTensor, a NumPy array or a list.
+// Around attention, with the reference's names (cuda_transformer.cu:178-370, 372-410,
+// 495-787), for every <T> in Float, BFloat, Half, Double: <T>LayerNormLayer, <T>LinearLayer,
+// <T>ActivationLayer, <T>MLPLayer, <T>CheckpointLayer, <T>TransformerBlockLayer,
+// <T>TransformerLayer and their factories (LayerNorm, Linear, Activation, ReLU, GELU, Sigmoid,
+// Tanh, MLP, Checkpoint, TransformerBlock, Transformer; with the <T> suffix, float without
+// one), <T>Softmax, <T>CrossEntropyLoss, <T>MSELoss, <T>TokenEmbedding, <T>PositionEmbedding,
+// <T>UnEmbedding, <T>NanoGPT, <T>SGDOptimizer, <T>AdamOptimizer, <T>AdamWOptimizer;
+// IntTensor for ids; enums ActivationType and SamplingMode.  Id arguments accept an
+// IntTensor, a NumPy array or a list.  Half and Double tensors take float32 / float64 numpy
+// arrays.
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -238,9 +240,14 @@ void declareLayers(py::module_ &m, const std::string &suffix) {
     py::class_<LN, L, std::shared_ptr<LN>>(m, (suffix + "LayerNormLayer").c_str(),
                                            "Layer normalisation over the last dimension with learnable scale "
                                            "(weights, initially 1) and shift (biases, initially 0).")
-        .def(py::init<int, float>(), py::arg("input_dim"), py::arg("epsilon") = 1e-5f)
+        .def(py::init<int, double>(), py::arg("input_dim"), py::arg("epsilon") = 1e-5)
         .def_readonly("inputDim", &LN::inputDim)
         .def_readonly("epsilon", &LN::epsilon);
+    py::class_<CheckpointLayer<DType>, L, std::shared_ptr<CheckpointLayer<DType>>>(
+        m, (suffix + "CheckpointLayer").c_str(),
+        "Gradient-checkpoint marker: forward stores its input and returns it, backward passes the gradient.")
+        .def(py::init<>())
+        .def("clear", &CheckpointLayer<DType>::clear, "Drops the stored activation.");
     py::class_<ACT, L, std::shared_ptr<ACT>>(m, (suffix + "ActivationLayer").c_str(),
                                              "Elementwise ReLU / GELU (tanh form) / Sigmoid / Tanh.")
         .def(py::init<int, ActivationType>(), py::arg("input_dim"), py::arg("activation_type"))
@@ -296,8 +303,9 @@ void declareFactories(py::module_ &m, const std::string &suffix) {
     using TB = TransformerBlockLayer<DType>;
     using TR = TransformerLayer<DType>;
     auto def = [&](const std::string &name, auto fn, auto... args) { m.def((name + suffix).c_str(), fn, args...); };
-    def("LayerNorm", [](int d, float eps) { return std::make_shared<LN>(d, eps); }, py::arg("input_dim"),
-        py::arg("epsilon") = 1e-5f);
+    def("LayerNorm", [](int d, double eps) { return std::make_shared<LN>(d, eps); }, py::arg("input_dim"),
+        py::arg("epsilon") = 1e-5);
+    def("Checkpoint", [] { return std::make_shared<CheckpointLayer<DType>>(); });
     def("Linear", [](int i, int o, bool b) { return std::make_shared<LIN>(i, o, b); }, py::arg("input_dim"),
         py::arg("output_dim"), py::arg("use_bias") = true);
     def("Activation", [](int d, ActivationType t) { return std::make_shared<ACT>(d, t); }, py::arg("input_dim"),
@@ -331,7 +339,8 @@ void declareLosses(py::module_ &m, const std::string &suffix) {
         .def("backward", &Softmax<DType>::backward, py::arg("input"), py::arg("grad_output"),
              "Gradient with respect to the softmax input, given that input.");
     py::class_<CrossEntropyLoss<DType>>(m, (suffix + "CrossEntropyLoss").c_str(),
-                                        "-log p[target] / N per row, on probabilities (fp32 loss tensor).")
+                                        "-log p[target] / N per row, on probabilities (loss tensor in fp32, "
+                                        "fp64 for Double).")
         .def(py::init<>())
         .def("forward", [](const CrossEntropyLoss<DType> &l, const T &p, py::object t) { return l.forward(p, idsFrom(t)); },
              py::arg("input"), py::arg("target"))
@@ -339,52 +348,67 @@ void declareLosses(py::module_ &m, const std::string &suffix) {
              py::arg("input"), py::arg("target"))
         .def("backward", [](const CrossEntropyLoss<DType> &l, const T &p, py::object t) { return l.backward(p, idsFrom(t)); },
              py::arg("input"), py::arg("target"));
+    py::class_<MSELoss<DType>>(m, (suffix + "MSELoss").c_str(),
+                               "Mean squared error per row, sum_j (x - y)^2 / D over the last dimension (loss tensor "
+                               "in fp32, fp64 for Double).")
+        .def(py::init<>())
+        .def("forward", &MSELoss<DType>::forward, py::arg("input"), py::arg("target"))
+        .def("__call__", &MSELoss<DType>::forward, py::arg("input"), py::arg("target"))
+        .def("backward", &MSELoss<DType>::backward, py::arg("input"), py::arg("target"),
+             "Gradient 2 (x - y) / D with respect to the input.");
 }
 
-// Embeddings, NanoGPT and the Adam optimizers (cuda_transformer.cu:384-410, 495-578, 634-787),
-// fp32 (their gradients accumulate in fp32).
-void declareNanoGPT(py::module_ &m) {
-    using T = Tensor<float>;
-    using G = NanoGPT<float>;
-    py::class_<TokenEmbedding<float>>(m, "FloatTokenEmbedding", "Token id -> embedding row lookup.")
+// Embeddings, NanoGPT and the optimizers (cuda_transformer.cu:372-410, 495-578, 634-787).
+template <typename DType>
+void declareNanoGPT(py::module_ &m, const std::string &suffix) {
+    using T = Tensor<DType>;
+    using G = NanoGPT<DType>;
+    using TE = TokenEmbedding<DType>;
+    using PE = PositionEmbedding<DType>;
+    using UE = UnEmbedding<DType>;
+    using ADAM = AdamOptimizer<DType>;
+    using ADAMW = AdamWOptimizer<DType>;
+    using SGD = SGDOptimizer<DType>;
+    const auto name = [&](const char *n) { return suffix + n; };
+    py::class_<TE>(m, name("TokenEmbedding").c_str(), "Token id -> embedding row lookup.")
         .def(py::init<int, int>(), py::arg("vocab_size"), py::arg("embedding_dim"))
-        .def("forward", [](const TokenEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+        .def("forward", [](const TE &e, py::object ids) { return e.forward(idsFrom(ids)); },
              py::arg("input"))
-        .def("__call__", [](const TokenEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+        .def("__call__", [](const TE &e, py::object ids) { return e.forward(idsFrom(ids)); },
              py::arg("input"))
-        .def("backward", [](TokenEmbedding<float> &e, py::object ids, const T &g) { e.backward(idsFrom(ids), g); },
+        .def("backward", [](TE &e, py::object ids, const T &g) { e.backward(idsFrom(ids), g); },
              py::arg("input"), py::arg("grad_output"))
-        .def("getParameters", &TokenEmbedding<float>::getParameters)
-        .def("setParameters", &TokenEmbedding<float>::setParameters, py::arg("tensor"))
-        .def("getGradients", &TokenEmbedding<float>::getGradients)
-        .def("zeroGrad", &TokenEmbedding<float>::zeroGrad)
-        .def("sgdUpdate", &TokenEmbedding<float>::sgdUpdate, py::arg("lr"))
-        .def("clone", &TokenEmbedding<float>::clone);
-    py::class_<PositionEmbedding<float>>(m, "FloatPositionEmbedding", "Learned position embedding [max_seq_len, E].")
+        .def("getParameters", &TE::getParameters)
+        .def("setParameters", &TE::setParameters, py::arg("tensor"))
+        .def("getGradients", &TE::getGradients)
+        .def("zeroGrad", &TE::zeroGrad)
+        .def("sgdUpdate", &TE::sgdUpdate, py::arg("lr"))
+        .def("clone", &TE::clone);
+    py::class_<PE>(m, name("PositionEmbedding").c_str(), "Learned position embedding [max_seq_len, E].")
         .def(py::init<int, int>(), py::arg("max_seq_len"), py::arg("embedding_dim"))
-        .def("forward", [](const PositionEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+        .def("forward", [](const PE &e, py::object ids) { return e.forward(idsFrom(ids)); },
              py::arg("input"))
-        .def("__call__", [](const PositionEmbedding<float> &e, py::object ids) { return e.forward(idsFrom(ids)); },
+        .def("__call__", [](const PE &e, py::object ids) { return e.forward(idsFrom(ids)); },
              py::arg("input"))
-        .def("backward", [](PositionEmbedding<float> &e, py::object ids, const T &g) { e.backward(idsFrom(ids), g); },
+        .def("backward", [](PE &e, py::object ids, const T &g) { e.backward(idsFrom(ids), g); },
              py::arg("input"), py::arg("grad_output"))
-        .def("getParameters", &PositionEmbedding<float>::getParameters)
-        .def("setParameters", &PositionEmbedding<float>::setParameters, py::arg("tensor"))
-        .def("getGradients", &PositionEmbedding<float>::getGradients)
-        .def("zeroGrad", &PositionEmbedding<float>::zeroGrad)
-        .def("sgdUpdate", &PositionEmbedding<float>::sgdUpdate, py::arg("lr"))
-        .def("clone", &PositionEmbedding<float>::clone);
-    py::class_<UnEmbedding<float>>(m, "FloatUnEmbedding", "Bias-free projection [..., E] -> [..., vocab].")
+        .def("getParameters", &PE::getParameters)
+        .def("setParameters", &PE::setParameters, py::arg("tensor"))
+        .def("getGradients", &PE::getGradients)
+        .def("zeroGrad", &PE::zeroGrad)
+        .def("sgdUpdate", &PE::sgdUpdate, py::arg("lr"))
+        .def("clone", &PE::clone);
+    py::class_<UE>(m, name("UnEmbedding").c_str(), "Bias-free projection [..., E] -> [..., vocab].")
         .def(py::init<int, int>(), py::arg("vocab_size"), py::arg("embedding_dim"))
-        .def("forward", &UnEmbedding<float>::forward, py::arg("input"))
-        .def("__call__", &UnEmbedding<float>::forward, py::arg("input"))
-        .def("backward", &UnEmbedding<float>::backward, py::arg("input"), py::arg("grad_output"))
-        .def("getParameters", &UnEmbedding<float>::getParameters)
-        .def("setParameters", &UnEmbedding<float>::setParameters, py::arg("tensor"))
-        .def("getGradients", &UnEmbedding<float>::getGradients)
-        .def("zeroGrad", &UnEmbedding<float>::zeroGrad)
-        .def("sgdUpdate", &UnEmbedding<float>::sgdUpdate, py::arg("lr"))
-        .def("clone", &UnEmbedding<float>::clone);
+        .def("forward", &UE::forward, py::arg("input"))
+        .def("__call__", &UE::forward, py::arg("input"))
+        .def("backward", &UE::backward, py::arg("input"), py::arg("grad_output"))
+        .def("getParameters", &UE::getParameters)
+        .def("setParameters", &UE::setParameters, py::arg("tensor"))
+        .def("getGradients", &UE::getGradients)
+        .def("zeroGrad", &UE::zeroGrad)
+        .def("sgdUpdate", &UE::sgdUpdate, py::arg("lr"))
+        .def("clone", &UE::clone);
 
     auto generate = [](G &g, py::object input, int n, SamplingMode mode, int K, double P) -> py::object {
         std::vector<int32_t> out = g.generate(idVector(input), n, mode, K, P);
@@ -394,7 +418,7 @@ void declareNanoGPT(py::module_ &m) {
         std::copy(out.begin(), out.end(), a.mutable_data());
         return std::move(a);
     };
-    py::class_<G>(m, "FloatNanoGPT",
+    py::class_<G>(m, name("NanoGPT").c_str(),
                   "GPT language model: token + position embedding -> Transformer -> un-embedding -> softmax.\n"
                   "forward returns probabilities [..., T, vocab]; backward(input, probs, target) accumulates the\n"
                   "gradients of the mean cross-entropy.  Weights start at zero (set them with setParameters).")
@@ -443,16 +467,21 @@ void declareNanoGPT(py::module_ &m) {
         .def("getGradients", &G::getGradients)
         .def_readonly("transformerLayer", &G::transformerLayer);
 
-    py::class_<AdamOptimizer>(m, "FloatAdamOptimizer", "Adam over a parameter map (decay folded into the gradient).")
+    py::class_<SGD>(m, name("SGDOptimizer").c_str(), "SGD over a parameter map: params[k] -= lr * grads[k].")
+        .def(py::init<std::map<std::string, T>, double>(), py::arg("params"), py::arg("lr"))
+        .def("step", &SGD::step, py::arg("grads"), "One update of every parameter from `grads`.")
+        .def("getLearningRate", &SGD::getLearningRate)
+        .def("setLearningRate", &SGD::setLearningRate, py::arg("lr"));
+    py::class_<ADAM>(m, name("AdamOptimizer").c_str(), "Adam over a parameter map (decay folded into the gradient).")
         .def(py::init<std::map<std::string, T>, double, double, double, double, double, bool>(), py::arg("params"),
              py::arg("lr") = 0.001, py::arg("b1") = 0.9, py::arg("b2") = 0.999, py::arg("eps") = 1e-8,
              py::arg("decay") = 0.0, py::arg("decoupled") = false)
-        .def("step", &AdamOptimizer::step, py::arg("grads"), "One update of every parameter from `grads`.")
-        .def("getLearningRate", &AdamOptimizer::getLearningRate)
-        .def("setLearningRate", &AdamOptimizer::setLearningRate, py::arg("lr"))
-        .def("getTimeStep", &AdamOptimizer::getTimeStep)
-        .def("setTimeStep", &AdamOptimizer::setTimeStep, py::arg("t"));
-    py::class_<AdamWOptimizer, AdamOptimizer>(m, "FloatAdamWOptimizer", "AdamW over a parameter map (decoupled decay).")
+        .def("step", &ADAM::step, py::arg("grads"), "One update of every parameter from `grads`.")
+        .def("getLearningRate", &ADAM::getLearningRate)
+        .def("setLearningRate", &ADAM::setLearningRate, py::arg("lr"))
+        .def("getTimeStep", &ADAM::getTimeStep)
+        .def("setTimeStep", &ADAM::setTimeStep, py::arg("t"));
+    py::class_<ADAMW, ADAM>(m, name("AdamWOptimizer").c_str(), "AdamW over a parameter map (decoupled decay).")
         .def(py::init<std::map<std::string, T>, double, double, double, double, double>(), py::arg("params"),
              py::arg("lr") = 0.001, py::arg("b1") = 0.9, py::arg("b2") = 0.999, py::arg("eps") = 1e-8,
              py::arg("decay") = 0.0);
@@ -462,17 +491,16 @@ void declareNanoGPT(py::module_ &m) {
 
 PYBIND11_MODULE(cuda_transformer, m) {
     m.doc() =
-        "cuda_transformer (MI355X): the flash-attention path of CudaTransformer on gfx950 HIP kernels.\n"
-        "Tensors: FloatTensor, BFloatTensor.  Layers: FloatModule / BFloatModule (base),\n"
-        "FloatAttentionLayer / BFloatAttentionLayer (AttentionFloat, AttentionBFloat, Attention),\n"
-        "FloatFlashAttentionLayer / BFloatFlashAttentionLayer (FlashAttention(head_dim, num_heads,\n"
-        "causal=False)).\n"
-        "Around attention: <T>LayerNormLayer, <T>LinearLayer, <T>ActivationLayer, <T>MLPLayer,\n"
-        "<T>TransformerBlockLayer, <T>TransformerLayer (factories LayerNorm, Linear, Activation, ReLU,\n"
-        "GELU, Sigmoid, Tanh, MLP, TransformerBlock, Transformer, with Float / BFloat suffixes),\n"
-        "<T>Softmax, <T>CrossEntropyLoss; IntTensor for token ids; FloatTokenEmbedding,\n"
-        "FloatPositionEmbedding, FloatUnEmbedding, FloatNanoGPT, FloatAdamOptimizer,\n"
-        "FloatAdamWOptimizer; enums ActivationType, SamplingMode.";
+        "cuda_transformer (MI355X): CudaTransformer's Python API on gfx950 HIP kernels.\n"
+        "<T> is Float, BFloat, Half or Double.  Tensors: <T>Tensor, IntTensor (token ids).\n"
+        "Layers: <T>Module (base), <T>AttentionLayer (Attention<T>, Attention), <T>FlashAttentionLayer\n"
+        "(FlashAttention<T>, FlashAttention(head_dim, num_heads, causal=False)), <T>LayerNormLayer,\n"
+        "<T>LinearLayer, <T>ActivationLayer, <T>MLPLayer, <T>CheckpointLayer, <T>TransformerBlockLayer,\n"
+        "<T>TransformerLayer (factories LayerNorm, Linear, Activation, ReLU, GELU, Sigmoid, Tanh, MLP,\n"
+        "Checkpoint, TransformerBlock, Transformer, with a <T> suffix, float without one).\n"
+        "Losses: <T>Softmax, <T>CrossEntropyLoss, <T>MSELoss.  Model: <T>TokenEmbedding,\n"
+        "<T>PositionEmbedding, <T>UnEmbedding, <T>NanoGPT.  Optimizers: <T>SGDOptimizer,\n"
+        "<T>AdamOptimizer, <T>AdamWOptimizer.  Enums ActivationType, SamplingMode.";
 
     py::enum_<ActivationType>(m, "ActivationType", "Activation of the MLP sub-layers.")
         .value("ReLU", ActivationType::ReLU)
@@ -504,12 +532,21 @@ PYBIND11_MODULE(cuda_transformer, m) {
     declareAttention<double>(m, "Double");
     declareLayers<float>(m, "Float");
     declareLayers<bf16>(m, "BFloat");
+    declareLayers<f16>(m, "Half");
+    declareLayers<double>(m, "Double");
     declareFactories<float>(m, "Float");
     declareFactories<bf16>(m, "BFloat");
+    declareFactories<f16>(m, "Half");
+    declareFactories<double>(m, "Double");
     declareFactories<float>(m, "");
     declareLosses<float>(m, "Float");
     declareLosses<bf16>(m, "BFloat");
-    declareNanoGPT(m);
+    declareLosses<f16>(m, "Half");
+    declareLosses<double>(m, "Double");
+    declareNanoGPT<float>(m, "Float");
+    declareNanoGPT<bf16>(m, "BFloat");
+    declareNanoGPT<f16>(m, "Half");
+    declareNanoGPT<double>(m, "Double");
     m.def("Attention",
           [](int inputDim, int numHeads, int headDim, bool causal) {
               return std::make_shared<AttentionLayer<float>>(inputDim, numHeads, headDim, causal);

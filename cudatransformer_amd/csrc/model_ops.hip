@@ -1,13 +1,13 @@
 // Kernels and C-ABI entry points of the layers around the attention path that a NanoGPT
 // training step needs (declared in include/ctattn.h): LayerNorm, the elementwise
 // activations, token + position embeddings, softmax with temperature, cross-entropy on
-// probabilities, and the Adam update.  The linear layers run on the MFMA GEMM family
-// (proj_capi.hip).
+// probabilities, mean squared error, and the Adam update.  The linear layers run on the
+// projection GEMM family (proj_capi.hip).
 //
 // These replace the reference's per-layer kernels (layer_norm_kernels.cu, relu_/gelu_/
 // sigmoid_/tanh_kernels.cu, embedding_kernels.cu, loss_kernels.cu, adam_kernels.cu) with
 // the same math, with these deliberate differences:
-//   * LayerNorm keeps its row statistics in fp32 buffers the caller owns and sums the gamma /
+//   * LayerNorm keeps its row statistics in buffers the caller owns and sums the gamma /
 //     beta gradients deterministically (two-stage column sums, no atomics; the reference
 //     atomically adds every row, layer_norm_kernels.cu backward);
 //   * one wave per row (64 lanes) for the row-wise kernels instead of one thread per row
@@ -19,8 +19,9 @@
 //   * Adam / AdamW are the textbook updates, the step counter advanced once per step by the
 //     caller (the reference increments it twice per step, AdamOptimizer.cu:75,95, and stores
 //     the bias-corrected moments back, adam_kernels.cu adamUpdateKernel).
-// Storage is fp32 or bf16 (bf16 widened to fp32 for arithmetic); the embedding backward and
-// Adam, which accumulate into fp32 state, take fp32 storage only.
+// Storage is fp32, bf16, fp16 or fp64.  Arithmetic is in the storage type's accumulation
+// type (the reference's ComputeType, headers.cu:47-48): fp64 for fp64 storage, fp32
+// otherwise; row statistics, losses and Adam moments are kept in that type too.
 #include "attn_common.h"
 #include "capi_util.h"
 #include "ctattn.h"
@@ -33,33 +34,31 @@
 namespace ctattn {
 namespace {
 
-template <typename T> __device__ __forceinline__ float ld(const T *p, int64_t i);
-template <> __device__ __forceinline__ float ld<float>(const float *p, int64_t i) { return p[i]; }
-template <> __device__ __forceinline__ float ld<bf16_t>(const bf16_t *p, int64_t i) { return to_f32(p[i]); }
-template <typename T> __device__ __forceinline__ void st(T *p, int64_t i, float x) { p[i] = from_f32<T>(x); }
+template <typename T> __device__ __forceinline__ acc_t<T> ld(const T *p, int64_t i) { return to_acc(p[i]); }
+template <typename T> __device__ __forceinline__ void st(T *p, int64_t i, acc_t<T> x) { p[i] = from_acc<T>(x); }
 
 // ---------------------------------------------------------------------------------------
 // LayerNorm over the last dimension (layer_norm_kernels.cu): y = (x - mean) rstd g + b.
 // One wave per row.
 // ---------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void layernorm_fwd_kernel(const T *__restrict__ x, const T *__restrict__ g,
                                                            const T *__restrict__ b, T *__restrict__ y,
-                                                           float *__restrict__ mean_out, float *__restrict__ rstd_out,
-                                                           int64_t N, int D, float eps) {
+                                                           A *__restrict__ mean_out, A *__restrict__ rstd_out,
+                                                           int64_t N, int D, A eps) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (row >= N) return;
     const T *xr = x + row * D;
-    float s = 0.f;
+    A s = 0;
     for (int c = lane; c < D; c += kWave) s += ld(xr, c);
-    const float mean = wave_sum(s) / float(D);
-    float v = 0.f;
+    const A mean = wave_sum(s) / A(D);
+    A v = 0;
     for (int c = lane; c < D; c += kWave) {
-        const float dx = ld(xr, c) - mean;
+        const A dx = ld(xr, c) - mean;
         v += dx * dx;
     }
-    const float rstd = 1.f / sqrtf(wave_sum(v) / float(D) + eps);
+    const A rstd = A(1) / acc_sqrt(wave_sum(v) / A(D) + eps);
     T *yr = y + row * D;
     for (int c = lane; c < D; c += kWave) st(yr, c, (ld(xr, c) - mean) * rstd * ld(g, c) + ld(b, c));
     if (lane == 0) {
@@ -69,28 +68,28 @@ __global__ __launch_bounds__(256) void layernorm_fwd_kernel(const T *__restrict_
 }
 
 // dx = rstd (dxhat - mean(dxhat) - xhat mean(dxhat xhat)), dxhat = dy g.  One wave per row.
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void layernorm_bwd_dx_kernel(const T *__restrict__ x, const T *__restrict__ g,
-                                                              const T *__restrict__ dy, const float *__restrict__ mean,
-                                                              const float *__restrict__ rstd, T *__restrict__ dx,
+                                                              const T *__restrict__ dy, const A *__restrict__ mean,
+                                                              const A *__restrict__ rstd, T *__restrict__ dx,
                                                               int64_t N, int D) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (row >= N) return;
     const T *xr = x + row * D;
     const T *dyr = dy + row * D;
-    const float mu = mean[row], rs = rstd[row];
-    float s1 = 0.f, s2 = 0.f;
+    const A mu = mean[row], rs = rstd[row];
+    A s1 = 0, s2 = 0;
     for (int c = lane; c < D; c += kWave) {
-        const float xh = (ld(xr, c) - mu) * rs;
-        const float dxh = ld(dyr, c) * ld(g, c);
+        const A xh = (ld(xr, c) - mu) * rs;
+        const A dxh = ld(dyr, c) * ld(g, c);
         s1 += dxh;
         s2 += dxh * xh;
     }
-    const float m1 = wave_sum(s1) / float(D), m2 = wave_sum(s2) / float(D);
+    const A m1 = wave_sum(s1) / A(D), m2 = wave_sum(s2) / A(D);
     T *dxr = dx + row * D;
     for (int c = lane; c < D; c += kWave) {
-        const float xh = (ld(xr, c) - mu) * rs;
+        const A xh = (ld(xr, c) - mu) * rs;
         st(dxr, c, rs * (ld(dyr, c) * ld(g, c) - m1 - xh * m2));
     }
 }
@@ -98,25 +97,25 @@ __global__ __launch_bounds__(256) void layernorm_bwd_dx_kernel(const T *__restri
 constexpr int kLnRowsPerChunk = 32;
 
 // Stage 1 of the gamma / beta gradients: part[chunk][c] = sum over the chunk's rows of
-// dy * xhat (first D floats) and dy (next D floats).  256 threads = 64 columns x 4 row lanes
+// dy * xhat (first D values) and dy (next D values).  256 threads = 64 columns x 4 row lanes
 // (8 rows each), combined in LDS in a fixed order.
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void layernorm_bwd_part_kernel(const T *__restrict__ x, const T *__restrict__ dy,
-                                                                const float *__restrict__ mean,
-                                                                const float *__restrict__ rstd,
-                                                                float *__restrict__ part, int64_t N, int D) {
-    __shared__ float red[2][4][64];
+                                                                const A *__restrict__ mean,
+                                                                const A *__restrict__ rstd,
+                                                                A *__restrict__ part, int64_t N, int D) {
+    __shared__ A red[2][4][64];
     const int cl = threadIdx.x & 63, rl = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + cl;
     const int64_t chunk = blockIdx.y;
     const int64_t r0 = chunk * kLnRowsPerChunk;
-    float sg = 0.f, sb = 0.f;
+    A sg = 0, sb = 0;
     if (c < D) {
 #pragma unroll
         for (int i = 0; i < kLnRowsPerChunk / 4; ++i) {
             const int64_t r = r0 + rl + 4 * i;
             if (r < N) {
-                const float d = ld(dy, r * D + c);
+                const A d = ld(dy, r * D + c);
                 sg += d * (ld(x, r * D + c) - mean[r]) * rstd[r];
                 sb += d;
             }
@@ -134,13 +133,13 @@ __global__ __launch_bounds__(256) void layernorm_bwd_part_kernel(const T *__rest
 // Stage 2: dgamma[c] += sum_chunk part[chunk][c], dbeta likewise.  16 columns x 16 lanes per
 // block; lane l takes chunks l, l+16, ... in increasing order, then lane 0 adds the 16 lane
 // sums in order.
-template <typename T>
-__global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *__restrict__ part, T *__restrict__ dg,
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const A *__restrict__ part, T *__restrict__ dg,
                                                                   T *__restrict__ db, int64_t chunks, int D) {
-    __shared__ float red[2][16][17];
+    __shared__ A red[2][16][17];
     const int cl = threadIdx.x & 15, rl = threadIdx.x >> 4;
     const int c = blockIdx.x * 16 + cl;
-    float sg = 0.f, sb = 0.f;
+    A sg = 0, sb = 0;
     if (c < D) {
         for (int64_t k = rl; k < chunks; k += 16) {
             sg += part[k * 2 * D + c];
@@ -151,8 +150,8 @@ __global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *
     red[1][rl][cl] = sb;
     __syncthreads();
     if (rl != 0 || c >= D) return;
-    sg = 0.f;
-    sb = 0.f;
+    sg = 0;
+    sb = 0;
 #pragma unroll
     for (int l = 0; l < 16; ++l) {
         sg += red[0][l][cl];
@@ -165,32 +164,32 @@ __global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const float *
 // ---------------------------------------------------------------------------------------
 // Activations (relu_/gelu_/sigmoid_/tanh_kernels.cu), elementwise.
 // ---------------------------------------------------------------------------------------
-constexpr float kGeluC = 0.7978845608028654f;  // sqrt(2 / pi)
-constexpr float kGeluA = 0.044715f;
+constexpr double kGeluC = 0.7978845608028654;  // sqrt(2 / pi)
+constexpr double kGeluA = 0.044715;
 
-__device__ __forceinline__ float act_fwd(int kind, float x) {
+template <typename A> __device__ __forceinline__ A act_fwd(int kind, A x) {
     switch (kind) {
-        case CTATTN_ACT_RELU: return x > 0.f ? x : 0.f;
-        case CTATTN_ACT_GELU: return 0.5f * x * (1.f + tanhf(kGeluC * (x + kGeluA * x * x * x)));
-        case CTATTN_ACT_SIGMOID: return 1.f / (1.f + expf(-x));
-        default: return tanhf(x);
+        case CTATTN_ACT_RELU: return x > A(0) ? x : A(0);
+        case CTATTN_ACT_GELU: return A(0.5) * x * (A(1) + acc_tanh(A(kGeluC) * (x + A(kGeluA) * x * x * x)));
+        case CTATTN_ACT_SIGMOID: return A(1) / (A(1) + acc_exp(-x));
+        default: return acc_tanh(x);
     }
 }
 
-__device__ __forceinline__ float act_grad(int kind, float x) {
+template <typename A> __device__ __forceinline__ A act_grad(int kind, A x) {
     switch (kind) {
-        case CTATTN_ACT_RELU: return x > 0.f ? 1.f : 0.f;
+        case CTATTN_ACT_RELU: return x > A(0) ? A(1) : A(0);
         case CTATTN_ACT_GELU: {
-            const float t = tanhf(kGeluC * (x + kGeluA * x * x * x));
-            return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * kGeluC * (1.f + 3.f * kGeluA * x * x);
+            const A t = acc_tanh(A(kGeluC) * (x + A(kGeluA) * x * x * x));
+            return A(0.5) * (A(1) + t) + A(0.5) * x * (A(1) - t * t) * A(kGeluC) * (A(1) + A(3) * A(kGeluA) * x * x);
         }
         case CTATTN_ACT_SIGMOID: {
-            const float s = 1.f / (1.f + expf(-x));
-            return s * (1.f - s);
+            const A s = A(1) / (A(1) + acc_exp(-x));
+            return s * (A(1) - s);
         }
         default: {
-            const float t = tanhf(x);
-            return 1.f - t * t;
+            const A t = acc_tanh(x);
+            return A(1) - t * t;
         }
     }
 }
@@ -211,7 +210,7 @@ __global__ __launch_bounds__(256) void act_bwd_kernel(int kind, const T *__restr
 // ---------------------------------------------------------------------------------------
 // Token + position embedding (embedding_kernels.cu).
 // ---------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void embedding_fwd_kernel(const int32_t *__restrict__ ids, const T *__restrict__ tok,
                                                            const T *__restrict__ pos, T *__restrict__ out, int64_t rows,
                                                            int T_, int E, int64_t vocab) {
@@ -220,7 +219,7 @@ __global__ __launch_bounds__(256) void embedding_fwd_kernel(const int32_t *__res
         const int64_t r = i / E;
         const int e = int(i - r * E);
         const int t = int(r % T_);
-        float v = pos != nullptr ? ld(pos, int64_t(t) * E + e) : 0.f;
+        A v = pos != nullptr ? ld(pos, int64_t(t) * E + e) : A(0);
         if (tok != nullptr) {
             const int64_t id = ids[r];
             if (id >= 0 && id < vocab) v += ld(tok, id * E + e);
@@ -229,59 +228,92 @@ __global__ __launch_bounds__(256) void embedding_fwd_kernel(const int32_t *__res
     }
 }
 
-// dtok[ids[r]][e] += dout[r][e] (fp32 atomics); dpos[t][e] += sum_b dout[b][t][e] (one thread
-// per (t, e), fixed order over b).
+// Atomic adds into the token-gradient table: hardware float / double atomics; a pair of
+// 16-bit values (one aligned 32-bit word) by compare-and-swap, each half rounded to nearest
+// even after its add.
+__device__ __forceinline__ void atomic_add(float *p, float x) { unsafeAtomicAdd(p, x); }
+__device__ __forceinline__ void atomic_add(double *p, double x) { unsafeAtomicAdd(p, x); }
+template <typename H> __device__ __forceinline__ void atomic_add_pair(H *p, float lo, float hi) {
+    uint32_t *w = reinterpret_cast<uint32_t *>(p);
+    uint32_t old = *w, assumed;
+    do {
+        assumed = old;
+        const uint16_t nlo = from_f32<H>(to_f32(H{uint16_t(assumed & 0xffffu)}) + lo).bits;
+        const uint16_t nhi = from_f32<H>(to_f32(H{uint16_t(assumed >> 16)}) + hi).bits;
+        old = atomicCAS(w, assumed, uint32_t(nlo) | (uint32_t(nhi) << 16));
+    } while (old != assumed);
+}
+
+// dtok[ids[r]][e] += dout[r][e].  fp32 / fp64: one element per thread.  16-bit: one pair of
+// columns (e, e + 1) per thread; E is even and the table 4-byte aligned (checked on the host),
+// so each pair is one aligned word inside the table.
+template <typename T>
 __global__ __launch_bounds__(256) void embedding_bwd_tok_kernel(const int32_t *__restrict__ ids,
-                                                               const float *__restrict__ dout, float *__restrict__ dtok,
+                                                               const T *__restrict__ dout, T *__restrict__ dtok,
                                                                int64_t rows, int E, int64_t vocab) {
-    const int64_t n = rows * E;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-        const int64_t r = i / E;
-        const int64_t id = ids[r];
-        if (id >= 0 && id < vocab) unsafeAtomicAdd(dtok + id * E + (i - r * E), dout[i]);
+    if constexpr (sizeof(T) >= 4) {
+        const int64_t n = rows * E;
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+            const int64_t r = i / E;
+            const int64_t id = ids[r];
+            if (id >= 0 && id < vocab) atomic_add(dtok + id * E + (i - r * E), dout[i]);
+        }
+    } else {
+        const int half = E / 2;
+        const int64_t n = rows * half;
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+            const int64_t r = i / half;
+            const int e = 2 * int(i - r * half);
+            const int64_t id = ids[r];
+            if (id >= 0 && id < vocab)
+                atomic_add_pair(dtok + id * E + e, to_f32(dout[r * E + e]), to_f32(dout[r * E + e + 1]));
+        }
     }
 }
 
-__global__ __launch_bounds__(256) void embedding_bwd_pos_kernel(const float *__restrict__ dout, float *__restrict__ dpos,
+// dpos[t][e] += sum_b dout[b][t][e]: one thread per (t, e), fixed order over b.
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void embedding_bwd_pos_kernel(const T *__restrict__ dout, T *__restrict__ dpos,
                                                                int64_t B, int T_, int E) {
     const int64_t n = int64_t(T_) * E;
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-        float s = 0.f;
-        for (int64_t b = 0; b < B; ++b) s += dout[b * n + i];
-        dpos[i] += s;
+        A s = 0;
+        for (int64_t b = 0; b < B; ++b) s += ld(dout, b * n + i);
+        st(dpos, i, ld(dpos, i) + s);
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// Softmax with temperature, cross-entropy (loss_kernels.cu).  One wave per row.
+// Softmax with temperature, cross-entropy, mean squared error (loss_kernels.cu).  One wave
+// per row for the row reductions.
 // ---------------------------------------------------------------------------------------
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void softmax_fwd_kernel(const T *__restrict__ z, T *__restrict__ p, int64_t N, int V,
-                                                         float inv_temp) {
+                                                         A inv_temp) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (row >= N) return;
     const T *zr = z + row * V;
-    float m = -INFINITY;
-    for (int c = lane; c < V; c += kWave) m = fmaxf(m, ld(zr, c));
+    A m = -INFINITY;
+    for (int c = lane; c < V; c += kWave) m = fmax(m, ld(zr, c));
     m = wave_max(m);
-    float s = 0.f;
-    for (int c = lane; c < V; c += kWave) s += expf((ld(zr, c) - m) * inv_temp);
-    const float inv_s = 1.f / wave_sum(s);
+    A s = 0;
+    for (int c = lane; c < V; c += kWave) s += acc_exp((ld(zr, c) - m) * inv_temp);
+    const A inv_s = A(1) / wave_sum(s);
     T *pr = p + row * V;
-    for (int c = lane; c < V; c += kWave) st(pr, c, expf((ld(zr, c) - m) * inv_temp) * inv_s);
+    for (int c = lane; c < V; c += kWave) st(pr, c, acc_exp((ld(zr, c) - m) * inv_temp) * inv_s);
 }
 
 // dz = p (dp - sum_c p dp) / temperature (softmaxBackwardKernel's formula, from p).
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void softmax_bwd_kernel(const T *__restrict__ p, const T *__restrict__ dp,
-                                                         T *__restrict__ dz, int64_t N, int V, float inv_temp) {
+                                                         T *__restrict__ dz, int64_t N, int V, A inv_temp) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (row >= N) return;
     const T *pr = p + row * V;
     const T *dpr = dp + row * V;
-    float s = 0.f;
+    A s = 0;
     for (int c = lane; c < V; c += kWave) s += ld(pr, c) * ld(dpr, c);
     s = wave_sum(s);
     T *dzr = dz + row * V;
@@ -289,40 +321,64 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const T *__restrict__ 
 }
 
 // loss[r] = -log(p[r][target[r]]) / N (0 for a target outside [0, V)).  One thread per row.
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void xent_fwd_kernel(const T *__restrict__ p, const int32_t *__restrict__ tgt,
-                                                      float *__restrict__ loss, int64_t N, int V) {
+                                                      A *__restrict__ loss, int64_t N, int V) {
     const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (r >= N) return;
     const int t = tgt[r];
-    loss[r] = (t >= 0 && t < V) ? -logf(ld(p, r * V + t)) / float(N) : 0.f;
+    loss[r] = (t >= 0 && t < V) ? -acc_log(ld(p, r * V + t)) / A(N) : A(0);
 }
 
 // dp[r][c] = -1 / (p N) at the target, 0 elsewhere (crossEntropyLossBackwardKernel).
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void xent_bwd_kernel(const T *__restrict__ p, const int32_t *__restrict__ tgt,
                                                       T *__restrict__ dp, int64_t N, int V) {
     const int64_t n = N * V;
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
         const int64_t r = i / V;
         const int c = int(i - r * V);
-        st(dp, i, c == tgt[r] ? -1.f / (ld(p, i) * float(N)) : 0.f);
+        st(dp, i, c == tgt[r] ? A(-1) / (ld(p, i) * A(N)) : A(0));
     }
 }
 
 // The two above composed with the softmax backward: dz = (p - onehot(target)) / (N T), the
 // same gradient without dividing by p.
-template <typename T>
+template <typename T, typename A = acc_t<T>>
 __global__ __launch_bounds__(256) void softmax_xent_bwd_kernel(const T *__restrict__ p, const int32_t *__restrict__ tgt,
-                                                              T *__restrict__ dz, int64_t N, int V, float scale) {
+                                                              T *__restrict__ dz, int64_t N, int V, A scale) {
     const int64_t n = N * V;
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
         const int64_t r = i / V;
         const int c = int(i - r * V);
         const int t = tgt[r];
-        const float onehot = c == t ? 1.f : 0.f;
-        st(dz, i, (t >= 0 && t < V) ? (ld(p, i) - onehot) * scale : 0.f);
+        const A onehot = c == t ? A(1) : A(0);
+        st(dz, i, (t >= 0 && t < V) ? (ld(p, i) - onehot) * scale : A(0));
     }
+}
+
+// loss[r] = sum_c (x[r][c] - y[r][c])^2 / D (mseLossKernel, loss_kernels.cu).  One wave per row.
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void mse_fwd_kernel(const T *__restrict__ x, const T *__restrict__ y,
+                                                     A *__restrict__ loss, int64_t N, int D) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= N) return;
+    A s = 0;
+    for (int c = lane; c < D; c += kWave) {
+        const A d = ld(x, row * D + c) - ld(y, row * D + c);
+        s += d * d;
+    }
+    s = wave_sum(s);
+    if (lane == 0) loss[row] = s / A(D);
+}
+
+// dx = 2 (x - y) / D (mseLossBackwardKernel).
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void mse_bwd_kernel(const T *__restrict__ x, const T *__restrict__ y,
+                                                     T *__restrict__ dx, int64_t n, int D) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+        st(dx, i, A(2) * (ld(x, i) - ld(y, i)) / A(D));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -330,22 +386,31 @@ __global__ __launch_bounds__(256) void softmax_xent_bwd_kernel(const T *__restri
 // bias-corrected form.  Adam folds the weight decay into the gradient (g + decay p, as
 // adamUpdateKernel does); AdamW decays the parameter itself, p (1 - lr decay) - lr update
 // (adamWUpdateKernel).  m and v keep the uncorrected moments (the reference stores the
-// bias-corrected ones back, so its correction compounds from step to step).
+// bias-corrected ones back, so its correction compounds from step to step), in the
+// accumulation type.
 // ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void adam_kernel(float *__restrict__ param, const float *__restrict__ grad,
-                                                  float *__restrict__ m, float *__restrict__ v, int64_t n, float lr,
-                                                  float b1, float b2, float eps, float decay, int decoupled, float c1,
-                                                  float c2) {
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-        const float p = param[i];
-        const float g = decoupled ? grad[i] : grad[i] + decay * p;
-        const float mi = b1 * m[i] + (1.f - b1) * g;
-        const float vi = b2 * v[i] + (1.f - b2) * g * g;
-        m[i] = mi;
-        v[i] = vi;
-        const float upd = lr * (mi * c1) / (sqrtf(vi * c2) + eps);
-        param[i] = decoupled ? p * (1.f - lr * decay) - upd : p - upd;
-    }
+template <typename A> struct AdamHyper {
+    A lr, b1, b2, eps, decay, c1, c2;
+    int decoupled;
+};
+
+template <typename T, typename A>
+__device__ __forceinline__ void adam_elem(T *param, const T *grad, A *m, A *v, int64_t i, const AdamHyper<A> &h) {
+    const A p = ld(param, i);
+    const A g = h.decoupled ? ld(grad, i) : ld(grad, i) + h.decay * p;
+    const A mi = h.b1 * m[i] + (A(1) - h.b1) * g;
+    const A vi = h.b2 * v[i] + (A(1) - h.b2) * g * g;
+    m[i] = mi;
+    v[i] = vi;
+    const A upd = h.lr * (mi * h.c1) / (acc_sqrt(vi * h.c2) + h.eps);
+    st(param, i, h.decoupled ? p * (A(1) - h.lr * h.decay) - upd : p - upd);
+}
+
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void adam_kernel(T *__restrict__ param, const T *__restrict__ grad,
+                                                  A *__restrict__ m, A *__restrict__ v, int64_t n, AdamHyper<A> h) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+        adam_elem(param, grad, m, v, i, h);
 }
 
 // Multi-tensor launches: up to kMultiMax tensors per launch, described in the kernel
@@ -355,10 +420,10 @@ constexpr int kMultiMax = 32;
 constexpr int kMultiChunk = 4096;  // elements per workgroup: 256 threads x 16
 
 struct AdamMulti {
-    float *param[kMultiMax];
-    const float *grad[kMultiMax];
-    float *m[kMultiMax];
-    float *v[kMultiMax];
+    void *param[kMultiMax];
+    const void *grad[kMultiMax];
+    void *m[kMultiMax];
+    void *v[kMultiMax];
     int64_t n[kMultiMax];
     int32_t chunk_begin[kMultiMax + 1];
     int32_t count;
@@ -378,25 +443,16 @@ __device__ __forceinline__ int multi_owner(const int32_t *chunk_begin, int count
     return t;
 }
 
-__global__ __launch_bounds__(256) void adam_multi_kernel(AdamMulti a, float lr, float b1, float b2, float eps,
-                                                        float decay, int decoupled, float c1, float c2) {
+template <typename T, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void adam_multi_kernel(AdamMulti a, AdamHyper<A> h) {
     const int t = multi_owner(a.chunk_begin, a.count, int(blockIdx.x));
     const int64_t base = int64_t(blockIdx.x - a.chunk_begin[t]) * kMultiChunk;
     const int64_t end = min(a.n[t], base + kMultiChunk);
-    float *__restrict__ param = a.param[t];
-    const float *__restrict__ grad = a.grad[t];
-    float *__restrict__ m = a.m[t];
-    float *__restrict__ v = a.v[t];
-    for (int64_t i = base + threadIdx.x; i < end; i += blockDim.x) {
-        const float p = param[i];
-        const float g = decoupled ? grad[i] : grad[i] + decay * p;
-        const float mi = b1 * m[i] + (1.f - b1) * g;
-        const float vi = b2 * v[i] + (1.f - b2) * g * g;
-        m[i] = mi;
-        v[i] = vi;
-        const float upd = lr * (mi * c1) / (sqrtf(vi * c2) + eps);
-        param[i] = decoupled ? p * (1.f - lr * decay) - upd : p - upd;
-    }
+    T *__restrict__ param = static_cast<T *>(a.param[t]);
+    const T *__restrict__ grad = static_cast<const T *>(a.grad[t]);
+    A *__restrict__ m = static_cast<A *>(a.m[t]);
+    A *__restrict__ v = static_cast<A *>(a.v[t]);
+    for (int64_t i = base + threadIdx.x; i < end; i += blockDim.x) adam_elem(param, grad, m, v, i, h);
 }
 
 // Zeroes whole 4-byte words; a byte tail (sizes not a multiple of 4) is cleared bytewise.
@@ -423,7 +479,9 @@ unsigned rows_grid(int64_t rows) { return unsigned((rows + 3) / 4); }  // 4 wave
 
 namespace {
 
+using ctattn::acc_t;
 using ctattn::bf16_t;
+using ctattn::f16_t;
 using ctattn::capi::align_up;
 using ctattn::capi::fail;
 using ctattn::capi::finish;
@@ -431,11 +489,13 @@ using ctattn::capi::ok;
 
 hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
-int check_dtype(const char *fn, int dtype, bool f32_only = false) {
-    if (dtype == CTATTN_F32 || (!f32_only && dtype == CTATTN_BF16)) return 0;
-    if (dtype == CTATTN_BF16) return fail(hipErrorNotSupported, "%s: bf16 storage is not supported (fp32 only)", fn);
-    return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16)", fn, dtype);
+int check_dtype(const char *fn, int dtype) {
+    if (dtype >= CTATTN_F32 && dtype <= CTATTN_F64) return 0;
+    return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16, 2 = f16, 3 = f64)", fn, dtype);
 }
+
+// Bytes of one row statistic / loss / Adam moment: fp64 for fp64 storage, fp32 otherwise.
+int64_t stat_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : 4; }
 
 int check_rows(const char *fn, int64_t N, int64_t D, const char *dname) {
     if (N < 0 || D < 1)
@@ -445,30 +505,57 @@ int check_rows(const char *fn, int64_t N, int64_t D, const char *dname) {
     return 0;
 }
 
+// Calls f with a null pointer of the storage type of `dtype` (checked beforehand).
 template <typename F>
 hipError_t by_dtype(int dtype, F f) {
-    if (dtype == CTATTN_F32) return f(static_cast<float *>(nullptr));
-    return f(static_cast<bf16_t *>(nullptr));
+    switch (dtype) {
+        case CTATTN_F32: return f(static_cast<float *>(nullptr));
+        case CTATTN_BF16: return f(static_cast<bf16_t *>(nullptr));
+        case CTATTN_F16: return f(static_cast<f16_t *>(nullptr));
+        default: return f(static_cast<double *>(nullptr));
+    }
+}
+
+template <typename T> ctattn::AdamHyper<acc_t<T>> adam_hyper(double lr, double b1, double b2, double eps, double decay,
+                                                              int64_t step, int decoupled) {
+    using A = acc_t<T>;
+    ctattn::AdamHyper<A> h;
+    h.lr = A(lr);
+    h.b1 = A(b1);
+    h.b2 = A(b2);
+    h.eps = A(eps);
+    h.decay = A(decay);
+    h.c1 = A(1.0 / (1.0 - pow(b1, double(step))));
+    h.c2 = A(1.0 / (1.0 - pow(b2, double(step))));
+    h.decoupled = decoupled ? 1 : 0;
+    return h;
+}
+
+int check_adam(const char *fn, int64_t step, double beta1, double beta2, double eps) {
+    if (step < 1 || !(beta1 >= 0.0 && beta1 < 1.0) || !(beta2 >= 0.0 && beta2 < 1.0) || !(eps > 0.0))
+        return fail(hipErrorInvalidValue, "%s: need step >= 1, 0 <= beta < 1, eps > 0", fn);
+    return 0;
 }
 
 }  // namespace
 
 extern "C" {
 
-int ctattn_layernorm_fwd(int dtype, const void *x, const void *gamma, const void *beta, void *y, float *mean,
-                         float *rstd, int64_t N, int64_t D, float eps, void *stream) {
+int ctattn_layernorm_fwd(int dtype, const void *x, const void *gamma, const void *beta, void *y, void *mean,
+                         void *rstd, int64_t N, int64_t D, double eps, void *stream) {
     const char *fn = "ctattn_layernorm_fwd";
     if (int rc = check_dtype(fn, dtype)) return rc;
     if (int rc = check_rows(fn, N, D, "D")) return rc;
     if (N == 0) return ok();
     if (!x || !gamma || !beta || !y || !mean || !rstd) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
-    if (!(eps >= 0.f)) return fail(hipErrorInvalidValue, "%s: eps must be >= 0", fn);
+    if (!(eps >= 0.0)) return fail(hipErrorInvalidValue, "%s: eps must be >= 0", fn);
     hipStream_t st = as_stream(stream);
     const hipError_t e = by_dtype(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
         hipLaunchKernelGGL(ctattn::layernorm_fwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
                            static_cast<const T *>(x), static_cast<const T *>(gamma), static_cast<const T *>(beta),
-                           static_cast<T *>(y), mean, rstd, N, int(D), eps);
+                           static_cast<T *>(y), static_cast<A *>(mean), static_cast<A *>(rstd), N, int(D), A(eps));
         return hipGetLastError();
     });
     return finish(fn, e, st);
@@ -480,11 +567,11 @@ int64_t ctattn_layernorm_bwd_workspace_bytes(int dtype, int64_t N, int64_t D) {
         return -1;
     ok();
     const int64_t chunks = (N + ctattn::kLnRowsPerChunk - 1) / ctattn::kLnRowsPerChunk;
-    return align_up(chunks * 2 * D * int64_t(sizeof(float)));
+    return align_up(chunks * 2 * D * stat_bytes(dtype));
 }
 
-int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void *dy, const float *mean,
-                         const float *rstd, void *dx, void *dgamma, void *dbeta, void *workspace,
+int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void *dy, const void *mean,
+                         const void *rstd, void *dx, void *dgamma, void *dbeta, void *workspace,
                          int64_t workspace_bytes, int64_t N, int64_t D, void *stream) {
     const char *fn = "ctattn_layernorm_bwd";
     if (int rc = check_dtype(fn, dtype)) return rc;
@@ -501,17 +588,21 @@ int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void
     hipStream_t st = as_stream(stream);
     const hipError_t e = by_dtype(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
         const T *xt = static_cast<const T *>(x);
         const T *dyt = static_cast<const T *>(dy);
+        const A *mu = static_cast<const A *>(mean);
+        const A *rs = static_cast<const A *>(rstd);
         if (dx)
             hipLaunchKernelGGL(ctattn::layernorm_bwd_dx_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st, xt,
-                               static_cast<const T *>(gamma), dyt, mean, rstd, static_cast<T *>(dx), N, int(D));
+                               static_cast<const T *>(gamma), dyt, mu, rs, static_cast<T *>(dx), N, int(D));
         if (dgamma || dbeta) {
-            float *part = static_cast<float *>(workspace);
+            A *part = static_cast<A *>(workspace);
             hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 63) / 64), unsigned(chunks)),
-                               dim3(256), 0, st, xt, dyt, mean, rstd, part, N, int(D));
+                               dim3(256), 0, st, xt, dyt, mu, rs, part, N, int(D));
             hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 15) / 16)), dim3(256), 0,
-                               st, part, static_cast<T *>(dgamma), static_cast<T *>(dbeta), chunks, int(D));
+                               st, static_cast<const A *>(part), static_cast<T *>(dgamma), static_cast<T *>(dbeta),
+                               chunks, int(D));
         }
         return hipGetLastError();
     });
@@ -577,59 +668,71 @@ int ctattn_embedding_fwd(int dtype, const int32_t *ids, const void *tok, const v
 int ctattn_embedding_bwd(int dtype, const int32_t *ids, const void *dout, void *dtok, void *dpos, int64_t B,
                          int64_t T, int64_t E, int64_t vocab, void *stream) {
     const char *fn = "ctattn_embedding_bwd";
-    if (int rc = check_dtype(fn, dtype, true)) return rc;
+    if (int rc = check_dtype(fn, dtype)) return rc;
     if (B < 0 || T < 0 || E < 1 || vocab < 1 || E > 2147483647 || T > 2147483647)
         return fail(hipErrorInvalidValue, "%s: invalid sizes", fn);
+    const bool narrow = dtype == CTATTN_BF16 || dtype == CTATTN_F16;
+    if (dtok && narrow && ((E & 1) != 0 || (uintptr_t(dtok) & 3) != 0))
+        return fail(hipErrorInvalidValue,
+                    "%s: 16-bit token gradients need an even embedding width and a 4-byte aligned table", fn);
     if (B * T == 0) return ok();
     if (!ids || !dout) return fail(hipErrorInvalidValue, "%s: null ids/dout pointer", fn);
     hipStream_t st = as_stream(stream);
-    const float *g = static_cast<const float *>(dout);
-    if (dtok)
-        hipLaunchKernelGGL(ctattn::embedding_bwd_tok_kernel, dim3(ctattn::grid_for(B * T * E)), dim3(256), 0, st, ids, g,
-                           static_cast<float *>(dtok), B * T, int(E), vocab);
-    if (dpos)
-        hipLaunchKernelGGL(ctattn::embedding_bwd_pos_kernel, dim3(ctattn::grid_for(T * E)), dim3(256), 0, st, g,
-                           static_cast<float *>(dpos), B, int(T), int(E));
-    return finish(fn, hipGetLastError(), st);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T_ = std::remove_pointer_t<decltype(tag)>;
+        const T_ *g = static_cast<const T_ *>(dout);
+        if (dtok) {
+            const int64_t work = narrow ? B * T * (E / 2) : B * T * E;
+            hipLaunchKernelGGL(ctattn::embedding_bwd_tok_kernel<T_>, dim3(ctattn::grid_for(work)), dim3(256), 0, st,
+                               ids, g, static_cast<T_ *>(dtok), B * T, int(E), vocab);
+        }
+        if (dpos)
+            hipLaunchKernelGGL(ctattn::embedding_bwd_pos_kernel<T_>, dim3(ctattn::grid_for(T * E)), dim3(256), 0, st,
+                               g, static_cast<T_ *>(dpos), B, int(T), int(E));
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
 }
 
-int ctattn_softmax_fwd(int dtype, const void *z, void *p, int64_t N, int64_t V, float temperature, void *stream) {
+int ctattn_softmax_fwd(int dtype, const void *z, void *p, int64_t N, int64_t V, double temperature, void *stream) {
     const char *fn = "ctattn_softmax_fwd";
     if (int rc = check_dtype(fn, dtype)) return rc;
     if (int rc = check_rows(fn, N, V, "V")) return rc;
-    if (!(temperature > 0.f)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
+    if (!(temperature > 0.0)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
     if (N == 0) return ok();
     if (!z || !p) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
     const hipError_t e = by_dtype(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
         hipLaunchKernelGGL(ctattn::softmax_fwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
-                           static_cast<const T *>(z), static_cast<T *>(p), N, int(V), 1.f / temperature);
+                           static_cast<const T *>(z), static_cast<T *>(p), N, int(V), A(1) / A(temperature));
         return hipGetLastError();
     });
     return finish(fn, e, st);
 }
 
-int ctattn_softmax_bwd(int dtype, const void *p, const void *dp, void *dz, int64_t N, int64_t V, float temperature,
+int ctattn_softmax_bwd(int dtype, const void *p, const void *dp, void *dz, int64_t N, int64_t V, double temperature,
                        void *stream) {
     const char *fn = "ctattn_softmax_bwd";
     if (int rc = check_dtype(fn, dtype)) return rc;
     if (int rc = check_rows(fn, N, V, "V")) return rc;
-    if (!(temperature > 0.f)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
+    if (!(temperature > 0.0)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
     if (N == 0) return ok();
     if (!p || !dp || !dz) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
     const hipError_t e = by_dtype(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
         hipLaunchKernelGGL(ctattn::softmax_bwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
                            static_cast<const T *>(p), static_cast<const T *>(dp), static_cast<T *>(dz), N, int(V),
-                           1.f / temperature);
+                           A(1) / A(temperature));
         return hipGetLastError();
     });
     return finish(fn, e, st);
 }
 
-int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, float *loss, int64_t N, int64_t V,
+int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, void *loss, int64_t N, int64_t V,
                              void *stream) {
     const char *fn = "ctattn_cross_entropy_fwd";
     if (int rc = check_dtype(fn, dtype)) return rc;
@@ -640,7 +743,7 @@ int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, fl
     const hipError_t e = by_dtype(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
         hipLaunchKernelGGL(ctattn::xent_fwd_kernel<T>, dim3(unsigned((N + 255) / 256)), dim3(256), 0, st,
-                           static_cast<const T *>(p), target, loss, N, int(V));
+                           static_cast<const T *>(p), target, static_cast<acc_t<T> *>(loss), N, int(V));
         return hipGetLastError();
     });
     return finish(fn, e, st);
@@ -664,47 +767,87 @@ int ctattn_cross_entropy_bwd(int dtype, const void *p, const int32_t *target, vo
 }
 
 int ctattn_softmax_cross_entropy_bwd(int dtype, const void *p, const int32_t *target, void *dz, int64_t N, int64_t V,
-                                     float temperature, void *stream) {
+                                     double temperature, void *stream) {
     const char *fn = "ctattn_softmax_cross_entropy_bwd";
     if (int rc = check_dtype(fn, dtype)) return rc;
     if (int rc = check_rows(fn, N, V, "V")) return rc;
-    if (!(temperature > 0.f)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
+    if (!(temperature > 0.0)) return fail(hipErrorInvalidValue, "%s: temperature must be > 0", fn);
     if (N == 0) return ok();
     if (!p || !target || !dz) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
-    const float scale = 1.f / (float(N) * temperature);
     const hipError_t e = by_dtype(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
         hipLaunchKernelGGL(ctattn::softmax_xent_bwd_kernel<T>, dim3(ctattn::grid_for(N * V)), dim3(256), 0, st,
-                           static_cast<const T *>(p), target, static_cast<T *>(dz), N, int(V), scale);
+                           static_cast<const T *>(p), target, static_cast<T *>(dz), N, int(V),
+                           A(1) / (A(N) * A(temperature)));
         return hipGetLastError();
     });
     return finish(fn, e, st);
 }
 
-int ctattn_adam_update(int dtype, void *param, const void *grad, float *m, float *v, int64_t n, float lr, float beta1,
-                       float beta2, float eps, float weight_decay, int64_t step, int decoupled, void *stream) {
-    const char *fn = "ctattn_adam_update";
-    if (int rc = check_dtype(fn, dtype, true)) return rc;
-    if (n < 0 || step < 1 || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps > 0.f))
-        return fail(hipErrorInvalidValue, "%s: need n >= 0, step >= 1, 0 <= beta < 1, eps > 0", fn);
-    if (n == 0) return ok();
-    if (!param || !grad || !m || !v) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
-    const float c1 = float(1.0 / (1.0 - pow(double(beta1), double(step))));
-    const float c2 = float(1.0 / (1.0 - pow(double(beta2), double(step))));
+int ctattn_mse_loss_fwd(int dtype, const void *x, const void *target, void *loss, int64_t N, int64_t D,
+                        void *stream) {
+    const char *fn = "ctattn_mse_loss_fwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, D, "D")) return rc;
+    if (N == 0) return ok();
+    if (!x || !target || !loss) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(ctattn::adam_kernel, dim3(ctattn::grid_for(n)), dim3(256), 0, st, static_cast<float *>(param),
-                       static_cast<const float *>(grad), m, v, n, lr, beta1, beta2, eps, weight_decay, decoupled ? 1 : 0,
-                       c1, c2);
-    return finish(fn, hipGetLastError(), st);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::mse_fwd_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st,
+                           static_cast<const T *>(x), static_cast<const T *>(target), static_cast<acc_t<T> *>(loss), N,
+                           int(D));
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
 }
 
-int ctattn_adam_update_multi(int count, void *const *param, const void *const *grad, float *const *m, float *const *v,
-                             const int64_t *n, float lr, float beta1, float beta2, float eps, float weight_decay,
-                             int64_t step, int decoupled, void *stream) {
+int ctattn_mse_loss_bwd(int dtype, const void *x, const void *target, void *dx, int64_t N, int64_t D, void *stream) {
+    const char *fn = "ctattn_mse_loss_bwd";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_rows(fn, N, D, "D")) return rc;
+    if (N == 0) return ok();
+    if (!x || !target || !dx) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL(ctattn::mse_bwd_kernel<T>, dim3(ctattn::grid_for(N * D)), dim3(256), 0, st,
+                           static_cast<const T *>(x), static_cast<const T *>(target), static_cast<T *>(dx), N * D,
+                           int(D));
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_adam_update(int dtype, void *param, const void *grad, void *m, void *v, int64_t n, double lr, double beta1,
+                       double beta2, double eps, double weight_decay, int64_t step, int decoupled, void *stream) {
+    const char *fn = "ctattn_adam_update";
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_adam(fn, step, beta1, beta2, eps)) return rc;
+    if (n < 0) return fail(hipErrorInvalidValue, "%s: negative size", fn);
+    if (n == 0) return ok();
+    if (!param || !grad || !m || !v) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
+    hipStream_t st = as_stream(stream);
+    const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using A = acc_t<T>;
+        hipLaunchKernelGGL(ctattn::adam_kernel<T>, dim3(ctattn::grid_for(n)), dim3(256), 0, st,
+                           static_cast<T *>(param), static_cast<const T *>(grad), static_cast<A *>(m),
+                           static_cast<A *>(v), n, adam_hyper<T>(lr, beta1, beta2, eps, weight_decay, step, decoupled));
+        return hipGetLastError();
+    });
+    return finish(fn, e, st);
+}
+
+int ctattn_adam_update_multi(int dtype, int count, void *const *param, const void *const *grad, void *const *m,
+                             void *const *v, const int64_t *n, double lr, double beta1, double beta2, double eps,
+                             double weight_decay, int64_t step, int decoupled, void *stream) {
     const char *fn = "ctattn_adam_update_multi";
-    if (count < 0 || step < 1 || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps > 0.f))
-        return fail(hipErrorInvalidValue, "%s: need count >= 0, step >= 1, 0 <= beta < 1, eps > 0", fn);
+    if (int rc = check_dtype(fn, dtype)) return rc;
+    if (int rc = check_adam(fn, step, beta1, beta2, eps)) return rc;
+    if (count < 0) return fail(hipErrorInvalidValue, "%s: negative count", fn);
     if (count == 0) return ok();
     if (!param || !grad || !m || !v || !n) return fail(hipErrorInvalidValue, "%s: null table", fn);
     for (int i = 0; i < count; ++i) {
@@ -714,8 +857,6 @@ int ctattn_adam_update_multi(int count, void *const *param, const void *const *g
         if ((n[i] + ctattn::kMultiChunk - 1) / ctattn::kMultiChunk > (int64_t(1) << 30))
             return fail(hipErrorInvalidValue, "%s: tensor %d too large", fn, i);
     }
-    const float c1 = float(1.0 / (1.0 - pow(double(beta1), double(step))));
-    const float c2 = float(1.0 / (1.0 - pow(double(beta2), double(step))));
     hipStream_t st = as_stream(stream);
     for (int first = 0; first < count; first += ctattn::kMultiMax) {
         ctattn::AdamMulti a{};
@@ -723,8 +864,8 @@ int ctattn_adam_update_multi(int count, void *const *param, const void *const *g
         for (int i = first; i < count && a.count < ctattn::kMultiMax; ++i) {
             if (n[i] == 0) continue;
             const int k = a.count++;
-            a.param[k] = static_cast<float *>(param[i]);
-            a.grad[k] = static_cast<const float *>(grad[i]);
+            a.param[k] = param[i];
+            a.grad[k] = grad[i];
             a.m[k] = m[i];
             a.v[k] = v[i];
             a.n[k] = n[i];
@@ -734,9 +875,13 @@ int ctattn_adam_update_multi(int count, void *const *param, const void *const *g
         }
         if (a.count == 0) continue;
         a.chunk_begin[a.count] = int32_t(chunks);
-        hipLaunchKernelGGL(ctattn::adam_multi_kernel, dim3(unsigned(chunks)), dim3(256), 0, st, a, lr, beta1, beta2,
-                           eps, weight_decay, decoupled ? 1 : 0, c1, c2);
-        if (hipError_t e = hipGetLastError(); e != hipSuccess) return finish(fn, e, st);
+        const hipError_t e = by_dtype(dtype, [&](auto *tag) {
+            using T = std::remove_pointer_t<decltype(tag)>;
+            hipLaunchKernelGGL(ctattn::adam_multi_kernel<T>, dim3(unsigned(chunks)), dim3(256), 0, st, a,
+                               adam_hyper<T>(lr, beta1, beta2, eps, weight_decay, step, decoupled));
+            return hipGetLastError();
+        });
+        if (e != hipSuccess) return finish(fn, e, st);
     }
     return finish(fn, hipSuccess, st);
 }

@@ -361,7 +361,7 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     return finish(fn, e, st);
 }
 
-int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n, void *stream) {
+int ctattn_sgd_update(int dtype, void *params, const void *grads, double lr, int64_t n, void *stream) {
     const char *fn = "ctattn_sgd_update";
     if (!known_dtype(dtype))
         return fail(hipErrorInvalidValue, "%s: unknown dtype %d (0 = f32, 1 = bf16, 2 = f16, 3 = f64)", fn, dtype);

@@ -458,10 +458,10 @@ __global__ __launch_bounds__(256) void colsum_final_kernel(const A *part, int nr
 
 // params[i] -= lr * grads[i]  (headers.cu:249-275: sgdUpdateKernel / runSgdUpdate).
 template <typename T>
-__global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, float lr, int64_t n) {
+__global__ __launch_bounds__(256) void sgd_kernel(T *params, const T *grads, acc_t<T> lr, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    store_a<T>(params + i, load_a<T>(params + i) - acc_t<T>(lr) * load_a<T>(grads + i));
+    store_a<T>(params + i, load_a<T>(params + i) - lr * load_a<T>(grads + i));
 }
 
 // fp64 GEMM for fp64 storage (the reference's Double classes): the same products and views as
@@ -684,13 +684,13 @@ hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *ou
     });
 }
 
-hipError_t launch_sgd(int dtype, void *params, const void *grads, float lr, int64_t n, hipStream_t stream) {
+hipError_t launch_sgd(int dtype, void *params, const void *grads, double lr, int64_t n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     const dim3 grid(unsigned((n + 255) / 256));
     return by_storage(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
         hipLaunchKernelGGL(sgd_kernel<T>, grid, dim3(256), 0, stream, static_cast<T *>(params),
-                           static_cast<const T *>(grads), lr, n);
+                           static_cast<const T *>(grads), acc_t<T>(lr), n);
         return hipGetLastError();
     });
 }

@@ -58,6 +58,6 @@ hipError_t launch_colsum_add(int dtype, const MatView &g, int R, int C, void *ou
                              hipStream_t stream);
 
 // params -= lr * grads, elementwise.
-hipError_t launch_sgd(int dtype, void *params, const void *grads, float lr, int64_t n, hipStream_t stream);
+hipError_t launch_sgd(int dtype, void *params, const void *grads, double lr, int64_t n, hipStream_t stream);
 
 }  // namespace ctattn

@@ -153,17 +153,19 @@ def native_parameter_name(name: str, checkpoint_gap: int = 0) -> str:
 _NATIVE_ACT = {"relu": "ReLU", "gelu": "GELU", "sigmoid": "Sigmoid", "tanh": "Tanh"}
 
 
-def to_native(model: "NanoGPT", checkpoint_gap: int = 0, temperature: float = 1.0):
-    """A cuda_transformer.FloatNanoGPT with this module's configuration and weights."""
+def to_native(model: "NanoGPT", checkpoint_gap: int = 0, temperature: float = 1.0, dtype: str = "Float"):
+    """A cuda_transformer.<dtype>NanoGPT (dtype "Float", "BFloat", "Half" or "Double") with this
+    module's configuration and weights (rounded to the dtype)."""
     from . import cuda_transformer as ctm
 
     c = model.config
-    nat = ctm.FloatNanoGPT(c["vocab"], c["max_seq_len"], c["d_model"], c["n_heads"], c["head_dim"], c["mlp_dim"],
+    tensor = getattr(ctm, f"{dtype}Tensor")
+    nat = getattr(ctm, f"{dtype}NanoGPT")(c["vocab"], c["max_seq_len"], c["d_model"], c["n_heads"], c["head_dim"], c["mlp_dim"],
                            c["n_layers"], checkpoint_gap=checkpoint_gap, temperature=temperature,
                            activation_type=getattr(ctm.ActivationType, _NATIVE_ACT[c["activation"]]),
                            causal=c["causal"])
     nat.setParameters({native_parameter_name(n, checkpoint_gap):
-                       ctm.FloatTensor.fromNumpy(p.detach().double().cpu().numpy())
+                       tensor.fromNumpy(p.detach().double().cpu().numpy())
                        for n, p in model.named_parameters()})
     return nat
 

@@ -173,14 +173,16 @@ CTATTN_API int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, con
  * params[i] -= lr * grads[i] for i < n.  Replaces runSgdUpdate / sgdUpdateKernel
  * (headers.cu:249-275), which every layer's sgdUpdate calls (AttentionLayer.cu:326-333).
  */
-CTATTN_API int ctattn_sgd_update(int dtype, void *params, const void *grads, float lr, int64_t n,
+CTATTN_API int ctattn_sgd_update(int dtype, void *params, const void *grads, double lr, int64_t n,
                                  void *stream);
 
 /* ---- Layers around the attention path that a NanoGPT training step needs ----
  *
  * Activations are row-major [rows, features]; ids / targets are int32 device arrays.  Same
- * dtype codes as above (fp32 or bf16 storage, fp32 arithmetic) unless noted; the embedding
- * backward and Adam take fp32 only.  Asynchronous on `stream`, 0 or a hipError_t value.
+ * dtype codes as above: fp32, bf16, fp16 or fp64 storage.  Arithmetic is fp64 for fp64
+ * storage and fp32 otherwise, and the "statistic" buffers below (LayerNorm row statistics,
+ * losses, Adam moments) hold that type: fp64 for CTATTN_F64, fp32 for every other dtype.
+ * Asynchronous on `stream`, 0 or a hipError_t value.
  */
 
 /*
@@ -207,12 +209,13 @@ CTATTN_API int ctattn_linear_bwd(int dtype, const void *x, const void *w, const 
 
 /*
  * LayerNorm over the last dimension of x [N][D]: y = (x - mean) * rstd * gamma + beta, with
- * the row statistics written to mean / rstd (fp32 [N]).  Replaces the layerNormForwardKernel
- * launch of LayerNormLayer::forward (LayerNorm.cu:119; kernel layer_norm_kernels.cu).
+ * the row statistics written to mean / rstd (statistic type, [N]).  Replaces the
+ * layerNormForwardKernel launch of LayerNormLayer::forward (LayerNorm.cu:119; kernel
+ * layer_norm_kernels.cu).
  */
 CTATTN_API int ctattn_layernorm_fwd(int dtype, const void *x, const void *gamma, const void *beta,
-                                    void *y, float *mean, float *rstd, int64_t N, int64_t D,
-                                    float eps, void *stream);
+                                    void *y, void *mean, void *rstd, int64_t N, int64_t D,
+                                    double eps, void *stream);
 
 /* Workspace bytes ctattn_layernorm_bwd needs for the gamma / beta gradients. */
 CTATTN_API int64_t ctattn_layernorm_bwd_workspace_bytes(int dtype, int64_t N, int64_t D);
@@ -223,7 +226,7 @@ CTATTN_API int64_t ctattn_layernorm_bwd_workspace_bytes(int dtype, int64_t N, in
  * Replaces the layerNormBackwardKernel launch of LayerNormLayer::backward (LayerNorm.cu:143).
  */
 CTATTN_API int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void *dy,
-                                    const float *mean, const float *rstd, void *dx, void *dgamma,
+                                    const void *mean, const void *rstd, void *dx, void *dgamma,
                                     void *dbeta, void *workspace, int64_t workspace_bytes,
                                     int64_t N, int64_t D, void *stream);
 
@@ -259,10 +262,11 @@ CTATTN_API int ctattn_embedding_fwd(int dtype, const int32_t *ids, const void *t
                                     int64_t max_len, void *stream);
 
 /*
- * dtok[ids[b][t]][:] += dout[b][t][:] (fp32 atomics), dpos[t][:] += sum_b dout[b][t][:]
- * (deterministic); dtok or dpos may be NULL.  fp32 only.  Replaces the
- * tokenEmbeddingBackwardKernel and positionEmbeddingBackwardKernel launches
- * (Embedding.cu:82,234; kernels embedding_kernels.cu:98,135).
+ * dtok[ids[b][t]][:] += dout[b][t][:] (atomic adds in the storage type: hardware fp32 / fp64
+ * atomics, a compare-and-swap per pair of 16-bit values, so bf16 / fp16 need an even E and a
+ * 4-byte aligned dtok), dpos[t][:] += sum_b dout[b][t][:] (deterministic); dtok or dpos may
+ * be NULL.  Replaces the tokenEmbeddingBackwardKernel and positionEmbeddingBackwardKernel
+ * launches (Embedding.cu:82,234; kernels embedding_kernels.cu:98,135).
  */
 CTATTN_API int ctattn_embedding_bwd(int dtype, const int32_t *ids, const void *dout, void *dtok,
                                     void *dpos, int64_t B, int64_t T, int64_t E, int64_t vocab,
@@ -273,7 +277,7 @@ CTATTN_API int ctattn_embedding_bwd(int dtype, const int32_t *ids, const void *d
  * softmaxKernel launch of Softmax::forward (SoftmaxLoss.cu:42; kernel loss_kernels.cu:29).
  */
 CTATTN_API int ctattn_softmax_fwd(int dtype, const void *z, void *p, int64_t N, int64_t V,
-                                  float temperature, void *stream);
+                                  double temperature, void *stream);
 
 /*
  * dz = p * (dp - sum_c p dp) / temperature from the forward's output p.  Replaces the
@@ -281,15 +285,15 @@ CTATTN_API int ctattn_softmax_fwd(int dtype, const void *z, void *p, int64_t N, 
  * loss_kernels.cu:87), which recomputes p from z.
  */
 CTATTN_API int ctattn_softmax_bwd(int dtype, const void *p, const void *dp, void *dz, int64_t N,
-                                  int64_t V, float temperature, void *stream);
+                                  int64_t V, double temperature, void *stream);
 
 /*
- * Cross-entropy on probabilities: loss[r] = -log(p[r][target[r]]) / N (fp32 [N]; 0 for a
- * target outside [0, V)), so sum(loss) is the mean loss.  Replaces the
+ * Cross-entropy on probabilities: loss[r] = -log(p[r][target[r]]) / N (statistic type, [N];
+ * 0 for a target outside [0, V)), so sum(loss) is the mean loss.  Replaces the
  * crossEntropyLossKernel launch of CrossEntropyLoss::forward (SoftmaxLoss.cu:177; kernel
  * loss_kernels.cu:150), with an output of N rows (the reference allocates shape[0]).
  */
-CTATTN_API int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, float *loss,
+CTATTN_API int ctattn_cross_entropy_fwd(int dtype, const void *p, const int32_t *target, void *loss,
                                         int64_t N, int64_t V, void *stream);
 
 /*
@@ -307,12 +311,28 @@ CTATTN_API int ctattn_cross_entropy_bwd(int dtype, const void *p, const int32_t 
  * Softmax::backward (NanoGPT.cu backward); used by NanoGPT training steps.
  */
 CTATTN_API int ctattn_softmax_cross_entropy_bwd(int dtype, const void *p, const int32_t *target,
-                                                void *dz, int64_t N, int64_t V, float temperature,
+                                                void *dz, int64_t N, int64_t V, double temperature,
                                                 void *stream);
 
 /*
- * One Adam or AdamW step on n fp32 parameters with fp32 moments m, v (step >= 1, the 1-based
- * count of this update), c1 = 1 / (1 - b1^step), c2 = 1 / (1 - b2^step):
+ * Mean squared error per row of x, target [N][D]: loss[r] = sum_c (x - target)^2 / D
+ * (statistic type, [N]).  Replaces the mseLossKernel launch of MSELoss::forward
+ * (SoftmaxLoss.cu:239; kernel loss_kernels.cu:233), with an output of N rows (the reference
+ * allocates shape[0]).
+ */
+CTATTN_API int ctattn_mse_loss_fwd(int dtype, const void *x, const void *target, void *loss,
+                                   int64_t N, int64_t D, void *stream);
+
+/*
+ * dx = 2 (x - target) / D, elementwise (dx overwritten).  Replaces the mseLossBackwardKernel
+ * launch of MSELoss::backward (SoftmaxLoss.cu:267; kernel loss_kernels.cu:267).
+ */
+CTATTN_API int ctattn_mse_loss_bwd(int dtype, const void *x, const void *target, void *dx,
+                                   int64_t N, int64_t D, void *stream);
+
+/*
+ * One Adam or AdamW step on n parameters with moments m, v in the statistic type (step >= 1,
+ * the 1-based count of this update), c1 = 1 / (1 - b1^step), c2 = 1 / (1 - b2^step):
  *   decoupled = 0 (Adam):  g = grad + weight_decay * param,
  *                          param -= lr * c1 m / (sqrt(c2 v) + eps);
  *   decoupled = 1 (AdamW): g = grad,
@@ -324,22 +344,22 @@ CTATTN_API int ctattn_softmax_cross_entropy_bwd(int dtype, const void *p, const 
  * stores the bias-corrected moments back; here the caller passes the step and the moments
  * stay uncorrected.
  */
-CTATTN_API int ctattn_adam_update(int dtype, void *param, const void *grad, float *m, float *v,
-                                  int64_t n, float lr, float beta1, float beta2, float eps,
-                                  float weight_decay, int64_t step, int decoupled, void *stream);
+CTATTN_API int ctattn_adam_update(int dtype, void *param, const void *grad, void *m, void *v,
+                                  int64_t n, double lr, double beta1, double beta2, double eps,
+                                  double weight_decay, int64_t step, int decoupled, void *stream);
 
 /*
- * ctattn_adam_update over `count` fp32 tensors in one launch per 32 tensors: tensor i has n[i]
+ * ctattn_adam_update over `count` tensors of one dtype in one launch per 32 tensors: tensor i has n[i]
  * elements at param[i], grad[i], m[i], v[i] (host arrays of device pointers; the tables are
  * copied into the launch, so they may be freed on return).  Same arithmetic as
  * ctattn_adam_update.  No counterpart in the reference, whose AdamOptimizer::step launches one
  * adamUpdateKernel per tensor (AdamOptimizer.cu:90); used by the optimizer classes here.
  */
-CTATTN_API int ctattn_adam_update_multi(int count, void *const *param, const void *const *grad,
-                                        float *const *m, float *const *v, const int64_t *n,
-                                        float lr, float beta1, float beta2, float eps,
-                                        float weight_decay, int64_t step, int decoupled,
-                                        void *stream);
+CTATTN_API int ctattn_adam_update_multi(int dtype, int count, void *const *param,
+                                        const void *const *grad, void *const *m, void *const *v,
+                                        const int64_t *n, double lr, double beta1, double beta2,
+                                        double eps, double weight_decay, int64_t step,
+                                        int decoupled, void *stream);
 
 /*
  * Zeroes `count` device buffers (bytes[i] bytes at ptr[i], 4-byte aligned; host tables) in one

@@ -1,5 +1,5 @@
 """fp16 and fp64 storage: the generic attention kernels, the fp16 / fp64 projection GEMMs and
-the Half / Double classes of the host module.
+the Half / Double (and BFloat) classes of the host module, up to a NanoGPT training step.
 
 fp64 runs accumulate in fp64 (LSE and delta are fp64 too), so they match the fp64 oracle to
 rounding: tolerance 1e-10 relative to the largest value.  fp16 stores IEEE binary16 and
@@ -11,8 +11,11 @@ import numpy as np
 import pytest
 import torch
 
+import torch.nn.functional as F
+
 from cudatransformer_amd import _capi as ct
 from cudatransformer_amd import cuda_transformer as ctm
+from cudatransformer_amd.nanogpt import NanoGPT, make_batch, native_parameter_name, to_native
 from oracle import attention_fp64 as ora
 from oracle import attention_layer_fp64 as lay
 
@@ -248,3 +251,152 @@ def test_attention_layer_half():
     layer = make_pybind_layer(ctm.AttentionHalf, ctm.HalfTensor, inp, h, d, True)
     y = layer(ctm.HalfTensor.fromNumpy(inp["x"]))
     rel_check(y.numpy(), want["y"], F16_REL, "f16 y")
+
+
+# ---- layers, losses, optimizers and NanoGPT in the other dtypes --------------------------
+
+TINY = dict(vocab=17, max_seq_len=32, d_model=32, n_heads=2, head_dim=16, mlp_dim=64, n_layers=2)
+
+
+@pytest.mark.gpu
+def test_double_layers_losses_optimizers():
+    say("double layers")
+    rng = np.random.default_rng(400)
+    x = rng.standard_normal((3, 10, 24))
+    dy = rng.standard_normal((3, 10, 40))
+    w = rng.standard_normal((40, 24)) * 0.2
+    b = rng.standard_normal(40)
+    lin = ctm.LinearDouble(24, 40)
+    lin.setParameters({"weights": ctm.DoubleTensor.fromNumpy(w), "biases": ctm.DoubleTensor.fromNumpy(b)})
+    tx, tdy = ctm.DoubleTensor.fromNumpy(x), ctm.DoubleTensor.fromNumpy(dy)
+    rel_check(lin(tx).numpy(), x @ w.T + b, F64_REL, "linear y")
+    rel_check(lin.backward(tx, tdy).numpy(), dy @ w, F64_REL, "linear dx")
+    g = lin.getGradients()
+    rel_check(g["weights"].numpy(), dy.reshape(-1, 40).T @ x.reshape(-1, 24), F64_REL, "linear dW")
+    rel_check(g["biases"].numpy(), dy.sum((0, 1)), F64_REL, "linear db")
+
+    sgd = ctm.DoubleSGDOptimizer(lin.getParameters(), 0.1)
+    sgd.step(g)
+    # one fused multiply-add per element: within an fp64 ulp of the two-step numpy result
+    rel_check(lin.getWeights().numpy(), w - 0.1 * g["weights"].numpy(), 1e-15, "sgd", floor=1.0)
+
+    ty = ctm.DoubleTensor.fromNumpy(x @ w.T)
+    ln = ctm.LayerNormDouble(40, 1e-5)
+    x64 = torch.from_numpy(x @ w.T).requires_grad_(True)
+    ref = F.layer_norm(x64, (40,), eps=1e-5)
+    ref.backward(torch.from_numpy(dy))
+    rel_check(ln(ty).numpy(), ref.detach().numpy(), F64_REL, "layernorm y")
+    rel_check(ln.backward(ty, tdy).numpy(), x64.grad.numpy(), F64_REL, "layernorm dx")
+
+    gelu = ctm.GELUDouble(40)
+    x64 = torch.from_numpy(x @ w.T).requires_grad_(True)
+    ref = F.gelu(x64, approximate="tanh")
+    ref.backward(torch.from_numpy(dy))
+    rel_check(gelu(ty).numpy(), ref.detach().numpy(), F64_REL, "gelu y")
+    rel_check(gelu.backward(ty, tdy).numpy(), x64.grad.numpy(), F64_REL, "gelu dx")
+
+    mse = ctm.DoubleMSELoss()
+    loss = mse(ty, tdy).numpy()
+    assert loss.shape == (3, 10) and loss.dtype == np.float64
+    rel_check(loss, ((x @ w.T - dy) ** 2).mean(-1), F64_REL, "mse")
+    rel_check(mse.backward(ty, tdy).numpy(), 2 * (x @ w.T - dy) / 40, F64_REL, "mse grad")
+
+    ck = ctm.CheckpointDouble()
+    assert isinstance(ck, ctm.DoubleCheckpointLayer)
+    np.testing.assert_array_equal(ck(ty).numpy(), x @ w.T)
+    np.testing.assert_array_equal(ck.backward(ty, tdy).numpy(), dy)
+    ck.clear()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("suffix", ["Half", "BFloat"])
+def test_narrow_layers_and_losses(suffix):
+    say(f"{suffix} layers")
+    tensor = getattr(ctm, f"{suffix}Tensor")
+    rnd = ora.round_to_f16 if suffix == "Half" else ora.round_to_bf16
+    rel = F16_REL if suffix == "Half" else 2e-2
+    rng = np.random.default_rng(401)
+    x = rnd(rng.standard_normal((4, 9, 48)))
+    dy = rnd(rng.standard_normal((4, 9, 48)))
+    tx, tdy = tensor.fromNumpy(x), tensor.fromNumpy(dy)
+    ln = getattr(ctm, f"LayerNorm{suffix}")(48)
+    x64 = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
+    ref = F.layer_norm(x64, (48,), eps=1e-5)
+    ref.backward(torch.from_numpy(dy.astype(np.float64)))
+    rel_check(ln(tx).numpy(), ref.detach().numpy(), rel, "layernorm y")
+    rel_check(ln.backward(tx, tdy).numpy(), x64.grad.numpy(), 2 * rel, "layernorm dx")
+    mse = getattr(ctm, f"{suffix}MSELoss")()
+    loss = mse(tx, tdy).numpy()
+    assert loss.dtype == np.float32
+    rel_check(loss, ((x.astype(np.float64) - dy) ** 2).mean(-1), 1e-5, "mse")
+    sm = getattr(ctm, f"{suffix}Softmax")(0.5)
+    p = sm(tx).numpy()
+    rel_check(p, torch.softmax(torch.from_numpy(x.astype(np.float64)) / 0.5, -1).numpy(), rel, "softmax")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("suffix", ["Double", "Half", "BFloat"])
+def test_nanogpt_step_other_dtypes(suffix):
+    """One forward + backward of the native NanoGPT in each dtype against the fp64 torch
+    model: fp64 to rounding; 16-bit dtypes by the loss, the probabilities and the direction
+    of every gradient (cosine similarity).  The 16-bit runs use weights 4x the default
+    initialisation: at 0.02 the query / key gradients (about 4e-6) fall below fp16's normal
+    range, which no loss-scale-free fp16 training step can resolve."""
+    say(f"nanogpt {suffix}")
+    ref = NanoGPT(**TINY, causal=True, activation="gelu", attention="sdpa").init_weights(7).double()
+    if suffix != "Double":
+        with torch.no_grad():
+            for prm in ref.parameters():
+                prm.mul_(4.0)
+    nat = to_native(ref, dtype=suffix)
+    ids, tgt = make_batch(4, 32, TINY["vocab"], seed=5)
+    ids_t = ctm.IntTensor.fromNumpy(ids.numpy().astype(np.int32))
+    tgt_t = ctm.IntTensor.fromNumpy(tgt.numpy().astype(np.int32))
+    probs = nat.forward(ids_t)
+    loss = nat.loss(probs, tgt_t).numpy()
+    assert loss.dtype == (np.float64 if suffix == "Double" else np.float32)
+    ref.zero_grad(set_to_none=True)
+    loss_ref = ref.loss(ids, tgt)
+    loss_ref.backward()
+    loss_ref = float(loss_ref.detach())
+    with torch.no_grad():
+        p_ref = torch.softmax(ref(ids), -1).numpy()
+    tol = {"Double": 1e-10, "Half": 5e-3, "BFloat": 3e-2}[suffix]
+    assert abs(loss.sum() - loss_ref) <= tol * abs(loss_ref)
+    assert np.abs(probs.numpy() - p_ref).max() <= tol
+    nat.zeroGrad()
+    nat.backward(ids_t, probs, tgt_t)
+    grads = nat.getGradients()
+    for n, prm in ref.named_parameters():
+        g = grads[native_parameter_name(n)].numpy().astype(np.float64).ravel()
+        r = prm.grad.numpy().ravel()
+        if suffix == "Double":
+            rel_check(g, r, 1e-9, n, floor=1e-6)  # floor: the key-bias gradient is zero in exact arithmetic
+        elif np.abs(r).max() > 1e-9:  # the key-bias gradient is zero in exact arithmetic
+            cos = float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r) + 1e-300))
+            assert cos >= (0.999 if suffix == "Half" else 0.99), (n, cos)
+
+
+@pytest.mark.gpu
+def test_double_adam_training_matches_torch():
+    say("nanogpt double adam")
+    ref = NanoGPT(**TINY, causal=True, activation="relu", attention="sdpa").init_weights(11).double()
+    nat = to_native(ref, dtype="Double")
+    ids, tgt = make_batch(4, 32, TINY["vocab"], seed=12)
+    ids_np, tgt_np = ids.numpy().astype(np.int32), tgt.numpy().astype(np.int32)
+    opt = ctm.DoubleAdamWOptimizer(nat.getParameters(), lr=3e-3, decay=0.01)
+    opt_ref = torch.optim.AdamW(ref.parameters(), lr=3e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    for _ in range(6):
+        probs = nat.forward(ids_np)
+        loss = float(nat.loss(probs, tgt_np).numpy().sum())
+        nat.zeroGrad()
+        nat.backward(ids_np, probs, tgt_np)
+        opt.step(nat.getGradients())
+        ref.zero_grad(set_to_none=True)
+        loss_ref = ref.loss(ids, tgt)
+        loss_ref.backward()
+        opt_ref.step()
+        assert abs(loss - float(loss_ref.detach())) <= 1e-9 * abs(float(loss_ref.detach()))
+    for n, prm in ref.named_parameters():
+        rel_check(nat.getParameters()[native_parameter_name(n)].numpy(), prm.detach().numpy(), 1e-9, n, floor=1.0)
+

@@ -6,8 +6,9 @@ sigmoid / tanh_kernels.cu, embedding_kernels.cu, loss_kernels.cu, adam_kernels.c
 float64 formulas here are the textbook definitions those kernels implement (GELU in its tanh
 form, LayerNorm with the biased variance and eps inside the square root, softmax with a
 temperature, cross-entropy -log p[target] / N).  Tolerances are stated per test: fp32
-storage is held to a few fp32 ulps of the result's scale, bf16 storage to bf16 rounding of
-the inputs and output.  Integer work (embedding lookup) is bit-exact.
+storage is held to a few fp32 ulps of the result's scale, bf16 and fp16 storage to their
+rounding of the inputs and output, fp64 storage (fp64 arithmetic) to 1e-12 of the result's
+scale.  Integer work (embedding lookup) is bit-exact.
 """
 import math
 
@@ -46,7 +47,14 @@ def _close(got, ref, rel, what, abs_floor=0.0):
     assert err <= rel * scale + abs_floor, f"{what}: max err {err:.3e} vs scale {scale:.3e} (rel {rel})"
 
 
-TOL = {torch.float32: 2e-5, torch.bfloat16: 1.6e-2}
+TOL = {torch.float32: 2e-5, torch.bfloat16: 1.6e-2, torch.float16: 2e-3, F64: 1e-12}
+DTYPES = [torch.float32, torch.bfloat16, torch.float16, F64]
+DT_IDS = ["f32", "bf16", "f16", "f64"]
+
+
+def _stat_tol(dtype):
+    """Tolerance of a statistic (row mean, rstd, loss): fp64 for fp64 storage, else fp32."""
+    return TOL[F64] if dtype == F64 else TOL[torch.float32]
 
 
 # ---- linear --------------------------------------------------------------------------------
@@ -54,7 +62,7 @@ TOL = {torch.float32: 2e-5, torch.bfloat16: 1.6e-2}
 LINEAR_SHAPES = [(1, 1, 1), (37, 130, 65), (256, 384, 384), (300, 65, 1536), (64, 4, 8)]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("mnk", LINEAR_SHAPES)
 @pytest.mark.parametrize("bias", [True, False])
 def test_linear_fwd_bwd(dtype, mnk, bias):
@@ -98,7 +106,7 @@ def test_linear_bwd_skips_and_empty():
 # ---- layernorm -----------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("nd", [(1, 32), (7, 65), (300, 384), (33, 1536)])
 def test_layernorm_fwd_bwd(dtype, nd):
     n, d = nd
@@ -120,8 +128,9 @@ def test_layernorm_fwd_bwd(dtype, nd):
     ref = F.layer_norm(x64, (d,), g64, b64, 1e-5)
     ref.backward(_as64(dy, dtype))
     _close(y, ref.detach(), TOL[dtype], "y")
-    _close(mean, x64.detach().mean(-1), TOL[torch.float32], "mean")
-    _close(rstd, 1 / torch.sqrt(x64.detach().var(-1, unbiased=False) + 1e-5), TOL[torch.float32], "rstd")
+    assert mean.dtype == rstd.dtype == _capi._stat_dtype(dtype)
+    _close(mean, x64.detach().mean(-1), _stat_tol(dtype), "mean")
+    _close(rstd, 1 / torch.sqrt(x64.detach().var(-1, unbiased=False) + 1e-5), _stat_tol(dtype), "rstd")
     _close(dx, x64.grad, TOL[dtype] * 2, "dx")
     _close(dg, _as64(dg0, dtype) + g64.grad, TOL[dtype] * 2, "dgamma")
     _close(db, _as64(db0, dtype) + b64.grad, TOL[dtype] * 2, "dbeta")
@@ -150,7 +159,7 @@ ACTS = {
 }
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("kind", sorted(ACTS))
 def test_activation_fwd_bwd(dtype, kind):
     n = 10007
@@ -176,7 +185,7 @@ def test_activation_rejects_unknown_kind():
 # ---- embeddings ----------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 def test_embedding_fwd_is_exact(dtype):
     b, t, e, vocab, max_len = 3, 50, 96, 65, 64
     ids = torch.randint(0, vocab, (b, t), generator=_gen(40), dtype=torch.int32)
@@ -188,31 +197,48 @@ def test_embedding_fwd_is_exact(dtype):
     only_pos = _capi.embedding_fwd(ids.to(DEV), None, pos.to(DEV))
     torch.cuda.synchronize()
     valid = (ids >= 0) & (ids < vocab)
-    rows = torch.where(valid[..., None], tok.float()[ids.clamp(0, vocab - 1).long()], torch.zeros(()))
+    # Sums of two stored values are exact in fp64 and in the fp32 the narrow kernels add in, so
+    # the rounded fp64 sum is the kernel's result bit for bit.
+    rows = torch.where(valid[..., None], tok.double()[ids.clamp(0, vocab - 1).long()], torch.zeros((), dtype=F64))
     ref_tok = rows
-    ref_pos = pos.float()[:t].expand(b, t, e)
-    assert torch.equal(only_tok.float().cpu(), ref_tok.to(dtype).float())
-    assert torch.equal(only_pos.float().cpu(), ref_pos)
-    assert torch.equal(got.float().cpu(), (ref_tok + ref_pos).to(dtype).float())
+    ref_pos = pos.double()[:t].expand(b, t, e)
+    assert torch.equal(only_tok.double().cpu(), ref_tok.to(dtype).double())
+    assert torch.equal(only_pos.double().cpu(), ref_pos)
+    assert torch.equal(got.double().cpu(), (ref_tok + ref_pos).to(dtype).double())
 
 
-def test_embedding_bwd():
+# Token-gradient rows collect about 8 contributions each here; every atomic add rounds to the
+# storage type, so 16-bit tables are held to a few roundings of that many adds.
+EMB_BWD_TOL = {torch.float32: 1e-6, torch.bfloat16: 4e-2, torch.float16: 5e-3, F64: 1e-12}
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_embedding_bwd(dtype):
     b, t, e, vocab, max_len = 4, 33, 40, 17, 40
     ids = torch.randint(0, vocab, (b, t), generator=_gen(43), dtype=torch.int32)
     ids[3, 3] = -2
     dout = _randn((b, t, e), 44)
     dtok0, dpos0 = _randn((vocab, e), 45), _randn((max_len, e), 46)
-    dtok, dpos = _dev(dtok0, torch.float32), _dev(dpos0, torch.float32)
-    _capi.embedding_bwd(ids.to(DEV), _dev(dout, torch.float32), dtok, dpos, vocab=vocab)
+    dtok, dpos = _dev(dtok0, dtype), _dev(dpos0, dtype)
+    _capi.embedding_bwd(ids.to(DEV), _dev(dout, dtype), dtok, dpos, vocab=vocab)
     torch.cuda.synchronize()
-    d32 = dout.float().double()
-    ref_tok = dtok0.float().double().clone()
+    d64 = _as64(dout, dtype)
+    ref_tok = _as64(dtok0, dtype).clone()
     valid = ids.flatten() >= 0
-    ref_tok.index_add_(0, ids.flatten()[valid].long(), d32.reshape(-1, e)[valid])
-    ref_pos = dpos0.float().double().clone()
-    ref_pos[:t] += d32.sum(0)
-    _close(dtok, ref_tok, 1e-6, "dtok")
-    _close(dpos, ref_pos, 1e-6, "dpos")
+    ref_tok.index_add_(0, ids.flatten()[valid].long(), d64.reshape(-1, e)[valid])
+    ref_pos = _as64(dpos0, dtype).clone()
+    ref_pos[:t] += d64.sum(0)
+    _close(dtok, ref_tok, EMB_BWD_TOL[dtype], "dtok")
+    _close(dpos, ref_pos, max(EMB_BWD_TOL[dtype], TOL[dtype]), "dpos")
+    assert torch.equal(dpos[t:].cpu(), _dev(dpos0, dtype)[t:].cpu())  # rows past T untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_embedding_bwd_16bit_needs_even_width(dtype):
+    ids = torch.zeros((1, 2), dtype=torch.int32, device=DEV)
+    dout = torch.zeros((1, 2, 5), dtype=dtype, device=DEV)
+    with pytest.raises(RuntimeError, match="even embedding width"):
+        _capi.embedding_bwd(ids, dout, torch.zeros((3, 5), dtype=dtype, device=DEV), None)
 
 
 def test_embedding_rejects_long_sequence():
@@ -225,7 +251,7 @@ def test_embedding_rejects_long_sequence():
 # ---- softmax / cross-entropy ---------------------------------------------------------------
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("nv", [(1, 1), (37, 65), (4, 50257)])
 @pytest.mark.parametrize("temp", [1.0, 0.7])
 def test_softmax_fwd_bwd(dtype, nv, temp):
@@ -238,17 +264,19 @@ def test_softmax_fwd_bwd(dtype, nv, temp):
     z64 = _as64(z, dtype).requires_grad_(True)
     ref = torch.softmax(z64 / temp, -1)
     ref.backward(_as64(dp, dtype))
-    tol = 1e-5 if dtype == torch.float32 else TOL[dtype]
+    tol = {torch.float32: 1e-5, F64: 1e-12}.get(dtype, TOL[dtype])
     _close(p, ref.detach(), tol, "p")
-    assert torch.allclose(p.double().sum(-1).cpu(), torch.ones(n, dtype=F64), atol=1e-5 if dtype == torch.float32 else 2e-2)
+    sum_atol = {torch.float32: 1e-5, F64: 1e-12}.get(dtype, 2e-2)
+    assert torch.allclose(p.double().sum(-1).cpu(), torch.ones(n, dtype=F64), atol=sum_atol)
     # The backward works from the forward's p; compare with the autograd gradient at z.
     _close(dz, z64.grad, tol * 4, "dz")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 def test_cross_entropy_and_fused_backward(dtype):
     n, v, temp = 300, 65, 0.8
-    z = _randn((n, v), 60, 2.0)
+    # fp16 keeps the probabilities clear of its subnormal range (smaller logit spread).
+    z = _randn((n, v), 60, 1.0 if dtype == torch.float16 else 2.0)
     tgt = torch.randint(0, v, (n,), generator=_gen(61), dtype=torch.int32)
     tgt[5], tgt[77] = -1, v  # outside [0, V): zero loss, zero gradient
     p = _dev(torch.softmax(z / temp, -1), dtype)
@@ -260,7 +288,8 @@ def test_cross_entropy_and_fused_backward(dtype):
     valid = (tgt >= 0) & (tgt < v)
     safe = tgt.clamp(0, v - 1).long()
     ref_loss = torch.where(valid, -torch.log(p64.gather(1, safe[:, None])[:, 0]) / n, torch.zeros((), dtype=F64))
-    _close(loss, ref_loss, 1e-6, "loss")
+    assert loss.dtype == _capi._stat_dtype(dtype)
+    _close(loss, ref_loss, 1e-12 if dtype == F64 else 1e-6, "loss")
     onehot = F.one_hot(safe, v).to(F64) * valid[:, None]
     ref_dp = torch.where(onehot > 0, -1.0 / (p64 * n), torch.zeros((), dtype=F64))
     _close(dp, ref_dp, TOL[dtype], "dp")
@@ -276,23 +305,47 @@ def test_cross_entropy_and_fused_backward(dtype):
 # ---- Adam / AdamW --------------------------------------------------------------------------
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, F64], ids=["f32", "f64"])
 @pytest.mark.parametrize("decoupled", [False, True])
-def test_adam_matches_torch(decoupled):
+def test_adam_matches_torch(dtype, decoupled):
     n, lr, wd = 5000, 1e-2, 0.05
     p0 = _randn((n,), 70)
     grads = [_randn((n,), 71 + s) for s in range(4)]
-    p = _dev(p0, torch.float32)
-    m = torch.zeros(n, device=DEV)
-    v = torch.zeros(n, device=DEV)
-    ref = p0.float().double().clone().requires_grad_(True)
+    p = _dev(p0, dtype)
+    m = torch.zeros(n, device=DEV, dtype=_capi._stat_dtype(dtype))
+    v = torch.zeros(n, device=DEV, dtype=_capi._stat_dtype(dtype))
+    ref = _as64(p0, dtype).clone().requires_grad_(True)
     opt_cls = torch.optim.AdamW if decoupled else torch.optim.Adam
     opt = opt_cls([ref], lr=lr, betas=(0.9, 0.999), eps=1e-8, weight_decay=wd)
     for step, g in enumerate(grads, start=1):
-        _capi.adam_update(p, _dev(g, torch.float32), m, v, step, lr=lr, weight_decay=wd, decoupled=decoupled)
-        ref.grad = g.float().double()
+        _capi.adam_update(p, _dev(g, dtype), m, v, step, lr=lr, weight_decay=wd, decoupled=decoupled)
+        ref.grad = _as64(g, dtype)
         opt.step()
     torch.cuda.synchronize()
-    assert float((p.double().cpu() - ref.detach()).abs().max()) <= 2e-6
+    assert float((p.double().cpu() - ref.detach()).abs().max()) <= (2e-6 if dtype == torch.float32 else 1e-13)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_adam_16bit_rounds_one_fp32_update(dtype):
+    """16-bit parameters: fp32 moments and arithmetic, the parameter rounded once per step."""
+    n, lr, wd = 3000, 1e-2, 0.05
+    p = _dev(_randn((n,), 72), dtype)
+    g = _dev(_randn((n,), 73), dtype)
+    p64, g64 = _as64(p, dtype), _as64(g, dtype)
+    m = torch.zeros(n, device=DEV)
+    v = torch.zeros(n, device=DEV)
+    _capi.adam_update(p, g, m, v, 1, lr=lr, weight_decay=wd)
+    torch.cuda.synchronize()
+    # The kernel holds the betas in fp32 (their bias corrections come from the exact betas).
+    b1, b2 = float(torch.tensor(0.9, dtype=torch.float32)), float(torch.tensor(0.999, dtype=torch.float32))
+    gd = g64 + wd * p64
+    m1, v1 = (1 - b1) * gd, (1 - b2) * gd * gd
+    ref = p64 - lr * (m1 / 0.1) / (torch.sqrt(v1 / 0.001) + 1e-8)
+    _close(m, m1, 1e-6, "m")
+    _close(v, v1, 1e-6, "v")
+    # one rounding of the fp32 result to the storage type: within one ulp of the exact update
+    ulp = ref.abs() * (2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10)
+    assert bool(((p.double().cpu() - ref).abs() <= ulp + 1e-30).all())
 
 
 def test_adam_rejects_step_zero():
@@ -301,13 +354,14 @@ def test_adam_rejects_step_zero():
         _capi.adam_update(t, t, t.clone(), t.clone(), 0)
 
 
-def test_adam_multi_matches_single_bitwise():
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+def test_adam_multi_matches_single_bitwise(dtype):
     """One launch per 32 tensors gives exactly the per-tensor update (same arithmetic)."""
     sizes = [1, 3, 4096, 4097, 70000] + [5 + 13 * i for i in range(35)]  # 40 tensors: two launches
-    ps = [_dev(_randn((n,), 80 + i), torch.float32) for i, n in enumerate(sizes)]
-    gs = [_dev(_randn((n,), 180 + i), torch.float32) for i, n in enumerate(sizes)]
-    ms = [torch.zeros(n, device=DEV) for n in sizes]
-    vs = [torch.zeros(n, device=DEV) for n in sizes]
+    ps = [_dev(_randn((n,), 80 + i), dtype) for i, n in enumerate(sizes)]
+    gs = [_dev(_randn((n,), 180 + i), dtype) for i, n in enumerate(sizes)]
+    ms = [torch.zeros(n, device=DEV, dtype=_capi._stat_dtype(dtype)) for n in sizes]
+    vs = [torch.zeros(n, device=DEV, dtype=_capi._stat_dtype(dtype)) for n in sizes]
     ref = [(p.clone(), m.clone(), v.clone()) for p, m, v in zip(ps, ms, vs)]
     for decoupled in (False, True):
         for step in (1, 2):
@@ -329,3 +383,22 @@ def test_zero_multi_clears_exactly_the_given_bytes():
     for o, n in spans:
         expect[o:o + n] = 0
     assert torch.equal(arena.cpu(), expect)
+
+
+# ---- mean squared error --------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("shape", [(1, 1), (37, 65), (3, 5, 130)])
+def test_mse_loss(dtype, shape):
+    x = _dev(_randn(shape, 90), dtype)
+    y = _dev(_randn(shape, 91), dtype)
+    loss = _capi.mse_loss_fwd(x, y)
+    dx = _capi.mse_loss_bwd(x, y)
+    torch.cuda.synchronize()
+    x64 = _as64(x, dtype).requires_grad_(True)
+    ref = ((x64 - _as64(y, dtype)) ** 2).mean(-1)
+    ref.sum().backward()
+    assert loss.shape == shape[:-1] and loss.dtype == _capi._stat_dtype(dtype)
+    _close(loss, ref.detach(), _stat_tol(dtype), "loss")
+    _close(dx, x64.grad, TOL[dtype], "dx")
