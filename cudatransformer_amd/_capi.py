@@ -102,6 +102,15 @@ def load() -> ctypes.CDLL:
         "ctattn_adam_update": ([c_int, vp, vp, vp, vp, i64] + [f64] * 5 + [i64, c_int, vp], c_int),
         "ctattn_adam_update_multi": ([c_int, c_int] + [vp] * 5 + [f64] * 5 + [i64, c_int, vp], c_int),
         "ctattn_zero_multi": ([c_int, vp, vp, vp], c_int),
+        "ctattn_tensor_cast": ([c_int, vp, c_int, vp, i64, vp], c_int),
+        "ctattn_tensor_binary": ([c_int, c_int, vp, c_int, vp, vp, c_int, vp, vp, vp], c_int),
+        "ctattn_tensor_scalar": ([c_int, c_int, vp, f64, c_int, vp, i64, vp], c_int),
+        "ctattn_tensor_unary": ([c_int, c_int, vp, vp, i64, vp], c_int),
+        "ctattn_tensor_reduce_workspace_bytes": ([c_int, i64, i64, i64], i64),
+        "ctattn_tensor_reduce": ([c_int, c_int, vp, i64, i64, i64, vp, vp, i64, vp], c_int),
+        "ctattn_tensor_permute": ([c_int, vp, c_int, vp, vp, vp, vp], c_int),
+        "ctattn_tensor_kron": ([c_int, vp, vp, c_int, vp, vp, vp, vp], c_int),
+        "ctattn_tensor_matmul": ([c_int, vp, vp, vp] + [i64] * 5 + [vp], c_int),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)

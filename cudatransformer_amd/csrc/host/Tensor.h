@@ -118,32 +118,45 @@ template <> struct DTypeCode<float> { static constexpr int value = CTATTN_F32; }
 template <> struct DTypeCode<bf16> { static constexpr int value = CTATTN_BF16; };
 template <> struct DTypeCode<f16> { static constexpr int value = CTATTN_F16; };
 template <> struct DTypeCode<double> { static constexpr int value = CTATTN_F64; };
+template <> struct DTypeCode<int32_t> { static constexpr int value = CTATTN_I32; };
+template <> struct DTypeCode<int64_t> { static constexpr int value = CTATTN_I64; };
+template <> struct DTypeCode<int16_t> { static constexpr int value = CTATTN_I16; };
+template <> struct DTypeCode<int8_t> { static constexpr int value = CTATTN_I8; };
+template <> struct DTypeCode<bool> { static constexpr int value = CTATTN_BOOL; };
 
 // Type of the statistics the kernels keep beside a tensor of DType (row statistics, LSE,
 // losses, optimizer moments): double for double, float for every narrower type.
 template <typename DType> using StatOf = std::conditional_t<std::is_same_v<DType, double>, double, float>;
 
-template <typename DType> inline DType fromFloat(float x);
-template <> inline float fromFloat<float>(float x) { return x; }
-template <> inline bf16 fromFloat<bf16>(float x) { return bf16::fromFloat(x); }
-template <> inline f16 fromFloat<f16>(float x) { return f16::fromFloat(x); }
-template <> inline double fromFloat<double>(float x) { return double(x); }
-template <> inline int32_t fromFloat<int32_t>(float x) { return int32_t(x); }
-inline float toFloat(float x) { return x; }
-inline float toFloat(bf16 x) { return x.toFloat(); }
-inline float toFloat(f16 x) { return x.toFloat(); }
-inline float toFloat(double x) { return float(x); }
-inline float toFloat(int32_t x) { return float(x); }
-// Scalars given or returned at full precision: exact for double tensors, rounded once to the
-// storage type otherwise.
-template <typename DType> inline DType fromDouble(double x) {
-    if constexpr (std::is_same_v<DType, double>) return x;
-    else if constexpr (std::is_same_v<DType, int32_t>) return int32_t(x);
-    else return fromFloat<DType>(float(x));
+// Host-side element type of a DType buffer (std::vector<bool> packs bits, so bool tensors
+// travel as bytes).
+template <typename DType> using HostElem = std::conditional_t<std::is_same_v<DType, bool>, uint8_t, DType>;
+
+template <typename V> constexpr bool kHalfLike = std::is_same_v<V, bf16> || std::is_same_v<V, f16>;
+
+// Scalar conversions on the host: round to nearest even into bf16 / f16, truncation into
+// integers, x != 0 into bool.
+template <typename DType> inline DType fromFloat(float x) {
+    if constexpr (std::is_same_v<DType, bf16>) return bf16::fromFloat(x);
+    else if constexpr (std::is_same_v<DType, f16>) return f16::fromFloat(x);
+    else if constexpr (std::is_same_v<DType, bool>) return x != 0.f;
+    else return DType(x);
 }
-inline double toDouble(double x) { return x; }
-inline double toDouble(int32_t x) { return x; }
-template <typename DType> inline double toDouble(DType x) { return double(toFloat(x)); }
+template <typename V> inline float toFloat(V x) {
+    if constexpr (kHalfLike<V>) return x.toFloat();
+    else return float(x);
+}
+// Scalars given or returned at full precision: exact for double (and integer) tensors,
+// rounded once to the storage type otherwise.
+template <typename DType> inline DType fromDouble(double x) {
+    if constexpr (kHalfLike<DType> || std::is_same_v<DType, float>) return fromFloat<DType>(float(x));
+    else if constexpr (std::is_same_v<DType, bool>) return x != 0.0;
+    else return DType(x);
+}
+template <typename V> inline double toDouble(V x) {
+    if constexpr (kHalfLike<V>) return double(x.toFloat());
+    else return double(x);
+}
 
 // Caching device allocator for the host layer's buffers.  A freed block goes to a free list
 // keyed by its rounded size and is handed out again to the next request of that size, with
@@ -281,15 +294,15 @@ public:
         if constexpr (std::is_same_v<DType, float>) {
             return fromPointer(shape, host);
         } else {
-            std::vector<DType> tmp(n);
-            for (size_t i = 0; i < n; ++i) tmp[i] = fromFloat<DType>(host[i]);
-            return fromPointer(shape, tmp.data());
+            std::vector<HostElem<DType>> tmp(n);
+            for (size_t i = 0; i < n; ++i) tmp[i] = HostElem<DType>(fromFloat<DType>(host[i]));
+            return fromPointer(shape, reinterpret_cast<const DType *>(tmp.data()));
         }
     }
 
     // Device values on the host in their own type (waits for the stream).
-    std::vector<DType> toHost() const {
-        std::vector<DType> raw(size_);
+    std::vector<HostElem<DType>> toHost() const {
+        std::vector<HostElem<DType>> raw(size_);
         if (size_ > 0) {
             hipCheck(hipMemcpyAsync(raw.data(), data_.get(), size_ * sizeof(DType), hipMemcpyDeviceToHost,
                                     Runtime::stream()),
@@ -301,13 +314,7 @@ public:
 
     // Device values as floats on the host (waits for the stream).
     std::vector<float> toFloats() const {
-        std::vector<DType> raw(size_);
-        if (size_ > 0) {
-            hipCheck(hipMemcpyAsync(raw.data(), data_.get(), size_ * sizeof(DType), hipMemcpyDeviceToHost,
-                                    Runtime::stream()),
-                     "hipMemcpyAsync D2H");
-            Runtime::synchronize();
-        }
+        std::vector<HostElem<DType>> raw = toHost();
         std::vector<float> out(size_);
         for (size_t i = 0; i < size_; ++i) out[i] = toFloat(raw[i]);
         return out;
@@ -339,7 +346,7 @@ public:
         if (bytewise) {
             hipCheck(hipMemsetAsync(data_.get(), first, size_ * sizeof(DType), Runtime::stream()), "hipMemsetAsync");
         } else {
-            std::vector<DType> tmp(size_, v);
+            std::vector<HostElem<DType>> tmp(size_, HostElem<DType>(v));
             hipCheck(hipMemcpyAsync(data_.get(), tmp.data(), size_ * sizeof(DType), hipMemcpyHostToDevice,
                                     Runtime::stream()),
                      "hipMemcpyAsync fill");

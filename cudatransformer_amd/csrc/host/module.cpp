@@ -39,19 +39,17 @@
 #include "ModuleLayer.h"
 #include "NanoGPT.h"
 #include "Tensor.h"
+#include "TensorOps.h"
 
 namespace py = pybind11;
 using namespace ct;
 
 namespace {
 
-// NumPy element type of a tensor: int32 for ids, float64 for double, float32 for the float,
-// bf16 and f16 tensors (numpy has no bfloat16; f16 values are rounded to nearest even).
-template <typename DType>
-using NpType = std::conditional_t<std::is_same_v<DType, int32_t>, int32_t,
-                                  std::conditional_t<std::is_same_v<DType, double>, double, float>>;
-template <typename DType>
-constexpr bool kRawNumpy = std::is_same_v<DType, int32_t> || std::is_same_v<DType, double>;
+// NumPy element type of a tensor: its own type, except float32 for the bf16 and f16 tensors
+// (numpy has no bfloat16; both are rounded to nearest even on upload).
+template <typename DType> using NpType = std::conditional_t<kHalfLike<DType>, float, DType>;
+template <typename DType> constexpr bool kRawNumpy = !kHalfLike<DType>;
 using IdArray = py::array_t<int32_t, py::array::c_style | py::array::forcecast>;
 
 template <typename DType>
@@ -69,7 +67,7 @@ py::array_t<NpType<DType>> tensorToNumpy(const Tensor<DType> &t) {
     std::vector<py::ssize_t> shape(t.shape().begin(), t.shape().end());
     py::array_t<NpType<DType>> out(shape);
     if constexpr (kRawNumpy<DType>) {
-        std::vector<DType> host = t.toHost();
+        std::vector<HostElem<DType>> host = t.toHost();
         if (!host.empty()) std::memcpy(out.mutable_data(), host.data(), host.size() * sizeof(DType));
     } else {
         std::vector<float> host = t.toFloats();
@@ -90,9 +88,88 @@ std::vector<int32_t> idVector(const py::object &o) {
     return std::vector<int32_t>(a.data(), a.data() + a.size());
 }
 
+// The reference's Tensor methods beyond storage (cuda_transformer.cu:40-119): conversions,
+// arithmetic and comparison operators with tensors or Python numbers, reductions,
+// transpose, kron, matmul.
+template <typename DType>
+void declareTensorOps(py::class_<Tensor<DType>> &c) {
+    using T = Tensor<DType>;
+    c.def("float", [](const T &t) { return ops::cast<float>(t); }, "Casts to 32-bit float.")
+        .def("half", [](const T &t) { return ops::cast<f16>(t); }, "Casts to 16-bit float (FP16).")
+        .def("bfloat", [](const T &t) { return ops::cast<bf16>(t); }, "Casts to bfloat16.")
+        .def("double", [](const T &t) { return ops::cast<double>(t); }, "Casts to 64-bit float.")
+        .def("int", [](const T &t) { return ops::cast<int32_t>(t); }, "Casts to 32-bit int.")
+        .def("long", [](const T &t) { return ops::cast<int64_t>(t); }, "Casts to 64-bit int.")
+        .def("short", [](const T &t) { return ops::cast<int16_t>(t); }, "Casts to 16-bit int.")
+        .def("byte", [](const T &t) { return ops::cast<int8_t>(t); }, "Casts to 8-bit int (ByteTensor).")
+        .def("bool", [](const T &t) { return ops::cast<bool>(t); }, "Casts to boolean (x != 0).");
+    struct Arith {
+        const char *name, *rname;
+        int op;
+    };
+    for (const Arith a : {Arith{"__add__", "__radd__", CTATTN_OP_ADD}, Arith{"__sub__", "__rsub__", CTATTN_OP_SUB},
+                          Arith{"__mul__", "__rmul__", CTATTN_OP_MUL}, Arith{"__truediv__", "__rtruediv__", CTATTN_OP_DIV},
+                          Arith{"__mod__", "__rmod__", CTATTN_OP_MOD}}) {
+        const int op = a.op;
+        c.def(a.name, [op](const T &x, const T &y) { return ops::binary<DType>(x, y, op); }, py::is_operator());
+        c.def(a.name, [op](const T &x, double s) { return ops::scalar<DType>(x, s, op); }, py::is_operator());
+        c.def(a.rname, [op](const T &x, double s) { return ops::scalar<DType>(x, s, op, true); }, py::is_operator());
+    }
+    struct Cmp {
+        const char *name;
+        int op;
+    };
+    for (const Cmp a : {Cmp{"__eq__", CTATTN_OP_EQ}, Cmp{"__ne__", CTATTN_OP_NE}, Cmp{"__lt__", CTATTN_OP_LT},
+                        Cmp{"__le__", CTATTN_OP_LE}, Cmp{"__gt__", CTATTN_OP_GT}, Cmp{"__ge__", CTATTN_OP_GE}}) {
+        const int op = a.op;
+        c.def(a.name, [op](const T &x, const T &y) { return ops::binary<bool>(x, y, op); }, py::is_operator());
+        c.def(a.name, [op](const T &x, double s) { return ops::scalar<bool>(x, s, op); }, py::is_operator());
+    }
+    c.def("__neg__", [](const T &t) { return ops::unary(t, CTATTN_UN_NEG); }, py::is_operator())
+        .def("__matmul__", [](const T &a, const T &b) { return ops::matmul(a, b); }, py::is_operator())
+        .def("__rmatmul__", [](const T &a, const T &b) { return ops::matmul(b, a); }, py::is_operator())
+        .def("matmul", [](const T &a, const T &b) { return ops::matmul(a, b); }, py::arg("other"),
+             "Matrix product over the last two dimensions (batched over the leading ones).")
+        .def("kron", [](const T &a, const T &b) { return ops::kron(a, b); }, py::arg("other"),
+             "Kronecker product with a tensor of the same number of dimensions.")
+        .def("transpose", [](const T &t, const std::vector<size_t> &perm) { return ops::permute(t, perm); },
+             py::arg("perm"), "Returns a tensor with axes permuted according to perm.")
+        .def("transpose", [](const T &t, size_t a1, size_t a2) { return ops::transpose(t, a1, a2); },
+             py::arg("axis1"), py::arg("axis2"), "Returns a tensor with axis1 and axis2 swapped.")
+        .def("reduce", [](const T &t, const std::vector<size_t> &axes, ReductionOp op) { return ops::reduce(t, axes, op); },
+             py::arg("axes"), py::arg("op"), "Reduces the given axes with a ReductionOp.");
+    struct Red {
+        const char *name;
+        ReductionOp op;
+        const char *doc;
+    };
+    for (const Red r : {Red{"sum", ReductionOp::SUM, "Sums elements."}, Red{"mean", ReductionOp::MEAN, "Computes the mean."},
+                        Red{"max", ReductionOp::MAX, "Computes the maximum."},
+                        Red{"min", ReductionOp::MIN, "Computes the minimum."},
+                        Red{"manhattan", ReductionOp::NORM_L1, "L1 (Manhattan) norm; alias of norm_l1."},
+                        Red{"norm_l1", ReductionOp::NORM_L1, "L1 norm (sum of absolute values)."},
+                        Red{"norm", ReductionOp::NORM_L2, "L2 (Euclidean) norm; alias of norm_l2."},
+                        Red{"norm_l2", ReductionOp::NORM_L2, "L2 norm (square root of the sum of squares)."}}) {
+        const ReductionOp op = r.op;
+        c.def(r.name, [op](const T &t, int dim) { return ops::reduceDim(t, dim, op); }, py::arg("dim") = -1,
+              (std::string(r.doc) + " dim=-1 reduces the whole tensor to a one-element tensor.").c_str());
+    }
+    c.def("cpu",
+          [](const T &t) {
+              py::list out;
+              if constexpr (kHalfLike<DType>) {
+                  for (float v : t.toFloats()) out.append(v);
+              } else {
+                  for (auto v : t.toHost()) out.append(py::cast(DType(v)));
+              }
+              return out;
+          },
+          "Copies the tensor to the CPU and returns its values as a flat list.");
+}
+
 template <typename DType>
 void declareTensor(py::module_ &m, const std::string &suffix) {
-    py::class_<Tensor<DType>>(m, (suffix + "Tensor").c_str(),
+    auto cls = py::class_<Tensor<DType>>(m, (suffix + "Tensor").c_str(),
                               "N-dimensional GPU tensor. Assignments and copies are shallow (shared buffer); "
                               "call clone() to obtain an independent copy.")
         .def(py::init<>(), "Constructs an empty tensor with no allocated memory.")
@@ -101,11 +178,18 @@ void declareTensor(py::module_ &m, const std::string &suffix) {
         .def_static("fromNumpy", &tensorFromNumpy<DType>, py::arg("array"),
                     "Copies a NumPy array (cast to the tensor's NumPy type, C order) to a new GPU tensor.")
         .def("numpy", &tensorToNumpy<DType>,
-             "Copies the tensor to the CPU and returns it as a NumPy array (float32; int32 for IntTensor).")
+             "Copies the tensor to the CPU and returns it as a NumPy array (its own type; float32 for the "
+             "BFloat and Half tensors).")
         .def("shape", [](const Tensor<DType> &t) { return t.shape(); }, "Returns the tensor shape as a list of ints.")
         .def("size", &Tensor<DType>::size, "Number of elements.")
         .def("clone", &Tensor<DType>::clone, "Returns a deep copy with its own GPU buffer.")
-        .def("item", &Tensor<DType>::item, "Returns the value of a single-element tensor.")
+        .def("item",
+             [](const Tensor<DType> &t) -> py::object {
+                 if (t.size() != 1) throw std::invalid_argument("Tensor is not a scalar");
+                 if constexpr (kHalfLike<DType>) return py::float_(t.item());
+                 else return py::cast(DType(t.toHost()[0]));
+             },
+             "Returns the value of a single-element tensor.")
         .def("fill", &Tensor<DType>::fill, py::arg("value"), "Fills every element in place.")
         .def("reshape", &Tensor<DType>::reshape, py::arg("shape"),
              "Returns a view with a new shape (same element count, shared buffer).")
@@ -114,6 +198,7 @@ void declareTensor(py::module_ &m, const std::string &suffix) {
             for (size_t i = 0; i < t.nDim(); ++i) s += (i ? ", " : "") + std::to_string(t.shape(i));
             return s + "])";
         });
+    declareTensorOps<DType>(cls);
 }
 
 template <typename DType>
@@ -507,6 +592,13 @@ PYBIND11_MODULE(cuda_transformer, m) {
         .value("GELU", ActivationType::GELU, "tanh approximation")
         .value("Sigmoid", ActivationType::Sigmoid)
         .value("Tanh", ActivationType::Tanh);
+    py::enum_<ReductionOp>(m, "ReductionOp", "Reduction of Tensor.reduce.")
+        .value("SUM", ReductionOp::SUM)
+        .value("MEAN", ReductionOp::MEAN)
+        .value("MAX", ReductionOp::MAX)
+        .value("MIN", ReductionOp::MIN)
+        .value("NORM_L1", ReductionOp::NORM_L1)
+        .value("NORM_L2", ReductionOp::NORM_L2);
     py::enum_<SamplingMode>(m, "SamplingMode", "Next-token choice of NanoGPT.predict / sample / generate.")
         .value("Greedy", SamplingMode::Greedy)
         .value("Random", SamplingMode::Random)
@@ -518,6 +610,10 @@ PYBIND11_MODULE(cuda_transformer, m) {
     declareTensor<f16>(m, "Half");
     declareTensor<double>(m, "Double");
     declareTensor<int32_t>(m, "Int");
+    declareTensor<int64_t>(m, "Long");
+    declareTensor<int16_t>(m, "Short");
+    declareTensor<int8_t>(m, "Byte");
+    declareTensor<bool>(m, "Bool");
     declareFlashAttention<float>(m, "Float");
     declareFlashAttention<bf16>(m, "BFloat");
     declareFlashAttention<f16>(m, "Half");

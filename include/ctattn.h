@@ -38,7 +38,20 @@
 extern "C" {
 #endif
 
-enum ctattn_dtype { CTATTN_F32 = 0, CTATTN_BF16 = 1, CTATTN_F16 = 2, CTATTN_F64 = 3 };
+/* Storage types.  The attention, projection and layer entry points take the four floating
+ * types; the tensor operations at the end of this header take all of them (bool is one byte
+ * holding 0 or 1). */
+enum ctattn_dtype {
+    CTATTN_F32 = 0,
+    CTATTN_BF16 = 1,
+    CTATTN_F16 = 2,
+    CTATTN_F64 = 3,
+    CTATTN_I32 = 4,
+    CTATTN_I64 = 5,
+    CTATTN_I16 = 6,
+    CTATTN_I8 = 7,
+    CTATTN_BOOL = 8
+};
 
 /* Kernel selection policy (process-wide).
  *   AUTO           MFMA kernels where they apply (fastest).  The fp32 MFMA backward adds
@@ -367,6 +380,81 @@ CTATTN_API int ctattn_adam_update_multi(int dtype, int count, void *const *param
  * own cudaMemset, e.g. LinearLayer.cu zeroGrad); used by NanoGPT::zeroGrad here.
  */
 CTATTN_API int ctattn_zero_multi(int count, void *const *ptr, const int64_t *bytes, void *stream);
+
+/* ---- Tensor operations behind the Python Tensor classes ----
+ *
+ * Contiguous row-major device tensors of any ctattn_dtype.  Arithmetic runs in fp32 for
+ * bf16 / fp16 storage, fp64 for fp64 and int64 for the integer and bool types, rounded once
+ * to the storage type; integer division and remainder by zero give 0.  Asynchronous on
+ * `stream`, 0 or a hipError_t value.
+ */
+
+/* Element-wise operations: the arithmetic ones write the operand dtype, the comparisons
+ * (EQ .. GE) write bool.  MOD is the integer remainder (truncated) and 0 for floating types,
+ * as the reference's binaryOpKernel has it (tensor_kernels.cu:245). */
+enum ctattn_tensor_op {
+    CTATTN_OP_ADD = 0, CTATTN_OP_SUB = 1, CTATTN_OP_MUL = 2, CTATTN_OP_DIV = 3, CTATTN_OP_MOD = 4,
+    CTATTN_OP_EQ = 5, CTATTN_OP_NE = 6, CTATTN_OP_LT = 7, CTATTN_OP_LE = 8, CTATTN_OP_GT = 9,
+    CTATTN_OP_GE = 10
+};
+/* Unary maps (the reference's UnaryOp, tensor_kernels.cu:159-190; NEG / NOT of bool are the
+ * logical not). */
+enum ctattn_unary_op {
+    CTATTN_UN_NEG = 0, CTATTN_UN_NOT = 1, CTATTN_UN_INV = 2, CTATTN_UN_EXP = 3, CTATTN_UN_LOG = 4,
+    CTATTN_UN_SQR = 5, CTATTN_UN_SQRT = 6, CTATTN_UN_ABS = 7
+};
+/* Reductions (the reference's ReductionOp, tensor_kernels.cu:537-543). */
+enum ctattn_reduce_op {
+    CTATTN_RED_SUM = 0, CTATTN_RED_MEAN = 1, CTATTN_RED_MAX = 2, CTATTN_RED_MIN = 3,
+    CTATTN_RED_NORM_L1 = 4, CTATTN_RED_NORM_L2 = 5
+};
+
+/* dst = src converted element by element (round to nearest even for floating targets,
+ * truncation toward zero and wrap-around for integer targets, x != 0 for bool).  Replaces
+ * Tensor::to<NewDType> (Tensor.cu:267; castKernel). */
+CTATTN_API int ctattn_tensor_cast(int src_dtype, const void *src, int dst_dtype, void *dst, int64_t n,
+                                  void *stream);
+
+/* out = a op b with numpy broadcasting of shapes a_shape [a_ndim] and b_shape [b_ndim]
+ * (ndim <= 8, aligned at the last dimension); out has the broadcast shape.  Replaces
+ * Tensor::binary / Tensor::predicate (Tensor.cu:650-740; binaryOpKernel,
+ * binaryPredicateOpKernel). */
+CTATTN_API int ctattn_tensor_binary(int dtype, int op, const void *a, int a_ndim, const int64_t *a_shape,
+                                    const void *b, int b_ndim, const int64_t *b_shape, void *out,
+                                    void *stream);
+
+/* out[i] = a[i] op s (scalar_left = 0) or s op a[i] (scalar_left = 1), s converted to the
+ * storage type first.  Replaces the scalar Tensor::binary / predicate (Tensor.cu:742-790). */
+CTATTN_API int ctattn_tensor_scalar(int dtype, int op, const void *a, double scalar, int scalar_left,
+                                    void *out, int64_t n, void *stream);
+
+/* out = op(a), element-wise.  Replaces Tensor::unary (Tensor.cu:624-637; unaryOpKernel). */
+CTATTN_API int ctattn_tensor_unary(int dtype, int op, const void *a, void *out, int64_t n, void *stream);
+
+/* Workspace bytes ctattn_tensor_reduce needs, or -1 on invalid arguments. */
+CTATTN_API int64_t ctattn_tensor_reduce_workspace_bytes(int dtype, int64_t outer, int64_t R, int64_t inner);
+
+/* a viewed as [outer][R][inner] reduced over R into out [outer][inner] (R >= 1; outer <= 65535
+ * when inner > 1).  Deterministic: a fixed order per output.  Replaces Tensor::reduce
+ * (Tensor.cu:807-870; reduceKernel) for one axis or all of them. */
+CTATTN_API int ctattn_tensor_reduce(int dtype, int op, const void *a, int64_t outer, int64_t R, int64_t inner,
+                                    void *out, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* out = a with its axes permuted: out axis k is input axis perm[k].  Replaces
+ * Tensor::transpose (Tensor.cu:577-616; transposeKernel). */
+CTATTN_API int ctattn_tensor_permute(int dtype, const void *a, int ndim, const int64_t *shape,
+                                     const int32_t *perm, void *out, void *stream);
+
+/* Kronecker product of two tensors of equal rank: out shape a_shape[k] * b_shape[k].
+ * Replaces Tensor::kron (Tensor.cu:877-905; kronKernel). */
+CTATTN_API int ctattn_tensor_kron(int dtype, const void *a, const void *b, int ndim, const int64_t *a_shape,
+                                  const int64_t *b_shape, void *out, void *stream);
+
+/* c[z] = a[z] (M x K) times b[z] (K x N), z < batch, with one b for every z when batch_b == 1.
+ * Floating types run on the projection GEMMs, integer and bool types on a per-output kernel.
+ * Replaces Tensor::matmul (Tensor.cu:912-950; matmulKernel). */
+CTATTN_API int ctattn_tensor_matmul(int dtype, const void *a, const void *b, void *c, int64_t batch,
+                                    int64_t batch_b, int64_t M, int64_t K, int64_t N, void *stream);
 
 #ifdef __cplusplus
 }
