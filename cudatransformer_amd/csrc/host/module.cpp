@@ -169,7 +169,7 @@ void declareTensorOps(py::class_<Tensor<DType>> &c) {
 
 template <typename DType>
 void declareTensor(py::module_ &m, const std::string &suffix) {
-    auto cls = py::class_<Tensor<DType>>(m, (suffix + "Tensor").c_str(),
+    py::class_<Tensor<DType>>(m, (suffix + "Tensor").c_str(),
                               "N-dimensional GPU tensor. Assignments and copies are shallow (shared buffer); "
                               "call clone() to obtain an independent copy.")
         .def(py::init<>(), "Constructs an empty tensor with no allocated memory.")
@@ -198,6 +198,13 @@ void declareTensor(py::module_ &m, const std::string &suffix) {
             for (size_t i = 0; i < t.nDim(); ++i) s += (i ? ", " : "") + std::to_string(t.shape(i));
             return s + "])";
         });
+}
+
+// Adds the operators after every tensor class exists, so that signatures name the Python
+// classes they return (BoolTensor for comparisons, the cast targets).
+template <typename DType>
+void addTensorOps(py::module_ &m, const std::string &suffix) {
+    auto cls = py::reinterpret_borrow<py::class_<Tensor<DType>>>(m.attr((suffix + "Tensor").c_str()));
     declareTensorOps<DType>(cls);
 }
 
@@ -614,6 +621,15 @@ PYBIND11_MODULE(cuda_transformer, m) {
     declareTensor<int16_t>(m, "Short");
     declareTensor<int8_t>(m, "Byte");
     declareTensor<bool>(m, "Bool");
+    addTensorOps<float>(m, "Float");
+    addTensorOps<bf16>(m, "BFloat");
+    addTensorOps<f16>(m, "Half");
+    addTensorOps<double>(m, "Double");
+    addTensorOps<int32_t>(m, "Int");
+    addTensorOps<int64_t>(m, "Long");
+    addTensorOps<int16_t>(m, "Short");
+    addTensorOps<int8_t>(m, "Byte");
+    addTensorOps<bool>(m, "Bool");
     declareFlashAttention<float>(m, "Float");
     declareFlashAttention<bf16>(m, "BFloat");
     declareFlashAttention<f16>(m, "Half");

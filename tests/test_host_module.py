@@ -122,3 +122,19 @@ def test_shape_errors_raise_value_error():
     k2 = ctm.FloatTensor([1, 4, 17, 64])
     with pytest.raises(ValueError):
         layer.computeAttention(q2, k2, k2)
+
+
+def test_type_stub_covers_the_module():
+    """cuda_transformer.pyi (written by the build, as the reference's Makefile runs stubgen)
+    parses and declares every public class and function of the module."""
+    import ast
+    import os
+
+    path = os.path.join(os.path.dirname(ctm.__file__), "cuda_transformer.pyi")
+    tree = ast.parse(open(path).read())
+    declared = {n.name for n in tree.body if isinstance(n, (ast.ClassDef, ast.FunctionDef))}
+    public = {n for n in dir(ctm) if not n.startswith("_")}
+    assert public <= declared, sorted(public - declared)
+    tensor = next(n for n in tree.body if isinstance(n, ast.ClassDef) and n.name == "FloatTensor")
+    methods = {n.name for n in tensor.body if isinstance(n, ast.FunctionDef)}
+    assert {"fromNumpy", "numpy", "matmul", "__add__", "sum", "transpose"} <= methods
