@@ -42,7 +42,16 @@ WORKLOADS = {
     "c4": dict(B=1, H=32, T=8192, D=128, dtype="bf16", std=0.5, peak=2516.6,
                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 bf16, 1 GPU",
                label="causal SDPA fwd+bwd, B1 H32 T8192 d128 bf16 in / fp32 accumulate (BASELINE configs[3])"),
+    "c4h": dict(B=1, H=32, T=8192, D=128, dtype="f16", std=0.5, peak=2516.6,
+                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 fp16, 1 GPU",
+                label="causal SDPA fwd+bwd, B1 H32 T8192 d128 fp16 in / fp32 accumulate (BASELINE configs[3] "
+                      "shape in the reference's Half precision)"),
+    "c3d": dict(B=8, H=12, T=1024, D=64, dtype="f64", std=1.0, peak=78.6,
+                metric="causal attn fwd+bwd TFLOP/s, B8 H12 T1024 d64 fp64, 1 GPU",
+                label="causal SDPA fwd+bwd, B8 H12 T1024 d64 fp64 (the headline shape in the reference's "
+                      "Double precision; generic kernels)"),
 }
+TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "f16": "float16", "f64": "float64"}
 B, H, T, D = 8, 12, 1024, 64
 CAUSAL = True
 FWD_FLOP = 4.0 * B * H * T * T * D / 2.0  # QK^T + PV, 2*T^2*d each; causal = half of T^2
@@ -146,11 +155,11 @@ def main():
               flush=True)
         return
     g = torch.Generator(device=dev).manual_seed(2)
-    tdt = torch.float32 if wl["dtype"] == "f32" else torch.bfloat16
+    tdt = getattr(torch, TORCH_DTYPE[wl["dtype"]])
     q, k, v, do = ((wl["std"] * torch.randn((B, H, T, D), generator=g, device=dev,
                                             dtype=torch.float32)).to(tdt) for _ in range(4))
     o = torch.empty_like(q)
-    lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+    lse = torch.empty((B, H, T), device=dev, dtype=torch.float64 if tdt == torch.float64 else torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
     ws = torch.empty(ct.bwd_workspace_bytes(tdt, B, H, T, D, CAUSAL), device=dev,
                      dtype=torch.uint8)

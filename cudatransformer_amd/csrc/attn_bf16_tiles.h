@@ -1,6 +1,6 @@
 // bf16 LDS tile machinery shared by the bf16 attention kernels (gfx950): swizzled row-major
 // tiles loaded global -> LDS directly, row and transposed (ds_read_b64_tr_b16) MFMA operand
-// reads by explicit LDS byte address, and the v_mfma_f32_32x32x16_bf16 wrapper.
+// reads by explicit LDS byte address, and the bf16 / fp16 32x32x16 MFMA formats.
 //
 // 32x32x16 operand layout (lane l, col = l & 31, half = l >> 5): A[i][k] comes from lane
 // (i, k / 8) element k % 8, B[k][j] from lane (j, k / 8) element k % 8; accumulator register r
@@ -23,9 +23,29 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-__device__ __forceinline__ floatx16 mfma_bf16(bf16x8 a, bf16x8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// The two 16-bit formats of these kernels.  bf16 and IEEE fp16 share the tiles, the
+// operand layout (32x32x16, 8 elements per lane) and every address; they differ in the MFMA
+// instruction and in the rounding of fp32 values to 16 bits (nearest even for both).
+struct Bf16Fmt {
+    using vec = bf16x8;
+    using elem = __bf16;
+    __device__ static floatx16 mfma(vec a, vec b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static uint16_t bits(float x) { return f32_to_bf16(x).bits; }
+    __device__ static float widen(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+};
+struct F16Fmt {
+    using vec = f16x8;
+    using elem = _Float16;
+    __device__ static floatx16 mfma(vec a, vec b, floatx16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    __device__ static uint16_t bits(float x) { return __builtin_bit_cast(uint16_t, _Float16(x)); }
+    __device__ static float widen(uint16_t b) { return float(__builtin_bit_cast(_Float16, b)); }
+};
 
 // Row-major bf16 tile with D elements (D / 8 16-byte chunks) per row.  Logical chunk c of
 // row r sits at physical chunk c ^ swz(r).  The LDS has 64 four-byte banks (256 bytes per
@@ -70,10 +90,12 @@ __device__ __forceinline__ void load_tile(char *tile, const uint16_t *src, int r
 }
 
 // LDS reads by byte address (LDS addresses are 32-bit).
-typedef __attribute__((address_space(3))) const bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) const u16x8 lds_u16x8;
 typedef __attribute__((address_space(3))) const floatx4 lds_floatx4;
 
-__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) { return *(lds_bf16x8 *)(uintptr_t)(addr); }
+template <typename V> __device__ __forceinline__ V lds_b128(uint32_t addr) {
+    return __builtin_bit_cast(V, *(lds_u16x8 *)(uintptr_t)(addr));
+}
 __device__ __forceinline__ floatx4 lds_f4(uint32_t addr) { return *(lds_floatx4 *)(uintptr_t)(addr); }
 
 // LDS byte address of a __shared__ object.
@@ -102,13 +124,13 @@ __device__ __forceinline__ uint32_t col_base(uint32_t tile, int r0, int hi, int 
     const int chunk = 2 * ((lane >> 4) & 1) + ((s & 3) >> 1);
     return tile + uint32_t(Tile<D>::off(r0 + 4 * half + (s >> 2) + 8 * hi, chunk) + 8 * (s & 1));
 }
-template <int D>
-__device__ __forceinline__ bf16x8 read_col(uint32_t cb0, uint32_t cb1, int kk, int dt) {
+template <int D, typename V>
+__device__ __forceinline__ V read_col(uint32_t cb0, uint32_t cb1, int kk, int dt) {
     const uint32_t off = uint32_t(16 * kk * 2 * D);
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb0 ^ uint32_t(dt << 6)) + off));
     const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb1 ^ uint32_t(dt << 6)) + off));
     const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8, x);
+    return __builtin_bit_cast(V, x);
 }
 
 // Scheduling fence between a step's operand reads and the previous step's MFMAs: nothing

@@ -1,4 +1,6 @@
-// bf16 flash-attention backward on bf16 MFMA (v_mfma_f32_32x32x16_bf16), fp32 accumulate.
+// bf16 / fp16 flash-attention backward on 16-bit MFMA (v_mfma_f32_32x32x16_bf16 / _f16), fp32
+// accumulate; the fp16 instantiation (F16Fmt) is the same code with the fp16 MFMA and fp16
+// rounding.
 //
 // Same math as the fp32 backward (attn_bwd_mfma.hip) and the reference's
 // flashAttentionBackward (flash_attention.cu:226-326, with correct dK / dV): P and dS are
@@ -71,35 +73,36 @@ struct KvCfg {
 //   ak   : row_base of this wave's first key in the K tile (V at + KV_BYTES)
 //   ac0/1: col_base of the wave's Q rows (dO at + Q_BYTES)
 //   anl  : address of nl2[32 rs + 4 half] of the block (delta at + BM * 4)
-template <int D, bool MASK>
+template <int D, bool MASK, typename F>
 __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32], uint32_t aq,
                                          uint32_t ak, uint32_t ac0, uint32_t ac1, uint32_t anl, int r0w,
                                          int key, int T, int causal, float c, int half) {
     using C = KvCfg<D>;
+    using V = typename F::vec;
     floatx16 s = zero16(), dp = zero16();
     {
-        bf16x8 qa[2], ka[2], da[2], va[2];
-        qa[0] = lds_b128(aq);
-        ka[0] = lds_b128(ak);
-        da[0] = lds_b128(aq + C::Q_BYTES);
-        va[0] = lds_b128(ak + C::KV_BYTES);
+        V qa[2], ka[2], da[2], va[2];
+        qa[0] = lds_b128<V>(aq);
+        ka[0] = lds_b128<V>(ak);
+        da[0] = lds_b128<V>(aq + C::Q_BYTES);
+        va[0] = lds_b128<V>(ak + C::KV_BYTES);
 #pragma unroll
         for (int st = 0; st < C::KSTEPS; ++st) {
             const int cur = st & 1, nxt = cur ^ 1;
             if (st + 1 < C::KSTEPS) {
                 const uint32_t xq = aq ^ uint32_t((st + 1) << 5), xk = ak ^ uint32_t((st + 1) << 5);
-                qa[nxt] = lds_b128(xq);
-                ka[nxt] = lds_b128(xk);
-                da[nxt] = lds_b128(xq + C::Q_BYTES);
-                va[nxt] = lds_b128(xk + C::KV_BYTES);
+                qa[nxt] = lds_b128<V>(xq);
+                ka[nxt] = lds_b128<V>(xk);
+                da[nxt] = lds_b128<V>(xq + C::Q_BYTES);
+                va[nxt] = lds_b128<V>(xk + C::KV_BYTES);
             }
             read_fence();
-            s = mfma_bf16(qa[cur], ka[cur], s);
-            dp = mfma_bf16(da[cur], va[cur], dp);
+            s = F::mfma(qa[cur], ka[cur], s);
+            dp = F::mfma(da[cur], va[cur], dp);
         }
     }
     // lane = key; register r = row r0w + acc_row(r, half)
-    bf16x8 pb[2], dsb[2];
+    V pb[2], dsb[2];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const floatx4 n4 = lds_f4(anl + 32 * g);
@@ -112,33 +115,33 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
                 const int row = r0w + acc_row(r, half);
                 p = (row >= T || key >= T || (causal && key > row)) ? 0.f : p;
             }
-            pb[r / 8][r % 8] = (__bf16)p;
-            dsb[r / 8][r % 8] = (__bf16)(p * (dp[r] - d4[t]));
+            pb[r / 8][r % 8] = (typename F::elem)p;
+            dsb[r / 8][r % 8] = (typename F::elem)(p * (dp[r] - d4[t]));
         }
     }
     // dV^T += dO^T P, dK^T += Q^T dS over the tile's 32 rows (two k-steps of 16).
     {
         constexpr int NS = 2 * C::DT;
-        bf16x8 ao[2], aqT[2];
-        ao[0] = read_col<D>(ac0 + C::Q_BYTES, ac1 + C::Q_BYTES, 0, 0);
-        aqT[0] = read_col<D>(ac0, ac1, 0, 0);
+        V ao[2], aqT[2];
+        ao[0] = read_col<D, V>(ac0 + C::Q_BYTES, ac1 + C::Q_BYTES, 0, 0);
+        aqT[0] = read_col<D, V>(ac0, ac1, 0, 0);
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int cur = i & 1, nxt = cur ^ 1;
             if (i + 1 < NS) {
                 const int kk = (i + 1) / C::DT, dt = (i + 1) % C::DT;
-                ao[nxt] = read_col<D>(ac0 + C::Q_BYTES, ac1 + C::Q_BYTES, kk, dt);
-                aqT[nxt] = read_col<D>(ac0, ac1, kk, dt);
+                ao[nxt] = read_col<D, V>(ac0 + C::Q_BYTES, ac1 + C::Q_BYTES, kk, dt);
+                aqT[nxt] = read_col<D, V>(ac0, ac1, kk, dt);
             }
             read_fence();
             const int kk = i / C::DT, dt = i % C::DT;
-            dv_acc[dt] = mfma_bf16(ao[cur], pb[kk], dv_acc[dt]);
-            dk_acc[dt] = mfma_bf16(aqT[cur], dsb[kk], dk_acc[dt]);
+            dv_acc[dt] = F::mfma(ao[cur], pb[kk], dv_acc[dt]);
+            dk_acc[dt] = F::mfma(aqT[cur], dsb[kk], dk_acc[dt]);
         }
     }
 }
 
-template <int D>
+template <int D, typename F>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_bf16_dkdv_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const uint16_t *__restrict__ dout, const float *__restrict__ nl2, const float *__restrict__ delta,
@@ -209,9 +212,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const uint32_t anl = L + C::S_OFF + uint32_t(buf * 2 * C::BM * 4) + rnl;
         const bool masked = (r0w + 32 > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0w);
         if (masked)
-            kv_block<D, true>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
+            kv_block<D, true, F>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
         else
-            kv_block<D, false>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
+            kv_block<D, false, F>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
     }
 
     // Row slice 1 hands its dK^T / dV^T sums to row slice 0 through LDS (no load is in flight
@@ -242,8 +245,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     const int r = 4 * g + t;
                     const float sk = dk_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 0) * 16 + r) * kWave + lane];
                     const float sv = dv_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 1) * 16 + r) * kWave + lane];
-                    xk[t] = f32_to_bf16(sk * inv_sqrt_d).bits;
-                    xv[t] = f32_to_bf16(sv).bits;
+                    xk[t] = F::bits(sk * inv_sqrt_d);
+                    xv[t] = F::bits(sv);
                 }
                 *reinterpret_cast<u16x4 *>(dkr + dt * 32 + 8 * g + 4 * half) = xk;
                 *reinterpret_cast<u16x4 *>(dvr + dt * 32 + 8 * g + 4 * half) = xv;
@@ -269,32 +272,33 @@ struct QCfg {
 // One 32-key block for one wave (32 rows): S^T, dP^T, P^T, dS^T and the dQ update.
 //   ak   : row_base of the block's K tile for key `col` (V at + KB)
 //   ac0/1: col_base of the K tile
-template <int D, bool MASK>
-__device__ __forceinline__ void dq_block(floatx16 (&dq_acc)[D / 32], const bf16x8 (&qB)[D / 16],
-                                         const bf16x8 (&doB)[D / 16], uint32_t ak, uint32_t ac0, uint32_t ac1,
-                                         float nlr, float dlr, int j0, int row, int T, int causal, float c,
-                                         int half) {
+template <int D, bool MASK, typename F>
+__device__ __forceinline__ void dq_block(floatx16 (&dq_acc)[D / 32], const typename F::vec (&qB)[D / 16],
+                                         const typename F::vec (&doB)[D / 16], uint32_t ak, uint32_t ac0,
+                                         uint32_t ac1, float nlr, float dlr, int j0, int row, int T, int causal,
+                                         float c, int half) {
     using C = QCfg<D>;
+    using V = typename F::vec;
     floatx16 s = zero16(), dp = zero16();
     {
-        bf16x8 ka[2], va[2];
-        ka[0] = lds_b128(ak);
-        va[0] = lds_b128(ak + C::KB);
+        V ka[2], va[2];
+        ka[0] = lds_b128<V>(ak);
+        va[0] = lds_b128<V>(ak + C::KB);
 #pragma unroll
         for (int st = 0; st < C::KSTEPS; ++st) {
             const int cur = st & 1, nxt = cur ^ 1;
             if (st + 1 < C::KSTEPS) {
                 const uint32_t x = ak ^ uint32_t((st + 1) << 5);
-                ka[nxt] = lds_b128(x);
-                va[nxt] = lds_b128(x + C::KB);
+                ka[nxt] = lds_b128<V>(x);
+                va[nxt] = lds_b128<V>(x + C::KB);
             }
             read_fence();
-            s = mfma_bf16(ka[cur], qB[st], s);
-            dp = mfma_bf16(va[cur], doB[st], dp);
+            s = F::mfma(ka[cur], qB[st], s);
+            dp = F::mfma(va[cur], doB[st], dp);
         }
     }
     // lane = query row; register r = key j0 + acc_row(r, half)
-    bf16x8 dsb[2];
+    V dsb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         float p = fast_exp2(fmaf(s[r], c, nlr));
@@ -302,29 +306,30 @@ __device__ __forceinline__ void dq_block(floatx16 (&dq_acc)[D / 32], const bf16x
             const int key = j0 + acc_row(r, half);
             p = (key >= T || row >= T || (causal && key > row)) ? 0.f : p;
         }
-        dsb[r / 8][r % 8] = (__bf16)(p * (dp[r] - dlr));
+        dsb[r / 8][r % 8] = (typename F::elem)(p * (dp[r] - dlr));
     }
     // dQ += dS K over the block's 32 keys (two k-steps of 16).
     {
         constexpr int NS = 2 * C::DT;
-        bf16x8 kt[2];
-        kt[0] = read_col<D>(ac0, ac1, 0, 0);
+        V kt[2];
+        kt[0] = read_col<D, V>(ac0, ac1, 0, 0);
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int cur = i & 1, nxt = cur ^ 1;
-            if (i + 1 < NS) kt[nxt] = read_col<D>(ac0, ac1, (i + 1) / C::DT, (i + 1) % C::DT);
+            if (i + 1 < NS) kt[nxt] = read_col<D, V>(ac0, ac1, (i + 1) / C::DT, (i + 1) % C::DT);
             read_fence();
-            dq_acc[i % C::DT] = mfma_bf16(dsb[i / C::DT], kt[cur], dq_acc[i % C::DT]);
+            dq_acc[i % C::DT] = F::mfma(dsb[i / C::DT], kt[cur], dq_acc[i % C::DT]);
         }
     }
 }
 
-template <int D>
+template <int D, typename F>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_bf16_dq_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const uint16_t *__restrict__ dout, const float *__restrict__ nl2, const float *__restrict__ delta,
     uint16_t *__restrict__ dq, int T, int BH, int causal, float c, float inv_sqrt_d) {
     using C = QCfg<D>;
+    using V = typename F::vec;
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
     const uint32_t L = lds_addr(smem);
 
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int row = wave_first_row + col;
 
     // Q^T and dO^T as B operands: lane (row, half) holds Q[row][16 st + 8 half ..].
-    bf16x8 qB[C::KSTEPS], doB[C::KSTEPS];
+    V qB[C::KSTEPS], doB[C::KSTEPS];
 #pragma unroll
     for (int st = 0; st < C::KSTEPS; ++st) {
         u16x8 xq = {0, 0, 0, 0, 0, 0, 0, 0}, xd = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -354,8 +359,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             xq = *reinterpret_cast<const u16x8 *>(q + base + int64_t(row) * D + 16 * st + 8 * half);
             xd = *reinterpret_cast<const u16x8 *>(dout + base + int64_t(row) * D + 16 * st + 8 * half);
         }
-        qB[st] = __builtin_bit_cast(bf16x8, xq);
-        doB[st] = __builtin_bit_cast(bf16x8, xd);
+        qB[st] = __builtin_bit_cast(V, xq);
+        doB[st] = __builtin_bit_cast(V, xd);
     }
     const float nlr = row < T ? nl2[rbase + row] : 0.f;
     const float dlr = row < T ? delta[rbase + row] : 0.f;
@@ -384,10 +389,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
         if (masked) {
             if (!causal || j0 <= wave_last_row)
-                dq_block<D, true>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
+                dq_block<D, true, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
                                   half);
         } else {
-            dq_block<D, false>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
+            dq_block<D, false, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
                                half);
         }
     }
@@ -400,14 +405,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (rr >= T) continue;
         uint16_t *p = dq + base + int64_t(rr) * D + col;
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) p[32 * dt] = f32_to_bf16(dq_acc[dt][r] * inv_sqrt_d).bits;
+        for (int dt = 0; dt < C::DT; ++dt) p[32 * dt] = F::bits(dq_acc[dt][r] * inv_sqrt_d);
     }
 }
 
 // delta[row] = sum_c dO[row][c] O[row][c] from bf16 (flash_attention.cu:269-273) and
 // nl2[row] = -LSE[row] * log2(e), the per-row term of P = exp2(S log2(e)/sqrt(d) + nl2).
 // D / 8 lanes per row, one 16-byte load of O and of dO each.
-template <int D>
+template <int D, typename F>
 __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t *__restrict__ o,
                                                                  const uint16_t *__restrict__ dout,
                                                                  const float *__restrict__ lse,
@@ -422,7 +427,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t
         const u16x8 a = *reinterpret_cast<const u16x8 *>(o + row * D + 8 * c8);
         const u16x8 b = *reinterpret_cast<const u16x8 *>(dout + row * D + 8 * c8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += to_f32(bf16_t{a[e]}) * to_f32(bf16_t{b[e]});
+        for (int e = 0; e < 8; ++e) s += F::widen(a[e]) * F::widen(b[e]);
     }
     s = group_sum<LPR>(s);
     if (row < rows && c8 == 0) {
@@ -431,7 +436,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t
     }
 }
 
-template <int D>
+template <int D, typename F>
 hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, const void *dout,
                     const float *lse, float *delta, void *dq, void *dk, void *dv, float *nl2,
                     const AttnShape &s, hipStream_t stream) {
@@ -445,18 +450,18 @@ hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, 
     const int64_t rows = s.rows();
     auto u16 = [](const void *p) { return static_cast<const uint16_t *>(p); };
     const int64_t pre_threads = rows * (D / 8);
-    hipLaunchKernelGGL(bwd_preprocess_bf16_kernel<D>, dim3(unsigned((pre_threads + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL((bwd_preprocess_bf16_kernel<D, F>), dim3(unsigned((pre_threads + 255) / 256)), dim3(256), 0, stream,
                        u16(o), u16(dout), lse, delta, nl2, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const float c = kLog2e / sqrtf(float(D));
     const float inv_sqrt_d = 1.f / sqrtf(float(D));
-    hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0, stream,
+    hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D, F>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0, stream,
                        u16(q), u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dk),
                        static_cast<uint16_t *>(dv), int(s.T), int(s.bh()), int(s.causal), c, inv_sqrt_d);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_bf16_dq_kernel<D>), dim3(unsigned(q_blocks)), dim3(QC::NW * kWave), 0, stream, u16(q),
+    hipLaunchKernelGGL((bwd_bf16_dq_kernel<D, F>), dim3(unsigned(q_blocks)), dim3(QC::NW * kWave), 0, stream, u16(q),
                        u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dq), int(s.T), int(s.bh()),
                        int(s.causal), c, inv_sqrt_d);
     return hipGetLastError();
@@ -475,9 +480,21 @@ hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const vo
     (void)deterministic;
     float *nl2 = static_cast<float *>(extra);
     switch (s.d) {
-        case 32: return bwd_bf16<32>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
-        case 64: return bwd_bf16<64>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
-        case 128: return bwd_bf16<128>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 32: return bwd_bf16<32, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 64: return bwd_bf16<64, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 128: return bwd_bf16<128, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_f16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
+                          const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
+                          const AttnShape &s, hipStream_t stream) {
+    float *nl2 = static_cast<float *>(extra);
+    switch (s.d) {
+        case 32: return bwd_bf16<32, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 64: return bwd_bf16<64, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 128: return bwd_bf16<128, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
         default: return hipErrorNotSupported;
     }
 }

@@ -425,12 +425,12 @@ int64_t partial_bytes(const AttnShape &s) {
 }  // namespace
 
 bool mfma_bwd_supported(int dtype, int64_t d) {
-    (void)dtype;  // fp32 and bf16 kernels both cover d in {32, 64, 128}
+    (void)dtype;  // the fp32, bf16 and fp16 kernels all cover d in {32, 64, 128}
     return d == 32 || d == 64 || d == 128;
 }
 
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic) {
-    if (dtype == 1) return bf16_bwd_workspace_bytes(s, deterministic);
+    if (dtype == 1 || dtype == 2) return bf16_bwd_workspace_bytes(s, deterministic);
     return deterministic ? partial_bytes(s) : 0;
 }
 
@@ -440,6 +440,7 @@ hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *
                            const AttnShape &s, hipStream_t stream) {
     if (dtype == 1)
         return launch_bf16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, deterministic, s, stream);
+    if (dtype == 2) return launch_f16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, s, stream);
     const DqMode mode = deterministic ? DqMode::Partial : DqMode::Atomic;
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };

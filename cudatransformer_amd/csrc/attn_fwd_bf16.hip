@@ -1,4 +1,6 @@
-// bf16 flash-attention forward on bf16 MFMA (v_mfma_f32_32x32x16_bf16), fp32 accumulate.
+// bf16 / fp16 flash-attention forward on 16-bit MFMA (v_mfma_f32_32x32x16_bf16 / _f16), fp32
+// accumulate.  The fp16 instantiation (F16Fmt) is the same code with the fp16 MFMA and fp16
+// rounding of P and O.
 //
 // Same result as the fp32 forward and as the reference's flashAttention<__nv_bfloat16>
 // (flash_attention.cu:57-169) except that scores and sums accumulate in fp32 (the reference
@@ -51,11 +53,12 @@ struct FwdBf16State {
 
 // One 64-key block for one wave.  ak: row_base of the block's K tile for key `col` (V at
 // + KB); vc0 / vc1: col_base of the V tile.  MASK selects the diagonal / sequence-end variant.
-template <int D, bool MASK>
-__device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8 (&qb)[D / 16], uint32_t ak,
+template <int D, bool MASK, typename F>
+__device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const typename F::vec (&qb)[D / 16], uint32_t ak,
                                                uint32_t vc0, uint32_t vc1, int j0, int row, int wave_last_row,
                                                int T, int causal, float c, int half) {
     using C = FwdBf16Cfg<D>;
+    using V = typename F::vec;
     bool active[C::KT];
 #pragma unroll
     for (int kt = 0; kt < C::KT; ++kt) {
@@ -68,13 +71,13 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8
         sacc[kt] = zero16();
         if (!active[kt]) continue;
         const uint32_t a = ak + uint32_t(32 * kt * C::ROW);
-        bf16x8 ka[2];
-        ka[0] = lds_b128(a);
+        V ka[2];
+        ka[0] = lds_b128<V>(a);
 #pragma unroll
         for (int s = 0; s < C::KSTEPS; ++s) {
-            if (s + 1 < C::KSTEPS) ka[(s + 1) & 1] = lds_b128(a ^ uint32_t((s + 1) << 5));
+            if (s + 1 < C::KSTEPS) ka[(s + 1) & 1] = lds_b128<V>(a ^ uint32_t((s + 1) << 5));
             read_fence();
-            sacc[kt] = mfma_bf16(ka[s & 1], qb[s], sacc[kt]);
+            sacc[kt] = F::mfma(ka[s & 1], qb[s], sacc[kt]);
         }
     }
     float mloc = -INFINITY;
@@ -103,7 +106,7 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8
     }
     // P^T = exp2(S c - m), rounded to bf16 as the B operand; the denominator sums the same
     // fp32 values.
-    bf16x8 pb[C::KT][2];
+    V pb[C::KT][2];
     float psum = 0.f;
 #pragma unroll
     for (int kt = 0; kt < C::KT; ++kt) {
@@ -114,7 +117,7 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8
             for (int e = 0; e < 8; ++e) {
                 const float p = fast_exp2(fmaf(sacc[kt][8 * s + e], c, -st.m_run));
                 psum += p;
-                pb[kt][s][e] = (__bf16)p;
+                pb[kt][s][e] = (typename F::elem)p;
             }
         }
     }
@@ -124,22 +127,23 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const bf16x8
     for (int kt = 0; kt < C::KT; ++kt) {
         if (!active[kt]) continue;
         constexpr int NS = 2 * C::DT;
-        bf16x8 va[2];
-        va[0] = read_col<D>(vc0, vc1, 2 * kt, 0);
+        V va[2];
+        va[0] = read_col<D, V>(vc0, vc1, 2 * kt, 0);
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            if (i + 1 < NS) va[(i + 1) & 1] = read_col<D>(vc0, vc1, 2 * kt + (i + 1) / C::DT, (i + 1) % C::DT);
+            if (i + 1 < NS) va[(i + 1) & 1] = read_col<D, V>(vc0, vc1, 2 * kt + (i + 1) / C::DT, (i + 1) % C::DT);
             read_fence();
-            st.oacc[i % C::DT] = mfma_bf16(va[i & 1], pb[kt][i / C::DT], st.oacc[i % C::DT]);
+            st.oacc[i % C::DT] = F::mfma(va[i & 1], pb[kt][i / C::DT], st.oacc[i % C::DT]);
         }
     }
 }
 
-template <int D>
+template <int D, typename F>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_mfma_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     uint16_t *__restrict__ o, float *__restrict__ lse, int T, int BH, int causal, float c) {
     using C = FwdBf16Cfg<D>;
+    using V = typename F::vec;
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
     const uint32_t L = lds_addr(smem);
 
@@ -160,12 +164,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int wave_last_row = wave_first_row + 31;
 
     // Q^T as the B operand: lane (row, half) holds Q[row][16s + 8*half .. +7].
-    bf16x8 qb[C::KSTEPS];
+    V qb[C::KSTEPS];
 #pragma unroll
     for (int s = 0; s < C::KSTEPS; ++s) {
         u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
         if (row < T) x = *reinterpret_cast<const u16x8 *>(q + base + int64_t(row) * D + 16 * s + 8 * half);
-        qb[s] = __builtin_bit_cast(bf16x8, x);
+        qb[s] = __builtin_bit_cast(V, x);
     }
 
     FwdBf16State<D> st;
@@ -197,10 +201,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
         if (masked) {
             if (!causal || j0 <= wave_last_row)
-                fwd_bf16_block<D, true>(st, qb, kt + rk, kt + C::KB + cv0, kt + C::KB + cv1, j0, row,
+                fwd_bf16_block<D, true, F>(st, qb, kt + rk, kt + C::KB + cv0, kt + C::KB + cv1, j0, row,
                                         wave_last_row, T, causal, c, half);
         } else {
-            fwd_bf16_block<D, false>(st, qb, kt + rk, kt + C::KB + cv0, kt + C::KB + cv1, j0, row, wave_last_row,
+            fwd_bf16_block<D, false, F>(st, qb, kt + rk, kt + C::KB + cv0, kt + C::KB + cv1, j0, row, wave_last_row,
                                      T, causal, c, half);
         }
     }
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int g = 0; g < 4; ++g) {
                 u16x4 x;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) x[t] = f32_to_bf16(st.oacc[dt][4 * g + t] * inv_l).bits;
+                for (int t = 0; t < 4; ++t) x[t] = F::bits(st.oacc[dt][4 * g + t] * inv_l);
                 *reinterpret_cast<u16x4 *>(orow + dt * 32 + 8 * g + 4 * half) = x;
             }
         }
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-template <int D>
+template <int D, typename F>
 hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse, const AttnShape &s,
                     hipStream_t stream) {
     using C = FwdBf16Cfg<D>;
@@ -231,7 +235,7 @@ hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float 
     const int64_t blocks = nqb * s.bh();
     if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float c = kLog2e / sqrtf(float(D));
-    hipLaunchKernelGGL(fwd_bf16_mfma_kernel<D>, dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
+    hipLaunchKernelGGL((fwd_bf16_mfma_kernel<D, F>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
                        static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
                        static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), lse, int(s.T),
                        int(s.bh()), int(s.causal), c);
@@ -243,9 +247,19 @@ hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float 
 hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
                            const AttnShape &s, hipStream_t stream) {
     switch (s.d) {
-        case 32: return fwd_bf16<32>(q, k, v, o, lse, s, stream);
-        case 64: return fwd_bf16<64>(q, k, v, o, lse, s, stream);
-        case 128: return fwd_bf16<128>(q, k, v, o, lse, s, stream);
+        case 32: return fwd_bf16<32, Bf16Fmt>(q, k, v, o, lse, s, stream);
+        case 64: return fwd_bf16<64, Bf16Fmt>(q, k, v, o, lse, s, stream);
+        case 128: return fwd_bf16<128, Bf16Fmt>(q, k, v, o, lse, s, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_f16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                          const AttnShape &s, hipStream_t stream) {
+    switch (s.d) {
+        case 32: return fwd_bf16<32, F16Fmt>(q, k, v, o, lse, s, stream);
+        case 64: return fwd_bf16<64, F16Fmt>(q, k, v, o, lse, s, stream);
+        case 128: return fwd_bf16<128, F16Fmt>(q, k, v, o, lse, s, stream);
         default: return hipErrorNotSupported;
     }
 }

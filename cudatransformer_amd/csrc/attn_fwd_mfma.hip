@@ -271,13 +271,14 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
 }  // namespace
 
 bool mfma_fwd_supported(int dtype, int64_t d) {
-    (void)dtype;  // fp32 and bf16 kernels both cover d in {32, 64, 128}
+    (void)dtype;  // the fp32, bf16 and fp16 kernels all cover d in {32, 64, 128}
     return d == 32 || d == 64 || d == 128;
 }
 
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
                            float *lse, const AttnShape &s, hipStream_t stream) {
     if (dtype == 1) return launch_bf16_fwd(q, k, v, o, lse, s, stream);
+    if (dtype == 2) return launch_f16_fwd(q, k, v, o, lse, s, stream);
     const float *qf = static_cast<const float *>(q);
     const float *kf = static_cast<const float *>(k);
     const float *vf = static_cast<const float *>(v);

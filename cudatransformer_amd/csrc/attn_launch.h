@@ -28,7 +28,7 @@ hipError_t launch_generic_bwd(int dtype, const void *q, const void *k, const voi
 hipError_t launch_bwd_preprocess(int dtype, const void *o, const void *dout, void *delta,
                                  const AttnShape &s, hipStream_t stream);
 
-// ---- MFMA kernels (fp32 and bf16: d in {32, 64, 128}) ----
+// ---- MFMA kernels (fp32, bf16 and fp16: d in {32, 64, 128}) ----
 bool mfma_fwd_supported(int dtype, int64_t d);
 bool mfma_bwd_supported(int dtype, int64_t d);
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
@@ -42,6 +42,13 @@ hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o,
 // Scratch: an fp32 dQ accumulator [B, H, T, d], or per-128-key-block partials when
 // deterministic.
 int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic);
+// fp16 forward / backward: the bf16 kernels instantiated for IEEE fp16 (fp16 MFMA), same
+// workspace as bf16.
+hipError_t launch_f16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                          const AttnShape &s, hipStream_t stream);
+hipError_t launch_f16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
+                          const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
+                          const AttnShape &s, hipStream_t stream);
 hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
                            bool deterministic, const AttnShape &s, hipStream_t stream);

@@ -86,11 +86,11 @@ int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, i
 
 // fp16 and fp64 storage always run the generic kernels.
 bool use_mfma_fwd(int dtype, int64_t d) {
-    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
+    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
            ctattn::mfma_fwd_supported(dtype, d);
 }
 bool use_mfma_bwd(int dtype, int64_t d) {
-    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
+    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
            ctattn::mfma_bwd_supported(dtype, d);
 }
 // Bytes of one LSE / delta element: fp64 for fp64 storage, fp32 otherwise.

@@ -96,18 +96,54 @@ def test_flash_attn_capi_matches_oracle(shape, causal, dtype):
 
 @pytest.mark.gpu
 def test_f16_output_is_rounded_to_nearest():
-    """fp16 O equals the fp64 oracle's O rounded to binary16 except where the fp32
-    accumulation lands within a few fp32 ulps of a rounding tie (at most one binary16 ulp
+    """Generic kernel: fp16 O equals the fp64 oracle's O rounded to binary16 except where the
+    fp32 accumulation lands within a few fp32 ulps of a rounding tie (at most one binary16 ulp
     away)."""
     shape = (1, 2, 96, 64)
     q, k, v, do = ora.make_inputs(shape, seed=310, dtype="f16")
     want = ora.attention_fwd(*ora.cast_inputs((q, k, v), "f16"), True)[0]
-    o, _ = ct.flash_attn_fwd(*(dev(a, torch.float16) for a in (q, k, v)), True)
+    prev = ct.set_policy(ct.POLICY_GENERIC)  # the generic kernel keeps P in fp32
+    try:
+        o, _ = ct.flash_attn_fwd(*(dev(a, torch.float16) for a in (q, k, v)), True)
+    finally:
+        ct.set_policy(prev)
     got = host(o)
     exact = ora.round_to_f16(want).astype(np.float64)
     ulp = np.abs(exact) * 2.0 ** -10 + 2.0 ** -24
     assert np.all(np.abs(got - exact) <= ulp * 1.0001)
     assert np.mean(got == exact) > 0.99
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_f16_mfma_matches_generic_and_oracle(causal, d):
+    """fp16 on the fp16 MFMA kernels (P and dS rounded to fp16 as MFMA operands, fp32
+    accumulation) against the generic fp16 kernels and the fp64 oracle."""
+    shape = (2, 3, 300, d)
+    say(f"f16 mfma vs generic causal={causal} d={d}")
+    q, k, v, do = ora.make_inputs(shape, seed=350 + d, dtype="f16")
+    want = ora.attention_fwd_bwd(*ora.cast_inputs((q, k, v, do), "f16"), causal)
+    t = [dev(a, torch.float16) for a in (q, k, v, do)]
+
+    def run():
+        o, lse = ct.flash_attn_fwd(t[0], t[1], t[2], causal)
+        dq, dk, dv = ct.flash_attn_bwd(t[0], t[1], t[2], o, t[3], lse, causal)
+        torch.cuda.synchronize()
+        return {"o": host(o), "lse": host(lse), "dq": host(dq), "dk": host(dk), "dv": host(dv)}
+
+    mfma = run()
+    prev = ct.set_policy(ct.POLICY_GENERIC)
+    try:
+        generic = run()
+    finally:
+        ct.set_policy(prev)
+    for key in mfma:
+        rel_check(mfma[key], want[key], F16_REL, f"mfma {key}")
+        rel_check(mfma[key], generic[key], F16_REL, f"mfma vs generic {key}")
+    r1 = run()
+    for key in mfma:  # no atomics in the 16-bit kernels: bitwise reproducible
+        assert np.array_equal(r1[key], mfma[key]), key
 
 
 @pytest.mark.gpu
