@@ -5,6 +5,7 @@
 // weights) and launches the MFMA GEMM family of proj_gemm.hip on the caller's stream.
 #include "capi_util.h"
 #include "ctattn.h"
+#include "blaslt_gemm.h"
 #include "proj_launch.h"
 
 #include <algorithm>
@@ -296,6 +297,9 @@ int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, vo
     if (int rc = validate_linear(fn, dtype, M, N, K)) return rc;
     if (M == 0) return ok();
     if (!x || !w || !y) return fail(hipErrorInvalidValue, "%s: null x/w/y pointer", fn);
+    // Column-major y^T (N x M, ld N) = W (op T of the K x N column-major w) x^T (K x M) + b.
+    if (ctattn::blaslt_gemm(dtype, true, false, N, M, K, w, K, x, K, y, N, 0.f, b, as_stream(stream)))
+        return finish(fn, hipSuccess, as_stream(stream));
     // y[m][n] = sum_k x[m][k] w[n][k] + b[n]: A = x [M][K], B = w [N][K], both K-contiguous.
     GemmParams p = make_params(M, N, K, 0, 1, linear_view(nullptr, N), nullptr);
     p.batch[0].nseg = 1;
@@ -330,6 +334,10 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     const bool v4 = linear_vec4(dtype, M, N, K, {x, w, dy, dx, dw});
     float *ws = static_cast<float *>(workspace);
     hipError_t e = hipSuccess;
+    // hipBLASLt (column-major): dW^T (K x N, ld K) += x^T (K x M) dy (op T of N x M);
+    // dX^T (K x M, ld K) = w^T (K x N) dy^T (N x M).
+    if (dw && ctattn::blaslt_gemm(dtype, false, true, K, N, M, x, K, dy, N, dw, K, 1.f, nullptr, st)) dw = nullptr;
+    if (dx && ctattn::blaslt_gemm(dtype, false, false, K, M, N, w, K, dy, N, dx, K, 0.f, nullptr, st)) dx = nullptr;
     if (dw) {
         // dw[n][k] += sum_m dy[m][n] x[m][k]: M' = N, N' = K, K' = M.  A(m'=n, k'=m) = dy stored
         // [k'][m']; B(k'=m, n'=k) = x stored [k'][n'].
