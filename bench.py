@@ -46,6 +46,10 @@ WORKLOADS = {
                 metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 fp16, 1 GPU",
                 label="causal SDPA fwd+bwd, B1 H32 T8192 d128 fp16 in / fp32 accumulate (BASELINE configs[3] "
                       "shape in the reference's Half precision)"),
+    "tensor": dict(B=1, H=1, T=1, D=1, dtype="f32", std=1.0, peak=8000.0,
+                   metric="Tensor operations HBM GB/s (elementwise add of 2 x 256 MiB fp32), 1 GPU",
+                   label="FloatTensor a + b on 64 Mi elements (768 MiB moved), with sum(), bfloat() cast, "
+                         "transpose(1, 0) of 8192 x 8192 and a 4096^3 matmul alongside"),
     "c3d": dict(B=8, H=12, T=1024, D=64, dtype="f64", std=1.0, peak=78.6,
                 metric="causal attn fwd+bwd TFLOP/s, B8 H12 T1024 d64 fp64, 1 GPU",
                 label="causal SDPA fwd+bwd, B8 H12 T1024 d64 fp64 (the headline shape in the reference's "
@@ -143,6 +147,8 @@ def main():
         return bench_native_nanogpt(args, wl)
     if args.workload == "layer":
         return bench_layer(args, wl)
+    if args.workload == "tensor":
+        return bench_tensor(args, wl)
     if args.copy_calibration:
         n = 64 << 20  # 64 Mi fp32 = 256 MiB read + 256 MiB written per copy
         src = torch.ones(n, device=dev, dtype=torch.float32)
@@ -248,6 +254,56 @@ def main():
     if not args.no_cpu_baseline:
         log("timing CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def bench_tensor(args, wl):
+    """The Tensor class's operations through the pybind module: host wall clock around
+    synchronised batches of launches (the module's work runs on its own stream), outputs from
+    the module's caching allocator (warm after the first call)."""
+    import time
+
+    import numpy as np
+    from cudatransformer_amd import cuda_transformer as ctm
+
+    n = 64 << 20
+    rng = np.random.default_rng(3)
+    a = ctm.FloatTensor.fromNumpy(rng.standard_normal(n, dtype=np.float32))
+    b = ctm.FloatTensor.fromNumpy(rng.standard_normal(n, dtype=np.float32))
+    sq = a.reshape([8192, 8192])
+    ma = ctm.FloatTensor.fromNumpy(rng.standard_normal((4096, 4096), dtype=np.float32))
+    mb = ctm.FloatTensor.fromNumpy(rng.standard_normal((4096, 4096), dtype=np.float32))
+
+    def timed(fn, reps):
+        for _ in range(max(args.warmup // 10, 2)):
+            fn()
+        ctm.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        ctm.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    reps = max(args.steps // 2, 10)
+    t_add = timed(lambda: a + b, reps)
+    t_sum = timed(lambda: a.sum(), reps)
+    t_cast = timed(lambda: a.bfloat(), reps)
+    t_tr = timed(lambda: sq.transpose(1, 0), reps)
+    t_mm = timed(lambda: ma @ mb, max(reps // 2, 5))
+    gbs = lambda nbytes, t: nbytes / t / 1e9
+    add_gbs = gbs(3 * 4 * n, t_add)
+    out = {
+        "metric": wl["metric"], "value": round(add_gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": reps, "warmup": max(args.warmup // 10, 2), "ms_per_step": round(t_add * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": wl["label"],
+                   "add_gbs": round(add_gbs, 1), "sum_gbs": round(gbs(4 * n, t_sum), 1),
+                   "cast_bf16_gbs": round(gbs(6 * n, t_cast), 1), "transpose_gbs": round(gbs(8 * n, t_tr), 1),
+                   "matmul_4096_tflops": round(2 * 4096 ** 3 / t_mm / 1e12, 1)},
+        "roofline": {"bound": "hbm", "kernel": "binary_kernel<float, false> (a + b)", "achieved": round(add_gbs, 1),
+                     "peak": 8000.0, "unit": "GB/s", "frac": round(add_gbs / 8000.0, 4), "traffic": None},
+        "cpu_baseline": None,
+    }
     print(json.dumps(out), flush=True)
 
 

@@ -14,12 +14,13 @@
 //   * integer division and remainder by zero give 0 (undefined in the reference);
 //   * reductions are two-stage and deterministic (a fixed order per output) instead of one
 //     thread walking every reduced element;
-//   * fp32 / bf16 / fp16 / fp64 products run on the projection GEMM family (MFMA for the
-//     narrow types) instead of one thread per output.
+//   * fp32 / bf16 / fp16 products run on hipBLASLt (plain row-major GEMMs), fp64 on the
+//     projection GEMM family, instead of one thread per output.
 // Storage codes: ctattn_dtype plus CTATTN_I32 .. CTATTN_BOOL.  bool is one byte, 0 or 1.
 #include "attn_common.h"
 #include "capi_util.h"
 #include "ctattn.h"
+#include "blaslt_gemm.h"
 #include "proj_launch.h"
 
 #include <math.h>
@@ -93,13 +94,36 @@ template <typename T> __device__ __forceinline__ calc_t<T> scalar_as(double s) {
 
 // ---- elementwise ------------------------------------------------------------------------
 
-template <typename S, typename D>
+template <typename S, typename D> __device__ __forceinline__ void cast_one(const S *src, D *dst, int64_t i) {
+    if constexpr (std::is_same_v<S, D>) dst[i] = src[i];
+    else if constexpr (std::is_same_v<S, bool>) stv(dst, i, int64_t(src[i] ? 1 : 0));
+    else if constexpr (std::is_same_v<S, bf16_t> || std::is_same_v<S, f16_t>) stv(dst, i, to_f32(src[i]));
+    else stv(dst, i, src[i]);  // fp32, fp64 and integers convert from their own value
+}
+
+// Four consecutive elements of T in one aligned load / store.
+template <typename T> struct alignas(4 * sizeof(T)) Quad {
+    T e[4];
+};
+
+// VEC4: n % 4 == 0 and both pointers aligned to four elements (checked on the host), so each
+// thread moves one Quad per step.
+template <typename S, typename D, bool VEC4>
 __global__ __launch_bounds__(256) void cast_kernel(const S *__restrict__ src, D *__restrict__ dst, int64_t n) {
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-        if constexpr (std::is_same_v<S, D>) dst[i] = src[i];
-        else if constexpr (std::is_same_v<S, bool>) stv(dst, i, int64_t(src[i] ? 1 : 0));
-        else if constexpr (std::is_same_v<S, bf16_t> || std::is_same_v<S, f16_t>) stv(dst, i, to_f32(src[i]));
-        else stv(dst, i, src[i]);  // fp32, fp64 and integers convert from their own value
+    if constexpr (VEC4) {
+        const Quad<S> *s4 = reinterpret_cast<const Quad<S> *>(src);
+        Quad<D> *d4 = reinterpret_cast<Quad<D> *>(dst);
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n / 4;
+             i += int64_t(gridDim.x) * blockDim.x) {
+            const Quad<S> x = s4[i];
+            Quad<D> y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cast_one(x.e, y.e, e);
+            d4[i] = y;
+        }
+    } else {
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+            cast_one(src, dst, i);
     }
 }
 
@@ -162,7 +186,23 @@ __device__ __forceinline__ void bcast_offsets(const Bcast &g, int64_t i, int64_t
 // CMP: a comparison writing bool; otherwise arithmetic writing T (bool included).
 template <typename T, bool CMP, typename O = std::conditional_t<CMP, bool, T>>
 __global__ __launch_bounds__(256) void binary_kernel(int op, const T *__restrict__ a, const T *__restrict__ b,
-                                                    O *__restrict__ out, Bcast g, int64_t n) {
+                                                    O *__restrict__ out, Bcast g, int64_t n, int vec4) {
+    if (vec4) {  // same shapes, n % 4 == 0, every pointer aligned to four elements
+        const Quad<T> *a4 = reinterpret_cast<const Quad<T> *>(a), *b4 = reinterpret_cast<const Quad<T> *>(b);
+        Quad<O> *o4 = reinterpret_cast<Quad<O> *>(out);
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n / 4;
+             i += int64_t(gridDim.x) * blockDim.x) {
+            const Quad<T> x = a4[i], y = b4[i];
+            Quad<O> z;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (CMP) z.e[e] = compare(op, ldv(x.e, e), ldv(y.e, e));
+                else stv(z.e, e, arith(op, ldv(x.e, e), ldv(y.e, e)));
+            }
+            o4[i] = z;
+        }
+        return;
+    }
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
         int64_t oa, ob;
         bcast_offsets(g, i, oa, ob);
@@ -271,15 +311,54 @@ template <typename C> __device__ __forceinline__ C wave_join(int op, C x) {
 
 // inner == 1, stage 1: workgroup (o, s) folds elements [s*chunk, (s+1)*chunk) of row o; the
 // four wave results are joined in wave order.
-template <typename T>
+// VEC: 16-byte loads (the row base and the chunk bounds are multiples of 16 bytes, checked on
+// the host); each thread folds its vector's elements in order.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void reduce_rows_kernel(int op, const T *__restrict__ a, int64_t R, int64_t chunk,
                                                          calc_t<T> *__restrict__ part, int S) {
     using C = calc_t<T>;
     __shared__ C waves[4];
     const int64_t o = blockIdx.x, s = blockIdx.y;
     const int64_t r0 = s * chunk, r1 = min(R, r0 + chunk);
-    C acc = red_init<C>(op);
-    for (int64_t r = r0 + threadIdx.x; r < r1; r += blockDim.x) acc = red_elem(op, acc, ldv(a, o * R + r));
+    // Four independent partial results per thread keep four loads in flight; they are joined
+    // in a fixed order.
+    const T *row = a + o * R;
+    C acc0 = red_init<C>(op), acc1 = acc0, acc2 = acc0, acc3 = acc0;
+    if constexpr (VEC) {
+        constexpr int V = 16 / int(sizeof(T));
+        struct alignas(16) Vec {
+            T e[V];
+        };
+        const Vec *vrow = reinterpret_cast<const Vec *>(row);
+        const int64_t v0 = r0 / V, v1 = r1 / V;
+        auto fold = [&](C acc, const Vec &x) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) acc = red_elem(op, acc, ldv(x.e, e));
+            return acc;
+        };
+        int64_t v = v0 + threadIdx.x;
+        for (; v + 3 * int64_t(blockDim.x) < v1; v += 4 * int64_t(blockDim.x)) {
+            const Vec x0 = vrow[v], x1 = vrow[v + blockDim.x], x2 = vrow[v + 2 * blockDim.x],
+                      x3 = vrow[v + 3 * blockDim.x];
+            acc0 = fold(acc0, x0);
+            acc1 = fold(acc1, x1);
+            acc2 = fold(acc2, x2);
+            acc3 = fold(acc3, x3);
+        }
+        for (; v < v1; v += blockDim.x) acc0 = fold(acc0, vrow[v]);
+    } else {
+        int64_t r = r0 + threadIdx.x;
+        for (; r + 3 * int64_t(blockDim.x) < r1; r += 4 * int64_t(blockDim.x)) {
+            const C x0 = ldv(row, r), x1 = ldv(row, r + blockDim.x), x2 = ldv(row, r + 2 * blockDim.x),
+                    x3 = ldv(row, r + 3 * blockDim.x);
+            acc0 = red_elem(op, acc0, x0);
+            acc1 = red_elem(op, acc1, x1);
+            acc2 = red_elem(op, acc2, x2);
+            acc3 = red_elem(op, acc3, x3);
+        }
+        for (; r < r1; r += blockDim.x) acc0 = red_elem(op, acc0, ldv(row, r));
+    }
+    C acc = red_join(op, red_join(op, acc0, acc1), red_join(op, acc2, acc3));
     acc = wave_join(op, acc);
     if ((threadIdx.x & (kWave - 1)) == 0) waves[threadIdx.x / kWave] = acc;
     __syncthreads();
@@ -314,6 +393,25 @@ __global__ __launch_bounds__(256) void reduce_final_kernel(int op, const calc_t<
     stv(out, j, red_final(op, acc, R));
 }
 
+// Stage 2 for few outputs: one workgroup per output; thread t joins partials t, t + 256, ...
+// in order, then the 256 results meet in a fixed order (waves, then the four wave results).
+template <typename T>
+__global__ __launch_bounds__(256) void reduce_final_wide_kernel(int op, const calc_t<T> *__restrict__ part,
+                                                               int64_t inner, int S, int64_t R,
+                                                               T *__restrict__ out) {
+    using C = calc_t<T>;
+    __shared__ C waves[4];
+    const int64_t j = blockIdx.x;
+    const int64_t o = j / inner, i = j - o * inner;
+    C acc = red_init<C>(op);
+    for (int s = threadIdx.x; s < S; s += blockDim.x) acc = red_join(op, acc, part[(o * S + s) * inner + i]);
+    acc = wave_join(op, acc);
+    if ((threadIdx.x & (kWave - 1)) == 0) waves[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        stv(out, j, red_final(op, red_join(op, red_join(op, waves[0], waves[1]), red_join(op, waves[2], waves[3])), R));
+}
+
 // ---- permutation, Kronecker product, integer matmul ---------------------------------------
 
 struct Perm {
@@ -332,6 +430,30 @@ __global__ __launch_bounds__(256) void permute_kernel(const W *__restrict__ a, W
             off += c * g.in_stride[k];
         }
         out[i] = a[off];
+    }
+}
+
+// out[z][c][r] = in[z][r][c] (the last two axes swapped) through a 64 x 64 LDS tile: reads and
+// writes both coalesced.  Grid (ceil(C / 64), ceil(R / 64), Z), 256 threads.
+template <typename W>
+__global__ __launch_bounds__(256) void transpose2d_kernel(const W *__restrict__ a, W *__restrict__ out, int64_t R,
+                                                         int64_t C) {
+    __shared__ W tile[64][65];
+    const int64_t z = blockIdx.z;
+    const int64_t c0 = int64_t(blockIdx.x) * 64, r0 = int64_t(blockIdx.y) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const W *src = a + z * R * C;
+    W *dst = out + z * R * C;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int64_t r = r0 + ty + 4 * i, c = c0 + tx;
+        if (r < R && c < C) tile[ty + 4 * i][tx] = src[r * C + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int64_t c = c0 + ty + 4 * i, r = r0 + tx;
+        if (r < R && c < C) dst[c * R + r] = tile[tx][ty + 4 * i];
     }
 }
 
@@ -465,8 +587,13 @@ int ctattn_tensor_cast(int src_dtype, const void *src, int dst_dtype, void *dst,
         using S = std::remove_pointer_t<decltype(stag)>;
         return by_type(dst_dtype, [&](auto *dtag) {
             using D = std::remove_pointer_t<decltype(dtag)>;
-            hipLaunchKernelGGL((ctattn::cast_kernel<S, D>), dim3(ctattn::grid_for(n)), dim3(256), 0, st,
-                               static_cast<const S *>(src), static_cast<D *>(dst), n);
+            const bool v4 = n % 4 == 0 && uintptr_t(src) % (4 * sizeof(S)) == 0 && uintptr_t(dst) % (4 * sizeof(D)) == 0;
+            if (v4)
+                hipLaunchKernelGGL((ctattn::cast_kernel<S, D, true>), dim3(ctattn::grid_for(n / 4)), dim3(256), 0, st,
+                                   static_cast<const S *>(src), static_cast<D *>(dst), n);
+            else
+                hipLaunchKernelGGL((ctattn::cast_kernel<S, D, false>), dim3(ctattn::grid_for(n)), dim3(256), 0, st,
+                                   static_cast<const S *>(src), static_cast<D *>(dst), n);
             return hipGetLastError();
         });
     });
@@ -503,12 +630,16 @@ int ctattn_tensor_binary(int dtype, int op, const void *a, int a_ndim, const int
     hipStream_t st = as_stream(stream);
     const hipError_t e = by_type(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
+        const uintptr_t al = 4 * sizeof(T), ol = op >= CTATTN_OP_EQ ? 4 : al;
+        const int v4 = g.plain && n % 4 == 0 && uintptr_t(a) % al == 0 && uintptr_t(b) % al == 0 &&
+                       uintptr_t(out) % ol == 0;
+        const dim3 grid(ctattn::grid_for(v4 ? n / 4 : n));
         if (op >= CTATTN_OP_EQ)
-            hipLaunchKernelGGL((ctattn::binary_kernel<T, true>), dim3(ctattn::grid_for(n)), dim3(256), 0, st, op,
-                               static_cast<const T *>(a), static_cast<const T *>(b), static_cast<bool *>(out), g, n);
+            hipLaunchKernelGGL((ctattn::binary_kernel<T, true>), grid, dim3(256), 0, st, op, static_cast<const T *>(a),
+                               static_cast<const T *>(b), static_cast<bool *>(out), g, n, v4);
         else
-            hipLaunchKernelGGL((ctattn::binary_kernel<T, false>), dim3(ctattn::grid_for(n)), dim3(256), 0, st, op,
-                               static_cast<const T *>(a), static_cast<const T *>(b), static_cast<T *>(out), g, n);
+            hipLaunchKernelGGL((ctattn::binary_kernel<T, false>), grid, dim3(256), 0, st, op, static_cast<const T *>(a),
+                               static_cast<const T *>(b), static_cast<T *>(out), g, n, v4);
         return hipGetLastError();
     });
     return finish(fn, e, st);
@@ -579,23 +710,34 @@ int ctattn_tensor_reduce(int dtype, int op, const void *a, int64_t outer, int64_
         return fail(hipErrorInvalidValue, "%s: workspace of %lld bytes given, %lld needed", fn,
                     (long long)workspace_bytes, (long long)need);
     const int S = reduce_splits(outer, R, inner);
-    const int64_t chunk = (R + S - 1) / S;
+    int64_t chunk = (R + S - 1) / S;
+    // 16-byte loads along contiguous rows when the rows and chunks stay 16-byte aligned.
+    const int64_t vw = 16 / elem_size(dtype);
+    const bool vec = inner == 1 && uintptr_t(a) % 16 == 0 && R % vw == 0;
+    if (vec) chunk = (chunk + vw - 1) / vw * vw;
     hipStream_t st = as_stream(stream);
     const hipError_t e = by_type(dtype, [&](auto *tag) {
         using T = std::remove_pointer_t<decltype(tag)>;
         using C = calc_t<T>;
         C *part = static_cast<C *>(workspace);
-        if (inner == 1)
-            hipLaunchKernelGGL(ctattn::reduce_rows_kernel<T>, dim3(unsigned(outer), unsigned(S)), dim3(256), 0, st, op,
-                               static_cast<const T *>(a), R, chunk, part, S);
+        if (inner == 1 && vec)
+            hipLaunchKernelGGL((ctattn::reduce_rows_kernel<T, true>), dim3(unsigned(outer), unsigned(S)), dim3(256), 0,
+                               st, op, static_cast<const T *>(a), R, chunk, part, S);
+        else if (inner == 1)
+            hipLaunchKernelGGL((ctattn::reduce_rows_kernel<T, false>), dim3(unsigned(outer), unsigned(S)), dim3(256),
+                               0, st, op, static_cast<const T *>(a), R, chunk, part, S);
         else
             hipLaunchKernelGGL(ctattn::reduce_cols_kernel<T>,
                                dim3(unsigned((inner + 255) / 256), unsigned(outer), unsigned(S)), dim3(256), 0, st, op,
                                static_cast<const T *>(a), R, inner, chunk, part);
         hipError_t le = hipGetLastError();
         if (le != hipSuccess) return le;
-        hipLaunchKernelGGL(ctattn::reduce_final_kernel<T>, dim3(unsigned((outer * inner + 255) / 256)), dim3(256), 0,
-                           st, op, static_cast<const C *>(part), outer, inner, S, R, static_cast<T *>(out));
+        if (outer * inner <= 4096 && S >= 64)
+            hipLaunchKernelGGL(ctattn::reduce_final_wide_kernel<T>, dim3(unsigned(outer * inner)), dim3(256), 0, st,
+                               op, static_cast<const C *>(part), inner, S, R, static_cast<T *>(out));
+        else
+            hipLaunchKernelGGL(ctattn::reduce_final_kernel<T>, dim3(unsigned((outer * inner + 255) / 256)), dim3(256),
+                               0, st, op, static_cast<const C *>(part), outer, inner, S, R, static_cast<T *>(out));
         return hipGetLastError();
     });
     return finish(fn, e, st);
@@ -629,6 +771,33 @@ int ctattn_tensor_permute(int dtype, const void *a, int ndim, const int64_t *sha
     if (n == 0) return ok();
     if (!a || !out) return fail(hipErrorInvalidValue, "%s: null pointer", fn);
     hipStream_t st = as_stream(stream);
+    // The last two axes swapped, the others in place: batched tiled transpose.
+    bool swap_last = ndim >= 2 && perm[ndim - 1] == ndim - 2 && perm[ndim - 2] == ndim - 1;
+    for (int k = 0; k + 2 < ndim && swap_last; ++k) swap_last = perm[k] == k;
+    if (swap_last) {
+        const int64_t R = shape[ndim - 2], C = shape[ndim - 1], Z = n / (R * C);
+        if (Z <= 65535 && (R + 63) / 64 <= 65535) {
+            const dim3 g2(unsigned((C + 63) / 64), unsigned((R + 63) / 64), unsigned(Z));
+            switch (elem_size(dtype)) {
+                case 8:
+                    hipLaunchKernelGGL(ctattn::transpose2d_kernel<uint64_t>, g2, dim3(256), 0, st,
+                                       static_cast<const uint64_t *>(a), static_cast<uint64_t *>(out), R, C);
+                    break;
+                case 4:
+                    hipLaunchKernelGGL(ctattn::transpose2d_kernel<uint32_t>, g2, dim3(256), 0, st,
+                                       static_cast<const uint32_t *>(a), static_cast<uint32_t *>(out), R, C);
+                    break;
+                case 2:
+                    hipLaunchKernelGGL(ctattn::transpose2d_kernel<uint16_t>, g2, dim3(256), 0, st,
+                                       static_cast<const uint16_t *>(a), static_cast<uint16_t *>(out), R, C);
+                    break;
+                default:
+                    hipLaunchKernelGGL(ctattn::transpose2d_kernel<uint8_t>, g2, dim3(256), 0, st,
+                                       static_cast<const uint8_t *>(a), static_cast<uint8_t *>(out), R, C);
+            }
+            return finish(fn, hipGetLastError(), st);
+        }
+    }
     const dim3 grid(ctattn::grid_for(n));
     switch (elem_size(dtype)) {
         case 8:
@@ -695,9 +864,23 @@ int ctattn_tensor_matmul(int dtype, const void *a, const void *b, void *c, int64
         });
         return finish(fn, e, st);
     }
-    // Floating types on the projection GEMMs: A [M][K] K-contiguous, B stored [K][N].  With one
-    // B the batches stack into one product of batch * M rows.
+    // fp32 / bf16 / fp16 on hipBLASLt (column-major: C^T = B^T A^T), one call when the batches
+    // stack (one B), one per batch for up to 16 batches.
     const int64_t rows = batch_b == 1 ? batch * M : M;
+    if (dtype != CTATTN_F64 && (batch_b == 1 || batch <= 16)) {
+        const int64_t es2 = elem_size(dtype);
+        bool done = true;
+        const int64_t calls = batch_b == 1 ? 1 : batch;
+        for (int64_t z = 0; z < calls && done; ++z)
+            done = ctattn::blaslt_gemm(dtype, false, false, N, rows, K, static_cast<const char *>(b) + z * K * N * es2,
+                                       N, static_cast<const char *>(a) + z * M * K * es2, K,
+                                       static_cast<char *>(c) + z * M * N * es2, N, 0.f, nullptr, st);
+        if (done) return finish(fn, hipSuccess, st);
+        // Otherwise every batch is (re)computed on the GEMM family below: the same result for
+        // batches hipBLASLt already wrote.
+    }
+    // The projection GEMMs: A [M][K] K-contiguous, B stored [K][N].  With one B the batches
+    // stack into one product of batch * M rows.
     if (rows > 2147483647 || N > 2147483647 || K > 2147483647)
         return fail(hipErrorInvalidValue, "%s: sizes must be below 2^31", fn);
     const int64_t es = elem_size(dtype);

@@ -252,6 +252,11 @@ def test_transpose_and_kron(kind):
     for perm in ([3, 1, 0, 2], [0, 1, 2, 3], [1, 0, 3, 2]):
         assert np.array_equal(t.transpose(perm).numpy(), a.transpose(perm)), perm
     assert np.array_equal(t.transpose(1, 3).numpy(), np.swapaxes(a, 1, 3))
+    # the last two axes swapped: the tiled transpose kernel (ragged tile edges included)
+    for shape in ((3, 70, 130), (1000, 7), (2, 1, 64, 65)):
+        c = (rng.integers(-5, 5, shape) if kind != "Bool" else rng.integers(0, 2, shape)).astype(npt)
+        tc = tensor(kind, c)
+        assert np.array_equal(tc.transpose(len(shape) - 2, len(shape) - 1).numpy(), np.swapaxes(c, -1, -2)), shape
     with pytest.raises(ValueError):
         t.transpose([0, 0, 1, 2])
     b = (rng.integers(-3, 3, (2, 1, 3, 2)) if kind != "Bool" else rng.integers(0, 2, (2, 1, 3, 2))).astype(npt)
