@@ -53,7 +53,7 @@ WORKLOADS = {
     "c3d": dict(B=8, H=12, T=1024, D=64, dtype="f64", std=1.0, peak=78.6,
                 metric="causal attn fwd+bwd TFLOP/s, B8 H12 T1024 d64 fp64, 1 GPU",
                 label="causal SDPA fwd+bwd, B8 H12 T1024 d64 fp64 (the headline shape in the reference's "
-                      "Double precision; generic kernels)"),
+                      "Double precision; fp64 MFMA kernels)"),
 }
 TORCH_DTYPE = {"f32": "float32", "bf16": "bfloat16", "f16": "float16", "f64": "float64"}
 B, H, T, D = 8, 12, 1024, 64

@@ -53,6 +53,15 @@ hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const vo
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
                            bool deterministic, const AttnShape &s, hipStream_t stream);
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic);
+// ---- fp64 kernels on fp64 MFMA (attn_f64_mfma.hip), d in {32, 64, 128}; lse and delta fp64.
+// The backward runs its own preprocess into `delta` ([B, H, T] fp64) and needs no other
+// scratch; dq, dk, dv are written, not accumulated. ----
+bool f64_mfma_supported(int64_t d);
+hipError_t launch_f64_fwd(const void *q, const void *k, const void *v, void *o, void *lse, const AttnShape &s,
+                          hipStream_t stream);
+hipError_t launch_f64_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
+                          const void *lse, void *delta, void *dq, void *dk, void *dv, const AttnShape &s,
+                          hipStream_t stream);
 // fp32 backward main kernel with 128-key workgroups (attn_bwd_k128.hip), d in {32, 64, 128}:
 // dq is accumulated with atomics (pre-zeroed), or, with `partial`, per-128-key-block
 // partials go to dq_part.  delta must already hold rowsum(dO * O).

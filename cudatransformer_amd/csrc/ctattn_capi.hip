@@ -84,7 +84,7 @@ int validate_shape(const char *fn, int dtype, int64_t B, int64_t H, int64_t T, i
     return 0;
 }
 
-// fp16 and fp64 storage always run the generic kernels.
+// fp32, bf16 and fp16 storage: the fp32-accumulating MFMA kernels (fp32 LSE / delta).
 bool use_mfma_fwd(int dtype, int64_t d) {
     return (dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
            ctattn::mfma_fwd_supported(dtype, d);
@@ -92,6 +92,10 @@ bool use_mfma_fwd(int dtype, int64_t d) {
 bool use_mfma_bwd(int dtype, int64_t d) {
     return (dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16) && g_policy.load() != CTATTN_POLICY_GENERIC &&
            ctattn::mfma_bwd_supported(dtype, d);
+}
+// fp64 storage: the fp64 MFMA kernels (fp64 LSE / delta, no scratch beyond delta).
+bool use_f64_mfma(int dtype, int64_t d) {
+    return dtype == CTATTN_F64 && g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::f64_mfma_supported(d);
 }
 // Bytes of one LSE / delta element: fp64 for fp64 storage, fp32 otherwise.
 int64_t stat_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : 4; }
@@ -109,9 +113,9 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
     if (!q || !k || !v || !o)
         return fail(hipErrorInvalidValue, "ctattn_fwd: null q/k/v/o pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = use_mfma_fwd(dtype, d)
-                       ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
-                       : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
+    hipError_t e = use_mfma_fwd(dtype, d)   ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
+                   : use_f64_mfma(dtype, d) ? ctattn::launch_f64_fwd(q, k, v, o, lse, s, st)
+                                            : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
     return finish("ctattn_fwd", e, st);
 }
 
@@ -149,6 +153,8 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
         e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, static_cast<const float *>(lse),
                                     static_cast<float *>(workspace), dq, dk, dv, extra, deterministic_policy(), s,
                                     st);
+    } else if (use_f64_mfma(dtype, d)) {
+        e = ctattn::launch_f64_bwd(q, k, v, o, dout, lse, workspace, dq, dk, dv, s, st);
     } else {
         e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, workspace, s, st);
     }

@@ -1,5 +1,5 @@
-"""fp16 and fp64 storage: the generic attention kernels, the fp16 / fp64 projection GEMMs and
-the Half / Double (and BFloat) classes of the host module, up to a NanoGPT training step.
+"""fp16 and fp64 storage: the attention kernels (fp16 / fp64 MFMA and generic), the fp16 / fp64
+projection GEMMs and the Half / Double (and BFloat) classes of the host module, up to a NanoGPT training step.
 
 fp64 runs accumulate in fp64 (LSE and delta are fp64 too), so they match the fp64 oracle to
 rounding: tolerance 1e-10 relative to the largest value.  fp16 stores IEEE binary16 and
@@ -67,7 +67,7 @@ def test_lse_dtype_follows_storage():
 
 
 ATTN_SHAPES = [
-    (2, 3, 77, 64),   # ragged T, MFMA-sized head dim (fp16 / fp64 always take the generic kernels)
+    (2, 3, 77, 64),   # ragged T, MFMA-sized head dim
     (1, 2, 130, 40),  # head dim off the MFMA set
     (1, 1, 1, 8),     # a single row
     (1, 2, 64, 128),
@@ -143,6 +143,43 @@ def test_f16_mfma_matches_generic_and_oracle(causal, d):
         rel_check(mfma[key], generic[key], F16_REL, f"mfma vs generic {key}")
     r1 = run()
     for key in mfma:  # no atomics in the 16-bit kernels: bitwise reproducible
+        assert np.array_equal(r1[key], mfma[key]), key
+
+
+F64_MFMA_SHAPES = [(2, 3, 300, 32), (2, 3, 300, 64), (1, 2, 300, 128), (1, 2, 1, 64), (3, 1, 17, 128),
+                   (1, 1, 513, 64)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", F64_MFMA_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_f64_mfma_matches_generic_and_oracle(shape, causal):
+    """fp64 on the fp64 MFMA kernels (16x16x4 f64, every product and sum in fp64) against the
+    generic fp64 kernels and the fp64 oracle: both to rounding.  Ragged T covers partial key
+    and query tiles, T = 1 a single row."""
+    say(f"f64 mfma vs generic shape={shape} causal={causal}")
+    q, k, v, do = ora.make_inputs(shape, seed=370 + shape[2] + shape[3], dtype="f64")
+    want = ora.attention_fwd_bwd(q, k, v, do, causal)
+    t = [dev(a, torch.float64) for a in (q, k, v, do)]
+
+    def run():
+        o, lse = ct.flash_attn_fwd(t[0], t[1], t[2], causal)
+        assert lse.dtype == torch.float64
+        dq, dk, dv = ct.flash_attn_bwd(t[0], t[1], t[2], o, t[3], lse, causal)
+        torch.cuda.synchronize()
+        return {"o": host(o), "lse": host(lse), "dq": host(dq), "dk": host(dk), "dv": host(dv)}
+
+    mfma = run()
+    prev = ct.set_policy(ct.POLICY_GENERIC)
+    try:
+        generic = run()
+    finally:
+        ct.set_policy(prev)
+    for key in mfma:  # floor 1: at T = 1 dQ is zero in exact arithmetic (dS = P (dP - delta) = 0)
+        rel_check(mfma[key], want[key], F64_REL, f"mfma {key}", floor=1.0)
+        rel_check(mfma[key], generic[key], F64_REL, f"mfma vs generic {key}", floor=1.0)
+    r1 = run()
+    for key in mfma:  # no atomics in the fp64 kernels: bitwise reproducible
         assert np.array_equal(r1[key], mfma[key]), key
 
 
