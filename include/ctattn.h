@@ -22,8 +22,9 @@
  *     hipErrorNotSupported (801).
  *   - supported: dtype f32, bf16 or f16 (storage; arithmetic accumulates in fp32) or f64
  *     (arithmetic in fp64, the reference's ComputeType<double>), 1 <= d <= 256, T >= 0,
- *     B, H >= 0.  f32 and bf16 with d in {32, 64, 128} run on the MFMA kernels; every
- *     other case on the generic kernels.
+ *     B, H >= 0.  d in {32, 64, 128} runs on the MFMA kernels (fp32 on f32 MFMA, bf16 and
+ *     f16 on 16-bit MFMA with fp32 accumulation, f64 on f64 MFMA); every other head dim on
+ *     the generic kernels.
  */
 #ifndef CTATTN_H
 #define CTATTN_H
