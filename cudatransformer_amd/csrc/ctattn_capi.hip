@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 
 namespace ctattn {
 namespace capi {
@@ -97,6 +98,15 @@ bool use_mfma_bwd(int dtype, int64_t d) {
 bool use_f64_mfma(int dtype, int64_t d) {
     return dtype == CTATTN_F64 && g_policy.load() != CTATTN_POLICY_GENERIC && ctattn::f64_mfma_supported(d);
 }
+// The MFMA kernels move 16 bytes per load (float4 / double2 / direct-to-LDS dwordx4); row
+// strides are multiples of 16 bytes for d in {32, 64, 128}, so 16-byte-aligned base pointers
+// suffice.  Element-aligned views that are not (a tensor offset into its storage) take the
+// generic kernels, which access element by element.
+bool aligned16(std::initializer_list<const void *> ps) {
+    for (const void *p : ps)
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+    return true;
+}
 // Bytes of one LSE / delta element: fp64 for fp64 storage, fp32 otherwise.
 int64_t stat_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : 4; }
 bool deterministic_policy() { return g_policy.load() == CTATTN_POLICY_DETERMINISTIC; }
@@ -113,9 +123,10 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
     if (!q || !k || !v || !o)
         return fail(hipErrorInvalidValue, "ctattn_fwd: null q/k/v/o pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = use_mfma_fwd(dtype, d)   ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
-                   : use_f64_mfma(dtype, d) ? ctattn::launch_f64_fwd(q, k, v, o, lse, s, st)
-                                            : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
+    const bool al = aligned16({q, k, v, o, lse});
+    hipError_t e = use_mfma_fwd(dtype, d) && al ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
+                   : use_f64_mfma(dtype, d) && al ? ctattn::launch_f64_fwd(q, k, v, o, lse, s, st)
+                                                  : ctattn::launch_generic_fwd(dtype, q, k, v, o, lse, s, st);
     return finish("ctattn_fwd", e, st);
 }
 
@@ -148,12 +159,15 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
                     (long long)workspace_bytes, (long long)need);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
-    if (use_mfma_bwd(dtype, d)) {
+    // Misaligned tensors take the generic kernels, whose workspace (delta only) is a prefix of
+    // what ctattn_bwd_workspace_bytes asked for.
+    const bool al = aligned16({q, k, v, o, dout, lse, dq, dk, dv, workspace});
+    if (use_mfma_bwd(dtype, d) && al) {
         void *extra = static_cast<char *>(workspace) + align_up(s.rows() * stat_bytes(dtype));
         e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, static_cast<const float *>(lse),
                                     static_cast<float *>(workspace), dq, dk, dv, extra, deterministic_policy(), s,
                                     st);
-    } else if (use_f64_mfma(dtype, d)) {
+    } else if (use_f64_mfma(dtype, d) && al) {
         e = ctattn::launch_f64_bwd(q, k, v, o, dout, lse, workspace, dq, dk, dv, s, st);
     } else {
         e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, workspace, s, st);

@@ -24,7 +24,9 @@
  *     (arithmetic in fp64, the reference's ComputeType<double>), 1 <= d <= 256, T >= 0,
  *     B, H >= 0.  d in {32, 64, 128} runs on the MFMA kernels (fp32 on f32 MFMA, bf16 and
  *     f16 on 16-bit MFMA with fp32 accumulation, f64 on f64 MFMA); every other head dim on
- *     the generic kernels.
+ *     the generic kernels.  Tensors must be element-aligned; the MFMA kernels also need
+ *     16-byte-aligned q, k, v, o, lse (and dout, dq, dk, dv, workspace in the backward); calls
+ *     whose pointers are not take the generic kernels (same results, slower).
  */
 #ifndef CTATTN_H
 #define CTATTN_H

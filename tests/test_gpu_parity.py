@@ -205,3 +205,45 @@ def test_invalid_inputs_raise():
     rc = lib.ctattn_fwd(0, q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(), None,
                         1, 2, 16, 300, 0, None)
     assert rc == 801
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.float64],
+                         ids=["f32", "bf16", "f16", "f64"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_misaligned_views_take_the_generic_kernels(dtype, causal):
+    """Contiguous [B, H, T, d] views one element into their storage (4, 2, 2 or 8 bytes off a
+    16-byte boundary) are valid C-ABI arguments; the MFMA kernels need 16-byte-aligned
+    pointers, so such calls run on the generic kernels: bitwise equal to the generic policy
+    on aligned copies of the same data, and close to the oracle."""
+    shape = (2, 3, 150, 64)
+    say(f"misaligned views dtype={dtype} causal={causal}")
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16", torch.float64: "f64"}[dtype]
+    q, k, v, do = ora.make_inputs(shape, seed=41, dtype=name)
+    n = int(np.prod(shape))
+
+    def offset_view(a):
+        buf = torch.empty(n + 1, device=DEV, dtype=dtype)
+        t = buf[1:].view(shape)
+        t.copy_(torch.from_numpy(np.ascontiguousarray(a, np.float64)).to(DEV, dtype))
+        assert t.is_contiguous() and t.data_ptr() % 16 != 0
+        return t
+
+    def run(ts):
+        o, lse = ct.flash_attn_fwd(ts[0], ts[1], ts[2], causal)
+        dq, dk, dv = ct.flash_attn_bwd(ts[0], ts[1], ts[2], o, ts[3], lse, causal)
+        torch.cuda.synchronize()
+        return {key: t.double().cpu().numpy() for key, t in
+                (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv))}
+
+    got = run([offset_view(a) for a in (q, k, v, do)])
+    prev = ct.set_policy(ct.POLICY_GENERIC)
+    try:
+        ref = run([torch.from_numpy(np.ascontiguousarray(a, np.float64)).to(DEV, dtype) for a in (q, k, v, do)])
+    finally:
+        ct.set_policy(prev)
+    want = ora.attention_fwd_bwd(*ora.cast_inputs((q, k, v, do), name), causal)
+    rel = {"f32": 1e-5, "bf16": BF16_REL_TOL, "f16": 4e-3, "f64": 1e-10}[name]
+    for key in got:
+        assert np.array_equal(got[key], ref[key]), key
+        err = float(np.max(np.abs(got[key] - want[key])))
+        assert err <= rel * max(float(np.max(np.abs(want[key]))), 1.0), (key, err)
