@@ -69,9 +69,13 @@ struct Stage {
 // ---------------------------------------------------------------------------------------
 template <int D>
 struct F64Fwd {
-    static constexpr int QT = D == 128 ? 1 : 2;  // 16-query tiles per wave
+    // Measured per d (B8 H12 T1024 causal): d = 64 runs best with 2 query tiles and 32-key
+    // blocks at 2 waves / SIMD; d = 32 with 1 tile and 16-key blocks at 4 waves / SIMD
+    // (187 vs 231 us); d = 128 is bounded by registers to 1 tile and 16 keys.
+    static constexpr int QT = D == 64 ? 2 : 1;   // 16-query tiles per wave
     static constexpr int BM = 64 * QT;           // query rows per workgroup
-    static constexpr int BN = D == 128 ? 16 : 32;
+    static constexpr int BN = D == 64 ? 32 : 16;
+    static constexpr int WAVES = D == 32 ? 4 : 2;  // waves per SIMD
     static constexpr int KT = BN / 16;
     static constexpr int DT = D / 16;
     static constexpr int KS = D / 4;             // k-steps over d
@@ -80,7 +84,7 @@ struct F64Fwd {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_f64_mfma_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(F64Fwd<D>::WAVES, F64Fwd<D>::WAVES))) void fwd_f64_mfma_kernel(
     const double *__restrict__ q, const double *__restrict__ k, const double *__restrict__ v, double *__restrict__ o,
     double *__restrict__ lse, int T, int BH, int causal, double c) {
     using C = F64Fwd<D>;
@@ -228,6 +232,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// Waves per SIMD of the backward kernels: d = 128 tiles take > 80 KiB of LDS (one workgroup
+// per CU); at d = 32 the dQ kernel fits four workgroups in registers and LDS, the dK / dV
+// kernel three (four would spill).
+template <int D, bool KV>
+struct F64BwdWaves {
+    static constexpr int value = D == 128 ? 1 : D == 32 ? (KV ? 3 : 4) : 2;
+};
+
 // ---------------------------------------------------------------------------------------
 // Backward dK / dV (key-major): a workgroup of 4 waves owns 64 keys (wave w: keys 16 w ..),
 // keeps K and V of its keys as B operands in registers and walks 32-query blocks.
@@ -244,7 +256,7 @@ struct F64Kv {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 1 : 2, 2))) void bwd_f64_dkdv_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(F64BwdWaves<D, true>::value, F64BwdWaves<D, true>::value))) void bwd_f64_dkdv_kernel(
     const double *__restrict__ q, const double *__restrict__ k, const double *__restrict__ v,
     const double *__restrict__ dout, const double *__restrict__ lse, const double *__restrict__ delta,
     double *__restrict__ dk, double *__restrict__ dv, int T, int BH, int causal, double c, double inv_sqrt_d) {
@@ -376,7 +388,7 @@ struct F64Dq {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 1 : 2, 2))) void bwd_f64_dq_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(F64BwdWaves<D, false>::value, F64BwdWaves<D, false>::value))) void bwd_f64_dq_kernel(
     const double *__restrict__ q, const double *__restrict__ k, const double *__restrict__ v,
     const double *__restrict__ dout, const double *__restrict__ lse, const double *__restrict__ delta,
     double *__restrict__ dq, int T, int BH, int causal, double c, double inv_sqrt_d) {

@@ -184,6 +184,38 @@ def test_f64_mfma_matches_generic_and_oracle(shape, causal):
 
 
 @pytest.mark.gpu
+def test_f64_mfma_full_size_c3d():
+    """The c3d bench shape (B8 H12 T1024 d64, causal, fp64): the fp64 MFMA kernels against the
+    generic fp64 kernels on the GPU (both fp64 throughout; the dense numpy oracle is too slow
+    at this size), plus the size-independent identities sum_t dV = sum_t dO (the softmax rows
+    sum to one) and sum_t dK = 0 (dS rows sum to zero)."""
+    shape = (8, 12, 1024, 64)
+    say("f64 mfma vs generic at c3d size")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q, k, v, do = (torch.randn(shape, device="cuda", dtype=torch.float64, generator=g) for _ in range(4))
+
+    def run():
+        o, lse = ct.flash_attn_fwd(q, k, v, True)
+        dq, dk, dv = ct.flash_attn_bwd(q, k, v, o, do, lse, True)
+        torch.cuda.synchronize()
+        return {"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}
+
+    mfma = run()
+    prev = ct.set_policy(ct.POLICY_GENERIC)
+    try:
+        generic = run()
+    finally:
+        ct.set_policy(prev)
+    for key in mfma:
+        err = float((mfma[key] - generic[key]).abs().max())
+        scale = max(float(generic[key].abs().max()), 1.0)
+        assert err <= F64_REL * scale, f"{key}: {err:.3e} vs {scale:.3e}"
+    dv_sum, do_sum = mfma["dv"].sum(2), do.sum(2)
+    assert float((dv_sum - do_sum).abs().max()) <= 1e-9 * float(do_sum.abs().max())
+    assert float(mfma["dk"].sum(2).abs().max()) <= 1e-9 * float(mfma["dk"].abs().max()) * 1024
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float16], ids=["f64", "f16"])
 def test_flash_layer_pybind(dtype):
     name = NAME[dtype]
