@@ -5,7 +5,8 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 ``torch.nn.functional.scaled_dot_product_attention`` is the routine the reference's own
 test compares against (``test_flash_attention.py:49``, there with ``is_causal=False``).
 In fp64 with autograd it is an independent library check of ``attention_fp64``; in fp32
-on all host cores it is the CPU baseline that ``bench.py`` reports.
+on all host cores it is the multi-threaded CPU figure that ``bench.py`` reports beside its
+CPU baseline (the C restatement ``attn_online.c``).
 """
 from __future__ import annotations
 
