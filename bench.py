@@ -64,32 +64,35 @@ STEP_FLOP = FWD_FLOP + BWD_FLOP
 PEAK_F32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 METRIC = WORKLOADS["c3"]["metric"]
 HERE = os.path.dirname(os.path.abspath(__file__))
-TRAFFIC_FILE = os.path.join(HERE, "profiles", "attn_bwd_f32_c3_traffic.txt")
+COUNTERS_FILE = os.path.join(HERE, "profiles", "attn_f32_c3_counters.txt")
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def read_traffic():
-    """HBM bytes per launch of the backward kernel, from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel calibration); None if absent."""
+def read_profile_figures(path):
+    """Machine-readable figures of a committed rocprofv3 summary: every line of the form
+    ``bench.<key>: <number>``.  Empty if the file is absent."""
+    figs = {}
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
+                if line.startswith("bench.") and ":" in line:
+                    key, val = line[len("bench."):].split(":", 1)
+                    figs[key.strip()] = float(val)
     except OSError:
         pass
-    return None
+    return figs
 
 
 def cpu_baseline(seconds: float):
-    """The C restatement of the reference algorithm (oracle/attn_online.c: fp64 tiled online
-    softmax forward, recompute backward; scalar, one thread) on the headline step, one
-    (b, h) slice after another until `seconds` have elapsed or the step is done; plus, for
-    comparison, torch SDPA on CPU tensors (the reference test's comparator) on all host
-    threads."""
+    """The north star's CPU comparator: torch.nn.functional.scaled_dot_product_attention in
+    fp32 on CPU tensors, forward + backward of the full headline step on every host thread
+    (the routine the reference's test_flash_attention.py:49 checks against), median of
+    repetitions over about `seconds`.  Beside it, the C restatement of the reference
+    algorithm (oracle/attn_online.c: fp64 tiled online softmax, recompute backward; scalar,
+    one thread) over one (b, h) slice after another until `seconds` have elapsed."""
     sys.path.insert(0, HERE)
     import time
 
@@ -97,6 +100,9 @@ def cpu_baseline(seconds: float):
 
     from oracle import c_oracle, torch_cpu
 
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    med, reps, threads = torch_cpu.time_fwd_bwd((B, H, T, D), CAUSAL, seconds=seconds,
+                                               threads=threads)
     rng = np.random.default_rng(3)
     try:
         c_oracle.load()
@@ -112,35 +118,31 @@ def cpu_baseline(seconds: float):
         c_oracle.bwd(q, k, v, o, do, lse, CAUSAL)
         busy += time.perf_counter() - t0
         done += 1
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    med, reps, threads = torch_cpu.time_fwd_bwd((B, H, T, D), CAUSAL, seconds=seconds,
-                                               threads=threads)
     return {
-        "value": STEP_FLOP * done / (B * H) / busy / 1e12,
+        "value": STEP_FLOP / med / 1e12,
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/attn_online.c (fp64, scalar, 1 thread) fwd+bwd of {done} of the "
-                   f"{B * H} (b, h) slices of the B{B} H{H} T{T} d{D} causal step in "
-                   f"{busy:.1f} s ({busy / done * B * H:.1f} s per full step)"),
-        "torch_sdpa_cpu": {
-            "value": STEP_FLOP / med / 1e12,
-            "unit": "TFLOP/s",
-            "cores": threads,
-            "sample": (f"torch.nn.functional.scaled_dot_product_attention fp32 causal fwd+bwd "
-                       f"on CPU tensors, full step, median of {reps} reps ({med * 1e3:.1f} "
-                       f"ms/step)"),
-        },
+        "sample": (f"oracle/torch_cpu.py: torch.nn.functional.scaled_dot_product_attention fp32 "
+                   f"causal fwd+bwd on CPU tensors (the comparator of the reference's "
+                   f"test_flash_attention.py:49), the full B{B} H{H} T{T} d{D} step on {threads} "
+                   f"host threads, median of {reps} reps = {med * 1e3:.1f} ms/step"),
+        "c_port_value": STEP_FLOP * done / (B * H) / busy / 1e12,
+        "c_port_sample": (f"oracle/attn_online.c (fp64, scalar, 1 thread) fwd+bwd of {done} of the "
+                          f"{B * H} (b, h) slices in {busy:.1f} s ({busy / done * B * H:.1f} s per "
+                          f"full step)"),
     }
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 50 warmup steps (~25 ms of kernels) let the GPU clocks ramp before timing; with only a
-    # handful the first timed steps still run at idle clocks (about 7% slower for c3).
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
+    # After the --warmup steps, more untimed steps run until this much wall time has passed:
+    # the GPU clocks take a few hundred ms of load to settle, and with a handful of warm-up
+    # steps the first timed steps run about 7-10% slower.  Reported as config.preroll_*.
+    ap.add_argument("--preroll-ms", type=float, default=1000.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c3")
@@ -216,6 +218,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    preroll_steps, preroll_s = preroll(step, args.preroll_ms)
 
     # Whole-step timing: exactly K steps between two events on the launch stream.
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -270,6 +273,8 @@ def main():
             # computeBackward per step, output / gradient / workspace allocation included,
             # host wall clock around synchronised steps.
             "layer_path_ms": None if layer_ms is None else round(layer_ms, 5),
+            "preroll_steps": preroll_steps,
+            "preroll_s": round(preroll_s, 3),
         },
         "roofline": {
             "bound": "mfma",
@@ -278,14 +283,48 @@ def main():
             "peak": PEAK_F32_MFMA,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_F32_MFMA, 4),
-            "traffic": read_traffic() if args.workload == "c3" else None,
+            "traffic": None,
         },
         "cpu_baseline": None,
     }
+    if args.workload == "c3":
+        # Counter-derived figures of the same kernels at the same shape, from the committed
+        # rocprofv3 --pmc summary: HBM bytes per backward call (FETCH_SIZE + WRITE_SIZE,
+        # copy-calibrated) -> GB/s over this run's measured backward time, and MFMA
+        # utilisation (SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' active cycles).
+        figs = read_profile_figures(COUNTERS_FILE)
+        if "bwd_traffic_bytes" in figs:
+            out["roofline"]["traffic"] = figs["bwd_traffic_bytes"]
+            out["roofline"]["hbm_gbs"] = round(figs["bwd_traffic_bytes"] / (bwd_ms * 1e-3) / 1e9, 1)
+        for key in ("bwd_mfma_util_pct", "fwd_mfma_util_pct"):
+            if key in figs:
+                out["roofline"][key] = figs[key]
+                out["config"][key] = figs[key]
+        if "fwd_traffic_bytes" in figs:
+            out["config"]["fwd_hbm_gbs"] = round(figs["fwd_traffic_bytes"] / (fwd_ms * 1e-3) / 1e9, 1)
+        if "hbm_gbs" in out["roofline"]:
+            out["config"]["bwd_hbm_gbs"] = out["roofline"]["hbm_gbs"]
+        out["roofline"]["counters_source"] = os.path.relpath(COUNTERS_FILE, HERE) if figs else None
     if not args.no_cpu_baseline:
         log("timing CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
+
+
+def preroll(step, ms):
+    """Untimed steps, in batches of 10 with a synchronisation after each, until `ms` of wall
+    time have passed (clock ramp-up).  Returns (steps, seconds)."""
+    import time
+
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
+        n += 10
+    return n, time.perf_counter() - t0
 
 
 def bench_tensor(args, wl):

@@ -419,20 +419,24 @@ __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t
                                                                  float *__restrict__ delta,
                                                                  float *__restrict__ nl2, int64_t rows) {
     constexpr int LPR = D / 8;  // lanes per row
-    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t row = t / LPR;
-    const int c8 = int(t % LPR);
-    float s = 0.f;
-    if (row < rows) {
-        const u16x8 a = *reinterpret_cast<const u16x8 *>(o + row * D + 8 * c8);
-        const u16x8 b = *reinterpret_cast<const u16x8 *>(dout + row * D + 8 * c8);
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    // Grid-stride; the block size and the stride are multiples of LPR, so the LPR lanes of a
+    // row enter and leave the loop together (group_sum stays inside the group).
+    for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t / LPR < rows; t += stride) {
+        const int64_t row = t / LPR;
+        const int c8 = int(t % LPR);
+        float s = 0.f;
+        if (row < rows) {
+            const u16x8 a = *reinterpret_cast<const u16x8 *>(o + row * D + 8 * c8);
+            const u16x8 b = *reinterpret_cast<const u16x8 *>(dout + row * D + 8 * c8);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += F::widen(a[e]) * F::widen(b[e]);
-    }
-    s = group_sum<LPR>(s);
-    if (row < rows && c8 == 0) {
-        delta[row] = s;
-        nl2[row] = -lse[row] * kLog2e;
+            for (int e = 0; e < 8; ++e) s += F::widen(a[e]) * F::widen(b[e]);
+        }
+        s = group_sum<LPR>(s);
+        if (row < rows && c8 == 0) {
+            delta[row] = s;
+            nl2[row] = -lse[row] * kLog2e;
+        }
     }
 }
 
@@ -444,13 +448,12 @@ hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, 
     using QC = QCfg<D>;
     const int64_t kv_blocks = ((s.T + KC::BN - 1) / KC::BN) * s.bh();
     const int64_t q_blocks = ((s.T + QC::BM - 1) / QC::BM) * s.bh();
-    if (kv_blocks > 2147483647 || q_blocks > 2147483647 || s.T > 2147483647 / D ||
-        s.rows() * (D / 8) / 256 >= 2147483647)
+    if (!grid_fits(kv_blocks, KC::NW * kWave) || !grid_fits(q_blocks, QC::NW * kWave) || s.T > 2147483647 / D)
         return hipErrorInvalidValue;
     const int64_t rows = s.rows();
     auto u16 = [](const void *p) { return static_cast<const uint16_t *>(p); };
     const int64_t pre_threads = rows * (D / 8);
-    hipLaunchKernelGGL((bwd_preprocess_bf16_kernel<D, F>), dim3(unsigned((pre_threads + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL((bwd_preprocess_bf16_kernel<D, F>), dim3(stride_grid((pre_threads + 255) / 256, 256)), dim3(256), 0, stream,
                        u16(o), u16(dout), lse, delta, nl2, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -318,7 +318,7 @@ hipError_t launch_k128(const float *q, const float *k, const float *v, const flo
                        const AttnShape &s, hipStream_t stream) {
     using C = BwdK128Cfg<D>;
     const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh();
-    if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float kscale = kLog2e / sqrtf(float(D));
     const float inv_sqrt_d = 1.f / sqrtf(float(D));
     if (partial)

@@ -337,18 +337,22 @@ __global__ __launch_bounds__(256) void bwd_preprocess_f32_kernel(const float *__
                                                                 float *__restrict__ dq,
                                                                 int64_t rows) {
     constexpr int LPR = D / 4;  // lanes per row
-    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t row = t / LPR;
-    const int c4 = int(t % LPR);
-    float s = 0.f;
-    if (row < rows) {
-        const floatx4 a = *reinterpret_cast<const floatx4 *>(o + row * D + 4 * c4);
-        const floatx4 b = *reinterpret_cast<const floatx4 *>(dout + row * D + 4 * c4);
-        s = (a[0] * b[0] + a[1] * b[1]) + (a[2] * b[2] + a[3] * b[3]);
-        if (ZERO_DQ) *reinterpret_cast<floatx4 *>(dq + row * D + 4 * c4) = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    // Grid-stride; the block size and the stride are multiples of LPR, so the LPR lanes of a
+    // row enter and leave the loop together (group_sum stays inside the group).
+    for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t / LPR < rows; t += stride) {
+        const int64_t row = t / LPR;
+        const int c4 = int(t % LPR);
+        float s = 0.f;
+        if (row < rows) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(o + row * D + 4 * c4);
+            const floatx4 b = *reinterpret_cast<const floatx4 *>(dout + row * D + 4 * c4);
+            s = (a[0] * b[0] + a[1] * b[1]) + (a[2] * b[2] + a[3] * b[3]);
+            if (ZERO_DQ) *reinterpret_cast<floatx4 *>(dq + row * D + 4 * c4) = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+        s = group_sum<LPR>(s);
+        if (row < rows && c4 == 0) delta[row] = s;
     }
-    s = group_sum<LPR>(s);
-    if (row < rows && c4 == 0) delta[row] = s;
 }
 
 // dq[bh][row][:] = sum over key blocks kb <= (causal ? row / BN : nkb - 1) of dq_part[kb][bh][row][:],
@@ -357,17 +361,17 @@ template <int D>
 __global__ __launch_bounds__(256) void dq_reduce_kernel(const float *__restrict__ dq_part,
                                                        float *__restrict__ dq, int T, int BH,
                                                        int causal, int nkb, int bn) {
-    const int64_t f = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t total = int64_t(BH) * T * (D / 4);
-    if (f >= total) return;
-    const int64_t row_g = f / (D / 4);  // bh * T + row
-    const int row = int(row_g % T);
-    const int last = causal ? row / bn : nkb - 1;
     const int64_t plane = int64_t(BH) * T * D;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = 0; kb <= last; ++kb)
-        acc += *reinterpret_cast<const floatx4 *>(dq_part + kb * plane + 4 * f);
-    *reinterpret_cast<floatx4 *>(dq + 4 * f) = acc;
+    for (int64_t f = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; f < total; f += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t row_g = f / (D / 4);  // bh * T + row
+        const int row = int(row_g % T);
+        const int last = causal ? row / bn : nkb - 1;
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb <= last; ++kb)
+            acc += *reinterpret_cast<const floatx4 *>(dq_part + kb * plane + 4 * f);
+        *reinterpret_cast<floatx4 *>(dq + 4 * f) = acc;
+    }
 }
 
 // Key-block size of the deterministic dQ partials: they come from the 128-key kernel.
@@ -384,13 +388,12 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
                    hipStream_t stream) {
     const int64_t rows = s.rows();
     if (s.T > 2147483647 / D) return hipErrorInvalidValue;
-    const int64_t pre_blocks = (rows * (D / 4) + 255) / 256;
-    if (pre_blocks > 2147483647) return hipErrorInvalidValue;
+    const unsigned pre_blocks = stride_grid((rows * (D / 4) + 255) / 256, 256);
     if (mode == DqMode::Atomic) {
-        hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, true>), dim3(unsigned(pre_blocks)), dim3(256), 0, stream,
+        hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, true>), dim3(pre_blocks), dim3(256), 0, stream,
                            o, dout, delta, dq, rows);
     } else {
-        hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, false>), dim3(unsigned(pre_blocks)), dim3(256), 0, stream,
+        hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, false>), dim3(pre_blocks), dim3(256), 0, stream,
                            o, dout, delta, dq, rows);
     }
     hipError_t e = hipGetLastError();
@@ -399,7 +402,7 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
       if (use_k64_kernel(s, mode)) {
         using C = BwdCfg<D>;
         const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh();
-        if (blocks > 2147483647) return hipErrorInvalidValue;
+        if (!grid_fits(blocks, C::NW * kWave)) return hipErrorInvalidValue;
         const float kscale = kLog2e / sqrtf(float(D));
         const float inv_sqrt_d = 1.f / sqrtf(float(D));
         hipLaunchKernelGGL((bwd_f32_mfma_kernel<D>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream, q, k,
@@ -412,7 +415,7 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
     if (e != hipSuccess || mode == DqMode::Atomic) return e;
     const int64_t nkb = (s.T + kPartialBN - 1) / kPartialBN;
     const int64_t n4 = rows * (D / 4);
-    hipLaunchKernelGGL(dq_reduce_kernel<D>, dim3(unsigned((n4 + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(dq_reduce_kernel<D>, dim3(stride_grid((n4 + 255) / 256, 256)), dim3(256), 0, stream,
                        dq_part, dq, int(s.T), int(s.bh()), int(s.causal), int(nkb), kPartialBN);
     return hipGetLastError();
 }

@@ -488,7 +488,7 @@ hipError_t fwd_f64(const void *q, const void *k, const void *v, void *o, void *l
                    hipStream_t stream) {
     using C = F64Fwd<D>;
     const int64_t blocks = ((s.T + C::BM - 1) / C::BM) * s.bh();
-    if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    if (!grid_fits(blocks, 256) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     hipLaunchKernelGGL(fwd_f64_mfma_kernel<D>, dim3(unsigned(blocks)), dim3(256), 0, stream,
                        static_cast<const double *>(q), static_cast<const double *>(k),
                        static_cast<const double *>(v), static_cast<double *>(o), static_cast<double *>(lse),
@@ -501,7 +501,7 @@ hipError_t bwd_f64(const void *q, const void *k, const void *v, const void *o, c
                    void *delta, void *dq, void *dk, void *dv, const AttnShape &s, hipStream_t stream) {
     const int64_t kv_blocks = ((s.T + F64Kv<D>::BN - 1) / F64Kv<D>::BN) * s.bh();
     const int64_t q_blocks = ((s.T + F64Dq<D>::BM - 1) / F64Dq<D>::BM) * s.bh();
-    if (kv_blocks > 2147483647 || q_blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    if (!grid_fits(kv_blocks, 256) || !grid_fits(q_blocks, 256) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     hipError_t e = launch_bwd_preprocess(3, o, dout, delta, s, stream);  // delta = rowsum(dO * O), fp64
     if (e != hipSuccess) return e;
     const double c = kLog2eD / sqrt(double(D)), inv_sqrt_d = 1.0 / sqrt(double(D));

@@ -233,7 +233,7 @@ hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float 
     using C = FwdBf16Cfg<D>;
     const int64_t nqb = (s.T + C::BM - 1) / C::BM;
     const int64_t blocks = nqb * s.bh();
-    if (blocks > 2147483647 || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float c = kLog2e / sqrtf(float(D));
     hipLaunchKernelGGL((fwd_bf16_mfma_kernel<D, F>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
                        static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),

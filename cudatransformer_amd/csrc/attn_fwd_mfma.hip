@@ -260,8 +260,7 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
     using C = FwdCfg<D, BN>;
     const int64_t nqb = (s.T + C::BM - 1) / C::BM;
     const int64_t blocks = nqb * s.bh();
-    if (blocks > 2147483647 || s.T > 2147483647 / D)
-        return hipErrorInvalidValue;
+    if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float qscale = kLog2e / sqrtf(float(D));
     hipLaunchKernelGGL((fwd_f32_mfma_kernel<D, BN>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
                        stream, q, k, v, o, lse, int(s.T), int(s.bh()), int(s.causal), qscale);

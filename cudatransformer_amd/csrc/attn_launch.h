@@ -15,6 +15,18 @@ struct AttnShape {
     int64_t rows() const { return B * H * T; }
 };
 
+// A launch may hold at most 2^32 - 1 work-items (gridDim.x * blockDim.x) and 2^31 - 1
+// workgroups.  Fixed-shape kernels check their grid with grid_fits and refuse larger
+// problems; grid-stride kernels (generic attention, preprocess, reductions) cap their grid
+// with stride_grid and loop.
+inline bool grid_fits(int64_t blocks, int threads) {
+    return blocks >= 0 && blocks <= 0x7FFFFFFFll && blocks * threads <= 0xFFFFFFFFll;
+}
+inline unsigned stride_grid(int64_t blocks, int threads) {
+    const int64_t cap = (int64_t(1) << 30) / threads;  // 2^30 work-items: fills the chip many times over
+    return unsigned(blocks < 1 ? 1 : (blocks < cap ? blocks : cap));
+}
+
 // ---- generic kernels: any 1 <= d <= 256; dtype 0 fp32, 1 bf16, 2 fp16, 3 fp64.  lse and
 // delta are fp64 for dtype 3 and fp32 otherwise. ----
 hipError_t launch_generic_fwd(int dtype, const void *q, const void *k, const void *v, void *o,

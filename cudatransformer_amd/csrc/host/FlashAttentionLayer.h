@@ -8,8 +8,10 @@
 //   * a `causal` member (default false = the reference's unmasked attention);
 //   * the cached state is the fp32 logsumexp [B, H, T] instead of (max, denominator);
 //   * the cached output shares the returned tensor's buffer instead of a D2D copy
-//     (FlashAttentionLayer.cu:81-84); callers must not modify the returned O in place
-//     between computeAttention(..., true) and computeBackward;
+//     (FlashAttentionLayer.cu:81-84), together with the tensor's version count: when the
+//     returned O was written in place through the Tensor API (fill, mutable data()) before
+//     computeBackward, the backward recomputes the forward instead of using the changed O,
+//     which gives the reference's result (it kept a private copy) without the copy;
 //   * the cache is only used when its batch size and sequence length match the call;
 //   * shapes are validated ([B, numHeads, T, headDim]) and every launch is checked.
 #pragma once
@@ -35,6 +37,7 @@ struct FlashAttentionLayer {
     // Cached forward state (FlashAttentionLayer.cu:18-22).
     Tensor<Stat> cachedLse;  // LSE [B, H, T]: fp64 for double, fp32 otherwise
     Tensor<DType> cachedOutput;
+    uint64_t cachedOutputVersion = 0;  // cachedOutput.version() when it was cached
     int cachedBatchSize = 0;
     int cachedSequenceLength = 0;
 
@@ -67,6 +70,7 @@ struct FlashAttentionLayer {
         if (saveStates) {
             cachedLse = lse;
             cachedOutput = output;
+            cachedOutputVersion = output.version();
             cachedBatchSize = int(B);
             cachedSequenceLength = int(T);
         }
@@ -84,8 +88,10 @@ struct FlashAttentionLayer {
         const size_t B = queries.shape(0), T = queries.shape(2);
         Tensor<Stat> lse = cachedLse;
         Tensor<DType> output = cachedOutput;
-        if (lse.empty() || output.empty() || cachedBatchSize != int(B) || cachedSequenceLength != int(T)) {
-            // No usable cached forward: recompute it (FlashAttentionLayer.cu:114-127).
+        if (lse.empty() || output.empty() || cachedBatchSize != int(B) || cachedSequenceLength != int(T) ||
+            output.version() != cachedOutputVersion) {
+            // No usable cached forward (none, another shape, or the returned O was written in
+            // place since): recompute it (FlashAttentionLayer.cu:114-127).
             lse = Tensor<Stat>::empty({B, size_t(numHeads), T});
             output = Tensor<DType>::empty(queries.shape());
             ctattnCheck(ctattn_fwd(DTypeCode<DType>::value, queries.get(), keys.get(), values.get(), output.get(),
@@ -113,6 +119,7 @@ struct FlashAttentionLayer {
     void clearCache() {
         cachedLse = Tensor<Stat>();
         cachedOutput = Tensor<DType>();
+        cachedOutputVersion = 0;
         cachedBatchSize = 0;
         cachedSequenceLength = 0;
     }

@@ -13,6 +13,7 @@
 // token ids.  The reference's tensor algebra (Tensor.cu:290-958) is not part of this path.
 #pragma once
 
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -257,6 +258,7 @@ public:
         if (shape_.size() > 8) throw std::invalid_argument("Tensor does not support more than 8 dimensions");
         size_ = std::accumulate(shape_.begin(), shape_.end(), size_t(1), std::multiplies<size_t>());
         data_ = deviceAlloc<DType>(size_);
+        version_ = std::make_shared<std::atomic<uint64_t>>(0);
         fill(value);
     }
 
@@ -267,13 +269,16 @@ public:
         t.shape_ = shape;
         t.size_ = std::accumulate(shape.begin(), shape.end(), size_t(1), std::multiplies<size_t>());
         t.data_ = deviceAlloc<DType>(t.size_);
+        t.version_ = std::make_shared<std::atomic<uint64_t>>(0);
         return t;
     }
 
-    // Shallow wrap of an existing buffer (Tensor.cu:62-66).
+    // Shallow wrap of an existing buffer (Tensor.cu:62-66).  The wrapper starts its own
+    // version count (see version()).
     Tensor(std::shared_ptr<DType[]> data, const std::vector<size_t> &shape) : shape_(shape) {
         size_ = std::accumulate(shape_.begin(), shape_.end(), size_t(1), std::multiplies<size_t>());
         data_ = std::move(data);
+        version_ = std::make_shared<std::atomic<uint64_t>>(0);
     }
 
     // Copies host values (in this DType's layout) into a new device tensor.
@@ -326,6 +331,7 @@ public:
         t.shape_ = shape_;
         t.size_ = size_;
         t.data_ = deviceAlloc<DType>(size_);
+        t.version_ = std::make_shared<std::atomic<uint64_t>>(0);
         if (size_ > 0)
             hipCheck(hipMemcpyAsync(t.data_.get(), data_.get(), size_ * sizeof(DType), hipMemcpyDeviceToDevice,
                                     Runtime::stream()),
@@ -336,6 +342,7 @@ public:
     // Fills every element with `value` (Tensor.cu:360).  Zero is a stream-ordered memset;
     // other values are staged on the host.
     void fill(double value) {
+        bumpVersion();
         if (size_ == 0) return;
         const DType v = fromDouble<DType>(value);
         uint8_t first;
@@ -358,7 +365,9 @@ public:
     Tensor reshape(const std::vector<size_t> &shape) const {
         const size_t n = std::accumulate(shape.begin(), shape.end(), size_t(1), std::multiplies<size_t>());
         if (n != size_) throw std::invalid_argument("reshape: element count changes");
-        return Tensor(data_, shape);
+        Tensor t(data_, shape);
+        t.version_ = version_;  // same buffer, same version count
+        return t;
     }
 
     double item() const {
@@ -374,15 +383,28 @@ public:
     size_t size() const { return size_; }
     size_t nDim() const { return shape_.size(); }
     DType *get() const { return data_.get(); }
-    DType *data() { return data_.get(); }
+    DType *data() {
+        bumpVersion();  // a mutable view of the buffer: assume it is written
+        return data_.get();
+    }
     const DType *data() const { return data_.get(); }
     std::shared_ptr<DType[]> dataPtr() const { return data_; }
     bool empty() const { return data_ == nullptr; }
+
+    // Count of in-place writes made through this tensor's API (fill, mutable data()), shared
+    // by every shallow copy and reshape of it.  A cache that keeps a tensor by reference
+    // records the count and treats a change as "contents changed" (FlashAttentionLayer's
+    // cached output).  Kernel writes through get() are not counted.
+    uint64_t version() const { return version_ ? version_->load() : 0; }
+    void bumpVersion() {
+        if (version_) version_->fetch_add(1);
+    }
 
 private:
     std::vector<size_t> shape_;
     size_t size_ = 0;
     std::shared_ptr<DType[]> data_;
+    std::shared_ptr<std::atomic<uint64_t>> version_;
 };
 
 }  // namespace ct

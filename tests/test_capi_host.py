@@ -152,3 +152,11 @@ def test_no_gpu_call_raises_cleanly(lib):
     rc = lib.ctattn_fwd(0, 1, 1, 1, 1, None, 1, 1, 8, 64, 0, None)
     assert rc != 0
     assert _capi.last_error() != ""
+
+
+def test_row_limit_boundary(lib):
+    """B*H*T up to 2^31 - 1 rows is accepted on the host (the kernels loop over rows with a
+    grid stride, so no launch exceeds 2^32 work-items); one row more is rejected."""
+    assert lib.ctattn_bwd_workspace_bytes(0, 1, 1, 2 ** 31 - 1, 8, 0) >= (2 ** 31 - 1) * 4
+    assert lib.ctattn_bwd_workspace_bytes(0, 1, 1, 2 ** 31, 8, 0) == -1
+    assert lib.ctattn_bwd_workspace_bytes(1, 1 << 16, 1 << 5, 1 << 10, 128, 1) == -1

@@ -109,23 +109,51 @@ def test_c2_c3_full_size_f32(causal):
     assert_close(got, want, "f32", f"c3 causal={causal}")
 
 
-def test_c4_long_context_bf16():
-    """Config 4: B1 H32 T8192 d128 bf16, N(0, 0.5^2) seed 4.  Heads 0 and 31 against the
-    oracle; every head through size-independent invariants."""
-    shape = (1, 32, 8192, 128)
-    q, k, v, do = ora.make_inputs(shape, seed=4, std=0.5, dtype="bf16")
+C4_SHAPE = (1, 32, 8192, 128)
+# Eight of the 32 heads, spread over the range, checked against the oracle two per test (the
+# fp64 oracle takes ~10 s per head at T = 8192); every head through the invariants.
+C4_HEAD_PAIRS = [(0, 4), (9, 13), (18, 22), (27, 31)]
+
+
+@pytest.fixture(scope="module")
+def c4_run():
+    """Config 4: B1 H32 T8192 d128 bf16, N(0, 0.5^2) seed 4, causal -- one GPU fwd+bwd shared
+    by the c4 tests."""
+    q, k, v, do = ora.make_inputs(C4_SHAPE, seed=4, std=0.5, dtype="bf16")
     say("c4 full size bf16")
     got = run_gpu(q, k, v, do, True, "bf16")
-    for h in (0, 31):
+    return q, k, v, do, got
+
+
+@pytest.mark.parametrize("heads", C4_HEAD_PAIRS, ids=lambda h: f"h{h[0]}_{h[1]}")
+def test_c4_long_context_bf16_vs_oracle(c4_run, heads):
+    q, k, v, do, got = c4_run
+    for h in heads:
+        say(f"c4 head {h} vs oracle")
         sl = lambda a: a[:, h:h + 1]  # noqa: E731
         want = ora.attention_fwd_bwd(sl(q), sl(k), sl(v), sl(do), True, chunk_heads=1)
         assert_close({kk: sl(vv) for kk, vv in got.items()}, want, "bf16", f"c4 head {h}")
-    # sum_j dK_j = 0 and sum_j dV_j = sum_i dO_i per (b, h)
-    scale_k = np.max(np.abs(got["dk"])) * 8192
-    assert np.max(np.abs(got["dk"].sum(axis=2))) <= 2e-2 * scale_k
-    dv_sum = got["dv"].sum(axis=2)
-    do_sum = do.astype(np.float64).sum(axis=2)
-    assert np.max(np.abs(dv_sum - do_sum)) <= 2e-2 * np.max(np.abs(do_sum))
+
+
+def test_c4_long_context_bf16_invariants(c4_run):
+    """Per (b, h): sum_j dK_j = 0 and sum_j dV_j = sum_i dO_i.  The exact sums are 0 and
+    sum_i dO_i; what remains is the bf16 rounding of dK / dV / O, measured on the fp64 oracle
+    at this shape (head 0) as 0.0043 (dK rounding) + 0.0046 (delta from the rounded O) times
+    sqrt(T) * rms(dK) and 0.005 sqrt(T) * rms(dV).  The bound is 0.05 sqrt(T) * rms per head;
+    a backward that drops delta from dS exceeds it 55-fold (2.8 sqrt(T) * rms)."""
+    q, k, v, do, got = c4_run
+    t = C4_SHAPE[2]
+    dk, dv = got["dk"], got["dv"]
+    rms_k = np.sqrt(np.mean(dk ** 2, axis=(2, 3)))        # [B, H]
+    rms_v = np.sqrt(np.mean(dv ** 2, axis=(2, 3)))
+    assert np.all(rms_k > 0) and np.all(rms_v > 0)
+    sum_k = np.max(np.abs(dk.sum(axis=2)), axis=-1)       # [B, H]
+    do_sum = ora.cast_inputs([do], "bf16")[0].sum(axis=2)
+    sum_v = np.max(np.abs(dv.sum(axis=2) - do_sum), axis=-1)
+    bad_k = np.argwhere(sum_k > 0.05 * np.sqrt(t) * rms_k)
+    bad_v = np.argwhere(sum_v > 0.05 * np.sqrt(t) * rms_v)
+    assert bad_k.size == 0, f"sum dK != 0 at (b, h) {bad_k.tolist()}: {sum_k.max():.3e}"
+    assert bad_v.size == 0, f"sum dV != sum dO at (b, h) {bad_v.tolist()}: {sum_v.max():.3e}"
 
 
 @pytest.mark.parametrize("d", [32, 64, 128])

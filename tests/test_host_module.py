@@ -96,6 +96,27 @@ def test_cache_is_ignored_when_shape_changes():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True])
+def test_in_place_write_to_output_does_not_corrupt_backward(causal):
+    """The cached output shares the returned O's buffer (the reference copies it,
+    FlashAttentionLayer.cu:81-84).  Writing O in place before computeBackward must not change
+    the gradients: the layer sees the tensor's version count move and recomputes the forward,
+    so dQ / dK / dV still match the oracle of the original inputs."""
+    shape = (1, 4, 130, 64)
+    q, k, v, do = ora.make_inputs(shape, seed=55)
+    layer = ctm.FlashAttention(64, 4, causal)
+    tq, tk, tv, tdo = _tensors(ctm.FloatTensor, q, k, v, do)
+    o = layer.computeAttention(tq, tk, tv, True)
+    o.fill(3.0)  # in place, after the state was cached
+    o.reshape([4, 130, 64]).fill(-1.0)  # through a view of the same buffer as well
+    dq, dk, dv = layer.computeBackward(tq, tk, tv, tdo)
+    want = ora.attention_fwd_bwd(q, k, v, do, causal)
+    for key, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        assert np.max(np.abs(t.numpy() - want[key])) <= 1e-4, key
+    assert np.all(o.numpy() == -1.0)  # the caller's write stands
+
+
+@pytest.mark.gpu
 def test_tensor_roundtrip_and_ops():
     x = np.random.default_rng(0).standard_normal((3, 4, 5)).astype(np.float32)
     t = ctm.FloatTensor.fromNumpy(x)
