@@ -57,6 +57,9 @@ def load() -> ctypes.CDLL:
     lib.ctattn_bwd.argtypes = [c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64,
                                i64, i64, i64, i64, c_int, vp]
     lib.ctattn_bwd.restype = c_int
+    lib.ctattn_bwd_noalloc.argtypes = [c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                       i64, i64, i64, i64, c_int, vp]
+    lib.ctattn_bwd_noalloc.restype = c_int
     lib.ctattn_last_error.argtypes = []
     lib.ctattn_last_error.restype = ctypes.c_char_p
     lib.ctattn_set_policy.argtypes = [c_int]
@@ -206,6 +209,31 @@ def flash_attn_bwd(q, k, v, o, do, lse, causal: bool = False, dq=None, dk=None, 
                            workspace.numel() * workspace.element_size(), b, h, t, d,
                            int(bool(causal)), _stream_handle(stream))
     _check(rc, "ctattn_bwd")
+    return dq, dk, dv
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # CTATTN_NOALLOC_SCRATCH_BYTES
+
+
+def flash_attn_bwd_noalloc(q, k, v, o, do, lse, causal: bool = False, dq=None, dk=None, dv=None,
+                           stream=None):
+    """flash_attn_bwd through ctattn_bwd_noalloc: no workspace, the library's static scratch.
+    dq / dk / dv are allocated here by torch when not given (the C entry point itself
+    allocates nothing)."""
+    _check_qkv("flash_attn_bwd_noalloc", q, k, v, o, do)
+    b, h, t, d = q.shape
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(q) if dk is None else dk
+    dv = torch.empty_like(q) if dv is None else dv
+    _check_qkv("flash_attn_bwd_noalloc", q, dq, dk, dv)
+    stat = _stat_dtype(q.dtype)
+    if lse.dtype != stat or tuple(lse.shape) != (b, h, t) or not lse.is_contiguous():
+        raise ValueError(f"flash_attn_bwd_noalloc: lse must be contiguous {stat} [B, H, T]")
+    rc = load().ctattn_bwd_noalloc(_DTYPE_CODE[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   o.data_ptr(), do.data_ptr(), lse.data_ptr(), dq.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), b, h, t, d, int(bool(causal)),
+                                   _stream_handle(stream))
+    _check(rc, "ctattn_bwd_noalloc")
     return dq, dk, dv
 
 

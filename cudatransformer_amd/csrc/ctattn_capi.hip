@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 
 namespace ctattn {
 namespace capi {
@@ -111,6 +112,49 @@ bool aligned16(std::initializer_list<const void *> ps) {
 int64_t stat_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : 4; }
 bool deterministic_policy() { return g_policy.load() == CTATTN_POLICY_DETERMINISTIC; }
 
+// ---- Scratch of ctattn_bwd_noalloc: the backward workspace (delta and friends) in a
+// file-scope device array instead of caller- or library-allocated memory.  Every GPU the
+// library runs on holds its own copy until the process ends; all calls on one GPU share it.
+// `scratch` names a host-side stand-in in host code: kernels receive the device address that
+// hipGetSymbolAddress returns for the stream's device, looked up once per device.
+static_assert(CTATTN_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+__device__ __align__(256) unsigned char scratch[CTATTN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (the current device for the
+// null stream).  Returns 0 or an error code (message set).
+int scratch_for_stream(hipStream_t stream, void **out) {
+    int dev = 0;
+    hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return fail(e, "ctattn_bwd_noalloc: cannot find the stream's device: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(hipErrorInvalidDevice, "ctattn_bwd_noalloc: device %d beyond the %d supported", dev,
+                    kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = 0;
+        e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        void *p = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            const hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess || p == nullptr)
+            return fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                        "ctattn_bwd_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -173,6 +217,32 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
         e = ctattn::launch_generic_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, workspace, s, st);
     }
     return finish("ctattn_bwd", e, st);
+}
+
+int ctattn_bwd_noalloc(int dtype, const void *q, const void *k, const void *v, const void *o,
+                       const void *dout, const void *lse, void *dq, void *dk, void *dv, int64_t B,
+                       int64_t H, int64_t T, int64_t d, int causal, void *stream) {
+    if (int rc = validate_shape("ctattn_bwd_noalloc", dtype, B, H, T, d)) return rc;
+    const int64_t need = ctattn_bwd_workspace_bytes(dtype, B, H, T, d, causal);
+    if (need > CTATTN_NOALLOC_SCRATCH_BYTES)
+        return fail(hipErrorInvalidValue,
+                    "ctattn_bwd_noalloc: this problem needs %lld bytes of scratch, more than the %lld of the "
+                    "static scratch buffer (use ctattn_bwd with a workspace)",
+                    (long long)need, (long long)CTATTN_NOALLOC_SCRATCH_BYTES);
+    if ((B * H * T) == 0) return ok();
+    if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
+        return fail(hipErrorInvalidValue, "ctattn_bwd_noalloc: null tensor pointer");
+    void *ws = nullptr;
+    if (int rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws)) return rc;
+    const int rc = ctattn_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, ws, CTATTN_NOALLOC_SCRATCH_BYTES, B, H,
+                              T, d, causal, stream);
+    if (rc != 0) {
+        // Keep ctattn_bwd's message, named for this entry point.
+        char msg[sizeof(ctattn::capi::g_err)];
+        std::snprintf(msg, sizeof(msg), "%s", ctattn::capi::g_err);
+        return fail(hipError_t(rc), "ctattn_bwd_noalloc: %s", msg);
+    }
+    return ok();
 }
 
 const char *ctattn_last_error(void) { return ctattn::capi::g_err; }

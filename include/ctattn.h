@@ -103,6 +103,29 @@ CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v
                void *workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
                int64_t d, int causal, void *stream);
 
+/* Size of the static device scratch buffer ctattn_bwd_noalloc works in (bytes, per GPU). */
+#define CTATTN_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+/*
+ * Backward that allocates nothing: ctattn_bwd with its workspace taken from a static device
+ * array of CTATTN_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on each GPU it runs
+ * on until the process ends.  No counterpart in the reference (its backward allocates through
+ * cudaMakeShared, FlashAttentionLayer.cu:103-106); it is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  It calls no hipMalloc / hipFree and no allocating library routine.
+ *   - same arguments, kernels and results as ctattn_bwd under the current policy, minus the
+ *     workspace; problems whose ctattn_bwd_workspace_bytes exceeds the scratch size are
+ *     rejected with hipErrorInvalidValue before any GPU work (AUTO needs 4 bytes per row
+ *     B*H*T for fp32, 8 for bf16 / fp16 / fp64: up to 8 Mi or 4 Mi rows).
+ *   - the scratch of the stream's device is found once per device (hipGetSymbolAddress) and
+ *     shared by every call on that GPU: calls that overlap on one GPU (two streams, two host
+ *     threads) race on it and must be serialised by the caller.  The kernels write every
+ *     scratch byte they read, so leftover contents from an earlier call do not matter.
+ */
+CTATTN_API int ctattn_bwd_noalloc(int dtype, const void *q, const void *k, const void *v, const void *o,
+                                  const void *dout, const void *lse, void *dq, void *dk, void *dv,
+                                  int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream);
+
 /* Message describing the last failure of a ctattn_* call on this thread ("" if none). */
 CTATTN_API const char *ctattn_last_error(void);
 
