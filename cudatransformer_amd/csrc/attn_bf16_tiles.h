@@ -89,6 +89,55 @@ __device__ __forceinline__ void load_tile(char *tile, const uint16_t *src, int r
     }
 }
 
+// The same load with a wave-uniform block base (src + r0 * D, in SGPRs) and a 32-bit per-lane
+// offset, so the load uses saddr + voffset addressing and keeps no 64-bit address per lane;
+// rows at or past `rows` (the rows left in the sequence, uniform) re-read row rows - 1.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void load_tile_u(char *tile, const uint16_t *block, int rows, int wave, int lane) {
+    using L = Tile<D>;
+    constexpr int TOTAL = ROWS * L::CH;
+    constexpr int NL = (TOTAL + NW * kWave - 1) / (NW * kWave);
+    static_assert(TOTAL % kWave == 0, "tile size");
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int P = (wave * NL + i) * kWave + lane;
+        if (TOTAL % (NW * kWave) == 0 || (wave * NL + i) * kWave < TOTAL) {
+            const int r = P / L::CH;
+            const int lc = (P % L::CH) ^ L::swz(r);
+            const uint32_t e = uint32_t(min(r, rows - 1) * D + 8 * lc);
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(block + e),
+                                             CTATTN_LDS(tile + (wave * NL + i) * kWave * 16), 16, 0, 0);
+        }
+    }
+}
+
+// The same load issued through inline asm.  The compiler does not see these loads, so it
+// never makes an LDS read wait (s_waitcnt vmcnt) for them -- it would for every read it cannot
+// prove disjoint from an in-flight load, which exposes a prefetch's whole latency at the next
+// read of the other buffer.  The kernel itself waits (wait_loads) before the barrier that
+// publishes the tile.  `wave` must be wave-uniform (the LDS destination goes to m0); a lane's
+// 16 bytes land at m0 + 16 lane.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void load_tile_dma(const char *tile, const uint16_t *block, int rows, int wave, int lane) {
+    using L = Tile<D>;
+    constexpr int TOTAL = ROWS * L::CH;
+    constexpr int NL = (TOTAL + NW * kWave - 1) / (NW * kWave);
+    static_assert(TOTAL % kWave == 0, "tile size");
+    const uint32_t tile_lds = uint32_t(uintptr_t((__attribute__((address_space(3))) const char *)tile));
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int P = (wave * NL + i) * kWave + lane;
+        if (TOTAL % (NW * kWave) == 0 || (wave * NL + i) * kWave < TOTAL) {
+            const int r = P / L::CH;
+            const int lc = (P % L::CH) ^ L::swz(r);
+            const uint16_t *g = block + uint32_t(min(r, rows - 1) * D + 8 * lc);
+            const uint32_t dst = tile_lds + uint32_t((wave * NL + i) * kWave * 16);
+            asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(dst)
+                         : "memory", "m0");
+        }
+    }
+}
+
 // LDS reads by byte address (LDS addresses are 32-bit).
 typedef __attribute__((address_space(3))) const u16x8 lds_u16x8;
 typedef __attribute__((address_space(3))) const floatx4 lds_floatx4;
@@ -131,6 +180,38 @@ __device__ __forceinline__ V read_col(uint32_t cb0, uint32_t cb1, int kk, int dt
     const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)((cb1 ^ uint32_t(dt << 6)) + off));
     const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(V, x);
+}
+
+// Operand reads through pointers into a __shared__ tile (`off` is the byte offset from the
+// tile's start, as row_base / col_base compute it for tile = 0).  Keeping the pointer's
+// provenance, instead of a raw LDS address, lets the compiler see which tile an access
+// touches: reads of one buffer then do not wait (s_waitcnt vmcnt) for global -> LDS loads
+// still in flight into another, provided the buffers are distinct __shared__ arrays.
+template <typename V> __device__ __forceinline__ V tile_b128(const char *tile, uint32_t off) {
+    return __builtin_bit_cast(V, *(__attribute__((address_space(3))) const u16x8 *)(tile + off));
+}
+template <int D, typename V>
+__device__ __forceinline__ V tile_col(const char *tile, uint32_t cb0, uint32_t cb1, int kk, int dt) {
+    const uint32_t off = uint32_t(16 * kk * 2 * D);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tile + ((cb0 ^ uint32_t(dt << 6)) + off)));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(tile + ((cb1 ^ uint32_t(dt << 6)) + off)));
+    const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(V, x);
+}
+
+// Workgroup barrier that leaves global -> LDS loads in flight (__syncthreads first waits for
+// every outstanding memory operation of the wave, prefetches included).  The wave's own LDS
+// reads and writes are complete when it arrives; the "memory" clobber keeps the compiler from
+// moving memory accesses across it.  Loads whose data the next phase reads must be awaited
+// (s_waitcnt vmcnt) before it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0xF70); }  // vmcnt(0)
+
+// max(x, x of lane ^ 32) in one v_permlane32_swap: the swap leaves the partner's value in one
+// of the two results and the lane's own in the other.
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Scheduling fence between a step's operand reads and the previous step's MFMAs: nothing

@@ -23,6 +23,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace ctattn {
 namespace {
 
@@ -227,6 +229,273 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// ---- Ping-pong forward: 8 waves, two groups offset by one phase ----
+//
+// The softmax of a 64-key block (max, exp2, sum, bf16 rounding: ~1000 VALU cycles per wave)
+// costs about as much as the block's MFMAs (32 x 32 cycles), and two independent waves on a
+// SIMD drift into running both phases at the same time.  Here a workgroup holds 8 waves, two
+// per SIMD (waves w and w + 4 share one): group A (waves 0-3) and group B (waves 4-7)
+// alternate between an MFMA phase M(j) -- S_j = K_j Q^T and O += V_{j-1} P_{j-1} -- and a
+// VALU phase V(j) -- the online softmax of S_j into P_j -- with a workgroup barrier after
+// every phase and group B one phase behind group A, so between two barriers one wave of each
+// SIMD runs MFMAs while the other runs VALU work (s_setprio raises the MFMA phase's issue
+// priority).  Each wave owns 32 query rows (256 per workgroup).
+//
+// K and V blocks are double-buffered (block j in buffer j & 1).  The loads of K_{j+1} and V_j
+// are issued at the start of the phase that begins with A's M(j) (A in M(j), B in V(j-1)) and
+// awaited (vmcnt) before the barrier that ends the next phase; they go through
+// load_tile_dma, and the barriers between phases (lds_barrier) do not drain them, so no
+// LDS read ever waits for a prefetch.
+template <int D>
+struct FwdPpCfg {
+    static constexpr int NW = 8;          // waves: group A = 0-3, group B = 4-7
+    static constexpr int BM = 32 * NW;    // query rows per workgroup
+    static constexpr int BN = 64;         // keys per block
+    static constexpr int KT = BN / 32;
+    static constexpr int DT = D / 32;
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int ROW = 2 * D;
+    static constexpr int KB = BN * ROW;   // bytes of one K or V tile
+    static constexpr int LDS_BYTES = 4 * KB;  // K0, K1, V0, V1
+};
+
+template <int D, typename F>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_pp_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+    uint16_t *__restrict__ o, float *__restrict__ lse, int T, int BH, int causal, float c) {
+    using C = FwdPpCfg<D>;
+    using V = typename F::vec;
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    // Wave-uniform: every branch on the wave index is a scalar branch.
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int group = wave >> 2;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    const int qblk = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
+    const int64_t base = int64_t(bh) * T * D;
+    const int q0 = qblk * C::BM;
+    const int row = q0 + wave * 32 + col;
+    const int wave_first_row = q0 + wave * 32;
+    const int wave_last_row = wave_first_row + 31;
+
+    V qb[C::KSTEPS];
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s) {
+        u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (row < T) x = *reinterpret_cast<const u16x8 *>(q + base + int64_t(row) * D + 16 * s + 8 * half);
+        qb[s] = __builtin_bit_cast(V, x);
+    }
+
+    floatx16 oacc[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) oacc[dt] = zero16();
+    float m_run = -INFINITY, l_run = 0.f;
+    floatx16 sacc[C::KT];
+    V pb[C::KT][2];
+
+    const uint32_t rk = uint32_t(Tile<D>::off(col, half));
+    const uint32_t cv0 = col_base<D>(0, 0, 0, lane), cv1 = col_base<D>(0, 0, 1, lane);
+    // Register r of a lane in `half` holds key j0 + 32 kt + acc_row(r, 0) + 4 half: masks
+    // compare that uniform part against per-lane bounds shifted by 4 half.
+    const int row_lim = causal ? row - 4 * half : 0x7fffffff;  // masked: key_u > row_lim
+    const int t_lim = T - 4 * half;                            // masked: key_u >= t_lim
+
+    const int kend = causal ? min(T, q0 + C::BM) : T;
+    const int nkb = (kend + C::BN - 1) / C::BN;
+    // Blocks this wave has keys in: the causal diagonal ends it early.
+    const int wave_nkb = causal ? min(nkb, min(wave_last_row, T - 1) / C::BN + 1) : nkb;
+
+    auto ktile = [&](int j) __attribute__((always_inline)) { return smem + (j & 1) * C::KB; };
+    auto vtile = [&](int j) __attribute__((always_inline)) { return smem + (2 + (j & 1)) * C::KB; };
+    // Key tiles of block j this wave computes: inside the sequence and, causal, not wholly
+    // above its diagonal.
+    auto tile_active = [&](int j, int kt) __attribute__((always_inline)) {
+        const int t0 = j * C::BN + kt * 32;
+        return t0 < T && (!causal || t0 <= wave_last_row);
+    };
+    // Batch j: K_{j+1} and V_j, each wave its share.
+    auto issue = [&](int j) __attribute__((always_inline)) {
+        if (j + 1 < nkb)
+            load_tile_dma<D, C::BN, C::NW>(ktile(j + 1), k + base + int64_t(j + 1) * C::BN * D, T - (j + 1) * C::BN,
+                                           wave, lane);
+        if (j < nkb) load_tile_dma<D, C::BN, C::NW>(vtile(j), v + base + int64_t(j) * C::BN * D, T - j * C::BN, wave, lane);
+    };
+
+    // M(j): O += V_{j-1} P_{j-1} (16 MFMAs at d = 128), then S_j = K_j Q^T (16), as one
+    // sequence whose operands come through a ring of kRing registers, read kRing - 1 MFMAs
+    // ahead so the LDS latency hides behind the MFMAs in between.  Key tiles above a wave's
+    // diagonal are computed anyway (their P is zero, their S is never read): the sequence has
+    // no branches.
+    constexpr int kRing = 4;
+    constexpr int NPV = C::KT * 2 * C::DT;
+    constexpr int NSC = C::KT * C::KSTEPS;
+    auto mphase_t = [&](auto has_pv, auto has_s, int j) __attribute__((always_inline)) {
+        constexpr bool PV = decltype(has_pv)::value, SC = decltype(has_s)::value;
+        constexpr int FIRST = PV ? 0 : NPV, LAST = SC ? NPV + NSC : NPV;
+        const char *vt_ = vtile(j - 1);
+        const char *kt_ = ktile(j);
+        auto operand = [&](int i) __attribute__((always_inline)) -> V {
+            if (i < NPV) {
+                const int kt = i / (2 * C::DT), ii = i % (2 * C::DT);
+                return tile_col<D, V>(vt_, cv0, cv1, 2 * kt + ii / C::DT, ii % C::DT);
+            }
+            const int kt = (i - NPV) / C::KSTEPS, st = (i - NPV) % C::KSTEPS;
+            return tile_b128<V>(kt_, (rk + uint32_t(32 * kt * C::ROW)) ^ uint32_t(st << 5));
+        };
+        V ring[kRing];
+#pragma unroll
+        for (int i = FIRST; i < FIRST + kRing - 1 && i < LAST; ++i) ring[i % kRing] = operand(i);
+#pragma unroll
+        for (int i = FIRST; i < LAST; ++i) {
+            if (i + kRing - 1 < LAST) ring[(i + kRing - 1) % kRing] = operand(i + kRing - 1);
+            read_fence();
+            if (i < NPV) {
+                const int kt = i / (2 * C::DT), ii = i % (2 * C::DT);
+                oacc[ii % C::DT] = F::mfma(ring[i % kRing], pb[kt][ii / C::DT], oacc[ii % C::DT]);
+            } else {
+                const int kt = (i - NPV) / C::KSTEPS, st = (i - NPV) % C::KSTEPS;
+                sacc[kt] = F::mfma(ring[i % kRing], qb[st], st == 0 ? zero16() : sacc[kt]);
+            }
+        }
+    };
+    // V(j): online softmax of S_j into P_j (bf16), running max / denominator, lazy rescale.
+    // MASK: the block crosses the wave's diagonal or the sequence end.
+    auto softmax = [&](auto mask, int j) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask)::value;
+        const int j0 = j * C::BN;
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (MASK && !tile_active(j, kt)) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float sv = sacc[kt][r];
+                if (MASK) {
+                    const int key_u = j0 + kt * 32 + acc_row(r, 0);
+                    sv = (key_u >= t_lim || key_u > row_lim) ? -INFINITY : sv;
+                    sacc[kt][r] = sv;
+                }
+                mloc = fmaxf(mloc, sv);
+            }
+        }
+        mloc = max_xor32(mloc) * c;  // c > 0: max(S) * c = max(S * c)
+        if (__any(mloc > m_run + kRescaleThresholdBf16)) {
+            const float m_new = fmaxf(m_run, mloc);
+            const float resc = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            l_run *= resc;
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) oacc[dt] *= resc;
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (MASK && !tile_active(j, kt)) {  // P = 0: the next M phase multiplies it anyway
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pb[kt][s2][e] = (typename F::elem)0.f;
+                continue;
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float p = fast_exp2(fmaf(sacc[kt][8 * s2 + e], c, -m_run));
+                    psum += p;
+                    pb[kt][s2][e] = (typename F::elem)p;
+                }
+            }
+        }
+        l_run += psum;
+    };
+    // Block j needs the masked softmax when it crosses the sequence end or, causal, the
+    // wave's diagonal; both conditions hold from some block on: masked(j) <=> j >= jm.
+    const int jm_t = T / C::BN;
+    const int jm = causal ? min(jm_t, max(0, (wave_first_row - 62 + C::BN - 1) / C::BN)) : jm_t;
+
+    // One iteration = both phases of block j for this wave, each closed by a barrier.  Group A
+    // issues batch j at the start of M(j) and awaits it at the end of V(j); group B issues
+    // batch j + 1 at the start of V(j) and awaits batch j at the end of M(j).  PV / SC / SM:
+    // what this wave computes (the O update of block j - 1, the scores of block j, their
+    // softmax: none, unmasked or masked); every wave runs every iteration up to nkb.
+    auto iter = [&](auto pv, auto sc, auto sm, int j) __attribute__((always_inline)) {
+        constexpr int SM = decltype(sm)::value;
+        if (group == 0) issue(j);
+        __builtin_amdgcn_s_setprio(1);
+        mphase_t(pv, sc, j);
+        __builtin_amdgcn_s_setprio(0);
+        if (group == 1) wait_loads();
+        lds_barrier();
+        if (group == 1) issue(j + 1);
+        if constexpr (SM == 1) softmax(std::false_type{}, j);
+        if constexpr (SM == 2) softmax(std::true_type{}, j);
+        if (group == 0) wait_loads();
+        lds_barrier();
+    };
+    using Y = std::true_type;
+    using N = std::false_type;
+    using NoSm = std::integral_constant<int, 0>;
+    using Plain = std::integral_constant<int, 1>;
+    using Masked = std::integral_constant<int, 2>;
+
+    // K_0 before the first phase; batch 0 (K_1, V_0) lands during the first two phases.
+    load_tile_dma<D, C::BN, C::NW>(ktile(0), k + base, T, wave, lane);
+    wait_loads();
+    lds_barrier();
+    if (group == 1) {
+        issue(0);
+        lds_barrier();  // group B runs one phase behind group A
+    }
+    if (jm > 0) iter(N{}, Y{}, Plain{}, 0);
+    else iter(N{}, Y{}, Masked{}, 0);
+    int j = 1;
+    for (; j < min(jm, wave_nkb); ++j) iter(Y{}, Y{}, Plain{}, j);
+    for (; j < wave_nkb; ++j) iter(Y{}, Y{}, Masked{}, j);
+    iter(Y{}, N{}, NoSm{}, j);  // j == wave_nkb: the last O update
+    for (++j; j <= nkb; ++j) iter(N{}, N{}, NoSm{}, j);  // keys past this wave's diagonal
+    if (group == 0) lds_barrier();  // matches group B's extra barrier
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float inv_l = 1.f / l_tot;
+    if (row < T) {
+        uint16_t *orow = o + base + int64_t(row) * D;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                u16x4 x;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) x[t] = F::bits(oacc[dt][4 * g + t] * inv_l);
+                *reinterpret_cast<u16x4 *>(orow + dt * 32 + 8 * g + 4 * half) = x;
+            }
+        }
+        if (lse != nullptr && half == 0) lse[int64_t(bh) * T + row] = (m_run + __log2f(l_tot)) * kLn2;
+    }
+}
+
+template <int D, typename F>
+hipError_t fwd_bf16_pp(const void *q, const void *k, const void *v, void *o, float *lse, const AttnShape &s,
+                       hipStream_t stream) {
+    using C = FwdPpCfg<D>;
+    const int64_t nqb = (s.T + C::BM - 1) / C::BM;
+    const int64_t blocks = nqb * s.bh();
+    if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
+    const float c = kLog2e / sqrtf(float(D));
+    hipLaunchKernelGGL((fwd_bf16_pp_kernel<D, F>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
+                       static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
+                       static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), lse, int(s.T),
+                       int(s.bh()), int(s.causal), c);
+    return hipGetLastError();
+}
+
 template <int D, typename F>
 hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse, const AttnShape &s,
                     hipStream_t stream) {
@@ -249,7 +518,7 @@ hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o,
     switch (s.d) {
         case 32: return fwd_bf16<32, Bf16Fmt>(q, k, v, o, lse, s, stream);
         case 64: return fwd_bf16<64, Bf16Fmt>(q, k, v, o, lse, s, stream);
-        case 128: return fwd_bf16<128, Bf16Fmt>(q, k, v, o, lse, s, stream);
+        case 128: return fwd_bf16_pp<128, Bf16Fmt>(q, k, v, o, lse, s, stream);
         default: return hipErrorNotSupported;
     }
 }
@@ -259,7 +528,7 @@ hipError_t launch_f16_fwd(const void *q, const void *k, const void *v, void *o, 
     switch (s.d) {
         case 32: return fwd_bf16<32, F16Fmt>(q, k, v, o, lse, s, stream);
         case 64: return fwd_bf16<64, F16Fmt>(q, k, v, o, lse, s, stream);
-        case 128: return fwd_bf16<128, F16Fmt>(q, k, v, o, lse, s, stream);
+        case 128: return fwd_bf16_pp<128, F16Fmt>(q, k, v, o, lse, s, stream);
         default: return hipErrorNotSupported;
     }
 }
