@@ -115,8 +115,8 @@ __device__ __forceinline__ void load_tile_u(char *tile, const uint16_t *block, i
 // never makes an LDS read wait (s_waitcnt vmcnt) for them -- it would for every read it cannot
 // prove disjoint from an in-flight load, which exposes a prefetch's whole latency at the next
 // read of the other buffer.  The kernel itself waits (wait_loads) before the barrier that
-// publishes the tile.  `wave` must be wave-uniform (the LDS destination goes to m0); a lane's
-// 16 bytes land at m0 + 16 lane.
+// publishes the tile.  The LDS destination of a wave's load goes to m0 (a lane's 16 bytes land
+// at m0 + 16 lane); it is wave-uniform.
 template <int D, int ROWS, int NW>
 __device__ __forceinline__ void load_tile_dma(const char *tile, const uint16_t *block, int rows, int wave, int lane) {
     using L = Tile<D>;
@@ -131,11 +131,20 @@ __device__ __forceinline__ void load_tile_dma(const char *tile, const uint16_t *
             const int r = P / L::CH;
             const int lc = (P % L::CH) ^ L::swz(r);
             const uint16_t *g = block + uint32_t(min(r, rows - 1) * D + 8 * lc);
-            const uint32_t dst = tile_lds + uint32_t((wave * NL + i) * kWave * 16);
+            // m0 takes an SGPR: the destination is wave-uniform, readfirstlane makes that explicit.
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(tile_lds + uint32_t((wave * NL + i) * kWave * 16));
             asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(dst)
                          : "memory", "m0");
         }
     }
+}
+
+// One dword per lane, global -> LDS, through inline asm like load_tile_dma: lane l's value
+// lands at LDS byte address `dst` + 4 l (`dst` wave-uniform).
+__device__ __forceinline__ void load_dword_dma(const void *g, uint32_t dst) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(dst))
+                 : "memory", "m0");
 }
 
 // LDS reads by byte address (LDS addresses are 32-bit).

@@ -167,8 +167,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int kw0 = k0 + 32 * ks;
     const int key = kw0 + col;
 
-    load_tile<D, C::BN, C::NW>(smem + C::K_OFF, k + base, k0, T, wave, lane);
-    load_tile<D, C::BN, C::NW>(smem + C::V_OFF, v + base, k0, T, wave, lane);
+    // Tile loads go through load_tile_dma / load_dword_dma, which the compiler does not see:
+    // it would otherwise make the block's first LDS read wait for the next block's prefetch.
+    // The loop waits for each block's loads itself, before the barrier that publishes them.
+    load_tile_dma<D, C::BN, C::NW>(smem + C::K_OFF, k + base + int64_t(k0) * D, T - k0, wave, lane);
+    load_tile_dma<D, C::BN, C::NW>(smem + C::V_OFF, v + base + int64_t(k0) * D, T - k0, wave, lane);
     floatx16 dk_acc[C::DT], dv_acc[C::DT];
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
@@ -187,13 +190,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int qb_first = causal ? k0 / C::BM : 0;
     auto issue = [&](int r0, int buf) {
         char *qt = smem + C::Q_OFF + buf * 2 * C::Q_BYTES;
-        load_tile<D, C::BM, C::NW>(qt, q + base, r0, T, wave, lane);
-        load_tile<D, C::BM, C::NW>(qt + C::Q_BYTES, dout + base, r0, T, wave, lane);
+        load_tile_dma<D, C::BM, C::NW>(qt, q + base + int64_t(r0) * D, T - r0, wave, lane);
+        load_tile_dma<D, C::BM, C::NW>(qt + C::Q_BYTES, dout + base + int64_t(r0) * D, T - r0, wave, lane);
         if (wave >= C::NW - 2) {  // nl2 / delta of the block's rows, one dword per lane
             const bool is_nl = wave == C::NW - 2;
-            __builtin_amdgcn_global_load_lds(
-                static_cast<const void *>((is_nl ? nl2 : delta) + rbase + min(r0 + lane, T - 1)),
-                CTATTN_LDS(smem + C::S_OFF + buf * 2 * C::BM * 4 + (is_nl ? 0 : C::BM * 4)), 4, 0, 0);
+            load_dword_dma((is_nl ? nl2 : delta) + rbase + min(r0 + lane, T - 1),
+                           lds_addr(smem + C::S_OFF + buf * 2 * C::BM * 4 + (is_nl ? 0 : C::BM * 4)));
         }
     };
 
@@ -335,7 +337,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
     const int col = lane & 31;
     const int half = lane >> 5;
 
@@ -373,9 +375,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     const int kend = causal ? min(T, r0 + C::BM) : T;
     const int nkb = (kend + C::BN - 1) / C::BN;
+    // K / V blocks through load_tile_dma (invisible to the compiler, so the block's LDS reads do
+    // not wait for the next block's prefetch); the loop awaits each block before its barrier.
     auto issue = [&](int j0, int buf) {
-        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB, k + base, j0, T, wave, lane);
-        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB + C::KB, v + base, j0, T, wave, lane);
+        load_tile_dma<D, C::BN, C::NW>(smem + 2 * buf * C::KB, k + base + int64_t(j0) * D, T - j0, wave, lane);
+        load_tile_dma<D, C::BN, C::NW>(smem + 2 * buf * C::KB + C::KB, v + base + int64_t(j0) * D, T - j0, wave, lane);
     };
 
     issue(0, 0);

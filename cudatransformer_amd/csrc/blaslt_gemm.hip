@@ -10,9 +10,14 @@
 //
 // hipBLASLt is column-major; a row-major [R][C] matrix is the column-major C x R matrix with
 // leading dimension C, so each product is written as its transpose (see proj_capi.hip).
-// Descriptors, layouts and the heuristic's algorithm are cached per problem; the workspace
-// is one 32 MiB buffer per device, allocated on first use and kept for the process.
+// Descriptors, layouts and the heuristic's algorithm are cached per problem.  Only algorithms
+// that need no workspace are accepted: there is then no scratch shared between calls, so two
+// products in flight on different streams cannot race on one, and nothing is allocated.
+// Under CTATTN_POLICY_GENERIC the products stay on the library's own GEMM kernels (the
+// cross-check path), as they do with CTATTN_NO_BLASLT=1 in the environment.
 #include "blaslt_gemm.h"
+
+#include "ctattn.h"
 
 #include <hipblaslt/hipblaslt.h>
 
@@ -24,7 +29,6 @@
 namespace ctattn {
 namespace {
 
-constexpr uint64_t kWorkspaceBytes = 32ull << 20;
 constexpr int kMaxDevices = 64;
 
 struct Plan {
@@ -39,7 +43,7 @@ using Key = std::tuple<int, int, int, int, int64_t, int64_t, int64_t, int64_t, i
 struct State {
     std::mutex mu;
     hipblasLtHandle_t handle[kMaxDevices] = {};
-    void *workspace[kMaxDevices] = {};
+    bool failed[kMaxDevices] = {};  // handle creation failed on this device: never retried
     std::map<Key, Plan> plans;
     bool disabled = std::getenv("CTATTN_NO_BLASLT") != nullptr && std::getenv("CTATTN_NO_BLASLT")[0] == '1';
 };
@@ -68,17 +72,22 @@ bool blaslt_gemm(int dtype, bool trans_a, bool trans_b, int64_t m, int64_t n, in
                  const void *B, int64_t ldb, void *C, int64_t ldc, float beta, const void *bias, hipStream_t stream) {
     if (dtype < 0 || dtype > 2 || m <= 0 || n <= 0 || k <= 0) return false;
     State &s = state();
-    if (s.disabled) return false;
+    if (s.disabled || ctattn_get_policy() == CTATTN_POLICY_GENERIC) return false;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    if ((stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 ||
+        dev >= kMaxDevices)
+        return false;
     std::lock_guard<std::mutex> lock(s.mu);
     if (s.handle[dev] == nullptr) {
-        if (hipblasLtCreate(&s.handle[dev]) != HIPBLAS_STATUS_SUCCESS) {
+        if (s.failed[dev]) return false;
+        int cur = 0;
+        if (hipGetDevice(&cur) != hipSuccess) return false;
+        if (cur != dev && hipSetDevice(dev) != hipSuccess) return false;
+        const bool created = hipblasLtCreate(&s.handle[dev]) == HIPBLAS_STATUS_SUCCESS;
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (!created) {
             s.handle[dev] = nullptr;
-            return false;
-        }
-        if (hipMalloc(&s.workspace[dev], kWorkspaceBytes) != hipSuccess) {
-            s.workspace[dev] = nullptr;
+            s.failed[dev] = true;
             return false;
         }
     }
@@ -106,7 +115,7 @@ bool blaslt_gemm(int dtype, bool trans_a, bool trans_b, int64_t m, int64_t n, in
         good = good && make_layout(&p.c, t, m, n, ldc);
         if (good) {
             hipblasLtMatmulPreference_t pref = nullptr;
-            const uint64_t ws = kWorkspaceBytes;
+            const uint64_t ws = 0;  // algorithms without workspace only
             hipblasLtMatmulHeuristicResult_t res[1];
             int found = 0;
             good = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
@@ -114,7 +123,7 @@ bool blaslt_gemm(int dtype, bool trans_a, bool trans_b, int64_t m, int64_t n, in
                                                          sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
                    hipblasLtMatmulAlgoGetHeuristic(s.handle[dev], p.desc, p.a, p.b, p.c, p.c, pref, 1, res, &found) ==
                        HIPBLAS_STATUS_SUCCESS &&
-                   found > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize <= kWorkspaceBytes;
+                   found > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && res[0].workspaceSize == 0;
             if (pref != nullptr) hipblasLtMatmulPreferenceDestroy(pref);
             if (good) p.algo = res[0].algo;
         }
@@ -128,8 +137,8 @@ bool blaslt_gemm(int dtype, bool trans_a, bool trans_b, int64_t m, int64_t n, in
             HIPBLAS_STATUS_SUCCESS)
         return false;
     const float alpha = 1.f;
-    return hipblasLtMatmul(s.handle[dev], p.desc, &alpha, A, p.a, B, p.b, &beta, C, p.c, C, p.c, &p.algo,
-                           s.workspace[dev], kWorkspaceBytes, stream) == HIPBLAS_STATUS_SUCCESS;
+    return hipblasLtMatmul(s.handle[dev], p.desc, &alpha, A, p.a, B, p.b, &beta, C, p.c, C, p.c, &p.algo, nullptr, 0,
+                           stream) == HIPBLAS_STATUS_SUCCESS;
 }
 
 }  // namespace ctattn

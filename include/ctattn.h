@@ -61,7 +61,9 @@ enum ctattn_dtype {
  *                  dQ contributions of different key blocks with fp32 atomics, so an fp32
  *                  dQ may differ between runs in the last bits; dK, dV, O and LSE do not,
  *                  and the bf16 MFMA backward uses no atomics (bitwise reproducible).
- *   GENERIC        the generic kernels only (used to cross-check the two paths).
+ *   GENERIC        the generic kernels only (used to cross-check the two paths); the linear
+ *                  layers' plain GEMMs (ctattn_linear_*, ctattn_tensor_matmul) then run on the
+ *                  library's own GEMM kernels instead of hipBLASLt.
  *   DETERMINISTIC  MFMA kernels, with the fp32 dQ summed over key blocks in a fixed order
  *                  through a workspace buffer: bitwise-reproducible gradients, larger
  *                  workspace (bf16: the same kernels as AUTO). */

@@ -62,12 +62,21 @@ def _stat_tol(dtype):
 LINEAR_SHAPES = [(1, 1, 1), (37, 130, 65), (256, 384, 384), (300, 65, 1536), (64, 4, 8)]
 
 
+@pytest.fixture(params=[_capi.POLICY_AUTO, _capi.POLICY_GENERIC], ids=["blaslt", "own_gemm"])
+def gemm_path(request):
+    """AUTO sends the linear products to hipBLASLt (fp32 / bf16 / fp16), GENERIC keeps them on
+    the library's own GEMM kernels: both paths are checked."""
+    prev = _capi.set_policy(request.param)
+    yield request.param
+    _capi.set_policy(prev)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("mnk", LINEAR_SHAPES)
 @pytest.mark.parametrize("bias", [True, False])
-def test_linear_fwd_bwd(dtype, mnk, bias):
+def test_linear_fwd_bwd(dtype, mnk, bias, gemm_path):
     m, n, k = mnk
-    print(f"linear {dtype} M={m} N={n} K={k} bias={bias}", flush=True)
+    print(f"linear {dtype} M={m} N={n} K={k} bias={bias} policy={gemm_path}", flush=True)
     x = _dev(_randn((m, k), 1), dtype)
     w = _dev(_randn((n, k), 2, 1 / math.sqrt(k)), dtype)
     b = _dev(_randn((n,), 3), dtype) if bias else None

@@ -280,3 +280,64 @@ def test_layers_through_the_module_match_torch():
     assert "attention.query.weights" in keys and "mlp.layer_2.biases" in keys and "secondNorm.weights" in keys
     tr = ctm.Transformer(40, 2, 20, 80, 3, checkpoint_gap=2)
     assert {k.split(".")[0] for k in tr.getParameters()} == {"layer_0", "layer_1", "layer_3"}
+
+
+# ---- config 5 at full size --------------------------------------------
+
+def config5_pair(seed=5):
+    from cudatransformer_amd.nanogpt import CONFIG5
+    model_cfg = {k: v for k, v in CONFIG5.items() if k not in ("batch", "seq_len", "lr")}
+    ref = NanoGPT(**model_cfg, causal=True, activation="gelu", attention="sdpa").init_weights(seed).double()
+    return CONFIG5, ref, to_native(ref)
+
+
+@pytest.mark.gpu
+def test_config5_step_matches_fp64_reference():
+    """NanoGPT.cu:83-94 (forward) and :357-378 (backward) on the native host at config 5 -- 6
+    layers, d_model 384, 6 heads of 64, T256, B16, vocab 65, GELU, causal -- against the float64
+    torch model with the same weights: loss within 1e-5 relative, every gradient within 1e-3
+    of its tensor's largest entry."""
+    cfg, ref, nat = config5_pair()
+    print("config 5 native step vs fp64", flush=True)
+    ids, tgt = make_batch(cfg["batch"], cfg["seq_len"], cfg["vocab"], seed=5)
+    ids_t = ctm.IntTensor.fromNumpy(ids.numpy().astype(np.int32))
+    tgt_t = ctm.IntTensor.fromNumpy(tgt.numpy().astype(np.int32))
+    probs = nat.forward(ids_t)
+    loss = float(nat.loss(probs, tgt_t).numpy().sum())
+    nat.zeroGrad()
+    nat.backward(ids_t, probs, tgt_t)
+    grads = nat.getGradients()
+    loss_ref = ref_step(ref, ids, tgt)
+    assert abs(loss - loss_ref) <= 1e-5 * abs(loss_ref), (loss, loss_ref)
+    for n, p in ref.named_parameters():
+        g = grads[native_key(n)].numpy().astype(np.float64)
+        r = p.grad.numpy()
+        assert g.shape == r.shape, n
+        err, scale = np.abs(g - r).max(), np.abs(r).max()
+        assert err <= 1e-3 * scale + 1e-9, f"{n}: max err {err:.3e}, max |grad| {scale:.3e}"
+
+
+@pytest.mark.gpu
+def test_config5_adam_steps_track_fp64_reference():
+    """20 Adam steps (lr 3e-4, betas 0.9 / 0.999, eps 1e-8) of config 5 on the native host
+    against torch.optim.Adam on the float64 model from the same weights: every step's loss
+    within 5e-3 relative, and the loss goes down."""
+    cfg, ref, nat = config5_pair(seed=6)
+    print("config 5 native Adam vs fp64", flush=True)
+    ids, tgt = make_batch(cfg["batch"], cfg["seq_len"], cfg["vocab"], seed=7)
+    ids_t = ctm.IntTensor.fromNumpy(ids.numpy().astype(np.int32))
+    tgt_t = ctm.IntTensor.fromNumpy(tgt.numpy().astype(np.int32))
+    opt = ctm.FloatAdamOptimizer(nat.getParameters(), lr=cfg["lr"], b1=0.9, b2=0.999, eps=1e-8)
+    opt_ref = torch.optim.Adam(ref.parameters(), lr=cfg["lr"], betas=(0.9, 0.999), eps=1e-8)
+    losses, losses_ref = [], []
+    for _ in range(20):
+        probs = nat.forward(ids_t)
+        losses.append(float(nat.loss(probs, tgt_t).numpy().sum()))
+        nat.zeroGrad()
+        nat.backward(ids_t, probs, tgt_t)
+        opt.step(nat.getGradients())
+        losses_ref.append(ref_step(ref, ids, tgt))
+        opt_ref.step()
+    print("losses", losses[0], losses[-1], "ref", losses_ref[0], losses_ref[-1], flush=True)
+    np.testing.assert_allclose(losses, losses_ref, rtol=5e-3)
+    assert losses[-1] < losses[0]
