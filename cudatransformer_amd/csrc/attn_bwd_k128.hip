@@ -18,9 +18,11 @@
 //   * dQ: each wave writes its dS tile to LDS, then every wave computes a quarter of the
 //     32 x d block of dQ = dS K over the workgroup's 128 keys with v_mfma_f32_16x16x4f32,
 //     added with fp32 atomics (Atomic) or stored as a per-128-key-block partial (Partial).
+//     Without dQ (None) the kernel produces dK and dV only, for the deterministic backward
+//     whose dQ comes from the query-major kernel of attn_bwd_dq_f32.hip.
 //   Against the 64-key kernel it issues half the dQ atomics (one set per 128 keys) but
-//   leaves more waves idle on the causal diagonal; it is the faster one without a mask, at
-//   d = 32 and for the partial (deterministic) dQ.
+//   leaves more waves idle on the causal diagonal; it is the faster one without a mask and
+//   at d = 32.
 #include "attn_launch.h"
 #include "attn_mfma_common.h"
 
@@ -29,7 +31,7 @@
 namespace ctattn {
 namespace {
 
-enum class DqMode { Atomic, Partial };
+
 
 __device__ __forceinline__ floatx4 mfma16x16x4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -57,10 +59,10 @@ struct BwdK128Cfg {
     static_assert(QF4 >= 1 && KF4 >= 1, "block load split");
 };
 
-// S, dP, P, dS and the dV^T / dK^T updates of one wave for one query block, then dS -> LDS.
-// MASK selects the diagonal / sequence-end variant (per-element causal and bounds checks);
-// the unmasked variant carries none.
-template <int D, bool MASK>
+// S, dP, P, dS and the dV^T / dK^T updates of one wave for one query block, then (WRITE_DS)
+// dS -> LDS.  MASK selects the diagonal / sequence-end variant (per-element causal and bounds
+// checks); the unmasked variant carries none.
+template <int D, bool MASK, bool WRITE_DS>
 __device__ __forceinline__ void bwd_k128_wave_block(floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32],
                                                const float (&vT)[D / 2], const float *q_lds,
                                                const float *do_lds, const float *k_lds,
@@ -108,22 +110,23 @@ __device__ __forceinline__ void bwd_k128_wave_block(floatx16 (&dk_acc)[D / 32], 
             dk_acc[dt] = mfma32x32x2(a_q, dp[st], dk_acc[dt]);
         }
     }
+    if constexpr (WRITE_DS) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
+        for (int r = 0; r < 16; ++r) ds_lds[acc_row(r, half) * C::SS + 32 * wave + col] = dp[r];
+    }
 }
 
 // Waves per SIMD the kernel is compiled for: two for d <= 64 (<= 256 VGPRs); d = 128 needs
 // more registers than that and runs one wave per SIMD.
 template <int D> struct BwdK128Occupancy { static constexpr int waves = D <= 64 ? 2 : 1; };
 
-template <int D, DqMode MODE>
+template <int D, K128Dq MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occupancy<D>::waves,
                                                                      BwdK128Occupancy<D>::waves))) void bwd_f32_k128_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dq_part,
-    float *__restrict__ dk, float *__restrict__ dv, int T, int BH, int causal, float kscale,
-    float inv_sqrt_d) {
+    float *__restrict__ dk, float *__restrict__ dv, int T, int BH, int causal, float kscale, float inv_sqrt_d) {
     using C = BwdK128Cfg<D>;
     __shared__ __attribute__((aligned(16))) float k_lds[C::BN * C::KS];
     __shared__ __attribute__((aligned(16))) float q_lds[C::BM * C::KS];
@@ -232,14 +235,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
         const bool wave_active = kw0 < T && (!causal || kw0 <= r0 + C::BM - 1);
         if (wave_active) {
             const bool masked = (r0 + C::BM > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0);
+            constexpr bool WDS = MODE != K128Dq::None;
             if (masked)
-                bwd_k128_wave_block<D, true>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
-                                        ds_lds, r0, key, T, causal, kscale, wave, col, half);
+                bwd_k128_wave_block<D, true, WDS>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
+                                                  ds_lds, r0, key, T, causal, kscale, wave, col, half);
             else
-                bwd_k128_wave_block<D, false>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
-                                         ds_lds, r0, key, T, causal, kscale, wave, col, half);
+                bwd_k128_wave_block<D, false, WDS>(dk_acc, dv_acc, vT, q_lds, do_lds, k_lds, lse_lds, dl_lds,
+                                                   ds_lds, r0, key, T, causal, kscale, wave, col, half);
         }
-        __syncthreads();  // dS of every wave visible
+        // dS of every wave visible; every wave is done reading this block's Q / dO / LSE /
+        // delta before the next iteration overwrites them.
+        __syncthreads();
+        if constexpr (MODE == K128Dq::None) continue;
 
         // dQ[r0 .. r0+31][wave * DQ_COLS ..] = sum over the workgroup's active keys of dS K.
         const int rt0 = D >= 64 ? 0 : (wave >> 1);                 // first 16-row tile
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
                 for (int ct = 0; ct < C::DQ_CT; ++ct) {
                     const int c = dq_col0 + ct * 16 + c16;
                     const float val = dq_acc[rt][ct][r] * inv_sqrt_d;
-                    if constexpr (MODE == DqMode::Atomic) {
+                    if constexpr (MODE == K128Dq::Atomic) {
                         unsafeAtomicAdd(dq + base + int64_t(row) * D + c, val);
                     } else {
                         dq_part[(int64_t(kb) * BH * T + rbase + row) * D + c] = val;
@@ -312,35 +319,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
     }
 }
 
+template <int D, K128Dq MODE>
+void launch_k128_mode(dim3 grid, const float *q, const float *k, const float *v, const float *dout, const float *lse,
+                      const float *delta, float *dq, float *dq_part, float *dk, float *dv, const AttnShape &s,
+                      float kscale, float inv_sqrt_d, hipStream_t stream) {
+    hipLaunchKernelGGL((bwd_f32_k128_kernel<D, MODE>), grid, dim3(BwdK128Cfg<D>::NW * kWave), 0, stream, q, k, v,
+                       dout, lse, delta, dq, dq_part, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
+                       inv_sqrt_d);
+}
+
 template <int D>
 hipError_t launch_k128(const float *q, const float *k, const float *v, const float *dout, const float *lse,
-                       const float *delta, float *dq, float *dq_part, float *dk, float *dv, bool partial,
+                       const float *delta, float *dq, float *dq_part, float *dk, float *dv, K128Dq mode,
                        const AttnShape &s, hipStream_t stream) {
     using C = BwdK128Cfg<D>;
     const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float kscale = kLog2e / sqrtf(float(D));
     const float inv_sqrt_d = 1.f / sqrtf(float(D));
-    if (partial)
-        hipLaunchKernelGGL((bwd_f32_k128_kernel<D, DqMode::Partial>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
-                           stream, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, int(s.T), int(s.bh()),
-                           int(s.causal), kscale, inv_sqrt_d);
-    else
-        hipLaunchKernelGGL((bwd_f32_k128_kernel<D, DqMode::Atomic>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
-                           stream, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, int(s.T), int(s.bh()),
-                           int(s.causal), kscale, inv_sqrt_d);
+    const dim3 grid{unsigned(blocks)};
+    switch (mode) {
+        case K128Dq::Atomic:
+            launch_k128_mode<D, K128Dq::Atomic>(grid, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, s, kscale,
+                                                inv_sqrt_d, stream);
+            break;
+        case K128Dq::Partial:
+            launch_k128_mode<D, K128Dq::Partial>(grid, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, s, kscale,
+                                                 inv_sqrt_d, stream);
+            break;
+        case K128Dq::None:
+            launch_k128_mode<D, K128Dq::None>(grid, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, s, kscale,
+                                              inv_sqrt_d, stream);
+            break;
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_bwd_f32_k128(const float *q, const float *k, const float *v, const float *dout,
-                               const float *lse, const float *delta, float *dq, float *dq_part, float *dk,
-                               float *dv, bool partial, const AttnShape &s, hipStream_t stream) {
+                               const float *lse, const float *delta, float *dq, float *dq_part, float *dk, float *dv,
+                               K128Dq mode, const AttnShape &s, hipStream_t stream) {
     switch (s.d) {
-        case 32: return launch_k128<32>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, partial, s, stream);
-        case 64: return launch_k128<64>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, partial, s, stream);
-        case 128: return launch_k128<128>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, partial, s, stream);
+        case 32: return launch_k128<32>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, s, stream);
+        case 64: return launch_k128<64>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, s, stream);
+        case 128: return launch_k128<128>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, s, stream);
         default: return hipErrorNotSupported;
     }
 }

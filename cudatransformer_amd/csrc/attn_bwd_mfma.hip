@@ -31,10 +31,13 @@
 //     two waves, 32 x 32 each) and adds it with fp32 atomics into dq (pre-zeroed by the
 //     preprocess kernel), one iteration later (see flush_dq).
 //
-// Which main kernel runs: this 64-key kernel for causal masks with atomic dQ and d >= 64
-// (where its balance and smaller diagonal win); the 128-key kernel of attn_bwd_k128.hip,
-// with half the dQ atomics, without a mask, at d = 32, and for the deterministic
-// per-key-block dQ partials, which the ordered reduction kernel here then sums.
+// Which kernels run: this 64-key kernel for causal masks with atomic dQ and d >= 64 (where
+// its balance and smaller diagonal win); the 128-key kernel of attn_bwd_k128.hip, with half
+// the dQ atomics, without a mask and at d = 32.  The deterministic policy takes no atomics:
+// up to 8 key blocks of 128 the 128-key kernel stores per-key-block dQ partials that the
+// reduction kernel here sums in a fixed order; beyond that it computes dK / dV only and the
+// query-major kernel of attn_bwd_dq_f32.hip computes dQ, each element summed by one lane in a
+// fixed order (two fewer planes of traffic per key block, two more matmuls).
 #include "attn_launch.h"
 #include "attn_mfma_common.h"
 
@@ -43,7 +46,10 @@
 namespace ctattn {
 namespace {
 
-enum class DqMode { Atomic, Partial };
+// dQ of the fp32 backward: fp32 atomics (AUTO); per-128-key-block partials summed in a fixed
+// order (DETERMINISTIC, up to kMaxPartialBlocks key blocks); the query-major dQ kernel
+// (DETERMINISTIC, longer sequences).
+enum class DqMode { Atomic, Partial, Separate };
 
 template <int D>
 struct BwdCfg {
@@ -374,8 +380,12 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float *__restrict_
     }
 }
 
-// Key-block size of the deterministic dQ partials: they come from the 128-key kernel.
+// Key-block size of the deterministic dQ partials: they come from the 128-key kernel.  The
+// partials cost one [B, H, T, d] fp32 plane per key block, so they are used only up to
+// kMaxPartialBlocks key blocks (workspace <= 8 planes, linear in B*H*T); longer sequences
+// take the query-major dQ kernel instead.
 constexpr int kPartialBN = 128;
+constexpr int kMaxPartialBlocks = 8;
 
 bool use_k64_kernel(const AttnShape &s, DqMode mode) {
     return s.causal && s.d >= 64 && mode == DqMode::Atomic;
@@ -384,8 +394,7 @@ bool use_k64_kernel(const AttnShape &s, DqMode mode) {
 template <int D>
 hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *o,
                    const float *dout, const float *lse, float *delta, float *dq, float *dk,
-                   float *dv, float *dq_part, DqMode mode, const AttnShape &s,
-                   hipStream_t stream) {
+                   float *dv, float *dq_part, DqMode mode, const AttnShape &s, hipStream_t stream) {
     const int64_t rows = s.rows();
     if (s.T > 2147483647 / D) return hipErrorInvalidValue;
     const unsigned pre_blocks = stride_grid((rows * (D / 4) + 255) / 256, 256);
@@ -411,8 +420,10 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
         return hipGetLastError();
       }
     }
-    e = launch_bwd_f32_k128(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode == DqMode::Partial, s, stream);
+    const K128Dq k128 = mode == DqMode::Atomic ? K128Dq::Atomic : mode == DqMode::Partial ? K128Dq::Partial : K128Dq::None;
+    e = launch_bwd_f32_k128(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, k128, s, stream);
     if (e != hipSuccess || mode == DqMode::Atomic) return e;
+    if (mode == DqMode::Separate) return launch_bwd_dq_f32(q, k, v, dout, lse, delta, dq, s, stream);
     const int64_t nkb = (s.T + kPartialBN - 1) / kPartialBN;
     const int64_t n4 = rows * (D / 4);
     hipLaunchKernelGGL(dq_reduce_kernel<D>, dim3(stride_grid((n4 + 255) / 256, 256)), dim3(256), 0, stream,
@@ -420,9 +431,9 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
     return hipGetLastError();
 }
 
-int64_t partial_bytes(const AttnShape &s) {
-    const int64_t nkb = (s.T + kPartialBN - 1) / kPartialBN;
-    return nkb * s.rows() * s.d * int64_t(sizeof(float));
+// The deterministic fp32 dQ scheme for this problem: partials while they stay small.
+DqMode deterministic_mode(const AttnShape &s) {
+    return (s.T + kPartialBN - 1) / kPartialBN <= kMaxPartialBlocks ? DqMode::Partial : DqMode::Separate;
 }
 
 }  // namespace
@@ -434,7 +445,8 @@ bool mfma_bwd_supported(int dtype, int64_t d) {
 
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic) {
     if (dtype == 1 || dtype == 2) return bf16_bwd_workspace_bytes(s, deterministic);
-    return deterministic ? partial_bytes(s) : 0;
+    if (!deterministic || deterministic_mode(s) != DqMode::Partial) return 0;  // fp32: delta only
+    return (s.T + kPartialBN - 1) / kPartialBN * s.rows() * s.d * int64_t(sizeof(float));  // <= 8 dQ planes
 }
 
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
@@ -444,19 +456,19 @@ hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *
     if (dtype == 1)
         return launch_bf16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, deterministic, s, stream);
     if (dtype == 2) return launch_f16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, s, stream);
-    const DqMode mode = deterministic ? DqMode::Partial : DqMode::Atomic;
+    const DqMode mode = deterministic ? deterministic_mode(s) : DqMode::Atomic;
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };
     switch (s.d) {
         case 32:
-            return bwd_f32<32>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
-                               g(extra), mode, s, stream);
+            return bwd_f32<32>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), mode, s,
+                               stream);
         case 64:
-            return bwd_f32<64>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
-                               g(extra), mode, s, stream);
+            return bwd_f32<64>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), mode, s,
+                               stream);
         case 128:
-            return bwd_f32<128>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv),
-                                g(extra), mode, s, stream);
+            return bwd_f32<128>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), mode, s,
+                                stream);
         default:
             return hipErrorNotSupported;
     }

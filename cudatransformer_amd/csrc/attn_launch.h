@@ -45,14 +45,11 @@ bool mfma_fwd_supported(int dtype, int64_t d);
 bool mfma_bwd_supported(int dtype, int64_t d);
 hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *v, void *o,
                            float *lse, const AttnShape &s, hipStream_t stream);
-// `deterministic` selects the ordered dQ reduction (per-key-block partials in the workspace)
-// instead of fp32 atomics.
 // bf16 forward on bf16 MFMA (d in {32, 64, 128}); called by launch_mfma_fwd for dtype 1.
 hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
                            const AttnShape &s, hipStream_t stream);
 // bf16 backward on bf16 MFMA (d in {32, 64, 128}); called by launch_mfma_bwd for dtype 1.
-// Scratch: an fp32 dQ accumulator [B, H, T, d], or per-128-key-block partials when
-// deterministic.
+// Scratch: -LSE log2(e) per row, [B, H, T] fp32.
 int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic);
 // fp16 forward / backward: the bf16 kernels instantiated for IEEE fp16 (fp16 MFMA), same
 // workspace as bf16.
@@ -75,14 +72,22 @@ hipError_t launch_f64_bwd(const void *q, const void *k, const void *v, const voi
                           const void *lse, void *delta, void *dq, void *dk, void *dv, const AttnShape &s,
                           hipStream_t stream);
 // fp32 backward main kernel with 128-key workgroups (attn_bwd_k128.hip), d in {32, 64, 128}:
-// dq is accumulated with atomics (pre-zeroed), or, with `partial`, per-128-key-block
-// partials go to dq_part.  delta must already hold rowsum(dO * O).
+// dK and dV, plus dQ accumulated into dq with atomics (Atomic: dq pre-zeroed), stored as
+// per-128-key-block partials in dq_part (Partial: plane kb holds key block kb's share), or
+// not at all (None).  delta must already hold rowsum(dO * O).
+enum class K128Dq { Atomic, Partial, None };
 hipError_t launch_bwd_f32_k128(const float *q, const float *k, const float *v, const float *dout,
-                               const float *lse, const float *delta, float *dq, float *dq_part, float *dk,
-                               float *dv, bool partial, const AttnShape &s, hipStream_t stream);
+                               const float *lse, const float *delta, float *dq, float *dq_part, float *dk, float *dv,
+                               K128Dq mode, const AttnShape &s, hipStream_t stream);
+// fp32 dQ, query-major and atomic-free (attn_bwd_dq_f32.hip), d in {32, 64, 128}: dq is
+// written, not accumulated; delta must already hold rowsum(dO * O).
+hipError_t launch_bwd_dq_f32(const float *q, const float *k, const float *v, const float *dout, const float *lse,
+                             const float *delta, float *dq, const AttnShape &s, hipStream_t stream);
 // Runs the whole MFMA backward: its own preprocess (delta = rowsum(dO * O) into `delta`,
 // fp32 [B, H, T]) and the main kernel(s).  `extra` points at mfma_bwd_workspace_bytes()
-// bytes of scratch (256-byte aligned).
+// bytes of scratch (256-byte aligned).  `deterministic` (fp32): no atomics -- dQ from
+// per-key-block partials summed in a fixed order (up to 8 blocks of 128 keys) or from the
+// query-major kernel, dK / dV from the 128-key kernel (bitwise reproducible).
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
                            const void *o, const void *dout, const float *lse, float *delta,
                            void *dq, void *dk, void *dv, void *extra, bool deterministic,

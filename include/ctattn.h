@@ -64,9 +64,13 @@ enum ctattn_dtype {
  *   GENERIC        the generic kernels only (used to cross-check the two paths); the linear
  *                  layers' plain GEMMs (ctattn_linear_*, ctattn_tensor_matmul) then run on the
  *                  library's own GEMM kernels instead of hipBLASLt.
- *   DETERMINISTIC  MFMA kernels, with the fp32 dQ summed over key blocks in a fixed order
- *                  through a workspace buffer: bitwise-reproducible gradients, larger
- *                  workspace (bf16: the same kernels as AUTO). */
+ *   DETERMINISTIC  MFMA kernels without atomics, bitwise-reproducible gradients.  The fp32
+ *                  backward stores dQ partials per 128-key block and sums them in a fixed
+ *                  order while T <= 1024 (workspace: ceil(T/128) * B*H*T*d fp32 more than
+ *                  AUTO, at most 8 dQ planes); for longer T it computes dK / dV in a
+ *                  key-major kernel and dQ in a query-major one (each element summed by one
+ *                  lane in a fixed order) with the same workspace as AUTO.  bf16 / fp16 /
+ *                  fp64: the same kernels as AUTO, which use no atomics. */
 enum ctattn_policy {
     CTATTN_POLICY_AUTO = 0,
     CTATTN_POLICY_GENERIC = 1,

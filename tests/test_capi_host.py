@@ -132,15 +132,26 @@ def test_policy_roundtrip(lib):
         _capi.set_policy(5)
 
 
-def test_deterministic_policy_needs_more_workspace(lib):
-    prev = _capi.set_policy(_capi.POLICY_DETERMINISTIC)
-    try:
-        n_det = lib.ctattn_bwd_workspace_bytes(0, 8, 12, 1024, 64, 1)
-    finally:
-        _capi.set_policy(prev)
-    n_auto = lib.ctattn_bwd_workspace_bytes(0, 8, 12, 1024, 64, 1)
-    # per-128-key-block dQ partials: 8 blocks x [B, H, T, d] fp32
-    assert n_det == n_auto + 8 * 8 * 12 * 1024 * 64 * 4
+def test_deterministic_workspace_stays_linear(lib):
+    """DETERMINISTIC fp32: dQ partials per 128-key block (one fp32 [B, H, T, d] plane each)
+    while T <= 1024, none beyond (the query-major dQ kernel), so the workspace is at most
+    AUTO's plus 8 dQ planes -- linear in B*H*T at every T.  AUTO needs delta only."""
+    for shape in [(8, 12, 1024, 64), (2, 4, 1000, 32), (1, 32, 1025, 128), (1, 32, 131072, 128),
+                  (16, 32, 32768, 64)]:
+        b, h, t, d = shape
+        rows_bytes = ((b * h * t * 4 + 255) // 256) * 256
+        nkb = (t + 127) // 128
+        partials = ((nkb * b * h * t * d * 4 + 255) // 256) * 256 if nkb <= 8 else 0
+        sizes = {}
+        for pol in (_capi.POLICY_AUTO, _capi.POLICY_DETERMINISTIC):
+            prev = _capi.set_policy(pol)
+            try:
+                sizes[pol] = lib.ctattn_bwd_workspace_bytes(0, b, h, t, d, 1)
+            finally:
+                _capi.set_policy(prev)
+        assert sizes[_capi.POLICY_AUTO] == rows_bytes, (shape, sizes)
+        assert sizes[_capi.POLICY_DETERMINISTIC] == rows_bytes + partials, (shape, sizes)
+        assert sizes[_capi.POLICY_DETERMINISTIC] <= rows_bytes + 8 * b * h * t * d * 4
 
 
 def test_no_gpu_call_raises_cleanly(lib):
