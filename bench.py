@@ -64,7 +64,11 @@ STEP_FLOP = FWD_FLOP + BWD_FLOP
 PEAK_F32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 METRIC = WORKLOADS["c3"]["metric"]
 HERE = os.path.dirname(os.path.abspath(__file__))
-COUNTERS_FILE = os.path.join(HERE, "profiles", "attn_f32_c3_counters.txt")
+# rocprofv3 counter summaries of the attention kernels at a workload's shape (bench.* lines)
+COUNTERS_FILES = {
+    "c3": os.path.join(HERE, "profiles", "attn_f32_c3_counters.txt"),
+    "c4": os.path.join(HERE, "profiles", "attn_bf16_c4_counters.txt"),
+}
 
 
 def log(msg):
@@ -287,12 +291,13 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if args.workload == "c3":
+    if args.workload in COUNTERS_FILES:
         # Counter-derived figures of the same kernels at the same shape, from the committed
-        # rocprofv3 --pmc summary: HBM bytes per backward call (FETCH_SIZE + WRITE_SIZE,
-        # copy-calibrated) -> GB/s over this run's measured backward time, and MFMA
-        # utilisation (SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' active cycles).
-        figs = read_profile_figures(COUNTERS_FILE)
+        # rocprofv3 --pmc summary: HBM bytes per call (FETCH_SIZE + WRITE_SIZE,
+        # copy-calibrated) -> GB/s over this run's measured times, and MFMA utilisation
+        # (SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' active cycles).
+        path = COUNTERS_FILES[args.workload]
+        figs = read_profile_figures(path)
         if "bwd_traffic_bytes" in figs:
             out["roofline"]["traffic"] = figs["bwd_traffic_bytes"]
             out["roofline"]["hbm_gbs"] = round(figs["bwd_traffic_bytes"] / (bwd_ms * 1e-3) / 1e9, 1)
@@ -304,7 +309,7 @@ def main():
             out["config"]["fwd_hbm_gbs"] = round(figs["fwd_traffic_bytes"] / (fwd_ms * 1e-3) / 1e9, 1)
         if "hbm_gbs" in out["roofline"]:
             out["config"]["bwd_hbm_gbs"] = out["roofline"]["hbm_gbs"]
-        out["roofline"]["counters_source"] = os.path.relpath(COUNTERS_FILE, HERE) if figs else None
+        out["roofline"]["counters_source"] = os.path.relpath(path, HERE) if figs else None
     if not args.no_cpu_baseline:
         log("timing CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
