@@ -45,6 +45,9 @@ struct FwdBf16Cfg {
 };
 
 constexpr float kRescaleThresholdBf16 = 8.0f;
+// Bound on a lane's share of one block's P in the ping-pong kernel (2^8, the same bound on
+// every P as kRescaleThresholdBf16 gives).
+constexpr float kPsumLimit = 256.0f;
 
 template <int D>
 struct FwdBf16State {
@@ -365,36 +368,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
         }
     };
-    // V(j): online softmax of S_j into P_j (bf16), running max / denominator, lazy rescale.
-    // MASK: the block crosses the wave's diagonal or the sequence end.
-    auto softmax = [&](auto mask, int j) __attribute__((always_inline)) {
+    // V(j): online softmax of S_j into P_j (bf16), running max / denominator.  MASK: the
+    // block crosses the wave's diagonal or the sequence end (masked scores become -inf).
+    // P is computed against the running max without a block max first: if every lane's share
+    // of the block's P stays <= 2^8 (so every P does), that P stands -- the same bound the
+    // lazy rescale keeps.  Otherwise (the max grew by more, or m_run is still -inf and the
+    // sums are inf / NaN) the wave takes the block max, rescales O and l and recomputes P.
+    // That is one max per score saved on every block where the max holds.
+    auto exp_block = [&](auto mask, int j, float &psum) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask)::value;
-        const int j0 = j * C::BN;
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-            if (MASK && !tile_active(j, kt)) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float sv = sacc[kt][r];
-                if (MASK) {
-                    const int key_u = j0 + kt * 32 + acc_row(r, 0);
-                    sv = (key_u >= t_lim || key_u > row_lim) ? -INFINITY : sv;
-                    sacc[kt][r] = sv;
-                }
-                mloc = fmaxf(mloc, sv);
-            }
-        }
-        mloc = max_xor32(mloc) * c;  // c > 0: max(S) * c = max(S * c)
-        if (__any(mloc > m_run + kRescaleThresholdBf16)) {
-            const float m_new = fmaxf(m_run, mloc);
-            const float resc = fast_exp2(m_run - m_new);
-            m_run = m_new;
-            l_run *= resc;
-#pragma unroll
-            for (int dt = 0; dt < C::DT; ++dt) oacc[dt] *= resc;
-        }
-        float psum = 0.f;
+        psum = 0.f;
 #pragma unroll
         for (int kt = 0; kt < C::KT; ++kt) {
             if (MASK && !tile_active(j, kt)) {  // P = 0: the next M phase multiplies it anyway
@@ -413,6 +396,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     pb[kt][s2][e] = (typename F::elem)p;
                 }
             }
+        }
+    };
+    auto softmax = [&](auto mask, int j) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask)::value;
+        if constexpr (MASK) {
+            const int j0 = j * C::BN;
+#pragma unroll
+            for (int kt = 0; kt < C::KT; ++kt) {
+                if (!tile_active(j, kt)) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key_u = j0 + kt * 32 + acc_row(r, 0);
+                    if (key_u >= t_lim || key_u > row_lim) sacc[kt][r] = -INFINITY;
+                }
+            }
+        }
+        float psum;
+        exp_block(mask, j, psum);
+        if (__any(!(psum <= kPsumLimit))) {
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < C::KT; ++kt) {
+                if (MASK && !tile_active(j, kt)) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[kt][r]);
+            }
+            mloc = max_xor32(mloc) * c;  // c > 0: max(S) * c = max(S * c)
+            // Every row has a valid key in the first block, so m_new is finite from there on.
+            const float m_new = fmaxf(m_run, mloc);
+            const float resc = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            l_run *= resc;
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) oacc[dt] *= resc;
+            exp_block(mask, j, psum);
         }
         l_run += psum;
     };
