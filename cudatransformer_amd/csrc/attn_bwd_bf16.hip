@@ -14,7 +14,8 @@
 //   * bwd_bf16_dkdv_kernel (key-major): a workgroup of 4 waves owns 128 keys (wave w: 32),
 //     keeps dK^T and dV^T in registers and walks 32-row query blocks (causal: from its
 //     diagonal on).  S = Q K^T, dP = dO V^T (lane = one key, registers = rows), then
-//     P = exp2(S c + nl2), dS = P (dP - delta) elementwise, and dV^T += dO^T P,
+//     P = exp2(S c + nl2), dS = P (dP - delta) elementwise (the dP accumulator starts from
+//     -delta), and dV^T += dO^T P,
 //     dK^T += Q^T dS with P / dS straight from the accumulator as B operands.
 //   * bwd_bf16_dq_kernel (query-major): a workgroup of 4 waves owns 128 query rows (wave w:
 //     32), keeps dQ in registers and walks 32-key blocks (causal: up to its diagonal).
@@ -79,7 +80,15 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
                                          int key, int T, int causal, float c, int half) {
     using C = KvCfg<D>;
     using V = typename F::vec;
-    floatx16 s = zero16(), dp = zero16();
+    // dP starts from -delta of the rows (register r: row acc_row(r, half)), so the
+    // accumulator ends as dP - delta and dS = P * acc.
+    floatx16 s = zero16(), dp;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const floatx4 d4 = lds_f4(anl + C::BM * 4 + 32 * g);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dp[4 * g + t] = d4[t];
+    }
     {
         V qa[2], ka[2], da[2], va[2];
         qa[0] = lds_b128<V>(aq);
@@ -106,7 +115,6 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         const floatx4 n4 = lds_f4(anl + 32 * g);
-        const floatx4 d4 = lds_f4(anl + C::BM * 4 + 32 * g);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int r = 4 * g + t;
@@ -116,7 +124,7 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
                 p = (row >= T || key >= T || (causal && key > row)) ? 0.f : p;
             }
             pb[r / 8][r % 8] = (typename F::elem)p;
-            dsb[r / 8][r % 8] = (typename F::elem)(p * (dp[r] - d4[t]));
+            dsb[r / 8][r % 8] = (typename F::elem)(p * dp[r]);
         }
     }
     // dV^T += dO^T P, dK^T += Q^T dS over the tile's 32 rows (two k-steps of 16).
@@ -277,11 +285,12 @@ struct QCfg {
 template <int D, bool MASK, typename F>
 __device__ __forceinline__ void dq_block(floatx16 (&dq_acc)[D / 32], const typename F::vec (&qB)[D / 16],
                                          const typename F::vec (&doB)[D / 16], uint32_t ak, uint32_t ac0,
-                                         uint32_t ac1, float nlr, float dlr, int j0, int row, int T, int causal,
-                                         float c, int half) {
+                                         uint32_t ac1, float nlr, const floatx16 &ndl, int j0, int row, int T,
+                                         int causal, float c, int half) {
     using C = QCfg<D>;
     using V = typename F::vec;
-    floatx16 s = zero16(), dp = zero16();
+    // dP^T starts from -delta of the lane's row, so the accumulator ends as dP^T - delta.
+    floatx16 s = zero16(), dp = ndl;
     {
         V ka[2], va[2];
         ka[0] = lds_b128<V>(ak);
@@ -308,7 +317,7 @@ __device__ __forceinline__ void dq_block(floatx16 (&dq_acc)[D / 32], const typen
             const int key = j0 + acc_row(r, half);
             p = (key >= T || row >= T || (causal && key > row)) ? 0.f : p;
         }
-        dsb[r / 8][r % 8] = (typename F::elem)(p * (dp[r] - dlr));
+        dsb[r / 8][r % 8] = (typename F::elem)(p * dp[r]);
     }
     // dQ += dS K over the block's 32 keys (two k-steps of 16).
     {
@@ -365,7 +374,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         doB[st] = __builtin_bit_cast(V, xd);
     }
     const float nlr = row < T ? nl2[rbase + row] : 0.f;
-    const float dlr = row < T ? delta[rbase + row] : 0.f;
+    const float ndr = row < T ? delta[rbase + row] : 0.f;  // -delta
+    floatx16 ndl;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ndl[r] = ndr;
     floatx16 dq_acc[C::DT];
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) dq_acc[dt] = zero16();
@@ -393,10 +405,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
         if (masked) {
             if (!causal || j0 <= wave_last_row)
-                dq_block<D, true, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
+                dq_block<D, true, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, ndl, j0, row, T, causal, c,
                                   half);
         } else {
-            dq_block<D, false, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, dlr, j0, row, T, causal, c,
+            dq_block<D, false, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, ndl, j0, row, T, causal, c,
                                half);
         }
     }
@@ -413,7 +425,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
-// delta[row] = sum_c dO[row][c] O[row][c] from bf16 (flash_attention.cu:269-273) and
+// delta[row] = -sum_c dO[row][c] O[row][c] from bf16 (the negated delta of
+// flash_attention.cu:269-273: the dP accumulators of both kernels start from it) and
 // nl2[row] = -LSE[row] * log2(e), the per-row term of P = exp2(S log2(e)/sqrt(d) + nl2).
 // D / 8 lanes per row, one 16-byte load of O and of dO each.
 template <int D, typename F>
@@ -438,7 +451,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t
         }
         s = group_sum<LPR>(s);
         if (row < rows && c8 == 0) {
-            delta[row] = s;
+            delta[row] = -s;
             nl2[row] = -lse[row] * kLog2e;
         }
     }

@@ -49,6 +49,10 @@ def run_gpu(q, k, v, do, causal, dtype):
 
 
 def assert_close(got, want, dtype, ctx):
+    # dQ and dK vanish in exact arithmetic where a row sees one key (T = 1: dS = P (dP - delta)
+    # = 0); their bf16 scale then falls back to 1e-4 of the dV scale instead of the fp64 zero.
+    floor = {"dq": 1e-4, "dk": 1e-4}
+    dv_scale = float(np.max(np.abs(want["dv"]))) if want["dv"].size else 0.0
     for key in ("o", "lse", "dq", "dk", "dv"):
         g, w = got[key], want[key]
         assert g.shape == w.shape, (ctx, key)
@@ -57,7 +61,8 @@ def assert_close(got, want, dtype, ctx):
         if dtype == "f32":
             assert err <= F32_TOL, f"{ctx} {key}: max abs err {err:.3e} > {F32_TOL}"
         else:
-            rel = err / max(float(np.max(np.abs(w))), 1e-30)
+            scale = max(float(np.max(np.abs(w))) if w.size else 0.0, floor.get(key, 0.0) * dv_scale, 1e-30)
+            rel = err / scale
             assert rel <= BF16_REL_TOL, f"{ctx} {key}: rel err {rel:.3e} > {BF16_REL_TOL}"
 
 
