@@ -394,24 +394,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         load_tile_dma<D, C::BN, C::NW>(smem + 2 * buf * C::KB + C::KB, v + base + int64_t(j0) * D, T - j0, wave, lane);
     };
 
-    issue(0, 0);
-    for (int kb = 0; kb < nkb; ++kb) {
+    // Block kb: wait for its loads (this wave's, then everyone's through the barrier, which
+    // also ends every wave's reads of the other buffer) and prefetch the next; returns the
+    // block's K tile address.
+    auto step = [&](int kb) __attribute__((always_inline)) {
         const int buf = kb & 1;
         __builtin_amdgcn_s_waitcnt(0xF70);
         __syncthreads();
         if (kb + 1 < nkb) issue((kb + 1) * C::BN, buf ^ 1);
-        const int j0 = kb * C::BN;
-        const uint32_t kt = L + uint32_t(2 * buf * C::KB);
-        const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
-        if (masked) {
-            if (!causal || j0 <= wave_last_row)
-                dq_block<D, true, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, ndl, j0, row, T, causal, c,
-                                  half);
-        } else {
-            dq_block<D, false, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, ndl, j0, row, T, causal, c,
-                               half);
-        }
+        return L + uint32_t(2 * buf * C::KB);
+    };
+    // Three loops without branches inside, so dq_acc keeps its registers across blocks (one
+    // loop over both variants made the compiler copy all 64 accumulator registers per block):
+    // [0, jm) unmasked, [jm, wave_nkb) masked (the wave's diagonal or the sequence end),
+    // [wave_nkb, nkb) keys wholly above the wave's rows (barriers and loads only).
+    const int jm = min(min(nkb, T / C::BN), causal ? (wave_first_row + 1) / C::BN : nkb);
+    const int wave_nkb = causal ? min(nkb, wave_last_row / C::BN + 1) : nkb;
+    issue(0, 0);
+    int kb = 0;
+    for (; kb < jm; ++kb) {
+        const uint32_t kt = step(kb);
+        dq_block<D, false, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, ndl, kb * C::BN, row, T, causal, c,
+                           half);
     }
+    for (; kb < wave_nkb; ++kb) {
+        const uint32_t kt = step(kb);
+        dq_block<D, true, F>(dq_acc, qB, doB, kt + rk, kt + ck0, kt + ck1, nlr, ndl, kb * C::BN, row, T, causal, c,
+                          half);
+    }
+    for (; kb < nkb; ++kb) step(kb);
 
     // dq_acc[dt]: lane (col, half), register r -> row wave_first_row + acc_row(r, half),
     // column 32 dt + col.
