@@ -82,16 +82,39 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
 
     // S^T = K Q^T for each active 32-key tile.
     floatx16 sacc[C::KT];
+    if constexpr (!MASK) {
+        // Every tile active: the K reads (one ds_read_b128 per 4 MFMAs) go through a ring and
+        // are issued two reads ahead of their MFMAs (sched_barrier keeps that order), so the
+        // LDS latency hides behind the 8 MFMAs in between.
+        constexpr int NL = C::KT * (D / 8);
+        auto kread = [&](int i) __attribute__((always_inline)) {
+            return *reinterpret_cast<const floatx4 *>(k_lds + ((i / (D / 8)) * 32 + col) * C::KS + 8 * (i % (D / 8)) +
+                                                      4 * half);
+        };
+        floatx4 ring[3];
+        ring[0] = kread(0);
+        if (NL > 1) ring[1] = kread(1);
 #pragma unroll
-    for (int kt = 0; kt < C::KT; ++kt) {
-        sacc[kt] = zero16();
-        if (!active[kt]) continue;
-        const int key = kt * 32 + col;
+        for (int i = 0; i < NL; ++i) {
+            if (i + 2 < NL) ring[(i + 2) % 3] = kread(i + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            const int kt = i / (D / 8), m = i % (D / 8);
 #pragma unroll
-        for (int m = 0; m < D / 8; ++m) {
-            const floatx4 kv = *reinterpret_cast<const floatx4 *>(k_lds + key * C::KS + 8 * m + 4 * half);
+            for (int t = 0; t < 4; ++t)
+                sacc[kt] = mfma32x32x2(ring[i % 3][t], qreg[4 * m + t], (m == 0 && t == 0) ? zero16() : sacc[kt]);
+        }
+    } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
+        for (int kt = 0; kt < C::KT; ++kt) {
+            sacc[kt] = zero16();
+            if (!active[kt]) continue;
+            const int key = kt * 32 + col;
+#pragma unroll
+            for (int m = 0; m < D / 8; ++m) {
+                const floatx4 kv = *reinterpret_cast<const floatx4 *>(k_lds + key * C::KS + 8 * m + 4 * half);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) sacc[kt] = mfma32x32x2(kv[t], qreg[4 * m + t], sacc[kt]);
+            }
         }
     }
 
@@ -135,15 +158,35 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
     st.l_run += psum;
 
     // O^T += V^T P^T: the exponentiated S^T registers are the B operand.
+    if constexpr (!MASK) {
+        // One ds_read_b32 of V per MFMA, through a ring of 8 issued 6 MFMAs ahead.
+        constexpr int NV = C::KT * C::DT * 16;
+        constexpr int R = 8, AHEAD = 6;
+        auto vread = [&](int i) __attribute__((always_inline)) {
+            const int kt = i / (C::DT * 16), dt = (i / 16) % C::DT, s2 = i % 16;
+            return v_lds[(kt * 32 + kstep_index(s2, half)) * C::KS + dt * 32 + col];
+        };
+        float ring[R];
 #pragma unroll
-    for (int kt = 0; kt < C::KT; ++kt) {
-        if (!active[kt]) continue;
+        for (int i = 0; i < AHEAD && i < NV; ++i) ring[i % R] = vread(i);
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
+        for (int i = 0; i < NV; ++i) {
+            if (i + AHEAD < NV) ring[(i + AHEAD) % R] = vread(i + AHEAD);
+            __builtin_amdgcn_sched_barrier(0);
+            const int kt = i / (C::DT * 16), dt = (i / 16) % C::DT, s2 = i % 16;
+            st.oacc[dt] = mfma32x32x2(ring[i % R], sacc[kt][s2], st.oacc[dt]);
+        }
+    } else {
 #pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::KS + dt * 32 + col];
-                st.oacc[dt] = mfma32x32x2(a, sacc[kt][s], st.oacc[dt]);
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+                for (int s = 0; s < 16; ++s) {
+                    const float a = v_lds[(kt * 32 + kstep_index(s, half)) * C::KS + dt * 32 + col];
+                    st.oacc[dt] = mfma32x32x2(a, sacc[kt][s], st.oacc[dt]);
+                }
             }
         }
     }
