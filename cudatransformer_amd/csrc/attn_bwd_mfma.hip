@@ -93,15 +93,26 @@ __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], float
     using C = BwdCfg<D>;
     floatx16 s = zero16(), dp = zero16();
     const int qrow = rb + col;  // A-operand row of this lane
+    // Q, dO and K reads (three ds_read_b128 per 8 MFMAs) double-buffered: group m + 1 is
+    // issued before the MFMAs of group m.
+    {
+        floatx4 qa[2], da[2], kb4[2];
+        auto rd = [&](int m, int b) __attribute__((always_inline)) {
+            qa[b] = *reinterpret_cast<const floatx4 *>(&q_lds[qrow * C::KS + 8 * m + 4 * half]);
+            da[b] = *reinterpret_cast<const floatx4 *>(&do_lds[qrow * C::KS + 8 * m + 4 * half]);
+            kb4[b] = *reinterpret_cast<const floatx4 *>(&k_lds[(kb_local + col) * C::KS + 8 * m + 4 * half]);
+        };
+        rd(0, 0);
 #pragma unroll
-    for (int m = 0; m < D / 8; ++m) {
-        const floatx4 qa = *reinterpret_cast<const floatx4 *>(&q_lds[qrow * C::KS + 8 * m + 4 * half]);
-        const floatx4 da = *reinterpret_cast<const floatx4 *>(&do_lds[qrow * C::KS + 8 * m + 4 * half]);
-        const floatx4 kb4 = *reinterpret_cast<const floatx4 *>(&k_lds[(kb_local + col) * C::KS + 8 * m + 4 * half]);
+        for (int m = 0; m < D / 8; ++m) {
+            if (m + 1 < D / 8) rd(m + 1, (m + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int b = m & 1;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            s = mfma32x32x2(qa[t], kb4[t], s);
-            dp = mfma32x32x2(da[t], vT[4 * m + t], dp);
+            for (int t = 0; t < 4; ++t) {
+                s = mfma32x32x2(qa[b][t], kb4[b][t], s);
+                dp = mfma32x32x2(da[b][t], vT[4 * m + t], dp);
+            }
         }
     }
 #pragma unroll
@@ -120,15 +131,26 @@ __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], float
             dp[r] = p * (dp[r] - d4[t]);
         }
     }
-    // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over the wave's 32 rows)
+    // dV^T += dO^T P,  dK^T += Q^T dS   (contraction over the wave's 32 rows).  One
+    // ds_read_b32 per MFMA, through a ring of 8 issued 6 reads ahead of their MFMAs.
+    {
+        constexpr int NR = 16 * C::DT * 2;
+        constexpr int R = 8, AHEAD = 6;
+        auto rd = [&](int i) __attribute__((always_inline)) {
+            const int st = i / (2 * C::DT), dt = (i / 2) % C::DT;
+            const int off = (rb + kstep_index(st, half)) * C::KS + dt * 32 + col;
+            return (i & 1) ? q_lds[off] : do_lds[off];
+        };
+        float ring[R];
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-        const int rl = rb + kstep_index(st, half);
+        for (int i = 0; i < AHEAD; ++i) ring[i % R] = rd(i);
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
-            const int off = rl * C::KS + dt * 32 + col;
-            dv_acc[dt] = mfma32x32x2(do_lds[off], s[st], dv_acc[dt]);
-            dk_acc[dt] = mfma32x32x2(q_lds[off], dp[st], dk_acc[dt]);
+        for (int i = 0; i < NR; ++i) {
+            if (i + AHEAD < NR) ring[(i + AHEAD) % R] = rd(i + AHEAD);
+            __builtin_amdgcn_sched_barrier(0);
+            const int st = i / (2 * C::DT), dt = (i / 2) % C::DT;
+            if (i & 1) dk_acc[dt] = mfma32x32x2(ring[i % R], dp[st], dk_acc[dt]);
+            else dv_acc[dt] = mfma32x32x2(ring[i % R], s[st], dv_acc[dt]);
         }
     }
 #pragma unroll
