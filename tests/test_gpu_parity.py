@@ -191,6 +191,27 @@ def test_deterministic_policy_is_bitwise_reproducible(dtype, causal):
         assert np.array_equal(r1[key], r2[key]), key
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_deterministic_long_sequence_f32(causal, d):
+    """DETERMINISTIC fp32 beyond 8 key blocks of 128 (T > 1024): dK / dV from the 128-key
+    kernel without its dQ part, dQ from the query-major kernel.  Against the oracle, and
+    bitwise equal over two runs."""
+    shape = (1, 2, 1100, d)
+    q, k, v, do = ora.make_inputs(shape, seed=43 + d)
+    say(f"deterministic long sequence shape={shape} causal={causal}")
+    prev = ct.set_policy(ct.POLICY_DETERMINISTIC)
+    try:
+        r1 = run_gpu(q, k, v, do, causal, "f32")
+        r2 = run_gpu(q, k, v, do, causal, "f32")
+    finally:
+        ct.set_policy(prev)
+    for key in r1:
+        assert np.array_equal(r1[key], r2[key]), key
+    want = ora.attention_fwd_bwd(q, k, v, do, causal)
+    assert_close(r1, want, "f32", f"{shape} causal={causal} deterministic")
+
+
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_auto_policy_reproducibility(causal):
     """AUTO: O, LSE, dK, dV bitwise reproducible; dQ (fp32 atomics across key blocks)
