@@ -6,7 +6,9 @@
 //
 // Work decomposition
 //   * one workgroup = 4 waves = BM = 128 query rows of one (batch, head); each wave owns
-//     32 rows and keeps them for the whole key loop.
+//     32 rows and keeps them for the whole key loop.  A causal grid (d <= 64) too short to
+//     fill the chip twice over instead runs split workgroups: 64 rows, the key range halved
+//     between two wave pairs, merged through LDS (fwd_split).
 //   * the key loop walks BN-key blocks.  K and V blocks go straight from global memory to
 //     LDS (global_load_lds_dwordx4, no staging registers), double-buffered: the next
 //     block's loads are in flight during the current block's MFMAs, one barrier per block.
@@ -29,6 +31,8 @@
 #include "attn_mfma_common.h"
 
 #include <math.h>
+
+#include <atomic>
 
 namespace ctattn {
 namespace {
@@ -192,35 +196,10 @@ __device__ __forceinline__ void fwd_block(FwdState<D> &st, const float (&qreg)[D
     }
 }
 
-template <int D, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_f32_mfma_kernel(const float *__restrict__ q,
-                                                          const float *__restrict__ k,
-                                                          const float *__restrict__ v,
-                                                          float *__restrict__ o,
-                                                          float *__restrict__ lse, int T,
-                                                          int BH, int causal, float qscale) {
-    using C = FwdCfg<D, BN>;
-    __shared__ __attribute__((aligned(16))) float k_lds[2][C::TILE];
-    __shared__ __attribute__((aligned(16))) float v_lds[2][C::TILE];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
-    const int col = lane & 31;
-    const int half = lane >> 5;
-
-    const int nqb = (T + C::BM - 1) / C::BM;
-    const int id = blockIdx.x;
-    const int bh = id % BH;
-    const int qb = causal ? (nqb - 1 - id / BH) : id / BH;
-    const int64_t base = int64_t(bh) * T * D;
-    const int q0 = qb * C::BM;
-    const int row = q0 + wave * 32 + col;  // query row owned by this lane
-    const int wave_first_row = q0 + wave * 32;
-    const int wave_last_row = wave_first_row + 31;
-
-    // Q^T as the B operand: lane (col=row, half) holds Q[row][kstep_index(s, half)].
-    float qreg[D / 2];
+// Q^T as the B operand: lane (col = row, half) holds Q[row][kstep_index(s, half)], scaled.
+template <int D>
+__device__ __forceinline__ void load_qT(float (&qreg)[D / 2], const float *q, int64_t base, int row, int T,
+                                        float qscale, int half) {
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
         floatx4 x = {0.f, 0.f, 0.f, 0.f};
@@ -228,6 +207,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int t = 0; t < 4; ++t) qreg[4 * m + t] = x[t] * qscale;
     }
+}
+
+// O row = O^T accumulators / l, LSE = (m + log2 l) ln 2 (l summed over the lane pair).
+template <int D>
+__device__ __forceinline__ void store_rows(const FwdState<D> &st, float *o, float *lse, int64_t base, int bh,
+                                           int row, int T, int half) {
+    const float l_tot = st.l_run + __shfl_xor(st.l_run, 32, kWave);
+    const float inv_l = 1.f / l_tot;
+    if (row < T) {
+        float *orow = o + base + int64_t(row) * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                floatx4 x;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) x[t] = st.oacc[dt][4 * g + t] * inv_l;
+                *reinterpret_cast<floatx4 *>(orow + dt * 32 + 8 * g + 4 * half) = x;
+            }
+        }
+        if (lse != nullptr && half == 0) lse[int64_t(bh) * T + row] = (st.m_run + __log2f(l_tot)) * kLn2;
+    }
+}
+
+// A whole 128-row query block: wave w owns rows q0 + 32 w .., the key loop walks BN-key blocks
+// up to the block's last row (causal) or T.
+template <int D, int BN>
+__device__ __forceinline__ void fwd_whole(float *k_lds, float *v_lds,
+                                          const float *__restrict__ q, const float *__restrict__ k,
+                                          const float *__restrict__ v, float *__restrict__ o,
+                                          float *__restrict__ lse, int T, int bh, int qb, int causal, float qscale,
+                                          int wave, int lane) {
+    using C = FwdCfg<D, BN>;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int64_t base = int64_t(bh) * T * D;
+    const int q0 = qb * C::BM;
+    const int row = q0 + wave * 32 + col;  // query row owned by this lane
+    const int wave_first_row = q0 + wave * 32;
+    const int wave_last_row = wave_first_row + 31;
+
+    float qreg[D / 2];
+    load_qT<D>(qreg, q, base, row, T, qscale, half);
 
     FwdState<D> st;
 #pragma unroll
@@ -250,9 +272,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const int c = P - r * C::C4P;
                 const int64_t goff = base + int64_t(min(j0 + r, T - 1)) * D + 4 * (c < C::C4 ? c : 0);
                 __builtin_amdgcn_global_load_lds(static_cast<const void *>(k + goff),
-                                                 CTATTN_LDS(&k_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+                                                 CTATTN_LDS(k_lds + buf * C::TILE + (wave * C::INSTR + i) * 4 * kWave), 16, 0, 0);
                 __builtin_amdgcn_global_load_lds(static_cast<const void *>(v + goff),
-                                                 CTATTN_LDS(&v_lds[buf][(wave * C::INSTR + i) * 4 * kWave]), 16, 0, 0);
+                                                 CTATTN_LDS(v_lds + buf * C::TILE + (wave * C::INSTR + i) * 4 * kWave), 16, 0, 0);
             }
         }
     };
@@ -271,30 +293,173 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const bool masked = (j0 + BN > T) || (causal && j0 + BN - 1 > wave_first_row);
         if (masked) {
             if (!causal || j0 <= wave_last_row)
-                fwd_block<D, BN, true>(st, qreg, k_lds[buf], v_lds[buf], j0, row, wave_first_row,
+                fwd_block<D, BN, true>(st, qreg, k_lds + buf * C::TILE, v_lds + buf * C::TILE, j0, row, wave_first_row,
                                        wave_last_row, T, causal, col, half);
         } else {
-            fwd_block<D, BN, false>(st, qreg, k_lds[buf], v_lds[buf], j0, row, wave_first_row,
+            fwd_block<D, BN, false>(st, qreg, k_lds + buf * C::TILE, v_lds + buf * C::TILE, j0, row, wave_first_row,
                                     wave_last_row, T, causal, col, half);
         }
     }
+    store_rows<D>(st, o, lse, base, bh, row, T, half);
+}
 
-    const float l_tot = st.l_run + __shfl_xor(st.l_run, 32, kWave);
-    const float inv_l = 1.f / l_tot;
-    if (row < T) {
-        float *orow = o + base + int64_t(row) * D;
+// A split workgroup (causal only): 64 query rows R0 .. R0 + 63, its key range [0, R0 + 64)
+// cut in two halves of 32-key blocks.  Waves 2 h and 2 h + 1 (rows R0 .. R0 + 31 and
+// R0 + 32 .. R0 + 63) walk half h with their own double-buffered tiles (the first / second
+// 32 rows of each BN = 64 tile buffer), then half 1 hands its O^T, m and l to half 0 through
+// LDS and half 0 merges and stores.  Each 128-row query block of a short causal grid becomes
+// two such workgroups, each with about a quarter of its key work, so the longest block no
+// longer sets the kernel's length.
+template <int D>
+__device__ __forceinline__ void fwd_split(float *k_lds, float *v_lds,
+                                          const float *__restrict__ q, const float *__restrict__ k,
+                                          const float *__restrict__ v, float *__restrict__ o,
+                                          float *__restrict__ lse, int T, int bh, int R0, float qscale, int wave,
+                                          int lane) {
+    using C = FwdCfg<D, 32>;
+    constexpr int GW = 2;                                      // waves per half
+    constexpr int INSTR = (C::CHUNKS + GW * kWave - 1) / (GW * kWave);  // loads per lane per tile
+    const int rs = wave & 1, h = wave >> 1;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int64_t base = int64_t(bh) * T * D;
+    const int wave_first_row = R0 + 32 * rs;
+    const int wave_last_row = wave_first_row + 31;
+    const int row = wave_first_row + col;
+
+    float qreg[D / 2];
+    load_qT<D>(qreg, q, base, row, T, qscale, half);
+
+    FwdState<D> st;
 #pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
+    for (int dt = 0; dt < C::DT; ++dt) st.oacc[dt] = zero16();
+    st.m_run = -INFINITY;
+    st.l_run = 0.f;
+
+    const int nk = (min(T, R0 + 64) + 31) / 32;  // 32-key blocks of the workgroup
+    const int n0 = (nk + 1) / 2;                  // half 0: [0, n0), half 1: [n0, nk)
+    const int kb0 = h ? n0 : 0, kb1 = h ? nk : n0;
+    float *kt0 = k_lds + h * C::TILE, *kt1 = k_lds + 2 * C::TILE + h * C::TILE;
+    float *vt0 = v_lds + h * C::TILE, *vt1 = v_lds + 2 * C::TILE + h * C::TILE;
+
+    auto issue = [&](int kb, int buf) {
+        float *kt = buf ? kt1 : kt0;
+        float *vt = buf ? vt1 : vt0;
+        const int j0 = kb * 32;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                floatx4 x;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) x[t] = st.oacc[dt][4 * g + t] * inv_l;
-                *reinterpret_cast<floatx4 *>(orow + dt * 32 + 8 * g + 4 * half) = x;
+        for (int i = 0; i < INSTR; ++i) {
+            const int P = (rs * INSTR + i) * kWave + lane;
+            if (C::CHUNKS % (GW * kWave) == 0 || P < C::CHUNKS) {
+                const int r = P / C::C4P;
+                const int c = P - r * C::C4P;
+                const int64_t goff = base + int64_t(min(j0 + r, T - 1)) * D + 4 * (c < C::C4 ? c : 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(k + goff),
+                                                 CTATTN_LDS(kt + (rs * INSTR + i) * 4 * kWave), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(v + goff),
+                                                 CTATTN_LDS(vt + (rs * INSTR + i) * 4 * kWave), 16, 0, 0);
             }
         }
-        if (lse != nullptr && half == 0) lse[int64_t(bh) * T + row] = (st.m_run + __log2f(l_tot)) * kLn2;
+    };
+
+    if (kb0 < kb1) issue(kb0, 0);
+    for (int it = 0; it < n0; ++it) {  // half 1 has n0 or n0 - 1 blocks: every wave meets n0 barriers
+        const int kb = kb0 + it;
+        const int buf = it & 1;
+        __builtin_amdgcn_s_waitcnt(0xF70);
+        __syncthreads();
+        if (kb + 1 < kb1) issue(kb + 1, buf ^ 1);
+        if (kb < kb1) {
+            const int j0 = kb * 32;
+            const float *kt = buf ? kt1 : kt0;
+            const float *vt = buf ? vt1 : vt0;
+            const bool masked = (j0 + 32 > T) || (j0 + 31 > wave_first_row);
+            if (masked) {
+                if (j0 <= wave_last_row)
+                    fwd_block<D, 32, true>(st, qreg, kt, vt, j0, row, wave_first_row, wave_last_row, T, 1, col,
+                                           half);
+            } else {
+                fwd_block<D, 32, false>(st, qreg, kt, vt, j0, row, wave_first_row, wave_last_row, T, 1, col, half);
+            }
+        }
     }
+
+    // Merge: half 1's lane (row, half) state lands at mb[(rs * NR + i) * 64 + lane]; both
+    // halves' O^T / l are relative to their own running max m (log2 units), so
+    //   m = max(m0, m1), O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise.
+    // Half 0 always holds key 0 of its rows, so m0 is finite; an empty half 1 has m1 = -inf,
+    // weight 0.
+    constexpr int NR = C::DT * 16 + 2;
+    float *mb = k_lds;
+    __syncthreads();  // every wave is done with the tiles
+    if (h == 1) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mb[(rs * NR + dt * 16 + r) * kWave + lane] = st.oacc[dt][r];
+        mb[(rs * NR + NR - 2) * kWave + lane] = st.m_run;
+        mb[(rs * NR + NR - 1) * kWave + lane] = st.l_run;
+    }
+    __syncthreads();
+    if (h == 0) {
+        const float m1 = mb[(rs * NR + NR - 2) * kWave + lane];
+        const float l1 = mb[(rs * NR + NR - 1) * kWave + lane];
+        const float m = fmaxf(st.m_run, m1);
+        const float a0 = fast_exp2(st.m_run - m), a1 = fast_exp2(m1 - m);
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st.oacc[dt][r] = st.oacc[dt][r] * a0 + mb[(rs * NR + dt * 16 + r) * kWave + lane] * a1;
+        st.l_run = st.l_run * a0 + l1 * a1;
+        st.m_run = m;
+        store_rows<D>(st, o, lse, base, bh, row, T, half);
+    }
+}
+
+template <int D, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_f32_mfma_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, float *__restrict__ o,
+    float *__restrict__ lse, int T, int BH, int causal, float qscale, int split) {
+    using C = FwdCfg<D, BN>;
+    __shared__ __attribute__((aligned(16))) float k_lds[2][C::TILE];
+    __shared__ __attribute__((aligned(16))) float v_lds[2][C::TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    if constexpr (BN == 64) {
+        if (split) {  // causal, 64-row split workgroups, longest first
+            const int rb = (T + 63) / 64 - 1 - id / BH;
+            fwd_split<D>(&k_lds[0][0], &v_lds[0][0], q, k, v, o, lse, T, bh, 64 * rb, qscale, wave, lane);
+            return;
+        }
+    }
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int qb = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
+    fwd_whole<D, BN>(&k_lds[0][0], &v_lds[0][0], q, k, v, o, lse, T, bh, qb, causal, qscale, wave, lane);
+}
+
+// Split workgroups pay for themselves when the causal grid of whole 128-row blocks has no more
+// workgroups than the chip has slots (two per CU): then the longest blocks are the whole
+// kernel, and cutting every block into two 64-row workgroups with halved key ranges shortens
+// them four times over.  Measured (B x H x T, d = 64): 1x4x2048 83.6 -> 50.7 us, 2x16x1024
+// 76.7 -> 61.7, 8x12x512 55.6 -> 47.9; at 768 and more whole blocks splitting is within
+// +-3 % (8x12x1024 133.4 / 132.1, 1x12x8192 859.5 / 877.4, 32x12x1024 479.4 / 494.2), so
+// those keep whole blocks.
+bool fwd_use_split(const AttnShape &s, hipStream_t stream) {
+    static std::atomic<int> cus_of[64];
+    int dev = 0;
+    if ((stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 || dev >= 64)
+        return false;
+    int cus = cus_of[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return false;
+        cus_of[dev].store(cus, std::memory_order_relaxed);
+    }
+    return (s.T + 127) / 128 * s.bh() <= int64_t(2) * cus;
 }
 
 template <int D, int BN>
@@ -305,8 +470,11 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
     const int64_t blocks = nqb * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float qscale = kLog2e / sqrtf(float(D));
-    hipLaunchKernelGGL((fwd_f32_mfma_kernel<D, BN>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0,
-                       stream, q, k, v, o, lse, int(s.T), int(s.bh()), int(s.causal), qscale);
+    const int split = BN == 64 && s.causal && fwd_use_split(s, stream);
+    const int64_t grid = split ? (s.T + 63) / 64 * s.bh() : blocks;
+    if (!grid_fits(grid, C::NW * kWave)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((fwd_f32_mfma_kernel<D, BN>), dim3(unsigned(grid)), dim3(C::NW * kWave), 0, stream, q, k, v,
+                       o, lse, int(s.T), int(s.bh()), int(s.causal), qscale, split);
     return hipGetLastError();
 }
 

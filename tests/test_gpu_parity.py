@@ -161,6 +161,25 @@ def test_c4_long_context_bf16_invariants(c4_run):
     assert bad_v.size == 0, f"sum dV != sum dO at (b, h) {bad_v.tolist()}: {sum_v.max():.3e}"
 
 
+@pytest.mark.parametrize("shape", [(1, 2, 1100, 64), (1, 2, 1100, 32), (4, 64, 300, 64), (4, 64, 300, 32)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_causal_forward_decompositions_f32(shape):
+    """The fp32 causal forward (d <= 64) cuts every query block into two 64-row workgroups with
+    halved key ranges when the grid of whole 128-row blocks, ceil(T / 128) * B * H, is no
+    larger than two workgroups per CU, and keeps whole blocks otherwise.  The B1 H2 T1100
+    shapes take the split workgroups, the B4 H64 T300 ones the whole blocks; both have a
+    ragged last block."""
+    b, h, t, d = shape
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    split = -(-t // 128) * b * h <= 2 * cus
+    assert split == (h == 2), f"{shape} is expected on the other side of the split rule ({cus} CUs)"
+    q, k, v, do = ora.make_inputs(shape, seed=57)
+    say(f"causal forward decomposition shape={shape} split={split}")
+    got = run_gpu(q, k, v, do, True, "f32")
+    want = ora.attention_fwd_bwd(q, k, v, do, True, chunk_heads=16)
+    assert_close(got, want, "f32", f"{shape} split={split}")
+
+
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_mfma_matches_generic(causal, d):
