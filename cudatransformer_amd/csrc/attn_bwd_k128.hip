@@ -120,7 +120,7 @@ __device__ __forceinline__ void bwd_k128_wave_block(floatx16 (&dk_acc)[D / 32], 
 // more registers than that and runs one wave per SIMD.
 template <int D> struct BwdK128Occupancy { static constexpr int waves = D <= 64 ? 2 : 1; };
 
-template <int D, K128Dq MODE>
+template <int D, K128Dq MODE, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occupancy<D>::waves,
                                                                      BwdK128Occupancy<D>::waves))) void bwd_f32_k128_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -128,6 +128,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
     const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dq_part,
     float *__restrict__ dk, float *__restrict__ dv, int T, int BH, int causal, float kscale, float inv_sqrt_d) {
     using C = BwdK128Cfg<D>;
+    constexpr int split = SPLIT ? 1 : 0;
     __shared__ __attribute__((aligned(16))) float k_lds[C::BN * C::KS];
     __shared__ __attribute__((aligned(16))) float q_lds[C::BM * C::KS];
     __shared__ __attribute__((aligned(16))) float do_lds[C::BM * C::KS];
@@ -143,9 +144,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
     const int c16 = lane & 15;
     const int quad = lane >> 4;
 
+    // split: key block kb's query blocks are shared by workgroups (kb, part 0) and (kb, part 1).
     const int id = blockIdx.x;
     const int bh = id % BH;
-    const int kb = id / BH;  // causal: key block 0 has the most query blocks -> launched first
+    const int kb = (id / BH) >> split;  // causal: key block 0 has the most query blocks -> launched first
+    const int part = (id / BH) & split;
     const int k0 = kb * C::BN;
     const int64_t base = int64_t(bh) * T * D;
     const int64_t rbase = int64_t(bh) * T;
@@ -181,8 +184,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
         dv_acc[dt] = zero16();
     }
 
-    const int nqb = (T + C::BM - 1) / C::BM;
-    const int qb_begin = causal ? k0 / C::BM : 0;
+    const int nqb_all = (T + C::BM - 1) / C::BM;
+    const int qb_first = causal ? k0 / C::BM : 0;
+    const int qb_mid = qb_first + (nqb_all - qb_first + 1) / 2;
+    const int qb_begin = split && part ? qb_mid : qb_first;
+    const int nqb = split && !part ? qb_mid : nqb_all;  // end of this workgroup's query blocks
 
     floatx4 qpre[C::QF4], dopre[C::QF4];
     float lpre = 0.f, dpre = 0.f;
@@ -299,6 +305,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
     }
 
     // dK = (Q^T dS)^T / sqrt(d), dV = (dO^T P)^T; lane (key, half) holds d = dt*32 + acc_row(r, half).
+    if constexpr (SPLIT) {
+        // Two workgroups add to each element (two addends: the same sum in either order).  The
+        // lane-per-key layout would scatter every atomic instruction over 64 rows, so each
+        // tensor goes through LDS (k_lds, [key][KS], free after the loop) and is added with
+        // lanes along d.
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            __syncthreads();  // every wave is done with k_lds (the loop, or the previous tensor)
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    floatx4 x;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        x[t] = which == 0 ? dk_acc[dt][4 * g + t] * inv_sqrt_d : dv_acc[dt][4 * g + t];
+                    *reinterpret_cast<floatx4 *>(&k_lds[(32 * wave + col) * C::KS + dt * 32 + 8 * g + 4 * half]) = x;
+                }
+            __syncthreads();
+            float *dst = (which == 0 ? dk : dv) + base + int64_t(k0) * D;
+            for (int e = tid; e < C::BN * D; e += C::NW * kWave) {
+                const int kr = e / D, c = e - (e / D) * D;
+                if (k0 + kr < T) unsafeAtomicAdd(dst + int64_t(kr) * D + c, k_lds[kr * C::KS + c]);
+            }
+        }
+        return;
+    }
     if (key < T) {
         float *dkr = dk + base + int64_t(key) * D;
         float *dvr = dv + base + int64_t(key) * D;
@@ -322,18 +355,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdK128Occu
 template <int D, K128Dq MODE>
 void launch_k128_mode(dim3 grid, const float *q, const float *k, const float *v, const float *dout, const float *lse,
                       const float *delta, float *dq, float *dq_part, float *dk, float *dv, const AttnShape &s,
-                      float kscale, float inv_sqrt_d, hipStream_t stream) {
-    hipLaunchKernelGGL((bwd_f32_k128_kernel<D, MODE>), grid, dim3(BwdK128Cfg<D>::NW * kWave), 0, stream, q, k, v,
-                       dout, lse, delta, dq, dq_part, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
-                       inv_sqrt_d);
+                      float kscale, float inv_sqrt_d, int split, hipStream_t stream) {
+    if (split)
+        hipLaunchKernelGGL((bwd_f32_k128_kernel<D, MODE, true>), grid, dim3(BwdK128Cfg<D>::NW * kWave), 0, stream, q,
+                           k, v, dout, lse, delta, dq, dq_part, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
+                           inv_sqrt_d);
+    else
+        hipLaunchKernelGGL((bwd_f32_k128_kernel<D, MODE, false>), grid, dim3(BwdK128Cfg<D>::NW * kWave), 0, stream, q,
+                           k, v, dout, lse, delta, dq, dq_part, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
+                           inv_sqrt_d);
 }
 
 template <int D>
 hipError_t launch_k128(const float *q, const float *k, const float *v, const float *dout, const float *lse,
                        const float *delta, float *dq, float *dq_part, float *dk, float *dv, K128Dq mode,
-                       const AttnShape &s, hipStream_t stream) {
+                       bool split, const AttnShape &s, hipStream_t stream) {
     using C = BwdK128Cfg<D>;
-    const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh();
+    const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh() * (split ? 2 : 1);
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float kscale = kLog2e / sqrtf(float(D));
     const float inv_sqrt_d = 1.f / sqrtf(float(D));
@@ -341,15 +379,15 @@ hipError_t launch_k128(const float *q, const float *k, const float *v, const flo
     switch (mode) {
         case K128Dq::Atomic:
             launch_k128_mode<D, K128Dq::Atomic>(grid, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, s, kscale,
-                                                inv_sqrt_d, stream);
+                                                inv_sqrt_d, int(split), stream);
             break;
         case K128Dq::Partial:
             launch_k128_mode<D, K128Dq::Partial>(grid, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, s, kscale,
-                                                 inv_sqrt_d, stream);
+                                                 inv_sqrt_d, int(split), stream);
             break;
         case K128Dq::None:
             launch_k128_mode<D, K128Dq::None>(grid, q, k, v, dout, lse, delta, dq, dq_part, dk, dv, s, kscale,
-                                              inv_sqrt_d, stream);
+                                              inv_sqrt_d, int(split), stream);
             break;
     }
     return hipGetLastError();
@@ -359,11 +397,11 @@ hipError_t launch_k128(const float *q, const float *k, const float *v, const flo
 
 hipError_t launch_bwd_f32_k128(const float *q, const float *k, const float *v, const float *dout,
                                const float *lse, const float *delta, float *dq, float *dq_part, float *dk, float *dv,
-                               K128Dq mode, const AttnShape &s, hipStream_t stream) {
+                               K128Dq mode, bool split, const AttnShape &s, hipStream_t stream) {
     switch (s.d) {
-        case 32: return launch_k128<32>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, s, stream);
-        case 64: return launch_k128<64>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, s, stream);
-        case 128: return launch_k128<128>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, s, stream);
+        case 32: return launch_k128<32>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, split, s, stream);
+        case 64: return launch_k128<64>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, split, s, stream);
+        case 128: return launch_k128<128>(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, mode, split, s, stream);
         default: return hipErrorNotSupported;
     }
 }

@@ -157,7 +157,7 @@ __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], float
     for (int r = 0; r < 16; ++r) ds_lds[(rb + acc_row(r, half)) * C::SS + kb_local + col] = dp[r];
 }
 
-template <int D>
+template <int D, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occupancy<D>::waves,
                                                                      BwdF32Occupancy<D>::waves))) void bwd_f32_mfma_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -165,6 +165,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
     const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dk,
     float *__restrict__ dv, int T, int BH, int causal, float kscale, float inv_sqrt_d) {
     using C = BwdCfg<D>;
+    constexpr int split = SPLIT ? 1 : 0;
     __shared__ __attribute__((aligned(16))) float qdo_lds[2 * C::TILE];  // Q then dO, [BM][KS] each
     float *q_lds = qdo_lds;
     float *do_lds = qdo_lds + C::TILE;
@@ -180,9 +181,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
     const int half = lane >> 5;
     const int ks = wave & 1, rs = wave >> 1;
 
+    // split: key block kb's query blocks are shared by workgroups (kb, part 0) and (kb, part 1).
     const int id = blockIdx.x;
     const int bh = id % BH;
-    const int kb = id / BH;  // causal: key block 0 has the most query blocks -> launched first
+    const int kb = (id / BH) >> split;  // causal: key block 0 has the most query blocks -> launched first
+    const int part = (id / BH) & split;
     const int k0 = kb * C::BN;
     const int64_t base = int64_t(bh) * T * D;
     const int64_t rbase = int64_t(bh) * T;
@@ -218,7 +221,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
     }
 
     const int nqb = (T + C::BM - 1) / C::BM;
-    const int qb_begin = causal ? k0 / C::BM : 0;
+    const int qb_first = causal ? k0 / C::BM : 0;
+    const int qb_mid = qb_first + (nqb - qb_first + 1) / 2;
+    const int qb_begin = split && part ? qb_mid : qb_first;
+    const int qb_end = split && !part ? qb_mid : nqb;
 
     // Global -> LDS for one query block: lane writes LDS chunk P = (wave * INSTR + i) * 64 +
     // lane of the padded block, i.e. row P / C4P, chunk P % C4P; the pad chunk (C4) re-reads
@@ -269,8 +275,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
         }
     };
 
-    issue(qb_begin * C::BM);
-    for (int qb = qb_begin; qb < nqb; ++qb) {
+    if (qb_begin < qb_end) issue(qb_begin * C::BM);
+    for (int qb = qb_begin; qb < qb_end; ++qb) {
         const int r0 = qb * C::BM;
         // The block's loads have landed (vmcnt = 0) and, after the barrier, every wave's are
         // visible; every wave is also done reading the previous block's dS.
@@ -290,7 +296,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
                                          32 * rs, r0w, 32 * ks, key, T, causal, kscale, col, half);
         }
         __syncthreads();  // dS of every wave visible; Q / dO / LSE / delta no longer read
-        if (qb + 1 < nqb) issue(r0 + C::BM);
+        if (qb + 1 < qb_end) issue(r0 + C::BM);
 
         // dQ[r0 + 32 qrs .. +31][dq_col0 ..] = sum over the block's active keys of dS K.
         if (dq_wave) {
@@ -334,6 +340,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
             }
     }
     __syncthreads();
+    // Lane (key, half), register r of tile dt: the final dK (g = 0) or dV (g = 1) value of
+    // d = dt * 32 + 8 * (r / 4) + 4 * half + r % 4, row-slice sums included.
+    auto final_val = [&](int which, int dt, int r) __attribute__((always_inline)) {
+        const float other = red[(((ks * C::DT + dt) * 2 + which) * 16 + r) * kWave + lane];
+        return which == 0 ? (dk_acc[dt][r] + other) * inv_sqrt_d : dv_acc[dt][r] + other;
+    };
+    if constexpr (SPLIT) {
+        // Two workgroups add to each element (two addends: the same sum in either order).  The
+        // lane-per-key layout would scatter every atomic instruction over 64 rows, so each
+        // tensor goes through LDS (k_lds, [key][KS]) and is added with lanes along d.
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            if (rs == 0) {
+#pragma unroll
+                for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        floatx4 x;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) x[t] = final_val(which, dt, 4 * g + t);
+                        *reinterpret_cast<floatx4 *>(&k_lds[(32 * ks + col) * C::KS + dt * 32 + 8 * g + 4 * half]) = x;
+                    }
+            }
+            __syncthreads();
+            float *dst = (which == 0 ? dk : dv) + base + int64_t(k0) * D;
+            for (int e = tid; e < C::BN * D; e += C::NW * kWave) {
+                const int kr = e / D, c = e - (e / D) * D;
+                if (k0 + kr < T) unsafeAtomicAdd(dst + int64_t(kr) * D + c, k_lds[kr * C::KS + c]);
+            }
+            __syncthreads();
+        }
+        return;
+    }
     if (rs == 0 && key < T) {
         float *dkr = dk + base + int64_t(key) * D;
         float *dvr = dv + base + int64_t(key) * D;
@@ -344,9 +383,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
                 floatx4 xk, xv;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const int r = 4 * g + t;
-                    xk[t] = (dk_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 0) * 16 + r) * kWave + lane]) * inv_sqrt_d;
-                    xv[t] = dv_acc[dt][r] + red[(((ks * C::DT + dt) * 2 + 1) * 16 + r) * kWave + lane];
+                    xk[t] = final_val(0, dt, 4 * g + t);
+                    xv[t] = final_val(1, dt, 4 * g + t);
                 }
                 *reinterpret_cast<floatx4 *>(dkr + dt * 32 + 8 * g + 4 * half) = xk;
                 *reinterpret_cast<floatx4 *>(dvr + dt * 32 + 8 * g + 4 * half) = xv;
@@ -356,13 +394,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
 }
 
 // delta[row] = sum_c dO[row][c] * O[row][c] (flash_attention.cu:269-273); also zeroes the
-// dq row when dQ is accumulated with atomics.  D / 4 lanes per row, one 16-byte load of O and
+// dq row when dQ is accumulated with atomics, and the dk / dv rows when the key blocks are
+// split (dk_zero / dv_zero non-null).  D / 4 lanes per row, one 16-byte load of O and
 // of dO (and one 16-byte store of zeros) each.
 template <int D, bool ZERO_DQ>
 __global__ __launch_bounds__(256) void bwd_preprocess_f32_kernel(const float *__restrict__ o,
                                                                 const float *__restrict__ dout,
                                                                 float *__restrict__ delta,
                                                                 float *__restrict__ dq,
+                                                                float *__restrict__ dk_zero,
+                                                                float *__restrict__ dv_zero,
                                                                 int64_t rows) {
     constexpr int LPR = D / 4;  // lanes per row
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
@@ -377,6 +418,10 @@ __global__ __launch_bounds__(256) void bwd_preprocess_f32_kernel(const float *__
             const floatx4 b = *reinterpret_cast<const floatx4 *>(dout + row * D + 4 * c4);
             s = (a[0] * b[0] + a[1] * b[1]) + (a[2] * b[2] + a[3] * b[3]);
             if (ZERO_DQ) *reinterpret_cast<floatx4 *>(dq + row * D + 4 * c4) = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (dk_zero != nullptr) {  // split key blocks: dK / dV are sums of atomic adds
+                *reinterpret_cast<floatx4 *>(dk_zero + row * D + 4 * c4) = floatx4{0.f, 0.f, 0.f, 0.f};
+                *reinterpret_cast<floatx4 *>(dv_zero + row * D + 4 * c4) = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
         }
         s = group_sum<LPR>(s);
         if (row < rows && c4 == 0) delta[row] = s;
@@ -420,30 +465,38 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
     const int64_t rows = s.rows();
     if (s.T > 2147483647 / D) return hipErrorInvalidValue;
     const unsigned pre_blocks = stride_grid((rows * (D / 4) + 255) / 256, 256);
+    const bool k64 = D >= 64 && use_k64_kernel(s, mode);
+    const bool split = bwd_f32_use_split(s, k64, stream);
+    float *dk_zero = split ? dk : nullptr, *dv_zero = split ? dv : nullptr;
     if (mode == DqMode::Atomic) {
         hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, true>), dim3(pre_blocks), dim3(256), 0, stream,
-                           o, dout, delta, dq, rows);
+                           o, dout, delta, dq, dk_zero, dv_zero, rows);
     } else {
         hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, false>), dim3(pre_blocks), dim3(256), 0, stream,
-                           o, dout, delta, dq, rows);
+                           o, dout, delta, dq, dk_zero, dv_zero, rows);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if constexpr (D >= 64) {
-      if (use_k64_kernel(s, mode)) {
+      if (k64) {
         using C = BwdCfg<D>;
-        const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh();
+        const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh() * (split ? 2 : 1);
         if (!grid_fits(blocks, C::NW * kWave)) return hipErrorInvalidValue;
         const float kscale = kLog2e / sqrtf(float(D));
         const float inv_sqrt_d = 1.f / sqrtf(float(D));
-        hipLaunchKernelGGL((bwd_f32_mfma_kernel<D>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream, q, k,
-                           v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
-                           inv_sqrt_d);
+        if (split)
+            hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, true>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
+                               q, k, v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
+                               inv_sqrt_d);
+        else
+            hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, false>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
+                               q, k, v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
+                               inv_sqrt_d);
         return hipGetLastError();
       }
     }
     const K128Dq k128 = mode == DqMode::Atomic ? K128Dq::Atomic : mode == DqMode::Partial ? K128Dq::Partial : K128Dq::None;
-    e = launch_bwd_f32_k128(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, k128, s, stream);
+    e = launch_bwd_f32_k128(q, k, v, dout, lse, delta, dq, dq_part, dk, dv, k128, split, s, stream);
     if (e != hipSuccess || mode == DqMode::Atomic) return e;
     if (mode == DqMode::Separate) return launch_bwd_dq_f32(q, k, v, dout, lse, delta, dq, s, stream);
     const int64_t nkb = (s.T + kPartialBN - 1) / kPartialBN;
@@ -452,6 +505,21 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
                        dq_part, dq, int(s.T), int(s.bh()), int(s.causal), int(nkb), kPartialBN);
     return hipGetLastError();
 }
+
+}  // namespace
+
+// A key-major grid with no more workgroups than the chip holds at once (two per CU at
+// d <= 64, one at d = 128) runs as long as its longest key block -- key block 0 with every
+// query row when causal -- while most CUs idle: then each key block's rows are split between
+// two workgroups.
+bool bwd_f32_use_split(const AttnShape &s, bool k64, hipStream_t stream) {
+    const int64_t bn = k64 ? 64 : 128;
+    const int per_cu = s.d <= 64 ? 2 : 1;
+    const int cus = device_cus(stream);
+    return cus > 0 && (s.T + bn - 1) / bn * s.bh() <= int64_t(per_cu) * cus;
+}
+
+namespace {
 
 // The deterministic fp32 dQ scheme for this problem: partials while they stay small.
 DqMode deterministic_mode(const AttnShape &s) {

@@ -449,17 +449,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // +-3 % (8x12x1024 133.4 / 132.1, 1x12x8192 859.5 / 877.4, 32x12x1024 479.4 / 494.2), so
 // those keep whole blocks.
 bool fwd_use_split(const AttnShape &s, hipStream_t stream) {
-    static std::atomic<int> cus_of[64];
-    int dev = 0;
-    if ((stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 || dev >= 64)
-        return false;
-    int cus = cus_of[dev].load(std::memory_order_relaxed);
-    if (cus == 0) {
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            return false;
-        cus_of[dev].store(cus, std::memory_order_relaxed);
-    }
-    return (s.T + 127) / 128 * s.bh() <= int64_t(2) * cus;
+    const int cus = device_cus(stream);
+    return cus > 0 && (s.T + 127) / 128 * s.bh() <= int64_t(2) * cus;
 }
 
 template <int D, int BN>
@@ -479,6 +470,20 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
 }
 
 }  // namespace
+
+int device_cus(hipStream_t stream) {
+    static std::atomic<int> cus_of[64];
+    int dev = 0;
+    if ((stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 || dev >= 64)
+        return 0;
+    int cus = cus_of[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return 0;
+        cus_of[dev].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
 
 bool mfma_fwd_supported(int dtype, int64_t d) {
     (void)dtype;  // the fp32, bf16 and fp16 kernels all cover d in {32, 64, 128}

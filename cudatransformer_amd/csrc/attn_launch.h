@@ -71,14 +71,22 @@ hipError_t launch_f64_fwd(const void *q, const void *k, const void *v, void *o, 
 hipError_t launch_f64_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                           const void *lse, void *delta, void *dq, void *dk, void *dv, const AttnShape &s,
                           hipStream_t stream);
+// Compute units of the device that owns `stream` (the current device for the null stream),
+// cached per device; 0 if it cannot be queried.
+int device_cus(hipStream_t stream);
 // fp32 backward main kernel with 128-key workgroups (attn_bwd_k128.hip), d in {32, 64, 128}:
 // dK and dV, plus dQ accumulated into dq with atomics (Atomic: dq pre-zeroed), stored as
 // per-128-key-block partials in dq_part (Partial: plane kb holds key block kb's share), or
-// not at all (None).  delta must already hold rowsum(dO * O).
+// not at all (None).  delta must already hold rowsum(dO * O).  split: every key block's query
+// rows are shared by two workgroups, each adding its dK / dV share to dk / dv (pre-zeroed)
+// with one atomic add per element -- two addends, so the sum is the same in either order.
 enum class K128Dq { Atomic, Partial, None };
 hipError_t launch_bwd_f32_k128(const float *q, const float *k, const float *v, const float *dout,
                                const float *lse, const float *delta, float *dq, float *dq_part, float *dk, float *dv,
-                               K128Dq mode, const AttnShape &s, hipStream_t stream);
+                               K128Dq mode, bool split, const AttnShape &s, hipStream_t stream);
+// Whether the fp32 backward's key-major grid is short enough (no more workgroups than the chip
+// holds at once: two per CU at d <= 64, one at d = 128) to split every key block's rows in two.
+bool bwd_f32_use_split(const AttnShape &s, bool k64, hipStream_t stream);
 // fp32 dQ, query-major and atomic-free (attn_bwd_dq_f32.hip), d in {32, 64, 128}: dq is
 // written, not accumulated; delta must already hold rowsum(dO * O).
 hipError_t launch_bwd_dq_f32(const float *q, const float *k, const float *v, const float *dout, const float *lse,

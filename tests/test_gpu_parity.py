@@ -161,23 +161,37 @@ def test_c4_long_context_bf16_invariants(c4_run):
     assert bad_v.size == 0, f"sum dV != sum dO at (b, h) {bad_v.tolist()}: {sum_v.max():.3e}"
 
 
+@pytest.mark.parametrize("pol", [ct.POLICY_AUTO, ct.POLICY_DETERMINISTIC], ids=["auto", "deterministic"])
 @pytest.mark.parametrize("shape", [(1, 2, 1100, 64), (1, 2, 1100, 32), (4, 64, 300, 64), (4, 64, 300, 32)],
                          ids=lambda s: "x".join(map(str, s)))
-def test_causal_forward_decompositions_f32(shape):
-    """The fp32 causal forward (d <= 64) cuts every query block into two 64-row workgroups with
-    halved key ranges when the grid of whole 128-row blocks, ceil(T / 128) * B * H, is no
-    larger than two workgroups per CU, and keeps whole blocks otherwise.  The B1 H2 T1100
-    shapes take the split workgroups, the B4 H64 T300 ones the whole blocks; both have a
-    ragged last block."""
+def test_causal_work_decompositions_f32(shape, pol):
+    """Short fp32 causal grids are cut finer, long ones are not; both sides of each rule.
+    Forward (d <= 64): every 128-row query block becomes two 64-row workgroups with halved
+    key ranges when ceil(T / 128) * B * H <= 2 * CUs.  Backward: every key block's query rows
+    are shared by two workgroups (dK / dV summed by two atomic adds each, order-independent)
+    when ceil(T / bn) * B * H workgroups fit the chip at once (bn = 64 for the AUTO causal
+    d >= 64 kernel, else 128; two per CU at d <= 64).  The B1 H2 T1100 shapes take the finer
+    grids, the B4 H64 T300 ones the plain grids; both have a ragged last block.  Against the
+    oracle, and dK / dV / O / LSE bitwise equal over two runs (all of them under
+    DETERMINISTIC)."""
     b, h, t, d = shape
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    split = -(-t // 128) * b * h <= 2 * cus
-    assert split == (h == 2), f"{shape} is expected on the other side of the split rule ({cus} CUs)"
+    fwd_split = -(-t // 128) * b * h <= 2 * cus
+    bn = 64 if (pol == ct.POLICY_AUTO and d >= 64) else 128
+    bwd_split = -(-t // bn) * b * h <= (2 if d <= 64 else 1) * cus
+    assert fwd_split == bwd_split == (h == 2), f"{shape} is expected on the other side of a rule ({cus} CUs)"
     q, k, v, do = ora.make_inputs(shape, seed=57)
-    say(f"causal forward decomposition shape={shape} split={split}")
-    got = run_gpu(q, k, v, do, True, "f32")
+    say(f"causal work decomposition shape={shape} policy={pol} split={fwd_split}")
+    prev = ct.set_policy(pol)
+    try:
+        r1 = run_gpu(q, k, v, do, True, "f32")
+        r2 = run_gpu(q, k, v, do, True, "f32")
+    finally:
+        ct.set_policy(prev)
     want = ora.attention_fwd_bwd(q, k, v, do, True, chunk_heads=16)
-    assert_close(got, want, "f32", f"{shape} split={split}")
+    assert_close(r1, want, "f32", f"{shape} split={fwd_split}")
+    for key in (("o", "lse", "dk", "dv") if pol == ct.POLICY_AUTO else r1):
+        assert np.array_equal(r1[key], r2[key]), key
 
 
 @pytest.mark.parametrize("d", [32, 64, 128])
