@@ -249,6 +249,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // awaited (vmcnt) before the barrier that ends the next phase; they go through
 // load_tile_dma, and the barriers between phases (lds_barrier) do not drain them, so no
 // LDS read ever waits for a prefetch.
+#ifndef FWD_PP_SPLIT_CUS
+#define FWD_PP_SPLIT_CUS 1
+#endif
 template <int D>
 struct FwdPpCfg {
     static constexpr int NW = 8;          // waves: group A = 0-3, group B = 4-7
@@ -262,30 +265,38 @@ struct FwdPpCfg {
     static constexpr int LDS_BYTES = 4 * KB;  // K0, K1, V0, V1
 };
 
-template <int D, typename F>
+template <int D, typename F, bool SPLIT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_pp_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     uint16_t *__restrict__ o, float *__restrict__ lse, int T, int BH, int causal, float c) {
     using C = FwdPpCfg<D>;
     using V = typename F::vec;
-    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+    // SPLIT (causal): the workgroup owns 128 query rows; both groups hold the same rows
+    // (waves w and w + 4 the same 32), group A walks the first half of the key blocks and
+    // group B the second, each with its own tiles, and B's O / m / l are merged into A's at
+    // the end.
+    constexpr int GW = SPLIT ? 4 : C::NW;    // waves that load one group's tiles
+    constexpr int RB = SPLIT ? 128 : C::BM;  // query rows per workgroup
+    __shared__ __attribute__((aligned(1024))) char smem_all[(SPLIT ? 2 : 1) * C::LDS_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     // Wave-uniform: every branch on the wave index is a scalar branch.
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int group = wave >> 2;
+    const int wl = SPLIT ? (wave & 3) : wave;  // row slot of the wave
     const int col = lane & 31;
     const int half = lane >> 5;
+    char *smem = smem_all + (SPLIT ? group * C::LDS_BYTES : 0);
 
-    const int nqb = (T + C::BM - 1) / C::BM;
+    const int nqb = (T + RB - 1) / RB;
     const int id = blockIdx.x;
     const int bh = id % BH;
     const int qblk = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
     const int64_t base = int64_t(bh) * T * D;
-    const int q0 = qblk * C::BM;
-    const int row = q0 + wave * 32 + col;
-    const int wave_first_row = q0 + wave * 32;
+    const int q0 = qblk * RB;
+    const int row = q0 + wl * 32 + col;
+    const int wave_first_row = q0 + wl * 32;
     const int wave_last_row = wave_first_row + 31;
 
     V qb[C::KSTEPS];
@@ -310,8 +321,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int row_lim = causal ? row - 4 * half : 0x7fffffff;  // masked: key_u > row_lim
     const int t_lim = T - 4 * half;                            // masked: key_u >= t_lim
 
-    const int kend = causal ? min(T, q0 + C::BM) : T;
+    const int kend = causal ? min(T, q0 + RB) : T;
     const int nkb = (kend + C::BN - 1) / C::BN;
+    // This group's key blocks: global block kb_lo + j for local j in [0, len); every wave runs
+    // local iterations 0 .. jlast (the last one only finishes O).
+    const int n0 = (nkb + 1) / 2;
+    const int kb_lo = SPLIT && group ? n0 : 0;
+    const int len = SPLIT ? (group ? nkb - n0 : n0) : nkb;
+    const int jlast = SPLIT ? n0 : nkb;
     // Blocks this wave has keys in: the causal diagonal ends it early.
     const int wave_nkb = causal ? min(nkb, min(wave_last_row, T - 1) / C::BN + 1) : nkb;
 
@@ -320,15 +337,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Key tiles of block j this wave computes: inside the sequence and, causal, not wholly
     // above its diagonal.
     auto tile_active = [&](int j, int kt) __attribute__((always_inline)) {
-        const int t0 = j * C::BN + kt * 32;
+        const int t0 = (kb_lo + j) * C::BN + kt * 32;
         return t0 < T && (!causal || t0 <= wave_last_row);
     };
     // Batch j: K_{j+1} and V_j, each wave its share.
     auto issue = [&](int j) __attribute__((always_inline)) {
-        if (j + 1 < nkb)
-            load_tile_dma<D, C::BN, C::NW>(ktile(j + 1), k + base + int64_t(j + 1) * C::BN * D, T - (j + 1) * C::BN,
-                                           wave, lane);
-        if (j < nkb) load_tile_dma<D, C::BN, C::NW>(vtile(j), v + base + int64_t(j) * C::BN * D, T - j * C::BN, wave, lane);
+        const int jk = kb_lo + j + 1, jv = kb_lo + j;  // global key blocks of K_{j+1} and V_j
+        if (j + 1 < len)
+            load_tile_dma<D, C::BN, GW>(ktile(j + 1), k + base + int64_t(jk) * C::BN * D, T - jk * C::BN,
+                                        SPLIT ? wl : wave, lane);
+        if (j < len)
+            load_tile_dma<D, C::BN, GW>(vtile(j), v + base + int64_t(jv) * C::BN * D, T - jv * C::BN,
+                                        SPLIT ? wl : wave, lane);
     };
 
     // M(j): O += V_{j-1} P_{j-1} (16 MFMAs at d = 128), then S_j = K_j Q^T (16), as one
@@ -401,7 +421,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto softmax = [&](auto mask, int j) __attribute__((always_inline)) {
         constexpr bool MASK = decltype(mask)::value;
         if constexpr (MASK) {
-            const int j0 = j * C::BN;
+            const int j0 = (kb_lo + j) * C::BN;
 #pragma unroll
             for (int kt = 0; kt < C::KT; ++kt) {
                 if (!tile_active(j, kt)) continue;
@@ -437,7 +457,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Block j needs the masked softmax when it crosses the sequence end or, causal, the
     // wave's diagonal; both conditions hold from some block on: masked(j) <=> j >= jm.
     const int jm_t = T / C::BN;
-    const int jm = causal ? min(jm_t, max(0, (wave_first_row - 62 + C::BN - 1) / C::BN)) : jm_t;
+    const int jm_g = causal ? min(jm_t, max(0, (wave_first_row - 62 + C::BN - 1) / C::BN)) : jm_t;
+    // Local forms of the first masked block and of this wave's block count.
+    const int jm = SPLIT ? min(len, max(0, jm_g - kb_lo)) : jm_g;
+    const int wnkb = SPLIT ? min(len, max(0, wave_nkb - kb_lo)) : wave_nkb;
 
     // One iteration = both phases of block j for this wave, each closed by a barrier.  Group A
     // issues batch j at the start of M(j) and awaits it at the end of V(j); group B issues
@@ -465,21 +488,59 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     using Masked = std::integral_constant<int, 2>;
 
     // K_0 before the first phase; batch 0 (K_1, V_0) lands during the first two phases.
-    load_tile_dma<D, C::BN, C::NW>(ktile(0), k + base, T, wave, lane);
+    if (len > 0)
+        load_tile_dma<D, C::BN, GW>(ktile(0), k + base + int64_t(kb_lo) * C::BN * D, T - kb_lo * C::BN,
+                                    SPLIT ? wl : wave, lane);
     wait_loads();
     lds_barrier();
     if (group == 1) {
         issue(0);
         lds_barrier();  // group B runs one phase behind group A
     }
-    if (jm > 0) iter(N{}, Y{}, Plain{}, 0);
-    else iter(N{}, Y{}, Masked{}, 0);
-    int j = 1;
-    for (; j < min(jm, wave_nkb); ++j) iter(Y{}, Y{}, Plain{}, j);
-    for (; j < wave_nkb; ++j) iter(Y{}, Y{}, Masked{}, j);
-    iter(Y{}, N{}, NoSm{}, j);  // j == wave_nkb: the last O update
-    for (++j; j <= nkb; ++j) iter(N{}, N{}, NoSm{}, j);  // keys past this wave's diagonal
+    int j = 0;
+    if (wnkb > 0) {  // always, unless SPLIT and none of the wave's keys is in its group's half
+        if (jm > 0) iter(N{}, Y{}, Plain{}, 0);
+        else iter(N{}, Y{}, Masked{}, 0);
+        j = 1;
+        for (; j < min(jm, wnkb); ++j) iter(Y{}, Y{}, Plain{}, j);
+        for (; j < wnkb; ++j) iter(Y{}, Y{}, Masked{}, j);
+        iter(Y{}, N{}, NoSm{}, j);  // j == wnkb: the last O update
+        ++j;
+    }
+    for (; j <= jlast; ++j) iter(N{}, N{}, NoSm{}, j);  // keys past this wave's diagonal
     if (group == 0) lds_barrier();  // matches group B's extra barrier
+
+    if constexpr (SPLIT) {
+        // Group B's lane state lands at mb[(wl NR + i) 64 + lane]; group A's wave wl merges it:
+        // m = max(mA, mB) (log2 units, times c), O = OA 2^(mA - m) + OB 2^(mB - m), l likewise.
+        // Group A holds key 0 of every row, so mA is finite; a wave of B without keys keeps
+        // m = -inf, weight 0.
+        constexpr int NR = C::DT * 16 + 2;
+        static_assert(4 * NR * kWave * 4 <= 2 * C::LDS_BYTES, "merge buffer");
+        float *mb = reinterpret_cast<float *>(smem_all);
+        lds_barrier();  // every wave is done with the tiles
+        if (group == 1) {
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mb[(wl * NR + dt * 16 + r) * kWave + lane] = oacc[dt][r];
+            mb[(wl * NR + NR - 2) * kWave + lane] = m_run;
+            mb[(wl * NR + NR - 1) * kWave + lane] = l_run;
+        }
+        lds_barrier();
+        if (group == 1) return;
+        const float m1 = mb[(wl * NR + NR - 2) * kWave + lane];
+        const float l1 = mb[(wl * NR + NR - 1) * kWave + lane];
+        const float m = fmaxf(m_run, m1);
+        const float a0 = fast_exp2(m_run - m), a1 = fast_exp2(m1 - m);
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                oacc[dt][r] = oacc[dt][r] * a0 + mb[(wl * NR + dt * 16 + r) * kWave + lane] * a1;
+        l_run = l_run * a0 + l1 * a1;
+        m_run = m;
+    }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
     const float inv_l = 1.f / l_tot;
@@ -507,10 +568,20 @@ hipError_t fwd_bf16_pp(const void *q, const void *k, const void *v, void *o, flo
     const int64_t blocks = nqb * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float c = kLog2e / sqrtf(float(D));
-    hipLaunchKernelGGL((fwd_bf16_pp_kernel<D, F>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
-                       static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
-                       static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), lse, int(s.T),
-                       int(s.bh()), int(s.causal), c);
+    // A causal grid of no more whole workgroups than CUs (one each) runs as long as its longest
+    // query block: then 128-row workgroups with the key range halved between the groups.
+    const int cus = device_cus(stream);
+    const bool split = s.causal && cus > 0 && blocks <= FWD_PP_SPLIT_CUS * int64_t(cus);
+    const int64_t grid = split ? (s.T + 127) / 128 * s.bh() : blocks;
+    if (!grid_fits(grid, C::NW * kWave)) return hipErrorInvalidValue;
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(unsigned(grid)), dim3(C::NW * kWave), 0, stream,
+                           static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
+                           static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), lse, int(s.T), int(s.bh()),
+                           int(s.causal), c);
+    };
+    if (split) launch(fwd_bf16_pp_kernel<D, F, true>);
+    else launch(fwd_bf16_pp_kernel<D, F, false>);
     return hipGetLastError();
 }
 

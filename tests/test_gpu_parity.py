@@ -194,6 +194,24 @@ def test_causal_work_decompositions_f32(shape, pol):
         assert np.array_equal(r1[key], r2[key]), key
 
 
+@pytest.mark.parametrize("shape", [(1, 2, 1100, 128), (4, 72, 300, 128)], ids=lambda s: "x".join(map(str, s)))
+def test_causal_forward_decompositions_bf16(shape):
+    """The bf16 d = 128 causal forward runs 256-row workgroups (two 4-wave groups alternating
+    MFMA and softmax phases) and, when those are no more than the CUs, 128-row workgroups
+    whose two groups take the two halves of the key range and merge through LDS.  B1 H2
+    T1100 takes the halved key ranges, B4 H72 T300 the whole ones; both have a ragged last
+    block."""
+    b, h, t, d = shape
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    split = -(-t // 256) * b * h <= cus
+    assert split == (h == 2), f"{shape} is expected on the other side of the split rule ({cus} CUs)"
+    q, k, v, do = ora.make_inputs(shape, seed=58, std=0.5, dtype="bf16")
+    say(f"bf16 causal forward decomposition shape={shape} split={split}")
+    got = run_gpu(q, k, v, do, True, "bf16")
+    want = ora.attention_fwd_bwd(q, k, v, do, True, chunk_heads=16)
+    assert_close(got, want, "bf16", f"{shape} split={split}")
+
+
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_mfma_matches_generic(causal, d):
