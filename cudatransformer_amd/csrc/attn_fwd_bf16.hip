@@ -143,29 +143,37 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const typena
     }
 }
 
-template <int D, typename F>
+template <int D, typename F, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fwd_bf16_mfma_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     uint16_t *__restrict__ o, float *__restrict__ lse, int T, int BH, int causal, float c) {
     using C = FwdBf16Cfg<D>;
     using V = typename F::vec;
-    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
-    const uint32_t L = lds_addr(smem);
+    // SPLIT (causal): 64 query rows per workgroup; waves 2 h and 2 h + 1 (rows q0 .. q0 + 31
+    // and q0 + 32 .. q0 + 63) walk half h of the key blocks with their own tiles, and half 1's
+    // O / m / l are merged into half 0's through LDS at the end.
+    constexpr int GW = SPLIT ? 2 : C::NW;    // waves that load one half's tiles
+    constexpr int RB = SPLIT ? 64 : C::BM;   // query rows per workgroup
+    __shared__ __attribute__((aligned(1024))) char smem_all[(SPLIT ? 2 : 1) * C::LDS_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
+    const int hk = SPLIT ? wave >> 1 : 0;      // key half
+    const int wl = SPLIT ? (wave & 1) : wave;  // row slot
     const int col = lane & 31;
     const int half = lane >> 5;
+    char *smem = smem_all + (SPLIT ? hk * C::LDS_BYTES : 0);
+    const uint32_t L = lds_addr(smem);
 
-    const int nqb = (T + C::BM - 1) / C::BM;
+    const int nqb = (T + RB - 1) / RB;
     const int id = blockIdx.x;
     const int bh = id % BH;
     const int qblk = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
     const int64_t base = int64_t(bh) * T * D;
-    const int q0 = qblk * C::BM;
-    const int row = q0 + wave * 32 + col;
-    const int wave_first_row = q0 + wave * 32;
+    const int q0 = qblk * RB;
+    const int row = q0 + wl * 32 + col;
+    const int wave_first_row = q0 + wl * 32;
     const int wave_last_row = wave_first_row + 31;
 
     // Q^T as the B operand: lane (row, half) holds Q[row][16s + 8*half .. +7].
@@ -186,21 +194,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint32_t rk = uint32_t(Tile<D>::off(col, half));
     const uint32_t cv0 = col_base<D>(0, 0, 0, lane), cv1 = col_base<D>(0, 0, 1, lane);
 
-    const int kend = causal ? min(T, q0 + C::BM) : T;
-    const int nkb = (kend + C::BN - 1) / C::BN;
+    const int kend = causal ? min(T, q0 + RB) : T;
+    const int nkb_all = (kend + C::BN - 1) / C::BN;
+    // This wave's key blocks: [kb_lo, kb_hi); every wave meets `iters` barriers.
+    const int n0 = (nkb_all + 1) / 2;
+    const int kb_lo = SPLIT && hk ? n0 : 0;
+    const int kb_hi = SPLIT && !hk ? n0 : nkb_all;
+    const int iters = SPLIT ? n0 : nkb_all;
     auto issue = [&](int j0, int buf) {
-        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB, k + base, j0, T, wave, lane);
-        load_tile<D, C::BN, C::NW>(smem + 2 * buf * C::KB + C::KB, v + base, j0, T, wave, lane);
+        load_tile<D, C::BN, GW>(smem + 2 * buf * C::KB, k + base, j0, T, wl, lane);
+        load_tile<D, C::BN, GW>(smem + 2 * buf * C::KB + C::KB, v + base, j0, T, wl, lane);
     };
 
-    issue(0, 0);
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
+    if (kb_lo < kb_hi) issue(kb_lo * C::BN, 0);
+    for (int it = 0; it < iters; ++it) {
+        const int kb = kb_lo + it;
+        const int buf = it & 1;
         // This wave's loads of `buf` have landed (vmcnt = 0); after the barrier every wave's
         // have, and every wave is done reading buf ^ 1.
         __builtin_amdgcn_s_waitcnt(0xF70);
         __syncthreads();
-        if (kb + 1 < nkb) issue((kb + 1) * C::BN, buf ^ 1);
+        if (kb + 1 < kb_hi) issue((kb + 1) * C::BN, buf ^ 1);
+        if (kb >= kb_hi) continue;
         const int j0 = kb * C::BN;
         const uint32_t kt = L + uint32_t(2 * buf * C::KB);
         const bool masked = (j0 + C::BN > T) || (causal && j0 + C::BN - 1 > wave_first_row);
@@ -214,6 +229,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
 
+    if constexpr (SPLIT) {
+        // Half 1's lane state at mb[(wl NR + i) 64 + lane]; half 0's wave wl merges it:
+        // m = max(m0, m1) (log2 units, times c), O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise.
+        // Half 0 holds key 0 of its rows, so m0 is finite; an empty half 1 has m1 = -inf.
+        constexpr int NR = C::DT * 16 + 2;
+        static_assert(2 * NR * kWave * 4 <= 2 * C::LDS_BYTES, "merge buffer");
+        float *mb = reinterpret_cast<float *>(smem_all);
+        __syncthreads();  // every wave is done with the tiles
+        if (hk == 1) {
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mb[(wl * NR + dt * 16 + r) * kWave + lane] = st.oacc[dt][r];
+            mb[(wl * NR + NR - 2) * kWave + lane] = st.m_run;
+            mb[(wl * NR + NR - 1) * kWave + lane] = st.l_run;
+        }
+        __syncthreads();
+        if (hk == 1) return;
+        const float m1 = mb[(wl * NR + NR - 2) * kWave + lane];
+        const float l1 = mb[(wl * NR + NR - 1) * kWave + lane];
+        const float m = fmaxf(st.m_run, m1);
+        const float a0 = fast_exp2(st.m_run - m), a1 = fast_exp2(m1 - m);
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                st.oacc[dt][r] = st.oacc[dt][r] * a0 + mb[(wl * NR + dt * 16 + r) * kWave + lane] * a1;
+        st.l_run = st.l_run * a0 + l1 * a1;
+        st.m_run = m;
+    }
     const float l_tot = st.l_run + __shfl_xor(st.l_run, 32, kWave);
     const float inv_l = 1.f / l_tot;
     if (row < T) {
@@ -593,10 +638,20 @@ hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float 
     const int64_t blocks = nqb * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     const float c = kLog2e / sqrtf(float(D));
-    hipLaunchKernelGGL((fwd_bf16_mfma_kernel<D, F>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
-                       static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
-                       static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), lse, int(s.T),
-                       int(s.bh()), int(s.causal), c);
+    // A causal grid of no more whole workgroups than the chip holds at once (two per CU) runs
+    // as long as its longest query block: then 64-row workgroups with halved key ranges.
+    const int cus = device_cus(stream);
+    const bool split = s.causal && cus > 0 && blocks <= 2 * int64_t(cus);
+    const int64_t grid = split ? (s.T + 63) / 64 * s.bh() : blocks;
+    if (!grid_fits(grid, C::NW * kWave)) return hipErrorInvalidValue;
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(unsigned(grid)), dim3(C::NW * kWave), 0, stream,
+                           static_cast<const uint16_t *>(q), static_cast<const uint16_t *>(k),
+                           static_cast<const uint16_t *>(v), static_cast<uint16_t *>(o), lse, int(s.T), int(s.bh()),
+                           int(s.causal), c);
+    };
+    if (split) launch(fwd_bf16_mfma_kernel<D, F, true>);
+    else launch(fwd_bf16_mfma_kernel<D, F, false>);
     return hipGetLastError();
 }
 

@@ -194,16 +194,19 @@ def test_causal_work_decompositions_f32(shape, pol):
         assert np.array_equal(r1[key], r2[key]), key
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 1100, 128), (4, 72, 300, 128)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(1, 2, 1100, 128), (4, 72, 300, 128), (1, 2, 1100, 64), (4, 72, 300, 64),
+                                   (1, 2, 1100, 32)], ids=lambda s: "x".join(map(str, s)))
 def test_causal_forward_decompositions_bf16(shape):
-    """The bf16 d = 128 causal forward runs 256-row workgroups (two 4-wave groups alternating
-    MFMA and softmax phases) and, when those are no more than the CUs, 128-row workgroups
-    whose two groups take the two halves of the key range and merge through LDS.  B1 H2
-    T1100 takes the halved key ranges, B4 H72 T300 the whole ones; both have a ragged last
-    block."""
+    """The bf16 causal forward halves the key range of each workgroup's rows between two wave
+    groups, merged through LDS, when the grid of whole workgroups fits the chip at once:
+    d = 128 (256-row workgroups of two 4-wave groups alternating MFMA and softmax phases,
+    one per CU) splits into 128-row workgroups when ceil(T / 256) * B * H <= CUs; d <= 64
+    (128-row 4-wave workgroups, two per CU) into 64-row ones when ceil(T / 128) * B * H <=
+    2 * CUs.  The B1 H2 T1100 shapes take the halved key ranges, B4 H72 T300 the whole ones;
+    all have a ragged last block."""
     b, h, t, d = shape
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    split = -(-t // 256) * b * h <= cus
+    split = (-(-t // 256) * b * h <= cus) if d == 128 else (-(-t // 128) * b * h <= 2 * cus)
     assert split == (h == 2), f"{shape} is expected on the other side of the split rule ({cus} CUs)"
     q, k, v, do = ora.make_inputs(shape, seed=58, std=0.5, dtype="bf16")
     say(f"bf16 causal forward decomposition shape={shape} split={split}")
