@@ -284,16 +284,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // SIMD drift into running both phases at the same time.  Here a workgroup holds 8 waves, two
 // per SIMD (waves w and w + 4 share one): group A (waves 0-3) and group B (waves 4-7)
 // alternate between an MFMA phase M(j) -- S_j = K_j Q^T and O += V_{j-1} P_{j-1} -- and a
-// VALU phase V(j) -- the online softmax of S_j into P_j -- with a workgroup barrier after
-// every phase and group B one phase behind group A, so between two barriers one wave of each
-// SIMD runs MFMAs while the other runs VALU work (s_setprio raises the MFMA phase's issue
-// priority).  Each wave owns 32 query rows (256 per workgroup).
+// VALU phase V(j) -- the online softmax of S_j into P_j -- with group B one phase behind
+// group A: between two workgroup barriers (one per iteration; SPLIT: one per phase) group A
+// runs M(j + 1), V(j + 1) and group B V(j), M(j + 1), so one wave of each SIMD runs MFMAs
+// while the other runs VALU work (s_setprio raises the MFMA phase's issue priority).  Each
+// wave owns 32 query rows (256 per workgroup).
 //
 // K and V blocks are double-buffered (block j in buffer j & 1).  The loads of K_{j+1} and V_j
-// are issued at the start of the phase that begins with A's M(j) (A in M(j), B in V(j-1)) and
-// awaited (vmcnt) before the barrier that ends the next phase; they go through
-// load_tile_dma, and the barriers between phases (lds_barrier) do not drain them, so no
-// LDS read ever waits for a prefetch.
+// are issued at the start of the iteration in which A runs M(j) and awaited (vmcnt) before
+// its closing barrier; they go through load_tile_dma, and the barrier (lds_barrier) does not
+// drain them, so no LDS read ever waits for a prefetch.
 #ifndef FWD_PP_SPLIT_CUS
 #define FWD_PP_SPLIT_CUS 1
 #endif
@@ -507,11 +507,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int jm = SPLIT ? min(len, max(0, jm_g - kb_lo)) : jm_g;
     const int wnkb = SPLIT ? min(len, max(0, wave_nkb - kb_lo)) : wave_nkb;
 
-    // One iteration = both phases of block j for this wave, each closed by a barrier.  Group A
-    // issues batch j at the start of M(j) and awaits it at the end of V(j); group B issues
-    // batch j + 1 at the start of V(j) and awaits batch j at the end of M(j).  PV / SC / SM:
-    // what this wave computes (the O update of block j - 1, the scores of block j, their
-    // softmax: none, unmasked or masked); every wave runs every iteration up to nkb.
+    // One iteration = both phases of block j for this wave, and one workgroup barrier: group A
+    // runs M(j), V(j), barrier; group B runs M(j), barrier, V(j).  Between two barriers group A
+    // runs M(j + 1) then V(j + 1) while group B runs V(j) then M(j + 1), so each SIMD's two
+    // waves meet MFMA phase against softmax phase without a barrier between the phases (a
+    // second barrier per iteration, at the phase change, cost ~250 cycles of its ~3 500).
+    // Group A issues batch j at the start of M(j) and awaits it at the end of V(j); group B
+    // issues batch j + 1 at the start of V(j) and awaits batch j at the end of M(j); the
+    // barrier then publishes batch j, which M(j + 1) reads.  No load overwrites a tile a wave
+    // may still read: batch j + 1 (K_{j+2}, V_{j+1}) replaces K_j and V_{j-1}, which M(j)
+    // read before the barrier.  PV / SC / SM: what this wave computes (the O update of block
+    // j - 1, the scores of block j, their softmax: none, unmasked or masked); every wave runs
+    // every iteration up to nkb.
+    // SPLIT keeps a barrier at every phase change (group B then waits one phase before its
+    // first M): with one per iteration its short grids ran ~3 % slower.
+    constexpr bool ONE_BARRIER = !SPLIT;
     auto iter = [&](auto pv, auto sc, auto sm, int j) __attribute__((always_inline)) {
         constexpr int SM = decltype(sm)::value;
         if (group == 0) issue(j);
@@ -519,12 +529,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         mphase_t(pv, sc, j);
         __builtin_amdgcn_s_setprio(0);
         if (group == 1) wait_loads();
-        lds_barrier();
+        if (!ONE_BARRIER || group == 1) lds_barrier();
         if (group == 1) issue(j + 1);
         if constexpr (SM == 1) softmax(std::false_type{}, j);
         if constexpr (SM == 2) softmax(std::true_type{}, j);
         if (group == 0) wait_loads();
-        lds_barrier();
+        if (!ONE_BARRIER || group == 0) lds_barrier();
     };
     using Y = std::true_type;
     using N = std::false_type;
@@ -532,7 +542,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     using Plain = std::integral_constant<int, 1>;
     using Masked = std::integral_constant<int, 2>;
 
-    // K_0 before the first phase; batch 0 (K_1, V_0) lands during the first two phases.
+    // K_0 before the first phase; batch 0 (K_1, V_0) lands during the first iteration.
     if (len > 0)
         load_tile_dma<D, C::BN, GW>(ktile(0), k + base + int64_t(kb_lo) * C::BN * D, T - kb_lo * C::BN,
                                     SPLIT ? wl : wave, lane);
@@ -540,7 +550,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     lds_barrier();
     if (group == 1) {
         issue(0);
-        lds_barrier();  // group B runs one phase behind group A
+        if (!ONE_BARRIER) lds_barrier();  // group B one phase behind group A
     }
     int j = 0;
     if (wnkb > 0) {  // always, unless SPLIT and none of the wave's keys is in its group's half
@@ -553,7 +563,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         ++j;
     }
     for (; j <= jlast; ++j) iter(N{}, N{}, NoSm{}, j);  // keys past this wave's diagonal
-    if (group == 0) lds_barrier();  // matches group B's extra barrier
+    if (!ONE_BARRIER && group == 0) lds_barrier();  // matches group B's extra barrier
 
     if constexpr (SPLIT) {
         // Group B's lane state lands at mb[(wl NR + i) 64 + lane]; group A's wave wl merges it:
