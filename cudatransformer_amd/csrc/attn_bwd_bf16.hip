@@ -11,9 +11,11 @@
 // key-major design's dQ atomics (T^2/2 * d / 128 per head, 4.3 GB at B1 H32 T8192 d128)
 // bound it at ~3 ms; recomputing S and dP in a second, query-major kernel costs 2 of the
 // backward's 5 matmuls again but runs at MFMA speed and is deterministic by construction.
-//   * bwd_bf16_dkdv_kernel (key-major): a workgroup of 4 waves owns 128 keys (wave w: 32),
-//     keeps dK^T and dV^T in registers and walks 32-row query blocks (causal: from its
-//     diagonal on).  S = Q K^T, dP = dO V^T (lane = one key, registers = rows), then
+//   * bwd_bf16_dkdv_kernel (key-major): a workgroup of 8 waves owns 128 keys (4 key slices
+//     of 32 x 2 row slices), keeps dK^T and dV^T in registers and walks 64-row query blocks
+//     (causal: from its diagonal on), row slice rs taking rows 32 rs .. 32 rs + 31 of each;
+//     the two row slices' sums meet in LDS at the end.  S = Q K^T, dP = dO V^T (lane = one
+//     key, registers = rows), then
 //     P = exp2(S c + nl2), dS = P (dP - delta) elementwise (the dP accumulator starts from
 //     -delta), and dV^T += dO^T P,
 //     dK^T += Q^T dS with P / dS straight from the accumulator as B operands.
