@@ -294,9 +294,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // are issued at the start of the iteration in which A runs M(j) and awaited (vmcnt) before
 // its closing barrier; they go through load_tile_dma, and the barrier (lds_barrier) does not
 // drain them, so no LDS read ever waits for a prefetch.
-#ifndef FWD_PP_SPLIT_CUS
-#define FWD_PP_SPLIT_CUS 1
-#endif
+// Short causal grids take the split kernel when they have at most this many whole
+// workgroups per CU (two per CU made B1 H32 T4096 and B2 H16 T4096 slower, 136 -> 160 us).
+constexpr int kPpSplitWorkgroupsPerCu = 1;
 template <int D>
 struct FwdPpCfg {
     static constexpr int NW = 8;          // waves: group A = 0-3, group B = 4-7
@@ -626,7 +626,7 @@ hipError_t fwd_bf16_pp(const void *q, const void *k, const void *v, void *o, flo
     // A causal grid of no more whole workgroups than CUs (one each) runs as long as its longest
     // query block: then 128-row workgroups with the key range halved between the groups.
     const int cus = device_cus(stream);
-    const bool split = s.causal && cus > 0 && blocks <= FWD_PP_SPLIT_CUS * int64_t(cus);
+    const bool split = s.causal && cus > 0 && blocks <= kPpSplitWorkgroupsPerCu * int64_t(cus);
     const int64_t grid = split ? (s.T + 127) / 128 * s.bh() : blocks;
     if (!grid_fits(grid, C::NW * kWave)) return hipErrorInvalidValue;
     auto launch = [&](auto kernel) {
