@@ -487,8 +487,8 @@ hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, 
                        u16(o), u16(dout), lse, delta, nl2, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const float c = kLog2e / sqrtf(float(D));
-    const float inv_sqrt_d = 1.f / sqrtf(float(D));
+    const float c = kLog2e / sqrtf(float(s.scale_dim()));
+    const float inv_sqrt_d = 1.f / sqrtf(float(s.scale_dim()));
     hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D, F>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0, stream,
                        u16(q), u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dk),
                        static_cast<uint16_t *>(dv), int(s.T), int(s.bh()), int(s.causal), c, inv_sqrt_d);

@@ -198,8 +198,8 @@ hipError_t launch_dq(const float *q, const float *k, const float *v, const float
     using C = DqF32Cfg<D>;
     const int64_t blocks = ((s.T + C::BM - 1) / C::BM) * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
-    const float qscale = kLog2e / sqrtf(float(D));
-    const float inv_sqrt_d = 1.f / sqrtf(float(D));
+    const float qscale = kLog2e / sqrtf(float(s.scale_dim()));
+    const float inv_sqrt_d = 1.f / sqrtf(float(s.scale_dim()));
     hipLaunchKernelGGL((bwd_dq_f32_kernel<D>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream, q, k, v, dout,
                        lse, delta, dq, int(s.T), int(s.bh()), int(s.causal), qscale, inv_sqrt_d);
     return hipGetLastError();

@@ -373,8 +373,8 @@ hipError_t launch_k128(const float *q, const float *k, const float *v, const flo
     using C = BwdK128Cfg<D>;
     const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh() * (split ? 2 : 1);
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
-    const float kscale = kLog2e / sqrtf(float(D));
-    const float inv_sqrt_d = 1.f / sqrtf(float(D));
+    const float kscale = kLog2e / sqrtf(float(s.scale_dim()));
+    const float inv_sqrt_d = 1.f / sqrtf(float(s.scale_dim()));
     const dim3 grid{unsigned(blocks)};
     switch (mode) {
         case K128Dq::Atomic:

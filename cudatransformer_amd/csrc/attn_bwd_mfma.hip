@@ -482,8 +482,8 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
         using C = BwdCfg<D>;
         const int64_t blocks = ((s.T + C::BN - 1) / C::BN) * s.bh() * (split ? 2 : 1);
         if (!grid_fits(blocks, C::NW * kWave)) return hipErrorInvalidValue;
-        const float kscale = kLog2e / sqrtf(float(D));
-        const float inv_sqrt_d = 1.f / sqrtf(float(D));
+        const float kscale = kLog2e / sqrtf(float(s.scale_dim()));
+        const float inv_sqrt_d = 1.f / sqrtf(float(s.scale_dim()));
         if (split)
             hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, true>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
                                q, k, v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,

@@ -492,7 +492,7 @@ hipError_t fwd_f64(const void *q, const void *k, const void *v, void *o, void *l
     hipLaunchKernelGGL(fwd_f64_mfma_kernel<D>, dim3(unsigned(blocks)), dim3(256), 0, stream,
                        static_cast<const double *>(q), static_cast<const double *>(k),
                        static_cast<const double *>(v), static_cast<double *>(o), static_cast<double *>(lse),
-                       int(s.T), int(s.bh()), int(s.causal), kLog2eD / sqrt(double(D)));
+                       int(s.T), int(s.bh()), int(s.causal), kLog2eD / sqrt(double(s.scale_dim())));
     return hipGetLastError();
 }
 
@@ -504,7 +504,7 @@ hipError_t bwd_f64(const void *q, const void *k, const void *v, const void *o, c
     if (!grid_fits(kv_blocks, 256) || !grid_fits(q_blocks, 256) || s.T > 2147483647 / D) return hipErrorInvalidValue;
     hipError_t e = launch_bwd_preprocess(3, o, dout, delta, s, stream);  // delta = rowsum(dO * O), fp64
     if (e != hipSuccess) return e;
-    const double c = kLog2eD / sqrt(double(D)), inv_sqrt_d = 1.0 / sqrt(double(D));
+    const double c = kLog2eD / sqrt(double(s.scale_dim())), inv_sqrt_d = 1.0 / sqrt(double(s.scale_dim()));
     auto cd = [](const void *p) { return static_cast<const double *>(p); };
     hipLaunchKernelGGL(bwd_f64_dkdv_kernel<D>, dim3(unsigned(kv_blocks)), dim3(256), 0, stream, cd(q), cd(k), cd(v),
                        cd(dout), cd(lse), cd(delta), static_cast<double *>(dk), static_cast<double *>(dv), int(s.T),

@@ -622,7 +622,7 @@ hipError_t fwd_bf16_pp(const void *q, const void *k, const void *v, void *o, flo
     const int64_t nqb = (s.T + C::BM - 1) / C::BM;
     const int64_t blocks = nqb * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
-    const float c = kLog2e / sqrtf(float(D));
+    const float c = kLog2e / sqrtf(float(s.scale_dim()));
     // A causal grid of no more whole workgroups than CUs (one each) runs as long as its longest
     // query block: then 128-row workgroups with the key range halved between the groups.
     const int cus = device_cus(stream);
@@ -647,7 +647,7 @@ hipError_t fwd_bf16(const void *q, const void *k, const void *v, void *o, float 
     const int64_t nqb = (s.T + C::BM - 1) / C::BM;
     const int64_t blocks = nqb * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
-    const float c = kLog2e / sqrtf(float(D));
+    const float c = kLog2e / sqrtf(float(s.scale_dim()));
     // A causal grid of no more whole workgroups than the chip holds at once (two per CU) runs
     // as long as its longest query block: then 64-row workgroups with halved key ranges.
     const int cus = device_cus(stream);

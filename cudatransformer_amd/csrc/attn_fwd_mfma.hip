@@ -460,7 +460,7 @@ hipError_t fwd_f32(const float *q, const float *k, const float *v, float *o, flo
     const int64_t nqb = (s.T + C::BM - 1) / C::BM;
     const int64_t blocks = nqb * s.bh();
     if (!grid_fits(blocks, C::NW * kWave) || s.T > 2147483647 / D) return hipErrorInvalidValue;
-    const float qscale = kLog2e / sqrtf(float(D));
+    const float qscale = kLog2e / sqrtf(float(s.scale_dim()));
     const int split = BN == 64 && s.causal && fwd_use_split(s, stream);
     const int64_t grid = split ? (s.T + 63) / 64 * s.bh() : blocks;
     if (!grid_fits(grid, C::NW * kWave)) return hipErrorInvalidValue;

@@ -11,8 +11,12 @@ namespace ctattn {
 struct AttnShape {
     int64_t B, H, T, d;
     bool causal;
+    // Head dim whose 1 / sqrt scales the scores: d itself, unless the tensors are copies
+    // zero-padded from a smaller head dim (scale_d), whose scale the kernels must keep.
+    int64_t scale_d = 0;
     int64_t bh() const { return B * H; }
     int64_t rows() const { return B * H * T; }
+    int64_t scale_dim() const { return scale_d > 0 ? scale_d : d; }
 };
 
 // A launch may hold at most 2^32 - 1 work-items (gridDim.x * blockDim.x) and 2^31 - 1
@@ -91,6 +95,16 @@ bool bwd_f32_use_split(const AttnShape &s, bool k64, hipStream_t stream);
 // written, not accumulated; delta must already hold rowsum(dO * O).
 hipError_t launch_bwd_dq_f32(const float *q, const float *k, const float *v, const float *dout, const float *lse,
                              const float *delta, float *dq, const AttnShape &s, hipStream_t stream);
+// Row copies for head dims without an MFMA kernel of their own (attn_pad.hip): pad copies
+// each of `count` (<= kMaxRowCopies) [rows][d] tensors in[i] into a [rows][dp] buffer out[i]
+// with columns d .. dp - 1 zero, unpad copies the d leading columns of each [rows][dp] buffer
+// in[i] into the [rows][d] tensor out[i]; elem_bytes is the storage element size (2, 4, 8).
+// One bandwidth-bound launch on `stream` per call.
+constexpr int kMaxRowCopies = 5;
+hipError_t launch_pad_rows(int elem_bytes, const void *const *in, void *const *out, int count, int64_t rows, int d,
+                           int dp, hipStream_t stream);
+hipError_t launch_unpad_rows(int elem_bytes, const void *const *in, void *const *out, int count, int64_t rows,
+                             int d, int dp, hipStream_t stream);
 // Runs the whole MFMA backward: its own preprocess (delta = rowsum(dO * O) into `delta`,
 // fp32 [B, H, T]) and the main kernel(s).  `extra` points at mfma_bwd_workspace_bytes()
 // bytes of scratch (256-byte aligned).  `deterministic` (fp32): no atomics -- dQ from

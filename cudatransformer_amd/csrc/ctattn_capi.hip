@@ -112,6 +112,34 @@ bool aligned16(std::initializer_list<const void *> ps) {
 int64_t stat_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : 4; }
 bool deterministic_policy() { return g_policy.load() == CTATTN_POLICY_DETERMINISTIC; }
 
+// Bytes of one storage element.
+int64_t elem_bytes(int dtype) { return dtype == CTATTN_F64 ? 8 : dtype == CTATTN_F32 ? 4 : 2; }
+
+// Head dims up to 128 without an MFMA kernel of their own (not 32, 64 or 128) run the MFMA
+// kernels of the next width on zero-padded copies of the tensors (attn_pad.hip), with the
+// scores scaled by 1 / sqrt(d) of the real head dim: that width, or 0 when d takes its own
+// MFMA kernels, is above 128, or the policy asks for the generic kernels.
+int64_t padded_width(int dtype, int64_t d) {
+    if (g_policy.load() == CTATTN_POLICY_GENERIC || d > 128) return 0;
+    const int64_t dp = d <= 32 ? 32 : d <= 64 ? 64 : 128;
+    if (dp == d) return 0;
+    const bool mfma = dtype == CTATTN_F64 ? ctattn::f64_mfma_supported(dp)
+                                          : ctattn::mfma_fwd_supported(dtype, dp) && ctattn::mfma_bwd_supported(dtype, dp);
+    return mfma ? dp : 0;
+}
+// The shape the MFMA kernels see for padded width dp.
+ctattn::AttnShape padded_shape(const ctattn::AttnShape &s, int64_t dp) {
+    ctattn::AttnShape sp = s;
+    sp.d = dp;
+    sp.scale_d = s.d;
+    return sp;
+}
+// Backward workspace of the padded path: the MFMA backward's own (delta and friends, for the
+// padded shape) followed by the eight padded copies q, k, v, o, dO, dQ, dK, dV.
+int64_t padded_copy_bytes(int dtype, const ctattn::AttnShape &s, int64_t dp) {
+    return align_up(s.rows() * dp * elem_bytes(dtype));
+}
+
 // ---- Scratch of ctattn_bwd_noalloc: the backward workspace (delta and friends) in a
 // file-scope device array instead of caller- or library-allocated memory.  Every GPU the
 // library runs on holds its own copy until the process ends; all calls on one GPU share it.
@@ -155,6 +183,71 @@ int scratch_for_stream(hipStream_t stream, void **out) {
     return 0;
 }
 
+// Stream-ordered memory for the forward's padded copies (ctattn_fwd takes no workspace): a
+// pool per device owned by the library, which keeps what it has allocated (release threshold
+// at its maximum) so that later calls reuse it without going back to the driver.
+std::mutex g_pool_mutex;
+hipMemPool_t g_pool[kMaxDevices] = {};
+
+int pool_for_stream(hipStream_t stream, hipMemPool_t *out) {
+    int dev = 0;
+    hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(e, "ctattn_fwd: cannot find the stream's device: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(hipErrorInvalidDevice, "ctattn_fwd: device %d beyond the %d supported", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    if (g_pool[dev] == nullptr) {
+        hipMemPoolProps props = {};
+        props.allocType = hipMemAllocationTypePinned;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = nullptr;
+        e = hipMemPoolCreate(&pool, &props);
+        if (e == hipSuccess) {
+            uint64_t keep = UINT64_MAX;
+            e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+            if (e != hipSuccess) (void)hipMemPoolDestroy(pool);
+        }
+        if (e != hipSuccess)
+            return fail(e, "ctattn_fwd: cannot create the memory pool of device %d: %s", dev, hipGetErrorString(e));
+        g_pool[dev] = pool;
+    }
+    *out = g_pool[dev];
+    return 0;
+}
+
+// ctattn_fwd for a head dim that runs on the MFMA kernels of width dp: q, k, v padded into
+// stream-ordered scratch, the kernels writing O into a padded buffer (LSE straight into the
+// caller's, whose layout does not depend on d), O copied back.
+int fwd_padded(int dtype, int64_t dp, const void *q, const void *k, const void *v, void *o, void *lse,
+               const ctattn::AttnShape &s, hipStream_t st) {
+    const int eb = int(elem_bytes(dtype));
+    const int64_t rows = s.rows();
+    const int64_t tb = padded_copy_bytes(dtype, s, dp);
+    hipMemPool_t pool = nullptr;
+    if (int rc = pool_for_stream(st, &pool)) return rc;
+    void *buf = nullptr;
+    hipError_t e = hipMallocFromPoolAsync(&buf, size_t(4 * tb), pool, st);
+    if (e != hipSuccess)
+        return fail(e, "ctattn_fwd: %lld bytes for the head dim %lld -> %lld copies: %s", (long long)(4 * tb),
+                    (long long)s.d, (long long)dp, hipGetErrorString(e));
+    char *p = static_cast<char *>(buf);
+    void *qp = p, *kp = p + tb, *vp = p + 2 * tb, *op = p + 3 * tb;
+    const ctattn::AttnShape sp = padded_shape(s, dp);
+    const int d = int(s.d), w = int(dp);
+    const void *in[3] = {q, k, v};
+    void *padded[3] = {qp, kp, vp};
+    e = ctattn::launch_pad_rows(eb, in, padded, 3, rows, d, w, st);
+    if (e == hipSuccess)
+        e = dtype == CTATTN_F64 ? ctattn::launch_f64_fwd(qp, kp, vp, op, lse, sp, st)
+                                : ctattn::launch_mfma_fwd(dtype, qp, kp, vp, op, static_cast<float *>(lse), sp, st);
+    const void *po[1] = {op};
+    void *oo[1] = {o};
+    if (e == hipSuccess) e = ctattn::launch_unpad_rows(eb, po, oo, 1, rows, d, w, st);
+    const hipError_t ef = hipFreeAsync(buf, st);  // after every use of buf on the stream
+    return finish("ctattn_fwd", e != hipSuccess ? e : ef, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -167,6 +260,7 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
     if (!q || !k || !v || !o)
         return fail(hipErrorInvalidValue, "ctattn_fwd: null q/k/v/o pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (const int64_t dp = padded_width(dtype, d)) return fwd_padded(dtype, dp, q, k, v, o, lse, s, st);
     const bool al = aligned16({q, k, v, o, lse});
     hipError_t e = use_mfma_fwd(dtype, d) && al ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
                    : use_f64_mfma(dtype, d) && al ? ctattn::launch_f64_fwd(q, k, v, o, lse, s, st)
@@ -180,8 +274,14 @@ int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, i
     const ctattn::AttnShape s{B, H, T, d, causal != 0};
     // delta = rowsum(dO * O), [B, H, T] (fp64 for fp64 storage, else fp32), always first.
     int64_t bytes = align_up(s.rows() * stat_bytes(dtype));
-    if (use_mfma_bwd(dtype, d))
+    if (const int64_t dp = padded_width(dtype, d)) {
+        // Then the MFMA backward's scratch for the padded shape and the eight padded copies.
+        if (dtype != CTATTN_F64)
+            bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, padded_shape(s, dp), deterministic_policy()));
+        bytes += 8 * padded_copy_bytes(dtype, s, dp);
+    } else if (use_mfma_bwd(dtype, d)) {
         bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s, deterministic_policy()));
+    }
     ok();
     return bytes;
 }
@@ -206,7 +306,33 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
     // Misaligned tensors take the generic kernels, whose workspace (delta only) is a prefix of
     // what ctattn_bwd_workspace_bytes asked for.
     const bool al = aligned16({q, k, v, o, dout, lse, dq, dk, dv, workspace});
-    if (use_mfma_bwd(dtype, d) && al) {
+    const int64_t dp = padded_width(dtype, d);
+    if (dp != 0 && aligned16({workspace})) {
+        // Head dim d on the MFMA kernels of width dp: the workspace holds delta, the padded
+        // shape's MFMA scratch, then the padded q, k, v, o, dO (inputs) and dQ, dK, dV.
+        const ctattn::AttnShape sp = padded_shape(s, dp);
+        const int eb = int(elem_bytes(dtype));
+        const int64_t rows = s.rows(), tb = padded_copy_bytes(dtype, s, dp);
+        char *w = static_cast<char *>(workspace);
+        void *delta = w;
+        w += align_up(rows * stat_bytes(dtype));
+        void *extra = w;
+        if (dtype != CTATTN_F64) w += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, sp, deterministic_policy()));
+        void *cp[8];
+        for (int i = 0; i < 8; ++i) cp[i] = w + i * tb;
+        const void *in[5] = {q, k, v, o, dout};
+        const int di = int(d), wi = int(dp);
+        e = ctattn::launch_pad_rows(eb, in, cp, 5, rows, di, wi, st);
+        if (e == hipSuccess)
+            e = dtype == CTATTN_F64
+                    ? ctattn::launch_f64_bwd(cp[0], cp[1], cp[2], cp[3], cp[4], lse, delta, cp[5], cp[6], cp[7], sp, st)
+                    : ctattn::launch_mfma_bwd(dtype, cp[0], cp[1], cp[2], cp[3], cp[4], static_cast<const float *>(lse),
+                                              static_cast<float *>(delta), cp[5], cp[6], cp[7], extra,
+                                              deterministic_policy(), sp, st);
+        const void *grads[3] = {cp[5], cp[6], cp[7]};
+        void *out[3] = {dq, dk, dv};
+        if (e == hipSuccess) e = ctattn::launch_unpad_rows(eb, grads, out, 3, rows, di, wi, st);
+    } else if (use_mfma_bwd(dtype, d) && al) {
         void *extra = static_cast<char *>(workspace) + align_up(s.rows() * stat_bytes(dtype));
         e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, static_cast<const float *>(lse),
                                     static_cast<float *>(workspace), dq, dk, dv, extra, deterministic_policy(), s,

@@ -23,10 +23,16 @@
  *   - supported: dtype f32, bf16 or f16 (storage; arithmetic accumulates in fp32) or f64
  *     (arithmetic in fp64, the reference's ComputeType<double>), 1 <= d <= 256, T >= 0,
  *     B, H >= 0.  d in {32, 64, 128} runs on the MFMA kernels (fp32 on f32 MFMA, bf16 and
- *     f16 on 16-bit MFMA with fp32 accumulation, f64 on f64 MFMA); every other head dim on
- *     the generic kernels.  Tensors must be element-aligned; the MFMA kernels also need
- *     16-byte-aligned q, k, v, o, lse (and dout, dq, dk, dv, workspace in the backward); calls
- *     whose pointers are not take the generic kernels (same results, slower).
+ *     f16 on 16-bit MFMA with fp32 accumulation, f64 on f64 MFMA).  Every other d <= 128
+ *     runs on the MFMA kernels of the next width (32, 64 or 128) over zero-padded copies of
+ *     the tensors, still scaled by 1/sqrt(d) (zero columns add nothing to a score; the
+ *     padded columns of the outputs are dropped): the backward keeps the copies in its
+ *     workspace, the forward takes them from a stream-ordered memory pool the library owns
+ *     per device (hipMallocFromPoolAsync / hipFreeAsync on `stream`).  d above 128 runs on
+ *     the generic kernels.  Tensors must be element-aligned; the MFMA kernels at d in
+ *     {32, 64, 128} also need 16-byte-aligned q, k, v, o, lse (and dout, dq, dk, dv,
+ *     workspace in the backward); calls whose pointers are not take the generic kernels
+ *     (same results, slower).
  */
 #ifndef CTATTN_H
 #define CTATTN_H
@@ -61,9 +67,10 @@ enum ctattn_dtype {
  *                  dQ contributions of different key blocks with fp32 atomics, so an fp32
  *                  dQ may differ between runs in the last bits; dK, dV, O and LSE do not,
  *                  and the bf16 MFMA backward uses no atomics (bitwise reproducible).
- *   GENERIC        the generic kernels only (used to cross-check the two paths); the linear
- *                  layers' plain GEMMs (ctattn_linear_*, ctattn_tensor_matmul) then run on the
- *                  library's own GEMM kernels instead of hipBLASLt.
+ *   GENERIC        the generic kernels only, at every head dim (used to cross-check the
+ *                  paths); the linear layers' plain GEMMs (ctattn_linear_*,
+ *                  ctattn_tensor_matmul) then run on the library's own GEMM kernels instead
+ *                  of hipBLASLt.
  *   DETERMINISTIC  MFMA kernels without atomics, bitwise-reproducible gradients.  The fp32
  *                  backward stores dQ partials per 128-key block and sums them in a fixed
  *                  order while T <= 1024 (workspace: ceil(T/128) * B*H*T*d fp32 more than
@@ -92,6 +99,8 @@ CTATTN_API int ctattn_fwd(int dtype, const void *q, const void *k, const void *v
  * Bytes of device workspace ctattn_bwd needs for this problem (>= 0), or -1 on invalid
  * arguments.  Replaces nothing in the reference: its backward zero-fills and atomically
  * accumulates straight into dq/dk/dv (FlashAttentionLayer.cu:103-106, flash_attention.cu:317-321).
+ * A head dim that runs padded to width dp (see the conventions above) also needs room for
+ * the eight padded copies (q, k, v, o, dout, dq, dk, dv: 8 * B*H*T*dp elements).
  */
 CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal);

@@ -132,6 +132,30 @@ def test_policy_roundtrip(lib):
         _capi.set_policy(5)
 
 
+def test_padded_head_dim_workspace(lib):
+    """A head dim without its own MFMA kernel (d <= 128, not 32 / 64 / 128) runs padded to the
+    next width: the backward workspace holds delta, the padded shape's MFMA scratch and eight
+    padded copies (q, k, v, o, dO, dQ, dK, dV); d = 64 needs delta only (fp32, AUTO), and a
+    head dim above 128 (generic kernels) as well."""
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    b, h, t = 2, 3, 150
+    rows = b * h * t
+    assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, 64, 1) == al(rows * 4)
+    for d, dp, eb, dtype in [(80, 128, 4, 0), (48, 64, 2, 1), (20, 32, 2, 2), (100, 128, 8, 3)]:
+        stat = 8 if dtype == 3 else 4
+        extra = al(rows * 4) if dtype in (1, 2) else 0  # bf16 / fp16: -LSE log2(e) per row
+        want = al(rows * stat) + extra + 8 * al(rows * dp * eb)
+        assert lib.ctattn_bwd_workspace_bytes(dtype, b, h, t, d, 1) == want, (d, dtype)
+    assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, 160, 1) == al(rows * 4)
+    prev = _capi.set_policy(_capi.POLICY_GENERIC)
+    try:
+        assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, 80, 1) == al(rows * 4)
+    finally:
+        _capi.set_policy(prev)
+
+
 def test_deterministic_workspace_stays_linear(lib):
     """DETERMINISTIC fp32: dQ partials per 128-key block (one fp32 [B, H, T, d] plane each)
     while T <= 1024, none beyond (the query-major dQ kernel), so the workspace is at most

@@ -89,9 +89,14 @@ def test_flash_attn_capi_matches_oracle(shape, causal, dtype):
     dq, dk, dv = ct.flash_attn_bwd(tq, tk, tv, o, tdo, lse, causal)
     torch.cuda.synchronize()
     rel = F64_REL if dtype == torch.float64 else F16_REL
+    # dQ and dK vanish in exact arithmetic where a row sees one key (T = 1); the fp16 MFMA
+    # backward (its dP accumulator starts from -delta) leaves a few ulps there, so their scale
+    # falls back to 1e-4 of the dV scale, as in the native-head-dim parity tests.
+    dv_scale = float(np.max(np.abs(want["dv"])))
     for key, t in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv)):
         assert t.dtype == (lse.dtype if key == "lse" else dtype)
-        rel_check(host(t), want[key], rel, f"{name} {key}")
+        floor = 1e-4 * dv_scale if key in ("dq", "dk") else 1e-30
+        rel_check(host(t), want[key], rel, f"{name} {key}", floor=floor)
 
 
 @pytest.mark.gpu

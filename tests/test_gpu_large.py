@@ -75,15 +75,20 @@ def test_more_than_2_31_elements_mfma(dtype):
 
 
 def test_more_than_2_26_rows_generic():
-    """d = 8 runs on the generic kernels; B (2^22 + 3) H1 T16 is 2^26 + 48 rows, past the
-    2^32 work-items one row-per-wave launch could hold."""
+    """The generic kernels (POLICY_GENERIC; d = 8 would otherwise run padded on the MFMA
+    kernels) at B (2^22 + 3) H1 T16 = 2^26 + 48 rows, past the 2^32 work-items one
+    row-per-wave launch could hold."""
     shape = ((1 << 22) + 3, 1, 16, 8)
     rows = shape[0] * shape[1] * shape[2]
     assert rows * 64 > 2 ** 32
     say(f"large generic problem {shape}")
-    for causal in (True, False):
-        t = run_big(shape, causal, torch.float32, 1.0, seed=72)
-        check_slices(t, causal, [(0, 0), (shape[0] - 1, 0), (shape[0] // 3, 0)], torch.float32,
-                     f"{shape} causal={causal}")
-        del t
+    prev = ct.set_policy(ct.POLICY_GENERIC)
+    try:
+        for causal in (True, False):
+            t = run_big(shape, causal, torch.float32, 1.0, seed=72)
+            check_slices(t, causal, [(0, 0), (shape[0] - 1, 0), (shape[0] // 3, 0)], torch.float32,
+                         f"{shape} causal={causal}")
+            del t
+    finally:
+        ct.set_policy(prev)
     torch.cuda.empty_cache()
