@@ -184,8 +184,10 @@ int scratch_for_stream(hipStream_t stream, void **out) {
 }
 
 // Stream-ordered memory for the forward's padded copies (ctattn_fwd takes no workspace): a
-// pool per device owned by the library, which keeps what it has allocated (release threshold
-// at its maximum) so that later calls reuse it without going back to the driver.
+// pool per device owned by the library.  Up to kPoolKeepBytes of freed memory stay in the
+// pool across synchronisations, so later calls reuse it without going back to the driver;
+// beyond that (very large problems) the pool returns memory at the next synchronisation.
+constexpr uint64_t kPoolKeepBytes = uint64_t(1) << 30;
 std::mutex g_pool_mutex;
 hipMemPool_t g_pool[kMaxDevices] = {};
 
@@ -204,7 +206,7 @@ int pool_for_stream(hipStream_t stream, hipMemPool_t *out) {
         hipMemPool_t pool = nullptr;
         e = hipMemPoolCreate(&pool, &props);
         if (e == hipSuccess) {
-            uint64_t keep = UINT64_MAX;
+            uint64_t keep = kPoolKeepBytes;
             e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
             if (e != hipSuccess) (void)hipMemPoolDestroy(pool);
         }
