@@ -69,6 +69,24 @@ def test_float_layer_matches_oracle(causal, save_states):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("head_dim", [40, 80, 96])
+def test_float_layer_padded_head_dims(head_dim):
+    """Head dims without their own MFMA kernel run padded on the next width; through the C++
+    layer (which sizes the backward workspace with ctattn_bwd_workspace_bytes) as through the
+    C-ABI."""
+    shape = (2, 3, 130, head_dim)
+    q, k, v, do = ora.make_inputs(shape, seed=53 + head_dim)
+    layer = ctm.FlashAttention(head_dim, 3, True)
+    tq, tk, tv, tdo = _tensors(ctm.FloatTensor, q, k, v, do)
+    o = layer.computeAttention(tq, tk, tv, True)
+    dq, dk, dv = layer.computeBackward(tq, tk, tv, tdo)
+    want = ora.attention_fwd_bwd(q, k, v, do, True)
+    for key, val in {"o": o.numpy(), "dq": dq.numpy(), "dk": dk.numpy(), "dv": dv.numpy()}.items():
+        assert val.shape == shape
+        assert np.max(np.abs(val - want[key])) <= 1e-4, key
+
+
+@pytest.mark.gpu
 def test_bfloat_layer_matches_oracle():
     shape = (1, 2, 150, 64)
     q, k, v, do = ora.make_inputs(shape, seed=52, std=0.5, dtype="bf16")
