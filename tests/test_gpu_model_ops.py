@@ -59,7 +59,10 @@ def _stat_tol(dtype):
 
 # ---- linear --------------------------------------------------------------------------------
 
-LINEAR_SHAPES = [(1, 1, 1), (37, 130, 65), (256, 384, 384), (300, 65, 1536), (64, 4, 8)]
+# (100, 96, 256): rows that no tile divides; (384, 128, 256): every product on the fast load
+# path; (2048, 64, 96): a weight gradient split over many K ranges.
+LINEAR_SHAPES = [(1, 1, 1), (37, 130, 65), (256, 384, 384), (300, 65, 1536), (64, 4, 8), (100, 96, 256),
+                 (384, 128, 256), (2048, 64, 96)]
 
 
 @pytest.fixture(params=[_capi.POLICY_AUTO, _capi.POLICY_GENERIC], ids=["blaslt", "own_gemm"])
