@@ -46,6 +46,34 @@ namespace {
 using namespace bf16tile;
 
 // ---------------------------------------------------------------------------------------
+// dS tiles (d = 128): the dK/dV kernel stores the bf16 dS it computes, and the dQ kernel
+// reads it back instead of recomputing S and dP.
+// ---------------------------------------------------------------------------------------
+// One 32-row x 32-key tile of dS, 2 KiB, laid out as the LDS tile Tile<32> of a [key][32]
+// matrix whose columns hold the tile's query rows in the accumulator order: column
+// 16 kk + 8 h + e is row 16 kk + 8 (e / 4) + 4 h + e % 4 (e < 8).
+// Copied byte for byte into LDS, its transposed reads (read_col<32>) are the A operands of
+// dQ += dS K, in the key order read_col gives the K operands.  Tiles of a (batch, head) are
+// packed by (row tile rt, key tile kt): rt (rt + 1) / 2 + kt with kt <= rt when causal,
+// rt * NT + kt otherwise (NT = ceil(T / 32)).
+constexpr int kDsTileElems = 32 * 32;
+
+__device__ __host__ inline int64_t ds_tiles_per_head(int64_t T, bool causal) {
+    const int64_t nt = (T + 31) / 32;
+    return causal ? nt * (nt + 1) / 2 : nt * nt;
+}
+__device__ __forceinline__ int64_t ds_tile_index(int bh, int rt, int kt, int T, int causal) {
+    const int64_t nt = (T + 31) / 32;
+    return int64_t(bh) * ds_tiles_per_head(T, causal != 0) +
+           (causal ? int64_t(rt) * (rt + 1) / 2 + kt : int64_t(rt) * nt + kt);
+}
+// Query row of DsTile column c.
+__device__ __forceinline__ int ds_col_row(int c) {
+    const int e = c & 7;
+    return (c & 16) + 8 * (e >> 2) + ((c >> 1) & 4) + (e & 3);
+}
+
+// ---------------------------------------------------------------------------------------
 // dK / dV (key-major)
 // ---------------------------------------------------------------------------------------
 template <int D>
@@ -76,10 +104,11 @@ struct KvCfg {
 //   ak   : row_base of this wave's first key in the K tile (V at + KV_BYTES)
 //   ac0/1: col_base of the wave's Q rows (dO at + Q_BYTES)
 //   anl  : address of nl2[32 rs + 4 half] of the block (delta at + BM * 4)
-template <int D, bool MASK, typename F>
+//   dsw  : when DS, where the tile's dS goes (a 32 x 32 DsTile, rows = keys)
+template <int D, bool MASK, bool DS, typename F>
 __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&dv_acc)[D / 32], uint32_t aq,
                                          uint32_t ak, uint32_t ac0, uint32_t ac1, uint32_t anl, int r0w,
-                                         int key, int T, int causal, float c, int half) {
+                                         int key, int T, int causal, float c, int half, uint16_t *dsw) {
     using C = KvCfg<D>;
     using V = typename F::vec;
     // dP starts from -delta of the rows (register r: row acc_row(r, half)), so the
@@ -129,6 +158,20 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
             dsb[r / 8][r % 8] = (typename F::elem)(p * dp[r]);
         }
     }
+    if (DS) {
+        // The tile's dS for the dQ kernel: lane (key, half) holds, in dsb[kk], the 8 rows of
+        // logical chunk 2 kk + half of the key's DsTile row.
+        const int key_l = __lane_id() & 31;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            u16x8 *dst = reinterpret_cast<u16x8 *>(reinterpret_cast<char *>(dsw) + Tile<32>::off(key_l, 2 * kk + half));
+#ifdef CTATTN_DS_NT
+            __builtin_nontemporal_store(__builtin_bit_cast(u16x8, dsb[kk]), dst);
+#else
+            *dst = __builtin_bit_cast(u16x8, dsb[kk]);
+#endif
+        }
+    }
     // dV^T += dO^T P, dK^T += Q^T dS over the tile's 32 rows (two k-steps of 16).
     {
         constexpr int NS = 2 * C::DT;
@@ -151,12 +194,12 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
     }
 }
 
-template <int D, typename F>
+template <int D, bool DS, typename F>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_bf16_dkdv_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const uint16_t *__restrict__ dout, const float *__restrict__ nl2, const float *__restrict__ delta,
-    uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, int T, int BH, int causal, float c,
-    float inv_sqrt_d) {
+    uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, uint16_t *__restrict__ ds, int T, int BH, int causal,
+    float c, float inv_sqrt_d) {
     using C = KvCfg<D>;
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
     const uint32_t L = lds_addr(smem);
@@ -210,23 +253,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
 
     if (qb_first < nqb) issue(qb_first * C::BM, 0);
+    bool stored = false;  // DS: this wave stored a dS tile (two stores) after its last loads
     for (int qb = qb_first; qb < nqb; ++qb) {
         const int buf = (qb - qb_first) & 1;
-        // This wave's loads of `buf` have landed (vmcnt = 0); after the barrier every wave's
-        // have, and every wave is done reading buf ^ 1.
-        __builtin_amdgcn_s_waitcnt(0xF70);
-        __syncthreads();
+        // This wave's loads of `buf` have landed; after the barrier every wave's have, and
+        // every wave is done reading buf ^ 1.  The dS stores of the previous block, issued
+        // after those loads, may stay in flight (vmcnt counts in issue order): nothing in this
+        // kernel reads them.
+        if (DS) {
+            if (stored) __builtin_amdgcn_s_waitcnt(0xF72);  // vmcnt(2)
+            else __builtin_amdgcn_s_waitcnt(0xF70);
+            lds_barrier();
+        } else {
+            __builtin_amdgcn_s_waitcnt(0xF70);
+            __syncthreads();
+        }
         if (qb + 1 < nqb) issue((qb + 1) * C::BM, buf ^ 1);
         const int r0w = qb * C::BM + 32 * rs;
         const bool active = kw0 < T && r0w < T && (!causal || kw0 <= r0w + 31);
+        stored = DS && active;
         if (!active) continue;
         const uint32_t qt = L + C::Q_OFF + uint32_t(buf * 2 * C::Q_BYTES);
         const uint32_t anl = L + C::S_OFF + uint32_t(buf * 2 * C::BM * 4) + rnl;
         const bool masked = (r0w + 32 > T) || (kw0 + 32 > T) || (causal && kw0 + 31 > r0w);
+        uint16_t *dsw = DS ? ds + ds_tile_index(bh, r0w / 32, kw0 / 32, T, causal) * kDsTileElems : nullptr;
         if (masked)
-            kv_block<D, true, F>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
+            kv_block<D, true, DS, F>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c,
+                                     half, dsw);
         else
-            kv_block<D, false, F>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c, half);
+            kv_block<D, false, DS, F>(dk_acc, dv_acc, qt + rq, ak, qt + cq0, qt + cq1, anl, r0w, key, T, causal, c,
+                                      half, dsw);
     }
 
     // Row slice 1 hands its dK^T / dV^T sums to row slice 0 through LDS (no load is in flight
@@ -438,6 +494,133 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// dQ from stored dS (d = 128)
+// ---------------------------------------------------------------------------------------
+// dQ = dS K / sqrt(d) from the dS tiles the dK/dV kernel stored: no recompute of S or dP.  A
+// workgroup of 8 waves owns 256 query rows (wave w: row tile r0 / 32 + w) and walks 64-key
+// blocks: the block's K rows (a Tile<D>) and each wave's two dS tiles go global -> LDS
+// directly, three blocks in flight; dS^T columns (read_col<32>) are the A operands, K^T columns
+// (read_col<D>) the B operands, both in the same key order.  Bound by the dS stream from HBM.
+template <int D>
+struct DqDsCfg {
+    static constexpr int NW = 8;
+    static constexpr int BM = 32 * NW;        // query rows per workgroup
+    static constexpr int BN = 64;             // keys per iteration: key tiles 2 kb, 2 kb + 1
+    static constexpr int DT = D / 32;
+    static constexpr int ROW = 2 * D;
+    static constexpr int D8 = D / 8;          // 16-byte chunks per row
+    static constexpr int KB = BN * ROW;       // K tile
+    static constexpr int SB = NW * 2 * 2048;  // the waves' dS tiles
+    static constexpr int BUF = KB + SB;
+    static constexpr int STAGES = 3;          // blocks kb + 1 and kb + 2 load during block kb
+    static constexpr int LDS_BYTES = STAGES * BUF;
+};
+
+// 2 KiB global -> LDS (one wave): lane l moves bytes 16 l and 1024 + 16 l.
+__device__ __forceinline__ void dma_2k(const uint16_t *src, uint32_t dst, int lane) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const char *g = reinterpret_cast<const char *>(src) + h * 1024 + 16 * lane;
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+                     "s"(__builtin_amdgcn_readfirstlane(dst + uint32_t(h * 1024)))
+                     : "memory", "m0");
+    }
+}
+
+template <int D, typename F>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_bf16_dq_ds_kernel(
+    const uint16_t *__restrict__ k, const uint16_t *__restrict__ ds, uint16_t *__restrict__ dq, int T, int BH,
+    int causal, float inv_sqrt_d) {
+    using C = DqDsCfg<D>;
+    using V = typename F::vec;
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+    const uint32_t L = lds_addr(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    const int qb = causal ? (nqb - 1 - id / BH) : id / BH;  // causal: longest first
+    const int64_t base = int64_t(bh) * T * D;
+    const int r0 = qb * C::BM;
+    const int nt = (T + 31) / 32;
+    const int rt = r0 / 32 + wave;  // this wave's row tile
+    // Key tiles [0, wave_nkt) of this wave (none when its rows are past T).
+    const int wave_nkt = rt >= nt ? 0 : causal ? rt + 1 : nt;
+    const int kend = causal ? min(T, r0 + C::BM) : T;
+    const int nkb = (kend + C::BN - 1) / C::BN;
+
+    floatx16 dq_acc[C::DT];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) dq_acc[dt] = zero16();
+    const uint32_t ck0 = col_base<D>(0, 0, 0, lane), ck1 = col_base<D>(0, 0, 1, lane);
+    const uint32_t cs0 = col_base<32>(0, 0, 0, lane), cs1 = col_base<32>(0, 0, 1, lane);
+
+    auto issue = [&](int kb, int buf) {
+        char *b = smem + buf * C::BUF;
+        load_tile_dma<D, C::BN, C::NW>(b, k + base + int64_t(kb) * C::BN * D, T - kb * C::BN, wave, lane);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int kt = 2 * kb + tt;
+            if (kt < wave_nkt)
+                dma_2k(ds + ds_tile_index(bh, rt, kt, T, causal) * kDsTileElems,
+                       lds_addr(b + C::KB + (wave * 2 + tt) * 2048), lane);
+        }
+    };
+    // Loads this wave issues for block kb: the K tile's share (load_tile_dma: 2 per wave) and
+    // two per live dS tile.  The wait before block kb lets block kb + 1's stay in flight
+    // (vmcnt counts in issue order).
+    auto wave_loads = [&](int kb) {
+        return kb >= nkb ? 0 : 2 + 2 * (int(2 * kb < wave_nkt) + int(2 * kb + 1 < wave_nkt));
+    };
+    static_assert(C::BN * C::D8 / (C::NW * kWave) == 2, "K tile loads per wave");
+    if (nkb > 0) issue(0, 0);
+    if (nkb > 1) issue(1, 1);
+    int buf = 0;
+    for (int kb = 0; kb < nkb; ++kb) {
+        switch (wave_loads(kb + 1)) {
+            case 0: __builtin_amdgcn_s_waitcnt(0xF70); break;
+            case 2: __builtin_amdgcn_s_waitcnt(0xF72); break;
+            case 4: __builtin_amdgcn_s_waitcnt(0xF74); break;
+            default: __builtin_amdgcn_s_waitcnt(0xF76); break;
+        }
+        lds_barrier();
+        if (kb + 2 < nkb) issue(kb + 2, buf == 0 ? 2 : buf - 1);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            if (2 * kb + tt >= wave_nkt) continue;
+            const uint32_t ka = L + uint32_t(buf * C::BUF + tt * 32 * C::ROW);
+            const uint32_t sa = L + uint32_t(buf * C::BUF + C::KB + (wave * 2 + tt) * 2048);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const V a = read_col<32, V>(sa + cs0, sa + cs1, kk, 0);
+#pragma unroll
+                for (int dt = 0; dt < C::DT; ++dt)
+                    dq_acc[dt] = F::mfma(a, read_col<D, V>(ka + ck0, ka + ck1, kk, dt), dq_acc[dt]);
+            }
+        }
+        buf = buf == 2 ? 0 : buf + 1;
+    }
+
+    // dq_acc[dt]: lane (col, half), register r -> dS column acc_row(r, half) of the tile, i.e.
+    // query row 32 rt + ds_col_row(acc_row(r, half)); d = 32 dt + col.
+    if (wave_nkt == 0) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 32 * rt + ds_col_row(acc_row(r, half));
+        if (row >= T) continue;
+        uint16_t *p = dq + base + int64_t(row) * D + col;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) p[32 * dt] = F::bits(dq_acc[dt][r] * inv_sqrt_d);
+    }
+}
+
 // delta[row] = -sum_c dO[row][c] O[row][c] from bf16 (the negated delta of
 // flash_attention.cu:269-273: the dP accumulators of both kernels start from it) and
 // nl2[row] = -LSE[row] * log2(e), the per-row term of P = exp2(S log2(e)/sqrt(d) + nl2).
@@ -472,7 +655,7 @@ __global__ __launch_bounds__(256) void bwd_preprocess_bf16_kernel(const uint16_t
 
 template <int D, typename F>
 hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, const void *dout,
-                    const float *lse, float *delta, void *dq, void *dk, void *dv, float *nl2,
+                    const float *lse, float *delta, void *dq, void *dk, void *dv, float *nl2, uint16_t *ds,
                     const AttnShape &s, hipStream_t stream) {
     using KC = KvCfg<D>;
     using QC = QCfg<D>;
@@ -489,9 +672,24 @@ hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, 
     if (e != hipSuccess) return e;
     const float c = kLog2e / sqrtf(float(s.scale_dim()));
     const float inv_sqrt_d = 1.f / sqrtf(float(s.scale_dim()));
-    hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D, F>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0, stream,
-                       u16(q), u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dk),
-                       static_cast<uint16_t *>(dv), int(s.T), int(s.bh()), int(s.causal), c, inv_sqrt_d);
+    if constexpr (D == 128) {
+        if (ds != nullptr) {
+            // dS through the workspace: the dK/dV kernel stores it, the dQ kernel multiplies it by K.
+            hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D, true, F>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0,
+                               stream, u16(q), u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dk),
+                               static_cast<uint16_t *>(dv), ds, int(s.T), int(s.bh()), int(s.causal), c, inv_sqrt_d);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            using DC = DqDsCfg<D>;
+            const int64_t dq_blocks = ((s.T + DC::BM - 1) / DC::BM) * s.bh();
+            hipLaunchKernelGGL((bwd_bf16_dq_ds_kernel<D, F>), dim3(unsigned(dq_blocks)), dim3(DC::NW * kWave), 0, stream,
+                               u16(k), ds, static_cast<uint16_t *>(dq), int(s.T), int(s.bh()), int(s.causal), inv_sqrt_d);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((bwd_bf16_dkdv_kernel<D, false, F>), dim3(unsigned(kv_blocks)), dim3(KC::NW * kWave), 0,
+                       stream, u16(q), u16(k), u16(v), u16(dout), nl2, delta, static_cast<uint16_t *>(dk),
+                       static_cast<uint16_t *>(dv), nullptr, int(s.T), int(s.bh()), int(s.causal), c, inv_sqrt_d);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_bf16_dq_kernel<D, F>), dim3(unsigned(q_blocks)), dim3(QC::NW * kWave), 0, stream, u16(q),
@@ -502,32 +700,53 @@ hipError_t bwd_bf16(const void *q, const void *k, const void *v, const void *o, 
 
 }  // namespace
 
-int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic) {
-    (void)deterministic;  // both kernels are deterministic: no atomics, fixed summation order
-    return s.rows() * int64_t(sizeof(float));  // nl2
+namespace {
+// The dS tiles take the workspace only up to this size; longer problems recompute S and dP in
+// the dQ kernel instead (their workspace stays linear in rows).
+constexpr int64_t kDsMaxBytes = int64_t(4) << 30;
+int64_t nl2_bytes(const AttnShape &s) { return (s.rows() * int64_t(sizeof(float)) + 255) / 256 * 256; }
+}  // namespace
+
+int64_t bf16_ds_bytes(const AttnShape &s) {
+    if (s.d != 128) return 0;
+    const int64_t b = s.bh() * ds_tiles_per_head(s.T, s.causal) * kDsTileElems * int64_t(sizeof(uint16_t));
+    return b <= kDsMaxBytes ? b : 0;
+}
+
+int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic, bool with_ds) {
+    (void)deterministic;  // both paths are deterministic: no atomics, fixed summation order
+    return nl2_bytes(s) + (with_ds ? bf16_ds_bytes(s) : 0);
 }
 
 hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
-                           bool deterministic, const AttnShape &s, hipStream_t stream) {
+                           int64_t extra_bytes, bool deterministic, const AttnShape &s, hipStream_t stream) {
     (void)deterministic;
     float *nl2 = static_cast<float *>(extra);
+    const int64_t dsb = bf16_ds_bytes(s);
+    uint16_t *ds = dsb > 0 && extra_bytes >= nl2_bytes(s) + dsb
+                       ? reinterpret_cast<uint16_t *>(static_cast<char *>(extra) + nl2_bytes(s))
+                       : nullptr;
     switch (s.d) {
-        case 32: return bwd_bf16<32, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
-        case 64: return bwd_bf16<64, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
-        case 128: return bwd_bf16<128, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 32: return bwd_bf16<32, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, nullptr, s, stream);
+        case 64: return bwd_bf16<64, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, nullptr, s, stream);
+        case 128: return bwd_bf16<128, Bf16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, ds, s, stream);
         default: return hipErrorNotSupported;
     }
 }
 
 hipError_t launch_f16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                           const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
-                          const AttnShape &s, hipStream_t stream) {
+                          int64_t extra_bytes, const AttnShape &s, hipStream_t stream) {
     float *nl2 = static_cast<float *>(extra);
+    const int64_t dsb = bf16_ds_bytes(s);
+    uint16_t *ds = dsb > 0 && extra_bytes >= nl2_bytes(s) + dsb
+                       ? reinterpret_cast<uint16_t *>(static_cast<char *>(extra) + nl2_bytes(s))
+                       : nullptr;
     switch (s.d) {
-        case 32: return bwd_bf16<32, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
-        case 64: return bwd_bf16<64, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
-        case 128: return bwd_bf16<128, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, s, stream);
+        case 32: return bwd_bf16<32, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, nullptr, s, stream);
+        case 64: return bwd_bf16<64, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, nullptr, s, stream);
+        case 128: return bwd_bf16<128, F16Fmt>(q, k, v, o, dout, lse, delta, dq, dk, dv, nl2, ds, s, stream);
         default: return hipErrorNotSupported;
     }
 }

@@ -533,19 +533,20 @@ bool mfma_bwd_supported(int dtype, int64_t d) {
     return d == 32 || d == 64 || d == 128;
 }
 
-int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic) {
-    if (dtype == 1 || dtype == 2) return bf16_bwd_workspace_bytes(s, deterministic);
+int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic, bool with_ds) {
+    if (dtype == 1 || dtype == 2) return bf16_bwd_workspace_bytes(s, deterministic, with_ds);
     if (!deterministic || deterministic_mode(s) != DqMode::Partial) return 0;  // fp32: delta only
     return (s.T + kPartialBN - 1) / kPartialBN * s.rows() * s.d * int64_t(sizeof(float));  // <= 8 dQ planes
 }
 
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
                            const void *o, const void *dout, const float *lse, float *delta,
-                           void *dq, void *dk, void *dv, void *extra, bool deterministic,
-                           const AttnShape &s, hipStream_t stream) {
+                           void *dq, void *dk, void *dv, void *extra, int64_t extra_bytes,
+                           bool deterministic, const AttnShape &s, hipStream_t stream) {
     if (dtype == 1)
-        return launch_bf16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, deterministic, s, stream);
-    if (dtype == 2) return launch_f16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, s, stream);
+        return launch_bf16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, extra_bytes, deterministic, s,
+                               stream);
+    if (dtype == 2) return launch_f16_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, extra, extra_bytes, s, stream);
     const DqMode mode = deterministic ? deterministic_mode(s) : DqMode::Atomic;
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };

@@ -53,19 +53,25 @@ hipError_t launch_mfma_fwd(int dtype, const void *q, const void *k, const void *
 hipError_t launch_bf16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
                            const AttnShape &s, hipStream_t stream);
 // bf16 backward on bf16 MFMA (d in {32, 64, 128}); called by launch_mfma_bwd for dtype 1.
-// Scratch: -LSE log2(e) per row, [B, H, T] fp32.
-int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic);
+// Scratch: -LSE log2(e) per row, [B, H, T] fp32 (256-byte aligned size), then at d = 128,
+// with_ds, the bf16 dS tiles (bf16_ds_bytes: causal about B H T^2 bytes, at most 4 GiB, 0
+// beyond).  Given a scratch of extra_bytes, the launch stores and reuses dS when it fits and
+// recomputes S and dP in the dQ kernel otherwise.
+int64_t bf16_ds_bytes(const AttnShape &s);
+int64_t bf16_bwd_workspace_bytes(const AttnShape &s, bool deterministic, bool with_ds);
 // fp16 forward / backward: the bf16 kernels instantiated for IEEE fp16 (fp16 MFMA), same
 // workspace as bf16.
 hipError_t launch_f16_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
                           const AttnShape &s, hipStream_t stream);
 hipError_t launch_f16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                           const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
-                          const AttnShape &s, hipStream_t stream);
+                          int64_t extra_bytes, const AttnShape &s, hipStream_t stream);
 hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
-                           bool deterministic, const AttnShape &s, hipStream_t stream);
-int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic);
+                           int64_t extra_bytes, bool deterministic, const AttnShape &s, hipStream_t stream);
+// Scratch of launch_mfma_bwd beyond delta; with_ds = false gives the smallest that works (the
+// bf16 / fp16 dS tiles left out).
+int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic, bool with_ds = true);
 // ---- fp64 kernels on fp64 MFMA (attn_f64_mfma.hip), d in {32, 64, 128}; lse and delta fp64.
 // The backward runs its own preprocess into `delta` ([B, H, T] fp64) and needs no other
 // scratch; dq, dk, dv are written, not accumulated. ----
@@ -112,7 +118,7 @@ hipError_t launch_unpad_rows(int elem_bytes, const void *const *in, void *const 
 // query-major kernel, dK / dV from the 128-key kernel (bitwise reproducible).
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
                            const void *o, const void *dout, const float *lse, float *delta,
-                           void *dq, void *dk, void *dv, void *extra, bool deterministic,
-                           const AttnShape &s, hipStream_t stream);
+                           void *dq, void *dk, void *dv, void *extra, int64_t extra_bytes,
+                           bool deterministic, const AttnShape &s, hipStream_t stream);
 
 }  // namespace ctattn

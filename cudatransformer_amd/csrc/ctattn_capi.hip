@@ -183,6 +183,22 @@ int scratch_for_stream(hipStream_t stream, void **out) {
     return 0;
 }
 
+// Backward workspace bytes: delta = rowsum(dO * O), [B, H, T] (fp64 for fp64 storage, else
+// fp32), always first; then the MFMA backward's scratch (with_ds: including the bf16 / fp16 dS
+// tiles, which a smaller workspace leaves out); for a padded head dim, the padded shape's
+// scratch and the eight padded copies.
+int64_t bwd_workspace_bytes(int dtype, const ctattn::AttnShape &s, bool with_ds) {
+    int64_t bytes = align_up(s.rows() * stat_bytes(dtype));
+    if (const int64_t dp = padded_width(dtype, s.d)) {
+        if (dtype != CTATTN_F64)
+            bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, padded_shape(s, dp), deterministic_policy(), with_ds));
+        bytes += 8 * padded_copy_bytes(dtype, s, dp);
+    } else if (use_mfma_bwd(dtype, s.d)) {
+        bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s, deterministic_policy(), with_ds));
+    }
+    return bytes;
+}
+
 // Stream-ordered memory for the forward's padded copies (ctattn_fwd takes no workspace): a
 // pool per device owned by the library.  Up to kPoolKeepBytes of freed memory stay in the
 // pool across synchronisations, so later calls reuse it without going back to the driver;
@@ -273,19 +289,8 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
 int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal) {
     if (validate_shape("ctattn_bwd_workspace_bytes", dtype, B, H, T, d)) return -1;
-    const ctattn::AttnShape s{B, H, T, d, causal != 0};
-    // delta = rowsum(dO * O), [B, H, T] (fp64 for fp64 storage, else fp32), always first.
-    int64_t bytes = align_up(s.rows() * stat_bytes(dtype));
-    if (const int64_t dp = padded_width(dtype, d)) {
-        // Then the MFMA backward's scratch for the padded shape and the eight padded copies.
-        if (dtype != CTATTN_F64)
-            bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, padded_shape(s, dp), deterministic_policy()));
-        bytes += 8 * padded_copy_bytes(dtype, s, dp);
-    } else if (use_mfma_bwd(dtype, d)) {
-        bytes += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, s, deterministic_policy()));
-    }
     ok();
-    return bytes;
+    return bwd_workspace_bytes(dtype, ctattn::AttnShape{B, H, T, d, causal != 0}, true);
 }
 
 int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
@@ -297,12 +302,15 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
     if (s.rows() == 0) return ok();
     if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
         return fail(hipErrorInvalidValue, "ctattn_bwd: null tensor pointer");
-    const int64_t need = ctattn_bwd_workspace_bytes(dtype, B, H, T, d, causal);
+    // ctattn_bwd_workspace_bytes asks for the fastest path's workspace; a smaller one down to
+    // `need` works too, without the bf16 / fp16 dS tiles.
+    const int64_t need = bwd_workspace_bytes(dtype, s, false);
     if (workspace == nullptr || workspace_bytes < need)
         return fail(hipErrorInvalidValue,
                     "ctattn_bwd: workspace of %lld bytes given, %lld needed "
                     "(ctattn_bwd_workspace_bytes)",
                     (long long)workspace_bytes, (long long)need);
+    const bool with_ds = workspace_bytes >= bwd_workspace_bytes(dtype, s, true);
     hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t e;
     // Misaligned tensors take the generic kernels, whose workspace (delta only) is a prefix of
@@ -319,7 +327,10 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
         void *delta = w;
         w += align_up(rows * stat_bytes(dtype));
         void *extra = w;
-        if (dtype != CTATTN_F64) w += align_up(ctattn::mfma_bwd_workspace_bytes(dtype, sp, deterministic_policy()));
+        const int64_t extra_bytes =
+            dtype != CTATTN_F64 ? align_up(ctattn::mfma_bwd_workspace_bytes(dtype, sp, deterministic_policy(), with_ds))
+                                : 0;
+        w += extra_bytes;
         void *cp[8];
         for (int i = 0; i < 8; ++i) cp[i] = w + i * tb;
         const void *in[5] = {q, k, v, o, dout};
@@ -329,16 +340,17 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
             e = dtype == CTATTN_F64
                     ? ctattn::launch_f64_bwd(cp[0], cp[1], cp[2], cp[3], cp[4], lse, delta, cp[5], cp[6], cp[7], sp, st)
                     : ctattn::launch_mfma_bwd(dtype, cp[0], cp[1], cp[2], cp[3], cp[4], static_cast<const float *>(lse),
-                                              static_cast<float *>(delta), cp[5], cp[6], cp[7], extra,
+                                              static_cast<float *>(delta), cp[5], cp[6], cp[7], extra, extra_bytes,
                                               deterministic_policy(), sp, st);
         const void *grads[3] = {cp[5], cp[6], cp[7]};
         void *out[3] = {dq, dk, dv};
         if (e == hipSuccess) e = ctattn::launch_unpad_rows(eb, grads, out, 3, rows, di, wi, st);
     } else if (use_mfma_bwd(dtype, d) && al) {
-        void *extra = static_cast<char *>(workspace) + align_up(s.rows() * stat_bytes(dtype));
+        const int64_t head = align_up(s.rows() * stat_bytes(dtype));
+        void *extra = static_cast<char *>(workspace) + head;
         e = ctattn::launch_mfma_bwd(dtype, q, k, v, o, dout, static_cast<const float *>(lse),
-                                    static_cast<float *>(workspace), dq, dk, dv, extra, deterministic_policy(), s,
-                                    st);
+                                    static_cast<float *>(workspace), dq, dk, dv, extra, workspace_bytes - head,
+                                    deterministic_policy(), s, st);
     } else if (use_f64_mfma(dtype, d) && al) {
         e = ctattn::launch_f64_bwd(q, k, v, o, dout, lse, workspace, dq, dk, dv, s, st);
     } else {
@@ -351,7 +363,8 @@ int ctattn_bwd_noalloc(int dtype, const void *q, const void *k, const void *v, c
                        const void *dout, const void *lse, void *dq, void *dk, void *dv, int64_t B,
                        int64_t H, int64_t T, int64_t d, int causal, void *stream) {
     if (int rc = validate_shape("ctattn_bwd_noalloc", dtype, B, H, T, d)) return rc;
-    const int64_t need = ctattn_bwd_workspace_bytes(dtype, B, H, T, d, causal);
+    // The smallest workspace that works (the bf16 / fp16 dS tiles only when they fit too).
+    const int64_t need = bwd_workspace_bytes(dtype, ctattn::AttnShape{B, H, T, d, causal != 0}, false);
     if (need > CTATTN_NOALLOC_SCRATCH_BYTES)
         return fail(hipErrorInvalidValue,
                     "ctattn_bwd_noalloc: this problem needs %lld bytes of scratch, more than the %lld of the "

@@ -101,6 +101,11 @@ CTATTN_API int ctattn_fwd(int dtype, const void *q, const void *k, const void *v
  * accumulates straight into dq/dk/dv (FlashAttentionLayer.cu:103-106, flash_attention.cu:317-321).
  * A head dim that runs padded to width dp (see the conventions above) also needs room for
  * the eight padded copies (q, k, v, o, dout, dq, dk, dv: 8 * B*H*T*dp elements).
+ * bf16 / fp16 at d = 128 (also padded onto it) include the dS tiles: the dK/dV kernel stores
+ * the bf16 dS it computes and the dQ kernel multiplies it by K instead of recomputing S and
+ * dP, 2 bytes per (row, key) pair of the mask rounded to 32 x 32 tiles (causal B*H*T^2
+ * bytes, B1 H32 T8192: 2.2 GB).  Above 4 GiB of dS they are left out (the recomputing dQ
+ * kernel runs, workspace linear in rows).
  */
 CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal);
@@ -109,9 +114,11 @@ CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, i
  * Backward: dQ, dK, dV given Q, K, V, the forward's O and LSE, and dO.
  * Replaces the flashAttentionBackward<DType> launch of FlashAttentionLayer::computeBackward
  * (reference FlashAttentionLayer.cu:129-140; kernel flash_attention.cu:226-326).
- * dq, dk, dv are fully overwritten (no pre-zeroing needed).  workspace must hold at least
- * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy.  Reproducibility
- * depends on the policy (see enum ctattn_policy).
+ * dq, dk, dv are fully overwritten (no pre-zeroing needed).  workspace should hold
+ * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy.  A smaller one works
+ * down to that size minus the bf16 / fp16 dS tiles (the error message names the minimum);
+ * then dQ recomputes S and dP, with the same results up to bf16 rounding of dS.
+ * Reproducibility depends on the policy (see enum ctattn_policy).
  */
 CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
                const void *dout, const void *lse, void *dq, void *dk, void *dv,
@@ -129,7 +136,8 @@ CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v
  * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  It calls no hipMalloc / hipFree and no allocating library routine.
  *   - same arguments, kernels and results as ctattn_bwd under the current policy, minus the
- *     workspace; problems whose ctattn_bwd_workspace_bytes exceeds the scratch size are
+ *     workspace; it uses the smallest workspace ctattn_bwd accepts (the bf16 / fp16 dS tiles
+ *     only when they fit too), and problems that need more than the scratch size are
  *     rejected with hipErrorInvalidValue before any GPU work (AUTO needs 4 bytes per row
  *     B*H*T for fp32, 8 for bf16 / fp16 / fp64: up to 8 Mi or 4 Mi rows).
  *   - the scratch of the stream's device is found once per device (hipGetSymbolAddress) and
