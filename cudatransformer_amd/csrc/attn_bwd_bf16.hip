@@ -708,7 +708,9 @@ int64_t nl2_bytes(const AttnShape &s) { return (s.rows() * int64_t(sizeof(float)
 }  // namespace
 
 int64_t bf16_ds_bytes(const AttnShape &s) {
-    if (s.d != 128) return 0;
+    // T > 65536 needs more than 4 GiB of tiles even for one causal head (and the product
+    // below could overflow for the longest sequences), so it never takes the dS path.
+    if (s.d != 128 || s.T > 65536) return 0;
     const int64_t b = s.bh() * ds_tiles_per_head(s.T, s.causal) * kDsTileElems * int64_t(sizeof(uint16_t));
     return b <= kDsMaxBytes ? b : 0;
 }

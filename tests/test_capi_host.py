@@ -195,3 +195,23 @@ def test_row_limit_boundary(lib):
     assert lib.ctattn_bwd_workspace_bytes(0, 1, 1, 2 ** 31 - 1, 8, 0) >= (2 ** 31 - 1) * 4
     assert lib.ctattn_bwd_workspace_bytes(0, 1, 1, 2 ** 31, 8, 0) == -1
     assert lib.ctattn_bwd_workspace_bytes(1, 1 << 16, 1 << 5, 1 << 10, 128, 1) == -1
+
+
+def test_bf16_ds_workspace(lib):
+    """bf16 / fp16 at d = 128 ask for the dS tiles (2 KiB per 32 x 32 tile of the mask: a
+    triangle when causal) on top of delta and -LSE log2(e); other head dims and fp32 do not,
+    and above 4 GiB of tiles (or T > 65536) the workspace stays linear in rows."""
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    for (b, h, t) in [(1, 32, 8192), (2, 3, 333)]:
+        rows, nt = b * h * t, (t + 31) // 32
+        base = al(rows * 4) + al(rows * 4)
+        for causal, tiles in ((1, nt * (nt + 1) // 2), (0, nt * nt)):
+            for dtype in (1, 2):
+                assert lib.ctattn_bwd_workspace_bytes(dtype, b, h, t, 128, causal) == base + b * h * tiles * 2048
+            assert lib.ctattn_bwd_workspace_bytes(1, b, h, t, 64, causal) == base
+            assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, 128, causal) == al(rows * 4)
+    # B1 H32 T16384 causal: 8.6 GB of tiles, above the 4 GiB limit.
+    assert lib.ctattn_bwd_workspace_bytes(1, 1, 32, 16384, 128, 1) == 2 * al(32 * 16384 * 4)
+    assert lib.ctattn_bwd_workspace_bytes(1, 1, 1, 1 << 20, 128, 1) == 2 * al((1 << 20) * 4)
