@@ -357,20 +357,22 @@ def test_misaligned_views_take_the_generic_kernels(dtype, causal):
         assert err <= rel * max(float(np.max(np.abs(want[key]))), 1.0), (key, err)
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "f16"])
 @pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
 @pytest.mark.parametrize("shape", [(1, 3, 333, 128), (2, 2, 64, 128)], ids=lambda s: "x".join(map(str, s)))
-def test_bf16_d128_ds_and_recompute_paths(shape, causal):
+def test_bf16_d128_ds_and_recompute_paths(shape, causal, fmt):
     """bf16 at d = 128 stores dS in the workspace and the dQ kernel multiplies it by K when the
     workspace ctattn_bwd_workspace_bytes asks for is given; a workspace without the dS tiles
     (the minimum ctattn_bwd accepts) recomputes S and dP instead.  Both against the oracle, and
     one byte less than the minimum is refused."""
     b, h, t, d = shape
-    q, k, v, do = ora.make_inputs(shape, 77, std=0.5, dtype="bf16")
-    say(f"dS / recompute paths shape={shape} causal={causal}")
-    tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(torch.bfloat16)
+    q, k, v, do = ora.make_inputs(shape, 77, std=0.5, dtype=fmt)
+    td, code = (torch.bfloat16, 1) if fmt == "bf16" else (torch.float16, 2)
+    say(f"dS / recompute paths shape={shape} causal={causal} {fmt}")
+    tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(td)
                        for a in (q, k, v, do))
     o, lse = ct.flash_attn_fwd(tq, tk, tv, causal)
-    full = ct._capi.bwd_workspace_bytes(torch.bfloat16, b, h, t, d, causal)
+    full = ct._capi.bwd_workspace_bytes(td, b, h, t, d, causal)
     nt = (t + 31) // 32
     ds_bytes = b * h * (nt * (nt + 1) // 2 if causal else nt * nt) * 2048
     lib = ct._capi.load()
@@ -379,15 +381,15 @@ def test_bf16_d128_ds_and_recompute_paths(shape, causal):
     for label, nbytes in (("dS", full), ("recompute", full - ds_bytes)):
         ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
         dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
-        rc = lib.ctattn_bwd(1, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o.data_ptr(), tdo.data_ptr(),
+        rc = lib.ctattn_bwd(code, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o.data_ptr(), tdo.data_ptr(),
                             lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), nbytes,
                             b, h, t, d, int(causal), None)
         assert rc == 0, ct._capi.last_error()
         torch.cuda.synchronize()
         got = {"o": f(o), "lse": f(lse), "dq": f(dq), "dk": f(dk), "dv": f(dv)}
-        assert_close(got, want, "bf16", f"{shape} causal={causal} {label}")
+        assert_close(got, want, "bf16", f"{shape} causal={causal} {fmt} {label}")
     ws = torch.empty(full - ds_bytes - 1, dtype=torch.uint8, device=DEV)
-    rc = lib.ctattn_bwd(1, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o.data_ptr(), tdo.data_ptr(),
+    rc = lib.ctattn_bwd(code, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o.data_ptr(), tdo.data_ptr(),
                         lse.data_ptr(), tq.data_ptr(), tq.data_ptr(), tq.data_ptr(), ws.data_ptr(),
                         full - ds_bytes - 1, b, h, t, d, int(causal), None)
     assert rc != 0 and "workspace" in ct._capi.last_error()
