@@ -1,11 +1,15 @@
-// C-ABI entry points of the attention layer's projections (declared in include/ctattn.h).
+// C-ABI entry points of the attention layer's projections and of the plain linear layers
+// (declared in include/ctattn.h).
 //
 // Each entry point validates its arguments on the host, describes its products as
 // separable views (row-major [B*T, E] activations, [B, H, T, d] attention tensors, [out][in]
-// weights) and launches the MFMA GEMM family of proj_gemm.hip on the caller's stream.
+// weights) and launches the MFMA GEMM family of proj_gemm.hip on the caller's stream.  The
+// linear layers' products are plain row-major fp32 GEMMs and run on the split-K-in-workgroup
+// kernels of linear_gemm.hip; shapes outside that family's domain (K not a multiple of 16,
+// an unaligned operand, other dtypes) and the GENERIC policy take the projection family.
 #include "capi_util.h"
 #include "ctattn.h"
-#include "blaslt_gemm.h"
+#include "linear_gemm.h"
 #include "proj_launch.h"
 
 #include <algorithm>
@@ -281,6 +285,29 @@ int validate_linear(const char *fn, int dtype, int64_t M, int64_t N, int64_t K) 
     return 0;
 }
 
+// The linear layers' products on linear_gemm.hip (fp32, unless the policy asks for the
+// projection family as a cross-check):
+//   forward  y[m][n] = sum_k x[m][k] w[n][k] + b[n]   A = x [M][K], B = w [N][K]
+//   dX       dx[m][k] = sum_n dy[m][n] w[n][k]       A = dy [M][N], B = w stored [n][k]
+//   dW       dw[n][k] += sum_m dy[m][n] x[m][k]      A = dy stored [m][n], B = x stored [m][k]
+bool lin_policy(int dtype) { return dtype == CTATTN_F32 && ctattn_get_policy() != CTATTN_POLICY_GENERIC; }
+
+ctattn::LinGemm lin_fwd(const void *x, const void *w, const void *b, void *y, int64_t M, int64_t N, int64_t K) {
+    return ctattn::LinGemm{0, true, true, M, N, K, x, K, w, K, y, N, b, false};
+}
+ctattn::LinGemm lin_dx(const void *dy, const void *w, void *dx, int64_t M, int64_t N, int64_t K) {
+    return ctattn::LinGemm{0, true, false, M, K, N, dy, N, w, K, dx, K, nullptr, false};
+}
+ctattn::LinGemm lin_dw(const void *x, const void *dy, void *dw, int64_t M, int64_t N, int64_t K) {
+    return ctattn::LinGemm{0, false, false, N, K, M, dy, N, x, K, dw, K, nullptr, true};
+}
+
+// Split-K partials of the weight gradient: room for either GEMM family's plan.
+int64_t linear_split_bytes(int dtype, int64_t M, int64_t N, int64_t K) {
+    const int64_t own = dtype == CTATTN_F32 ? ctattn::lin_gemm_workspace_bytes(lin_dw(nullptr, nullptr, nullptr, M, N, K)) : 0;
+    return std::max(splitk_bytes(dtype, N, K, M, 1), align_up(own));
+}
+
 bool linear_vec4(int dtype, int64_t M, int64_t N, int64_t K, std::initializer_list<const void *> ptrs) {
     if (M % 4 != 0 || N % 4 != 0 || K % 4 != 0) return false;
     const uintptr_t a = uintptr_t(4 * elem_bytes(dtype));
@@ -297,9 +324,11 @@ int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, vo
     if (int rc = validate_linear(fn, dtype, M, N, K)) return rc;
     if (M == 0) return ok();
     if (!x || !w || !y) return fail(hipErrorInvalidValue, "%s: null x/w/y pointer", fn);
-    // Column-major y^T (N x M, ld N) = W (op T of the K x N column-major w) x^T (K x M) + b.
-    if (ctattn::blaslt_gemm(dtype, true, false, N, M, K, w, K, x, K, y, N, 0.f, b, as_stream(stream)))
-        return finish(fn, hipSuccess, as_stream(stream));
+    if (lin_policy(dtype)) {
+        const ctattn::LinGemm g = lin_fwd(x, w, b, y, M, N, K);
+        if (ctattn::lin_gemm_supported(g))
+            return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, as_stream(stream)), as_stream(stream));
+    }
     // y[m][n] = sum_k x[m][k] w[n][k] + b[n]: A = x [M][K], B = w [N][K], both K-contiguous.
     GemmParams p = make_params(M, N, K, 0, 1, linear_view(nullptr, N), nullptr);
     p.batch[0].nseg = 1;
@@ -314,7 +343,7 @@ int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, vo
 int64_t ctattn_linear_bwd_workspace_bytes(int dtype, int64_t M, int64_t N, int64_t K) {
     if (validate_linear("ctattn_linear_bwd_workspace_bytes", dtype, M, N, K)) return -1;
     ok();
-    return splitk_bytes(dtype, N, K, M, 1) + align_up(ctattn::colsum_workspace_bytes(dtype, M, N));
+    return linear_split_bytes(dtype, M, N, K) + align_up(ctattn::colsum_workspace_bytes(dtype, M, N));
 }
 
 int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, void *dx, void *dw, void *db,
@@ -334,10 +363,15 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     const bool v4 = linear_vec4(dtype, M, N, K, {x, w, dy, dx, dw});
     float *ws = static_cast<float *>(workspace);
     hipError_t e = hipSuccess;
-    // hipBLASLt (column-major): dW^T (K x N, ld K) += x^T (K x M) dy (op T of N x M);
-    // dX^T (K x M, ld K) = w^T (K x N) dy^T (N x M).
-    if (dw && ctattn::blaslt_gemm(dtype, false, true, K, N, M, x, K, dy, N, dw, K, 1.f, nullptr, st)) dw = nullptr;
-    if (dx && ctattn::blaslt_gemm(dtype, false, false, K, M, N, w, K, dy, N, dx, K, 0.f, nullptr, st)) dx = nullptr;
+    const int64_t split_bytes = linear_split_bytes(dtype, M, N, K);
+    if (dw && lin_policy(dtype)) {
+        const ctattn::LinGemm g = lin_dw(x, dy, dw, M, N, K);
+        if (ctattn::lin_gemm_supported(g)) {
+            e = ctattn::launch_lin_gemm(g, workspace, split_bytes, st);
+            if (e != hipSuccess) return finish(fn, e, st);
+            dw = nullptr;
+        }
+    }
     if (dw) {
         // dw[n][k] += sum_m dy[m][n] x[m][k]: M' = N, N' = K, K' = M.  A(m'=n, k'=m) = dy stored
         // [k'][m']; B(k'=m, n'=k) = x stored [k'][n'].
@@ -352,9 +386,13 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (db) {
-        void *cws = static_cast<char *>(workspace) + splitk_bytes(dtype, N, K, M, 1);
+        void *cws = static_cast<char *>(workspace) + split_bytes;
         e = ctattn::launch_colsum_add(dtype, linear_view(dy, N), int(M), int(N), db, cws, st);
         if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (dx && lin_policy(dtype)) {
+        const ctattn::LinGemm g = lin_dx(dy, w, dx, M, N, K);
+        if (ctattn::lin_gemm_supported(g)) return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, st), st);
     }
     if (dx) {
         // dx[m][k] = sum_n dy[m][n] w[n][k]: A = dy [M][N] (K-contiguous), B = w stored [k'][n'].

@@ -68,9 +68,9 @@ enum ctattn_dtype {
  *                  dQ may differ between runs in the last bits; dK, dV, O and LSE do not,
  *                  and the bf16 MFMA backward uses no atomics (bitwise reproducible).
  *   GENERIC        the generic kernels only, at every head dim (used to cross-check the
- *                  paths); the linear layers' plain GEMMs (ctattn_linear_*,
- *                  ctattn_tensor_matmul) then run on the library's own GEMM kernels instead
- *                  of hipBLASLt.
+ *                  paths); the linear layers' fp32 GEMMs (ctattn_linear_*,
+ *                  ctattn_tensor_matmul) then run on the projection GEMM family instead of
+ *                  the split-K-in-workgroup linear GEMMs.
  *   DETERMINISTIC  MFMA kernels without atomics, bitwise-reproducible gradients.  The fp32
  *                  backward stores dQ partials per 128-key block and sums them in a fixed
  *                  order while T <= 1024 (workspace: ceil(T/128) * B*H*T*d fp32 more than

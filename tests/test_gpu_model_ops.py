@@ -65,10 +65,11 @@ LINEAR_SHAPES = [(1, 1, 1), (37, 130, 65), (256, 384, 384), (300, 65, 1536), (64
                  (384, 128, 256), (2048, 64, 96)]
 
 
-@pytest.fixture(params=[_capi.POLICY_AUTO, _capi.POLICY_GENERIC], ids=["blaslt", "own_gemm"])
+@pytest.fixture(params=[_capi.POLICY_AUTO, _capi.POLICY_GENERIC], ids=["lin_gemm", "proj_gemm"])
 def gemm_path(request):
-    """AUTO sends the linear products to hipBLASLt (fp32 / bf16 / fp16), GENERIC keeps them on
-    the library's own GEMM kernels: both paths are checked."""
+    """AUTO sends the fp32 linear products to the split-K-in-workgroup GEMMs (linear_gemm.hip)
+    where their shape allows it, GENERIC keeps every product on the projection GEMM family
+    (proj_gemm.hip): both paths are checked."""
     prev = _capi.set_policy(request.param)
     yield request.param
     _capi.set_policy(prev)
@@ -101,6 +102,60 @@ def test_linear_fwd_bwd(dtype, mnk, bias, gemm_path):
     _close(dw, _as64(dw0, dtype) + dy64.T @ x64, TOL[dtype], "dw")
     if bias:
         _close(db, _as64(db0, dtype) + dy64.sum(0), TOL[dtype], "db")
+
+
+# fp32 shapes on linear_gemm.hip, one per launch plan (tile, waves, stages, K split):
+#   (4096, 1536, 384)  forward 3072 64x32 tiles -> one wave per tile, 2 stages; dW split 4 ways
+#   (4096, 384, 1536)  forward / dW four waves per tile; dX 3072 tiles, one wave
+#   (8192, 1024, 1024) one wave per tile, 3 stages (K = 1024); dW on 64 x 64 tiles of 8 waves
+#   (1008, 208, 1008)  ragged tiles in M, N and K-chunk count on all three products
+#   (64, 16, 4096)     dX with one K chunk for four waves (three waves add a zero tile)
+#   (8192, 64, 64)     dW split 10 ways (each wave keeps 12 of the 512 K chunks)
+#   (4096, 1152, 384)  the QKV-width product of the NanoGPT configuration
+LIN_SHAPES = [(4096, 1536, 384), (4096, 384, 1536), (8192, 1024, 1024), (1008, 208, 1008), (64, 16, 4096),
+              (8192, 64, 64), (4096, 1152, 384)]
+
+
+@pytest.mark.parametrize("mnk", LIN_SHAPES)
+def test_linear_fp32_plans(mnk):
+    """Every launch configuration of the fp32 linear GEMMs against fp64, bias on, dW / db
+    accumulating into non-zero buffers."""
+    m, n, k = mnk
+    dt = torch.float32
+    print(f"linear plans M={m} N={n} K={k}", flush=True)
+    x = _dev(_randn((m, k), 21), dt)
+    w = _dev(_randn((n, k), 22, 1 / math.sqrt(k)), dt)
+    b = _dev(_randn((n,), 23), dt)
+    dy = _dev(_randn((m, n), 24), dt)
+    dw0, db0 = _randn((n, k), 25), _randn((n,), 26)
+    dw, db = _dev(dw0, dt), _dev(db0, dt)
+    y = _capi.linear_fwd(x, w, b)
+    dx = _capi.linear_bwd(x, w, dy, dw, db)
+    torch.cuda.synchronize()
+    x64, w64, dy64 = _as64(x, dt), _as64(w, dt), _as64(dy, dt)
+    _close(y, x64 @ w64.T + _as64(b, dt), TOL[dt], "y")
+    _close(dx, dy64 @ w64, TOL[dt], "dx")
+    _close(dw, _as64(dw0, dt) + dy64.T @ x64, TOL[dt], "dw")
+    _close(db, _as64(db0, dt) + dy64.sum(0), TOL[dt], "db")
+
+
+def test_linear_fp32_bitwise_repeatable():
+    """The fp32 linear products use no atomics: a split-K weight gradient and the forward /
+    dX are bitwise equal across calls."""
+    m, n, k = 4096, 384, 384
+    x = _dev(_randn((m, k), 27), torch.float32)
+    w = _dev(_randn((n, k), 28), torch.float32)
+    dy = _dev(_randn((m, n), 29), torch.float32)
+    outs = []
+    for _ in range(3):
+        dw = torch.zeros(n, k, device="cuda")
+        y = _capi.linear_fwd(x, w)
+        dx = _capi.linear_bwd(x, w, dy, dw, None)
+        torch.cuda.synchronize()
+        outs.append((y.cpu(), dx.cpu(), dw.cpu()))
+    for o in outs[1:]:
+        for a, b_ in zip(outs[0], o):
+            assert torch.equal(a, b_)
 
 
 def test_linear_bwd_skips_and_empty():

@@ -267,7 +267,8 @@ def test_transpose_and_kron(kind):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("kind", FLOAT + ["Int", "Long"])
-@pytest.mark.parametrize("shapes", [((5, 7), (7, 3)), ((4, 33, 20), (4, 20, 12)), ((3, 2, 16, 64), (64, 32)),
+@pytest.mark.parametrize("shapes", [((5, 7), (7, 3)), ((4, 33, 20), (4, 20, 12)), ((4, 33, 32), (4, 32, 12)),
+                                    ((3, 2, 16, 64), (64, 32)),
                                     ((8, 128), (128, 256)), ((2, 3, 0), (0, 4))])
 def test_matmul(kind, shapes):
     sa, sb = shapes
