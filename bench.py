@@ -126,7 +126,9 @@ def cpu_baseline(seconds: float):
         "value": STEP_FLOP / med / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
-        "kind": "port",
+        # torch's CPU SDPA (a library routine, the reference test's comparator), not a port of
+        # the reference: the C port's figure is c_port_value beside it.
+        "kind": "torch-cpu",
         "sample": (f"oracle/torch_cpu.py: torch.nn.functional.scaled_dot_product_attention fp32 "
                    f"causal fwd+bwd on CPU tensors (the comparator of the reference's "
                    f"test_flash_attention.py:49), the full B{B} H{H} T{T} d{D} step on {threads} "
@@ -204,8 +206,11 @@ def main():
     o = torch.empty_like(q)
     lse = torch.empty((B, H, T), device=dev, dtype=torch.float64 if tdt == torch.float64 else torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-    ws = torch.empty(ct.bwd_workspace_bytes(tdt, B, H, T, D, CAUSAL), device=dev,
-                     dtype=torch.uint8)
+    # The backward gets the workspace of its fastest path (ctattn_bwd_workspace_bytes_max: at
+    # bf16 / fp16 d = 128 the dS tiles, 2.2 GB at c4; the same as the default elsewhere).
+    ws_bytes = ct.bwd_workspace_bytes(tdt, B, H, T, D, CAUSAL, fastest=True)
+    ws_default = ct.bwd_workspace_bytes(tdt, B, H, T, D, CAUSAL)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     stream = torch.cuda.current_stream()
 
     def fwd():
@@ -277,6 +282,8 @@ def main():
             # computeBackward per step, output / gradient / workspace allocation included,
             # host wall clock around synchronised steps.
             "layer_path_ms": None if layer_ms is None else round(layer_ms, 5),
+            "bwd_workspace_bytes": ws_bytes,
+            "bwd_workspace_default_bytes": ws_default,
             "preroll_steps": preroll_steps,
             "preroll_s": round(preroll_s, 3),
         },

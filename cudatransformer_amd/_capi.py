@@ -52,8 +52,14 @@ def load() -> ctypes.CDLL:
     vp, i64, c_int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
     lib.ctattn_fwd.argtypes = [c_int, vp, vp, vp, vp, vp, i64, i64, i64, i64, c_int, vp]
     lib.ctattn_fwd.restype = c_int
+    lib.ctattn_fwd_workspace_bytes.argtypes = [c_int, i64, i64, i64, i64]
+    lib.ctattn_fwd_workspace_bytes.restype = i64
+    lib.ctattn_fwd_ws.argtypes = [c_int, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, c_int, vp]
+    lib.ctattn_fwd_ws.restype = c_int
     lib.ctattn_bwd_workspace_bytes.argtypes = [c_int, i64, i64, i64, i64, c_int]
     lib.ctattn_bwd_workspace_bytes.restype = i64
+    lib.ctattn_bwd_workspace_bytes_max.argtypes = [c_int, i64, i64, i64, i64, c_int]
+    lib.ctattn_bwd_workspace_bytes_max.restype = i64
     lib.ctattn_bwd.argtypes = [c_int, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64,
                                i64, i64, i64, i64, c_int, vp]
     lib.ctattn_bwd.restype = c_int
@@ -171,24 +177,34 @@ def flash_attn_fwd(q, k, v, causal: bool = False, out=None, lse=None, stream=Non
     _check_qkv("flash_attn_fwd", q, out)
     if lse.dtype != stat or tuple(lse.shape) != (b, h, t) or not lse.is_contiguous():
         raise ValueError(f"flash_attn_fwd: lse must be contiguous {stat} [B, H, T]")
-    rc = load().ctattn_fwd(_DTYPE_CODE[q.dtype], q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                           out.data_ptr(), lse.data_ptr(), b, h, t, d, int(bool(causal)),
-                           _stream_handle(stream))
-    _check(rc, "ctattn_fwd")
+    lib = load()
+    code = _DTYPE_CODE[q.dtype]
+    need = lib.ctattn_fwd_workspace_bytes(code, b, h, t, d)
+    if need < 0:
+        raise RuntimeError(f"ctattn_fwd_workspace_bytes failed: {last_error()}")
+    ws = torch.empty(need, dtype=torch.uint8, device=q.device) if need > 0 else None
+    rc = lib.ctattn_fwd_ws(code, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                           _ptr(ws), need, b, h, t, d, int(bool(causal)), _stream_handle(stream))
+    _check(rc, "ctattn_fwd_ws")
     return out, lse
 
 
-def bwd_workspace_bytes(dtype, b, h, t, d, causal) -> int:
+def bwd_workspace_bytes(dtype, b, h, t, d, causal, fastest: bool = False) -> int:
+    """ctattn_bwd_workspace_bytes (linear in B*H*T), or with fastest=True
+    ctattn_bwd_workspace_bytes_max (the bf16 / fp16 d = 128 dS tiles, about B*H*T^2 bytes)."""
     code = _DTYPE_CODE[dtype] if isinstance(dtype, torch.dtype) else int(dtype)
-    n = load().ctattn_bwd_workspace_bytes(code, b, h, t, d, int(bool(causal)))
+    fn = "ctattn_bwd_workspace_bytes_max" if fastest else "ctattn_bwd_workspace_bytes"
+    n = getattr(load(), fn)(code, b, h, t, d, int(bool(causal)))
     if n < 0:
-        raise RuntimeError(f"ctattn_bwd_workspace_bytes failed: {last_error()}")
+        raise RuntimeError(f"{fn} failed: {last_error()}")
     return n
 
 
 def flash_attn_bwd(q, k, v, o, do, lse, causal: bool = False, dq=None, dk=None, dv=None,
                    workspace=None, stream=None):
-    """dQ, dK, dV of attention given the forward's O and LSE and the upstream dO."""
+    """dQ, dK, dV of attention given the forward's O and LSE and the upstream dO.  Without a
+    workspace one of ctattn_bwd_workspace_bytes is allocated here; a larger one (up to
+    bwd_workspace_bytes(..., fastest=True)) lets the bf16 / fp16 d = 128 path store dS."""
     _check_qkv("flash_attn_bwd", q, k, v, o, do)
     b, h, t, d = q.shape
     dq = torch.empty_like(q) if dq is None else dq

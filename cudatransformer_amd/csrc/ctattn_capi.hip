@@ -234,36 +234,52 @@ int pool_for_stream(hipStream_t stream, hipMemPool_t *out) {
     return 0;
 }
 
-// ctattn_fwd for a head dim that runs on the MFMA kernels of width dp: q, k, v padded into
-// stream-ordered scratch, the kernels writing O into a padded buffer (LSE straight into the
-// caller's, whose layout does not depend on d), O copied back.
-int fwd_padded(int dtype, int64_t dp, const void *q, const void *k, const void *v, void *o, void *lse,
-               const ctattn::AttnShape &s, hipStream_t st) {
+// The forward for a head dim that runs on the MFMA kernels of width dp: q, k, v padded into
+// buf (4 padded copies: q, k, v, o), the kernels writing O into a padded buffer (LSE straight
+// into the caller's, whose layout does not depend on d), O copied back.
+hipError_t fwd_padded_in(int dtype, int64_t dp, const void *q, const void *k, const void *v, void *o, void *lse,
+                         const ctattn::AttnShape &s, hipStream_t st, void *buf) {
     const int eb = int(elem_bytes(dtype));
     const int64_t rows = s.rows();
     const int64_t tb = padded_copy_bytes(dtype, s, dp);
-    hipMemPool_t pool = nullptr;
-    if (int rc = pool_for_stream(st, &pool)) return rc;
-    void *buf = nullptr;
-    hipError_t e = hipMallocFromPoolAsync(&buf, size_t(4 * tb), pool, st);
-    if (e != hipSuccess)
-        return fail(e, "ctattn_fwd: %lld bytes for the head dim %lld -> %lld copies: %s", (long long)(4 * tb),
-                    (long long)s.d, (long long)dp, hipGetErrorString(e));
     char *p = static_cast<char *>(buf);
     void *qp = p, *kp = p + tb, *vp = p + 2 * tb, *op = p + 3 * tb;
     const ctattn::AttnShape sp = padded_shape(s, dp);
     const int d = int(s.d), w = int(dp);
     const void *in[3] = {q, k, v};
     void *padded[3] = {qp, kp, vp};
-    e = ctattn::launch_pad_rows(eb, in, padded, 3, rows, d, w, st);
+    hipError_t e = ctattn::launch_pad_rows(eb, in, padded, 3, rows, d, w, st);
     if (e == hipSuccess)
         e = dtype == CTATTN_F64 ? ctattn::launch_f64_fwd(qp, kp, vp, op, lse, sp, st)
                                 : ctattn::launch_mfma_fwd(dtype, qp, kp, vp, op, static_cast<float *>(lse), sp, st);
     const void *po[1] = {op};
     void *oo[1] = {o};
     if (e == hipSuccess) e = ctattn::launch_unpad_rows(eb, po, oo, 1, rows, d, w, st);
+    return e;
+}
+
+// ctattn_fwd's padded path: the copies in stream-ordered memory from the library's pool.
+int fwd_padded_pool(int dtype, int64_t dp, const void *q, const void *k, const void *v, void *o, void *lse,
+                    const ctattn::AttnShape &s, hipStream_t st) {
+    const int64_t bytes = 4 * padded_copy_bytes(dtype, s, dp);
+    hipMemPool_t pool = nullptr;
+    if (int rc = pool_for_stream(st, &pool)) return rc;
+    void *buf = nullptr;
+    hipError_t e = hipMallocFromPoolAsync(&buf, size_t(bytes), pool, st);
+    if (e != hipSuccess)
+        return fail(e, "ctattn_fwd: %lld bytes for the head dim %lld -> %lld copies: %s", (long long)bytes,
+                    (long long)s.d, (long long)dp, hipGetErrorString(e));
+    e = fwd_padded_in(dtype, dp, q, k, v, o, lse, s, st, buf);
     const hipError_t ef = hipFreeAsync(buf, st);  // after every use of buf on the stream
     return finish("ctattn_fwd", e != hipSuccess ? e : ef, st);
+}
+
+// The bf16 / fp16 dS tiles go into the default backward workspace only while they take no
+// more than twice the bytes of q, k and v together, so that workspace stays linear in
+// B * H * T; ctattn_bwd_workspace_bytes_max always includes them.
+bool ds_in_default(int dtype, const ctattn::AttnShape &s) {
+    const int64_t ds = bwd_workspace_bytes(dtype, s, true) - bwd_workspace_bytes(dtype, s, false);
+    return ds <= 2 * 3 * s.rows() * s.d * elem_bytes(dtype);
 }
 
 }  // namespace
@@ -278,7 +294,7 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
     if (!q || !k || !v || !o)
         return fail(hipErrorInvalidValue, "ctattn_fwd: null q/k/v/o pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (const int64_t dp = padded_width(dtype, d)) return fwd_padded(dtype, dp, q, k, v, o, lse, s, st);
+    if (const int64_t dp = padded_width(dtype, d)) return fwd_padded_pool(dtype, dp, q, k, v, o, lse, s, st);
     const bool al = aligned16({q, k, v, o, lse});
     hipError_t e = use_mfma_fwd(dtype, d) && al ? ctattn::launch_mfma_fwd(dtype, q, k, v, o, static_cast<float *>(lse), s, st)
                    : use_f64_mfma(dtype, d) && al ? ctattn::launch_f64_fwd(q, k, v, o, lse, s, st)
@@ -286,9 +302,43 @@ int ctattn_fwd(int dtype, const void *q, const void *k, const void *v, void *o, 
     return finish("ctattn_fwd", e, st);
 }
 
+int64_t ctattn_fwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d) {
+    if (validate_shape("ctattn_fwd_workspace_bytes", dtype, B, H, T, d)) return -1;
+    ok();
+    const ctattn::AttnShape s{B, H, T, d, false};
+    const int64_t dp = padded_width(dtype, d);
+    return dp != 0 ? 4 * padded_copy_bytes(dtype, s, dp) : 0;
+}
+
+int ctattn_fwd_ws(int dtype, const void *q, const void *k, const void *v, void *o, void *lse, void *workspace,
+                  int64_t workspace_bytes, int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream) {
+    if (int rc = validate_shape("ctattn_fwd_ws", dtype, B, H, T, d)) return rc;
+    const ctattn::AttnShape s{B, H, T, d, causal != 0};
+    if (s.rows() == 0) return ok();
+    const int64_t dp = padded_width(dtype, d);
+    if (dp == 0) return ctattn_fwd(dtype, q, k, v, o, lse, B, H, T, d, causal, stream);
+    if (!q || !k || !v || !o) return fail(hipErrorInvalidValue, "ctattn_fwd_ws: null q/k/v/o pointer");
+    const int64_t need = 4 * padded_copy_bytes(dtype, s, dp);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16({workspace}))
+        return fail(hipErrorInvalidValue,
+                    "ctattn_fwd_ws: a 16-byte aligned workspace of %lld bytes is needed "
+                    "(ctattn_fwd_workspace_bytes), %lld given",
+                    (long long)need, (long long)workspace_bytes);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return finish("ctattn_fwd_ws", fwd_padded_in(dtype, dp, q, k, v, o, lse, s, st, workspace), st);
+}
+
 int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal) {
     if (validate_shape("ctattn_bwd_workspace_bytes", dtype, B, H, T, d)) return -1;
+    ok();
+    const ctattn::AttnShape s{B, H, T, d, causal != 0};
+    return bwd_workspace_bytes(dtype, s, ds_in_default(dtype, s));
+}
+
+int64_t ctattn_bwd_workspace_bytes_max(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
+                                       int causal) {
+    if (validate_shape("ctattn_bwd_workspace_bytes_max", dtype, B, H, T, d)) return -1;
     ok();
     return bwd_workspace_bytes(dtype, ctattn::AttnShape{B, H, T, d, causal != 0}, true);
 }
@@ -302,8 +352,8 @@ int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const voi
     if (s.rows() == 0) return ok();
     if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
         return fail(hipErrorInvalidValue, "ctattn_bwd: null tensor pointer");
-    // ctattn_bwd_workspace_bytes asks for the fastest path's workspace; a smaller one down to
-    // `need` works too, without the bf16 / fp16 dS tiles.
+    // Any workspace from `need` (no bf16 / fp16 dS tiles) up works; the dS tiles are used when
+    // it holds them (ctattn_bwd_workspace_bytes_max).
     const int64_t need = bwd_workspace_bytes(dtype, s, false);
     if (workspace == nullptr || workspace_bytes < need)
         return fail(hipErrorInvalidValue,

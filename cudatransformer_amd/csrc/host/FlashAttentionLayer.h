@@ -63,10 +63,7 @@ struct FlashAttentionLayer {
         const size_t B = queries.shape(0), T = queries.shape(2);
         Tensor<DType> output = Tensor<DType>::empty(queries.shape());  // fully written by the kernel
         Tensor<Stat> lse = Tensor<Stat>::empty({B, size_t(numHeads), T});
-        ctattnCheck(ctattn_fwd(DTypeCode<DType>::value, queries.get(), keys.get(), values.get(), output.get(),
-                               lse.get(), int64_t(B), numHeads, int64_t(T), headDim, causal ? 1 : 0,
-                               Runtime::stream()),
-                    "ctattn_fwd");
+        forward(queries, keys, values, output, lse);
         if (saveStates) {
             cachedLse = lse;
             cachedOutput = output;
@@ -94,12 +91,10 @@ struct FlashAttentionLayer {
             // place since): recompute it (FlashAttentionLayer.cu:114-127).
             lse = Tensor<Stat>::empty({B, size_t(numHeads), T});
             output = Tensor<DType>::empty(queries.shape());
-            ctattnCheck(ctattn_fwd(DTypeCode<DType>::value, queries.get(), keys.get(), values.get(), output.get(),
-                                   lse.get(), int64_t(B), numHeads, int64_t(T), headDim, causal ? 1 : 0,
-                                   Runtime::stream()),
-                        "ctattn_fwd");
+            forward(queries, keys, values, output, lse);
         }
         // Fully overwritten by ctattn_bwd (the reference zero-fills and accumulates atomically).
+        // The default workspace is linear in B * H * T, like the reference's backward memory.
         std::array<Tensor<DType>, 3> grads = {Tensor<DType>::empty(queries.shape()),
                                               Tensor<DType>::empty(queries.shape()),
                                               Tensor<DType>::empty(queries.shape())};
@@ -125,6 +120,21 @@ struct FlashAttentionLayer {
     }
 
 private:
+    // ctattn_fwd_ws with a workspace from the caching allocator (non-empty only for head dims
+    // that run padded), so the library itself allocates nothing.
+    void forward(const Tensor<DType> &queries, const Tensor<DType> &keys, const Tensor<DType> &values,
+                 Tensor<DType> &output, Tensor<Stat> &lse) const {
+        const int64_t B = int64_t(queries.shape(0)), T = int64_t(queries.shape(2));
+        const int64_t wsBytes = ctattn_fwd_workspace_bytes(DTypeCode<DType>::value, B, numHeads, T, headDim);
+        if (wsBytes < 0) ctattnCheck(int(hipErrorInvalidValue), "ctattn_fwd_workspace_bytes");
+        std::shared_ptr<uint8_t[]> workspace;
+        if (wsBytes > 0) workspace = deviceAlloc<uint8_t>(size_t(wsBytes));
+        ctattnCheck(ctattn_fwd_ws(DTypeCode<DType>::value, queries.get(), keys.get(), values.get(), output.get(),
+                                  lse.get(), workspace.get(), wsBytes, B, numHeads, T, headDim, causal ? 1 : 0,
+                                  Runtime::stream()),
+                    "ctattn_fwd_ws");
+    }
+
     void check(const Tensor<DType> &t, const char *name) const {
         if (t.nDim() != 4 || int(t.shape(1)) != numHeads || int(t.shape(3)) != headDim)
             throw std::invalid_argument(std::string(name) + " must be [batch, " + std::to_string(numHeads) +

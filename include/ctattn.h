@@ -96,28 +96,57 @@ CTATTN_API int ctattn_fwd(int dtype, const void *q, const void *k, const void *v
                int64_t B, int64_t H, int64_t T, int64_t d, int causal, void *stream);
 
 /*
+ * Bytes of device workspace ctattn_fwd_ws needs (>= 0), or -1 on invalid arguments: 0 unless
+ * the head dim runs padded (see the conventions above), then four [B,H,T,dp] copies (q, k,
+ * v, o).  ctattn_fwd takes that memory from a stream-ordered pool the library owns (up to
+ * 1 GiB of it stays cached per device); ctattn_fwd_ws takes it from the caller instead.
+ */
+CTATTN_API int64_t ctattn_fwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d);
+
+/*
+ * ctattn_fwd with a caller workspace of at least ctattn_fwd_workspace_bytes bytes (16-byte
+ * aligned; may be NULL when that is 0): the same kernels and results, and no memory
+ * allocated by the library.  Replaces the same launch as ctattn_fwd
+ * (FlashAttentionLayer.cu:73-79); the C++ layer and the Python wrapper call this one.
+ */
+CTATTN_API int ctattn_fwd_ws(int dtype, const void *q, const void *k, const void *v, void *o, void *lse,
+                             void *workspace, int64_t workspace_bytes, int64_t B, int64_t H, int64_t T,
+                             int64_t d, int causal, void *stream);
+
+/*
  * Bytes of device workspace ctattn_bwd needs for this problem (>= 0), or -1 on invalid
  * arguments.  Replaces nothing in the reference: its backward zero-fills and atomically
  * accumulates straight into dq/dk/dv (FlashAttentionLayer.cu:103-106, flash_attention.cu:317-321).
  * A head dim that runs padded to width dp (see the conventions above) also needs room for
  * the eight padded copies (q, k, v, o, dout, dq, dk, dv: 8 * B*H*T*dp elements).
- * bf16 / fp16 at d = 128 (also padded onto it) include the dS tiles: the dK/dV kernel stores
- * the bf16 dS it computes and the dQ kernel multiplies it by K instead of recomputing S and
- * dP, 2 bytes per (row, key) pair of the mask rounded to 32 x 32 tiles (causal B*H*T^2
- * bytes, B1 H32 T8192: 2.2 GB).  Above 4 GiB of dS they are left out (the recomputing dQ
- * kernel runs, workspace linear in rows).
+ * The size is linear in B*H*T, as the reference's backward memory is (it never holds a
+ * T x T object): bf16 / fp16 at d = 128 (also padded onto it) include the dS tiles below
+ * only while they take at most twice the bytes of q, k and v together (causal: T <= 12 d).
  */
 CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal);
+
+/*
+ * The workspace of ctattn_bwd's fastest path (>= ctattn_bwd_workspace_bytes), or -1 on
+ * invalid arguments.  No counterpart in the reference.  bf16 / fp16 at d = 128 (also padded
+ * onto it): the dS tiles -- the dK/dV kernel stores the bf16 dS it computes and the dQ kernel
+ * multiplies it by K instead of recomputing S and dP, 2 bytes per (row, key) pair of the mask
+ * rounded to 32 x 32 tiles (causal B*H*T^2 bytes, B1 H32 T8192: 2.2 GB; 2-7 % faster
+ * backward).  Above 4 GiB of dS they are left out and this equals ctattn_bwd_workspace_bytes.
+ */
+CTATTN_API int64_t ctattn_bwd_workspace_bytes_max(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
+                                                  int causal);
 
 /*
  * Backward: dQ, dK, dV given Q, K, V, the forward's O and LSE, and dO.
  * Replaces the flashAttentionBackward<DType> launch of FlashAttentionLayer::computeBackward
  * (reference FlashAttentionLayer.cu:129-140; kernel flash_attention.cu:226-326).
  * dq, dk, dv are fully overwritten (no pre-zeroing needed).  workspace should hold
- * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy.  A smaller one works
- * down to that size minus the bf16 / fp16 dS tiles (the error message names the minimum);
- * then dQ recomputes S and dP, with the same results up to bf16 rounding of dS.
+ * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy, or any size up to
+ * ctattn_bwd_workspace_bytes_max(...); a smaller one works down to the size without the
+ * bf16 / fp16 dS tiles (the error message names the minimum).  With a workspace that holds
+ * the dS tiles dQ = dS K reads them back, else dQ recomputes S and dP: the same results up to
+ * bf16 rounding of dS.
  * Reproducibility depends on the policy (see enum ctattn_policy).
  */
 CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
@@ -131,10 +160,9 @@ CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v
 /*
  * Backward that allocates nothing: ctattn_bwd with its workspace taken from a static device
  * array of CTATTN_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on each GPU it runs
- * on until the process ends.  No counterpart in the reference (its backward allocates through
- * cudaMakeShared, FlashAttentionLayer.cu:103-106); it is for callers that cannot allocate
- * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc.  It calls no hipMalloc / hipFree and no allocating library routine.
+ * on until the process ends.  No counterpart in the reference; it is for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  It calls no hipMalloc / hipFree and no allocating library routine.
  *   - same arguments, kernels and results as ctattn_bwd under the current policy, minus the
  *     workspace; it uses the smallest workspace ctattn_bwd accepts (the bf16 / fp16 dS tiles
  *     only when they fit too), and problems that need more than the scratch size are

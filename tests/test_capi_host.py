@@ -198,9 +198,11 @@ def test_row_limit_boundary(lib):
 
 
 def test_bf16_ds_workspace(lib):
-    """bf16 / fp16 at d = 128 ask for the dS tiles (2 KiB per 32 x 32 tile of the mask: a
-    triangle when causal) on top of delta and -LSE log2(e); other head dims and fp32 do not,
-    and above 4 GiB of tiles (or T > 65536) the workspace stays linear in rows."""
+    """bf16 / fp16 at d = 128: ctattn_bwd_workspace_bytes_max asks for the dS tiles (2 KiB per
+    32 x 32 tile of the mask: a triangle when causal) on top of delta and -LSE log2(e); other
+    head dims and fp32 do not, and above 4 GiB of tiles (or T > 65536) it stays linear in rows.
+    The default ctattn_bwd_workspace_bytes includes the tiles only while they take at most
+    twice the bytes of q, k and v."""
     def al(x):
         return (x + 255) // 256 * 256
 
@@ -209,9 +211,50 @@ def test_bf16_ds_workspace(lib):
         base = al(rows * 4) + al(rows * 4)
         for causal, tiles in ((1, nt * (nt + 1) // 2), (0, nt * nt)):
             for dtype in (1, 2):
-                assert lib.ctattn_bwd_workspace_bytes(dtype, b, h, t, 128, causal) == base + b * h * tiles * 2048
-            assert lib.ctattn_bwd_workspace_bytes(1, b, h, t, 64, causal) == base
-            assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, 128, causal) == al(rows * 4)
+                ds = b * h * tiles * 2048
+                assert lib.ctattn_bwd_workspace_bytes_max(dtype, b, h, t, 128, causal) == base + ds
+                in_default = ds <= 2 * 3 * rows * 128 * 2
+                assert in_default == (t == 333)
+                assert lib.ctattn_bwd_workspace_bytes(dtype, b, h, t, 128, causal) == base + (ds if in_default else 0)
+            for fn in (lib.ctattn_bwd_workspace_bytes, lib.ctattn_bwd_workspace_bytes_max):
+                assert fn(1, b, h, t, 64, causal) == base
+                assert fn(0, b, h, t, 128, causal) == al(rows * 4)
     # B1 H32 T16384 causal: 8.6 GB of tiles, above the 4 GiB limit.
-    assert lib.ctattn_bwd_workspace_bytes(1, 1, 32, 16384, 128, 1) == 2 * al(32 * 16384 * 4)
-    assert lib.ctattn_bwd_workspace_bytes(1, 1, 1, 1 << 20, 128, 1) == 2 * al((1 << 20) * 4)
+    assert lib.ctattn_bwd_workspace_bytes_max(1, 1, 32, 16384, 128, 1) == 2 * al(32 * 16384 * 4)
+    assert lib.ctattn_bwd_workspace_bytes_max(1, 1, 1, 1 << 20, 128, 1) == 2 * al((1 << 20) * 4)
+
+
+def test_default_bwd_workspace_is_linear_in_rows(lib):
+    """The default backward workspace grows linearly with B * H * T at every T, like the
+    reference's backward memory (which never holds a T x T object): at most 8 bytes per row
+    of statistics plus, while they are included, dS tiles of at most 2 x (q + k + v) =
+    1536 bytes per row at bf16 d = 128, plus alignment.  B1 H32 T32768 d128 bf16 included."""
+    for dtype in (1, 2):
+        for causal in (0, 1):
+            for t in [64, 128, 333, 1024, 1536, 2048, 4096, 8192, 16384, 32768, 65536]:
+                rows = 32 * t
+                n = lib.ctattn_bwd_workspace_bytes(dtype, 1, 32, t, 128, causal)
+                assert 0 < n <= rows * (8 + 1536) + 512, (dtype, causal, t, n)
+                assert n <= lib.ctattn_bwd_workspace_bytes_max(dtype, 1, 32, t, 128, causal)
+    assert lib.ctattn_bwd_workspace_bytes(1, 1, 32, 32768, 128, 1) <= 32 * 32768 * 8 + 512
+
+
+def test_fwd_workspace_bytes(lib):
+    """The forward needs a workspace only for head dims that run padded: four [B,H,T,dp]
+    copies (q, k, v, o), each 256-byte aligned; none for 32 / 64 / 128 or above 128."""
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    b, h, t = 2, 3, 100
+    rows = b * h * t
+    for d in (32, 64, 128, 160):
+        assert lib.ctattn_fwd_workspace_bytes(0, b, h, t, d) == 0
+    assert lib.ctattn_fwd_workspace_bytes(0, b, h, t, 48) == 4 * al(rows * 64 * 4)
+    assert lib.ctattn_fwd_workspace_bytes(1, b, h, t, 80) == 4 * al(rows * 128 * 2)
+    assert lib.ctattn_fwd_workspace_bytes(3, b, h, t, 16) == 4 * al(rows * 32 * 8)
+    assert lib.ctattn_fwd_workspace_bytes(0, b, -1, t, 48) == -1
+    prev = _capi.set_policy(_capi.POLICY_GENERIC)
+    try:
+        assert lib.ctattn_fwd_workspace_bytes(0, b, h, t, 48) == 0
+    finally:
+        _capi.set_policy(prev)

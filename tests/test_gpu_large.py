@@ -6,7 +6,9 @@ elements.  This build computes element offsets in int64 and launches its row-par
 kernels with grid-stride loops, so both limits are gone:
 
 * more than 2^31 elements per tensor on the MFMA kernels (fp32 and bf16): the first and the
-  last (b, h) slice -- whose element offsets are above 2^31 -- against the fp64 oracle;
+  last (b, h) slice -- whose element offsets are above 2^31 -- against the fp64 oracle; bf16
+  d = 128 both with the recomputing dQ kernel and with the dS tiles stored in the workspace
+  (2.7 GB of tiles at 131073 heads of T = 128);
 * more than 2^26 rows on the generic kernels (one wave per row: 2^26 rows x 64 lanes is the
   2^32 work-item limit of one launch), again first and last slices against the oracle.
 
@@ -48,12 +50,16 @@ def check_slices(tensors, causal, bh_list, dtype, ctx):
                 assert rel <= 2e-2, f"{ctx} slice ({b}, {h}) {name}: rel err {rel:.3e}"
 
 
-def run_big(shape, causal, dtype, std, seed):
+def run_big(shape, causal, dtype, std, seed, fastest=False):
     g = torch.Generator(device=DEV).manual_seed(seed)
     t = {n: (std * torch.randn(shape, generator=g, device=DEV, dtype=torch.float32)).to(dtype)
          for n in ("q", "k", "v", "do")}
     o, lse = ct.flash_attn_fwd(t["q"], t["k"], t["v"], causal)
-    dq, dk, dv = ct.flash_attn_bwd(t["q"], t["k"], t["v"], o, t["do"], lse, causal)
+    ws = None
+    if fastest:
+        ws = torch.empty(ct._capi.bwd_workspace_bytes(dtype, *shape, causal, fastest=True), dtype=torch.uint8,
+                         device=DEV)
+    dq, dk, dv = ct.flash_attn_bwd(t["q"], t["k"], t["v"], o, t["do"], lse, causal, workspace=ws)
     torch.cuda.synchronize()
     t.update(o=o, lse=lse, dq=dq, dk=dk, dv=dv)
     return t
@@ -70,6 +76,26 @@ def test_more_than_2_31_elements_mfma(dtype):
     t = run_big(shape, True, dtype, 1.0 if dtype == torch.float32 else 0.5, seed=71)
     check_slices(t, True, [(0, 0), (shape[0] - 1, shape[1] - 1), (shape[0] // 2, 3)], dtype,
                  f"{shape} {dtype}")
+    del t
+    torch.cuda.empty_cache()
+
+
+def test_more_than_2_31_elements_bf16_ds_tiles():
+    """B1 H131073 T128 d128 bf16 causal: 2,147,500,032 elements per tensor (> 2^31) with the
+    dS tiles in the workspace (131073 heads x 10 tiles x 2 KiB = 2.7 GB, under the 4 GiB limit),
+    so the dK/dV kernel's tile stores and the dQ kernel's tile reads use 64-bit offsets; the
+    first, middle and last heads against the oracle."""
+    shape = (1, 131073, 128, 128)
+    n = shape[1] * shape[2] * shape[3]
+    assert n > 2 ** 31
+    nt = shape[2] // 32
+    ds_bytes = shape[1] * nt * (nt + 1) // 2 * 2048
+    assert 2 ** 31 < ds_bytes <= 4 << 30
+    full = ct._capi.bwd_workspace_bytes(torch.bfloat16, *shape, True, fastest=True)
+    assert full - ct._capi.bwd_workspace_bytes(torch.bfloat16, *shape, True) == ds_bytes
+    say(f"large bf16 problem with dS tiles {shape}")
+    t = run_big(shape, True, torch.bfloat16, 0.5, seed=73, fastest=True)
+    check_slices(t, True, [(0, 0), (0, shape[1] // 2), (0, shape[1] - 1)], torch.bfloat16, f"{shape} dS tiles")
     del t
     torch.cuda.empty_cache()
 

@@ -37,12 +37,17 @@ def policy(request):
     ct.set_policy(prev)
 
 
-def run_gpu(q, k, v, do, causal, dtype):
+def run_gpu(q, k, v, do, causal, dtype, fastest=False):
+    """Forward + backward on the GPU; fastest: the backward gets the workspace of its fastest
+    path (ctattn_bwd_workspace_bytes_max), else the default one."""
     td = torch.float32 if dtype == "f32" else torch.bfloat16
     tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(td)
                        for a in (q, k, v, do))
     o, lse = ct.flash_attn_fwd(tq, tk, tv, causal)
-    dq, dk, dv = ct.flash_attn_bwd(tq, tk, tv, o, tdo, lse, causal)
+    b, h, t, d = tq.shape
+    ws = torch.empty(ct._capi.bwd_workspace_bytes(td, b, h, t, d, causal, fastest=fastest), dtype=torch.uint8,
+                     device=DEV)
+    dq, dk, dv = ct.flash_attn_bwd(tq, tk, tv, o, tdo, lse, causal, workspace=ws)
     torch.cuda.synchronize()
     f = lambda t: t.float().cpu().numpy().astype(np.float64)  # noqa: E731
     return {"o": f(o), "lse": f(lse), "dq": f(dq), "dk": f(dk), "dv": f(dv)}
@@ -123,10 +128,10 @@ C4_HEAD_PAIRS = [(0, 4), (9, 13), (18, 22), (27, 31)]
 @pytest.fixture(scope="module")
 def c4_run():
     """Config 4: B1 H32 T8192 d128 bf16, N(0, 0.5^2) seed 4, causal -- one GPU fwd+bwd shared
-    by the c4 tests."""
+    by the c4 tests, with the workspace of the fastest path (the dK/dV kernel stores dS)."""
     q, k, v, do = ora.make_inputs(C4_SHAPE, seed=4, std=0.5, dtype="bf16")
     say("c4 full size bf16")
-    got = run_gpu(q, k, v, do, True, "bf16")
+    got = run_gpu(q, k, v, do, True, "bf16", fastest=True)
     return q, k, v, do, got
 
 
@@ -362,7 +367,7 @@ def test_misaligned_views_take_the_generic_kernels(dtype, causal):
 @pytest.mark.parametrize("shape", [(1, 3, 333, 128), (2, 2, 64, 128)], ids=lambda s: "x".join(map(str, s)))
 def test_bf16_d128_ds_and_recompute_paths(shape, causal, fmt):
     """bf16 at d = 128 stores dS in the workspace and the dQ kernel multiplies it by K when the
-    workspace ctattn_bwd_workspace_bytes asks for is given; a workspace without the dS tiles
+    workspace ctattn_bwd_workspace_bytes_max asks for is given; a workspace without the dS tiles
     (the minimum ctattn_bwd accepts) recomputes S and dP instead.  Both against the oracle, and
     one byte less than the minimum is refused."""
     b, h, t, d = shape
@@ -372,7 +377,7 @@ def test_bf16_d128_ds_and_recompute_paths(shape, causal, fmt):
     tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV).to(td)
                        for a in (q, k, v, do))
     o, lse = ct.flash_attn_fwd(tq, tk, tv, causal)
-    full = ct._capi.bwd_workspace_bytes(td, b, h, t, d, causal)
+    full = ct._capi.bwd_workspace_bytes(td, b, h, t, d, causal, fastest=True)
     nt = (t + 31) // 32
     ds_bytes = b * h * (nt * (nt + 1) // 2 if causal else nt * nt) * 2048
     lib = ct._capi.load()
@@ -396,8 +401,9 @@ def test_bf16_d128_ds_and_recompute_paths(shape, causal, fmt):
 
 
 def test_c4_ds_path_matches_recompute_path(c4_run):
-    """Config 4 at full size through the recomputing dQ kernel (a workspace without the dS
-    tiles) against the default run (dS stored by the dK/dV kernel): dK and dV come from the
+    """Config 4 at full size through the recomputing dQ kernel (the default workspace, which
+    at this shape holds no dS tiles) against the fastest-workspace run (dS stored by the dK/dV
+    kernel): dK and dV come from the
     same dK/dV kernel and agree bitwise; dQ agrees to bf16 rounding of dS (2e-2 of max |dQ| per
     head), and two heads of the recompute run against the oracle."""
     q, k, v, do, got = c4_run
@@ -407,7 +413,9 @@ def test_c4_ds_path_matches_recompute_path(c4_run):
                        for a in (q, k, v, do))
     o, lse = ct.flash_attn_fwd(tq, tk, tv, True)
     nt = (t + 31) // 32
-    nbytes = ct._capi.bwd_workspace_bytes(torch.bfloat16, b, h, t, d, True) - b * h * nt * (nt + 1) // 2 * 2048
+    nbytes = ct._capi.bwd_workspace_bytes(torch.bfloat16, b, h, t, d, True)
+    assert nbytes == ct._capi.bwd_workspace_bytes(torch.bfloat16, b, h, t, d, True, fastest=True) - \
+        b * h * nt * (nt + 1) // 2 * 2048
     ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
     rc = ct._capi.load().ctattn_bwd(1, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(), o.data_ptr(), tdo.data_ptr(),

@@ -3,8 +3,10 @@
 The entry point allocates nothing; its results must equal ctattn_bwd's (same kernels, the
 workspace only moves), on two calls in a row with the second problem smaller than the first
 (the scratch keeps the first call's contents), under the AUTO and DETERMINISTIC policies, on
-the MFMA (fp32, bf16, fp64) and generic (d = 48) kernels, on torch's current stream and on a
-second stream.  Bar: fp32 / fp64 max-abs <= 1e-4 (fp32 dQ is summed with atomics under AUTO,
+the MFMA kernels (fp32, bf16, fp64; d = 48 runs padded onto the d = 64 fp32 kernels) and the
+generic kernels (d = 160), on torch's current stream and on a second stream; a bf16 d = 128
+problem whose dS tiles exceed the scratch takes the recomputing dQ kernel; and a warmed-up
+call changes the device's free memory by nothing.  Bar: fp32 / fp64 max-abs <= 1e-4 (fp32 dQ is summed with atomics under AUTO,
 so it may differ in the last bits), bf16 max-rel <= 2e-2, and dK / dV -- written without
 atomics on every path -- bitwise equal.
 """
@@ -19,7 +21,8 @@ from cudatransformer_amd import _capi
 
 DEV = "cuda:0"
 SHAPES = [(2, 4, 300, None), (1, 2, 100, None)]  # second call smaller than the first
-CASES = [(torch.float32, 64), (torch.bfloat16, 128), (torch.float64, 64), (torch.float32, 48)]
+CASES = [(torch.float32, 64), (torch.bfloat16, 128), (torch.float64, 64), (torch.float32, 48),
+         (torch.float32, 160)]
 
 
 def say(msg):
@@ -70,3 +73,28 @@ def test_noalloc_matches_bwd(dtype, d, policy):
                     assert np.array_equal(x, y), f"{name}: not bitwise equal to ctattn_bwd ({err:.3e})"
     finally:
         _capi.set_policy(prev)
+
+
+@pytest.mark.gpu
+def test_noalloc_recompute_fallback_and_no_allocation():
+    """B1 H8 T4096 d128 bf16 causal: 135 MB of dS tiles, more than the 32 MiB scratch, so the
+    entry point runs the recomputing dQ kernel -- the path ctattn_bwd takes with its default
+    workspace at this shape -- and matches it bitwise.  A second call with preallocated
+    outputs leaves hipMemGetInfo's free memory unchanged."""
+    shape, causal = (1, 8, 4096, 128), True
+    say(f"noalloc bf16 recompute fallback shape={shape}")
+    nt = 4096 // 32
+    assert 8 * nt * (nt + 1) // 2 * 2048 > _capi.NOALLOC_SCRATCH_BYTES
+    g = torch.Generator(device=DEV).manual_seed(97)
+    q, k, v, do = ((0.5 * torch.randn(shape, generator=g, device=DEV)).to(torch.bfloat16) for _ in range(4))
+    o, lse = ct.flash_attn_fwd(q, k, v, causal)
+    ref = ct.flash_attn_bwd(q, k, v, o, do, lse, causal)
+    outs = tuple(torch.empty_like(q) for _ in range(3))
+    _capi.flash_attn_bwd_noalloc(q, k, v, o, do, lse, causal, *outs)
+    torch.cuda.synchronize()
+    for name, a, r in zip(("dq", "dk", "dv"), outs, ref):
+        assert torch.equal(a, r), f"{name}: not bitwise equal to ctattn_bwd's default path"
+    free0 = torch.cuda.mem_get_info()[0]
+    _capi.flash_attn_bwd_noalloc(q, k, v, o, do, lse, causal, *outs)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
