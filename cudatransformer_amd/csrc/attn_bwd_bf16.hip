@@ -165,11 +165,7 @@ __device__ __forceinline__ void kv_block(floatx16 (&dk_acc)[D / 32], floatx16 (&
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             u16x8 *dst = reinterpret_cast<u16x8 *>(reinterpret_cast<char *>(dsw) + Tile<32>::off(key_l, 2 * kk + half));
-#ifdef CTATTN_DS_NT
-            __builtin_nontemporal_store(__builtin_bit_cast(u16x8, dsb[kk]), dst);
-#else
             *dst = __builtin_bit_cast(u16x8, dsb[kk]);
-#endif
         }
     }
     // dV^T += dO^T P, dK^T += Q^T dS over the tile's 32 rows (two k-steps of 16).
