@@ -39,6 +39,12 @@ WORKLOADS = {
                          "B8 N1024 E1024 H16 D64 fp32, 1 GPU",
                   label="AttentionFloat(input_dim=1024, num_heads=16, head_dim=64) on X[8, 1024, 1024], "
                         "non-causal, the reference test's configuration (test_flash_attention.py:9-12) at N=1024"),
+    "layerbf": dict(B=8, H=16, T=1024, D=64, E=1024, dtype="bf16", std=1.0, peak=2516.6,
+                    metric="attention layer (QKV proj + attention + out proj) fwd+bwd TFLOP/s, "
+                           "B8 N1024 E1024 H16 D64 bf16, 1 GPU",
+                    label="AttentionBFloat(input_dim=1024, num_heads=16, head_dim=64) on X[8, 1024, 1024], "
+                          "non-causal: the reference test's configuration in bf16 storage (fp32 accumulation; "
+                          "projections on the 16-bit MFMA GEMMs)"),
     "c4": dict(B=1, H=32, T=8192, D=128, dtype="bf16", std=0.5, peak=2516.6,
                metric="causal attn fwd+bwd TFLOP/s + % MFMA peak, B1 H32 T8192 d128 bf16, 1 GPU",
                label="causal SDPA fwd+bwd, B1 H32 T8192 d128 bf16 in / fp32 accumulate (BASELINE configs[3])"),
@@ -184,7 +190,7 @@ def main():
         return bench_nanogpt(args, wl, dev)
     if args.workload == "c5n":
         return bench_native_nanogpt(args, wl)
-    if args.workload == "layer":
+    if args.workload in ("layer", "layerbf"):
         return bench_layer(args, wl)
     if args.workload == "tensor":
         return bench_tensor(args, wl)
@@ -430,13 +436,15 @@ def bench_layer(args, wl):
     b, h, n, d, e = wl["B"], wl["H"], wl["T"], wl["D"], wl["E"]
     hd = h * d
     rng = np.random.default_rng(12)
-    layer = ctm.AttentionFloat(input_dim=e, num_heads=h, head_dim=d)
+    suffix = "BFloat" if wl["dtype"] == "bf16" else "Float"
+    tensor = getattr(ctm, suffix + "Tensor")
+    layer = getattr(ctm, "Attention" + suffix)(input_dim=e, num_heads=h, head_dim=d)
     for part, shape, scale in (("Query", (hd, e), e), ("Key", (hd, e), e), ("Value", (hd, e), e),
                                ("Output", (e, hd), hd)):
-        getattr(layer, f"set{part}Weights")(ctm.FloatTensor.fromNumpy(
+        getattr(layer, f"set{part}Weights")(tensor.fromNumpy(
             (rng.standard_normal(shape) / np.sqrt(scale)).astype(np.float32)))
-    x = ctm.FloatTensor.fromNumpy(rng.standard_normal((b, n, e)).astype(np.float32))
-    dy = ctm.FloatTensor.fromNumpy(rng.standard_normal((b, n, e)).astype(np.float32))
+    x = tensor.fromNumpy(rng.standard_normal((b, n, e)).astype(np.float32))
+    dy = tensor.fromNumpy(rng.standard_normal((b, n, e)).astype(np.float32))
 
     def fwd():
         return layer(x)
@@ -466,7 +474,7 @@ def bench_layer(args, wl):
     out = {
         "metric": wl["metric"], "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None, "dtype": wl["dtype"], "data": "synthetic",
         "pct_of_peak": round(100.0 * value / wl["peak"], 2),
         "config": {"workload": wl["label"], "B": b, "N": n, "E": e, "H": h, "d": d, "causal": False,
                    "step_gflop": round(step_flop / 1e9, 3), "fwd_ms": round(fwd_ms, 5),

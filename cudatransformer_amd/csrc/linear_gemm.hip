@@ -1,10 +1,18 @@
-// Plain row-major fp32 GEMMs on v_mfma_f32_32x32x2f32 (gfx950): the linear layers' three
-// products and the Tensor matmul.
+// Split-K-in-workgroup MFMA GEMMs (gfx950): the linear layers' three products, the attention
+// layer's projections and the Tensor matmul, fp32 on v_mfma_f32_32x32x2f32 and bf16 / fp16 on
+// v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulation.
 //
 // Replaces the reference's tiled linear kernels (linear_kernels.cu:36-241: the forward
 // y = x W^T + b, the input gradient dX = dY W and the weight gradient dW += dY^T X, launched
-// from LinearLayer.cu:52-63,81-102 and from the un-embedding, Embedding.cu:344-397) and the
-// Tensor matmul (Tensor.cu:912-950).
+// from LinearLayer.cu:52-63,81-102 and from the un-embedding, Embedding.cu:344-397), its
+// projection kernels (attention_qkv_kernels.cu:51-364, attention_proj_kernels.cu:48-290) and
+// the Tensor matmul (Tensor.cu:912-950).
+//
+// Every operand is a separable 2-D view of memory (element (i, j) at row_off(i) + col_off(j)):
+// row-major, or the head-split view of a [B, H, T, d] tensor as a [B*T, H*d] matrix, so the
+// projections read and write the attention layout in place.  A launch computes up to three
+// independent products (Q, K, V) and sums up to three K segments into one output
+// (dX = dQ Wq + dK Wk + dV Wv).
 //
 // The products of a small transformer are skinny: 4096 x 384 outputs with K = 1536, or
 // 1536 x 384 weight gradients with K = 4096.  A classic 2-D tiling gives such an output only
@@ -13,31 +21,37 @@
 // the workgroup instead:
 //
 //   * a workgroup of NW waves owns one (32 TM) x (32 TN) tile of C; every wave accumulates
-//     the WHOLE tile over its own share of K -- the KW-deep K chunks w, w + NW, w + 2 NW, ...
-//     of the workgroup's K range -- so the tile count times NW fills the SIMDs evenly;
+//     the WHOLE tile over its own share of K -- the 64-byte K chunks w, w + NW, w + 2 NW, ...
+//     of the workgroup's K range (16 fp32 or 32 16-bit elements) -- so the tile count times
+//     NW fills the SIMDs evenly;
 //   * each wave streams its chunks global -> LDS directly (global_load_lds_dwordx4, 16 bytes
 //     per lane, no staging registers) through a private S-slot ring: the wave waits only for
 //     its own loads (s_waitcnt vmcnt) and no barrier runs in the main loop;
 //   * at the end the NW partial tiles meet in LDS and are added in wave order (fixed order:
 //     bitwise reproducible), bias and the old C (beta) are added, and the tile is stored with
-//     coalesced 16-byte stores;
+//     coalesced vector stores;
 //   * when even that leaves SIMDs idle (weight gradients: small C, long K), K is also split
 //     across workgroups; their partial tiles go to a caller workspace and a second kernel adds
 //     them in split order (still deterministic, no atomics).
 //
-// Operand tiles in LDS.  The MFMA takes A[i][kk] from lane (i, kk) and B[kk][j] from lane
+// Operand tiles in LDS.  The fp32 MFMA takes A[i][kk] from lane (i, kk) and B[kk][j] from lane
 // (j, kk); a lane reads four contraction indices k = 8 s + 4 h + t (t = 0..3) at once and
-// feeds them to four consecutive MFMAs (h = lane / 32), for both operands, so the pairing of
-// A and B indices is consistent.
-//   * K-contiguous operand (A stored [m][k], B stored [n][k]): LDS [row][KW] -- one
-//     ds_read_b128 per lane gives four MFMAs' operands.  16-byte chunk c of row r sits at
-//     physical chunk c ^ swz(r), so the 16 lanes that one LDS cycle serves (16 rows, one
-//     chunk) hit 16 distinct bank groups.
-//   * M/N-contiguous operand (A stored [k][m], B stored [k][n]): LDS [k][rows] -- one
+// feeds them to four consecutive MFMAs (h = lane / 32).  The 16-bit MFMA takes eight
+// consecutive k = 16 s + 8 h + 0..7 from one lane per instruction.  Either way a lane's
+// operand for step s is 16 bytes, and A and B pair the same indices.
+//   * K-contiguous operand (A stored [m][k], B stored [n][k]): LDS [row][64 bytes] -- one
+//     ds_read_b128 per lane per step.  16-byte chunk c of row r sits at physical chunk
+//     c ^ swz(r), so the 16 lanes that one LDS cycle serves (16 rows, one chunk) hit 16
+//     distinct bank groups.
+//   * M/N-contiguous operand (A stored [k][m], B stored [k][n]), fp32: LDS [16 k][rows] -- one
 //     ds_read_b32 per lane per MFMA, lanes 0-31 on k-row kk and lanes 32-63 on kk + 4.  Those
 //     two k-rows are kept on different halves of the 64 banks: by swapping row positions
 //     (tiles 32 or 96 wide, whose rows alternate halves) or by flipping chunk bit 3 (64 or 128
 //     wide).
+//   * M/N-contiguous operand, 16-bit: LDS [32 k][rows] -- two ds_read_b64_tr_b16 per lane per
+//     step (each: a 16-lane group reads 4 k-rows x 16 columns and lane l receives column l's
+//     four values).  The 64-byte segment index of a k-row is XOR-swizzled by the row so the 32
+//     lanes of one LDS cycle (4 k-rows x 32 columns) cover the 64 banks once.
 // The direct-to-LDS load writes 64 consecutive 16-byte chunks per instruction; the swizzle
 // is applied by choosing which global chunk each lane fetches.  Rows / columns past the
 // matrix edge re-read the last valid one; their results are never stored.
@@ -46,6 +60,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "attn_common.h"
 #include "attn_mfma_common.h"
 
 namespace ctattn {
@@ -54,10 +69,19 @@ namespace lin {
 typedef __attribute__((address_space(3))) const floatx4 lds_cf4;
 typedef __attribute__((address_space(3))) const float lds_cf;
 typedef __attribute__((address_space(3))) float lds_f;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ floatx4 ld4(uint32_t addr) { return *(lds_cf4 *)(uintptr_t)addr; }
 __device__ __forceinline__ float ld1(uint32_t addr) { return *(lds_cf *)(uintptr_t)addr; }
 __device__ __forceinline__ void st1(uint32_t addr, float x) { *(lds_f *)(uintptr_t)addr = x; }
+__device__ __forceinline__ i16x4 ldtr(uint32_t addr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(uintptr_t)addr);
+}
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return uint32_t(uintptr_t((__attribute__((address_space(3))) const char *)p));
@@ -79,56 +103,122 @@ template <int N> __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// K-contiguous operand: R rows x KW k per stage, LDS [r][KW], chunk c of row r at physical
-// chunk c ^ swz(r).  Rows are 4 KW bytes: for KW = 32 (8 chunks) the 16 rows of one LDS cycle
-// cover bank groups 8 (r & 1) + (c ^ ((r >> 1) & 7)); for KW = 16 (4 chunks) 4 (r & 3) +
-// (c ^ ((r >> 2) & 3)): distinct either way.
-template <int R, int KW>
+// ---- element formats ----
+
+struct F32Fmt {
+    static constexpr int EB = 4;    // bytes per element
+    static constexpr int KWE = 16;  // elements per 64-byte K chunk
+    static constexpr bool WIDE = true;
+    __device__ static float load(const char *p) { return *reinterpret_cast<const float *>(p); }
+    __device__ static floatx4 load4(const char *p) { return *reinterpret_cast<const floatx4 *>(p); }
+    __device__ static void store(char *p, float x) { *reinterpret_cast<float *>(p) = x; }
+    __device__ static void store4(char *p, floatx4 x) { *reinterpret_cast<floatx4 *>(p) = x; }
+};
+template <bool BF>
+struct H16Fmt {
+    static constexpr int EB = 2;
+    static constexpr int KWE = 32;
+    static constexpr bool WIDE = false;
+    __device__ static float widen(uint16_t b) {
+        return BF ? __uint_as_float(uint32_t(b) << 16) : float(__builtin_bit_cast(_Float16, b));
+    }
+    __device__ static uint16_t narrow(float x) {
+        return BF ? f32_to_bf16(x).bits : __builtin_bit_cast(uint16_t, _Float16(x));
+    }
+    __device__ static floatx16 mfma(floatx4 a, floatx4 b, floatx16 c) {
+        if constexpr (BF)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                           c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                          0, 0, 0);
+    }
+    __device__ static float load(const char *p) { return widen(*reinterpret_cast<const uint16_t *>(p)); }
+    __device__ static floatx4 load4(const char *p) {
+        const u16x4 u = *reinterpret_cast<const u16x4 *>(p);
+        return floatx4{widen(u[0]), widen(u[1]), widen(u[2]), widen(u[3])};
+    }
+    __device__ static void store(char *p, float x) { *reinterpret_cast<uint16_t *>(p) = narrow(x); }
+    __device__ static void store4(char *p, floatx4 x) {
+        *reinterpret_cast<u16x4 *>(p) = u16x4{narrow(x[0]), narrow(x[1]), narrow(x[2]), narrow(x[3])};
+    }
+};
+using BF16Fmt = H16Fmt<true>;
+using F16Fmt = H16Fmt<false>;
+
+// ---- views ----
+
+// A LinView on the device, in bytes.  Indices are below 2^31 (checked on the host).
+struct DView {
+    int64_t ld_b;    // linear: row pitch
+    int64_t bstr_b;  // head-split: one batch, H*T*d elements
+    int64_t hstr_b;  // head-split: one head, T*d elements
+    int32_t heads, T, d, eb;
+};
+__device__ __forceinline__ int64_t rowoff(const DView &v, int i) {
+    if (v.heads == 0) return int64_t(i) * v.ld_b;
+    const int b = i / v.T;
+    return int64_t(b) * v.bstr_b + int64_t(i - b * v.T) * (v.d * v.eb);
+}
+__device__ __forceinline__ int64_t coloff(const DView &v, int j) {
+    if (v.heads == 0) return int64_t(j) * v.eb;
+    const int h = j / v.d;
+    return int64_t(h) * v.hstr_b + int64_t(j - h * v.d) * v.eb;
+}
+// Byte distance between consecutive rows inside one K chunk of an M/N-contiguous operand (a
+// chunk never crosses a batch of a head-split view: T is a multiple of the chunk).
+__device__ __forceinline__ int64_t krow_b(const DView &v) { return v.heads == 0 ? v.ld_b : int64_t(v.d) * v.eb; }
+
+// ---- operand tiles ----
+
+// K-contiguous operand: R rows x 64 bytes per stage, LDS [r][64 B], chunk c of row r at
+// physical chunk c ^ swz(r): the 16 rows of one LDS cycle cover bank groups
+// 4 (r & 3) + (c ^ ((r >> 2) & 3)), all distinct.
+template <int R>
 struct OpKC {
-    static constexpr int CH = KW / 4;
-    static constexpr int BYTES = R * KW * 4;
+    static constexpr int CH = 4;  // 16-byte chunks per row
+    static constexpr int BYTES = R * 64;
     static constexpr int NL = BYTES / 1024;  // load instructions per stage
-    static_assert(KW == 16 || KW == 32, "K chunk of 16 or 32 fp32");
     static_assert(BYTES % 1024 == 0, "a stage is whole 1 KiB load instructions");
-    __host__ __device__ static constexpr int swz(int r) { return CH == 8 ? (r >> 1) & 7 : (r >> 2) & 3; }
-    // Byte offset of load instruction i's lane from the stage origin (row 0, chunk 0); rows at
-    // or past `rows_left` re-read row rows_left - 1.
-    __device__ static uint32_t voff(int i, int lane, int64_t ld_bytes, int rows_left) {
+    __host__ __device__ static constexpr int swz(int r) { return (r >> 2) & 3; }
+    // Lane offset of load instruction i from the stage origin (row 0, chunk 0 of the tile);
+    // rows at or past `rows` re-read row rows - 1.
+    __device__ static uint32_t voff(int i, int lane, const DView &v, int r0, int rows) {
         const int P = 64 * i + lane;
         const int r = P / CH;
         const int lc = (P % CH) ^ swz(r);
-        return uint32_t(int64_t(min(r, rows_left - 1)) * ld_bytes + 16 * lc);
+        return uint32_t(rowoff(v, r0 + min(r, rows - 1)) - rowoff(v, r0) + 16 * lc);
     }
-    // Per-lane read offsets: offs[s] for k-group s (k = 8 s .. 8 s + 7) of 32-row tile 0.
+    // Read of step s (16 bytes: k-group s of lane half h) of 32-row tile tt.
     struct Lane {
-        uint32_t offs[KW / 8];
-        __device__ void init(int col, int h) {
+        uint32_t offs[2];
+        __device__ void init(int lane) {
+            const int col = lane & 31, h = lane >> 5;
 #pragma unroll
-            for (int s = 0; s < KW / 8; ++s) offs[s] = uint32_t(col * KW * 4 + ((((2 * s) | h) ^ swz(col)) << 4));
+            for (int s = 0; s < 2; ++s) offs[s] = uint32_t(col * 64 + ((((2 * s) | h) ^ swz(col)) << 4));
         }
-        __device__ floatx4 read(uint32_t base, int tt, int s) const { return ld4(base + tt * 32 * KW * 4 + offs[s]); }
+        __device__ floatx4 read(uint32_t base, int tt, int s) const { return ld4(base + tt * 32 * 64 + offs[s]); }
     };
 };
 
-// M/N-contiguous operand: KW k-rows x R columns per stage, LDS [k][R] (row pitch 4 R bytes).
-template <int R, int KW>
-struct OpMN {
-    static constexpr int CHR = R / 4;
-    static constexpr int BYTES = R * KW * 4;
+// M/N-contiguous fp32 operand: 16 k-rows x R columns per stage, LDS [k][R] (row pitch 4 R).
+template <int R>
+struct OpMN32 {
+    static constexpr int CHR = R / 4;  // 16-byte chunks per k-row
+    static constexpr int BYTES = R * 64;
     static constexpr int NL = BYTES / 1024;
     static constexpr bool ODD = (R / 32) % 2 == 1;  // rows alternate bank halves
     static_assert(R % 32 == 0 && R <= 128, "tile width 32, 64, 96 or 128");
-    static_assert(BYTES % 1024 == 0, "a stage is whole 1 KiB load instructions");
     // k-row kk sits at row position kk ^ ((kk >> 2) & 1) (ODD); chunk c of k-row kk at
     // physical chunk c ^ (8 ((kk >> 2) & 1)) (!ODD).  Both maps are involutions.
     __host__ __device__ static constexpr int rowpos(int kk) { return ODD ? kk ^ ((kk >> 2) & 1) : kk; }
     __host__ __device__ static constexpr int chunk(int kk, int c) { return ODD ? c : c ^ (((kk >> 2) & 1) << 3); }
-    // Columns at or past `cols_left` (a multiple of 4) re-read the last valid chunk.
-    __device__ static uint32_t voff(int i, int lane, int64_t ld_bytes, int cols_left) {
+    // Columns at or past `cols` (a multiple of 4) re-read the last valid chunk.
+    __device__ static uint32_t voff(int i, int lane, const DView &v, int c0, int cols) {
         const int P = 64 * i + lane;
         const int kk = rowpos(P / CHR);
         const int lc = chunk(kk, P % CHR);
-        return uint32_t(int64_t(kk) * ld_bytes + 4 * min(4 * lc, cols_left - 4));
+        return uint32_t(int64_t(kk) * krow_b(v) + coloff(v, c0 + min(4 * lc, cols - 4)) - coloff(v, c0));
     }
     // Element (kk = 8 s + 4 h + t, column 32 tt + col) at
     //   ODD:  rowpos(kk) * 4R + 4 (32 tt + col), rowpos(kk) = 8 s + 4 h + (t ^ h);
@@ -136,8 +226,9 @@ struct OpMN {
     struct Lane {
         uint32_t offt[4];  // per t, tile 0
         int h;
-        __device__ void init(int col, int hh) {
-            h = hh;
+        __device__ void init(int lane) {
+            const int col = lane & 31;
+            h = lane >> 5;
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 offt[t] = uint32_t((ODD ? 4 * h + (t ^ h) : 4 * h + t) * 4 * R + 4 * col + (ODD ? 0 : 128 * h));
@@ -153,27 +244,69 @@ struct OpMN {
     };
 };
 
-struct Args {
-    const char *a, *b;
-    float *c;
-    const float *bias;
-    float *ws;             // split-K partials: splits x M x N floats
-    int64_t lda_b, ldb_b;  // operand pitches in bytes
-    int64_t ldc;           // elements
-    int32_t M, N;
-    int32_t tiles_m, tiles_n;
-    int32_t splits;
-    int32_t chunks;  // K / KW
-    int32_t cps;     // chunks per split
-    int32_t beta;
-    int32_t vec_out;  // C takes 16-byte stores (N % 4 == 0, ldc % 4 == 0, c aligned)
+// M/N-contiguous 16-bit operand: 32 k-rows x R columns per stage, LDS [k][R] (row pitch 2 R),
+// the 64-byte segment sg of k-row kr at physical segment sg ^ gsw(kr).
+template <int R>
+struct OpMN16 {
+    static constexpr int BYTES = R * 64;
+    static constexpr int NL = BYTES / 1024;
+    static constexpr int PITCH = 2 * R;
+    static constexpr int SEGS = R / 32;
+    static_assert(R == 32 || R == 64 || R == 128, "tile width 32, 64 or 128");
+    __host__ __device__ static constexpr int gsw(int kr) {
+        return SEGS == 4 ? (kr & 3) : SEGS == 2 ? ((kr >> 1) & 1) : 0;
+    }
+    // Columns at or past `cols` (a multiple of 8) re-read the last valid chunk.
+    __device__ static uint32_t voff(int i, int lane, const DView &v, int c0, int cols) {
+        const int P = 64 * i + lane;
+        const int kr = P / (R / 8);
+        const int lc = (P % (R / 8)) ^ (gsw(kr) << 2);
+        return uint32_t(int64_t(kr) * krow_b(v) + coloff(v, c0 + min(8 * lc, cols - 8)) - coloff(v, c0));
+    }
+    // Step s, lane (16-lane group g, sl = lane % 16): rows 16 s + 8 (g >> 1) + sl / 4 (+ 4 for
+    // the second read), columns 32 tt + 16 (g & 1) + 4 (sl % 4) .. + 3; the lane receives its
+    // column's 4 + 4 values, k = 16 s + 8 h + 0..7 in order.  gsw of those rows is the same
+    // for every s and both reads.
+    struct Lane {
+        uint32_t off;
+        int gs;
+        __device__ void init(int lane) {
+            const int g = lane >> 4, sl = lane & 15;
+            const int row = 8 * (g >> 1) + (sl >> 2);
+            gs = gsw(row);
+            off = uint32_t(row * PITCH + 32 * (g & 1) + 8 * (sl & 3));
+        }
+        __device__ floatx4 read(uint32_t base, int tt, int s) const {
+            const uint32_t a = base + off + uint32_t((tt ^ gs) * 64 + 16 * s * PITCH);
+            const i16x4 lo = ldtr(a), hi = ldtr(a + 4 * PITCH);
+            const i16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            return __builtin_bit_cast(floatx4, x);
+        }
+    };
 };
 
-template <bool A_KC, bool B_KC, int TM, int TN, int NW, int KW, int S>
+struct Args {
+    const char *a[kLinMaxBatch][kLinMaxSeg];
+    const char *b[kLinMaxBatch][kLinMaxSeg];
+    char *c[kLinMaxBatch];
+    const char *bias[kLinMaxBatch];
+    float *ws;  // split-K partials: [batch][split][M][N] fp32
+    DView av, bv, cv;
+    int32_t M, N;
+    int32_t tiles_m, tiles_n;
+    int32_t splits, nbatch;
+    int32_t chunks;      // K chunks over all segments
+    int32_t seg_chunks;  // K chunks per segment
+    int32_t cps;         // chunks per split
+    int32_t beta;
+    int32_t vec_out;  // C takes 4-column vector stores
+};
+
+template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
 struct Cfg {
     static constexpr int BM = 32 * TM, BN = 32 * TN;
-    using OA = std::conditional_t<A_KC, OpKC<BM, KW>, OpMN<BM, KW>>;
-    using OB = std::conditional_t<B_KC, OpKC<BN, KW>, OpMN<BN, KW>>;
+    using OA = std::conditional_t<A_KC, OpKC<BM>, std::conditional_t<F::WIDE, OpMN32<BM>, OpMN16<BM>>>;
+    using OB = std::conditional_t<B_KC, OpKC<BN>, std::conditional_t<F::WIDE, OpMN32<BN>, OpMN16<BN>>>;
     static constexpr int STAGE = OA::BYTES + OB::BYTES;
     static constexpr int L = OA::NL + OB::NL;  // load instructions per stage
     static constexpr int PIPE = NW * S * STAGE;
@@ -195,9 +328,14 @@ __device__ __forceinline__ void wait_tail(int r) {
     }
 }
 
-template <bool A_KC, bool B_KC, int TM, int TN, int NW, int KW, int S>
-__global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
-    using C = Cfg<A_KC, B_KC, TM, TN, NW, KW, S>;
+// Wave-uniform base of segment `seg` (seg < 3): a select, not an indexed register array.
+__device__ __forceinline__ const char *pick(const char *const (&arr)[kLinMaxSeg], int seg) {
+    return seg == 0 ? arr[0] : seg == 1 ? arr[1] : arr[2];
+}
+
+template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
+__global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
+    using C = Cfg<F, A_KC, B_KC, TM, TN, NW, S>;
     using OA = typename C::OA;
     using OB = typename C::OB;
     constexpr int BM = C::BM, BN = C::BN;
@@ -205,7 +343,7 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-    const int col = lane & 31, h = lane >> 5;
+    const int h = lane >> 5, col = lane & 31;
 
     // Workgroup b runs on XCD b % 8.  XCD x takes the contiguous work items [x q, x q + q), so
     // the workgroups of one XCD share A row blocks (consecutive items: same tile row) in its L2.
@@ -213,8 +351,11 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
     const int q = nblk >> 3;
     const int work = blk < 8 * q ? (blk & 7) * q + (blk >> 3) : blk;
     const int ntiles = p.tiles_m * p.tiles_n;
-    const int split = work / ntiles;
-    const int tile = work - split * ntiles;
+    const int per_batch = ntiles * p.splits;
+    const int z = work / per_batch;
+    const int rem = work - z * per_batch;
+    const int split = rem / ntiles;
+    const int tile = rem - split * ntiles;
     const int ti = tile / p.tiles_n;
     const int m0 = ti * BM, n0 = (tile - ti * p.tiles_n) * BN;
 
@@ -224,26 +365,34 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
     const int c_first = c_begin + wave;
     const int nst = c_first < c_end ? (c_end - c_first + NW - 1) / NW : 0;
 
-    const char *ga = p.a + (A_KC ? int64_t(m0) * p.lda_b + int64_t(c_first) * KW * 4
-                                 : int64_t(c_first) * KW * p.lda_b + int64_t(m0) * 4);
-    const char *gb = p.b + (B_KC ? int64_t(n0) * p.ldb_b + int64_t(c_first) * KW * 4
-                                 : int64_t(c_first) * KW * p.ldb_b + int64_t(n0) * 4);
-    const int64_t da = A_KC ? int64_t(NW) * KW * 4 : int64_t(NW) * KW * p.lda_b;
-    const int64_t db = B_KC ? int64_t(NW) * KW * 4 : int64_t(NW) * KW * p.ldb_b;
+    // Tile origins (the M / N offset of the tile; the K offset is added per chunk).
+    const char *a_seg[kLinMaxSeg], *b_seg[kLinMaxSeg];
+    const int64_t a_t = A_KC ? rowoff(p.av, m0) : coloff(p.av, m0);
+    const int64_t b_t = B_KC ? rowoff(p.bv, n0) : coloff(p.bv, n0);
+#pragma unroll
+    for (int s = 0; s < kLinMaxSeg; ++s) {
+        a_seg[s] = p.a[z][s] + a_t;
+        b_seg[s] = p.b[z][s] + b_t;
+    }
 
     uint32_t va[OA::NL], vb[OB::NL];
 #pragma unroll
-    for (int i = 0; i < OA::NL; ++i) va[i] = OA::voff(i, lane, p.lda_b, p.M - m0);
+    for (int i = 0; i < OA::NL; ++i) va[i] = OA::voff(i, lane, p.av, m0, p.M - m0);
 #pragma unroll
-    for (int i = 0; i < OB::NL; ++i) vb[i] = OB::voff(i, lane, p.ldb_b, p.N - n0);
+    for (int i = 0; i < OB::NL; ++i) vb[i] = OB::voff(i, lane, p.bv, n0, p.N - n0);
     typename OA::Lane ra;
     typename OB::Lane rb;
-    ra.init(col, h);
-    rb.init(col, h);
+    ra.init(lane);
+    rb.init(lane);
 
     const uint32_t wbase = lds_addr(smem) + uint32_t(wave * S * C::STAGE);
 
-    auto issue = [&](int slot) {
+    auto issue = [&](int slot, int j) {
+        const int c = c_first + j * NW;
+        const int seg = p.seg_chunks == p.chunks ? 0 : c / p.seg_chunks;
+        const int kk = (c - seg * p.seg_chunks) * F::KWE;
+        const char *ga = pick(a_seg, seg) + (A_KC ? coloff(p.av, kk) : rowoff(p.av, kk));
+        const char *gb = pick(b_seg, seg) + (B_KC ? coloff(p.bv, kk) : rowoff(p.bv, kk));
         const uint32_t sa = wbase + uint32_t(slot * C::STAGE);
         // The slot's previous contents were read by the last stage's MFMAs: those reads have
         // returned (their results were consumed), this makes it explicit.
@@ -252,8 +401,6 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
         for (int i = 0; i < OA::NL; ++i) dma16(ga, va[i], sa + uint32_t(1024 * i));
 #pragma unroll
         for (int i = 0; i < OB::NL; ++i) dma16(gb, vb[i], sa + uint32_t(OA::BYTES + 1024 * i));
-        ga += da;
-        gb += db;
     };
 
     floatx16 acc[TM][TN];
@@ -263,11 +410,11 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
         for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
 
     const int pro = min(S - 1, nst);
-    for (int j = 0; j < pro; ++j) issue(j);
+    for (int j = 0; j < pro; ++j) issue(j, j);
     int slot = 0, islot = S - 1;
     for (int j = 0; j < nst; ++j) {
         if (j + S - 1 < nst) {
-            issue(islot);
+            issue(islot, j + S - 1);
             wait_vm<(S - 1) * C::L>();
         } else {
             wait_tail<C::L, S>(nst - 1 - j);
@@ -275,19 +422,26 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
         const uint32_t sa = wbase + uint32_t(slot * C::STAGE);
         const uint32_t sb = sa + uint32_t(OA::BYTES);
 #pragma unroll
-        for (int s = 0; s < KW / 8; ++s) {
+        for (int s = 0; s < 2; ++s) {
             floatx4 av[TM], bv[TN];
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) av[tm] = ra.read(sa, tm, s);
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) bv[tn] = rb.read(sb, tn, s);
+            if constexpr (F::WIDE) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < TN; ++tn)
+                            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[tm][t], bv[tn][t], acc[tm][tn], 0, 0, 0);
+            } else {
 #pragma unroll
                 for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-                    for (int tn = 0; tn < TN; ++tn)
-                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[tm][t], bv[tn][t], acc[tm][tn], 0, 0, 0);
+                    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = F::mfma(av[tm], bv[tn], acc[tm][tn]);
+            }
         }
         slot = slot + 1 == S ? 0 : slot + 1;
         islot = islot + 1 == S ? 0 : islot + 1;
@@ -309,6 +463,8 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
 
     // Sum the partials in wave order and store, 4 columns per thread.
     constexpr int Q = BM * BN / 4;
+    char *const cz = p.c[z];
+    const char *const bz = p.bias[z];
     for (int qi = int(threadIdx.x); qi < Q; qi += NW * 64) {
         const int m = qi / (BN / 4);
         const int n = (qi - m * (BN / 4)) * 4;
@@ -318,7 +474,7 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
 #pragma unroll
         for (int w = 1; w < NW; ++w) x += ld4(red + uint32_t(((w * BM + m) * BN + n) * 4));
         if (p.splits > 1) {
-            float *dst = p.ws + (int64_t(split) * p.M + gm) * p.N + gn;
+            float *dst = p.ws + ((int64_t(z) * p.splits + split) * p.M + gm) * p.N + gn;
             if (p.N % 4 == 0) {
                 *reinterpret_cast<floatx4 *>(dst) = x;
             } else {
@@ -328,47 +484,51 @@ __global__ __launch_bounds__(NW * 64) void lin_f32_kernel(Args p) {
             }
             continue;
         }
-        float *dst = p.c + int64_t(gm) * p.ldc + gn;
         if (p.vec_out) {
-            if (p.bias != nullptr) x += *reinterpret_cast<const floatx4 *>(p.bias + gn);
-            if (p.beta) x += *reinterpret_cast<const floatx4 *>(dst);
-            *reinterpret_cast<floatx4 *>(dst) = x;
+            char *dst = cz + rowoff(p.cv, gm) + coloff(p.cv, gn);
+            if (bz != nullptr) x += F::load4(bz + int64_t(gn) * F::EB);
+            if (p.beta) x += F::load4(dst);
+            F::store4(dst, x);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (gn + e >= p.N) break;
+                char *de = cz + rowoff(p.cv, gm) + coloff(p.cv, gn + e);
                 float y = x[e];
-                if (p.bias != nullptr) y += p.bias[gn + e];
-                if (p.beta) y += dst[e];
-                dst[e] = y;
+                if (bz != nullptr) y += F::load(bz + int64_t(gn + e) * F::EB);
+                if (p.beta) y += F::load(de);
+                F::store(de, y);
             }
         }
     }
 }
 
-// C(m, n) [+]= sum over splits z = 0, 1, ... of ws[z][m][n] (+ bias[n]), 4 columns per thread
-// when N % 4 == 0 (vec), else one.
-__global__ __launch_bounds__(256) void lin_splitk_reduce_kernel(const float *ws, int splits, int M, int N, float *c,
-                                                                int64_t ldc, const float *bias, int beta, int vec) {
+// C_z(m, n) [+]= sum over splits s = 0, 1, ... of ws[z][s][m][n] (+ bias_z[n]), 4 columns per
+// thread when vec (N % 4 == 0, aligned C), else one.
+template <typename F>
+__global__ __launch_bounds__(256) void lin_splitk_reduce_kernel(Args p, int64_t items_per_batch, int vec) {
     const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t mn = int64_t(M) * N;
+    const int z = int(blockIdx.y);
+    if (idx >= items_per_batch) return;
     const int w = vec ? 4 : 1;
-    if (idx * w >= mn) return;
+    const int64_t mn = int64_t(p.M) * p.N;
     const int64_t e0 = idx * w;
-    const int m = int(e0 / N), n = int(e0 - int64_t(m) * N);
-    float *dst = c + int64_t(m) * ldc + n;
+    const int m = int(e0 / p.N), n = int(e0 - int64_t(m) * p.N);
+    const float *src = p.ws + int64_t(z) * p.splits * mn + e0;
+    const char *bz = p.bias[z];
+    char *dst = p.c[z] + rowoff(p.cv, m) + coloff(p.cv, n);
     if (vec) {
-        floatx4 x = *reinterpret_cast<const floatx4 *>(ws + e0);
-        for (int z = 1; z < splits; ++z) x += *reinterpret_cast<const floatx4 *>(ws + z * mn + e0);
-        if (bias != nullptr) x += *reinterpret_cast<const floatx4 *>(bias + n);
-        if (beta) x += *reinterpret_cast<const floatx4 *>(dst);
-        *reinterpret_cast<floatx4 *>(dst) = x;
+        floatx4 x = *reinterpret_cast<const floatx4 *>(src);
+        for (int s = 1; s < p.splits; ++s) x += *reinterpret_cast<const floatx4 *>(src + s * mn);
+        if (bz != nullptr) x += F::load4(bz + int64_t(n) * F::EB);
+        if (p.beta) x += F::load4(dst);
+        F::store4(dst, x);
     } else {
-        float x = ws[e0];
-        for (int z = 1; z < splits; ++z) x += ws[z * mn + e0];
-        if (bias != nullptr) x += bias[n];
-        if (beta) x += *dst;
-        *dst = x;
+        float x = src[0];
+        for (int s = 1; s < p.splits; ++s) x += src[s * mn];
+        if (bz != nullptr) x += F::load(bz + int64_t(n) * F::EB);
+        if (p.beta) x += F::load(dst);
+        F::store(dst, x);
     }
 }
 
@@ -381,160 +541,251 @@ struct Plan {
 
 // One launchable configuration.
 struct CfgInfo {
-    int tm, tn, nw, kw, s;
-    int lds;
+    int tm, tn, nw, s;
     hipError_t (*launch)(const Args &, int nblk, hipStream_t);
 };
 
-template <bool A_KC, bool B_KC, int TM, int TN, int NW, int KW, int S>
+template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
 hipError_t launch_cfg(const Args &a, int nblk, hipStream_t stream) {
-    hipLaunchKernelGGL((lin_f32_kernel<A_KC, B_KC, TM, TN, NW, KW, S>), dim3(unsigned(nblk)), dim3(NW * 64), 0,
-                       stream, a);
+    hipLaunchKernelGGL((lin_kernel<F, A_KC, B_KC, TM, TN, NW, S>), dim3(unsigned(nblk)), dim3(NW * 64), 0, stream,
+                       a);
     return hipGetLastError();
 }
 
-template <bool A_KC, bool B_KC, int TM, int TN, int NW, int KW, int S>
+template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
 constexpr CfgInfo cfg_info() {
-    return CfgInfo{TM, TN, NW, KW, S, Cfg<A_KC, B_KC, TM, TN, NW, KW, S>::LDS,
-                   &launch_cfg<A_KC, B_KC, TM, TN, NW, KW, S>};
+    return CfgInfo{TM, TN, NW, S, &launch_cfg<F, A_KC, B_KC, TM, TN, NW, S>};
+}
+
+inline int elem_bytes(int dtype) { return dtype == 0 ? 4 : 2; }
+inline int chunk_elems(int dtype) { return 64 / elem_bytes(dtype); }
+
+inline DView dview(const LinView &v, int eb) {
+    DView d{};
+    d.heads = v.heads;
+    d.T = v.T;
+    d.d = v.d;
+    d.eb = eb;
+    d.ld_b = v.ld * eb;
+    d.hstr_b = int64_t(v.T) * v.d * eb;
+    d.bstr_b = int64_t(v.heads) * v.T * v.d * eb;
+    return d;
+}
+
+inline int64_t splits_bytes(const LinGemm &g, int splits) {
+    return splits > 1 ? int64_t(splits) * g.nbatch * g.M * g.N * 4 : 0;
 }
 
 // Builds the kernel arguments of a product for a configuration and split count; returns the
 // workgroup count.
 inline int make_args(const LinGemm &g, const CfgInfo &c, int splits, void *ws, Args &a) {
+    const int eb = elem_bytes(g.dtype);
     const int bm = 32 * c.tm, bn = 32 * c.tn;
-    a.a = static_cast<const char *>(g.a);
-    a.b = static_cast<const char *>(g.b);
-    a.c = static_cast<float *>(g.c);
-    a.bias = static_cast<const float *>(g.bias);
+    for (int z = 0; z < kLinMaxBatch; ++z) {
+        const int zz = z < g.nbatch ? z : 0;
+        for (int s = 0; s < kLinMaxSeg; ++s) {
+            const int ss = s < g.nseg ? s : 0;
+            a.a[z][s] = static_cast<const char *>(g.a[zz][ss]);
+            a.b[z][s] = static_cast<const char *>(g.b[zz][ss]);
+        }
+        a.c[z] = static_cast<char *>(g.c[zz]);
+        a.bias[z] = static_cast<const char *>(g.bias[zz]);
+    }
     a.ws = static_cast<float *>(ws);
-    a.lda_b = g.lda * 4;
-    a.ldb_b = g.ldb * 4;
-    a.ldc = g.ldc;
+    a.av = dview(g.av, eb);
+    a.bv = dview(g.bv, eb);
+    a.cv = dview(g.cv, eb);
     a.M = int32_t(g.M);
     a.N = int32_t(g.N);
     a.tiles_m = int32_t((g.M + bm - 1) / bm);
     a.tiles_n = int32_t((g.N + bn - 1) / bn);
-    a.chunks = int32_t(g.K / c.kw);
+    a.nbatch = g.nbatch;
+    a.seg_chunks = int32_t(g.K / chunk_elems(g.dtype));
+    a.chunks = a.seg_chunks * g.nseg;
     a.cps = (a.chunks + splits - 1) / splits;
     a.splits = (a.chunks + a.cps - 1) / a.cps;  // no empty split
     a.beta = g.beta ? 1 : 0;
-    a.vec_out = g.N % 4 == 0 && g.ldc % 4 == 0 && uintptr_t(g.c) % 16 == 0 &&
-                (g.bias == nullptr || uintptr_t(g.bias) % 16 == 0);
-    return a.tiles_m * a.tiles_n * a.splits;
+    bool vec = g.N % 4 == 0;
+    for (int z = 0; z < g.nbatch; ++z)
+        vec = vec && uintptr_t(g.c[z]) % (4 * eb) == 0 && (g.bias[z] == nullptr || uintptr_t(g.bias[z]) % (4 * eb) == 0);
+    if (g.cv.heads == 0) vec = vec && g.cv.ld % 4 == 0;
+    a.vec_out = vec ? 1 : 0;
+    return a.tiles_m * a.tiles_n * a.splits * g.nbatch;
 }
 
-inline hipError_t run(const LinGemm &g, const CfgInfo &c, int splits, void *ws, int64_t ws_bytes,
-                      hipStream_t stream) {
+template <typename F>
+hipError_t run(const LinGemm &g, const CfgInfo &c, int splits, void *ws, int64_t ws_bytes, hipStream_t stream) {
     Args a{};
     const int nblk = make_args(g, c, splits, ws, a);
-    // Split-K partials: a.splits x M x N floats, which the workspace must hold.
-    if (a.splits > 1 && (ws == nullptr || ws_bytes < int64_t(a.splits) * g.M * g.N * 4)) return hipErrorInvalidValue;
+    if (a.splits > 1 && (ws == nullptr || ws_bytes < splits_bytes(g, a.splits))) return hipErrorInvalidValue;
     hipError_t e = c.launch(a, nblk, stream);
     if (e != hipSuccess || a.splits == 1) return e;
-    const int vec = g.N % 4 == 0 && g.ldc % 4 == 0 && uintptr_t(g.c) % 16 == 0 &&
-                    (g.bias == nullptr || uintptr_t(g.bias) % 16 == 0);
-    const int64_t items = vec ? g.M * g.N / 4 : g.M * g.N;
-    hipLaunchKernelGGL(lin_splitk_reduce_kernel, dim3(unsigned((items + 255) / 256)), dim3(256), 0, stream,
-                       static_cast<const float *>(ws), a.splits, a.M, a.N, static_cast<float *>(g.c), g.ldc,
-                       static_cast<const float *>(g.bias), a.beta, vec);
+    const int64_t items = a.vec_out ? g.M * g.N / 4 : g.M * g.N;
+    hipLaunchKernelGGL(lin_splitk_reduce_kernel<F>, dim3(unsigned((items + 255) / 256), unsigned(g.nbatch)), dim3(256),
+                       0, stream, a, items, a.vec_out);
     return hipGetLastError();
 }
 
-inline int64_t splits_bytes(const LinGemm &g, int splits) { return splits > 1 ? int64_t(splits) * g.M * g.N * 4 : 0; }
-
 }  // namespace lin
-}  // namespace ctattn
 
-namespace ctattn {
 namespace {
 
+using lin::BF16Fmt;
 using lin::CfgInfo;
 using lin::cfg_info;
+using lin::F16Fmt;
+using lin::F32Fmt;
 
-// The launchable configurations, per operand layout (tile 32 TM x 32 TN, NW waves, K chunks of
-// KW, S-stage ring).  The choice among them (plan below) was fitted to a forced-configuration
-// sweep of 132 configurations per layout over the products of a d384 / d1024 transformer and
-// a 4096^3 matmul.
-const CfgInfo kFwd[] = {cfg_info<true, true, 2, 1, 4, 16, 2>(), cfg_info<true, true, 2, 1, 1, 16, 2>(),
-                        cfg_info<true, true, 2, 1, 1, 16, 3>()};
-const CfgInfo kDx[] = {cfg_info<true, false, 2, 1, 4, 16, 2>(), cfg_info<true, false, 2, 1, 1, 16, 2>(),
-                       cfg_info<true, false, 2, 1, 1, 16, 3>()};
-const CfgInfo kDw[] = {cfg_info<false, false, 1, 1, 4, 16, 2>(), cfg_info<false, false, 2, 2, 8, 16, 2>()};
+// The launchable configurations per operand layout (tile 32 TM x 32 TN, NW waves, S-stage
+// ring).  The choice among them (plan below) was fitted to forced-configuration sweeps over the
+// products of a d384 and a d1024 transformer and a 4096^3 matmul: 132 fp32 configurations per
+// layout, 82 bf16 ones.
+template <typename F>
+struct Tables {
+    static constexpr CfgInfo fwd[] = {cfg_info<F, true, true, 2, 1, 4, 2>(), cfg_info<F, true, true, 2, 1, 1, 2>(),
+                                      cfg_info<F, true, true, 2, 1, 1, 3>()};
+    static constexpr CfgInfo dx[] = {cfg_info<F, true, false, 2, 1, 4, 2>(), cfg_info<F, true, false, 2, 1, 1, 2>(),
+                                     cfg_info<F, true, false, 2, 1, 1, 3>()};
+    static constexpr CfgInfo dw[] = {cfg_info<F, false, false, 1, 1, 4, 2>(), cfg_info<F, false, false, 2, 2, 8, 2>()};
+};
+// 16-bit storage: the MFMA does 16x the work per operand byte, so the tiles are larger (the
+// 64 x 32 tiles of fp32 leave the 16-bit kernels bound by L2 and LDS bandwidth).
+template <typename F>
+struct Tables16 {
+    static constexpr CfgInfo fwd[] = {cfg_info<F, true, true, 4, 2, 1, 3>(), cfg_info<F, true, true, 2, 2, 4, 2>()};
+    static constexpr CfgInfo dx[] = {cfg_info<F, true, false, 2, 4, 1, 2>(), cfg_info<F, true, false, 2, 2, 4, 2>()};
+    static constexpr CfgInfo dw[] = {cfg_info<F, false, false, 2, 2, 2, 2>()};
+};
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Chooses a configuration and a K split count.  allow_split: the caller has workspace for
-// split-K partials.
+// Chooses a configuration (index into the layout's table) and a K split count.
+// allow_split: the caller has workspace for split-K partials.
+// fp32:
 //   * Both operands M/N-contiguous (weight gradients: small output, K = rows): 64 x 64 tiles
 //     of 8 waves when there are at least 256 of them, else 32 x 32 tiles of 4 waves with K
 //     split across workgroups up to 2048 workgroups, each wave keeping >= 12 K chunks.
 //   * Otherwise 64 x 32 tiles: 4 waves (K split inside the workgroup) while there are fewer
-//     than 3072 tiles, else one wave per tile (3 stages once K reaches 1024).
-lin::Plan plan(const LinGemm &g, bool allow_split, const CfgInfo **cfg) {
-    const int64_t chunks = g.K / 16;
+//     than 3072 tiles, else one wave per tile (3 stages once K reaches 64 chunks, else 2).
+// bf16 / fp16:
+//   * weight gradients: 64 x 64 tiles of 2 waves, K split across workgroups below 512 tiles
+//     (up to 1024 workgroups, each wave keeping >= 12 K chunks);
+//   * otherwise, with at least 1024 64 x 64 tiles and 24 K chunks: one wave per 128 x 64
+//     (forward) or 64 x 128 (dX) tile; else 64 x 64 tiles of 4 waves.
+lin::Plan plan(const LinGemm &g, bool allow_split) {
+    const int64_t chunks = g.K / lin::chunk_elems(g.dtype) * g.nseg;
+    if (g.dtype != 0) {
+        const int64_t t64 = cdiv(g.M, 64) * cdiv(g.N, 64) * g.nbatch;
+        if (g.a_kc) return lin::Plan{t64 >= 1024 && chunks >= 24 ? 0 : 1, 1};
+        if (t64 >= 512 || !allow_split) return lin::Plan{0, 1};
+        const int64_t sp = std::min<int64_t>(cdiv(1024, t64), chunks / 24);
+        return lin::Plan{0, int(std::max<int64_t>(1, std::min<int64_t>(sp, 16)))};
+    }
     if (!g.a_kc) {
-        if (cdiv(g.M, 64) * cdiv(g.N, 64) >= 256) {
-            *cfg = &kDw[1];
-            return lin::Plan{1, 1};
-        }
-        const int64_t tiles = cdiv(g.M, 32) * cdiv(g.N, 32);
+        if (cdiv(g.M, 64) * cdiv(g.N, 64) * g.nbatch >= 256) return lin::Plan{1, 1};
+        const int64_t tiles = cdiv(g.M, 32) * cdiv(g.N, 32) * g.nbatch;
         int64_t sp = std::min<int64_t>(cdiv(2048, tiles), chunks / 48);
         sp = allow_split ? std::max<int64_t>(1, std::min<int64_t>(sp, 16)) : 1;
-        *cfg = &kDw[0];
         return lin::Plan{0, int(sp)};
     }
-    const CfgInfo *tab = g.b_kc ? kFwd : kDx;
-    const int64_t tiles = cdiv(g.M, 64) * cdiv(g.N, 32);
-    const int i = tiles < 3072 ? 0 : chunks >= 64 ? 2 : 1;
-    *cfg = &tab[i];
-    return lin::Plan{i, 1};
+    const int64_t tiles = cdiv(g.M, 64) * cdiv(g.N, 32) * g.nbatch;
+    return lin::Plan{tiles < 3072 ? 0 : chunks >= 64 ? 2 : 1, 1};
 }
 
-}  // namespace
+template <typename Tb>
+const CfgInfo &cfg_of(const LinGemm &g, const lin::Plan &pl) {
+    if (!g.a_kc) return Tb::dw[pl.cfg];
+    return g.b_kc ? Tb::fwd[pl.cfg] : Tb::dx[pl.cfg];
+}
+const CfgInfo &cfg_for(const LinGemm &g, const lin::Plan &pl) {
+    return g.dtype == 0   ? cfg_of<Tables<F32Fmt>>(g, pl)
+           : g.dtype == 1 ? cfg_of<Tables16<BF16Fmt>>(g, pl)
+                          : cfg_of<Tables16<F16Fmt>>(g, pl);
+}
 
-namespace {
+// A view the kernels can address: 16-byte aligned row pitch and 32-bit lane offsets within a
+// tile (linear); or head-split with every 64-byte K chunk inside one head (K-contiguous), or
+// every 16-byte column chunk inside one head and every stage of k-rows inside one batch
+// (M/N-contiguous).
+bool view_ok(const LinView &v, bool kc, int dtype) {
+    const int eb = lin::elem_bytes(dtype), kwe = lin::chunk_elems(dtype), ce = 16 / eb;
+    if (v.heads == 0) return v.ld >= 0 && v.ld % ce == 0 && v.ld * eb <= (int64_t(1) << 24);
+    if (v.heads < 1 || v.T < 1 || v.d < 1) return false;
+    if (int64_t(v.heads) * v.T * v.d * eb >= (int64_t(1) << 30)) return false;  // tile offsets stay 32-bit
+    return kc ? v.d % kwe == 0 : v.d % ce == 0 && v.T % kwe == 0;
+}
 
 // The shape / pitch part of lin_gemm_supported (pointers are not looked at).
 bool shape_ok(const LinGemm &g) {
-    if (g.dtype != 0 || (!g.a_kc && g.b_kc)) return false;
-    if (g.M < 1 || g.N < 1 || g.K < 16 || g.K % 16 != 0) return false;
-    if (g.M > 2147483647 || g.N > 2147483647 || g.K > 2147483647) return false;
-    // 16-byte operand rows for the direct-to-LDS loads.
-    if (g.lda % 4 != 0 || g.ldb % 4 != 0) return false;
+    if (g.dtype < 0 || g.dtype > 2 || (!g.a_kc && g.b_kc)) return false;
+    if (g.nbatch < 1 || g.nbatch > kLinMaxBatch || g.nseg < 1 || g.nseg > kLinMaxSeg) return false;
+    const int kwe = lin::chunk_elems(g.dtype), ce = 16 / lin::elem_bytes(g.dtype);
+    if (g.M < 1 || g.N < 1 || g.K < kwe || g.K % kwe != 0) return false;
+    if (g.M > 2147483647 || g.N > 2147483647 || g.K * g.nseg > 2147483647) return false;
     // An M/N-contiguous operand is read in whole 16-byte chunks of its M / N extent.
-    if ((!g.a_kc && g.M % 4 != 0) || (!g.b_kc && g.N % 4 != 0)) return false;
-    // Lane offsets within a stage are 32-bit: at most 128 rows (or 16 k-rows) of one pitch.
-    if (g.lda > (int64_t(1) << 22) || g.ldb > (int64_t(1) << 22)) return false;
-    if (g.ldc < g.N) return false;
+    if ((!g.a_kc && g.M % ce != 0) || (!g.b_kc && g.N % ce != 0)) return false;
+    if (!view_ok(g.av, g.a_kc, g.dtype) || !view_ok(g.bv, g.b_kc, g.dtype)) return false;
+    // The output: a linear pitch of at least N, or head-split with 4-column groups in one head.
+    if (g.cv.heads == 0 ? g.cv.ld < g.N : (g.cv.d % 4 != 0 || g.cv.T < 1)) return false;
     // Launch size: workgroups x threads below 2^32.
-    const CfgInfo *c = nullptr;
-    const lin::Plan pl = plan(g, true, &c);
-    const int64_t wg = cdiv(g.M, 32 * c->tm) * cdiv(g.N, 32 * c->tn) * pl.splits;
-    return wg * c->nw * 64 < (int64_t(1) << 32);
+    const lin::Plan pl = plan(g, true);
+    const CfgInfo &c = cfg_for(g, pl);
+    const int64_t wg = cdiv(g.M, 32 * c.tm) * cdiv(g.N, 32 * c.tn) * pl.splits * g.nbatch;
+    return wg * c.nw * 64 < (int64_t(1) << 32);
 }
 
 }  // namespace
 
+LinGemm lin_plain(int dtype, bool a_kc, bool b_kc, int64_t M, int64_t N, int64_t K, const void *a, int64_t lda,
+                  const void *b, int64_t ldb, void *c, int64_t ldc, const void *bias, bool beta) {
+    LinGemm g{};
+    g.dtype = dtype;
+    g.a_kc = a_kc;
+    g.b_kc = b_kc;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.nbatch = 1;
+    g.nseg = 1;
+    g.av = lin_linear(lda);
+    g.bv = lin_linear(ldb);
+    g.cv = lin_linear(ldc);
+    g.a[0][0] = a;
+    g.b[0][0] = b;
+    g.c[0] = c;
+    g.bias[0] = bias;
+    g.beta = beta;
+    return g;
+}
+
 bool lin_gemm_supported(const LinGemm &g) {
-    if (!shape_ok(g) || !g.a || !g.b || !g.c) return false;
-    return uintptr_t(g.a) % 16 == 0 && uintptr_t(g.b) % 16 == 0;
+    if (!shape_ok(g)) return false;
+    for (int z = 0; z < g.nbatch; ++z) {
+        if (g.c[z] == nullptr) return false;
+        for (int s = 0; s < g.nseg; ++s)
+            if (g.a[z][s] == nullptr || g.b[z][s] == nullptr || uintptr_t(g.a[z][s]) % 16 != 0 ||
+                uintptr_t(g.b[z][s]) % 16 != 0)
+                return false;
+    }
+    return true;
 }
 
 int64_t lin_gemm_workspace_bytes(const LinGemm &g) {
     if (!shape_ok(g)) return 0;
-    const CfgInfo *c = nullptr;
-    const lin::Plan pl = plan(g, true, &c);
-    // The launch trims empty splits, never adds any: splits x M x N floats is an upper bound.
-    return pl.splits > 1 ? lin::splits_bytes(g, pl.splits) : 0;
+    // The launch trims empty splits, never adds any: this is an upper bound.
+    return lin::splits_bytes(g, plan(g, true).splits);
 }
 
 hipError_t launch_lin_gemm(const LinGemm &g, void *ws, int64_t ws_bytes, hipStream_t stream) {
     if (!lin_gemm_supported(g)) return hipErrorInvalidValue;
-    const CfgInfo *c = nullptr;
-    lin::Plan pl = plan(g, true, &c);
-    if (pl.splits > 1 && (ws == nullptr || ws_bytes < lin::splits_bytes(g, pl.splits))) pl = plan(g, false, &c);
-    return lin::run(g, *c, pl.splits, ws, ws_bytes, stream);
+    lin::Plan pl = plan(g, true);
+    if (pl.splits > 1 && (ws == nullptr || ws_bytes < lin::splits_bytes(g, pl.splits))) pl = plan(g, false);
+    const CfgInfo &c = cfg_for(g, pl);
+    switch (g.dtype) {
+        case 0: return lin::run<F32Fmt>(g, c, pl.splits, ws, ws_bytes, stream);
+        case 1: return lin::run<BF16Fmt>(g, c, pl.splits, ws, ws_bytes, stream);
+        default: return lin::run<F16Fmt>(g, c, pl.splits, ws, ws_bytes, stream);
+    }
 }
 
 }  // namespace ctattn

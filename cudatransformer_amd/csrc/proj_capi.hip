@@ -3,10 +3,10 @@
 //
 // Each entry point validates its arguments on the host, describes its products as
 // separable views (row-major [B*T, E] activations, [B, H, T, d] attention tensors, [out][in]
-// weights) and launches the MFMA GEMM family of proj_gemm.hip on the caller's stream.  The
-// linear layers' products are plain row-major fp32 GEMMs and run on the split-K-in-workgroup
-// kernels of linear_gemm.hip; shapes outside that family's domain (K not a multiple of 16,
-// an unaligned operand, other dtypes) and the GENERIC policy take the projection family.
+// weights) and launches the split-K-in-workgroup MFMA GEMMs of linear_gemm.hip (fp32, bf16,
+// fp16) on the caller's stream.  fp64, shapes outside that family's domain (K not a multiple
+// of the K chunk, an unaligned operand, head dims that split a chunk) and the GENERIC policy
+// take the projection family of proj_gemm.hip.
 #include "capi_util.h"
 #include "ctattn.h"
 #include "linear_gemm.h"
@@ -93,6 +93,70 @@ GemmParams make_params(int64_t M, int64_t N, int64_t K, int beta, int splits, Ma
 
 hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
+// ---- the products on linear_gemm.hip (fp32 / bf16 / fp16; the GENERIC policy keeps every
+// product on the projection family as the cross-check) ----
+
+bool lin_policy(int dtype) {
+    return (dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16) &&
+           ctattn_get_policy() != CTATTN_POLICY_GENERIC;
+}
+int lin_dtype(int dtype) { return dtype == CTATTN_F32 ? 0 : dtype == CTATTN_BF16 ? 1 : 2; }
+
+ctattn::LinGemm lin_base(int dtype, bool a_kc, bool b_kc, int64_t M, int64_t N, int64_t K, int nbatch, int nseg,
+                         ctattn::LinView av, ctattn::LinView bv, ctattn::LinView cv, bool beta) {
+    ctattn::LinGemm g{};
+    g.dtype = lin_dtype(dtype);
+    g.a_kc = a_kc;
+    g.b_kc = b_kc;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.nbatch = nbatch;
+    g.nseg = nseg;
+    g.av = av;
+    g.bv = bv;
+    g.cv = cv;
+    g.beta = beta;
+    return g;
+}
+
+// The six projection products, pointers filled in by the caller (null for workspace queries):
+//   QKV forward  q/k/v(r, j) = sum_i x[r][i] w[j][i] + b[j]     A = x, B = w (both [.][E]), C head-split
+//   QKV dW       dw[j][i] += sum_r g(r, j) x[r][i]              A = g head-split [k][m], B = x [k][n]
+//   QKV dX       dx[r][i] = sum_z sum_j g_z(r, j) w_z[j][i]     A = g head-split, B = w [k][n], 3 K segments
+//   out forward  y[r][e] = sum_c attn(r, c) wo[e][c] + bo[e]    A = attn head-split, B = wo [E][HD]
+//   out dW       dwo[e][c] += sum_r dy[r][e] attn(r, c)         A = dy [k][m], B = attn head-split [k][n]
+//   out dX       dc(r, c) = sum_e dy[r][e] wo[e][c]             A = dy, B = wo [k][n], C head-split
+ctattn::LinGemm lin_qkv_fwd(int dtype, const ProjShape &s) {
+    return lin_base(dtype, true, true, s.rows(), s.hd(), s.E, 3, 1, ctattn::lin_linear(s.E), ctattn::lin_linear(s.E),
+                    ctattn::lin_heads(s.T, s.H, s.d), false);
+}
+ctattn::LinGemm lin_qkv_dw(int dtype, const ProjShape &s) {
+    return lin_base(dtype, false, false, s.hd(), s.E, s.rows(), 3, 1, ctattn::lin_heads(s.T, s.H, s.d),
+                    ctattn::lin_linear(s.E), ctattn::lin_linear(s.E), true);
+}
+ctattn::LinGemm lin_qkv_dx(int dtype, const ProjShape &s) {
+    return lin_base(dtype, true, false, s.rows(), s.E, s.hd(), 1, 3, ctattn::lin_heads(s.T, s.H, s.d),
+                    ctattn::lin_linear(s.E), ctattn::lin_linear(s.E), false);
+}
+ctattn::LinGemm lin_out_fwd(int dtype, const ProjShape &s) {
+    return lin_base(dtype, true, true, s.rows(), s.E, s.hd(), 1, 1, ctattn::lin_heads(s.T, s.H, s.d),
+                    ctattn::lin_linear(s.hd()), ctattn::lin_linear(s.E), false);
+}
+ctattn::LinGemm lin_out_dw(int dtype, const ProjShape &s) {
+    return lin_base(dtype, false, false, s.E, s.hd(), s.rows(), 1, 1, ctattn::lin_linear(s.E),
+                    ctattn::lin_heads(s.T, s.H, s.d), ctattn::lin_linear(s.hd()), true);
+}
+ctattn::LinGemm lin_out_dx(int dtype, const ProjShape &s) {
+    return lin_base(dtype, true, false, s.rows(), s.hd(), s.E, 1, 1, ctattn::lin_linear(s.E),
+                    ctattn::lin_linear(s.hd()), ctattn::lin_heads(s.T, s.H, s.d), false);
+}
+
+// Split-K bytes for either family's plan of a weight gradient.
+int64_t lin_split_bytes(int dtype, const ctattn::LinGemm &g) {
+    return lin_policy(dtype) ? align_up(ctattn::lin_gemm_workspace_bytes(g)) : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -117,6 +181,17 @@ int ctattn_qkv_proj_fwd(int dtype, const void *x, const void *wq, const void *wk
         p.batch[z].out = o[z];
         p.batch[z].bias = b[z];
     }
+    if (lin_policy(dtype)) {
+        ctattn::LinGemm g = lin_qkv_fwd(dtype, s);
+        for (int z = 0; z < 3; ++z) {
+            g.a[z][0] = x;
+            g.b[z][0] = w[z];
+            g.c[z] = o[z];
+            g.bias[z] = b[z];
+        }
+        if (ctattn::lin_gemm_supported(g))
+            return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, as_stream(stream)), as_stream(stream));
+    }
     const bool v4 = vec4_ok(dtype, s, {x, wq, wk, wv, q, k, v});
     return finish(fn, ctattn::launch_proj_gemm(dtype, p, 3, true, true, v4, as_stream(stream)), as_stream(stream));
 }
@@ -125,7 +200,7 @@ int64_t ctattn_qkv_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int
     const ProjShape s{B, T, E, H, d};
     if (validate_proj("ctattn_qkv_proj_bwd_workspace_bytes", dtype, s)) return -1;
     ok();
-    return splitk_bytes(dtype, s.hd(), E, s.rows(), 3) +
+    return std::max(splitk_bytes(dtype, s.hd(), E, s.rows(), 3), lin_split_bytes(dtype, lin_qkv_dw(dtype, s))) +
            align_up(ctattn::colsum_workspace_bytes(dtype, s.rows(), s.hd()));
 }
 
@@ -152,7 +227,38 @@ int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk
     const void *g[3] = {dq, dk, dv};
     hipError_t e = hipSuccess;
     float *ws = static_cast<float *>(workspace);
-    if (want_dw) {
+    const int64_t split_bytes =
+        std::max(splitk_bytes(dtype, s.hd(), E, s.rows(), 3), lin_split_bytes(dtype, lin_qkv_dw(dtype, s)));
+    bool dw_done = false, dx_done = false;
+    if (want_dw && lin_policy(dtype)) {
+        ctattn::LinGemm lg = lin_qkv_dw(dtype, s);
+        void *o[3] = {dwq, dwk, dwv};
+        for (int z = 0; z < 3; ++z) {
+            lg.a[z][0] = g[z];
+            lg.b[z][0] = x;
+            lg.c[z] = o[z];
+        }
+        if (ctattn::lin_gemm_supported(lg)) {
+            e = ctattn::launch_lin_gemm(lg, workspace, split_bytes, st);
+            if (e != hipSuccess) return finish(fn, e, st);
+            dw_done = true;
+        }
+    }
+    if (dx && lin_policy(dtype)) {
+        ctattn::LinGemm lg = lin_qkv_dx(dtype, s);
+        const void *w[3] = {wq, wk, wv};
+        for (int z = 0; z < 3; ++z) {
+            lg.a[0][z] = g[z];
+            lg.b[0][z] = w[z];
+        }
+        lg.c[0] = dx;
+        if (ctattn::lin_gemm_supported(lg)) {
+            e = ctattn::launch_lin_gemm(lg, nullptr, 0, st);
+            if (e != hipSuccess) return finish(fn, e, st);
+            dx_done = true;
+        }
+    }
+    if (want_dw && !dw_done) {
         // dw[j][i] += sum_r g(r, j) x[r][i]: M = HD, N = E, K = rows.  A(m=j, k=r) = g stored
         // [k][m] (head-split), B(k=r, n=i) = x stored [k][n].
         const int splits = choose_splits(dtype, s.hd(), E, s.rows(), 3);
@@ -169,13 +275,13 @@ int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (want_db) {
-        void *cws = static_cast<char *>(workspace) + splitk_bytes(dtype, s.hd(), E, s.rows(), 3);
+        void *cws = static_cast<char *>(workspace) + split_bytes;
         void *o[3] = {dbq, dbk, dbv};
         for (int z = 0; z < 3 && e == hipSuccess; ++z)
             e = ctattn::launch_colsum_add(dtype, head_view(g[z], T, H, d), int(s.rows()), int(s.hd()), o[z], cws, st);
         if (e != hipSuccess) return finish(fn, e, st);
     }
-    if (dx) {
+    if (dx && !dx_done) {
         // dx[r][i] = sum_z sum_j g_z(r, j) w_z[j][i]: A = g (head-split, K-contiguous), B = w
         // stored [k][n]; three K segments into one output.
         GemmParams p = make_params(s.rows(), E, s.hd(), 0, 1, linear_view(nullptr, E), nullptr);
@@ -207,6 +313,15 @@ int ctattn_out_proj_fwd(int dtype, const void *c, const void *wo, const void *bo
     p.batch[0].b[0] = linear_view(wo, s.hd());
     p.batch[0].out = y;
     p.batch[0].bias = bo;
+    if (lin_policy(dtype)) {
+        ctattn::LinGemm g = lin_out_fwd(dtype, s);
+        g.a[0][0] = c;
+        g.b[0][0] = wo;
+        g.c[0] = y;
+        g.bias[0] = bo;
+        if (ctattn::lin_gemm_supported(g))
+            return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, as_stream(stream)), as_stream(stream));
+    }
     const bool v4 = vec4_ok(dtype, s, {c, wo, y});
     return finish(fn, ctattn::launch_proj_gemm(dtype, p, 1, true, true, v4, as_stream(stream)), as_stream(stream));
 }
@@ -215,7 +330,7 @@ int64_t ctattn_out_proj_bwd_workspace_bytes(int dtype, int64_t B, int64_t T, int
     const ProjShape s{B, T, E, H, d};
     if (validate_proj("ctattn_out_proj_bwd_workspace_bytes", dtype, s)) return -1;
     ok();
-    return splitk_bytes(dtype, E, s.hd(), s.rows(), 1) +
+    return std::max(splitk_bytes(dtype, E, s.hd(), s.rows(), 1), lin_split_bytes(dtype, lin_out_dw(dtype, s))) +
            align_up(ctattn::colsum_workspace_bytes(dtype, s.rows(), E));
 }
 
@@ -238,6 +353,19 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
     const bool v4 = vec4_ok(dtype, s, {c, dy, wo, dwo, dc});
     float *ws = static_cast<float *>(workspace);
     hipError_t e = hipSuccess;
+    const int64_t split_bytes =
+        std::max(splitk_bytes(dtype, E, s.hd(), s.rows(), 1), lin_split_bytes(dtype, lin_out_dw(dtype, s)));
+    if (dwo && lin_policy(dtype)) {
+        ctattn::LinGemm g = lin_out_dw(dtype, s);
+        g.a[0][0] = dy;
+        g.b[0][0] = c;
+        g.c[0] = dwo;
+        if (ctattn::lin_gemm_supported(g)) {
+            e = ctattn::launch_lin_gemm(g, workspace, split_bytes, st);
+            if (e != hipSuccess) return finish(fn, e, st);
+            dwo = nullptr;
+        }
+    }
     if (dwo) {
         // dwo[e][c] += sum_r dy[r][e] attn(r, c): M = E, N = HD, K = rows.  A(m=e, k=r) = dy
         // stored [k][m]; B(k=r, n=c) = attention output stored [k][n] (head-split).
@@ -252,9 +380,16 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (dbo) {
-        void *cws = static_cast<char *>(workspace) + splitk_bytes(dtype, E, s.hd(), s.rows(), 1);
+        void *cws = static_cast<char *>(workspace) + split_bytes;
         e = ctattn::launch_colsum_add(dtype, linear_view(dy, E), int(s.rows()), int(E), dbo, cws, st);
         if (e != hipSuccess) return finish(fn, e, st);
+    }
+    if (dc && lin_policy(dtype)) {
+        ctattn::LinGemm g = lin_out_dx(dtype, s);
+        g.a[0][0] = dy;
+        g.b[0][0] = wo;
+        g.c[0] = dc;
+        if (ctattn::lin_gemm_supported(g)) return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, st), st);
     }
     if (dc) {
         // dc(r, c) = sum_e dy[r][e] wo[e][c]: A = dy (K-contiguous), B = wo stored [k][n]; out
@@ -285,27 +420,25 @@ int validate_linear(const char *fn, int dtype, int64_t M, int64_t N, int64_t K) 
     return 0;
 }
 
-// The linear layers' products on linear_gemm.hip (fp32, unless the policy asks for the
-// projection family as a cross-check):
+// The linear layers' products on linear_gemm.hip (fp32 / bf16 / fp16, unless the policy asks
+// for the projection family as a cross-check):
 //   forward  y[m][n] = sum_k x[m][k] w[n][k] + b[n]   A = x [M][K], B = w [N][K]
 //   dX       dx[m][k] = sum_n dy[m][n] w[n][k]       A = dy [M][N], B = w stored [n][k]
 //   dW       dw[n][k] += sum_m dy[m][n] x[m][k]      A = dy stored [m][n], B = x stored [m][k]
-bool lin_policy(int dtype) { return dtype == CTATTN_F32 && ctattn_get_policy() != CTATTN_POLICY_GENERIC; }
-
-ctattn::LinGemm lin_fwd(const void *x, const void *w, const void *b, void *y, int64_t M, int64_t N, int64_t K) {
-    return ctattn::LinGemm{0, true, true, M, N, K, x, K, w, K, y, N, b, false};
+ctattn::LinGemm lin_fwd(int dtype, const void *x, const void *w, const void *b, void *y, int64_t M, int64_t N,
+                        int64_t K) {
+    return ctattn::lin_plain(lin_dtype(dtype), true, true, M, N, K, x, K, w, K, y, N, b, false);
 }
-ctattn::LinGemm lin_dx(const void *dy, const void *w, void *dx, int64_t M, int64_t N, int64_t K) {
-    return ctattn::LinGemm{0, true, false, M, K, N, dy, N, w, K, dx, K, nullptr, false};
+ctattn::LinGemm lin_dx(int dtype, const void *dy, const void *w, void *dx, int64_t M, int64_t N, int64_t K) {
+    return ctattn::lin_plain(lin_dtype(dtype), true, false, M, K, N, dy, N, w, K, dx, K, nullptr, false);
 }
-ctattn::LinGemm lin_dw(const void *x, const void *dy, void *dw, int64_t M, int64_t N, int64_t K) {
-    return ctattn::LinGemm{0, false, false, N, K, M, dy, N, x, K, dw, K, nullptr, true};
+ctattn::LinGemm lin_dw(int dtype, const void *x, const void *dy, void *dw, int64_t M, int64_t N, int64_t K) {
+    return ctattn::lin_plain(lin_dtype(dtype), false, false, N, K, M, dy, N, x, K, dw, K, nullptr, true);
 }
 
 // Split-K partials of the weight gradient: room for either GEMM family's plan.
 int64_t linear_split_bytes(int dtype, int64_t M, int64_t N, int64_t K) {
-    const int64_t own = dtype == CTATTN_F32 ? ctattn::lin_gemm_workspace_bytes(lin_dw(nullptr, nullptr, nullptr, M, N, K)) : 0;
-    return std::max(splitk_bytes(dtype, N, K, M, 1), align_up(own));
+    return std::max(splitk_bytes(dtype, N, K, M, 1), lin_split_bytes(dtype, lin_dw(dtype, nullptr, nullptr, nullptr, M, N, K)));
 }
 
 bool linear_vec4(int dtype, int64_t M, int64_t N, int64_t K, std::initializer_list<const void *> ptrs) {
@@ -325,7 +458,7 @@ int ctattn_linear_fwd(int dtype, const void *x, const void *w, const void *b, vo
     if (M == 0) return ok();
     if (!x || !w || !y) return fail(hipErrorInvalidValue, "%s: null x/w/y pointer", fn);
     if (lin_policy(dtype)) {
-        const ctattn::LinGemm g = lin_fwd(x, w, b, y, M, N, K);
+        const ctattn::LinGemm g = lin_fwd(dtype, x, w, b, y, M, N, K);
         if (ctattn::lin_gemm_supported(g))
             return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, as_stream(stream)), as_stream(stream));
     }
@@ -365,7 +498,7 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     hipError_t e = hipSuccess;
     const int64_t split_bytes = linear_split_bytes(dtype, M, N, K);
     if (dw && lin_policy(dtype)) {
-        const ctattn::LinGemm g = lin_dw(x, dy, dw, M, N, K);
+        const ctattn::LinGemm g = lin_dw(dtype, x, dy, dw, M, N, K);
         if (ctattn::lin_gemm_supported(g)) {
             e = ctattn::launch_lin_gemm(g, workspace, split_bytes, st);
             if (e != hipSuccess) return finish(fn, e, st);
@@ -391,7 +524,7 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
         if (e != hipSuccess) return finish(fn, e, st);
     }
     if (dx && lin_policy(dtype)) {
-        const ctattn::LinGemm g = lin_dx(dy, w, dx, M, N, K);
+        const ctattn::LinGemm g = lin_dx(dtype, dy, w, dx, M, N, K);
         if (ctattn::lin_gemm_supported(g)) return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, st), st);
     }
     if (dx) {

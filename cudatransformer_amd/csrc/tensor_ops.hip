@@ -14,9 +14,9 @@
 //   * integer division and remainder by zero give 0 (undefined in the reference);
 //   * reductions are two-stage and deterministic (a fixed order per output) instead of one
 //     thread walking every reduced element;
-//   * fp32 products run on the plain MFMA GEMMs of linear_gemm.hip, bf16 / fp16 / fp64 and
-//     shapes outside that family's domain on the projection GEMM family, instead of one
-//     thread per output.
+//   * fp32 / bf16 / fp16 products run on the MFMA GEMMs of linear_gemm.hip (16-bit storage on
+//     the 16-bit MFMA), fp64 and shapes outside that family's domain on the projection GEMM
+//     family, instead of one thread per output.
 // Storage codes: ctattn_dtype plus CTATTN_I32 .. CTATTN_BOOL.  bool is one byte, 0 or 1.
 #include "attn_common.h"
 #include "capi_util.h"
@@ -865,23 +865,23 @@ int ctattn_tensor_matmul(int dtype, const void *a, const void *b, void *c, int64
         });
         return finish(fn, e, st);
     }
-    // fp32 on the plain GEMMs of linear_gemm.hip (A [M][K] K-contiguous, B stored [K][N]):
-    // one launch when the batches stack (one B), one per batch for up to 16 batches.
+    // fp32 / bf16 / fp16 on the plain GEMMs of linear_gemm.hip (A [M][K] K-contiguous, B stored
+    // [K][N]): one launch when the batches stack (one B), one per batch for up to 16 batches.
     const int64_t rows = batch_b == 1 ? batch * M : M;
-    if (dtype == CTATTN_F32 && ctattn_get_policy() != CTATTN_POLICY_GENERIC && (batch_b == 1 || batch <= 16)) {
+    if ((dtype == CTATTN_F32 || dtype == CTATTN_BF16 || dtype == CTATTN_F16) &&
+        ctattn_get_policy() != CTATTN_POLICY_GENERIC && (batch_b == 1 || batch <= 16)) {
+        const int ld = dtype == CTATTN_F32 ? 0 : dtype == CTATTN_BF16 ? 1 : 2;
+        const int64_t es1 = elem_size(dtype);
         const int64_t calls = batch_b == 1 ? 1 : batch;
+        auto product = [&](int64_t z) {
+            return ctattn::lin_plain(ld, true, false, rows, N, K, static_cast<const char *>(a) + z * M * K * es1, K,
+                                     static_cast<const char *>(b) + z * K * N * es1, N,
+                                     static_cast<char *>(c) + z * M * N * es1, N, nullptr, false);
+        };
         bool all = true;
-        for (int64_t z = 0; z < calls && all; ++z)
-            all = ctattn::lin_gemm_supported(ctattn::LinGemm{0, true, false, rows, N, K,
-                                                             static_cast<const float *>(a) + z * M * K, K,
-                                                             static_cast<const float *>(b) + z * K * N, N,
-                                                             static_cast<float *>(c) + z * M * N, N, nullptr, false});
+        for (int64_t z = 0; z < calls && all; ++z) all = ctattn::lin_gemm_supported(product(z));
         for (int64_t z = 0; z < calls && all; ++z) {
-            const hipError_t e = ctattn::launch_lin_gemm(
-                ctattn::LinGemm{0, true, false, rows, N, K, static_cast<const float *>(a) + z * M * K, K,
-                                static_cast<const float *>(b) + z * K * N, N, static_cast<float *>(c) + z * M * N, N,
-                                nullptr, false},
-                nullptr, 0, st);
+            const hipError_t e = ctattn::launch_lin_gemm(product(z), nullptr, 0, st);
             if (e != hipSuccess) return finish(fn, e, st);
         }
         if (all) return finish(fn, hipSuccess, st);

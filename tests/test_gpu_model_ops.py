@@ -112,17 +112,20 @@ def test_linear_fwd_bwd(dtype, mnk, bias, gemm_path):
 #   (64, 16, 4096)     dX with one K chunk for four waves (three waves add a zero tile)
 #   (8192, 64, 64)     dW split 10 ways (each wave keeps 12 of the 512 K chunks)
 #   (4096, 1152, 384)  the QKV-width product of the NanoGPT configuration
+#   (8100, 1024, 992)  16-bit: the one-wave 128 x 64 forward and 64 x 128 dX tiles with ragged
+#                      M (forward) and N (dX) edges
 LIN_SHAPES = [(4096, 1536, 384), (4096, 384, 1536), (8192, 1024, 1024), (1008, 208, 1008), (64, 16, 4096),
-              (8192, 64, 64), (4096, 1152, 384)]
+              (8192, 64, 64), (4096, 1152, 384), (8100, 1024, 992)]
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("mnk", LIN_SHAPES)
-def test_linear_fp32_plans(mnk):
-    """Every launch configuration of the fp32 linear GEMMs against fp64, bias on, dW / db
-    accumulating into non-zero buffers."""
+def test_linear_plans(mnk, dt):
+    """Every launch configuration of the linear GEMMs (fp32 MFMA for fp32, the 16-bit MFMA for
+    bf16 / fp16 storage) against fp64 on the same rounded inputs, bias on, dW / db accumulating
+    into non-zero buffers."""
     m, n, k = mnk
-    dt = torch.float32
-    print(f"linear plans M={m} N={n} K={k}", flush=True)
+    print(f"linear plans M={m} N={n} K={k} {dt}", flush=True)
     x = _dev(_randn((m, k), 21), dt)
     w = _dev(_randn((n, k), 22, 1 / math.sqrt(k)), dt)
     b = _dev(_randn((n,), 23), dt)
