@@ -37,6 +37,9 @@ struct LinGemm {
     const void *b[kLinMaxBatch][kLinMaxSeg];
     void *c[kLinMaxBatch];
     const void *bias[kLinMaxBatch];  // per column n, storage type, or null
+    // Weight gradients (A M/N-contiguous, A = dY^T): db[m] += sum_k A(m, k), the bias
+    // gradient, accumulated in storage type; null for none.  Ignored for K-contiguous A.
+    void *db[kLinMaxBatch];
     bool beta;
 };
 

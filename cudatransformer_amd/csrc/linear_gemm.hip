@@ -32,7 +32,10 @@
 //     coalesced vector stores;
 //   * when even that leaves SIMDs idle (weight gradients: small C, long K), K is also split
 //     across workgroups; their partial tiles go to a caller workspace and a second kernel adds
-//     them in split order (still deterministic, no atomics).
+//     them in split order (still deterministic, no atomics);
+//   * a weight gradient can also produce its bias gradient db[m] += sum_k A(m, k) (A = dY: the
+//     column sums of dY): every wave adds up the A operand values it already reads for its
+//     MFMAs, the workgroups of the first tile column store the sums (fixed order).
 //
 // Operand tiles in LDS.  The fp32 MFMA takes A[i][kk] from lane (i, kk) and B[kk][j] from lane
 // (j, kk); a lane reads four contraction indices k = 8 s + 4 h + t (t = 0..3) at once and
@@ -113,6 +116,8 @@ struct F32Fmt {
     __device__ static floatx4 load4(const char *p) { return *reinterpret_cast<const floatx4 *>(p); }
     __device__ static void store(char *p, float x) { *reinterpret_cast<float *>(p) = x; }
     __device__ static void store4(char *p, floatx4 x) { *reinterpret_cast<floatx4 *>(p) = x; }
+    // Sum of the 16-byte MFMA operand (4 fp32 values).
+    __device__ static float sum(floatx4 v) { return (v[0] + v[1]) + (v[2] + v[3]); }
 };
 template <bool BF>
 struct H16Fmt {
@@ -141,6 +146,14 @@ struct H16Fmt {
     __device__ static void store(char *p, float x) { *reinterpret_cast<uint16_t *>(p) = narrow(x); }
     __device__ static void store4(char *p, floatx4 x) {
         *reinterpret_cast<u16x4 *>(p) = u16x4{narrow(x[0]), narrow(x[1]), narrow(x[2]), narrow(x[3])};
+    }
+    // Sum of the 16-byte MFMA operand (8 16-bit values).
+    __device__ static float sum(floatx4 v) {
+        const i16x8 u = __builtin_bit_cast(i16x8, v);
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += widen(uint16_t(u[e]));
+        return s;
     }
 };
 using BF16Fmt = H16Fmt<true>;
@@ -290,7 +303,8 @@ struct Args {
     const char *b[kLinMaxBatch][kLinMaxSeg];
     char *c[kLinMaxBatch];
     const char *bias[kLinMaxBatch];
-    float *ws;  // split-K partials: [batch][split][M][N] fp32
+    char *db[kLinMaxBatch];  // bias gradients (M-contiguous A only), or null
+    float *ws;  // split-K partials: [batch][split][M][N] fp32, then [batch][split][M] of db
     DView av, bv, cv;
     int32_t M, N;
     int32_t tiles_m, tiles_n;
@@ -311,7 +325,8 @@ struct Cfg {
     static constexpr int L = OA::NL + OB::NL;  // load instructions per stage
     static constexpr int PIPE = NW * S * STAGE;
     static constexpr int RED = NW * BM * BN * 4;
-    static constexpr int LDS = PIPE > RED ? PIPE : RED;
+    static constexpr int DBR = A_KC ? 0 : NW * 2 * BM * 4;  // per-wave, per-lane-half bias sums
+    static constexpr int LDS = PIPE > RED + DBR ? PIPE : RED + DBR;
     static_assert(S >= 2 && (S - 1) * L < 64, "outstanding loads must fit vmcnt");
     static_assert(LDS <= 160 * 1024, "LDS of one workgroup");
 };
@@ -408,6 +423,11 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
+    // Bias gradient of an M-contiguous A: the workgroups of the first tile column sum A.
+    const bool want_db = !A_KC && p.db[z] != nullptr && n0 == 0;
+    float dsum[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) dsum[i] = 0.f;
 
     const int pro = min(S - 1, nst);
     for (int j = 0; j < pro; ++j) issue(j, j);
@@ -428,6 +448,10 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
             for (int tm = 0; tm < TM; ++tm) av[tm] = ra.read(sa, tm, s);
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) bv[tn] = rb.read(sb, tn, s);
+            if (!A_KC && want_db) {
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) dsum[tm] += F::sum(av[tm]);
+            }
             if constexpr (F::WIDE) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
@@ -459,7 +483,28 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 st1(mine + uint32_t(((32 * tm + acc_row(r, h)) * BN + 32 * tn + col) * 4), acc[tm][tn][r]);
+    if (!A_KC && want_db) {
+        // Lane (col, h) holds the sum over its k of A row 32 tm + col: LDS [wave][h][BM].
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+            st1(red + uint32_t(C::RED + ((wave * 2 + h) * BM + 32 * tm + col) * 4), dsum[tm]);
+    }
     __syncthreads();
+    if (!A_KC && want_db && int(threadIdx.x) < BM && m0 + int(threadIdx.x) < p.M) {
+        // Sum in wave order, then lane-half order; one thread per row.
+        const int m = int(threadIdx.x);
+        float x = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) x += ld1(red + uint32_t(C::RED + ((w * 2 + hh) * BM + m) * 4));
+        if (p.splits > 1) {
+            p.ws[int64_t(p.nbatch) * p.splits * p.M * p.N + (int64_t(z) * p.splits + split) * p.M + m0 + m] = x;
+        } else {
+            char *dst = p.db[z] + int64_t(m0 + m) * F::EB;
+            F::store(dst, F::load(dst) + x);
+        }
+    }
 
     // Sum the partials in wave order and store, 4 columns per thread.
     constexpr int Q = BM * BN / 4;
@@ -509,13 +554,21 @@ template <typename F>
 __global__ __launch_bounds__(256) void lin_splitk_reduce_kernel(Args p, int64_t items_per_batch, int vec) {
     const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
     const int z = int(blockIdx.y);
-    if (idx >= items_per_batch) return;
     const int w = vec ? 4 : 1;
     const int64_t mn = int64_t(p.M) * p.N;
     const int64_t e0 = idx * w;
     const int m = int(e0 / p.N), n = int(e0 - int64_t(m) * p.N);
     const float *src = p.ws + int64_t(z) * p.splits * mn + e0;
     const char *bz = p.bias[z];
+    if (p.db[z] != nullptr && idx < p.M) {
+        // Bias gradient: db[idx] += its split partials, in split order.
+        const float *dsrc = p.ws + int64_t(p.nbatch) * p.splits * mn + int64_t(z) * p.splits * p.M + idx;
+        float x = dsrc[0];
+        for (int s = 1; s < p.splits; ++s) x += dsrc[int64_t(s) * p.M];
+        char *dst = p.db[z] + idx * F::EB;
+        F::store(dst, F::load(dst) + x);
+    }
+    if (idx >= items_per_batch) return;
     char *dst = p.c[z] + rowoff(p.cv, m) + coloff(p.cv, n);
     if (vec) {
         floatx4 x = *reinterpret_cast<const floatx4 *>(src);
@@ -573,7 +626,7 @@ inline DView dview(const LinView &v, int eb) {
 }
 
 inline int64_t splits_bytes(const LinGemm &g, int splits) {
-    return splits > 1 ? int64_t(splits) * g.nbatch * g.M * g.N * 4 : 0;
+    return splits > 1 ? int64_t(splits) * g.nbatch * (g.M * g.N + g.M) * 4 : 0;
 }
 
 // Builds the kernel arguments of a product for a configuration and split count; returns the
@@ -590,6 +643,7 @@ inline int make_args(const LinGemm &g, const CfgInfo &c, int splits, void *ws, A
         }
         a.c[z] = static_cast<char *>(g.c[zz]);
         a.bias[z] = static_cast<const char *>(g.bias[zz]);
+        a.db[z] = g.a_kc || z >= g.nbatch ? nullptr : static_cast<char *>(g.db[z]);
     }
     a.ws = static_cast<float *>(ws);
     a.av = dview(g.av, eb);
@@ -621,8 +675,9 @@ hipError_t run(const LinGemm &g, const CfgInfo &c, int splits, void *ws, int64_t
     hipError_t e = c.launch(a, nblk, stream);
     if (e != hipSuccess || a.splits == 1) return e;
     const int64_t items = a.vec_out ? g.M * g.N / 4 : g.M * g.N;
-    hipLaunchKernelGGL(lin_splitk_reduce_kernel<F>, dim3(unsigned((items + 255) / 256), unsigned(g.nbatch)), dim3(256),
-                       0, stream, a, items, a.vec_out);
+    const int64_t threads = std::max<int64_t>(items, g.M);  // bias gradients: one thread per row
+    hipLaunchKernelGGL(lin_splitk_reduce_kernel<F>, dim3(unsigned((threads + 255) / 256), unsigned(g.nbatch)),
+                       dim3(256), 0, stream, a, items, a.vec_out);
     return hipGetLastError();
 }
 

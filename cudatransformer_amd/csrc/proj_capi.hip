@@ -230,18 +230,22 @@ int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk
     const int64_t split_bytes =
         std::max(splitk_bytes(dtype, s.hd(), E, s.rows(), 3), lin_split_bytes(dtype, lin_qkv_dw(dtype, s)));
     bool dw_done = false, dx_done = false;
+    bool db_done = false;
     if (want_dw && lin_policy(dtype)) {
+        // The bias gradients (column sums of dq / dk / dv) come out of the same launch.
         ctattn::LinGemm lg = lin_qkv_dw(dtype, s);
-        void *o[3] = {dwq, dwk, dwv};
+        void *o[3] = {dwq, dwk, dwv}, *ob[3] = {dbq, dbk, dbv};
         for (int z = 0; z < 3; ++z) {
             lg.a[z][0] = g[z];
             lg.b[z][0] = x;
             lg.c[z] = o[z];
+            lg.db[z] = ob[z];
         }
         if (ctattn::lin_gemm_supported(lg)) {
             e = ctattn::launch_lin_gemm(lg, workspace, split_bytes, st);
             if (e != hipSuccess) return finish(fn, e, st);
             dw_done = true;
+            db_done = want_db;
         }
     }
     if (dx && lin_policy(dtype)) {
@@ -274,7 +278,7 @@ int ctattn_qkv_proj_bwd(int dtype, const void *x, const void *dq, const void *dk
         e = ctattn::launch_proj_gemm(dtype, p, 3, false, false, v4, st);
         if (e != hipSuccess) return finish(fn, e, st);
     }
-    if (want_db) {
+    if (want_db && !db_done) {
         void *cws = static_cast<char *>(workspace) + split_bytes;
         void *o[3] = {dbq, dbk, dbv};
         for (int z = 0; z < 3 && e == hipSuccess; ++z)
@@ -360,10 +364,12 @@ int ctattn_out_proj_bwd(int dtype, const void *c, const void *dy, const void *wo
         g.a[0][0] = dy;
         g.b[0][0] = c;
         g.c[0] = dwo;
+        g.db[0] = dbo;  // the bias gradient (column sums of dy) from the same launch
         if (ctattn::lin_gemm_supported(g)) {
             e = ctattn::launch_lin_gemm(g, workspace, split_bytes, st);
             if (e != hipSuccess) return finish(fn, e, st);
             dwo = nullptr;
+            dbo = nullptr;
         }
     }
     if (dwo) {
@@ -498,11 +504,13 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     hipError_t e = hipSuccess;
     const int64_t split_bytes = linear_split_bytes(dtype, M, N, K);
     if (dw && lin_policy(dtype)) {
-        const ctattn::LinGemm g = lin_dw(dtype, x, dy, dw, M, N, K);
+        ctattn::LinGemm g = lin_dw(dtype, x, dy, dw, M, N, K);
+        g.db[0] = db;  // the bias gradient (column sums of dy) from the same launch
         if (ctattn::lin_gemm_supported(g)) {
             e = ctattn::launch_lin_gemm(g, workspace, split_bytes, st);
             if (e != hipSuccess) return finish(fn, e, st);
             dw = nullptr;
+            db = nullptr;
         }
     }
     if (dw) {
