@@ -51,6 +51,9 @@
 //     two k-rows are kept on different halves of the 64 banks: by swapping row positions
 //     (tiles 32 or 96 wide, whose rows alternate halves) or by flipping chunk bit 3 (64 or 128
 //     wide).
+//     A 64-wide fp32 operand of two 32-wide MFMA tiles instead interleaves them: row i of
+//     tile t is column 2 i + t of the 64, so one ds_read_b64 per lane gives both tiles'
+//     operands at one k (the partial-tile epilogue undoes the interleave).
 //   * M/N-contiguous operand, 16-bit: LDS [32 k][rows] -- two ds_read_b64_tr_b16 per lane per
 //     step (each: a 16-lane group reads 4 k-rows x 16 columns and lane l receives column l's
 //     four values).  The 64-byte segment index of a k-row is XOR-swizzled by the row so the 32
@@ -69,6 +72,7 @@
 namespace ctattn {
 namespace lin {
 
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) const floatx4 lds_cf4;
 typedef __attribute__((address_space(3))) const float lds_cf;
 typedef __attribute__((address_space(3))) float lds_f;
@@ -212,6 +216,8 @@ struct OpKC {
         }
         __device__ floatx4 read(uint32_t base, int tt, int s) const { return ld4(base + tt * 32 * 64 + offs[s]); }
     };
+    // Index (row of A / column of B) of MFMA row i of 32-wide tile t.
+    __host__ __device__ static constexpr int idx(int t, int i) { return 32 * t + i; }
 };
 
 // M/N-contiguous fp32 operand: 16 k-rows x R columns per stage, LDS [k][R] (row pitch 4 R).
@@ -255,6 +261,28 @@ struct OpMN32 {
             return x;
         }
     };
+    __host__ __device__ static constexpr int idx(int t, int i) { return 32 * t + i; }
+};
+
+// M/N-contiguous fp32 operand of two interleaved 32-wide tiles: 16 k-rows x 64 columns per
+// stage, LDS [k][64] (row pitch 256 bytes, no swizzle), MFMA row i of tile t at column 2 i + t.
+// Lane (col, h) reads columns 2 col, 2 col + 1 of k-row 8 s + 4 h + t with one ds_read_b64:
+// each half-wave reads one whole 256-byte k-row, the 64 banks once.
+struct OpMN32P {
+    static constexpr int R = 64;
+    static constexpr int CHR = 16;  // 16-byte chunks per k-row
+    static constexpr int BYTES = R * 64;
+    static constexpr int NL = BYTES / 1024;
+    __device__ static uint32_t voff(int i, int lane, const DView &v, int c0, int cols) {
+        const int P = 64 * i + lane;
+        const int kk = P / CHR, lc = P % CHR;
+        return uint32_t(int64_t(kk) * krow_b(v) + coloff(v, c0 + min(4 * lc, cols - 4)) - coloff(v, c0));
+    }
+    struct Lane {
+        uint32_t off;
+        __device__ void init(int lane) { off = uint32_t((4 * (lane >> 5)) * 4 * R + 8 * (lane & 31)); }
+    };
+    __host__ __device__ static constexpr int idx(int t, int i) { return 2 * i + t; }
 };
 
 // M/N-contiguous 16-bit operand: 32 k-rows x R columns per stage, LDS [k][R] (row pitch 2 R),
@@ -296,7 +324,27 @@ struct OpMN16 {
             return __builtin_bit_cast(floatx4, x);
         }
     };
+    __host__ __device__ static constexpr int idx(int t, int i) { return 32 * t + i; }
 };
+
+typedef __attribute__((address_space(3))) const floatx2 lds_cf2;
+
+// Operands of step s of every 32-wide tile of an operand (NT tiles).
+template <typename Op, int NT>
+__device__ __forceinline__ void read_all(const typename Op::Lane &l, uint32_t base, int s, floatx4 (&out)[NT]) {
+    if constexpr (std::is_same_v<Op, OpMN32P>) {
+        static_assert(NT == 2, "the interleaved operand holds two tiles");
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const floatx2 x = *(lds_cf2 *)(uintptr_t)(base + l.off + uint32_t((8 * s + t) * 4 * Op::R));
+            out[0][t] = x[0];
+            out[1][t] = x[1];
+        }
+    } else {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) out[tt] = l.read(base, tt, s);
+    }
+}
 
 struct Args {
     const char *a[kLinMaxBatch][kLinMaxSeg];
@@ -319,8 +367,13 @@ struct Args {
 template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
 struct Cfg {
     static constexpr int BM = 32 * TM, BN = 32 * TN;
-    using OA = std::conditional_t<A_KC, OpKC<BM>, std::conditional_t<F::WIDE, OpMN32<BM>, OpMN16<BM>>>;
-    using OB = std::conditional_t<B_KC, OpKC<BN>, std::conditional_t<F::WIDE, OpMN32<BN>, OpMN16<BN>>>;
+    // An fp32 M/N-contiguous operand two tiles wide reads both tiles at once (OpMN32P).
+    template <bool KC, int NT>
+    using Op = std::conditional_t<KC, OpKC<32 * NT>,
+                                  std::conditional_t<!F::WIDE, OpMN16<32 * NT>,
+                                                     std::conditional_t<NT == 2, OpMN32P, OpMN32<32 * NT>>>>;
+    using OA = Op<A_KC, TM>;
+    using OB = Op<B_KC, TN>;
     static constexpr int STAGE = OA::BYTES + OB::BYTES;
     static constexpr int L = OA::NL + OB::NL;  // load instructions per stage
     static constexpr int PIPE = NW * S * STAGE;
@@ -444,10 +497,8 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             floatx4 av[TM], bv[TN];
-#pragma unroll
-            for (int tm = 0; tm < TM; ++tm) av[tm] = ra.read(sa, tm, s);
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) bv[tn] = rb.read(sb, tn, s);
+            read_all<OA>(ra, sa, s, av);
+            read_all<OB>(rb, sb, s, bv);
             if (!A_KC && want_db) {
 #pragma unroll
                 for (int tm = 0; tm < TM; ++tm) dsum[tm] += F::sum(av[tm]);
@@ -482,12 +533,12 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
         for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                st1(mine + uint32_t(((32 * tm + acc_row(r, h)) * BN + 32 * tn + col) * 4), acc[tm][tn][r]);
+                st1(mine + uint32_t((OA::idx(tm, acc_row(r, h)) * BN + OB::idx(tn, col)) * 4), acc[tm][tn][r]);
     if (!A_KC && want_db) {
         // Lane (col, h) holds the sum over its k of A row 32 tm + col: LDS [wave][h][BM].
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
-            st1(red + uint32_t(C::RED + ((wave * 2 + h) * BM + 32 * tm + col) * 4), dsum[tm]);
+            st1(red + uint32_t(C::RED + ((wave * 2 + h) * BM + OA::idx(tm, col)) * 4), dsum[tm]);
     }
     __syncthreads();
     if (!A_KC && want_db && int(threadIdx.x) < BM && m0 + int(threadIdx.x) < p.M) {
@@ -701,7 +752,8 @@ struct Tables {
                                       cfg_info<F, true, true, 2, 1, 1, 3>()};
     static constexpr CfgInfo dx[] = {cfg_info<F, true, false, 2, 1, 4, 2>(), cfg_info<F, true, false, 2, 1, 1, 2>(),
                                      cfg_info<F, true, false, 2, 1, 1, 3>()};
-    static constexpr CfgInfo dw[] = {cfg_info<F, false, false, 1, 1, 4, 2>(), cfg_info<F, false, false, 2, 2, 8, 2>()};
+    static constexpr CfgInfo dw[] = {cfg_info<F, false, false, 2, 1, 4, 2>(), cfg_info<F, false, false, 2, 2, 8, 2>(),
+                                     cfg_info<F, false, false, 2, 1, 8, 2>()};
 };
 // 16-bit storage: the MFMA does 16x the work per operand byte, so the tiles are larger (the
 // 64 x 32 tiles of fp32 leave the 16-bit kernels bound by L2 and LDS bandwidth).
@@ -718,8 +770,9 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // allow_split: the caller has workspace for split-K partials.
 // fp32:
 //   * Both operands M/N-contiguous (weight gradients: small output, K = rows): 64 x 64 tiles
-//     of 8 waves when there are at least 256 of them, else 32 x 32 tiles of 4 waves with K
-//     split across workgroups up to 2048 workgroups, each wave keeping >= 12 K chunks.
+//     of 8 waves when there are at least 256 of them; else 64 x 32 tiles, of 8 waves with K
+//     split across workgroups up to 256 workgroups below 256 tiles, of 4 waves up to 1280
+//     workgroups otherwise, each wave keeping >= 8 K chunks.
 //   * Otherwise 64 x 32 tiles: 4 waves (K split inside the workgroup) while there are fewer
 //     than 3072 tiles, else one wave per tile (3 stages once K reaches 64 chunks, else 2).
 // bf16 / fp16:
@@ -738,10 +791,11 @@ lin::Plan plan(const LinGemm &g, bool allow_split) {
     }
     if (!g.a_kc) {
         if (cdiv(g.M, 64) * cdiv(g.N, 64) * g.nbatch >= 256) return lin::Plan{1, 1};
-        const int64_t tiles = cdiv(g.M, 32) * cdiv(g.N, 32) * g.nbatch;
-        int64_t sp = std::min<int64_t>(cdiv(2048, tiles), chunks / 48);
+        const int64_t tiles = cdiv(g.M, 64) * cdiv(g.N, 32) * g.nbatch;
+        const bool few = tiles < 256;
+        int64_t sp = few ? std::min<int64_t>(256 / tiles, chunks / 64) : std::min<int64_t>(1280 / tiles, chunks / 32);
         sp = allow_split ? std::max<int64_t>(1, std::min<int64_t>(sp, 16)) : 1;
-        return lin::Plan{0, int(sp)};
+        return lin::Plan{few ? 2 : 0, int(sp)};
     }
     const int64_t tiles = cdiv(g.M, 64) * cdiv(g.N, 32) * g.nbatch;
     return lin::Plan{tiles < 3072 ? 0 : chunks >= 64 ? 2 : 1, 1};

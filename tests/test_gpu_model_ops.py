@@ -110,7 +110,7 @@ def test_linear_fwd_bwd(dtype, mnk, bias, gemm_path):
 #   (8192, 1024, 1024) one wave per tile, 3 stages (K = 1024); dW on 64 x 64 tiles of 8 waves
 #   (1008, 208, 1008)  ragged tiles in M, N and K-chunk count on all three products
 #   (64, 16, 4096)     dX with one K chunk for four waves (three waves add a zero tile)
-#   (8192, 64, 64)     dW split 10 ways (each wave keeps 12 of the 512 K chunks)
+#   (8192, 64, 64)     dW split 8 ways on 8-wave 64 x 32 tiles (8 of the 512 K chunks per wave)
 #   (4096, 1152, 384)  the QKV-width product of the NanoGPT configuration
 #   (8100, 1024, 992)  16-bit: the one-wave 128 x 64 forward and 64 x 128 dX tiles with ragged
 #                      M (forward) and N (dX) edges
