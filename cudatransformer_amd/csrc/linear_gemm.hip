@@ -401,13 +401,21 @@ __device__ __forceinline__ const char *pick(const char *const (&arr)[kLinMaxSeg]
     return seg == 0 ? arr[0] : seg == 1 ? arr[1] : arr[2];
 }
 
-template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
+// GEN: some operand or the output is a head-split view, or K has several segments, so every K
+// chunk's origin is computed from the views; otherwise (row-major matrices, one segment) the
+// stage pointers just advance by a fixed stride per chunk.
+template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S, bool GEN>
 __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
     using C = Cfg<F, A_KC, B_KC, TM, TN, NW, S>;
     using OA = typename C::OA;
     using OB = typename C::OB;
     constexpr int BM = C::BM, BN = C::BN;
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+
+    // Without GEN every view is linear: heads = 0 as a constant folds the head-split arithmetic
+    // (divisions by T and d) out of the origins, lane offsets and stores.
+    DView view_a = p.av, view_b = p.bv, view_c = p.cv;
+    if constexpr (!GEN) view_a.heads = view_b.heads = view_c.heads = 0;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
@@ -435,8 +443,8 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
 
     // Tile origins (the M / N offset of the tile; the K offset is added per chunk).
     const char *a_seg[kLinMaxSeg], *b_seg[kLinMaxSeg];
-    const int64_t a_t = A_KC ? rowoff(p.av, m0) : coloff(p.av, m0);
-    const int64_t b_t = B_KC ? rowoff(p.bv, n0) : coloff(p.bv, n0);
+    const int64_t a_t = A_KC ? rowoff(view_a, m0) : coloff(view_a, m0);
+    const int64_t b_t = B_KC ? rowoff(view_b, n0) : coloff(view_b, n0);
 #pragma unroll
     for (int s = 0; s < kLinMaxSeg; ++s) {
         a_seg[s] = p.a[z][s] + a_t;
@@ -445,9 +453,9 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
 
     uint32_t va[OA::NL], vb[OB::NL];
 #pragma unroll
-    for (int i = 0; i < OA::NL; ++i) va[i] = OA::voff(i, lane, p.av, m0, p.M - m0);
+    for (int i = 0; i < OA::NL; ++i) va[i] = OA::voff(i, lane, view_a, m0, p.M - m0);
 #pragma unroll
-    for (int i = 0; i < OB::NL; ++i) vb[i] = OB::voff(i, lane, p.bv, n0, p.N - n0);
+    for (int i = 0; i < OB::NL; ++i) vb[i] = OB::voff(i, lane, view_b, n0, p.N - n0);
     typename OA::Lane ra;
     typename OB::Lane rb;
     ra.init(lane);
@@ -455,12 +463,28 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
 
     const uint32_t wbase = lds_addr(smem) + uint32_t(wave * S * C::STAGE);
 
+    // Row-major operands: chunk c's origin is base + c * (64 bytes along a K-contiguous row,
+    // or KWE rows of an M/N-contiguous operand), issued in order.
+    const int64_t da = A_KC ? 64 : int64_t(F::KWE) * view_a.ld_b;
+    const int64_t db = B_KC ? 64 : int64_t(F::KWE) * view_b.ld_b;
+    const char *ga_next = a_seg[0] + int64_t(c_first) * da;
+    const char *gb_next = b_seg[0] + int64_t(c_first) * db;
+
     auto issue = [&](int slot, int j) {
-        const int c = c_first + j * NW;
-        const int seg = p.seg_chunks == p.chunks ? 0 : c / p.seg_chunks;
-        const int kk = (c - seg * p.seg_chunks) * F::KWE;
-        const char *ga = pick(a_seg, seg) + (A_KC ? coloff(p.av, kk) : rowoff(p.av, kk));
-        const char *gb = pick(b_seg, seg) + (B_KC ? coloff(p.bv, kk) : rowoff(p.bv, kk));
+        const char *ga, *gb;
+        if constexpr (GEN) {
+            const int c = c_first + j * NW;
+            const int seg = p.seg_chunks == p.chunks ? 0 : c / p.seg_chunks;
+            const int kk = (c - seg * p.seg_chunks) * F::KWE;
+            ga = pick(a_seg, seg) + (A_KC ? coloff(view_a, kk) : rowoff(view_a, kk));
+            gb = pick(b_seg, seg) + (B_KC ? coloff(view_b, kk) : rowoff(view_b, kk));
+        } else {
+            (void)j;
+            ga = ga_next;
+            gb = gb_next;
+            ga_next += NW * da;
+            gb_next += NW * db;
+        }
         const uint32_t sa = wbase + uint32_t(slot * C::STAGE);
         // The slot's previous contents were read by the last stage's MFMAs: those reads have
         // returned (their results were consumed), this makes it explicit.
@@ -581,7 +605,7 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
             continue;
         }
         if (p.vec_out) {
-            char *dst = cz + rowoff(p.cv, gm) + coloff(p.cv, gn);
+            char *dst = cz + rowoff(view_c, gm) + coloff(view_c, gn);
             if (bz != nullptr) x += F::load4(bz + int64_t(gn) * F::EB);
             if (p.beta) x += F::load4(dst);
             F::store4(dst, x);
@@ -589,7 +613,7 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (gn + e >= p.N) break;
-                char *de = cz + rowoff(p.cv, gm) + coloff(p.cv, gn + e);
+                char *de = cz + rowoff(view_c, gm) + coloff(view_c, gn + e);
                 float y = x[e];
                 if (bz != nullptr) y += F::load(bz + int64_t(gn + e) * F::EB);
                 if (p.beta) y += F::load(de);
@@ -646,19 +670,21 @@ struct Plan {
 // One launchable configuration.
 struct CfgInfo {
     int tm, tn, nw, s;
-    hipError_t (*launch)(const Args &, int nblk, hipStream_t);
+    hipError_t (*launch)(const Args &, int nblk, hipStream_t);      // row-major, one segment
+    hipError_t (*launch_gen)(const Args &, int nblk, hipStream_t);  // any views / segments
 };
 
-template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
+template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S, bool GEN>
 hipError_t launch_cfg(const Args &a, int nblk, hipStream_t stream) {
-    hipLaunchKernelGGL((lin_kernel<F, A_KC, B_KC, TM, TN, NW, S>), dim3(unsigned(nblk)), dim3(NW * 64), 0, stream,
-                       a);
+    hipLaunchKernelGGL((lin_kernel<F, A_KC, B_KC, TM, TN, NW, S, GEN>), dim3(unsigned(nblk)), dim3(NW * 64), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
 template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
 constexpr CfgInfo cfg_info() {
-    return CfgInfo{TM, TN, NW, S, &launch_cfg<F, A_KC, B_KC, TM, TN, NW, S>};
+    return CfgInfo{TM, TN, NW, S, &launch_cfg<F, A_KC, B_KC, TM, TN, NW, S, false>,
+                   &launch_cfg<F, A_KC, B_KC, TM, TN, NW, S, true>};
 }
 
 inline int elem_bytes(int dtype) { return dtype == 0 ? 4 : 2; }
@@ -723,7 +749,8 @@ hipError_t run(const LinGemm &g, const CfgInfo &c, int splits, void *ws, int64_t
     Args a{};
     const int nblk = make_args(g, c, splits, ws, a);
     if (a.splits > 1 && (ws == nullptr || ws_bytes < splits_bytes(g, a.splits))) return hipErrorInvalidValue;
-    hipError_t e = c.launch(a, nblk, stream);
+    const bool gen = g.nseg > 1 || g.av.heads != 0 || g.bv.heads != 0 || g.cv.heads != 0;
+    hipError_t e = (gen ? c.launch_gen : c.launch)(a, nblk, stream);
     if (e != hipSuccess || a.splits == 1) return e;
     const int64_t items = a.vec_out ? g.M * g.N / 4 : g.M * g.N;
     const int64_t threads = std::max<int64_t>(items, g.M);  // bias gradients: one thread per row
