@@ -777,10 +777,11 @@ template <typename F>
 struct Tables {
     static constexpr CfgInfo fwd[] = {cfg_info<F, true, true, 2, 1, 4, 2>(), cfg_info<F, true, true, 2, 1, 1, 2>(),
                                       cfg_info<F, true, true, 2, 1, 1, 3>()};
-    static constexpr CfgInfo dx[] = {cfg_info<F, true, false, 2, 1, 4, 2>(), cfg_info<F, true, false, 2, 1, 1, 2>(),
-                                     cfg_info<F, true, false, 2, 1, 1, 3>()};
-    static constexpr CfgInfo dw[] = {cfg_info<F, false, false, 2, 1, 4, 2>(), cfg_info<F, false, false, 2, 2, 8, 2>(),
-                                     cfg_info<F, false, false, 2, 1, 8, 2>()};
+    // An M/N-contiguous B is read through the two-tile interleaved operand (32 x 64 tiles).
+    static constexpr CfgInfo dx[] = {cfg_info<F, true, false, 1, 2, 4, 2>(), cfg_info<F, true, false, 1, 2, 1, 2>(),
+                                     cfg_info<F, true, false, 1, 2, 1, 3>()};
+    static constexpr CfgInfo dw[] = {cfg_info<F, false, false, 1, 2, 4, 2>(), cfg_info<F, false, false, 2, 2, 8, 2>(),
+                                     cfg_info<F, false, false, 1, 2, 8, 2>()};
 };
 // 16-bit storage: the MFMA does 16x the work per operand byte, so the tiles are larger (the
 // 64 x 32 tiles of fp32 leave the 16-bit kernels bound by L2 and LDS bandwidth).
@@ -797,11 +798,12 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // allow_split: the caller has workspace for split-K partials.
 // fp32:
 //   * Both operands M/N-contiguous (weight gradients: small output, K = rows): 64 x 64 tiles
-//     of 8 waves when there are at least 256 of them; else 64 x 32 tiles, of 8 waves with K
+//     of 8 waves when there are at least 256 of them; else 32 x 64 tiles, of 8 waves with K
 //     split across workgroups up to 256 workgroups below 256 tiles, of 4 waves up to 1280
 //     workgroups otherwise, each wave keeping >= 8 K chunks.
-//   * Otherwise 64 x 32 tiles: 4 waves (K split inside the workgroup) while there are fewer
-//     than 3072 tiles, else one wave per tile (3 stages once K reaches 64 chunks, else 2).
+//   * Otherwise 64 x 32 (forward) or 32 x 64 (dX) tiles: 4 waves (K split inside the
+//     workgroup) while there are fewer than 3072 tiles, else one wave per tile (3 stages once
+//     K reaches 64 chunks, else 2).
 // bf16 / fp16:
 //   * weight gradients: 64 x 64 tiles of 2 waves, K split across workgroups below 512 tiles
 //     (up to 1024 workgroups, each wave keeping >= 12 K chunks);
