@@ -191,7 +191,9 @@ def flash_attn_fwd(q, k, v, causal: bool = False, out=None, lse=None, stream=Non
 
 def bwd_workspace_bytes(dtype, b, h, t, d, causal, fastest: bool = False) -> int:
     """ctattn_bwd_workspace_bytes (linear in B*H*T), or with fastest=True
-    ctattn_bwd_workspace_bytes_max (the bf16 / fp16 d = 128 dS tiles, about B*H*T^2 bytes)."""
+    ctattn_bwd_workspace_bytes_max (with the dS tiles where the kernels take them: bf16 / fp16
+    at d = 128, fp32 at d in {64, 128} under DETERMINISTIC and at d = 128 on large grids under
+    AUTO; about B*H*T^2 bytes at 16-bit, twice that at fp32)."""
     code = _DTYPE_CODE[dtype] if isinstance(dtype, torch.dtype) else int(dtype)
     fn = "ctattn_bwd_workspace_bytes_max" if fastest else "ctattn_bwd_workspace_bytes"
     n = getattr(load(), fn)(code, b, h, t, d, int(bool(causal)))

@@ -30,6 +30,12 @@
 //     computes a 32-row x (d/2)-column tile of dQ = dS K over the block's 64 keys (d = 32:
 //     two waves, 32 x 32 each) and adds it with fp32 atomics into dq (pre-zeroed by the
 //     preprocess kernel), one iteration later (see flush_dq).
+//   * dS mode (DS, d >= 64, when the workspace holds every 64 x 64 dS tile of the mask): no
+//     dQ work and no atomics here.  Each wave copies a quarter of the block's dS from LDS to
+//     the workspace instead, in the order of the A operands of dQ = dS K, and
+//     bwd_f32_dq_ds_kernel then computes dQ query-major from those tiles, each element summed
+//     by one lane in key-block order: deterministic, and the atomics' write traffic (about
+//     ten times the dQ bytes) becomes one pass of dS stores and loads.
 //
 // Which kernels run: this 64-key kernel for causal masks with atomic dQ and d >= 64 (where
 // its balance and smaller diagonal win); the 128-key kernel of attn_bwd_k128.hip, with half
@@ -42,6 +48,8 @@
 #include "attn_mfma_common.h"
 
 #include <math.h>
+
+#include <algorithm>
 
 namespace ctattn {
 namespace {
@@ -75,6 +83,22 @@ struct BwdCfg {
 };
 
 #define CTATTN_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+// dS tiles of the dS mode: one 64 x 64 tile (16 KB) per (query block, key block) pair of 64,
+// causal: key block <= query block, packed per head in row-major (triangle) order.  A tile is
+// four 32 x 32 sub-tiles, sub-tile (row slice rs, key slice ks) at 1024 (2 rs + ks); in a
+// sub-tile, float4 m (m = 0..3) of lane (col, half) holds dS[row 32 rs + col][key 32 ks + 8 m
+// + 4 half + t], t = 0..3, at floats 4 (64 m + lane) .. + 3: the A operands of four MFMA steps
+// of dQ = dS K, so one 16-byte store per lane writes (and one load reads) 1 KB contiguously.
+constexpr int kDsTileFloats = 64 * 64;
+__host__ __device__ inline int64_t f32_ds_tiles_per_head(int64_t T, bool causal) {
+    const int64_t n = (T + 63) / 64;
+    return causal ? n * (n + 1) / 2 : n * n;
+}
+__device__ inline int64_t f32_ds_tile(int bh, int qb, int kb, int nqb, int causal, int64_t tph) {
+    const int64_t t = causal ? int64_t(qb) * (qb + 1) / 2 + kb : int64_t(qb) * nqb + kb;
+    return (int64_t(bh) * tph + t) * kDsTileFloats;
+}
 
 // Waves per SIMD the kernel is compiled for: two for d <= 64 (<= 256 VGPRs); d = 128 needs
 // more registers than that and runs one wave per SIMD.
@@ -157,13 +181,14 @@ __device__ __forceinline__ void bwd_wave_block(floatx16 (&dk_acc)[D / 32], float
     for (int r = 0; r < 16; ++r) ds_lds[(rb + acc_row(r, half)) * C::SS + kb_local + col] = dp[r];
 }
 
-template <int D, bool SPLIT>
+template <int D, bool SPLIT, bool DS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occupancy<D>::waves,
                                                                      BwdF32Occupancy<D>::waves))) void bwd_f32_mfma_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ dout, const float *__restrict__ lse,
     const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dk,
-    float *__restrict__ dv, int T, int BH, int causal, float kscale, float inv_sqrt_d) {
+    float *__restrict__ dv, float *__restrict__ ds_ws, int T, int BH, int causal, float kscale,
+    float inv_sqrt_d) {
     using C = BwdCfg<D>;
     constexpr int split = SPLIT ? 1 : 0;
     __shared__ __attribute__((aligned(16))) float qdo_lds[2 * C::TILE];  // Q then dO, [BM][KS] each
@@ -275,14 +300,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
         }
     };
 
+    // DS: this wave's quarter of the previous block's dS (row slice wave >> 1, key slice
+    // wave & 1), read from LDS before the barrier that lets the next block overwrite it and
+    // stored after that barrier, so the loop-top wait never waits on fresh stores.
+    const int64_t ds_tph = f32_ds_tiles_per_head(T, causal != 0);
+    floatx4 ds_pend[4];
+    float *ds_dst = nullptr;  // the pending sub-tile's place in the workspace, null if none
+    auto flush_ds = [&]() {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) *reinterpret_cast<floatx4 *>(ds_dst + (m * kWave + lane) * 4) = ds_pend[m];
+    };
+
     if (qb_begin < qb_end) issue(qb_begin * C::BM);
     for (int qb = qb_begin; qb < qb_end; ++qb) {
         const int r0 = qb * C::BM;
         // The block's loads have landed (vmcnt = 0) and, after the barrier, every wave's are
-        // visible; every wave is also done reading the previous block's dS.
-        __builtin_amdgcn_s_waitcnt(0xF70);
+        // visible; every wave is also done reading the previous block's dS (DS: its LDS reads
+        // of that dS have returned, lgkmcnt = 0).
+        __builtin_amdgcn_s_waitcnt(DS ? 0x070 : 0xF70);
         __syncthreads();
-        if (pend_rq0 >= 0) flush_dq();
+        if constexpr (DS) {
+            if (ds_dst != nullptr) flush_ds();
+        } else {
+            if (pend_rq0 >= 0) flush_dq();
+        }
 
         const int r0w = r0 + 32 * rs;
         const bool wave_active = kw0 < T && r0w < T && (!causal || kw0 <= r0w + 31);
@@ -298,8 +339,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
         __syncthreads();  // dS of every wave visible; Q / dO / LSE / delta no longer read
         if (qb + 1 < qb_end) issue(r0 + C::BM);
 
-        // dQ[r0 + 32 qrs .. +31][dq_col0 ..] = sum over the block's active keys of dS K.
-        if (dq_wave) {
+        if constexpr (DS) {
+            const int srs = wave >> 1, sks = wave & 1;
+            const int rq0 = r0 + 32 * srs, kw2 = k0 + 32 * sks;
+            ds_dst = nullptr;
+            if (kw2 < T && rq0 < T && (!causal || kw2 <= rq0 + 31)) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    ds_pend[m] = *reinterpret_cast<const floatx4 *>(
+                        &ds_lds[(32 * srs + col) * C::SS + 32 * sks + 8 * m + 4 * half]);
+                ds_dst = ds_ws + f32_ds_tile(bh, qb, kb, nqb, causal, ds_tph) + (2 * srs + sks) * 1024;
+            }
+        } else if (dq_wave) {
+            // dQ[r0 + 32 qrs .. +31][dq_col0 ..] = sum over the block's active keys of dS K.
 #pragma unroll
             for (int j = 0; j < C::DQ_T; ++j) dq_pend[j] = zero16();
             const int rq0 = r0 + 32 * qrs;
@@ -322,7 +374,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BwdF32Occup
             pend_rq0 = rq0;
         }
     }
-    if (pend_rq0 >= 0) flush_dq();
+    if constexpr (DS) {
+        if (ds_dst != nullptr) flush_ds();
+    } else {
+        if (pend_rq0 >= 0) flush_dq();
+    }
 
     // dK^T / dV^T of the two row slices: rs = 1 hands its sums to rs = 0 through LDS (the Q /
     // dO blocks are free: no load is in flight after the last block, and every wave has
@@ -447,6 +503,159 @@ __global__ __launch_bounds__(256) void dq_reduce_kernel(const float *__restrict_
     }
 }
 
+// dQ = dS K / sqrt(d) from the dS tiles of the dS mode (d >= 64), query-major: a workgroup
+// owns 64 rows of one head and walks its key blocks (causal: up to the diagonal); causal
+// workgroups run longest first.  Four waves:
+//   KH = 1 (d = 128): row slice w >> 1, column half w & 1, every key block in order;
+//   KH = 2 (d = 64):  row slice w >> 1, all d columns, key blocks of parity w & 1 (its own
+//     double-buffered K tiles), so the longest workgroup takes half as many steps and each
+//     dS sub-tile is loaded once; the odd half hands its sums to the even half through LDS
+//     at the end.
+// Each dQ element is thus summed in a fixed order and stored once.  K blocks go global ->
+// LDS directly (padded rows; rows past T re-read row T - 1, whose dS is 0); dS goes global ->
+// registers a step ahead, one 16-byte load per lane per four MFMA steps.
+template <int D, int KH>
+__global__ __launch_bounds__(256) void bwd_f32_dq_ds_kernel(const float *__restrict__ k,
+                                                           const float *__restrict__ ds_ws,
+                                                           float *__restrict__ dq, int T, int BH, int causal,
+                                                           float inv_sqrt_d) {
+    using C = BwdCfg<D>;
+    static_assert(KH == 1 || KH == 2, "key halves");
+    constexpr int DT = KH == 1 ? D / 64 : D / 32;  // 32-wide dQ tiles per wave
+    constexpr int LW = C::NW / KH;                 // waves loading one K tile
+    constexpr int KI = (C::CHUNKS + LW * kWave - 1) / (LW * kWave);  // its loads per lane
+    __shared__ __attribute__((aligned(16))) float k_lds[KH][2][C::TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    const int qrs = wave >> 1;
+    const int kh = KH == 2 ? (wave & 1) : 0;
+    const int lw = KH == 2 ? qrs : wave;  // index among the waves loading this K tile
+    const int dq_col0 = KH == 1 ? (wave & 1) * (D / 2) : 0;
+
+    const int id = blockIdx.x;
+    const int bh = id % BH;
+    const int nqb = (T + C::BM - 1) / C::BM;
+    const int qb = causal ? nqb - 1 - id / BH : id / BH;
+    const int rq0 = qb * C::BM + 32 * qrs;  // first row of this wave's tile
+    const int nkb = causal ? qb + 1 : nqb;
+    const int nit = (nkb + KH - 1) / KH;
+    const int64_t base = int64_t(bh) * T * D;
+    const int64_t tph = f32_ds_tiles_per_head(T, causal != 0);
+
+    // Key block kb -> k_lds[kh][buf]: lane writes chunk P = (lw * KI + i) * 64 + lane of the
+    // padded block (row P / C4P, chunk P % C4P; the pad chunk re-reads chunk 0).
+    auto issue_k = [&](int kb, int buf) {
+        const int j0 = kb * C::BN;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int P = (lw * KI + i) * kWave + lane;
+            if (C::CHUNKS % (LW * kWave) == 0 || P < C::CHUNKS) {
+                const int r = P / C::C4P;
+                const int c = P - r * C::C4P;
+                const int64_t goff = base + int64_t(min(j0 + r, T - 1)) * D + 4 * (c < C::C4 ? c : 0);
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(k + goff),
+                                                 CTATTN_LDS(&k_lds[kh][buf][(lw * KI + i) * 4 * kWave]), 16, 0, 0);
+            }
+        }
+    };
+    // Sub-tile (qrs, ks2) of key block kb holds dS only where the key-major kernel stored it.
+    auto active = [&](int kb, int ks2) {
+        const int kw2 = kb * C::BN + 32 * ks2;
+        return kb < nkb && kw2 < T && rq0 < T && (!causal || kw2 <= rq0 + 31);
+    };
+    auto load_ds = [&](int kb, floatx4 (&a)[2][4]) {
+        const float *t = ds_ws + f32_ds_tile(bh, qb, kb, nqb, causal, tph) + 2 * qrs * 1024;
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+            if (!active(kb, ks2)) continue;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                a[ks2][m] = *reinterpret_cast<const floatx4 *>(t + ks2 * 1024 + (m * kWave + lane) * 4);
+        }
+    };
+
+    floatx16 acc[DT];
+#pragma unroll
+    for (int j = 0; j < DT; ++j) acc[j] = zero16();
+    // Step it: this wave's key block kb = KH it + kh.  Wait for its K and dS, prefetch the
+    // next, then the MFMAs.
+    auto step = [&](int it, floatx4 (&cur)[2][4], floatx4 (&nxt)[2][4]) __attribute__((always_inline)) {
+        const int buf = it & 1;
+        const int kb = KH * it + kh;
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt = 0: this block's K (to LDS) and dS (to registers)
+        __syncthreads();                    // every lane's K visible; every wave done with buf ^ 1
+        if (kb + KH < nkb) {
+            issue_k(kb + KH, buf ^ 1);
+            load_ds(kb + KH, nxt);
+        }
+        const float *kt = k_lds[kh][buf];
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+            if (!active(kb, ks2)) continue;
+            // MFMA i = (4 m + t) DT + j: A = dS of key 32 ks2 + 8 m + 4 half + t, B = K of that
+            // key, column dq_col0 + 32 j + col.  The B reads (one ds_read_b32 each) go through
+            // a ring of 8 issued 6 MFMAs ahead, so no MFMA waits on its own read.
+            constexpr int NV = 16 * DT, R = 8, AHEAD = 6;
+            auto bread = [&](int i) __attribute__((always_inline)) {
+                const int st = i / DT, j = i % DT;
+                return kt[(32 * ks2 + 8 * (st / 4) + 4 * half + st % 4) * C::KS + dq_col0 + 32 * j + col];
+            };
+            float ring[R];
+#pragma unroll
+            for (int i = 0; i < AHEAD; ++i) ring[i % R] = bread(i);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                if (i + AHEAD < NV) ring[(i + AHEAD) % R] = bread(i + AHEAD);
+                __builtin_amdgcn_sched_barrier(0);
+                const int st = i / DT, j = i % DT;
+                acc[j] = mfma32x32x2(cur[ks2][st / 4][st % 4], ring[i % R], acc[j]);
+            }
+        }
+    };
+    floatx4 a0[2][4], a1[2][4];
+    if (kh < nkb) {
+        issue_k(kh, 0);
+        load_ds(kh, a0);
+    }
+    for (int it = 0; it < nit; it += 2) {
+        step(it, a0, a1);
+        if (it + 1 < nit) step(it + 1, a1, a0);
+    }
+    if constexpr (KH == 2) {
+        // The odd key half's sums -> LDS (the K tiles are free once every wave is past its
+        // last step), added by the even half in that order.
+        float *red = &k_lds[0][0][0];  // [qrs][DT][16][64]
+        static_assert(2 * DT * 16 * kWave <= KH * 2 * C::TILE, "reduction buffer");
+        __syncthreads();
+        if (kh == 1) {
+#pragma unroll
+            for (int j = 0; j < DT; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[((qrs * DT + j) * 16 + r) * kWave + lane] = acc[j][r];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int j = 0; j < DT; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[j][r] += red[((qrs * DT + j) * 16 + r) * kWave + lane];
+    }
+    if (rq0 >= T) return;
+    // Lane (col, half), register r of tile j: row rq0 + acc_row(r, half), column dq_col0 + 32 j + col.
+    float *p0 = dq + base + int64_t(rq0) * D + dq_col0 + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int dr = acc_row(r, half);
+        if (rq0 + dr >= T) continue;
+#pragma unroll
+        for (int j = 0; j < DT; ++j) p0[dr * D + 32 * j] = acc[j][r] * inv_sqrt_d;
+    }
+}
+
 // Key-block size of the deterministic dQ partials: they come from the 128-key kernel.  The
 // partials cost one [B, H, T, d] fp32 plane per key block, so they are used only up to
 // kMaxPartialBlocks key blocks (workspace <= 8 planes, linear in B*H*T); longer sequences
@@ -458,17 +667,21 @@ bool use_k64_kernel(const AttnShape &s, DqMode mode) {
     return s.causal && s.d >= 64 && mode == DqMode::Atomic;
 }
 
+// ds: the dS tiles' workspace (d >= 64, f32_ds_bytes of it), or null.  With it the 64-key
+// kernel runs in dS mode (any mask, either policy: no atomics on dQ) and the query-major
+// bwd_f32_dq_ds_kernel computes dQ.
 template <int D>
 hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *o,
                    const float *dout, const float *lse, float *delta, float *dq, float *dk,
-                   float *dv, float *dq_part, DqMode mode, const AttnShape &s, hipStream_t stream) {
+                   float *dv, float *dq_part, float *ds, DqMode mode, const AttnShape &s, hipStream_t stream) {
     const int64_t rows = s.rows();
     if (s.T > 2147483647 / D) return hipErrorInvalidValue;
     const unsigned pre_blocks = stride_grid((rows * (D / 4) + 255) / 256, 256);
-    const bool k64 = D >= 64 && use_k64_kernel(s, mode);
+    const bool ds_mode = D >= 64 && ds != nullptr;
+    const bool k64 = D >= 64 && (ds_mode || use_k64_kernel(s, mode));
     const bool split = bwd_f32_use_split(s, k64, stream);
     float *dk_zero = split ? dk : nullptr, *dv_zero = split ? dv : nullptr;
-    if (mode == DqMode::Atomic) {
+    if (mode == DqMode::Atomic && !ds_mode) {
         hipLaunchKernelGGL((bwd_preprocess_f32_kernel<D, true>), dim3(pre_blocks), dim3(256), 0, stream,
                            o, dout, delta, dq, dk_zero, dv_zero, rows);
     } else {
@@ -484,14 +697,17 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
         if (!grid_fits(blocks, C::NW * kWave)) return hipErrorInvalidValue;
         const float kscale = kLog2e / sqrtf(float(s.scale_dim()));
         const float inv_sqrt_d = 1.f / sqrtf(float(s.scale_dim()));
-        if (split)
-            hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, true>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
-                               q, k, v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
-                               inv_sqrt_d);
-        else
-            hipLaunchKernelGGL((bwd_f32_mfma_kernel<D, false>), dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream,
-                               q, k, v, dout, lse, delta, dq, dk, dv, int(s.T), int(s.bh()), int(s.causal), kscale,
-                               inv_sqrt_d);
+        auto kern = split ? (ds_mode ? bwd_f32_mfma_kernel<D, true, true> : bwd_f32_mfma_kernel<D, true, false>)
+                          : (ds_mode ? bwd_f32_mfma_kernel<D, false, true> : bwd_f32_mfma_kernel<D, false, false>);
+        hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(C::NW * kWave), 0, stream, q, k, v, dout, lse, delta,
+                           dq, dk, dv, ds, int(s.T), int(s.bh()), int(s.causal), kscale, inv_sqrt_d);
+        e = hipGetLastError();
+        if (e != hipSuccess || !ds_mode) return e;
+        const int64_t qblocks = (s.T + C::BM - 1) / C::BM * s.bh();
+        if (!grid_fits(qblocks, C::NW * kWave)) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((bwd_f32_dq_ds_kernel<D, D == 64 ? 2 : 1>), dim3(unsigned(qblocks)), dim3(C::NW * kWave), 0,
+                           stream, k, ds,
+                           dq, int(s.T), int(s.bh()), int(s.causal), inv_sqrt_d);
         return hipGetLastError();
       }
     }
@@ -526,7 +742,29 @@ DqMode deterministic_mode(const AttnShape &s) {
     return (s.T + kPartialBN - 1) / kPartialBN <= kMaxPartialBlocks ? DqMode::Partial : DqMode::Separate;
 }
 
+// The fp32 dS tiles take the workspace only up to this size.
+constexpr int64_t kF32DsMaxBytes = int64_t(4) << 30;
+
 }  // namespace
+
+int64_t f32_ds_bytes(const AttnShape &s) {
+    if ((s.d != 64 && s.d != 128) || s.T > 32768) return 0;
+    const int64_t per_head = f32_ds_tiles_per_head(s.T, s.causal) * kDsTileFloats * int64_t(sizeof(float));
+    if (per_head > kF32DsMaxBytes || s.bh() > kF32DsMaxBytes / per_head) return 0;
+    return s.bh() * per_head;
+}
+
+// Whether the fp32 backward takes the dS path when its scratch holds the tiles.  DETERMINISTIC:
+// always -- same-process A/B against the dQ partials / query-major kernel, 0.54-0.95 of their
+// time (B8 H12 T1024 d64 causal 337 against 355 us, B4 H12 T4096 d64 2241 against 2889).
+// AUTO: only at d = 128 with at least 1024 key blocks of 64 in the grid, where it beat the
+// atomic kernel (0.974-0.989: B8 H12 T1024, B4 H16 T2048, causal and full); at d = 64 the
+// separate dQ pass costs more than the atomics it removes (+3 to +8 % on the same grids), and
+// short grids pay its launch and tail (+3 to +27 %).
+bool f32_ds_wanted(const AttnShape &s, bool deterministic) {
+    if (f32_ds_bytes(s) == 0) return false;
+    return deterministic || (s.d == 128 && (s.T + 63) / 64 * s.bh() >= 1024);
+}
 
 bool mfma_bwd_supported(int dtype, int64_t d) {
     (void)dtype;  // the fp32, bf16 and fp16 kernels all cover d in {32, 64, 128}
@@ -535,8 +773,12 @@ bool mfma_bwd_supported(int dtype, int64_t d) {
 
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic, bool with_ds) {
     if (dtype == 1 || dtype == 2) return bf16_bwd_workspace_bytes(s, deterministic, with_ds);
-    if (!deterministic || deterministic_mode(s) != DqMode::Partial) return 0;  // fp32: delta only
-    return (s.T + kPartialBN - 1) / kPartialBN * s.rows() * s.d * int64_t(sizeof(float));  // <= 8 dQ planes
+    // fp32: the deterministic partials (<= 8 dQ planes) or nothing beyond delta; with_ds, room
+    // for the dS tiles where the policy takes them (f32_ds_wanted), which then use the scratch.
+    int64_t b = 0;
+    if (deterministic && deterministic_mode(s) == DqMode::Partial)
+        b = (s.T + kPartialBN - 1) / kPartialBN * s.rows() * s.d * int64_t(sizeof(float));
+    return with_ds && f32_ds_wanted(s, deterministic) ? std::max(b, f32_ds_bytes(s)) : b;
 }
 
 hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *v,
@@ -550,16 +792,18 @@ hipError_t launch_mfma_bwd(int dtype, const void *q, const void *k, const void *
     const DqMode mode = deterministic ? deterministic_mode(s) : DqMode::Atomic;
     auto f = [](const void *p) { return static_cast<const float *>(p); };
     auto g = [](void *p) { return static_cast<float *>(p); };
+    const int64_t dsb = f32_ds_bytes(s);
+    float *ds = f32_ds_wanted(s, deterministic) && extra != nullptr && extra_bytes >= dsb ? g(extra) : nullptr;
     switch (s.d) {
         case 32:
-            return bwd_f32<32>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), mode, s,
-                               stream);
+            return bwd_f32<32>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), nullptr,
+                               mode, s, stream);
         case 64:
-            return bwd_f32<64>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), mode, s,
-                               stream);
+            return bwd_f32<64>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), ds, mode,
+                               s, stream);
         case 128:
-            return bwd_f32<128>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), mode, s,
-                                stream);
+            return bwd_f32<128>(f(q), f(k), f(v), f(o), f(dout), lse, delta, g(dq), g(dk), g(dv), g(extra), ds, mode,
+                                s, stream);
         default:
             return hipErrorNotSupported;
     }

@@ -69,8 +69,14 @@ hipError_t launch_f16_bwd(const void *q, const void *k, const void *v, const voi
 hipError_t launch_bf16_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
                            const float *lse, float *delta, void *dq, void *dk, void *dv, void *extra,
                            int64_t extra_bytes, bool deterministic, const AttnShape &s, hipStream_t stream);
+// fp32 dS tiles (d in {64, 128}): 16 KB per pair of 64-row query and 64-key blocks of the mask,
+// at most 4 GiB (0 beyond).  Given that much scratch, the fp32 backward stores dS from its
+// key-major kernel and computes dQ query-major from it, without atomics: under DETERMINISTIC,
+// and under AUTO at d = 128 on grids of at least 1024 key blocks (f32_ds_wanted).
+int64_t f32_ds_bytes(const AttnShape &s);
+bool f32_ds_wanted(const AttnShape &s, bool deterministic);
 // Scratch of launch_mfma_bwd beyond delta; with_ds = false gives the smallest that works (the
-// bf16 / fp16 dS tiles left out).
+// bf16 / fp16 / fp32 dS tiles left out).
 int64_t mfma_bwd_workspace_bytes(int dtype, const AttnShape &s, bool deterministic, bool with_ds = true);
 // ---- fp64 kernels on fp64 MFMA (attn_f64_mfma.hip), d in {32, 64, 128}; lse and delta fp64.
 // The backward runs its own preprocess into `delta` ([B, H, T] fp64) and needs no other

@@ -72,12 +72,15 @@ enum ctattn_dtype {
  *                  ctattn_tensor_matmul) then run on the projection GEMM family instead of
  *                  the split-K-in-workgroup linear GEMMs.
  *   DETERMINISTIC  MFMA kernels without atomics, bitwise-reproducible gradients.  The fp32
- *                  backward stores dQ partials per 128-key block and sums them in a fixed
- *                  order while T <= 1024 (workspace: ceil(T/128) * B*H*T*d fp32 more than
- *                  AUTO, at most 8 dQ planes); for longer T it computes dK / dV in a
- *                  key-major kernel and dQ in a query-major one (each element summed by one
- *                  lane in a fixed order) with the same workspace as AUTO.  bf16 / fp16 /
- *                  fp64: the same kernels as AUTO, which use no atomics. */
+ *                  backward at d in {64, 128}, given a workspace that holds its dS tiles
+ *                  (ctattn_bwd_workspace_bytes_max), stores dS from the key-major kernel
+ *                  and computes dQ = dS K query-major (each element summed by one lane in a
+ *                  fixed order).  Otherwise it stores dQ partials per 128-key block and sums
+ *                  them in a fixed order while T <= 1024 (workspace: ceil(T/128) * B*H*T*d
+ *                  fp32 more than AUTO, at most 8 dQ planes); for longer T it computes dK /
+ *                  dV in a key-major kernel and dQ in a query-major one that recomputes S and
+ *                  dP, with the same workspace as AUTO.  bf16 / fp16 / fp64: the same kernels
+ *                  as AUTO, which use no atomics. */
 enum ctattn_policy {
     CTATTN_POLICY_AUTO = 0,
     CTATTN_POLICY_GENERIC = 1,
@@ -120,8 +123,8 @@ CTATTN_API int ctattn_fwd_ws(int dtype, const void *q, const void *k, const void
  * A head dim that runs padded to width dp (see the conventions above) also needs room for
  * the eight padded copies (q, k, v, o, dout, dq, dk, dv: 8 * B*H*T*dp elements).
  * The size is linear in B*H*T, as the reference's backward memory is (it never holds a
- * T x T object): bf16 / fp16 at d = 128 (also padded onto it) include the dS tiles below
- * only while they take at most twice the bytes of q, k and v together (causal: T <= 12 d).
+ * T x T object): the dS tiles below are included only while the bytes they add take at most
+ * twice the bytes of q, k and v together (bf16 / fp16 causal: T <= 12 d).
  */
 CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                    int causal);
@@ -132,7 +135,11 @@ CTATTN_API int64_t ctattn_bwd_workspace_bytes(int dtype, int64_t B, int64_t H, i
  * onto it): the dS tiles -- the dK/dV kernel stores the bf16 dS it computes and the dQ kernel
  * multiplies it by K instead of recomputing S and dP, 2 bytes per (row, key) pair of the mask
  * rounded to 32 x 32 tiles (causal B*H*T^2 bytes, B1 H32 T8192: 2.2 GB; 2-7 % faster
- * backward).  Above 4 GiB of dS they are left out and this equals ctattn_bwd_workspace_bytes.
+ * backward).  fp32 at d in {64, 128} under DETERMINISTIC, and at d = 128 with at least 1024
+ * key blocks of 64 (ceil(T/64)*B*H) under AUTO: the fp32 dS tiles, 16 KiB per 64 x 64 tile of
+ * the mask (causal about 2*B*H*T^2 bytes; B8 H12 T1024: 214 MB), from which dQ is computed
+ * without atomics (DETERMINISTIC 5-46 % faster than without them, AUTO at d = 128 1-3 %).
+ * Above 4 GiB of dS they are left out and this equals ctattn_bwd_workspace_bytes.
  */
 CTATTN_API int64_t ctattn_bwd_workspace_bytes_max(int dtype, int64_t B, int64_t H, int64_t T, int64_t d,
                                                   int causal);
@@ -144,9 +151,9 @@ CTATTN_API int64_t ctattn_bwd_workspace_bytes_max(int dtype, int64_t B, int64_t 
  * dq, dk, dv are fully overwritten (no pre-zeroing needed).  workspace should hold
  * ctattn_bwd_workspace_bytes(...) bytes, queried under the same policy, or any size up to
  * ctattn_bwd_workspace_bytes_max(...); a smaller one works down to the size without the
- * bf16 / fp16 dS tiles (the error message names the minimum).  With a workspace that holds
- * the dS tiles dQ = dS K reads them back, else dQ recomputes S and dP: the same results up to
- * bf16 rounding of dS.
+ * dS tiles (the error message names the minimum).  With a workspace that holds the dS tiles
+ * dQ = dS K reads them back; else bf16 / fp16 dQ recomputes S and dP (the same results up to
+ * bf16 rounding of dS) and fp32 takes the policy's other dQ scheme.
  * Reproducibility depends on the policy (see enum ctattn_policy).
  */
 CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v, const void *o,
@@ -164,8 +171,8 @@ CTATTN_API int ctattn_bwd(int dtype, const void *q, const void *k, const void *v
  * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc.  It calls no hipMalloc / hipFree and no allocating library routine.
  *   - same arguments, kernels and results as ctattn_bwd under the current policy, minus the
- *     workspace; it uses the smallest workspace ctattn_bwd accepts (the bf16 / fp16 dS tiles
- *     only when they fit too), and problems that need more than the scratch size are
+ *     workspace; it uses the smallest workspace ctattn_bwd accepts (the dS tiles only when
+ *     they fit too), and problems that need more than the scratch size are
  *     rejected with hipErrorInvalidValue before any GPU work (AUTO needs 4 bytes per row
  *     B*H*T for fp32, 8 for bf16 / fp16 / fp64: up to 8 Mi or 4 Mi rows).
  *   - the scratch of the stream's device is found once per device (hipGetSymbolAddress) and

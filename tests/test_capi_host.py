@@ -158,8 +158,10 @@ def test_padded_head_dim_workspace(lib):
 
 def test_deterministic_workspace_stays_linear(lib):
     """DETERMINISTIC fp32: dQ partials per 128-key block (one fp32 [B, H, T, d] plane each)
-    while T <= 1024, none beyond (the query-major dQ kernel), so the workspace is at most
-    AUTO's plus 8 dQ planes -- linear in B*H*T at every T.  AUTO needs delta only."""
+    while T <= 1024, none beyond (the query-major dQ kernel); the dS tiles (d >= 64) in their
+    room while they add at most 2 x (q + k + v).  So the workspace is at most AUTO's plus 8 dQ
+    planes plus 24 bytes per row element -- linear in B*H*T at every T.  AUTO needs delta only
+    (d <= 64; its dS tiles are never in the default at these shapes)."""
     for shape in [(8, 12, 1024, 64), (2, 4, 1000, 32), (1, 32, 1025, 128), (1, 32, 131072, 128),
                   (16, 32, 32768, 64)]:
         b, h, t, d = shape
@@ -174,8 +176,13 @@ def test_deterministic_workspace_stays_linear(lib):
             finally:
                 _capi.set_policy(prev)
         assert sizes[_capi.POLICY_AUTO] == rows_bytes, (shape, sizes)
-        assert sizes[_capi.POLICY_DETERMINISTIC] == rows_bytes + partials, (shape, sizes)
-        assert sizes[_capi.POLICY_DETERMINISTIC] <= rows_bytes + 8 * b * h * t * d * 4
+        n64 = (t + 63) // 64
+        ds = b * h * n64 * (n64 + 1) // 2 * 16384 if d >= 64 and t <= 32768 else 0
+        ds = ds if ds <= 4 << 30 else 0
+        room = ((max(partials, ds) + 255) // 256) * 256
+        with_ds = room - partials <= 2 * 3 * b * h * t * d * 4
+        assert sizes[_capi.POLICY_DETERMINISTIC] == rows_bytes + (room if with_ds else partials), (shape, sizes)
+        assert sizes[_capi.POLICY_DETERMINISTIC] <= rows_bytes + (8 + 24) * b * h * t * d * 4
 
 
 def test_no_gpu_call_raises_cleanly(lib):
@@ -200,7 +207,7 @@ def test_row_limit_boundary(lib):
 def test_bf16_ds_workspace(lib):
     """bf16 / fp16 at d = 128: ctattn_bwd_workspace_bytes_max asks for the dS tiles (2 KiB per
     32 x 32 tile of the mask: a triangle when causal) on top of delta and -LSE log2(e); other
-    head dims and fp32 do not, and above 4 GiB of tiles (or T > 65536) it stays linear in rows.
+    head dims do not, and above 4 GiB of tiles (or T > 65536) it stays linear in rows.
     The default ctattn_bwd_workspace_bytes includes the tiles only while they take at most
     twice the bytes of q, k and v."""
     def al(x):
@@ -218,24 +225,64 @@ def test_bf16_ds_workspace(lib):
                 assert lib.ctattn_bwd_workspace_bytes(dtype, b, h, t, 128, causal) == base + (ds if in_default else 0)
             for fn in (lib.ctattn_bwd_workspace_bytes, lib.ctattn_bwd_workspace_bytes_max):
                 assert fn(1, b, h, t, 64, causal) == base
-                assert fn(0, b, h, t, 128, causal) == al(rows * 4)
     # B1 H32 T16384 causal: 8.6 GB of tiles, above the 4 GiB limit.
     assert lib.ctattn_bwd_workspace_bytes_max(1, 1, 32, 16384, 128, 1) == 2 * al(32 * 16384 * 4)
     assert lib.ctattn_bwd_workspace_bytes_max(1, 1, 1, 1 << 20, 128, 1) == 2 * al((1 << 20) * 4)
+
+
+def test_f32_ds_workspace(lib):
+    """fp32 dS tiles (16 KiB per 64 x 64 tile of the mask, a triangle when causal), asked for by
+    ctattn_bwd_workspace_bytes_max where the policy takes the dS path: DETERMINISTIC at d in
+    {64, 128} (in the room of the dQ partials, one plane per 128-key block up to T = 1024,
+    whichever is larger); AUTO only at d = 128 on grids of at least 1024 key blocks of 64.
+    Never at d = 32, nor above 4 GiB of tiles.  The default includes them only while the bytes
+    they add take at most twice the bytes of q, k and v."""
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    for (b, h, t) in [(8, 12, 1024), (2, 3, 333), (1, 2, 64), (2, 64, 512)]:
+        rows, n = b * h * t, (t + 63) // 64
+        for causal, tiles in ((1, n * (n + 1) // 2), (0, n * n)):
+            for d in (64, 128):
+                ds = b * h * tiles * 16384
+                in_default = ds <= 2 * 3 * rows * d * 4
+                auto_ds = d == 128 and n * b * h >= 1024
+                want_max = al(rows * 4) + (al(ds) if auto_ds else 0)
+                assert lib.ctattn_bwd_workspace_bytes_max(0, b, h, t, d, causal) == want_max
+                want = al(rows * 4) + (al(ds) if auto_ds and in_default else 0)
+                assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, d, causal) == want
+                prev = _capi.set_policy(_capi.POLICY_DETERMINISTIC)
+                try:
+                    planes = -(-t // 128) * rows * d * 4 if t <= 1024 else 0
+                    assert lib.ctattn_bwd_workspace_bytes_max(0, b, h, t, d, causal) == al(rows * 4) + al(max(planes, ds))
+                    adds = al(max(planes, ds)) - al(planes)
+                    want = al(rows * 4) + (al(max(planes, ds)) if adds <= 2 * 3 * rows * d * 4 else al(planes))
+                    assert lib.ctattn_bwd_workspace_bytes(0, b, h, t, d, causal) == want
+                finally:
+                    _capi.set_policy(prev)
+            for fn in (lib.ctattn_bwd_workspace_bytes, lib.ctattn_bwd_workspace_bytes_max):
+                assert fn(0, b, h, t, 32, causal) == al(rows * 4)
+    # B1 H32 T8192 d128 causal: 4.3 GB of tiles, above the 4 GiB limit.
+    prev = _capi.set_policy(_capi.POLICY_DETERMINISTIC)
+    try:
+        assert lib.ctattn_bwd_workspace_bytes_max(0, 1, 32, 8192, 128, 1) == al(32 * 8192 * 4)
+    finally:
+        _capi.set_policy(prev)
 
 
 def test_default_bwd_workspace_is_linear_in_rows(lib):
     """The default backward workspace grows linearly with B * H * T at every T, like the
     reference's backward memory (which never holds a T x T object): at most 8 bytes per row
     of statistics plus, while they are included, dS tiles of at most 2 x (q + k + v) =
-    1536 bytes per row at bf16 d = 128, plus alignment.  B1 H32 T32768 d128 bf16 included."""
-    for dtype in (1, 2):
+    1536 bytes per row at bf16 d = 128 (fp32: 1536 at d = 64, 3072 at d = 128), plus alignment.
+    B1 H32 T32768 d128 bf16 included."""
+    for dtype, d, per_row in ((1, 128, 1536), (2, 128, 1536), (0, 64, 1536), (0, 128, 3072)):
         for causal in (0, 1):
             for t in [64, 128, 333, 1024, 1536, 2048, 4096, 8192, 16384, 32768, 65536]:
                 rows = 32 * t
-                n = lib.ctattn_bwd_workspace_bytes(dtype, 1, 32, t, 128, causal)
-                assert 0 < n <= rows * (8 + 1536) + 512, (dtype, causal, t, n)
-                assert n <= lib.ctattn_bwd_workspace_bytes_max(dtype, 1, 32, t, 128, causal)
+                n = lib.ctattn_bwd_workspace_bytes(dtype, 1, 32, t, d, causal)
+                assert 0 < n <= rows * (8 + per_row) + 512, (dtype, causal, t, n)
+                assert n <= lib.ctattn_bwd_workspace_bytes_max(dtype, 1, 32, t, d, causal)
     assert lib.ctattn_bwd_workspace_bytes(1, 1, 32, 32768, 128, 1) <= 32 * 32768 * 8 + 512
 
 

@@ -271,6 +271,54 @@ def test_deterministic_long_sequence_f32(causal, d):
     assert_close(r1, want, "f32", f"{shape} causal={causal} deterministic")
 
 
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+@pytest.mark.parametrize("shape", [(1, 3, 333, 64), (2, 2, 64, 128), (1, 2, 1100, 64), (4, 64, 300, 64),
+                                   (1, 3, 333, 128)], ids=lambda s: "x".join(map(str, s)))
+def test_f32_ds_path_deterministic(shape, causal):
+    """fp32 DETERMINISTIC with the workspace ctattn_bwd_workspace_bytes_max asks for (d in
+    {64, 128}): the 64-key kernel stores dS in the workspace and the query-major kernel
+    multiplies it by K -- no atomics on dQ, no partials, no recompute.  Ragged last blocks,
+    split key blocks (B1 H2 T1100) and T > 1024 included.  Against the oracle, every output
+    bitwise equal over two runs, and (causal) dK / dV bitwise equal to AUTO's, whose default
+    run takes the same 64-key kernel with atomic dQ."""
+    q, k, v, do = ora.make_inputs(shape, seed=91)
+    say(f"fp32 dS path deterministic shape={shape} causal={causal}")
+    prev = ct.set_policy(ct.POLICY_DETERMINISTIC)
+    try:
+        r1 = run_gpu(q, k, v, do, causal, "f32", fastest=True)
+        r2 = run_gpu(q, k, v, do, causal, "f32", fastest=True)
+    finally:
+        ct.set_policy(prev)
+    for key in r1:
+        assert np.array_equal(r1[key], r2[key]), key
+    want = ora.attention_fwd_bwd(q, k, v, do, causal)
+    assert_close(r1, want, "f32", f"{shape} causal={causal} dS path")
+    if causal:
+        ra = run_gpu(q, k, v, do, True, "f32")
+        assert np.array_equal(ra["dk"], r1["dk"]) and np.array_equal(ra["dv"], r1["dv"])
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "full"])
+def test_f32_ds_path_auto_d128(causal):
+    """AUTO takes the fp32 dS path at d = 128 on grids of at least 1024 key blocks of 64 when
+    the workspace holds the tiles (B2 H64 T500: 8 x 128 key blocks, ragged): dQ then comes
+    without atomics, so all five outputs are bitwise reproducible; against the oracle."""
+    shape = (2, 64, 500, 128)
+    q, k, v, do = ora.make_inputs(shape, seed=92)
+    say(f"fp32 dS path auto shape={shape} causal={causal}")
+    b, h, t, d = shape
+    n = (t + 63) // 64
+    ds = b * h * (n * (n + 1) // 2 if causal else n * n) * 16384
+    assert ct._capi.bwd_workspace_bytes(torch.float32, b, h, t, d, causal, fastest=True) == \
+        (b * h * t * 4 + 255) // 256 * 256 + ds
+    r1 = run_gpu(q, k, v, do, causal, "f32", fastest=True)
+    r2 = run_gpu(q, k, v, do, causal, "f32", fastest=True)
+    for key in r1:
+        assert np.array_equal(r1[key], r2[key]), key
+    want = ora.attention_fwd_bwd(q, k, v, do, causal, chunk_heads=16)
+    assert_close(r1, want, "f32", f"{shape} causal={causal} auto dS path")
+
+
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_auto_policy_reproducibility(causal):
     """AUTO: O, LSE, dK, dV bitwise reproducible; dQ (fp32 atomics across key blocks)
