@@ -94,6 +94,8 @@ def load() -> ctypes.CDLL:
         "ctattn_linear_fwd": ([c_int] + [vp] * 4 + [i64] * 3 + [vp], c_int),
         "ctattn_linear_bwd_workspace_bytes": ([c_int] + [i64] * 3, i64),
         "ctattn_linear_bwd": ([c_int] + [vp] * 7 + [i64] * 4 + [vp], c_int),
+        "ctattn_linear_act_fwd": ([c_int, c_int] + [vp] * 5 + [i64] * 3 + [vp], c_int),
+        "ctattn_linear_act_bwd": ([c_int, c_int] + [vp] * 8 + [i64] * 4 + [vp], c_int),
         "ctattn_layernorm_fwd": ([c_int] + [vp] * 6 + [i64, i64, f64, vp], c_int),
         "ctattn_layernorm_bwd_workspace_bytes": ([c_int, i64, i64], i64),
         "ctattn_layernorm_bwd": ([c_int] + [vp] * 9 + [i64] * 3 + [vp], c_int),
@@ -426,6 +428,38 @@ def linear_bwd(x, w, dy, dw=None, db=None, want_dx=True, stream=None):
                                ws.numel(), m, n, k, _stream_handle(stream))
     _check(rc, "ctattn_linear_bwd")
     return dx
+
+
+def linear_act_fwd(x, w, b, kind: int, stream=None):
+    """(pre, y): pre = x w^T + b and y = act(pre) from one launch (ctattn_linear_act_fwd)."""
+    n, k = w.shape
+    m = _rows(x, k, "linear_act_fwd")
+    _check_dev("linear_act_fwd", x.dtype, x, w, b)
+    pre = torch.empty((*x.shape[:-1], n), dtype=x.dtype, device=x.device)
+    y = torch.empty_like(pre)
+    rc = load().ctattn_linear_act_fwd(_DTYPE_CODE[x.dtype], int(kind), _ptr(x), _ptr(w), _ptr(b), _ptr(pre), _ptr(y),
+                                      m, n, k, _stream_handle(stream))
+    _check(rc, "ctattn_linear_act_fwd")
+    return pre, y
+
+
+def linear_act_bwd(x, w, dy, pre, kind: int, dw=None, db=None, stream=None):
+    """Backward of act then linear (x = act(pre) is the linear layer's input): dw += dy^T x,
+    db += colsum(dy) in place (None to skip); returns dpre = act'(pre) * (dy w)."""
+    n, k = w.shape
+    m = _rows(x, k, "linear_act_bwd")
+    if _rows(dy, n, "linear_act_bwd") != m or pre.shape != x.shape:
+        raise ValueError("linear_act_bwd: dy / pre shapes do not match x")
+    _check_dev("linear_act_bwd", x.dtype, x, w, dy, pre, dw, db)
+    code = _DTYPE_CODE[x.dtype]
+    lib = load()
+    ws = _workspace(lib.ctattn_linear_bwd_workspace_bytes(code, m, n, k), "ctattn_linear_bwd_workspace_bytes",
+                    x.device)
+    dpre = torch.empty_like(x)
+    rc = lib.ctattn_linear_act_bwd(code, int(kind), _ptr(x), _ptr(w), _ptr(dy), _ptr(pre), _ptr(dpre), _ptr(dw),
+                                   _ptr(db), _ptr(ws), ws.numel(), m, n, k, _stream_handle(stream))
+    _check(rc, "ctattn_linear_act_bwd")
+    return dpre
 
 
 def layernorm_fwd(x, gamma, beta, eps: float = 1e-5, stream=None):

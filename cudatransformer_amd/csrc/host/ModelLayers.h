@@ -154,6 +154,40 @@ struct LinearLayer : public Layer<DType> {
         return out;
     }
 
+    // forward() followed by an activation, in one launch (ctattn_linear_act_fwd): returns the
+    // pre-activation (the activation layer's input) and the activated output.
+    std::pair<Tensor<DType>, Tensor<DType>> forwardAct(const Tensor<DType> &input, int act) {
+        const size_t rows = detail::rowsOf(input, size_t(inputDim), "LinearLayer input");
+        std::vector<size_t> shape = input.shape();
+        shape.back() = size_t(outputDim);
+        Tensor<DType> pre = Tensor<DType>::empty(shape), out = Tensor<DType>::empty(shape);
+        ctattnCheck(ctattn_linear_act_fwd(DTypeCode<DType>::value, act, input.get(), weights.get(),
+                                          useBias ? biases.get() : nullptr, pre.get(), out.get(), int64_t(rows),
+                                          outputDim, inputDim, Runtime::stream()),
+                    "ctattn_linear_act_fwd");
+        return {pre, out};
+    }
+
+    // backward() whose dInput also goes through the preceding activation (input = act(pre)):
+    // returns the gradient of pre (ctattn_linear_act_bwd).
+    Tensor<DType> backwardAct(const Tensor<DType> &input, const Tensor<DType> &gradOutput, const Tensor<DType> &pre,
+                              int act) {
+        const size_t rows = detail::rowsOf(input, size_t(inputDim), "LinearLayer input");
+        if (detail::rowsOf(gradOutput, size_t(outputDim), "LinearLayer grad_output") != rows ||
+            pre.size() != input.size())
+            throw std::invalid_argument("LinearLayer: grad_output / pre-activation shape");
+        ensureGrads();
+        Tensor<DType> preGrad = Tensor<DType>::empty(input.shape());
+        const int dt = DTypeCode<DType>::value;
+        const int64_t wsBytes = ctattn_linear_bwd_workspace_bytes(dt, int64_t(rows), outputDim, inputDim);
+        auto ws = detail::workspace(wsBytes, "ctattn_linear_bwd_workspace_bytes");
+        ctattnCheck(ctattn_linear_act_bwd(dt, act, input.get(), weights.get(), gradOutput.get(), pre.get(),
+                                          preGrad.get(), weightsGrad.get(), useBias ? biasesGrad.get() : nullptr,
+                                          ws.get(), wsBytes, int64_t(rows), outputDim, inputDim, Runtime::stream()),
+                    "ctattn_linear_act_bwd");
+        return preGrad;
+    }
+
     // Accumulates dW (and dB), returns dInput (LinearLayer.cu backward).
     Tensor<DType> backward(Tensor<DType> input, Tensor<DType> gradOutput) override {
         const size_t rows = detail::rowsOf(input, size_t(inputDim), "LinearLayer input");
@@ -356,11 +390,20 @@ struct MLPLayer : public Layer<DType> {
         for (auto &l : layers) c.push_back(l->clone());
         return std::make_shared<MLPLayer<DType>>(c);
     }
+    // A linear layer followed by an activation runs as one GEMM launch (its epilogue applies
+    // the activation); the activation's input, the pre-activation, is kept like any layer input.
     Tensor<DType> forward(Tensor<DType> input) override {
         cachedInputs.clear();
-        for (auto &l : layers) {
+        for (size_t i = 0; i < layers.size(); ++i) {
             cachedInputs.push_back(input);
-            input = l->forward(input);
+            if (auto *act = activationAfterLinear(i)) {
+                auto po = static_cast<LinearLayer<DType> *>(layers[i].get())->forwardAct(input, int(act->activationType));
+                cachedInputs.push_back(po.first);
+                input = po.second;
+                ++i;
+                continue;
+            }
+            input = layers[i]->forward(input);
         }
         return input;
     }
@@ -376,6 +419,15 @@ struct MLPLayer : public Layer<DType> {
             for (size_t i = 0; i + 1 < layers.size(); ++i) inputs.push_back(layers[i]->forward(inputs.back()));
         }
         for (size_t i = layers.size(); i-- > 0;) {
+            auto *lin = dynamic_cast<LinearLayer<DType> *>(layers[i].get());
+            auto *act = i > 0 ? dynamic_cast<ActivationLayer<DType> *>(layers[i - 1].get()) : nullptr;
+            if (lin != nullptr && act != nullptr) {
+                // The linear layer's dX and the preceding activation's backward in one launch.
+                gradOutput = lin->backwardAct(inputs[i], gradOutput, inputs[i - 1], int(act->activationType));
+                inputs[i] = inputs[i - 1] = Tensor<DType>();
+                --i;
+                continue;
+            }
             gradOutput = layers[i]->backward(inputs[i], gradOutput);
             inputs[i] = Tensor<DType>();
         }
@@ -408,6 +460,11 @@ struct MLPLayer : public Layer<DType> {
 private:
     std::vector<Tensor<DType>> cachedInputs;  // each layer's input in the last forward
     static std::string key(size_t i) { return "layer_" + std::to_string(i); }
+    // The activation layer at i + 1 when layer i is a linear layer, else null.
+    ActivationLayer<DType> *activationAfterLinear(size_t i) const {
+        if (i + 1 >= layers.size() || dynamic_cast<LinearLayer<DType> *>(layers[i].get()) == nullptr) return nullptr;
+        return dynamic_cast<ActivationLayer<DType> *>(layers[i + 1].get());
+    }
 };
 
 template <typename DType = float>

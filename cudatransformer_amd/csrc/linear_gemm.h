@@ -41,6 +41,14 @@ struct LinGemm {
     // gradient, accumulated in storage type; null for none.  Ignored for K-contiguous A.
     void *db[kLinMaxBatch];
     bool beta;
+    // An elementwise activation (act_kind: enum ctattn_activation) fused into the epilogue of
+    // a K-contiguous-A product without beta, aux[z] in out's view (0: none):
+    //   act_mode 1: out = the pre-activation p (bias included), aux[z] = act(p);
+    //   act_mode 2: out = act'(aux[z]) * product, aux[z] holding the pre-activation.
+    // Each value is rounded to storage type where the separate kernels would round it, so the
+    // results equal a product followed by the activation kernel.
+    int act_mode, act_kind;
+    void *aux[kLinMaxBatch];
 };
 
 // One row-major product: C[m][n] (+)= sum_k A(m, k) B(k, n) (+ bias[n]) with

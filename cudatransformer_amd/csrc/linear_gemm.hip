@@ -66,6 +66,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "act_math.h"
 #include "attn_common.h"
 #include "attn_mfma_common.h"
 
@@ -120,6 +121,8 @@ struct F32Fmt {
     __device__ static floatx4 load4(const char *p) { return *reinterpret_cast<const floatx4 *>(p); }
     __device__ static void store(char *p, float x) { *reinterpret_cast<float *>(p) = x; }
     __device__ static void store4(char *p, floatx4 x) { *reinterpret_cast<floatx4 *>(p) = x; }
+    // The value a store and a load back give (the storage type's rounding).
+    __device__ static float round(float x) { return x; }
     // Sum of the 16-byte MFMA operand (4 fp32 values).
     __device__ static float sum(floatx4 v) { return (v[0] + v[1]) + (v[2] + v[3]); }
 };
@@ -143,6 +146,7 @@ struct H16Fmt {
                                                           0, 0, 0);
     }
     __device__ static float load(const char *p) { return widen(*reinterpret_cast<const uint16_t *>(p)); }
+    __device__ static float round(float x) { return widen(narrow(x)); }
     __device__ static floatx4 load4(const char *p) {
         const u16x4 u = *reinterpret_cast<const u16x4 *>(p);
         return floatx4{widen(u[0]), widen(u[1]), widen(u[2]), widen(u[3])};
@@ -362,6 +366,8 @@ struct Args {
     int32_t cps;         // chunks per split
     int32_t beta;
     int32_t vec_out;  // C takes 4-column vector stores
+    int32_t act_mode, act_kind;  // fused activation (LinGemm::act_mode), aux in C's view
+    char *aux[kLinMaxBatch];
 };
 
 template <typename F, bool A_KC, bool B_KC, int TM, int TN, int NW, int S>
@@ -605,18 +611,32 @@ __global__ __launch_bounds__(NW * 64) void lin_kernel(Args p) {
             continue;
         }
         if (p.vec_out) {
-            char *dst = cz + rowoff(view_c, gm) + coloff(view_c, gn);
+            const int64_t off = rowoff(view_c, gm) + coloff(view_c, gn);
+            char *dst = cz + off;
             if (bz != nullptr) x += F::load4(bz + int64_t(gn) * F::EB);
             if (p.beta) x += F::load4(dst);
+            if (p.act_mode == 1) {
+                floatx4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = act_fwd(p.act_kind, F::round(x[e]));
+                F::store4(p.aux[z] + off, y);
+            } else if (p.act_mode == 2) {
+                const floatx4 pre = F::load4(p.aux[z] + off);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] = act_bwd_value(p.act_kind, pre[e], F::round(x[e]));
+            }
             F::store4(dst, x);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (gn + e >= p.N) break;
-                char *de = cz + rowoff(view_c, gm) + coloff(view_c, gn + e);
+                const int64_t off = rowoff(view_c, gm) + coloff(view_c, gn + e);
+                char *de = cz + off;
                 float y = x[e];
                 if (bz != nullptr) y += F::load(bz + int64_t(gn + e) * F::EB);
                 if (p.beta) y += F::load(de);
+                if (p.act_mode == 1) F::store(p.aux[z] + off, act_fwd(p.act_kind, F::round(y)));
+                else if (p.act_mode == 2) y = act_bwd_value(p.act_kind, F::load(p.aux[z] + off), F::round(y));
                 F::store(de, y);
             }
         }
@@ -721,7 +741,10 @@ inline int make_args(const LinGemm &g, const CfgInfo &c, int splits, void *ws, A
         a.c[z] = static_cast<char *>(g.c[zz]);
         a.bias[z] = static_cast<const char *>(g.bias[zz]);
         a.db[z] = g.a_kc || z >= g.nbatch ? nullptr : static_cast<char *>(g.db[z]);
+        a.aux[z] = static_cast<char *>(g.aux[zz]);
     }
+    a.act_mode = g.act_mode;
+    a.act_kind = g.act_kind;
     a.ws = static_cast<float *>(ws);
     a.av = dview(g.av, eb);
     a.bv = dview(g.bv, eb);
@@ -738,7 +761,8 @@ inline int make_args(const LinGemm &g, const CfgInfo &c, int splits, void *ws, A
     a.beta = g.beta ? 1 : 0;
     bool vec = g.N % 4 == 0;
     for (int z = 0; z < g.nbatch; ++z)
-        vec = vec && uintptr_t(g.c[z]) % (4 * eb) == 0 && (g.bias[z] == nullptr || uintptr_t(g.bias[z]) % (4 * eb) == 0);
+        vec = vec && uintptr_t(g.c[z]) % (4 * eb) == 0 && (g.bias[z] == nullptr || uintptr_t(g.bias[z]) % (4 * eb) == 0) &&
+              (g.act_mode == 0 || uintptr_t(g.aux[z]) % (4 * eb) == 0);
     if (g.cv.heads == 0) vec = vec && g.cv.ld % 4 == 0;
     a.vec_out = vec ? 1 : 0;
     return a.tiles_m * a.tiles_n * a.splits * g.nbatch;
@@ -749,6 +773,7 @@ hipError_t run(const LinGemm &g, const CfgInfo &c, int splits, void *ws, int64_t
     Args a{};
     const int nblk = make_args(g, c, splits, ws, a);
     if (a.splits > 1 && (ws == nullptr || ws_bytes < splits_bytes(g, a.splits))) return hipErrorInvalidValue;
+    if (a.splits > 1 && g.act_mode != 0) return hipErrorInvalidValue;  // the epilogue applies it
     const bool gen = g.nseg > 1 || g.av.heads != 0 || g.bv.heads != 0 || g.cv.heads != 0;
     hipError_t e = (gen ? c.launch_gen : c.launch)(a, nblk, stream);
     if (e != hipSuccess || a.splits == 1) return e;
@@ -856,6 +881,10 @@ bool view_ok(const LinView &v, bool kc, int dtype) {
 // The shape / pitch part of lin_gemm_supported (pointers are not looked at).
 bool shape_ok(const LinGemm &g) {
     if (g.dtype < 0 || g.dtype > 2 || (!g.a_kc && g.b_kc)) return false;
+    // A fused activation: forward / dX layouts (never split), output not accumulated.
+    if (g.act_mode != 0 && (g.act_mode > 2 || !g.a_kc || g.beta || g.act_kind < CTATTN_ACT_RELU ||
+                            g.act_kind > CTATTN_ACT_TANH))
+        return false;
     if (g.nbatch < 1 || g.nbatch > kLinMaxBatch || g.nseg < 1 || g.nseg > kLinMaxSeg) return false;
     const int kwe = lin::chunk_elems(g.dtype), ce = 16 / lin::elem_bytes(g.dtype);
     if (g.M < 1 || g.N < 1 || g.K < kwe || g.K % kwe != 0) return false;
@@ -899,7 +928,7 @@ LinGemm lin_plain(int dtype, bool a_kc, bool b_kc, int64_t M, int64_t N, int64_t
 bool lin_gemm_supported(const LinGemm &g) {
     if (!shape_ok(g)) return false;
     for (int z = 0; z < g.nbatch; ++z) {
-        if (g.c[z] == nullptr) return false;
+        if (g.c[z] == nullptr || (g.act_mode != 0 && g.aux[z] == nullptr)) return false;
         for (int s = 0; s < g.nseg; ++s)
             if (g.a[z][s] == nullptr || g.b[z][s] == nullptr || uintptr_t(g.a[z][s]) % 16 != 0 ||
                 uintptr_t(g.b[z][s]) % 16 != 0)

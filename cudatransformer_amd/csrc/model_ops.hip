@@ -22,6 +22,7 @@
 // Storage is fp32, bf16, fp16 or fp64.  Arithmetic is in the storage type's accumulation
 // type (the reference's ComputeType, headers.cu:47-48): fp64 for fp64 storage, fp32
 // otherwise; row statistics, losses and Adam moments are kept in that type too.
+#include "act_math.h"
 #include "attn_common.h"
 #include "capi_util.h"
 #include "ctattn.h"
@@ -164,47 +165,19 @@ __global__ __launch_bounds__(256) void layernorm_bwd_reduce_kernel(const A *__re
 // ---------------------------------------------------------------------------------------
 // Activations (relu_/gelu_/sigmoid_/tanh_kernels.cu), elementwise.
 // ---------------------------------------------------------------------------------------
-constexpr double kGeluC = 0.7978845608028654;  // sqrt(2 / pi)
-constexpr double kGeluA = 0.044715;
+// act_fwd / act_grad: act_math.h (shared with the GEMM epilogues that fuse them).
 
-template <typename A> __device__ __forceinline__ A act_fwd(int kind, A x) {
-    switch (kind) {
-        case CTATTN_ACT_RELU: return x > A(0) ? x : A(0);
-        case CTATTN_ACT_GELU: return A(0.5) * x * (A(1) + acc_tanh(A(kGeluC) * (x + A(kGeluA) * x * x * x)));
-        case CTATTN_ACT_SIGMOID: return A(1) / (A(1) + acc_exp(-x));
-        default: return acc_tanh(x);
-    }
-}
-
-template <typename A> __device__ __forceinline__ A act_grad(int kind, A x) {
-    switch (kind) {
-        case CTATTN_ACT_RELU: return x > A(0) ? A(1) : A(0);
-        case CTATTN_ACT_GELU: {
-            const A t = acc_tanh(A(kGeluC) * (x + A(kGeluA) * x * x * x));
-            return A(0.5) * (A(1) + t) + A(0.5) * x * (A(1) - t * t) * A(kGeluC) * (A(1) + A(3) * A(kGeluA) * x * x);
-        }
-        case CTATTN_ACT_SIGMOID: {
-            const A s = A(1) / (A(1) + acc_exp(-x));
-            return s * (A(1) - s);
-        }
-        default: {
-            const A t = acc_tanh(x);
-            return A(1) - t * t;
-        }
-    }
-}
-
+// Elementwise with each element read before it is written: y may alias x, dx may alias dy.
 template <typename T>
-__global__ __launch_bounds__(256) void act_fwd_kernel(int kind, const T *__restrict__ x, T *__restrict__ y, int64_t n) {
+__global__ __launch_bounds__(256) void act_fwd_kernel(int kind, const T *x, T *y, int64_t n) {
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
         st(y, i, act_fwd(kind, ld(x, i)));
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void act_bwd_kernel(int kind, const T *__restrict__ x, const T *__restrict__ dy,
-                                                     T *__restrict__ dx, int64_t n) {
+__global__ __launch_bounds__(256) void act_bwd_kernel(int kind, const T *x, const T *dy, T *dx, int64_t n) {
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
-        st(dx, i, act_grad(kind, ld(x, i)) * ld(dy, i));
+        st(dx, i, act_bwd_value(kind, ld(x, i), ld(dy, i)));
 }
 
 // ---------------------------------------------------------------------------------------

@@ -548,6 +548,50 @@ int ctattn_linear_bwd(int dtype, const void *x, const void *w, const void *dy, v
     return finish(fn, e, st);
 }
 
+int ctattn_linear_act_fwd(int dtype, int act, const void *x, const void *w, const void *b, void *pre, void *y,
+                          int64_t M, int64_t N, int64_t K, void *stream) {
+    const char *fn = "ctattn_linear_act_fwd";
+    if (int rc = validate_linear(fn, dtype, M, N, K)) return rc;
+    if (act < CTATTN_ACT_RELU || act > CTATTN_ACT_TANH) return fail(hipErrorInvalidValue, "%s: unknown activation %d", fn, act);
+    if (M == 0) return ok();
+    if (!x || !w || !pre || !y) return fail(hipErrorInvalidValue, "%s: null x/w/pre/y pointer", fn);
+    if (lin_policy(dtype)) {
+        ctattn::LinGemm g = lin_fwd(dtype, x, w, b, pre, M, N, K);
+        g.act_mode = 1;
+        g.act_kind = act;
+        g.aux[0] = y;
+        if (ctattn::lin_gemm_supported(g))
+            return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, as_stream(stream)), as_stream(stream));
+    }
+    if (int rc = ctattn_linear_fwd(dtype, x, w, b, pre, M, N, K, stream)) return rc;
+    return ctattn_activation_fwd(dtype, act, pre, y, M * N, stream);
+}
+
+int ctattn_linear_act_bwd(int dtype, int act, const void *x, const void *w, const void *dy, const void *pre,
+                          void *dpre, void *dw, void *db, void *workspace, int64_t workspace_bytes, int64_t M,
+                          int64_t N, int64_t K, void *stream) {
+    const char *fn = "ctattn_linear_act_bwd";
+    if (int rc = validate_linear(fn, dtype, M, N, K)) return rc;
+    if (act < CTATTN_ACT_RELU || act > CTATTN_ACT_TANH) return fail(hipErrorInvalidValue, "%s: unknown activation %d", fn, act);
+    if (M == 0) return ok();
+    if (!dy || !w || !pre || !dpre) return fail(hipErrorInvalidValue, "%s: null dy/w/pre/dpre pointer", fn);
+    if (dw || db) {
+        if (int rc = ctattn_linear_bwd(dtype, x, w, dy, nullptr, dw, db, workspace, workspace_bytes, M, N, K, stream))
+            return rc;
+    }
+    if (lin_policy(dtype)) {
+        ctattn::LinGemm g = lin_dx(dtype, dy, w, dpre, M, N, K);
+        g.act_mode = 2;
+        g.act_kind = act;
+        g.aux[0] = const_cast<void *>(pre);
+        if (ctattn::lin_gemm_supported(g))
+            return finish(fn, ctattn::launch_lin_gemm(g, nullptr, 0, as_stream(stream)), as_stream(stream));
+    }
+    if (int rc = ctattn_linear_bwd(dtype, x, w, dy, dpre, nullptr, nullptr, workspace, workspace_bytes, M, N, K, stream))
+        return rc;
+    return ctattn_activation_bwd(dtype, act, pre, dpre, dpre, M * K, stream);
+}
+
 int ctattn_sgd_update(int dtype, void *params, const void *grads, double lr, int64_t n, void *stream) {
     const char *fn = "ctattn_sgd_update";
     if (!known_dtype(dtype))

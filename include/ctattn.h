@@ -305,6 +305,29 @@ CTATTN_API int ctattn_linear_bwd(int dtype, const void *x, const void *w, const 
                                  int64_t M, int64_t N, int64_t K, void *stream);
 
 /*
+ * A linear layer followed by an activation, in one GEMM launch where the MFMA GEMMs take the
+ * shape (else the two steps): pre = x w^T + b as ctattn_linear_fwd, y = act(pre) as
+ * ctattn_activation_fwd; both written, results equal to those two calls.  No counterpart in
+ * the reference, which runs the two kernels (LinearLayer.cu:55 then ActivationLayer.cu:55-64);
+ * for the MLP of a transformer block, whose backward needs pre.
+ */
+CTATTN_API int ctattn_linear_act_fwd(int dtype, int act, const void *x, const void *w, const void *b,
+                                     void *pre, void *y, int64_t M, int64_t N, int64_t K, void *stream);
+
+/*
+ * Backward of an activation followed by a linear layer: with x [M][K] the linear layer's input
+ * (= act(pre)), dw += dy^T x and db += column sums of dy as ctattn_linear_bwd, and
+ * dpre[m][k] = act'(pre[m][k]) * sum_n dy[m][n] w[n][k] -- the linear layer's dX and the
+ * activation's backward in one GEMM epilogue where the MFMA GEMMs take the shape.  Results equal
+ * ctattn_linear_bwd followed by ctattn_activation_bwd; dw / db may be NULL; the workspace is
+ * only needed for dw / db (ctattn_linear_bwd_workspace_bytes).  No counterpart in the
+ * reference (LinearLayer.cu:83,95 then ActivationLayer.cu:83-92).
+ */
+CTATTN_API int ctattn_linear_act_bwd(int dtype, int act, const void *x, const void *w, const void *dy,
+                                     const void *pre, void *dpre, void *dw, void *db, void *workspace,
+                                     int64_t workspace_bytes, int64_t M, int64_t N, int64_t K, void *stream);
+
+/*
  * LayerNorm over the last dimension of x [N][D]: y = (x - mean) * rstd * gamma + beta, with
  * the row statistics written to mean / rstd (statistic type, [N]).  Replaces the
  * layerNormForwardKernel launch of LayerNormLayer::forward (LayerNorm.cu:119; kernel
@@ -331,7 +354,7 @@ CTATTN_API int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma,
 enum ctattn_activation { CTATTN_ACT_RELU = 0, CTATTN_ACT_GELU = 1, CTATTN_ACT_SIGMOID = 2, CTATTN_ACT_TANH = 3 };
 
 /*
- * y = act(x), elementwise over n values.  Replaces the four forward launches of
+ * y = act(x), elementwise over n values (y may be x).  Replaces the four forward launches of
  * ActivationLayer::forward (ActivationLayer.cu:55-64; kernels relu_kernels.cu:26,
  * gelu_kernels.cu:31, sigmoid_kernels.cu:26, tanh_kernels.cu:27).
  */
@@ -339,7 +362,7 @@ CTATTN_API int ctattn_activation_fwd(int dtype, int kind, const void *x, void *y
                                      void *stream);
 
 /*
- * dx = act'(x) * dy, elementwise (dx overwritten).  Replaces the backward launches of
+ * dx = act'(x) * dy, elementwise (dx overwritten; it may be dy).  Replaces the backward launches of
  * ActivationLayer::backward (ActivationLayer.cu:83-92; kernels relu_kernels.cu:62,
  * gelu_kernels.cu:79, sigmoid_kernels.cu:63, tanh_kernels.cu:62).
  */

@@ -246,6 +246,41 @@ def test_activation_fwd_bwd(dtype, kind):
     _close(dx, x64.grad, tol, "dx")
 
 
+FUSED_SHAPES = [(300, 1536, 384), (4096, 384, 1536), (100, 96, 256), (37, 130, 65)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3], ids=["relu", "gelu", "sigmoid", "tanh"])
+@pytest.mark.parametrize("mnk", FUSED_SHAPES)
+def test_linear_act_fused_equals_separate(dtype, kind, mnk, gemm_path):
+    """ctattn_linear_act_fwd / _bwd (the activation in the GEMM epilogue where the MFMA GEMMs
+    take the shape, else the two launches) against ctattn_linear_* followed by
+    ctattn_activation_*: pre, y, dpre, dw and db bitwise equal, for every activation, storage
+    type and GEMM path, aligned and ragged shapes (N = 130 / K = 65: the two-step fallback)."""
+    m, n, k = mnk
+    print(f"fused linear+act {dtype} kind={kind} M={m} N={n} K={k} policy={gemm_path}", flush=True)
+    x = _dev(_randn((m, k), 80 + kind), dtype)
+    w = _dev(_randn((n, k), 81, 1.0 / math.sqrt(k)), dtype)
+    b = _dev(_randn((n,), 82), dtype)
+    pre, y = _capi.linear_act_fwd(x, w, b, kind)
+    pre_ref = _capi.linear_fwd(x, w, b)
+    y_ref = _capi.activation_fwd(pre_ref, kind)
+    torch.cuda.synchronize()
+    assert torch.equal(pre, pre_ref) and torch.equal(y, y_ref)
+    # Backward of act -> linear(w2): the linear layer's input is y = act(pre), its output dim n2.
+    n2 = 2 * k + 32
+    w2 = _dev(_randn((n2, n), 83, 1.0 / math.sqrt(n)), dtype)
+    dy = _dev(_randn((m, n2), 84), dtype)
+    dw, db = torch.zeros_like(w2), torch.zeros(n2, dtype=dtype, device=DEV)
+    dw_ref, db_ref = torch.zeros_like(w2), torch.zeros(n2, dtype=dtype, device=DEV)
+    dpre = _capi.linear_act_bwd(y, w2, dy, pre, kind, dw, db)
+    dx_ref = _capi.linear_bwd(y, w2, dy, dw_ref, db_ref)
+    dpre_ref = _capi.activation_bwd(pre, dx_ref, kind)
+    torch.cuda.synchronize()
+    assert torch.equal(dpre, dpre_ref)
+    assert torch.equal(dw, dw_ref) and torch.equal(db, db_ref)
+
+
 def test_activation_rejects_unknown_kind():
     x = torch.zeros(8, device=DEV)
     with pytest.raises(RuntimeError, match="unknown activation"):
