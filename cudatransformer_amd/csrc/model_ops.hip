@@ -36,7 +36,14 @@ namespace ctattn {
 namespace {
 
 template <typename T> __device__ __forceinline__ acc_t<T> ld(const T *p, int64_t i) { return to_acc(p[i]); }
-template <typename T> __device__ __forceinline__ void st(T *p, int64_t i, acc_t<T> x) { p[i] = from_acc<T>(x); }
+// Stores round the fp32 (fp64) value to the storage type as computed: for fp16 the empty asm
+// keeps the backend from folding the last multiply or add and the conversion into one
+// mixed-precision FMA, which rounds once and would make the result depend on which kernel
+// computed it (the fused LayerNorm / activation paths must equal the separate ones).
+template <typename T> __device__ __forceinline__ void st(T *p, int64_t i, acc_t<T> x) {
+    if constexpr (std::is_same_v<T, f16_t>) asm volatile("" : "+v"(x));
+    p[i] = from_acc<T>(x);
+}
 
 // ---------------------------------------------------------------------------------------
 // LayerNorm over the last dimension (layer_norm_kernels.cu): y = (x - mean) rstd g + b.
@@ -128,6 +135,81 @@ __global__ __launch_bounds__(256) void layernorm_bwd_part_kernel(const T *__rest
     if (rl == 0 && c < D) {
         part[chunk * 2 * D + c] = ((red[0][0][cl] + red[0][1][cl]) + red[0][2][cl]) + red[0][3][cl];
         part[chunk * 2 * D + D + c] = ((red[1][0][cl] + red[1][1][cl]) + red[1][2][cl]) + red[1][3][cl];
+    }
+}
+
+// dx and the stage-1 gamma / beta partial sums of one 32-row chunk in one pass over x and dy
+// (D <= 64 CPL): wave w takes rows w, w + 4, ..., w + 28 of the chunk -- the rows lane w of the
+// stage-1 kernel sums -- computing each row's dx as layernorm_bwd_dx_kernel does and keeping
+// the partial sums of its columns c = lane + 64 j in registers in the same row order; the four
+// waves' sums are combined in LDS in the stage-1 kernel's order, so both paths give the same
+// bits.  The loads of RB rows are issued before any of them is used.
+template <typename T, int CPL, typename A = acc_t<T>>
+__global__ __launch_bounds__(256) void layernorm_bwd_fused_kernel(const T *__restrict__ x, const T *__restrict__ g,
+                                                                 const T *__restrict__ dy, const A *__restrict__ mean,
+                                                                 const A *__restrict__ rstd, T *__restrict__ dx,
+                                                                 A *__restrict__ part, int64_t N, int D) {
+    constexpr int RB = CPL <= 6 ? 8 : CPL <= 8 ? 4 : 2;  // rows loaded ahead
+    __shared__ A red[2][4][64 * CPL];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int64_t r0 = int64_t(blockIdx.x) * kLnRowsPerChunk;
+    A sg[CPL], sb[CPL], gv[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        sg[j] = sb[j] = A(0);
+        gv[j] = lane + 64 * j < D ? ld(g, lane + 64 * j) : A(0);
+    }
+#pragma unroll
+    for (int i0 = 0; i0 < kLnRowsPerChunk / 4; i0 += RB) {
+        A xv[RB][CPL], dv[RB][CPL];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int64_t r = r0 + w + 4 * (i0 + i);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                const bool in = r < N && c < D;
+                xv[i][j] = in ? ld(x, r * D + c) : A(0);
+                dv[i][j] = in ? ld(dy, r * D + c) : A(0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int64_t r = r0 + w + 4 * (i0 + i);
+            if (r >= N) break;  // wave-uniform
+            const A mu = mean[r], rs = rstd[r];
+            A s1 = 0, s2 = 0;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                if (lane + 64 * j >= D) continue;
+                sg[j] += dv[i][j] * (xv[i][j] - mu) * rs;
+                sb[j] += dv[i][j];
+                const A xh = (xv[i][j] - mu) * rs;
+                const A dxh = dv[i][j] * gv[j];
+                s1 += dxh;
+                s2 += dxh * xh;
+            }
+            const A m1 = wave_sum(s1) / A(D), m2 = wave_sum(s2) / A(D);
+            T *dxr = dx + r * D;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                if (c >= D) continue;
+                const A xh = (xv[i][j] - mu) * rs;
+                st(dxr, c, rs * (dv[i][j] * gv[j] - m1 - xh * m2));
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        red[0][w][lane + 64 * j] = sg[j];
+        red[1][w][lane + 64 * j] = sb[j];
+    }
+    __syncthreads();
+    A *pc = part + int64_t(blockIdx.x) * 2 * D;
+    for (int c = threadIdx.x; c < D; c += 256) {
+        pc[c] = ((red[0][0][c] + red[0][1][c]) + red[0][2][c]) + red[0][3][c];
+        pc[D + c] = ((red[1][0][c] + red[1][1][c]) + red[1][2][c]) + red[1][3][c];
     }
 }
 
@@ -566,13 +648,28 @@ int ctattn_layernorm_bwd(int dtype, const void *x, const void *gamma, const void
         const T *dyt = static_cast<const T *>(dy);
         const A *mu = static_cast<const A *>(mean);
         const A *rs = static_cast<const A *>(rstd);
-        if (dx)
+        A *part = static_cast<A *>(workspace);
+        // dx and the partial sums together while the columns fit a lane's registers.
+        auto fused = [&](auto cpl) {
+            constexpr int CPL = decltype(cpl)::value;
+            hipLaunchKernelGGL((ctattn::layernorm_bwd_fused_kernel<T, CPL>), dim3(unsigned(chunks)), dim3(256), 0, st,
+                               xt, static_cast<const T *>(gamma), dyt, mu, rs, static_cast<T *>(dx), part, N, int(D));
+        };
+        const bool both = dx && (dgamma || dbeta) && D <= 1024;
+        if (both) {
+            if (D <= 128) fused(std::integral_constant<int, 2>{});
+            else if (D <= 256) fused(std::integral_constant<int, 4>{});
+            else if (D <= 384) fused(std::integral_constant<int, 6>{});
+            else if (D <= 512) fused(std::integral_constant<int, 8>{});
+            else fused(std::integral_constant<int, 16>{});
+        } else if (dx) {
             hipLaunchKernelGGL(ctattn::layernorm_bwd_dx_kernel<T>, dim3(ctattn::rows_grid(N)), dim3(256), 0, st, xt,
                                static_cast<const T *>(gamma), dyt, mu, rs, static_cast<T *>(dx), N, int(D));
+        }
         if (dgamma || dbeta) {
-            A *part = static_cast<A *>(workspace);
-            hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 63) / 64), unsigned(chunks)),
-                               dim3(256), 0, st, xt, dyt, mu, rs, part, N, int(D));
+            if (!both)
+                hipLaunchKernelGGL(ctattn::layernorm_bwd_part_kernel<T>, dim3(unsigned((D + 63) / 64), unsigned(chunks)),
+                                   dim3(256), 0, st, xt, dyt, mu, rs, part, N, int(D));
             hipLaunchKernelGGL(ctattn::layernorm_bwd_reduce_kernel<T>, dim3(unsigned((D + 15) / 16)), dim3(256), 0,
                                st, static_cast<const A *>(part), static_cast<T *>(dgamma), static_cast<T *>(dbeta),
                                chunks, int(D));

@@ -219,6 +219,34 @@ def test_layernorm_bwd_is_deterministic():
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("nd", [(4096, 384), (77, 96), (300, 1000), (65, 1024), (40, 1100)])
+def test_layernorm_bwd_one_pass_equals_two(dtype, nd):
+    """dx with dgamma / dbeta in one pass (D <= 1024: one workgroup per 32-row chunk, the
+    partial sums kept per lane) against dx alone and dgamma / dbeta alone (the dx kernel and
+    the two-stage column sums): bitwise equal, ragged chunks included; D = 1100 takes the
+    separate kernels either way."""
+    n, d = nd
+    print(f"layernorm one pass {dtype} N={n} D={d}", flush=True)
+    x = _dev(_randn((n, d), 60, 2.0) + 0.5, dtype)
+    g = _dev(1.0 + 0.1 * _randn((d,), 61), dtype)
+    dy = _dev(_randn((n, d), 62), dtype)
+    _, mean, rstd = _capi.layernorm_fwd(x, g, torch.zeros_like(g))
+    dg1, db1 = torch.zeros_like(g), torch.zeros_like(g)
+    dx1 = _capi.layernorm_bwd(x, g, dy, mean, rstd, dg1, db1)
+    dx2 = _capi.layernorm_bwd(x, g, dy, mean, rstd)
+    dg2, db2 = torch.zeros_like(g), torch.zeros_like(g)
+    lib = _capi.load()
+    code = _capi._DTYPE_CODE[dtype]
+    nbytes = lib.ctattn_layernorm_bwd_workspace_bytes(code, n, d)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=DEV)
+    rc = lib.ctattn_layernorm_bwd(code, x.data_ptr(), g.data_ptr(), dy.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+                                  None, dg2.data_ptr(), db2.data_ptr(), ws.data_ptr(), nbytes, n, d, None)
+    assert rc == 0, _capi.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(dx1, dx2) and torch.equal(dg1, dg2) and torch.equal(db1, db2)
+
+
 # ---- activations ---------------------------------------------------------------------------
 
 ACTS = {
