@@ -727,12 +727,23 @@ hipError_t bwd_f32(const float *q, const float *k, const float *v, const float *
 // A key-major grid with no more workgroups than the chip holds at once (two per CU at
 // d <= 64, one at d = 128) runs as long as its longest key block -- key block 0 with every
 // query row when causal -- while most CUs idle: then each key block's rows are split between
-// two workgroups.
+// two workgroups.  For the 64-key kernel that pays only when the halved walk is long enough
+// to outweigh the dK / dV atomics the split adds: with 16 or more query blocks of 64 up to a
+// full chip, with 4 to 15 only while the grid fills at most half of it, with fewer never.
+// Same-process A/B, d = 64 (split / not, us): B16 H6 T256 56.1 / 44.7, B16 H6 T128 28.0 /
+// 21.0, B4 H12 T512 75.1 / 72.0 (grids of 0.4-0.75 of the chip, short walks: not split);
+// B8 H6 T256 29.9 / 32.3, B4 H6 T256 22.3 / 30.8, B2 H12 T512 45.4 / 54.7, B2 H16 T1024 129.7
+// / 143.8 (split); d = 128: B8 H6 T256 61.9 / 60.7, B4 H8 T512 97.2 / 107.4.
 bool bwd_f32_use_split(const AttnShape &s, bool k64, hipStream_t stream) {
     const int64_t bn = k64 ? 64 : 128;
     const int per_cu = s.d <= 64 ? 2 : 1;
     const int cus = device_cus(stream);
-    return cus > 0 && (s.T + bn - 1) / bn * s.bh() <= int64_t(per_cu) * cus;
+    if (cus <= 0) return false;
+    const int64_t blocks = (s.T + bn - 1) / bn * s.bh();
+    const int64_t slots = int64_t(per_cu) * cus;
+    if (!k64) return blocks <= slots;
+    const int64_t nqb = (s.T + 63) / 64;
+    return nqb >= 16 ? blocks <= slots : nqb >= 4 && 2 * blocks <= slots;
 }
 
 namespace {

@@ -175,15 +175,19 @@ def test_causal_work_decompositions_f32(shape, pol):
     key ranges when ceil(T / 128) * B * H <= 2 * CUs.  Backward: every key block's query rows
     are shared by two workgroups (dK / dV summed by two atomic adds each, order-independent)
     when ceil(T / bn) * B * H workgroups fit the chip at once (bn = 64 for the AUTO causal
-    d >= 64 kernel, else 128; two per CU at d <= 64).  The B1 H2 T1100 shapes take the finer
-    grids, the B4 H64 T300 ones the plain grids; both have a ragged last block.  Against the
-    oracle, and dK / dV / O / LSE bitwise equal over two runs (all of them under
-    DETERMINISTIC)."""
+    d >= 64 kernel, else 128; two per CU at d <= 64; the 64-key kernel with fewer than 16
+    query blocks of 64 only while the grid fills at most half the chip).  The B1 H2 T1100
+    shapes take the finer grids, the B4 H64 T300 ones the plain grids; both have a ragged last
+    block.  Against the oracle, and dK / dV / O / LSE bitwise equal over two runs (all of them
+    under DETERMINISTIC)."""
     b, h, t, d = shape
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     fwd_split = -(-t // 128) * b * h <= 2 * cus
     bn = 64 if (pol == ct.POLICY_AUTO and d >= 64) else 128
-    bwd_split = -(-t // bn) * b * h <= (2 if d <= 64 else 1) * cus
+    slots = (2 if d <= 64 else 1) * cus
+    blocks = -(-t // bn) * b * h
+    nqb = -(-t // 64)
+    bwd_split = blocks <= slots if (bn == 128 or nqb >= 16) else (nqb >= 4 and 2 * blocks <= slots)
     assert fwd_split == bwd_split == (h == 2), f"{shape} is expected on the other side of a rule ({cus} CUs)"
     q, k, v, do = ora.make_inputs(shape, seed=57)
     say(f"causal work decomposition shape={shape} policy={pol} split={fwd_split}")
@@ -196,6 +200,26 @@ def test_causal_work_decompositions_f32(shape, pol):
     want = ora.attention_fwd_bwd(q, k, v, do, True, chunk_heads=16)
     assert_close(r1, want, "f32", f"{shape} split={fwd_split}")
     for key in (("o", "lse", "dk", "dv") if pol == ct.POLICY_AUTO else r1):
+        assert np.array_equal(r1[key], r2[key]), key
+
+
+@pytest.mark.parametrize("shape", [(16, 6, 256, 64), (4, 6, 256, 64)], ids=lambda s: "x".join(map(str, s)))
+def test_short_sequence_backward_split_rule_f32(shape):
+    """The fp32 64-key backward at short sequences: with fewer than 16 query blocks of 64 a key
+    block is split between two workgroups only while the grid fills at most half the chip.
+    B16 H6 T256 (config 5's attention: 384 key blocks) runs them whole, B4 H6 T256 (96) split.
+    Against the oracle, dK / dV / O / LSE bitwise equal over two runs."""
+    b, h, t, d = shape
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    split = 2 * (-(-t // 64)) * b * h <= 2 * cus
+    assert split == (b == 4), f"{shape} is expected on the other side of the split rule ({cus} CUs)"
+    q, k, v, do = ora.make_inputs(shape, seed=59)
+    say(f"short sequence backward shape={shape} split={split}")
+    r1 = run_gpu(q, k, v, do, True, "f32")
+    r2 = run_gpu(q, k, v, do, True, "f32")
+    want = ora.attention_fwd_bwd(q, k, v, do, True, chunk_heads=16)
+    assert_close(r1, want, "f32", f"{shape} split={split}")
+    for key in ("o", "lse", "dk", "dv"):
         assert np.array_equal(r1[key], r2[key]), key
 
 
