@@ -224,6 +224,36 @@ struct OpKC {
     __host__ __device__ static constexpr int idx(int t, int i) { return 32 * t + i; }
 };
 
+// K-contiguous operand two 64-byte K chunks deep: R rows x 128 bytes per stage, LDS
+// [r][128 B], chunk c of row r at physical chunk c ^ swz(r): the 16 lanes of one LDS cycle of
+// a step's read (16 consecutive rows, one chunk) cover bank groups 8 (r & 1) + (c ^ swz(r)),
+// all distinct.
+template <int R>
+struct OpKC2 {
+    static constexpr int CH = 8;
+    static constexpr int BYTES = R * 128;
+    static constexpr int NL = BYTES / 1024;
+    static_assert(BYTES % 1024 == 0, "a stage is whole 1 KiB load instructions");
+    __host__ __device__ static constexpr int swz(int r) { return (r >> 1) & 7; }
+    __device__ static uint32_t voff(int i, int lane, const DView &v, int r0, int rows) {
+        const int P = 64 * i + lane;
+        const int r = P / CH;
+        const int lc = (P % CH) ^ swz(r);
+        return uint32_t(rowoff(v, r0 + min(r, rows - 1)) - rowoff(v, r0) + 16 * lc);
+    }
+    // Read of step s (0..3: 16 bytes, k-group s of lane half h) of 32-row tile tt.
+    struct Lane {
+        uint32_t offs[4];
+        __device__ void init(int lane) {
+            const int col = lane & 31, h = lane >> 5;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) offs[s] = uint32_t(col * 128 + ((((2 * s) | h) ^ swz(col)) << 4));
+        }
+        __device__ floatx4 read(uint32_t base, int tt, int s) const { return ld4(base + tt * 32 * 128 + offs[s]); }
+    };
+    __host__ __device__ static constexpr int idx(int t, int i) { return 32 * t + i; }
+};
+
 // M/N-contiguous fp32 operand: 16 k-rows x R columns per stage, LDS [k][R] (row pitch 4 R).
 template <int R>
 struct OpMN32 {
@@ -289,15 +319,16 @@ struct OpMN32P {
     __host__ __device__ static constexpr int idx(int t, int i) { return 2 * i + t; }
 };
 
-// M/N-contiguous 16-bit operand: 32 k-rows x R columns per stage, LDS [k][R] (row pitch 2 R),
-// the 64-byte segment sg of k-row kr at physical segment sg ^ gsw(kr).
-template <int R>
+// M/N-contiguous 16-bit operand: KR k-rows (32 or 64) x R columns per stage, LDS [k][R] (row
+// pitch 2 R), the 64-byte segment sg of k-row kr at physical segment sg ^ gsw(kr).
+template <int R, int KR = 32>
 struct OpMN16 {
-    static constexpr int BYTES = R * 64;
+    static constexpr int BYTES = R * 2 * KR;
     static constexpr int NL = BYTES / 1024;
     static constexpr int PITCH = 2 * R;
     static constexpr int SEGS = R / 32;
     static_assert(R == 32 || R == 64 || R == 128, "tile width 32, 64 or 128");
+    static_assert(KR == 32 || KR == 64, "one or two 32-row K chunks");
     __host__ __device__ static constexpr int gsw(int kr) {
         return SEGS == 4 ? (kr & 3) : SEGS == 2 ? ((kr >> 1) & 1) : 0;
     }
@@ -308,7 +339,7 @@ struct OpMN16 {
         const int lc = (P % (R / 8)) ^ (gsw(kr) << 2);
         return uint32_t(int64_t(kr) * krow_b(v) + coloff(v, c0 + min(8 * lc, cols - 8)) - coloff(v, c0));
     }
-    // Step s, lane (16-lane group g, sl = lane % 16): rows 16 s + 8 (g >> 1) + sl / 4 (+ 4 for
+    // Step s (< KR / 16), lane (16-lane group g, sl = lane % 16): rows 16 s + 8 (g >> 1) + sl / 4 (+ 4 for
     // the second read), columns 32 tt + 16 (g & 1) + 4 (sl % 4) .. + 3; the lane receives its
     // column's 4 + 4 values, k = 16 s + 8 h + 0..7 in order.  gsw of those rows is the same
     // for every s and both reads.
@@ -680,6 +711,238 @@ __global__ __launch_bounds__(256) void lin_splitk_reduce_kernel(Args p, int64_t 
     }
 }
 
+// ---- shared-tile products (16-bit storage) ----
+//
+// The kernels above give every wave its own tile, so each wave streams its own A and B rows
+// from L2: a one-wave 128 x 64 tile stages 12 KB per 32-deep K chunk for 0.5 MFLOP, which at
+// the 16-bit MFMA rate needs several times the L2 bandwidth a CU gets.  Here WM x WN waves
+// share one (32 TM WM) x (32 TN WN) tile: each K stage (KS 64-byte chunks of every
+// K-contiguous row, or KS 32-row chunks of an M/N-contiguous operand) goes global -> LDS once
+// per workgroup, the direct loads split across the waves, through an S-slot ring with one
+// barrier per stage, and wave (wm, wn) multiplies A rows wm by B columns wn.  Operands in any
+// layout and view (a K-contiguous head-split stage inside one head, an M/N-contiguous one
+// inside one batch), K segments and K splits across workgroups as lin_kernel, the bias
+// gradient of an M-contiguous A summed by the first tile column.  GEN: some view is
+// head-split or K has several segments.
+template <typename F, bool A_KC, bool B_KC, int WM, int WN, int TM, int TN, int S, int KS>
+struct ShCfg {
+    static constexpr int NW = WM * WN;
+    static constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
+    template <bool KC, int R>
+    using Op = std::conditional_t<KC, std::conditional_t<KS == 1, OpKC<R>, OpKC2<R>>, OpMN16<R, 32 * KS>>;
+    using OA = Op<A_KC, BM>;
+    using OB = Op<B_KC, BN>;
+    static constexpr int STAGE = OA::BYTES + OB::BYTES;
+    static constexpr int LA = OA::NL / NW, LB = OB::NL / NW;  // load instructions per wave per stage
+    static constexpr int L = LA + LB;
+    static_assert(OA::NL % NW == 0 && OB::NL % NW == 0, "a stage's loads split evenly over the waves");
+    static constexpr int PIPE = S * STAGE;
+    static constexpr int EPI = 32 * TM * BN * 4;     // one wave row of the tile, fp32, for the stores
+    static constexpr int DBB = A_KC ? 0 : 2 * BM * 4;  // bias-gradient sums per lane half
+    static constexpr int LDS = PIPE > EPI + DBB ? PIPE : EPI + DBB;
+    static_assert(LDS <= 160 * 1024, "LDS of one workgroup");
+    static_assert(S >= 2 && (S - 1) * L < 64, "outstanding loads must fit vmcnt");
+};
+
+template <typename F, bool A_KC, bool B_KC, int WM, int WN, int TM, int TN, int S, int KS, bool GEN>
+__global__ __launch_bounds__(WM * WN * 64) void lin_shared_kernel(Args p) {
+    using C = ShCfg<F, A_KC, B_KC, WM, WN, TM, TN, S, KS>;
+    using OA = typename C::OA;
+    using OB = typename C::OB;
+    constexpr int BM = C::BM, BN = C::BN, NW = C::NW;
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+    DView view_a = p.av, view_b = p.bv, view_c = p.cv;
+    if constexpr (!GEN) view_a.heads = view_b.heads = view_c.heads = 0;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const int wm = wave / WN, wn = wave - (wave / WN) * WN;
+    const int h = lane >> 5, col = lane & 31;
+
+    // XCD-aware order, as lin_kernel: XCD x runs the contiguous work items [x q, x q + q).
+    const int nblk = int(gridDim.x), blk = int(blockIdx.x);
+    const int q = nblk >> 3;
+    const int work = blk < 8 * q ? (blk & 7) * q + (blk >> 3) : blk;
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int per_batch = ntiles * p.splits;
+    const int z = work / per_batch;
+    const int rem = work - z * per_batch;
+    const int split = rem / ntiles;
+    const int tile = rem - split * ntiles;
+    const int ti = tile / p.tiles_n;
+    const int m0 = ti * BM, n0 = (tile - ti * p.tiles_n) * BN;
+    // This workgroup's stages (KS K chunks each; cps is a multiple of KS).
+    const int st0 = split * (p.cps / KS);
+    const int nst = min(p.chunks / KS - st0, p.cps / KS);
+    const int sst = p.seg_chunks / KS;  // stages per segment
+
+    const int64_t a_t = A_KC ? rowoff(view_a, m0) : coloff(view_a, m0);
+    const int64_t b_t = B_KC ? rowoff(view_b, n0) : coloff(view_b, n0);
+    uint32_t va[C::LA], vb[C::LB];
+#pragma unroll
+    for (int u = 0; u < C::LA; ++u) va[u] = OA::voff(wave + NW * u, lane, view_a, m0, p.M - m0);
+#pragma unroll
+    for (int u = 0; u < C::LB; ++u) vb[u] = OB::voff(wave + NW * u, lane, view_b, n0, p.N - n0);
+    typename OA::Lane ra;
+    typename OB::Lane rb;
+    ra.init(lane);
+    rb.init(lane);
+    const uint32_t base = lds_addr(smem);
+
+    auto issue = [&](int slot, int c) {
+        const uint32_t sa = base + uint32_t(slot * C::STAGE);
+        int seg = 0, cs = c;
+        if constexpr (GEN) {
+            seg = c / sst;
+            cs = c - seg * sst;
+        }
+        // Stage cs of segment seg: K [kk, kk + KS KWE), inside one head / one batch.
+        const int kk = cs * KS * F::KWE;
+        const char *gac = pick(p.a[z], seg) + a_t + (A_KC ? coloff(view_a, kk) : rowoff(view_a, kk));
+        const char *gbc = pick(p.b[z], seg) + b_t + (B_KC ? coloff(view_b, kk) : rowoff(view_b, kk));
+#pragma unroll
+        for (int u = 0; u < C::LA; ++u) dma16(gac, va[u], sa + uint32_t(1024 * (wave + NW * u)));
+#pragma unroll
+        for (int u = 0; u < C::LB; ++u) dma16(gbc, vb[u], sa + uint32_t(OA::BYTES + 1024 * (wave + NW * u)));
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
+    // Bias gradient of an M-contiguous A: the first tile column's waves of column 0 sum A.
+    const bool want_db = !A_KC && p.db[z] != nullptr && n0 == 0;
+    const bool sum_a = want_db && wn == 0;
+    float dsum[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) dsum[i] = 0.f;
+
+    const int pro = min(S - 1, nst);
+    for (int j = 0; j < pro; ++j) issue(j, st0 + j);
+    int slot = 0, islot = S - 1;
+    for (int j = 0; j < nst; ++j) {
+        // This wave's loads of stage j have landed once at most the later stages' are in
+        // flight; after the barrier every wave's have, and every wave is done with the slot
+        // the next issue refills (read in the previous iteration).
+        wait_tail<C::L, S>(min(S - 2, nst - 1 - j));
+        __syncthreads();
+        if (j + S - 1 < nst) issue(islot, st0 + j + S - 1);
+        const uint32_t sa = base + uint32_t(slot * C::STAGE);
+        const uint32_t sb = sa + uint32_t(OA::BYTES);
+#pragma unroll
+        for (int s = 0; s < 2 * KS; ++s) {
+            floatx4 av[TM], bv[TN];
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) av[tm] = ra.read(sa, TM * wm + tm, s);
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) bv[tn] = rb.read(sb, TN * wn + tn, s);
+            if (!A_KC && sum_a) {
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) dsum[tm] += F::sum(av[tm]);
+            }
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = F::mfma(av[tm], bv[tn], acc[tm][tn]);
+        }
+        slot = slot + 1 == S ? 0 : slot + 1;
+        islot = islot + 1 == S ? 0 : islot + 1;
+    }
+
+    const uint32_t ebuf = base;
+    if (!A_KC && want_db) {
+        // Lane (col, h) holds the sum over its k of A row 32 (TM wm + tm) + col: LDS [h][BM]
+        // past the store buffer; one thread per row adds the halves in order.
+        const uint32_t dbuf = base + uint32_t(C::EPI);
+        __syncthreads();  // the ring is no longer read
+        if (sum_a) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) st1(dbuf + uint32_t((h * BM + 32 * (TM * wm + tm) + col) * 4), dsum[tm]);
+        }
+        __syncthreads();
+        const int m = int(threadIdx.x);
+        if (m < BM && m0 + m < p.M) {
+            const float x = ld1(dbuf + uint32_t(m * 4)) + ld1(dbuf + uint32_t((BM + m) * 4));
+            if (p.splits > 1) {
+                p.ws[int64_t(p.nbatch) * p.splits * p.M * p.N + (int64_t(z) * p.splits + split) * p.M + m0 + m] = x;
+            } else {
+                char *dst = p.db[z] + int64_t(m0 + m) * F::EB;
+                F::store(dst, F::load(dst) + x);
+            }
+        }
+    }
+
+    // Stores, one wave row of the tile (32 TM rows x BN columns) at a time through LDS:
+    // register r of lane (col, h) holds row acc_row(r, h) of column col of each 32 x 32 tile.
+    char *const cz = p.c[z];
+    const char *const bz = p.bias[z];
+    constexpr int Q = 32 * TM * BN / 4;
+#pragma unroll 1
+    for (int pm = 0; pm < WM; ++pm) {
+        __syncthreads();  // the ring (or the previous pass) is no longer read
+        if (wm == pm) {
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        st1(ebuf + uint32_t(((32 * tm + acc_row(r, h)) * BN + 32 * (TN * wn + tn) + col) * 4),
+                            acc[tm][tn][r]);
+        }
+        __syncthreads();
+        for (int qi = int(threadIdx.x); qi < Q; qi += NW * 64) {
+            const int m = qi / (BN / 4);
+            const int n = (qi - m * (BN / 4)) * 4;
+            const int gm = m0 + pm * 32 * TM + m, gn = n0 + n;
+            if (gm >= p.M || gn >= p.N) continue;
+            floatx4 x = ld4(ebuf + uint32_t((m * BN + n) * 4));
+            if (p.splits > 1) {
+                float *dst = p.ws + ((int64_t(z) * p.splits + split) * p.M + gm) * p.N + gn;
+                if (p.N % 4 == 0) {
+                    *reinterpret_cast<floatx4 *>(dst) = x;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (gn + e < p.N) dst[e] = x[e];
+                }
+                continue;
+            }
+            if (p.vec_out) {
+                const int64_t off = rowoff(view_c, gm) + coloff(view_c, gn);
+                char *dst = cz + off;
+                if (bz != nullptr) x += F::load4(bz + int64_t(gn) * F::EB);
+                if (p.beta) x += F::load4(dst);
+                if (p.act_mode == 1) {
+                    floatx4 y;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) y[e] = act_fwd(p.act_kind, F::round(x[e]));
+                    F::store4(p.aux[z] + off, y);
+                } else if (p.act_mode == 2) {
+                    const floatx4 pre = F::load4(p.aux[z] + off);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = act_bwd_value(p.act_kind, pre[e], F::round(x[e]));
+                }
+                F::store4(dst, x);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (gn + e >= p.N) break;
+                    const int64_t off = rowoff(view_c, gm) + coloff(view_c, gn + e);
+                    char *de = cz + off;
+                    float y = x[e];
+                    if (bz != nullptr) y += F::load(bz + int64_t(gn + e) * F::EB);
+                    if (p.beta) y += F::load(de);
+                    if (p.act_mode == 1) F::store(p.aux[z] + off, act_fwd(p.act_kind, F::round(y)));
+                    else if (p.act_mode == 2) y = act_bwd_value(p.act_kind, F::load(p.aux[z] + off), F::round(y));
+                    F::store(de, y);
+                }
+            }
+        }
+    }
+}
+
 // ---- host side ----
 
 struct Plan {
@@ -768,20 +1031,104 @@ inline int make_args(const LinGemm &g, const CfgInfo &c, int splits, void *ws, A
     return a.tiles_m * a.tiles_n * a.splits * g.nbatch;
 }
 
+// Some view is head-split or K has several segments (the kernels' GEN variant).
+inline bool lin_gen(const LinGemm &g) {
+    return g.nseg > 1 || g.av.heads != 0 || g.bv.heads != 0 || g.cv.heads != 0;
+}
+
+// The split-K reduction: C (and the bias gradients) from the partials of a.splits splits.
+template <typename F>
+hipError_t launch_reduce(const LinGemm &g, const Args &a, hipStream_t stream) {
+    const int64_t items = a.vec_out ? g.M * g.N / 4 : g.M * g.N;
+    const int64_t threads = std::max<int64_t>(items, g.M);  // bias gradients: one thread per row
+    hipLaunchKernelGGL(lin_splitk_reduce_kernel<F>, dim3(unsigned((threads + 255) / 256), unsigned(g.nbatch)),
+                       dim3(256), 0, stream, a, items, a.vec_out);
+    return hipGetLastError();
+}
+
 template <typename F>
 hipError_t run(const LinGemm &g, const CfgInfo &c, int splits, void *ws, int64_t ws_bytes, hipStream_t stream) {
     Args a{};
     const int nblk = make_args(g, c, splits, ws, a);
     if (a.splits > 1 && (ws == nullptr || ws_bytes < splits_bytes(g, a.splits))) return hipErrorInvalidValue;
     if (a.splits > 1 && g.act_mode != 0) return hipErrorInvalidValue;  // the epilogue applies it
-    const bool gen = g.nseg > 1 || g.av.heads != 0 || g.bv.heads != 0 || g.cv.heads != 0;
-    hipError_t e = (gen ? c.launch_gen : c.launch)(a, nblk, stream);
+    hipError_t e = (lin_gen(g) ? c.launch_gen : c.launch)(a, nblk, stream);
     if (e != hipSuccess || a.splits == 1) return e;
-    const int64_t items = a.vec_out ? g.M * g.N / 4 : g.M * g.N;
-    const int64_t threads = std::max<int64_t>(items, g.M);  // bias gradients: one thread per row
-    hipLaunchKernelGGL(lin_splitk_reduce_kernel<F>, dim3(unsigned((threads + 255) / 256), unsigned(g.nbatch)),
-                       dim3(256), 0, stream, a, items, a.vec_out);
-    return hipGetLastError();
+    return launch_reduce<F>(g, a, stream);
+}
+
+// Launch of the shared-tile kernel: WM x WN waves on a (32 TM WM) x (32 TN WN) tile, an S-slot
+// ring of KS-chunk stages, K split across up to `splits` workgroups (ws: the partials).  The
+// product must be one shared_plan (below) takes with KS.
+template <typename F, bool A_KC, bool B_KC, int WM, int WN, int TM, int TN, int S, int KS>
+hipError_t run_shared(const LinGemm &g, int splits, void *ws, int64_t ws_bytes, hipStream_t stream) {
+    Args a{};
+    const CfgInfo c{TM * WM, TN * WN, WM * WN, S, nullptr, nullptr};
+    make_args(g, c, splits, ws, a);
+    if (a.seg_chunks % KS != 0) return hipErrorInvalidValue;
+    a.cps = (a.cps + KS - 1) / KS * KS;  // whole stages per split
+    a.splits = (a.chunks + a.cps - 1) / a.cps;
+    if (a.splits > 1 && (ws == nullptr || ws_bytes < splits_bytes(g, a.splits) || g.act_mode != 0))
+        return hipErrorInvalidValue;
+    const int nblk = a.tiles_m * a.tiles_n * a.splits * g.nbatch;
+    if (lin_gen(g))
+        hipLaunchKernelGGL((lin_shared_kernel<F, A_KC, B_KC, WM, WN, TM, TN, S, KS, true>), dim3(unsigned(nblk)),
+                           dim3(WM * WN * 64), 0, stream, a);
+    else
+        hipLaunchKernelGGL((lin_shared_kernel<F, A_KC, B_KC, WM, WN, TM, TN, S, KS, false>), dim3(unsigned(nblk)),
+                           dim3(WM * WN * 64), 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.splits == 1) return e;
+    return launch_reduce<F>(g, a, stream);
+}
+
+// The shared-tile plan of a supported product: ks 0 (not taken), or the stage depth in K
+// chunks (1 or 2) and the K split count.
+struct SharedPlan {
+    int ks, splits;
+};
+
+// Whether a view holds whole stages of `rows` K elements: a K-contiguous head-split stage
+// inside one head, an M/N-contiguous one inside one batch.
+inline bool stage_in_view(const LinView &v, bool kc, int rows) {
+    return v.heads == 0 || (kc ? v.d % rows == 0 : v.T % rows == 0);
+}
+
+// 16-bit products take the shared-tile kernel, with two-chunk stages where every segment is an
+// even number of chunks and the views hold whole stages:
+//   * K-contiguous A (forward, dX): with at least 256 128 x 128 tiles, K never split (smaller
+//     grids keep lin_kernel's smaller tiles and more workgroups);
+//   * weight gradients (M/N-contiguous A): with at least 64 tiles, K split across
+//     floor(512 / tiles) workgroups (two workgroups per CU fill the chip once; a split keeps
+//     >= 8 stages, at most 16 splits) when the caller has workspace, else unsplit from 256
+//     tiles.  Fitted to sweeps of 1024..4096-wide products: e.g. 3 x 1024 x 1024 x 8192
+//     (192 tiles, 2 splits) 81 us against lin_kernel's 88, 4096^3 164 against 312.
+inline SharedPlan shared_plan(const LinGemm &g, bool allow_split) {
+    if (g.dtype == 0) return SharedPlan{0, 1};
+    const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128) * g.nbatch;
+    if (tiles >= (int64_t(1) << 24)) return SharedPlan{0, 1};
+    const int64_t seg_chunks = g.K / 32;
+    const bool two = seg_chunks % 2 == 0 && stage_in_view(g.av, g.a_kc, 64) && stage_in_view(g.bv, g.b_kc, 64);
+    const int ks = two ? 2 : 1;
+    if (g.a_kc) return tiles >= 256 ? SharedPlan{ks, 1} : SharedPlan{0, 1};
+    if (tiles < 64) return SharedPlan{0, 1};
+    const int64_t stages = seg_chunks * g.nseg / ks;
+    const int64_t sp = allow_split ? std::min<int64_t>(std::min<int64_t>(512 / tiles, stages / 8), 16) : 1;
+    if (sp >= 2) return SharedPlan{ks, int(sp)};
+    return tiles >= 256 ? SharedPlan{ks, 1} : SharedPlan{0, 1};
+}
+
+// The shared-tile launch of a plan: 128 x 128 tiles of 4 waves, 2 stages.
+template <typename F, bool A_KC, bool B_KC>
+hipError_t run_shared_ks(const LinGemm &g, const SharedPlan &sp, void *ws, int64_t ws_bytes, hipStream_t stream) {
+    return sp.ks == 2 ? run_shared<F, A_KC, B_KC, 2, 2, 2, 2, 2, 2>(g, sp.splits, ws, ws_bytes, stream)
+                      : run_shared<F, A_KC, B_KC, 2, 2, 2, 2, 2, 1>(g, sp.splits, ws, ws_bytes, stream);
+}
+template <typename F>
+hipError_t run_shared_plan(const LinGemm &g, const SharedPlan &sp, void *ws, int64_t ws_bytes, hipStream_t stream) {
+    if (!g.a_kc) return run_shared_ks<F, false, false>(g, sp, ws, ws_bytes, stream);
+    return g.b_kc ? run_shared_ks<F, true, true>(g, sp, ws, ws_bytes, stream)
+                  : run_shared_ks<F, true, false>(g, sp, ws, ws_bytes, stream);
 }
 
 }  // namespace lin
@@ -832,6 +1179,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // bf16 / fp16:
 //   * weight gradients: 64 x 64 tiles of 2 waves, K split across workgroups below 512 tiles
 //     (up to 1024 workgroups, each wave keeping >= 12 K chunks);
+//   * the shared-tile kernel where shared_plan takes the product (chosen before this plan);
 //   * otherwise, with at least 1024 64 x 64 tiles and 24 K chunks: one wave per 128 x 64
 //     (forward) or 64 x 128 (dX) tile; else 64 x 64 tiles of 4 waves.
 lin::Plan plan(const LinGemm &g, bool allow_split) {
@@ -940,11 +1288,17 @@ bool lin_gemm_supported(const LinGemm &g) {
 int64_t lin_gemm_workspace_bytes(const LinGemm &g) {
     if (!shape_ok(g)) return 0;
     // The launch trims empty splits, never adds any: this is an upper bound.
-    return lin::splits_bytes(g, plan(g, true).splits);
+    const lin::SharedPlan sp = lin::shared_plan(g, true);
+    return lin::splits_bytes(g, sp.ks != 0 ? sp.splits : plan(g, true).splits);
 }
 
 hipError_t launch_lin_gemm(const LinGemm &g, void *ws, int64_t ws_bytes, hipStream_t stream) {
     if (!lin_gemm_supported(g)) return hipErrorInvalidValue;
+    lin::SharedPlan sp = lin::shared_plan(g, true);
+    if (sp.splits > 1 && (ws == nullptr || ws_bytes < lin::splits_bytes(g, sp.splits))) sp = lin::shared_plan(g, false);
+    if (sp.ks != 0)
+        return g.dtype == 1 ? lin::run_shared_plan<BF16Fmt>(g, sp, ws, ws_bytes, stream)
+                            : lin::run_shared_plan<F16Fmt>(g, sp, ws, ws_bytes, stream);
     lin::Plan pl = plan(g, true);
     if (pl.splits > 1 && (ws == nullptr || ws_bytes < lin::splits_bytes(g, pl.splits))) pl = plan(g, false);
     const CfgInfo &c = cfg_for(g, pl);

@@ -115,7 +115,7 @@ def test_linear_fwd_bwd(dtype, mnk, bias, gemm_path):
 #   (8100, 1024, 992)  16-bit: the one-wave 128 x 64 forward and 64 x 128 dX tiles with ragged
 #                      M (forward) and N (dX) edges
 LIN_SHAPES = [(4096, 1536, 384), (4096, 384, 1536), (8192, 1024, 1024), (1008, 208, 1008), (64, 16, 4096),
-              (8192, 64, 64), (4096, 1152, 384), (8100, 1024, 992)]
+              (8192, 64, 64), (4096, 1152, 384), (8100, 1024, 992), (2000, 1984, 2016), (2048, 2048, 2048)]
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
@@ -140,6 +140,57 @@ def test_linear_plans(mnk, dt):
     _close(dx, dy64 @ w64, TOL[dt], "dx")
     _close(dw, _as64(dw0, dt) + dy64.T @ x64, TOL[dt], "dw")
     _close(db, _as64(db0, dt) + dy64.sum(0), TOL[dt], "db")
+
+
+# (B, T, E, H, d): products of at least 256 128 x 128 tiles take the 16-bit shared-tile GEMM;
+# d = 64 stages two K chunks per head, d = 32 one; T = 700 puts batch boundaries inside tiles.
+PROJ_SHAPES = [(4, 1024, 1024, 16, 64), (2, 2048, 1024, 32, 32), (3, 700, 768, 12, 64)]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("dims", PROJ_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_projection_products_16bit_large(dims, dt):
+    """The attention layer's projections at sizes of the shared-tile GEMM (head-split Q / K / V /
+    C operands and outputs, dX summing three K segments) against float64 products of the same
+    rounded inputs."""
+    b, t, e, h, d = dims
+    hd = h * d
+    print(f"projection products {dims} {dt}", flush=True)
+    x = _dev(_randn((b, t, e), 30), dt)
+    ws = [_dev(_randn((hd, e), 31 + i, 1 / math.sqrt(e)), dt) for i in range(3)]
+    bs = [_dev(_randn((hd,), 34 + i), dt) for i in range(3)]
+    qkv = _capi.qkv_proj_fwd(x, *ws, *bs, h, d)
+    x64 = _as64(x, dt).reshape(b * t, e)
+
+    def heads(r):  # [B*T, H*d] rows -> [B, H, T, d]
+        return r.reshape(b, t, h, d).permute(0, 2, 1, 3)
+
+    def rows(g):  # [B, H, T, d] -> [B*T, H*d] rows, float64
+        return _as64(g, dt).permute(0, 2, 1, 3).reshape(b * t, hd)
+
+    for o, w, bb, n in zip(qkv, ws, bs, "qkv"):
+        _close(o, heads(x64 @ _as64(w, dt).T + _as64(bb, dt)), TOL[dt], n)
+    c = _dev(_randn((b, h, t, d), 40), dt)
+    wo = _dev(_randn((e, hd), 41, 1 / math.sqrt(hd)), dt)
+    bo = _dev(_randn((e,), 42), dt)
+    y = _capi.out_proj_fwd(c, wo, bo)
+    _close(y, (rows(c) @ _as64(wo, dt).T + _as64(bo, dt)).reshape(b, t, e), TOL[dt], "y")
+    dy = _dev(_randn((b, t, e), 43), dt)
+    dwo, dbo = torch.zeros_like(wo), torch.zeros_like(bo)
+    dc = _capi.out_proj_bwd(c, dy, wo, dwo, dbo)
+    dy64 = _as64(dy, dt).reshape(b * t, e)
+    _close(dc, heads(dy64 @ _as64(wo, dt)), TOL[dt], "dc")
+    _close(dwo, dy64.T @ rows(c), TOL[dt], "dwo")
+    _close(dbo, dy64.sum(0), TOL[dt], "dbo")
+    grads = [_dev(_randn((b, h, t, d), 50 + i), dt) for i in range(3)]
+    dw = tuple(torch.zeros_like(w) for w in ws)
+    db = tuple(torch.zeros_like(bb) for bb in bs)
+    dx = _capi.qkv_proj_bwd(x, *grads, *ws, dw=dw, db=db)
+    torch.cuda.synchronize()
+    _close(dx, sum(rows(g) @ _as64(w, dt) for g, w in zip(grads, ws)).reshape(b, t, e), TOL[dt], "dx")
+    for g, dwi, dbi, n in zip(grads, dw, db, "qkv"):
+        _close(dwi, rows(g).T @ x64, TOL[dt], "dw" + n)
+        _close(dbi, rows(g).sum(0), TOL[dt], "db" + n)
 
 
 def test_linear_fp32_bitwise_repeatable():
@@ -274,7 +325,7 @@ def test_activation_fwd_bwd(dtype, kind):
     _close(dx, x64.grad, tol, "dx")
 
 
-FUSED_SHAPES = [(300, 1536, 384), (4096, 384, 1536), (100, 96, 256), (37, 130, 65)]
+FUSED_SHAPES = [(300, 1536, 384), (4096, 384, 1536), (4096, 1024, 512), (100, 96, 256), (37, 130, 65)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
@@ -284,7 +335,8 @@ def test_linear_act_fused_equals_separate(dtype, kind, mnk, gemm_path):
     """ctattn_linear_act_fwd / _bwd (the activation in the GEMM epilogue where the MFMA GEMMs
     take the shape, else the two launches) against ctattn_linear_* followed by
     ctattn_activation_*: pre, y, dpre, dw and db bitwise equal, for every activation, storage
-    type and GEMM path, aligned and ragged shapes (N = 130 / K = 65: the two-step fallback)."""
+    type and GEMM path, aligned and ragged shapes (N = 130 / K = 65: the two-step fallback;
+    4096 x 1024 x 512: the shared-tile GEMM, one- and two-chunk stages)."""
     m, n, k = mnk
     print(f"fused linear+act {dtype} kind={kind} M={m} N={n} K={k} policy={gemm_path}", flush=True)
     x = _dev(_randn((m, k), 80 + kind), dtype)
