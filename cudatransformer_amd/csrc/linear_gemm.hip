@@ -1101,8 +1101,8 @@ inline bool stage_in_view(const LinView &v, bool kc, int rows) {
 //   * weight gradients (M/N-contiguous A): with at least 64 tiles, K split across
 //     floor(512 / tiles) workgroups (two workgroups per CU fill the chip once; a split keeps
 //     >= 8 stages, at most 16 splits) when the caller has workspace, else unsplit from 256
-//     tiles.  Fitted to sweeps of 1024..4096-wide products: e.g. 3 x 1024 x 1024 x 8192
-//     (192 tiles, 2 splits) 81 us against lin_kernel's 88, 4096^3 164 against 312.
+//     tiles.  Fitted to sweeps of 384..4096-wide products: e.g. dW of 3072 x 1024 over 8192
+//     rows (192 tiles, 2 splits) 81 us against lin_kernel's 88, 4096^3 164 against 312.
 inline SharedPlan shared_plan(const LinGemm &g, bool allow_split) {
     if (g.dtype == 0) return SharedPlan{0, 1};
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128) * g.nbatch;
