@@ -513,12 +513,16 @@ struct DqDsCfg {
     static constexpr int LDS_BYTES = STAGES * BUF;
 };
 
-// 2 KiB global -> LDS (one wave): lane l moves bytes 16 l and 1024 + 16 l.
+// 2 KiB global -> LDS (one wave): lane l moves bytes 16 l and 1024 + 16 l.  Non-temporal
+// (`nt`): each dS tile is read once, and streaming it through L2 as evict-first keeps the K
+// blocks, which every query block re-reads, resident there.  Same-process A/B of the dQ pass
+// (outputs bitwise equal): B1 H32 T8192 causal 459 -> 426 us, B1 H64 T4096 251 -> 219, B1 H64
+// T2048 67.0 -> 60.3.
 __device__ __forceinline__ void dma_2k(const uint16_t *src, uint32_t dst, int lane) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const char *g = reinterpret_cast<const char *>(src) + h * 1024 + 16 * lane;
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g),
                      "s"(__builtin_amdgcn_readfirstlane(dst + uint32_t(h * 1024)))
                      : "memory", "m0");
     }
