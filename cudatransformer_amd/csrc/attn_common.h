@@ -62,8 +62,6 @@ __device__ __forceinline__ float acc_log(float x) { return logf(x); }
 __device__ __forceinline__ double acc_log(double x) { return log(x); }
 __device__ __forceinline__ float acc_sqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double acc_sqrt(double x) { return sqrt(x); }
-__device__ __forceinline__ float acc_tanh(float x) { return tanhf(x); }
-__device__ __forceinline__ double acc_tanh(double x) { return tanh(x); }
 
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
