@@ -144,12 +144,14 @@ def test_linear_plans(mnk, dt):
     _close(db, _as64(db0, dt) + dy64.sum(0), TOL[dt], "db")
 
 
-# (B, T, E, H, d): products of at least 256 128 x 128 tiles take the 16-bit shared-tile GEMM;
-# d = 64 stages two K chunks per head, d = 32 one; T = 700 puts batch boundaries inside tiles.
-PROJ_SHAPES = [(4, 1024, 1024, 16, 64), (2, 2048, 1024, 32, 32), (3, 700, 768, 12, 64)]
+# (B, T, E, H, d): products of at least 256 128 x 128 tiles take the 16-bit shared-tile GEMM
+# (fp32: forward products of at least 768 128 x 64 tiles, the B8 shape's head-split output
+# projection among them); d = 64 stages two K chunks per head, d = 32 one; T = 700 puts batch
+# boundaries inside tiles.
+PROJ_SHAPES = [(4, 1024, 1024, 16, 64), (2, 2048, 1024, 32, 32), (3, 700, 768, 12, 64), (8, 1024, 1024, 16, 64)]
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("dims", PROJ_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_projection_products_16bit_large(dims, dt):
     """The attention layer's projections at sizes of the shared-tile GEMM (head-split Q / K / V /
@@ -343,7 +345,8 @@ def test_tanh_fp32_within_4_ulp():
     assert torch.equal(y[:1_000_000], -y[1_000_001:2_000_001].flip(0)), "tanh(-x) = -tanh(x)"
 
 
-FUSED_SHAPES = [(300, 1536, 384), (4096, 384, 1536), (4096, 1024, 512), (100, 96, 256), (37, 130, 65)]
+FUSED_SHAPES = [(300, 1536, 384), (4096, 384, 1536), (4096, 1024, 512), (4096, 1536, 384), (100, 96, 256),
+                (37, 130, 65)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
@@ -354,7 +357,8 @@ def test_linear_act_fused_equals_separate(dtype, kind, mnk, gemm_path):
     take the shape, else the two launches) against ctattn_linear_* followed by
     ctattn_activation_*: pre, y, dpre, dw and db bitwise equal, for every activation, storage
     type and GEMM path, aligned and ragged shapes (N = 130 / K = 65: the two-step fallback;
-    4096 x 1024 x 512: the shared-tile GEMM, one- and two-chunk stages)."""
+    4096 x 1024 x 512: the 16-bit shared-tile GEMM, one- and two-chunk stages; 4096 x 1536 x 384:
+    the fp32 one)."""
     m, n, k = mnk
     print(f"fused linear+act {dtype} kind={kind} M={m} N={n} K={k} policy={gemm_path}", flush=True)
     x = _dev(_randn((m, k), 80 + kind), dtype)
