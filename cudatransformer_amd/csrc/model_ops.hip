@@ -449,16 +449,26 @@ template <typename A> struct AdamHyper {
     int decoupled;
 };
 
+typedef float adam_f4 __attribute__((ext_vector_type(4)));
+
+// One element's update from its loaded values: p (parameter), gr (gradient), mo / vo (moments);
+// returns the new parameter and writes the new moments.
+template <typename A>
+__device__ __forceinline__ A adam_math(A p, A gr, A mo, A vo, A &mi, A &vi, const AdamHyper<A> &h) {
+    const A g = h.decoupled ? gr : gr + h.decay * p;
+    mi = h.b1 * mo + (A(1) - h.b1) * g;
+    vi = h.b2 * vo + (A(1) - h.b2) * g * g;
+    const A upd = h.lr * (mi * h.c1) / (acc_sqrt(vi * h.c2) + h.eps);
+    return h.decoupled ? p * (A(1) - h.lr * h.decay) - upd : p - upd;
+}
+
 template <typename T, typename A>
 __device__ __forceinline__ void adam_elem(T *param, const T *grad, A *m, A *v, int64_t i, const AdamHyper<A> &h) {
-    const A p = ld(param, i);
-    const A g = h.decoupled ? ld(grad, i) : ld(grad, i) + h.decay * p;
-    const A mi = h.b1 * m[i] + (A(1) - h.b1) * g;
-    const A vi = h.b2 * v[i] + (A(1) - h.b2) * g * g;
+    A mi, vi;
+    const A pn = adam_math(ld(param, i), ld(grad, i), m[i], v[i], mi, vi, h);
     m[i] = mi;
     v[i] = vi;
-    const A upd = h.lr * (mi * h.c1) / (acc_sqrt(vi * h.c2) + h.eps);
-    st(param, i, h.decoupled ? p * (A(1) - h.lr * h.decay) - upd : p - upd);
+    st(param, i, pn);
 }
 
 template <typename T, typename A = acc_t<T>>
@@ -507,6 +517,34 @@ __global__ __launch_bounds__(256) void adam_multi_kernel(AdamMulti a, AdamHyper<
     const T *__restrict__ grad = static_cast<const T *>(a.grad[t]);
     A *__restrict__ m = static_cast<A *>(a.m[t]);
     A *__restrict__ v = static_cast<A *>(a.v[t]);
+    if constexpr (std::is_same_v<T, float>) {
+        // fp32 tensors with 16-byte aligned bases (chunks are 4096 elements): four consecutive
+        // elements per thread in 16-byte accesses, the gradient (read once, never written)
+        // non-temporal; the same per-element arithmetic as adam_elem.
+        if (((uintptr_t(param) | uintptr_t(grad) | uintptr_t(m) | uintptr_t(v)) & 15) == 0) {
+            const int64_t n4 = (end - base) / 4;
+            for (int64_t q = threadIdx.x; q < n4; q += blockDim.x) {
+                const int64_t i = base + 4 * q;
+                const adam_f4 p4 = *reinterpret_cast<const adam_f4 *>(param + i);
+                const adam_f4 g4 = __builtin_nontemporal_load(reinterpret_cast<const adam_f4 *>(grad + i));
+                const adam_f4 m4 = *reinterpret_cast<const adam_f4 *>(m + i);
+                const adam_f4 v4 = *reinterpret_cast<const adam_f4 *>(v + i);
+                adam_f4 pn, mn, vn;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float me, ve;
+                    pn[e] = adam_math(p4[e], g4[e], m4[e], v4[e], me, ve, h);
+                    mn[e] = me;
+                    vn[e] = ve;
+                }
+                *reinterpret_cast<adam_f4 *>(m + i) = mn;
+                *reinterpret_cast<adam_f4 *>(v + i) = vn;
+                *reinterpret_cast<adam_f4 *>(param + i) = pn;
+            }
+            for (int64_t i = base + 4 * n4 + threadIdx.x; i < end; i += blockDim.x) adam_elem(param, grad, m, v, i, h);
+            return;
+        }
+    }
     for (int64_t i = base + threadIdx.x; i < end; i += blockDim.x) adam_elem(param, grad, m, v, i, h);
 }
 
