@@ -580,6 +580,27 @@ def test_adam_multi_matches_single_bitwise(dtype):
         assert torch.equal(p, p2) and torch.equal(m, m2) and torch.equal(v, v2)
 
 
+def test_adam_multi_misaligned_views_match_single():
+    """fp32 tensors whose bases are not 16-byte aligned (views one element into a buffer, some
+    of the four per tensor only) take the element-wise path of the multi-tensor launch and
+    still equal the per-tensor update bitwise."""
+    sizes = [4096, 4099, 9000, 17]
+    def view(n, seed, off):
+        return _dev(_randn((n + 1,), seed), torch.float32)[off:off + n]
+    ps = [view(n, 300 + i, i % 2) for i, n in enumerate(sizes)]
+    gs = [view(n, 400 + i, 1) for i, n in enumerate(sizes)]
+    ms = [torch.zeros(n + 1, device=DEV)[(i + 1) % 2:(i + 1) % 2 + n] for i, n in enumerate(sizes)]
+    vs = [torch.zeros(n + 1, device=DEV)[:n] for n in sizes]
+    ref = [(p.clone(), m.clone(), v.clone()) for p, m, v in zip(ps, ms, vs)]
+    for step in (1, 2):
+        _capi.adam_update_multi(ps, gs, ms, vs, step, lr=3e-3, weight_decay=0.01, decoupled=True)
+        for (p, m, v), g in zip(ref, gs):
+            _capi.adam_update(p, g, m, v, step, lr=3e-3, weight_decay=0.01, decoupled=True)
+    torch.cuda.synchronize()
+    for (p, m, v), p2, m2, v2 in zip(ref, ps, ms, vs):
+        assert torch.equal(p, p2) and torch.equal(m, m2) and torch.equal(v, v2)
+
+
 def test_zero_multi_clears_exactly_the_given_bytes():
     arena = torch.full((1 << 16,), 0xAB, dtype=torch.uint8, device=DEV)
     spans = [(0, 4), (16, 7), (64, 4096 * 4 + 3), (40000, 1)] + [(50000 + 64 * i, 12) for i in range(34)]
