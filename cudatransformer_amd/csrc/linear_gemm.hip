@@ -711,7 +711,7 @@ __global__ __launch_bounds__(256) void lin_splitk_reduce_kernel(Args p, int64_t 
     }
 }
 
-// ---- shared-tile products (16-bit storage) ----
+// ---- shared-tile products (16-bit storage; fp32 forwards) ----
 //
 // The kernels above give every wave its own tile, so each wave streams its own A and B rows
 // from L2: a one-wave 128 x 64 tile stages 12 KB per 32-deep K chunk for 0.5 MFLOP, which at
@@ -722,8 +722,9 @@ __global__ __launch_bounds__(256) void lin_splitk_reduce_kernel(Args p, int64_t 
 // barrier per stage, and wave (wm, wn) multiplies A rows wm by B columns wn.  Operands in any
 // layout and view (a K-contiguous head-split stage inside one head, an M/N-contiguous one
 // inside one batch), K segments and K splits across workgroups as lin_kernel, the bias
-// gradient of an M-contiguous A summed by the first tile column.  GEN: some view is
-// head-split or K has several segments.
+// gradient of an M-contiguous A summed by the first tile column.  fp32 (four k-steps of
+// v_mfma_f32_32x32x2f32 per 16-byte operand) takes K-contiguous operands only.  GEN: some
+// view is head-split or K has several segments.
 template <typename F, bool A_KC, bool B_KC, int WM, int WN, int TM, int TN, int S, int KS>
 struct ShCfg {
     static_assert(!F::WIDE || (A_KC && B_KC), "fp32: K-contiguous operands only");
@@ -1140,7 +1141,8 @@ inline SharedPlan shared_plan(const LinGemm &g, bool allow_split) {
     return tiles >= 256 ? SharedPlan{ks, 1} : SharedPlan{0, 1};
 }
 
-// The shared-tile launch of a plan: 128 x 128 tiles of 4 waves, 2 stages.
+// The shared-tile launch of a plan: 16-bit, 128 x 128 tiles of 2 x 2 waves; fp32, 128 x 64 tiles
+// of 4 x 1 waves; 2 stages.
 template <typename F, bool A_KC, bool B_KC>
 hipError_t run_shared_ks(const LinGemm &g, const SharedPlan &sp, void *ws, int64_t ws_bytes, hipStream_t stream) {
     return sp.ks == 2 ? run_shared<F, A_KC, B_KC, 2, 2, 2, 2, 2, 2>(g, sp.splits, ws, ws_bytes, stream)
