@@ -85,46 +85,61 @@ __device__ __forceinline__ void fwd_bf16_block(FwdBf16State<D> &st, const typena
             sacc[kt] = F::mfma(ka[s & 1], qb[s], sacc[kt]);
         }
     }
-    float mloc = -INFINITY;
+    if (MASK) {
 #pragma unroll
-    for (int kt = 0; kt < C::KT; ++kt) {
-        if (!active[kt]) continue;
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float s = sacc[kt][r];
-            if (MASK) {
+            for (int r = 0; r < 16; ++r) {
                 const int key = j0 + kt * 32 + acc_row(r, half);
-                s = (key >= T || (causal && key > row)) ? -INFINITY : s;
-                sacc[kt][r] = s;
+                if (key >= T || (causal && key > row)) sacc[kt][r] = -INFINITY;
             }
-            mloc = fmaxf(mloc, s);
         }
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;  // c > 0: max(S) * c = max(S * c)
-    if (__any(mloc > st.m_run + kRescaleThresholdBf16)) {
-        const float m_new = fmaxf(st.m_run, mloc);
-        const float resc = fast_exp2(st.m_run - m_new);
-        st.m_run = m_new;
-        st.l_run *= resc;
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) st.oacc[dt] *= resc;
     }
     // P^T = exp2(S c - m), rounded to bf16 as the B operand; the denominator sums the same
-    // fp32 values.
+    // fp32 values.  First against the running max without the block's max: if every lane's
+    // share of the block's P stays <= 2^8, so does every P, i.e. the block max is within the
+    // lazy-rescale threshold of m and the max-based rule would not rescale either.  Otherwise
+    // (the max grew by more, or m is still -inf and the sums are inf / NaN) the block max is
+    // taken, the rule applied as before and P recomputed: the same values either way, one
+    // max per score saved on every block where the max holds.
     V pb[C::KT][2];
     float psum = 0.f;
+    auto exp_block = [&]() __attribute__((always_inline)) {
+        psum = 0.f;
 #pragma unroll
-    for (int kt = 0; kt < C::KT; ++kt) {
-        if (!active[kt]) continue;
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+            for (int s = 0; s < 2; ++s) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float p = fast_exp2(fmaf(sacc[kt][8 * s + e], c, -st.m_run));
-                psum += p;
-                pb[kt][s][e] = (typename F::elem)p;
+                for (int e = 0; e < 8; ++e) {
+                    const float p = fast_exp2(fmaf(sacc[kt][8 * s + e], c, -st.m_run));
+                    psum += p;
+                    pb[kt][s][e] = (typename F::elem)p;
+                }
             }
         }
+    };
+    exp_block();
+    if (__any(!(psum <= kPsumLimit))) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < C::KT; ++kt) {
+            if (!active[kt]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, sacc[kt][r]);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave)) * c;  // c > 0: max(S) * c = max(S * c)
+        if (__any(mloc > st.m_run + kRescaleThresholdBf16)) {
+            const float m_new = fmaxf(st.m_run, mloc);
+            const float resc = fast_exp2(st.m_run - m_new);
+            st.m_run = m_new;
+            st.l_run *= resc;
+#pragma unroll
+            for (int dt = 0; dt < C::DT; ++dt) st.oacc[dt] *= resc;
+        }
+        exp_block();
     }
     st.l_run += psum;
     // O^T += V^T P^T: k-step kk of key tile kt covers tile rows 16 (2 kt + kk) + ...
