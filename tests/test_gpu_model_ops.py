@@ -106,18 +106,24 @@ def test_linear_fwd_bwd(dtype, mnk, bias, gemm_path):
         _close(db, _as64(db0, dtype) + dy64.sum(0), TOL[dtype], "db")
 
 
-# fp32 shapes on linear_gemm.hip, one per launch plan (tile, waves, stages, K split):
-#   (4096, 1536, 384)  forward 3072 64x32 tiles -> one wave per tile, 2 stages; dW split 4 ways
+# Shapes on linear_gemm.hip covering its launch plans (fp32 / 16-bit; forward, dX, dW):
+#   (4096, 1536, 384)  fp32 forward on the shared-tile kernel (768 128 x 64 tiles, GELU-MLP
+#                      width); dW split 4 ways; 16-bit forward shared-tile, two-chunk stages
 #   (4096, 384, 1536)  forward / dW four waves per tile; dX 3072 tiles, one wave
-#   (8192, 1024, 1024) one wave per tile, 3 stages (K = 1024); dW on 64 x 64 tiles of 8 waves
+#   (8192, 1024, 1024) fp32 forward shared-tile, dX one wave per tile, 3 stages, dW 64 x 64 tiles
+#                      of 8 waves; 16-bit: every product shared-tile (dW unsplit from 256 tiles)
 #   (1008, 208, 1008)  ragged tiles in M, N and K-chunk count on all three products
 #   (64, 16, 4096)     dX with one K chunk for four waves (three waves add a zero tile)
 #   (8192, 64, 64)     dW split 8 ways on 8-wave 64 x 32 tiles (8 of the 512 K chunks per wave)
-#   (4096, 1152, 384)  the QKV-width product of the NanoGPT configuration
-#   (8100, 1024, 992)  16-bit: the one-wave 128 x 64 forward and 64 x 128 dX tiles with ragged
-#                      M (forward) and N (dX) edges
+#   (4096, 1152, 384)  the QKV-width product of the NanoGPT configuration (576 tiles: lin_kernel)
+#   (8100, 1024, 992)  ragged M (forward) and N (dX); 16-bit forward with one-chunk stages
+#   (2000, 1984, 2016) 16-bit shared-tile forward and dX with ragged M and N, one- and
+#                      two-chunk stages
+#   (2048, 2048, 2048) 16-bit dW on the shared-tile kernel without a K split (256 tiles)
+#   (4096, 2050, 512)  N not a multiple of 4: the shared-tile kernel's element-wise epilogue
 LIN_SHAPES = [(4096, 1536, 384), (4096, 384, 1536), (8192, 1024, 1024), (1008, 208, 1008), (64, 16, 4096),
-              (8192, 64, 64), (4096, 1152, 384), (8100, 1024, 992), (2000, 1984, 2016), (2048, 2048, 2048)]
+              (8192, 64, 64), (4096, 1152, 384), (8100, 1024, 992), (2000, 1984, 2016), (2048, 2048, 2048),
+              (4096, 2050, 512)]
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
@@ -147,8 +153,9 @@ def test_linear_plans(mnk, dt):
 # (B, T, E, H, d): products of at least 256 128 x 128 tiles take the 16-bit shared-tile GEMM
 # (fp32: forward products of at least 768 128 x 64 tiles, the B8 shape's head-split output
 # projection among them); d = 64 stages two K chunks per head, d = 32 one; T = 700 puts batch
-# boundaries inside tiles.
-PROJ_SHAPES = [(4, 1024, 1024, 16, 64), (2, 2048, 1024, 32, 32), (3, 700, 768, 12, 64), (8, 1024, 1024, 16, 64)]
+# boundaries inside tiles; d = 12 writes a head-split output in 4-column groups.
+PROJ_SHAPES = [(4, 1024, 1024, 16, 64), (2, 2048, 1024, 32, 32), (3, 700, 768, 12, 64), (8, 1024, 1024, 16, 64),
+               (4, 1024, 512, 32, 12)]
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
