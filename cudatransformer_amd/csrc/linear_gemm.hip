@@ -169,21 +169,43 @@ using F16Fmt = H16Fmt<false>;
 
 // ---- views ----
 
-// A LinView on the device, in bytes.  Indices are below 2^31 (checked on the host).
+// Division by a run-time divisor D >= 1 of indices 0 <= i < 2^31 as a multiply and a shift
+// (Granlund & Montgomery, "Division by invariant integers using multiplication", 1994, the
+// unsigned case): with l = ceil(log2 D) and m = floor(2^32 (2^l - D) / D) + 1,
+// i / D = (mulhi(i, m) + i) >> l exactly for every 32-bit i; mulhi(i, m) < i keeps the sum
+// below 2^32 for i < 2^31.
+struct FastDiv {
+    uint32_t mul, shift;
+};
+inline FastDiv make_fastdiv(uint32_t D) {
+    if (D == 0) return FastDiv{0, 0};  // no index to divide (an empty view)
+    uint32_t l = 0;
+    while (l < 32 && (uint64_t(1) << l) < D) ++l;
+    const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << l) - D)) / D + 1;
+    return FastDiv{uint32_t(m), l};
+}
+__device__ __forceinline__ int fastdiv(int i, FastDiv f) {
+    return int((__umulhi(uint32_t(i), f.mul) + uint32_t(i)) >> f.shift);
+}
+
+// A LinView on the device, in bytes.  Indices are below 2^31 (checked on the host).  The
+// head-split offsets divide by T and d through FastDiv: the store loops of a tile compute
+// one row and one column offset per 4 elements.
 struct DView {
     int64_t ld_b;    // linear: row pitch
     int64_t bstr_b;  // head-split: one batch, H*T*d elements
     int64_t hstr_b;  // head-split: one head, T*d elements
     int32_t heads, T, d, eb;
+    FastDiv tdiv, ddiv;  // head-split: i / T, j / d
 };
 __device__ __forceinline__ int64_t rowoff(const DView &v, int i) {
     if (v.heads == 0) return int64_t(i) * v.ld_b;
-    const int b = i / v.T;
+    const int b = fastdiv(i, v.tdiv);
     return int64_t(b) * v.bstr_b + int64_t(i - b * v.T) * (v.d * v.eb);
 }
 __device__ __forceinline__ int64_t coloff(const DView &v, int j) {
     if (v.heads == 0) return int64_t(j) * v.eb;
-    const int h = j / v.d;
+    const int h = fastdiv(j, v.ddiv);
     return int64_t(h) * v.hstr_b + int64_t(j - h * v.d) * v.eb;
 }
 // Byte distance between consecutive rows inside one K chunk of an M/N-contiguous operand (a
@@ -995,6 +1017,10 @@ inline DView dview(const LinView &v, int eb) {
     d.ld_b = v.ld * eb;
     d.hstr_b = int64_t(v.T) * v.d * eb;
     d.bstr_b = int64_t(v.heads) * v.T * v.d * eb;
+    if (v.heads != 0) {
+        d.tdiv = make_fastdiv(uint32_t(v.T));
+        d.ddiv = make_fastdiv(uint32_t(v.d));
+    }
     return d;
 }
 
