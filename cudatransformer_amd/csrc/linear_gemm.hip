@@ -854,31 +854,62 @@ __global__ __launch_bounds__(WM * WN * 64) void lin_shared_kernel(Args p) {
         if (j + S - 1 < nst) issue(islot, st0 + j + S - 1);
         const uint32_t sa = base + uint32_t(slot * C::STAGE);
         const uint32_t sb = sa + uint32_t(OA::BYTES);
+        if constexpr (!F::WIDE && A_KC) {
+            // 16-bit products with a K-contiguous A (forwards, dX): step s + 1's operands are
+            // read before step s's MFMAs, and the scheduling fence keeps the compiler from
+            // hoisting every step's reads to the top of the stage, so each step's MFMAs wait
+            // only for reads issued a whole step earlier.
+            floatx4 av[2][TM], bv[2][TN];
 #pragma unroll
-        for (int s = 0; s < 2 * KS; ++s) {
-            floatx4 av[TM], bv[TN];
+            for (int tm = 0; tm < TM; ++tm) av[0][tm] = ra.read(sa, TM * wm + tm, 0);
 #pragma unroll
-            for (int tm = 0; tm < TM; ++tm) av[tm] = ra.read(sa, TM * wm + tm, s);
+            for (int tn = 0; tn < TN; ++tn) bv[0][tn] = rb.read(sb, TN * wn + tn, 0);
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn) bv[tn] = rb.read(sb, TN * wn + tn, s);
-            if (!A_KC && sum_a) {
+            for (int s = 0; s < 2 * KS; ++s) {
+                const int cur = s & 1;
+                if (s + 1 < 2 * KS) {
 #pragma unroll
-                for (int tm = 0; tm < TM; ++tm) dsum[tm] += F::sum(av[tm]);
-            }
-            if constexpr (F::WIDE) {
-                // fp32: the 16-byte operand is four k-steps of v_mfma_f32_32x32x2f32.
+                    for (int tm = 0; tm < TM; ++tm) av[cur ^ 1][tm] = ra.read(sa, TM * wm + tm, s + 1);
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-                        for (int tn = 0; tn < TN; ++tn)
-                            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[tm][t], bv[tn][t], acc[tm][tn], 0, 0, 0);
-            } else {
+                    for (int tn = 0; tn < TN; ++tn) bv[cur ^ 1][tn] = rb.read(sb, TN * wn + tn, s + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-                    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = F::mfma(av[tm], bv[tn], acc[tm][tn]);
+                    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = F::mfma(av[cur][tm], bv[cur][tn], acc[tm][tn]);
+            }
+        } else {
+            // fp32 and the 16-bit weight gradients: the compiler schedules the stage's reads
+            // (the same fence measured neutral in fp32 and 2-3.5 % slower on the transposed
+            // M/N-contiguous reads).
+#pragma unroll
+            for (int s = 0; s < 2 * KS; ++s) {
+                floatx4 av[TM], bv[TN];
+#pragma unroll
+                for (int tm = 0; tm < TM; ++tm) av[tm] = ra.read(sa, TM * wm + tm, s);
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn) bv[tn] = rb.read(sb, TN * wn + tn, s);
+                if (!A_KC && sum_a) {
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm) dsum[tm] += F::sum(av[tm]);
+                }
+                if constexpr (F::WIDE) {
+                    // fp32: the 16-byte operand is four k-steps of v_mfma_f32_32x32x2f32.
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+#pragma unroll
+                        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                            for (int tn = 0; tn < TN; ++tn)
+                                acc[tm][tn] =
+                                    __builtin_amdgcn_mfma_f32_32x32x2f32(av[tm][t], bv[tn][t], acc[tm][tn], 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                        for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = F::mfma(av[tm], bv[tn], acc[tm][tn]);
+                }
             }
         }
         slot = slot + 1 == S ? 0 : slot + 1;
