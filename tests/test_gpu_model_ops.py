@@ -154,8 +154,10 @@ def test_linear_plans(mnk, dt):
 # (fp32: forward products of at least 768 128 x 64 tiles, the B8 shape's head-split output
 # projection among them); d = 64 stages two K chunks per head, d = 32 one; T = 700 puts batch
 # boundaries inside tiles; d = 12 writes a head-split output in 4-column groups.
+# The last three put odd and small T and small d under the head-split row / column offsets
+# (divisions by T and d done as multiply-high and shift on the device).
 PROJ_SHAPES = [(4, 1024, 1024, 16, 64), (2, 2048, 1024, 32, 32), (3, 700, 768, 12, 64), (8, 1024, 1024, 16, 64),
-               (4, 1024, 512, 32, 12)]
+               (4, 1024, 512, 32, 12), (2, 1025, 256, 8, 32), (3, 17, 128, 4, 32), (2, 333, 64, 16, 4)]
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
